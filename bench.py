@@ -1,0 +1,338 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Headline workload (M = 1): one step is the decode
+pass of a Llama-3-8B-shaped stack's linears -- q, k, v, o, gate, up, down
+(N x K = 4096x4096, 1024x4096, 1024x4096, 4096x4096, 14336x4096, 14336x4096,
+4096x14336) for each of 32 layers, 224 quantized matmuls at M = 1 with 4-bit,
+group-64 weights and bf16 activations/scales/biases.  Every layer has its
+own weights (3.93 GB in HBM), so the 256 MB Infinity Cache cannot serve
+repeats.  The step is captured once as a HIP graph and replayed; inputs are
+resident in HBM before the timed region starts.
+
+value = algorithmic bytes of the step / step time, in GB/s
+(bytes per linear: N*K/2 packed codes + 4*N*K/64 scale+bias + 2*M*K + 2*M*N).
+
+Also reported (not the headline): per-shape qmv GB/s at M = 1 and 8,
+prefill qmm TFLOP/s, GGUF dequant/convert GB/s,
+the roofline record of the dominant kernel and the CPU baseline (the
+restated MLX CPU qmm loop from oracle/, timed on this host).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+LAYERS = 32
+HIDDEN, FFN, KV = 4096, 14336, 1024
+LAYER_SHAPES = [  # (name, N, K)
+    ("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
+    ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN),
+]
+GS, BITS = 64, 4
+
+
+def qmv_bytes(M, N, K, bits=BITS, gs=GS):
+    return N * K * bits // 8 + 2 * 2 * N * (K // gs) + 2 * M * K + 2 * M * N
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Linear:
+    """One layer's packed weight on the GPU (random codes; bf16 scales/biases of
+    the magnitude a N(0, 0.02) weight quantizes to)."""
+
+    def __init__(self, N, K, gen, bits=BITS, gs=GS):
+        import torch
+
+        self.N, self.K = N, K
+        self.w = torch.randint(-(2**31), 2**31 - 1, (N, K * bits // 32), dtype=torch.int32, device="cuda",
+                               generator=gen)
+        self.s = (torch.rand((N, K // gs), device="cuda", generator=gen) * 0.004 + 0.004).to(torch.bfloat16)
+        self.b = (-7.5 * self.s.float()).to(torch.bfloat16)
+
+
+def run_qmv(lin, x, y, bits=BITS, gs=GS):
+    from eredu_amd import _native
+
+    _native.check(_native.lib().eq_quantized_matmul(
+        y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(), x.shape[0], lin.N, lin.K,
+        True, gs, bits, b"affine", _native.EQ_DTYPE_BF16, _native.EQ_DTYPE_BF16, _stream()))
+
+
+def _stream():
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def capture(fn):
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm the kernels once outside capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per replay
+
+
+def bench_decode_stack(layers, M, steps, warmup):
+    """The headline: all 7 linears of all layers at batch M, as one graph."""
+    import torch
+
+    xs = {K: torch.randn((M, K), device="cuda").to(torch.bfloat16) for K in (HIDDEN, FFN)}
+    ys = {N: torch.empty((M, N), device="cuda", dtype=torch.bfloat16) for N in (HIDDEN, FFN, KV)}
+
+    def step():
+        for layer in layers:
+            for (name, N, K), lin in zip(LAYER_SHAPES, layer):
+                run_qmv(lin, xs[K], ys[N])
+
+    g = capture(step)
+    ms = time_graph(g, steps, warmup)
+    nbytes = len(layers) * sum(qmv_bytes(M, N, K) for _, N, K in LAYER_SHAPES)
+    return ms, nbytes, len(layers) * len(LAYER_SHAPES)
+
+
+def bench_per_shape(layers, M, steps, warmup):
+    import torch
+
+    out = {}
+    for i, (name, N, K) in enumerate(LAYER_SHAPES):
+        if name in ("v", "up"):
+            continue  # same shapes as k and gate
+        x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        g = capture(lambda: [run_qmv(layer[i], x, y) for layer in layers])
+        ms = time_graph(g, max(steps // 2, 10), warmup)
+        us = ms * 1e3 / len(layers)
+        gbs = qmv_bytes(M, N, K) / (us * 1e-6) / 1e9
+        out[f"{N}x{K}"] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
+    """Prefill qmm TFLOP/s at the Llama shapes; weights rotate over 4 copies."""
+    import torch
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    out = {}
+    for bits in bits_list:
+        for (name, N, K) in [("q/o", HIDDEN, HIDDEN), ("k/v", KV, HIDDEN), ("gate/up", FFN, HIDDEN),
+                             ("down", HIDDEN, FFN)]:
+            lins = [Linear(N, K, gen, bits=bits) for _ in range(4)]
+            for M in Ms:
+                x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+                y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+                g = capture(lambda: [run_qmv(l, x, y, bits=bits) for l in lins])
+                ms = time_graph(g, max(steps // 4, 5), warmup) / len(lins)
+                tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+                out[f"b{bits} M{M} {N}x{K}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
+                                                "frac_mfma": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
+            del lins
+            torch.cuda.empty_cache()
+    return out
+
+
+def bench_gguf(steps, warmup):
+    """GGUF 4096x14336 dequant (bf16) and convert (affine) GB/s."""
+    import torch
+
+    from eredu_amd import gguf as G
+
+    rows, cols = 4096, 14336
+    out = {}
+    for ty in (G.GgmlType.Q4_0, G.GgmlType.Q8_0, G.GgmlType.Q4K):
+        vals, nbytes = ty.block_and_bytes()
+        nraw = rows * cols // vals * nbytes
+        copies = 3
+        raws = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        desc = G.TensorDescriptor("t", [cols, rows], ty, nraw)
+        dense = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
+        bits, gs = G.affine_config(ty)
+        aw = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device="cuda")
+        asb = torch.empty((rows, cols // gs), dtype=torch.float16, device="cuda")
+        abb = torch.empty_like(asb)
+        from eredu_amd import _native
+
+        def deq():
+            for r in raws:
+                G.dequantize(desc, r, G.Endian.Little, G.DequantDefinition.Affine, torch.bfloat16, out=dense)
+
+        def conv():
+            for r in raws:
+                _native.check(_native.lib().eq_gguf_convert_affine(
+                    aw.data_ptr(), asb.data_ptr(), abb.data_ptr(), r.data_ptr(), nraw, int(ty), rows, cols, 0,
+                    _stream()))
+
+        for label, fn, out_bytes in (("dequant_bf16", deq, rows * cols * 2),
+                                     ("convert_affine_g32", conv, aw.numel() * 4 + 2 * asb.numel() * 2)):
+            g = capture(fn)
+            ms = time_graph(g, max(steps // 4, 5), warmup) / copies
+            gbs = (nraw + out_bytes) / (ms * 1e-3) / 1e9
+            out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del raws
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(layer, budget_s=12.0):
+    """The restated MLX CPU quantized matmul (oracle/eq_oracle.c or_qmm_t_f32),
+    on the same packed inputs of one layer's 7 linears at M = 1."""
+    import torch
+
+    from oracle import oracle as orc
+
+    host = []
+    for (name, N, K), lin in zip(LAYER_SHAPES, layer):
+        host.append((N, K, lin.w.cpu().numpy().view(np.uint32), lin.s.view(torch.int16).cpu().numpy().view(np.uint16),
+                     lin.b.view(torch.int16).cpu().numpy().view(np.uint16)))
+    x = {K: np.ascontiguousarray(orc.f32_to_bf16_bits(np.random.default_rng(0).standard_normal((1, K), dtype=np.float32)))
+         for K in (HIDDEN, FFN)}
+    threads = max(1, min(16, os.cpu_count() or 1))
+    res = {}
+    for nthreads in sorted({1, threads}):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            for N, K, w, s, b in host:
+                orc.qmm_t_f32(x[K], orc.BF16, w, s, b, orc.BF16, 1, N, K, GS, BITS, threads=nthreads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > budget_s / 2 or reps >= 50:
+                break
+        nbytes = reps * sum(qmv_bytes(1, N, K) for N, K, *_ in host)
+        res[nthreads] = (nbytes / el / 1e9, reps, el)
+    return res, threads
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline only (no qmm / gguf / per-shape sweeps)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build is single-GPU)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from eredu_amd import _native
+
+    _native.lib()
+    torch.cuda.set_device(0)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    log("[bench] allocating 32 layers of 4-bit weights")
+    layers = [[Linear(N, K, gen) for _, N, K in LAYER_SHAPES] for _ in range(LAYERS)]
+    torch.cuda.synchronize()
+
+    log("[bench] decode stack M=1")
+    ms, nbytes, launches = bench_decode_stack(layers, 1, args.steps, args.warmup)
+    value = nbytes / (ms * 1e-3) / 1e9
+    detail = {}
+    log("[bench] decode stack M=8")
+    ms8, nbytes8, _ = bench_decode_stack(layers, 8, max(args.steps // 2, 5), args.warmup)
+    detail["decode_stack_M8_GB/s"] = round(nbytes8 / (ms8 * 1e-3) / 1e9, 1)
+    if not args.quick:
+        log("[bench] per-shape qmv")
+        detail["qmv_M1"] = bench_per_shape(layers, 1, args.steps, args.warmup)
+        detail["qmv_M8"] = bench_per_shape(layers, 8, args.steps, args.warmup)
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline")
+        res, threads = cpu_baseline(layers[0])
+        v1 = res[1]
+        vt = res[threads]
+        cpu = {"value": round(vt[0], 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"one layer's 7 linears (122.8 MB packed) at M=1, {vt[1]} passes in {vt[2]:.1f} s; "
+                         f"restated MLX CPU _qmm_t loop (oracle/eq_oracle.c or_qmm_t_f32), f32 accumulate",
+               "single_thread_GB/s": round(v1[0], 3)}
+    del layers
+    torch.cuda.empty_cache()
+    if not args.quick:
+        log("[bench] qmm prefill")
+        detail["qmm"] = bench_qmm(args.steps, args.warmup)
+        log("[bench] gguf")
+        detail["gguf"] = bench_gguf(args.steps, args.warmup)
+
+    per_launch_bytes = nbytes / launches
+    avg_launch_us = ms * 1e3 / launches
+    achieved = per_launch_bytes / (avg_launch_us * 1e-6) / 1e9
+    line = {
+        "metric": "4-bit qmv achieved HBM GB/s (% peak); decode tok/s for 8B-shaped 4-bit stack",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random 4-bit codes, bf16 scales/biases, x ~ N(0,1) bf16)",
+        "config": {
+            "workload": "decode qmv sweep: Llama-3-8B linears q,k,v,o,gate,up,down x 32 layers, M=1, "
+                        "4-bit group-64, bf16 activations/scales/biases, one HIP graph per step",
+            "M": 1, "layers": LAYERS, "bits": BITS, "group_size": GS,
+            "bytes_per_step": nbytes, "launches_per_step": launches,
+        },
+        "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "qmv_mfma_kernel<4,64,BF16T,1>",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "per_launch_bytes": int(per_launch_bytes),
+            "avg_launch_us": round(avg_launch_us, 3),
+        },
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,37 @@
+"""eredu_amd -- MI355X (gfx950) quantized-linear hot path.
+
+Group-wise affine quantized matmul (qmv for decode, qmm for prefill) and the
+GGUF Q4_0 / Q8_0 / Q4_K block dequant and convert that feeds it, as
+hand-written HIP kernels behind a C ABI (``include/eredu_hip.h``), with a
+host-side mirror of the reference's operator API:
+
+* :mod:`eredu_amd.quantization` -- safemlx ``quantized_matmul[_with_mode]``,
+  ``dequantize[_with_mode]``, ``QuantizedLinear``.
+* :mod:`eredu_amd.gguf` -- eredu-gguf ``convert_affine`` / ``AffineTensor``
+  and dense dequantization.
+"""
+from ._native import EreduError
+from .quantization import (
+    DEFAULT_BITS,
+    DEFAULT_GROUP_SIZE,
+    QuantizationMode,
+    QuantizedLinear,
+    dequantize,
+    dequantize_with_mode,
+    quantized_matmul,
+    quantized_matmul_with_mode,
+    quantized_packed_dimension,
+)
+
+__all__ = [
+    "EreduError",
+    "DEFAULT_BITS",
+    "DEFAULT_GROUP_SIZE",
+    "QuantizationMode",
+    "QuantizedLinear",
+    "dequantize",
+    "dequantize_with_mode",
+    "quantized_matmul",
+    "quantized_matmul_with_mode",
+    "quantized_packed_dimension",
+]

@@ -1,0 +1,57 @@
+"""ctypes binding of the C ABI in ``include/eredu_hip.h``.
+
+The shared library is built in-tree by ``eredu_amd.build``.  There is no
+fallback: if the library is missing, loading fails with an error that says so.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from .build import LIB_PATH
+
+EQ_DTYPE_F32, EQ_DTYPE_F16, EQ_DTYPE_BF16 = 0, 1, 2
+EQ_ENDIAN_LITTLE, EQ_ENDIAN_BIG = 0, 1
+EQ_DEQUANT_AFFINE, EQ_DEQUANT_NATIVE = 0, 1
+
+# Every exported entry point with its ctypes signature (mirrors include/eredu_hip.h).
+_vp, _i64, _i32, _b = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_bool
+SIGNATURES = {
+    "eq_last_error": ([], ctypes.c_char_p),
+    "eq_version": ([], _i32),
+    "eq_quantized_matmul": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _b, _i32, _i32, ctypes.c_char_p, _i32, _i32, _vp], _i32),
+    "eq_dequantize": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, ctypes.c_char_p, _i32, _i32, _vp], _i32),
+    "eq_gguf_convert_affine": ([_vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i32, _vp], _i32),
+    "eq_gguf_dequantize": ([_vp, _vp, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _vp], _i32),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class EreduError(RuntimeError):
+    """Error raised when a library call fails (the reference's Exception{what})."""
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise EreduError(
+                    f"HIP kernel library not found at {LIB_PATH}; build it with `python -m eredu_amd.build`"
+                )
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = lib().eq_last_error().decode("utf-8", "replace")
+        raise EreduError(msg or "unknown error")

@@ -1,0 +1,307 @@
+// C ABI entry points, argument validation and dispatch, plus the general
+// (any activation/scale dtype, any layout) quantized matmul and dequantize
+// kernels that back the shapes the matrix-core paths do not take.
+//
+// Dispatch of eq_quantized_matmul (transpose = true, bf16 activations,
+// bits 4/8, bf16/f16 scales):
+//   M <= 16  -> qmv_mfma (qmv.hip), the decode path
+//   M  > 16  -> qmm_mfma (qmm.hip), the prefill path (N % 128 == 0)
+// Everything else (f32/f16 activations, f32 scales, bits 2, transpose =
+// false, ragged N) runs the f32 kernels below.  There is no host fallback: a
+// shape no kernel takes is an error.
+#include <cstring>
+#include <type_traits>
+
+#include "eq_common.hpp"
+
+namespace eq {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error(std::string(what) + ": kernel launch failed: " + hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                     const void* s, const void* b, int M, int N, int K, hipStream_t st);
+bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                     const void* s, const void* b, int M, int N, int K, hipStream_t st);
+
+namespace {
+
+// ------------------------------------------------------------ general kernels
+
+// LSB-first code c of a packed row (bits in {2, 4, 8} never straddle words).
+template <int BITS>
+__device__ __forceinline__ uint32_t code_at(const uint32_t* row, int64_t c) {
+    constexpr int PACK = 32 / BITS;
+    return (row[c / PACK] >> ((c % PACK) * BITS)) & ((1u << BITS) - 1u);
+}
+
+constexpr int kGenRowsPerWG = 4;
+constexpr int kGenMChunk = 8;
+
+// transpose = true: one wave per output feature n, lanes stride over K;
+// activations in chunks of 8 rows.  f32 arithmetic throughout.
+template <int BITS, typename XT, typename ST>
+__global__ __launch_bounds__(64 * kGenRowsPerWG) void qmm_t_general(
+    typename XT::storage* __restrict__ y, const typename XT::storage* __restrict__ x,
+    const uint32_t* __restrict__ w, const typename ST::storage* __restrict__ s,
+    const typename ST::storage* __restrict__ b, int64_t M, int64_t N, int64_t K, int gs) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = int64_t(blockIdx.x) * kGenRowsPerWG + (threadIdx.x >> 6);
+    if (n >= N) return;
+    const int64_t G = K / gs;
+    const uint32_t* row = w + n * (K * BITS / 32);
+    for (int64_t m0 = 0; m0 < M; m0 += kGenMChunk) {
+        float acc[kGenMChunk];
+#pragma unroll
+        for (int i = 0; i < kGenMChunk; i++) acc[i] = 0.f;
+        for (int64_t k = lane; k < K; k += 64) {
+            const int64_t g = k / gs;
+            const float wv = load_param<ST>(s, n * G + g) * float(code_at<BITS>(row, k)) +
+                             (b ? load_param<ST>(b, n * G + g) : 0.f);
+#pragma unroll
+            for (int i = 0; i < kGenMChunk; i++)
+                if (m0 + i < M) acc[i] = fmaf(load_param<XT>(x, (m0 + i) * K + k), wv, acc[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kGenMChunk; i++) {
+            float v = acc[i];
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0 && m0 + i < M) store_out<XT>(y, (m0 + i) * N + n, v);
+        }
+    }
+}
+
+// transpose = false: W is [K, N] packed along N.  One thread per output
+// column n and chunk of 8 activation rows, walking K.
+template <int BITS, typename XT, typename ST>
+__global__ __launch_bounds__(256) void qmm_n_general(typename XT::storage* __restrict__ y,
+                                                     const typename XT::storage* __restrict__ x,
+                                                     const uint32_t* __restrict__ w,
+                                                     const typename ST::storage* __restrict__ s,
+                                                     const typename ST::storage* __restrict__ b, int64_t M,
+                                                     int64_t N, int64_t K, int gs) {
+    const int64_t n = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t m0 = int64_t(blockIdx.y) * kGenMChunk;
+    if (n >= N) return;
+    const int64_t G = N / gs;
+    float acc[kGenMChunk];
+#pragma unroll
+    for (int i = 0; i < kGenMChunk; i++) acc[i] = 0.f;
+    for (int64_t k = 0; k < K; k++) {
+        const uint32_t* row = w + k * (N * BITS / 32);
+        const float wv = load_param<ST>(s, k * G + n / gs) * float(code_at<BITS>(row, n)) +
+                         (b ? load_param<ST>(b, k * G + n / gs) : 0.f);
+#pragma unroll
+        for (int i = 0; i < kGenMChunk; i++)
+            if (m0 + i < M) acc[i] = fmaf(load_param<XT>(x, (m0 + i) * K + k), wv, acc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kGenMChunk; i++)
+        if (m0 + i < M) store_out<XT>(y, (m0 + i) * N + n, acc[i]);
+}
+
+// out[r, c] = f32(s) * q + f32(b), one rounding each (convert.rs:81-101).
+template <int BITS, typename ST, typename OT>
+__global__ __launch_bounds__(256) void dequant_kernel(typename OT::storage* __restrict__ out,
+                                                      const uint32_t* __restrict__ w,
+                                                      const typename ST::storage* __restrict__ s,
+                                                      const typename ST::storage* __restrict__ b, int64_t rows,
+                                                      int64_t cols, int gs) {
+    constexpr int PACK = 32 / BITS;
+    const int64_t words = rows * cols / PACK;
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= words) return;
+    const uint32_t word = w[i];
+    const int64_t base = i * PACK;  // element index of the word's first code
+    const int64_t r = base / cols, c0 = base % cols;
+    const int64_t G = cols / gs;
+#pragma unroll
+    for (int p = 0; p < PACK; p++) {
+        const int64_t g = r * G + (c0 + p) / gs;
+        const float sc = load_param<ST>(s, g);
+        const float bi = b ? load_param<ST>(b, g) : 0.f;
+        const float prod = sc * float((word >> (p * BITS)) & ((1u << BITS) - 1u));
+        store_out<OT>(out, base + p, __fadd_rn(prod, bi));
+    }
+}
+
+// --------------------------------------------------------------- dispatch
+
+template <typename F>
+bool with_dtype(int dt, F&& f) {
+    switch (dt) {
+    case EQ_DTYPE_F32: f(F32T{}); return true;
+    case EQ_DTYPE_F16: f(F16T{}); return true;
+    case EQ_DTYPE_BF16: f(BF16T{}); return true;
+    default: return false;
+    }
+}
+
+template <typename F>
+bool with_bits(int bits, F&& f) {
+    switch (bits) {
+    case 2: f(std::integral_constant<int, 2>{}); return true;
+    case 4: f(std::integral_constant<int, 4>{}); return true;
+    case 8: f(std::integral_constant<int, 8>{}); return true;
+    default: return false;
+    }
+}
+
+bool valid_dtype(int d) { return d == EQ_DTYPE_F32 || d == EQ_DTYPE_F16 || d == EQ_DTYPE_BF16; }
+
+int check_mode(const char* mode) {
+    if (mode == nullptr || std::strcmp(mode, "affine") == 0) return 0;
+    if (std::strcmp(mode, "mxfp4") == 0) {
+        set_error("quantization mode 'mxfp4' is not implemented on this device path (affine only)");
+        return 1;
+    }
+    set_error(std::string("invalid quantization mode '") + mode + "'");
+    return 1;
+}
+
+// Group size / bits rules of the affine contract (eredu-checkpoint/src/lib.rs:69-123,
+// safemlx/src/ops/quantization.rs:62-64); this library implements gs 32/64/128, bits 2/4/8.
+int check_gs_bits(int group_size, int bits) {
+    if (bits != 2 && bits != 4 && bits != 8) {
+        set_error("bits must be 2, 4 or 8 on this device path, got " + std::to_string(bits));
+        return 1;
+    }
+    if (group_size != 32 && group_size != 64 && group_size != 128) {
+        set_error("group_size must be 32, 64 or 128, got " + std::to_string(group_size));
+        return 1;
+    }
+    return 0;
+}
+
+}  // namespace
+}  // namespace eq
+
+using namespace eq;
+
+extern "C" const char* eq_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int eq_version(void) { return 100; }
+
+extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                                   int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
+                                   const char* mode, int x_dtype, int scale_dtype, eq_stream_t stream) {
+    clear_error();
+    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype)) {
+        set_error("invalid dtype code");
+        return 1;
+    }
+    if (M < 0 || N <= 0 || K <= 0) {
+        set_error("invalid shape: M >= 0, N > 0 and K > 0 required");
+        return 1;
+    }
+    // The packed (quantized) dimension must hold whole groups
+    // (MLX: "last dimension is not divisible by group size").
+    const int64_t packed_dim = transpose ? K : N;
+    if (packed_dim % group_size != 0) {
+        set_error("the quantized dimension (" + std::to_string(packed_dim) + ") is not divisible by group_size " +
+                  std::to_string(group_size));
+        return 1;
+    }
+    if (!y || !x || !w || !scales) {
+        set_error("null pointer argument");
+        return 1;
+    }
+    if (M == 0) return 0;
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
+        set_error("dimension exceeds 2^31 - 1");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+
+    const bool mfma_ok = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
+                         (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && aligned(x, 16) &&
+                         aligned(w, 16);
+    if (mfma_ok && M <= 16 && N % 16 == 0) {
+        if (launch_qmv_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
+                            w, scales, biases, int(M), int(N), int(K), st))
+            return check_launch("quantized_matmul (qmv)");
+    }
+    if (mfma_ok && M > 16 && N % 128 == 0 && K % 64 == 0) {
+        if (launch_qmm_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
+                            w, scales, biases, int(M), int(N), int(K), st))
+            return check_launch("quantized_matmul (qmm)");
+    }
+
+    bool launched = false;
+    with_bits(bits, [&](auto bc) {
+        constexpr int B = decltype(bc)::value;
+        with_dtype(x_dtype, [&](auto xt) {
+            typedef decltype(xt) XT;
+            with_dtype(scale_dtype, [&](auto stt) {
+                typedef decltype(stt) ST;
+                typedef typename XT::storage XS;
+                typedef typename ST::storage SS;
+                if (transpose) {
+                    const dim3 grid(unsigned((N + kGenRowsPerWG - 1) / kGenRowsPerWG));
+                    qmm_t_general<B, XT, ST><<<grid, 64 * kGenRowsPerWG, 0, st>>>(
+                        static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
+                        static_cast<const SS*>(biases), M, N, K, group_size);
+                } else {
+                    const dim3 grid(unsigned((N + 255) / 256), unsigned((M + kGenMChunk - 1) / kGenMChunk));
+                    qmm_n_general<B, XT, ST><<<grid, 256, 0, st>>>(
+                        static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
+                        static_cast<const SS*>(biases), M, N, K, group_size);
+                }
+                launched = true;
+            });
+        });
+    });
+    if (!launched) {
+        set_error("no kernel for this combination");
+        return 1;
+    }
+    return check_launch("quantized_matmul (general)");
+}
+
+extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases, int64_t rows,
+                             int64_t cols, int group_size, int bits, const char* mode, int scale_dtype,
+                             int out_dtype, eq_stream_t stream) {
+    clear_error();
+    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    if (!valid_dtype(scale_dtype) || !valid_dtype(out_dtype)) {
+        set_error("invalid dtype code");
+        return 1;
+    }
+    if (rows < 0 || cols < 0 || (cols % group_size) != 0) {
+        set_error("cols must be a non-negative multiple of group_size");
+        return 1;
+    }
+    if (rows == 0 || cols == 0) return 0;
+    if (!out || !w || !scales) {
+        set_error("null pointer argument");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int64_t words = rows * cols * bits / 32;
+    const dim3 grid(unsigned((words + 255) / 256));
+    with_bits(bits, [&](auto bc) {
+        constexpr int B = decltype(bc)::value;
+        with_dtype(scale_dtype, [&](auto stt) {
+            typedef decltype(stt) ST;
+            with_dtype(out_dtype, [&](auto ot) {
+                typedef decltype(ot) OT;
+                dequant_kernel<B, ST, OT><<<grid, 256, 0, st>>>(
+                    static_cast<typename OT::storage*>(out), w, static_cast<const typename ST::storage*>(scales),
+                    static_cast<const typename ST::storage*>(biases), rows, cols, group_size);
+            });
+        });
+    });
+    return check_launch("dequantize");
+}

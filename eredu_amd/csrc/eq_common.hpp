@@ -1,0 +1,88 @@
+// Shared device helpers and host error plumbing for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/eredu_hip.h"
+
+namespace eq {
+
+// ------------------------------------------------------------------ host side
+
+// Thread-local message of the last failed call (the mlx-c convention of
+// safemlx/src/error.rs:239-269: status code plus a per-thread message).
+void set_error(const std::string& msg);
+void clear_error();
+
+// Checks the launch status of the kernels just enqueued.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ---------------------------------------------------------------- device side
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// f32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu)) return (x >> 16) | 0x40u;
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return x >> 16;
+}
+
+// f32 -> IEEE binary16 bits with round-to-nearest-even, overflow to infinity
+// and NaN quieted with the top payload bits kept: the rounding of the `half`
+// crate's f16::from_f32 that eredu-gguf/src/convert.rs:409-411 uses.  Done in
+// integer arithmetic so the result does not depend on the hardware mode bits.
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xffu) return sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u);
+    int e = static_cast<int>(exp) - 112;  // rebias 127 -> 15
+    if (e >= 0x1f) return sign | 0x7c00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        uint32_t m = man | 0x800000u;
+        uint32_t shift = static_cast<uint32_t>(14 - e);
+        uint32_t h = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (h & 1u))) h += 1u;
+        return sign | h;
+    }
+    uint32_t h = (static_cast<uint32_t>(e) << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+    return sign | h;
+}
+
+// Scalar parameter loads for each scale/activation element type.
+struct BF16T { typedef uint16_t storage; };
+struct F16T { typedef uint16_t storage; };
+struct F32T { typedef float storage; };
+
+template <typename T> __device__ __forceinline__ float load_param(const typename T::storage* p, int64_t i);
+template <> __device__ __forceinline__ float load_param<BF16T>(const uint16_t* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+template <> __device__ __forceinline__ float load_param<F16T>(const uint16_t* p, int64_t i) { return f16_bits_to_f32(p[i]); }
+template <> __device__ __forceinline__ float load_param<F32T>(const float* p, int64_t i) { return p[i]; }
+
+template <typename T> __device__ __forceinline__ void store_out(typename T::storage* p, int64_t i, float v);
+template <> __device__ __forceinline__ void store_out<BF16T>(uint16_t* p, int64_t i, float v) { p[i] = static_cast<uint16_t>(f32_to_bf16_bits(v)); }
+template <> __device__ __forceinline__ void store_out<F16T>(uint16_t* p, int64_t i, float v) { p[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
+template <> __device__ __forceinline__ void store_out<F32T>(float* p, int64_t i, float v) { p[i] = v; }
+
+}  // namespace eq

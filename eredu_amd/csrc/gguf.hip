@@ -1,0 +1,441 @@
+// GGML block dequant and convert on gfx950.
+//
+// Restates, per block and bit for bit, eredu-gguf/src/convert.rs:318-465
+// (convert_affine for Q4_0 / Q8_0 / Q4_K), AffineTensor::dequantize
+// (convert.rs:81-101) and the native decoders of
+// safemlx/src/native_quantization.rs:3445-3469 (Q4_K) and :3539-3542 (Q8_0).
+//
+// All kernels are HBM-bound byte work.  Q4_0 (18 B) and Q8_0 (34 B) blocks are
+// not 4-byte aligned, so a workgroup stages its 256 blocks through LDS with
+// 16-byte coalesced loads and each thread then decodes one block from LDS.
+// Q4_K superblocks (144 B) are 16-byte aligned and are read directly, one
+// thread per 32-value group.  Every product in these decoders is exact in f32
+// (an 11-bit f16 significand times a code of at most 8 bits), so each output
+// carries exactly one rounding, as on the reference's CPU.
+#include "eq_common.hpp"
+
+namespace eq {
+namespace {
+
+constexpr int kBlocksPerWG = 256;
+
+__device__ __forceinline__ uint32_t bswap16(uint32_t v) { return ((v & 0xffu) << 8) | ((v >> 8) & 0xffu); }
+
+// Four low nibbles of the bytes of x, compressed into 16 bits (byte i's low
+// nibble lands in bits 4i..4i+3): the 4-bit LSB-first pack of convert.rs:413-427
+// for codes taken byte by byte.
+__device__ __forceinline__ uint32_t lo_nibbles(uint32_t x) {
+    x &= 0x0f0f0f0fu;
+    x |= x >> 4;
+    return (x & 0xffu) | ((x >> 8) & 0xff00u);
+}
+__device__ __forceinline__ uint32_t hi_nibbles(uint32_t x) { return lo_nibbles(x >> 4); }
+
+// Copies `nb` blocks of `bytes` each (starting at block blk0) into LDS.
+// Full workgroups on a 16-byte-aligned payload use 16-byte loads; a ragged
+// tail uses 2-byte loads (block sizes here are even), so nothing past the
+// payload is ever read.
+template <int BYTES>
+__device__ __forceinline__ void stage_blocks(uint16_t* lds, const uint8_t* raw, int64_t blk0, int nb,
+                                             bool vec_ok) {
+    const uint8_t* src = raw + blk0 * BYTES;
+    if (vec_ok && nb == kBlocksPerWG) {
+        constexpr int kVec = kBlocksPerWG * BYTES / 16;
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+        uint4* d4 = reinterpret_cast<uint4*>(lds);
+        for (int i = threadIdx.x; i < kVec; i += blockDim.x) d4[i] = s4[i];
+    } else {
+        const uint16_t* s2 = reinterpret_cast<const uint16_t*>(src);
+        const int n2 = nb * BYTES / 2;
+        for (int i = threadIdx.x; i < n2; i += blockDim.x) lds[i] = s2[i];
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t lds_u32(const uint16_t* p) { return uint32_t(p[0]) | (uint32_t(p[1]) << 16); }
+
+// ------------------------------------------------------------- Q4_0 / Q8_0
+
+// Decodes one Q4_0 block from LDS: f16 d, and the 16 quant bytes as 4 words.
+template <bool BIG>
+__device__ __forceinline__ void q4_0_block(const uint16_t* b, uint32_t& d, uint32_t q[4]) {
+    d = BIG ? bswap16(b[0]) : b[0];
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = lds_u32(b + 1 + 2 * i);
+}
+
+template <bool BIG>
+__global__ __launch_bounds__(256) void q4_0_to_affine(const uint8_t* __restrict__ raw, int64_t nblocks,
+                                                      bool vec_ok, uint4* __restrict__ w,
+                                                      uint16_t* __restrict__ s, uint16_t* __restrict__ bias) {
+    __shared__ uint16_t lds[kBlocksPerWG * 18 / 2];
+    const int64_t blk0 = int64_t(blockIdx.x) * kBlocksPerWG;
+    const int nb = int(min<int64_t>(kBlocksPerWG, nblocks - blk0));
+    stage_blocks<18>(lds, raw, blk0, nb, vec_ok);
+    const int t = threadIdx.x;
+    if (t >= nb) return;
+    uint32_t d, q[4];
+    q4_0_block<BIG>(lds + t * 9, d, q);
+    const int64_t blk = blk0 + t;
+    // codes[0..16) = low nibbles, codes[16..32) = high nibbles (convert.rs:355-358)
+    w[blk] = make_uint4(lo_nibbles(q[0]) | (lo_nibbles(q[1]) << 16), lo_nibbles(q[2]) | (lo_nibbles(q[3]) << 16),
+                        hi_nibbles(q[0]) | (hi_nibbles(q[1]) << 16), hi_nibbles(q[2]) | (hi_nibbles(q[3]) << 16));
+    s[blk] = uint16_t(d);
+    bias[blk] = uint16_t(f32_to_f16_bits(-8.0f * f16_bits_to_f32(d)));  // convert.rs:352
+}
+
+template <bool BIG>
+__global__ __launch_bounds__(256) void q8_0_to_affine(const uint8_t* __restrict__ raw, int64_t nblocks,
+                                                      bool vec_ok, uint4* __restrict__ w,
+                                                      uint16_t* __restrict__ s, uint16_t* __restrict__ bias) {
+    __shared__ uint16_t lds[kBlocksPerWG * 34 / 2];
+    const int64_t blk0 = int64_t(blockIdx.x) * kBlocksPerWG;
+    const int nb = int(min<int64_t>(kBlocksPerWG, nblocks - blk0));
+    stage_blocks<34>(lds, raw, blk0, nb, vec_ok);
+    const int t = threadIdx.x;
+    if (t >= nb) return;
+    const uint16_t* b = lds + t * 17;
+    const uint32_t d = BIG ? bswap16(b[0]) : b[0];
+    uint32_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = lds_u32(b + 1 + 2 * i) ^ 0x80808080u;  // convert.rs:381
+    const int64_t blk = blk0 + t;
+    w[2 * blk] = make_uint4(q[0], q[1], q[2], q[3]);
+    w[2 * blk + 1] = make_uint4(q[4], q[5], q[6], q[7]);
+    s[blk] = uint16_t(d);
+    bias[blk] = uint16_t(f32_to_f16_bits(-128.0f * f16_bits_to_f32(d)));  // convert.rs:380
+}
+
+// Dense output: 32 consecutive values per thread.
+template <typename OUT>
+__device__ __forceinline__ void store32(typename OUT::storage* out, int64_t base, const float v[32]);
+template <>
+__device__ __forceinline__ void store32<BF16T>(uint16_t* out, int64_t base, const float v[32]) {
+    uint4* o = reinterpret_cast<uint4*>(out + base);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t p[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            p[j] = f32_to_bf16_bits(v[8 * i + 2 * j]) | (f32_to_bf16_bits(v[8 * i + 2 * j + 1]) << 16);
+        o[i] = make_uint4(p[0], p[1], p[2], p[3]);
+    }
+}
+template <>
+__device__ __forceinline__ void store32<F32T>(float* out, int64_t base, const float v[32]) {
+    float4* o = reinterpret_cast<float4*>(out + base);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+// Q4_0 dense: affine route only (Q4_0 has no native decoder, format.rs:423-428):
+// w = f32(d) * code + f32(f16(-8 d)).
+template <bool BIG, typename OUT>
+__global__ __launch_bounds__(256) void q4_0_dense(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
+                                                  typename OUT::storage* __restrict__ out) {
+    __shared__ uint16_t lds[kBlocksPerWG * 18 / 2];
+    const int64_t blk0 = int64_t(blockIdx.x) * kBlocksPerWG;
+    const int nb = int(min<int64_t>(kBlocksPerWG, nblocks - blk0));
+    stage_blocks<18>(lds, raw, blk0, nb, vec_ok);
+    const int t = threadIdx.x;
+    if (t >= nb) return;
+    uint32_t d, q[4];
+    q4_0_block<BIG>(lds + t * 9, d, q);
+    const float scale = f16_bits_to_f32(d);
+    const float bias = f16_bits_to_f32(f32_to_f16_bits(-8.0f * scale));
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t byte = (q[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        v[i] = scale * float(byte & 15u) + bias;
+        v[16 + i] = scale * float(byte >> 4) + bias;
+    }
+    store32<OUT>(out, (blk0 + t) * 32, v);
+}
+
+// Q8_0 dense.  Affine route: f32(d) * (q ^ 0x80) + f32(f16(-128 d));
+// native route: f32(d) * int8(q).  Identical unless -128 d overflows f16.
+template <bool BIG, bool NATIVE, typename OUT>
+__global__ __launch_bounds__(256) void q8_0_dense(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
+                                                  typename OUT::storage* __restrict__ out) {
+    __shared__ uint16_t lds[kBlocksPerWG * 34 / 2];
+    const int64_t blk0 = int64_t(blockIdx.x) * kBlocksPerWG;
+    const int nb = int(min<int64_t>(kBlocksPerWG, nblocks - blk0));
+    stage_blocks<34>(lds, raw, blk0, nb, vec_ok);
+    const int t = threadIdx.x;
+    if (t >= nb) return;
+    const uint16_t* b = lds + t * 17;
+    const uint32_t dbits = BIG ? bswap16(b[0]) : b[0];
+    const float d = f16_bits_to_f32(dbits);
+    const float bias = f16_bits_to_f32(f32_to_f16_bits(-128.0f * d));
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t pair = b[1 + i];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t byte = (pair >> (8 * h)) & 0xffu;
+            if (NATIVE)
+                v[2 * i + h] = d * float(int8_t(byte));
+            else
+                v[2 * i + h] = d * float(byte ^ 0x80u) + bias;
+        }
+    }
+    store32<OUT>(out, (blk0 + t) * 32, v);
+}
+
+// ------------------------------------------------------------------- Q4_K
+
+struct Q4KGroup {
+    float d, dmin;
+    uint32_t sc, m;
+    uint32_t q[8];  // the 32 quant bytes holding this group's nibbles
+};
+
+// One 32-value group g of a 144-byte superblock (convert.rs:439-465,
+// native_quantization.rs:3445-3469): header = d, dmin, 12 scale bytes; group g
+// takes the low (g even) or high (g odd) nibbles of quant bytes [(g/2)*32, +32).
+template <bool BIG>
+__device__ __forceinline__ Q4KGroup load_q4k_group(const uint8_t* __restrict__ raw, int64_t sb, int g, bool vec_ok) {
+    const uint8_t* p = raw + sb * 144;
+    uint32_t h[4], q[8];
+    if (vec_ok) {
+        const uint4 hv = *reinterpret_cast<const uint4*>(p);
+        const uint4 qa = *reinterpret_cast<const uint4*>(p + 16 + (g >> 1) * 32);
+        const uint4 qb = *reinterpret_cast<const uint4*>(p + 32 + (g >> 1) * 32);
+        h[0] = hv.x; h[1] = hv.y; h[2] = hv.z; h[3] = hv.w;
+        q[0] = qa.x; q[1] = qa.y; q[2] = qa.z; q[3] = qa.w;
+        q[4] = qb.x; q[5] = qb.y; q[6] = qb.z; q[7] = qb.w;
+    } else {
+        const uint16_t* p2 = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) h[i] = uint32_t(p2[2 * i]) | (uint32_t(p2[2 * i + 1]) << 16);
+        const uint16_t* q2 = p2 + 8 + (g >> 1) * 16;
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = uint32_t(q2[2 * i]) | (uint32_t(q2[2 * i + 1]) << 16);
+    }
+    Q4KGroup r;
+    const uint32_t dbits = BIG ? bswap16(h[0] & 0xffffu) : (h[0] & 0xffffu);
+    const uint32_t mbits = BIG ? bswap16(h[0] >> 16) : (h[0] >> 16);
+    r.d = f16_bits_to_f32(dbits);
+    r.dmin = f16_bits_to_f32(mbits);
+    // 12 scale bytes s[0..12) = bytes of h[1], h[2], h[3]; scale_min, convert.rs:429-438
+    auto sbyte = [&](int i) -> uint32_t { return (h[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu; };
+    if (g < 4) {
+        r.sc = sbyte(g) & 63u;
+        r.m = sbyte(g + 4) & 63u;
+    } else {
+        r.sc = (sbyte(g + 4) & 15u) | ((sbyte(g - 4) >> 6) << 4);
+        r.m = (sbyte(g + 4) >> 4) | ((sbyte(g) >> 6) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.q[i] = q[i];
+    return r;
+}
+
+template <bool BIG>
+__global__ __launch_bounds__(256) void q4k_to_affine(const uint8_t* __restrict__ raw, int64_t ngroups, bool vec_ok,
+                                                     uint4* __restrict__ w, uint16_t* __restrict__ s,
+                                                     uint16_t* __restrict__ bias) {
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= ngroups) return;
+    const int g = int(idx & 7);
+    const Q4KGroup r = load_q4k_group<BIG>(raw, idx >> 3, g, vec_ok);
+    uint32_t wd[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t a = r.q[2 * j], b = r.q[2 * j + 1];
+        wd[j] = (g & 1) ? (hi_nibbles(a) | (hi_nibbles(b) << 16)) : (lo_nibbles(a) | (lo_nibbles(b) << 16));
+    }
+    w[idx] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    s[idx] = uint16_t(f32_to_f16_bits(r.d * float(r.sc)));       // convert.rs:449
+    bias[idx] = uint16_t(f32_to_f16_bits(-r.dmin * float(r.m)));  // convert.rs:450
+}
+
+template <bool BIG, bool NATIVE, typename OUT>
+__global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw, int64_t ngroups, bool vec_ok,
+                                                 typename OUT::storage* __restrict__ out) {
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= ngroups) return;
+    const int g = int(idx & 7);
+    const Q4KGroup r = load_q4k_group<BIG>(raw, idx >> 3, g, vec_ok);
+    const int sh = (g & 1) * 4;
+    float v[32];
+    if (NATIVE) {
+        // d * sc * q - dmin * m, left to right (native_quantization.rs:3466)
+        const float ds = r.d * float(r.sc);
+        const float dm = r.dmin * float(r.m);
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = ds * float((r.q[i >> 2] >> (8 * (i & 3) + sh)) & 15u) - dm;
+    } else {
+        // f32(f16(d sc)) * q + f32(f16(-dmin m)) (convert.rs:81-101 on the q45k output)
+        const float scale = f16_bits_to_f32(f32_to_f16_bits(r.d * float(r.sc)));
+        const float bias = f16_bits_to_f32(f32_to_f16_bits(-r.dmin * float(r.m)));
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = scale * float((r.q[i >> 2] >> (8 * (i & 3) + sh)) & 15u) + bias;
+    }
+    store32<OUT>(out, idx * 32, v);
+}
+
+struct Geometry {
+    int values, bytes, bits;
+};
+
+bool geometry(int type, Geometry& g) {
+    switch (type) {  // eredu-gguf/src/format.rs:368-400, convert.rs:142-152
+    case EQ_GGML_Q4_0: g = {32, 18, 4}; return true;
+    case EQ_GGML_Q8_0: g = {32, 34, 8}; return true;
+    case EQ_GGML_Q4_K: g = {256, 144, 4}; return true;
+    default: return false;
+    }
+}
+
+// Shared argument checks of the two GGUF entry points (convert.rs:158-176,319-324).
+int validate(const uint8_t* raw, int64_t raw_len, int type, int64_t rows, int64_t cols, int endian,
+             Geometry& geo, int64_t& nblocks) {
+    if (!geometry(type, geo)) {
+        set_error("unsupported GGML tensor type " + std::to_string(type) + " (device path covers Q4_0, Q8_0, Q4_K)");
+        return 1;
+    }
+    if (endian != EQ_ENDIAN_LITTLE && endian != EQ_ENDIAN_BIG) {
+        set_error("invalid endian " + std::to_string(endian));
+        return 1;
+    }
+    if (rows <= 0 || cols <= 0) {
+        set_error("quantized scalar is invalid: rows and cols must be positive");
+        return 1;
+    }
+    if (cols % 32 != 0) {
+        set_error("last dimension is not divisible by group size 32");
+        return 1;
+    }
+    if (cols % geo.values != 0) {
+        set_error("row width " + std::to_string(cols) + " is not divisible by block length " +
+                  std::to_string(geo.values));
+        return 1;
+    }
+    if (rows > INT64_MAX / cols) {
+        set_error("tensor element count overflows");
+        return 1;
+    }
+    nblocks = rows * cols / geo.values;
+    if (raw_len != nblocks * geo.bytes) {
+        set_error("payload length does not match descriptor: got " + std::to_string(raw_len) + " bytes, expected " +
+                  std::to_string(nblocks * geo.bytes));
+        return 1;
+    }
+    if (!raw) {
+        set_error("null payload pointer");
+        return 1;
+    }
+    return 0;
+}
+
+}  // namespace
+}  // namespace eq
+
+using namespace eq;
+
+extern "C" int eq_gguf_convert_affine(uint32_t* weights, uint16_t* scales, uint16_t* biases, const uint8_t* raw,
+                                      int64_t raw_len, int ggml_type, int64_t rows, int64_t cols, int endian,
+                                      eq_stream_t stream) {
+    clear_error();
+    Geometry geo;
+    int64_t nblocks;
+    if (validate(raw, raw_len, ggml_type, rows, cols, endian, geo, nblocks)) return 1;
+    if (!weights || !scales || !biases) {
+        set_error("null output pointer");
+        return 1;
+    }
+    if (!aligned(weights, 16) || !aligned(scales, 2) || !aligned(biases, 2)) {
+        set_error("weights must be 16-byte aligned and scales/biases 2-byte aligned");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool vec_ok = aligned(raw, 16);
+    const bool big = endian == EQ_ENDIAN_BIG;
+    uint4* w4 = reinterpret_cast<uint4*>(weights);
+    if (ggml_type == EQ_GGML_Q4_K) {
+        const int64_t ngroups = nblocks * 8;
+        const dim3 grid(unsigned((ngroups + 255) / 256));
+        if (big)
+            q4k_to_affine<true><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, w4, scales, biases);
+        else
+            q4k_to_affine<false><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, w4, scales, biases);
+    } else {
+        const dim3 grid(unsigned((nblocks + kBlocksPerWG - 1) / kBlocksPerWG));
+        if (ggml_type == EQ_GGML_Q4_0) {
+            if (big)
+                q4_0_to_affine<true><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+            else
+                q4_0_to_affine<false><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+        } else {
+            if (big)
+                q8_0_to_affine<true><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+            else
+                q8_0_to_affine<false><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+        }
+    }
+    return check_launch("gguf convert_affine");
+}
+
+namespace {
+template <typename OUT>
+void launch_dense(int type, bool big, bool native, const uint8_t* raw, int64_t nblocks, bool vec_ok,
+                  typename OUT::storage* out, hipStream_t st) {
+    if (type == EQ_GGML_Q4_K) {
+        const int64_t ngroups = nblocks * 8;
+        const dim3 grid(unsigned((ngroups + 255) / 256));
+        if (big) {
+            if (native) q4k_dense<true, true, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
+            else q4k_dense<true, false, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
+        } else {
+            if (native) q4k_dense<false, true, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
+            else q4k_dense<false, false, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
+        }
+        return;
+    }
+    const dim3 grid(unsigned((nblocks + kBlocksPerWG - 1) / kBlocksPerWG));
+    if (type == EQ_GGML_Q4_0) {
+        if (big) q4_0_dense<true, OUT><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, out);
+        else q4_0_dense<false, OUT><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, out);
+    } else {
+        if (big) {
+            if (native) q8_0_dense<true, true, OUT><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, out);
+            else q8_0_dense<true, false, OUT><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, out);
+        } else {
+            if (native) q8_0_dense<false, true, OUT><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, out);
+            else q8_0_dense<false, false, OUT><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, out);
+        }
+    }
+}
+}  // namespace
+
+extern "C" int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t rows,
+                                  int64_t cols, int endian, int definition, int out_dtype, eq_stream_t stream) {
+    clear_error();
+    Geometry geo;
+    int64_t nblocks;
+    if (validate(raw, raw_len, ggml_type, rows, cols, endian, geo, nblocks)) return 1;
+    if (definition != EQ_DEQUANT_AFFINE && definition != EQ_DEQUANT_NATIVE) {
+        set_error("invalid dequant definition " + std::to_string(definition));
+        return 1;
+    }
+    if (out_dtype != EQ_DTYPE_BF16 && out_dtype != EQ_DTYPE_F32) {
+        set_error("dense GGUF output must be bf16 or f32");
+        return 1;
+    }
+    if (!out || !aligned(out, 16)) {
+        set_error("output must be a non-null 16-byte aligned pointer");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool vec_ok = aligned(raw, 16);
+    const bool big = endian == EQ_ENDIAN_BIG;
+    const bool native = definition == EQ_DEQUANT_NATIVE;
+    if (out_dtype == EQ_DTYPE_BF16)
+        launch_dense<BF16T>(ggml_type, big, native, raw, nblocks, vec_ok, static_cast<uint16_t*>(out), st);
+    else
+        launch_dense<F32T>(ggml_type, big, native, raw, nblocks, vec_ok, static_cast<float*>(out), st);
+    return check_launch("gguf dequantize");
+}

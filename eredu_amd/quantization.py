@@ -1,0 +1,241 @@
+"""Host-side mirror of safemlx's quantization operators on the gfx950 kernels.
+
+Names, defaults, argument meaning and error behaviour follow
+``safemlx/src/ops/quantization.rs`` (the drop-in boundary eredu's
+``QuantizedLinear`` calls) and ``safemlx/src/nn/quantized.rs``.  Tensors are
+torch tensors on the GPU (PyTorch is used only for device memory and streams);
+all arithmetic runs in the HIP library through the C ABI.  Packed weights are
+u32 words; torch.int32 / torch.uint32 tensors are accepted as their bit
+containers.
+"""
+from __future__ import annotations
+
+import enum
+from typing import Optional
+
+import torch
+
+from . import _native
+from ._native import EreduError, check
+
+DEFAULT_GROUP_SIZE = 64  # safemlx/src/ops/quantization.rs:11
+DEFAULT_BITS = 4  # safemlx/src/ops/quantization.rs:12
+
+_DTYPE_CODE = {
+    torch.float32: _native.EQ_DTYPE_F32,
+    torch.float16: _native.EQ_DTYPE_F16,
+    torch.bfloat16: _native.EQ_DTYPE_BF16,
+}
+_WORD_DTYPES = (torch.int32, getattr(torch, "uint32", torch.int32))
+
+
+class QuantizationMode(enum.Enum):
+    """safemlx/src/ops/quantization.rs:16-46."""
+
+    Affine = "affine"
+    MxFp4 = "mxfp4"
+
+    def has_biases(self) -> bool:
+        return self is QuantizationMode.Affine
+
+    def validate(self, group_size: int, bits: int) -> None:
+        if self is QuantizationMode.MxFp4 and (group_size != 32 or bits != 4):
+            raise EreduError(
+                f"MXFP4 requires group_size=32 and bits=4, got group_size={group_size} bits={bits}"
+            )
+
+
+def quantized_packed_dimension(dimension: int, bits: int) -> int:
+    """Number of u32 words per packed row (safemlx/src/ops/quantization.rs:62-64)."""
+    return dimension * bits // 32
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise EreduError(f"{what} must be float32, float16 or bfloat16, got {t.dtype}") from None
+
+
+def _require_device(*tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise EreduError("all arrays must live on the GPU (the library has no host path)")
+
+
+def _words(w: torch.Tensor) -> torch.Tensor:
+    if w.dtype not in _WORD_DTYPES:
+        raise EreduError(f"quantized weights must be packed u32 words, got {w.dtype}")
+    return w
+
+
+def quantized_matmul_with_mode(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    biases: Optional[torch.Tensor],
+    transpose: bool,
+    group_size: int,
+    bits: int,
+    mode: QuantizationMode = QuantizationMode.Affine,
+) -> torch.Tensor:
+    """Quantized matmul with an explicit encoding
+    (safemlx/src/ops/quantization.rs:190-226; C ABI: eq_quantized_matmul).
+
+    transpose=True : w [N, K*bits/32], scales/biases [N, K/gs], y = x @ W^T.
+    transpose=False: w [K, N*bits/32], scales/biases [K, N/gs], y = x @ W.
+    x [..., K] -> y [..., N] in x's dtype.
+    """
+    mode.validate(group_size, bits)
+    if mode is not QuantizationMode.Affine:
+        raise EreduError("only affine quantization is implemented on the device path")
+    _require_device(x, w, scales, biases)
+    w = _words(w)
+    if w.dim() != 2 or scales.dim() != 2:
+        raise EreduError("w and scales must be 2-D")
+    if bits not in (2, 3, 4, 5, 6, 8):
+        raise EreduError(f"bits must be one of 2, 3, 4, 5, 6, 8, got {bits}")
+    if transpose:
+        N = w.shape[0]
+        K = w.shape[1] * 32 // bits
+    else:
+        K = w.shape[0]
+        N = w.shape[1] * 32 // bits
+    if x.shape[-1] != K:
+        raise EreduError(
+            f"shapes {tuple(x.shape)} and {tuple(w.shape)} are incompatible for quantized matmul "
+            f"(x's last dimension must be {K})"
+        )
+    packed_dim = K if transpose else N
+    if group_size <= 0 or packed_dim % group_size != 0:
+        raise EreduError(f"the quantized dimension {packed_dim} is not divisible by group_size {group_size}")
+    expect_scales = (w.shape[0], packed_dim // group_size)
+    if tuple(scales.shape) != expect_scales:
+        raise EreduError(f"scales has shape {tuple(scales.shape)}, expected {expect_scales}")
+    if biases is not None:
+        if tuple(biases.shape) != expect_scales or biases.dtype != scales.dtype:
+            raise EreduError("biases must match scales in shape and dtype")
+    x_code = _dtype_code(x, "x")
+    s_code = _dtype_code(scales, "scales")
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    w = w.contiguous()
+    scales = scales.contiguous()
+    biases = biases.contiguous() if biases is not None else None
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    check(
+        _native.lib().eq_quantized_matmul(
+            y.data_ptr(), x2.data_ptr(), w.data_ptr(), scales.data_ptr(),
+            biases.data_ptr() if biases is not None else None,
+            M, N, K, bool(transpose), int(group_size), int(bits), mode.value.encode(), x_code, s_code, _stream(),
+        )
+    )
+    return y.reshape(*x.shape[:-1], N)
+
+
+def quantized_matmul(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    biases: Optional[torch.Tensor] = None,
+    transpose: bool = False,
+    group_size: int = DEFAULT_GROUP_SIZE,
+    bits: int = DEFAULT_BITS,
+) -> torch.Tensor:
+    """Affine quantized matmul with safemlx's defaults (transpose=False, gs 64,
+    bits 4; safemlx/src/ops/quantization.rs:165-184)."""
+    return quantized_matmul_with_mode(x, w, scales, biases, transpose, group_size, bits, QuantizationMode.Affine)
+
+
+def dequantize_with_mode(
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    biases: Optional[torch.Tensor],
+    group_size: int,
+    bits: int,
+    mode: QuantizationMode = QuantizationMode.Affine,
+    dtype: Optional[torch.dtype] = None,
+) -> torch.Tensor:
+    """w_hat = scales * q + biases in the scales' dtype unless ``dtype`` is given
+    (safemlx/src/ops/quantization.rs:256-289; C ABI: eq_dequantize)."""
+    mode.validate(group_size, bits)
+    if mode is not QuantizationMode.Affine:
+        raise EreduError("only affine quantization is implemented on the device path")
+    _require_device(w, scales, biases)
+    w = _words(w).contiguous()
+    if w.dim() != 2:
+        raise EreduError("w must be 2-D")
+    rows = w.shape[0]
+    cols = w.shape[1] * 32 // bits
+    if cols % group_size != 0 or tuple(scales.shape) != (rows, cols // group_size):
+        raise EreduError(f"scales has shape {tuple(scales.shape)}, expected {(rows, cols // group_size)}")
+    if biases is not None and (tuple(biases.shape) != tuple(scales.shape) or biases.dtype != scales.dtype):
+        raise EreduError("biases must match scales in shape and dtype")
+    out_dtype = dtype or scales.dtype
+    out = torch.empty((rows, cols), dtype=out_dtype, device=w.device)
+    scales = scales.contiguous()
+    biases = biases.contiguous() if biases is not None else None
+    check(
+        _native.lib().eq_dequantize(
+            out.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr() if biases is not None else None,
+            rows, cols, int(group_size), int(bits), mode.value.encode(), _dtype_code(scales, "scales"),
+            _DTYPE_CODE[out_dtype], _stream(),
+        )
+    )
+    return out
+
+
+def dequantize(
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    biases: Optional[torch.Tensor] = None,
+    group_size: int = DEFAULT_GROUP_SIZE,
+    bits: int = DEFAULT_BITS,
+) -> torch.Tensor:
+    """safemlx/src/ops/quantization.rs:228-254."""
+    return dequantize_with_mode(w, scales, biases, group_size, bits, QuantizationMode.Affine)
+
+
+class QuantizedLinear:
+    """Affine quantized linear layer (safemlx/src/nn/quantized.rs:582-615,787-835):
+    forward = quantized_matmul(x, weight, scales, biases, transpose=True) + bias."""
+
+    def __init__(
+        self,
+        weight: torch.Tensor,
+        scales: torch.Tensor,
+        biases: Optional[torch.Tensor],
+        group_size: int = DEFAULT_GROUP_SIZE,
+        bits: int = DEFAULT_BITS,
+        bias: Optional[torch.Tensor] = None,
+        mode: QuantizationMode = QuantizationMode.Affine,
+    ):
+        self.weight = weight
+        self.scales = scales
+        self.biases = biases
+        self.group_size = group_size
+        self.bits = bits
+        self.bias = bias
+        self.mode = mode
+
+    @property
+    def output_dims(self) -> int:
+        return self.weight.shape[0]
+
+    @property
+    def input_dims(self) -> int:
+        return self.weight.shape[1] * 32 // self.bits
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        y = quantized_matmul_with_mode(
+            x, self.weight, self.scales, self.biases, True, self.group_size, self.bits, self.mode
+        )
+        if self.bias is not None:
+            y = y + self.bias
+        return y
+
+    __call__ = forward

@@ -1,0 +1,145 @@
+"""The C-ABI boundary on the CPU: the library loads, exports every entry point
+declared in include/eredu_hip.h, and rejects bad arguments with a status and
+a thread-local message before anything is launched (no compute here)."""
+import ctypes
+import os
+import re
+import subprocess
+import threading
+
+import pytest
+
+from eredu_amd import _native
+from eredu_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "eredu_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(eq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    assert declared_functions() == sorted(
+        ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_dequantize",
+         "eq_gguf_convert_affine", "eq_gguf_dequantize"]
+    )
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(LIB_PATH), "build the library first (python -m eredu_amd.build)"
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (eq_[a-z0-9_]+)", out))
+    for name in declared_functions():
+        assert name in exported, name
+    # and the ctypes table covers them all
+    assert set(_native.SIGNATURES) == set(declared_functions())
+
+
+def test_header_compiles_as_c():
+    src = f'#include "{HEADER}"\nint (*f)(void) = eq_version;\nint main(void) {{ return f != 0; }}\n'
+    res = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-x", "c", "-fsyntax-only", "-"],
+                         input=src, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+
+
+L = _native.lib()
+
+
+def call_qmm(**kw):
+    args = dict(y=1, x=1, w=1, s=1, b=None, M=1, N=16, K=64, transpose=True, gs=64, bits=4, mode=b"affine",
+                xd=2, sd=2)
+    args.update(kw)
+    return L.eq_quantized_matmul(args["y"], args["x"], args["w"], args["s"], args["b"], args["M"], args["N"],
+                                 args["K"], args["transpose"], args["gs"], args["bits"], args["mode"], args["xd"],
+                                 args["sd"], None)
+
+
+@pytest.mark.parametrize(
+    "kw,needle",
+    [
+        (dict(gs=48), "group_size must be 32, 64 or 128"),
+        (dict(bits=3), "bits must be 2, 4 or 8"),
+        (dict(K=96), "not divisible by group_size"),
+        (dict(transpose=False, N=40), "not divisible by group_size"),
+        (dict(mode=b"mxfp4"), "mxfp4"),
+        (dict(mode=b"nf4"), "invalid quantization mode"),
+        (dict(xd=7), "invalid dtype"),
+        (dict(N=0), "invalid shape"),
+        (dict(y=None), "null pointer"),
+    ],
+)
+def test_quantized_matmul_rejects(kw, needle):
+    assert call_qmm(**kw) != 0
+    assert needle in L.eq_last_error().decode()
+
+
+def test_zero_rows_is_a_no_op():
+    assert call_qmm(M=0, y=None, x=None) != 0  # null pointers are still rejected
+    assert call_qmm(M=0) == 0
+    assert L.eq_last_error().decode() == ""
+
+
+def test_error_message_is_thread_local():
+    assert call_qmm(gs=48) != 0
+    seen = {}
+
+    def other():
+        seen["before"] = L.eq_last_error().decode()
+        call_qmm(bits=3)
+        seen["after"] = L.eq_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["before"] == ""
+    assert "bits" in seen["after"]
+    assert "group_size" in L.eq_last_error().decode()
+
+
+@pytest.mark.parametrize(
+    "args,needle",
+    [
+        (dict(ty=3), "unsupported GGML tensor type"),
+        (dict(cols=48), "not divisible by group size 32"),
+        (dict(cols=288, ty=12), "not divisible by block length 256"),
+        (dict(raw_len=17), "payload length does not match descriptor"),
+        (dict(endian=5), "invalid endian"),
+    ],
+)
+def test_gguf_convert_rejects(args, needle):
+    a = dict(ty=2, rows=2, cols=64, raw_len=None, endian=0)
+    a.update(args)
+    if a["raw_len"] is None:
+        vals, nbytes = {2: (32, 18), 8: (32, 34), 12: (256, 144)}.get(a["ty"], (32, 18))
+        a["raw_len"] = a["rows"] * a["cols"] // vals * nbytes
+    buf = ctypes.create_string_buffer(64)
+    ptr = ctypes.cast(buf, ctypes.c_void_p)
+    rc = L.eq_gguf_convert_affine(ptr, ptr, ptr, ptr, a["raw_len"], a["ty"], a["rows"], a["cols"], a["endian"], None)
+    assert rc != 0
+    assert needle in L.eq_last_error().decode()
+
+
+def test_gguf_dequant_rejects_bad_definition_and_dtype():
+    buf = ctypes.create_string_buffer(4096)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    aligned = (p.value + 15) // 16 * 16
+    assert L.eq_gguf_dequantize(aligned, aligned, 36, 2, 2, 32, 0, 9, 2, None) != 0
+    assert "definition" in L.eq_last_error().decode()
+    assert L.eq_gguf_dequantize(aligned, aligned, 36, 2, 2, 32, 0, 0, 1, None) != 0
+    assert "bf16 or f32" in L.eq_last_error().decode()
+
+
+def test_host_mirror_fails_loudly_without_gpu_tensors():
+    import torch
+
+    from eredu_amd import EreduError, quantized_matmul
+
+    x = torch.zeros(1, 64, dtype=torch.bfloat16)
+    w = torch.zeros(16, 8, dtype=torch.int32)
+    s = torch.zeros(16, 1, dtype=torch.bfloat16)
+    with pytest.raises(EreduError, match="GPU"):
+        quantized_matmul(x, w, s, s, transpose=True)

@@ -1,0 +1,154 @@
+"""Parity of the HIP quantized matmul (qmv / qmm / general kernels) with the
+fp64 oracle, through the C ABI (via the eredu_amd host mirror).
+
+Tolerance (written here, as the rule the north star states): elementwise
+|y - y_ref| <= 1e-2 * RMS(y_ref) + 1/2 ulp_bf16(y_ref) for bf16 outputs
+(the half-ulp is the unavoidable rounding of the bf16 result), and the
+strict |y - y_ref| <= 1e-2 * RMS(y_ref) for f32 outputs.  y_ref is the exact
+(f64) product of the same packed inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from eredu_amd import EreduError, QuantizedLinear, dequantize_with_mode, quantized_matmul, quantized_matmul_with_mode
+from oracle import oracle as orc
+from tests.fixtures import (dev_bf16, dev_param, dev_words, host_bits16, host_f32, synthetic_linear,
+                            synthetic_x)
+
+pytestmark = pytest.mark.gpu
+
+LLAMA_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+
+
+def run_case(M, N, K, gs, bits, sdt=orc.BF16, xdt=orc.BF16, seed=0, transpose=True, biases=True):
+    print(f"[case] M={M} N={N} K={K} gs={gs} bits={bits} sdt={sdt} xdt={xdt} transpose={transpose}", flush=True)
+    if transpose:
+        w, s, b = synthetic_linear(N, K, gs, bits, seed, scale_dtype=sdt)
+    else:
+        w, s, b = synthetic_linear(K, N, gs, bits, seed, scale_dtype=sdt)
+    if not biases:
+        b = None
+    xb = synthetic_x(M, K, seed + 1)
+    if xdt == orc.BF16:
+        x_host, xd = xb, dev_bf16(xb)
+    else:
+        xf = orc.bf16_bits_to_f32(xb)
+        if xdt == orc.F16:
+            x_host = xf.astype(np.float16).view(np.uint16)
+        else:
+            x_host = xf
+        xd = dev_param(x_host, xdt)
+    y = quantized_matmul_with_mode(xd, dev_words(w), dev_param(s, sdt), None if b is None else dev_param(b, sdt),
+                                   transpose, gs, bits)
+    torch.cuda.synchronize()
+    y_ref = orc.quantized_matmul_f64(x_host, xdt, w, s, b, sdt, transpose, gs, bits, N, K)
+    ok, worst, rms = orc.matmul_within_tolerance(host_f32(y), y_ref, out_is_bf16=(xdt != orc.F32))
+    assert y.shape == (M, N)
+    assert ok, f"max|err|/RMS = {worst:.3e} (RMS {rms:.3f})"
+    return worst
+
+
+@pytest.mark.parametrize("N,K", LLAMA_SHAPES)
+@pytest.mark.parametrize("M", [1, 8])
+def test_qmv_llama_shapes(cuda, M, N, K):
+    run_case(M, N, K, 64, 4, seed=N + K + M)
+
+
+@pytest.mark.parametrize("M", list(range(1, 17)))
+def test_qmv_every_small_batch(cuda, M):
+    run_case(M, 256, 1024, 64, 4, seed=M)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("sdt", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("M", [1, 5])
+def test_qmv_contract_grid(cuda, bits, gs, sdt, M):
+    run_case(M, 128, 2048, gs, bits, sdt=sdt, seed=bits * gs + M)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M", [17, 128, 300])
+def test_qmm_grid(cuda, bits, gs, M):
+    run_case(M, 256, 1024, gs, bits, seed=bits + gs + M)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_prefill_shape(cuda, bits):
+    run_case(512, 4096, 4096, 64, bits, seed=bits)
+
+
+def test_qmm_f16_scales(cuda):
+    run_case(64, 256, 512, 32, 4, sdt=orc.F16, seed=3)
+
+
+@pytest.mark.parametrize("xdt", [orc.F32, orc.F16])
+@pytest.mark.parametrize("M", [1, 33])
+def test_general_activation_dtypes(cuda, xdt, M):
+    # f32 activations give f32 output and must meet the strict 1e-2*RMS rule
+    run_case(M, 64, 512, 64, 4, xdt=xdt, seed=M)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_general_bits_and_f32_scales(cuda, bits):
+    run_case(3, 48, 256, 64, bits, sdt=orc.F32, seed=bits)
+
+
+@pytest.mark.parametrize("M", [1, 7, 20])
+def test_transpose_false(cuda, M):
+    # W stored [K, N] packed along N (quantized KV attention, tensor.rs:133-140)
+    run_case(M, 128, 192, 64, 4, transpose=False, seed=M)
+
+
+def test_ragged_n_and_no_biases(cuda):
+    run_case(2, 40, 256, 32, 4, seed=9, biases=False)   # N % 16 != 0 -> general kernel
+    run_case(2, 64, 256, 32, 4, seed=10, biases=False)  # qmv without biases
+    run_case(40, 256, 256, 64, 4, seed=11, biases=False)  # qmm without biases
+
+
+def test_all_zero_codes_give_bias_term(cuda):
+    N, K, gs = 64, 512, 64
+    s = orc.f32_to_bf16_bits(np.full((N, K // gs), 0.5, np.float32))
+    b = orc.f32_to_bf16_bits(np.random.default_rng(0).normal(0, 0.1, (N, K // gs)).astype(np.float32))
+    w = np.zeros((N, K // 8), np.uint32)
+    for M in (1, 9, 64):
+        xb = synthetic_x(M, K, M)
+        y = quantized_matmul(dev_bf16(xb), dev_words(w), dev_bf16(s), dev_bf16(b), transpose=True, group_size=gs)
+        xs = orc.bf16_bits_to_f32(xb).astype(np.float64).reshape(M, K // gs, gs).sum(-1)
+        ref = xs @ orc.bf16_bits_to_f32(b).astype(np.float64).T
+        assert orc.matmul_within_tolerance(host_f32(y), ref, True)[0]
+
+
+def test_batch_dims_flatten_into_m(cuda):
+    N, K = 128, 256
+    w, s, b = synthetic_linear(N, K, 64, 4, 1)
+    xb = synthetic_x(6, K, 2)
+    lin = QuantizedLinear(dev_words(w), dev_bf16(s), dev_bf16(b), 64, 4)
+    y = lin(dev_bf16(xb).view(2, 3, K))
+    assert y.shape == (2, 3, N)
+    y_ref = orc.quantized_matmul_f64(xb, orc.BF16, w, s, b, orc.BF16, True, 64, 4, N, K)
+    assert orc.matmul_within_tolerance(host_f32(y).reshape(6, N), y_ref, True)[0]
+
+
+def test_dequantize_bit_exact(cuda):
+    for bits, gs, sdt in [(4, 64, orc.BF16), (8, 32, orc.F16), (2, 128, orc.F32), (4, 32, orc.F16)]:
+        rows, cols = 96, 512
+        w, s, b = synthetic_linear(rows, cols, gs, bits, bits + gs, scale_dtype=sdt)
+        ref = orc.affine_dequant_f32(w, s, b, sdt, rows, cols, gs, bits)
+        out = dequantize_with_mode(dev_words(w), dev_param(s, sdt), dev_param(b, sdt), gs, bits, dtype=torch.float32)
+        assert np.array_equal(out.cpu().numpy(), ref)
+        out16 = dequantize_with_mode(dev_words(w), dev_param(s, sdt), dev_param(b, sdt), gs, bits,
+                                     dtype=torch.bfloat16)
+        assert np.array_equal(host_bits16(out16), orc.f32_to_bf16_bits(ref))
+
+
+def test_errors_surface_as_exceptions(cuda):
+    x = torch.zeros(1, 96, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(16, 12, dtype=torch.int32, device="cuda")
+    s = torch.zeros(16, 2, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(EreduError, match="group_size"):
+        quantized_matmul(x, w, s, s, transpose=True, group_size=48)
+    with pytest.raises(EreduError, match="incompatible"):
+        quantized_matmul(x[:, :64], w, s, s, transpose=True, group_size=48)
