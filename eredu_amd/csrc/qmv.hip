@@ -1,59 +1,60 @@
-// Decode-shaped quantized matmul (M <= 16, bf16 activations, transpose = true)
+// Decode-shaped quantized matmul (small M, bf16 activations, transpose = true)
 // on gfx950 matrix cores.
 //
 // y[m, n] = sum_g s[n,g] * sum_{k in g} x[m,k] q[n,k] + b[n,g] * sum_{k in g} x[m,k]
 // (the affine contract of safemlx/src/ops/quantization.rs:190-226 with W = [N, K]).
 //
-// Layout of the work.  A workgroup owns 16 output features (rows of W) and its
-// waves split K by whole quantization groups.  Each wave runs
-// v_mfma_f32_16x16x32_bf16 with A = activations (16 rows, M of them real) and
-// B = codes of the 16 rows, one MFMA per 32 codes:
-//   lane l: column n = l % 16, k-slot block kq = l / 16.
-//   Per group a lane loads the gs/4 consecutive codes of row n starting at
-//   kq*gs/4 (a single 4/8/16/32-byte load), so every MFMA sums codes of one
-//   group only and the per-group scale can be applied to its result.
-// 4-bit codes become bf16 (128 + q) with one byte permute and one and-or per
-// pair; 8-bit codes go through v_cvt_f32_ubyte.  A second MFMA against a
-// constant all-ones B gives sum_k x per group in the same accumulator layout,
-// which carries both the bias term and the removal of the +128 offset.
-// Per group each lane then does acc += s * t + (b - 128 s) * xs in f32.
-// Waves reduce through LDS; the result is rounded once to bf16.
+// The weight stream is the whole cost, so the layout of the work is chosen for
+// it.  A workgroup owns 16 output features (rows of W); its waves split K into
+// "spans".  In one span every lane issues ONE 16-byte load of packed codes:
+// lane l reads row n = l % 16 at byte offset 16 * (l / 16) of the span, so a
+// wave load covers 64 contiguous bytes of each of 16 rows (128 codes per row
+// at 4 bits, 64 at 8 bits).  The codes then feed v_mfma_f32_16x16x32_bf16
+// directly in the lane layout they were loaded in: B[k][n] = codes of row n,
+// with the k-slot block of lane l equal to l / 16.
 //
-// The weight stream is read exactly once with coalesced loads; activations
-// (at most 16 x K bf16) stay in L1/L2.
+// Per-group scales must be applied to per-group partial sums, but one MFMA
+// sums 32 k-slots that straddle 2 or 4 quantization groups (when a span holds
+// P = span / gs > 1 groups).  The A operand separates them at no cost: its 16
+// rows are split into P blocks of 16/P rows, block p carrying the activations
+// of the k-slots that belong to group p of the span and zeros elsewhere.  Row
+// (p, m) of the MFMA result is then the group-p partial dot product of
+// activation row m, and lanes of the result own exactly one group each.  This
+// limits one launch to M <= 16/P activation rows; larger M is split into
+// chunks by the launcher.
+//
+// 4-bit codes become bf16 (128 + q) with one byte permute and one and-or per
+// pair; 8-bit codes go through v_cvt_f32_ubyte.  A second MFMA against an
+// all-ones B gives sum_k x per group in the same layout, which carries both
+// the bias term and the removal of the +128 offset:
+//   acc += s * t + (b - 128 s) * xs         (f32, per span)
+// Waves combine through LDS; the result is rounded once to bf16.
+#include <atomic>
+
 #include "eq_common.hpp"
 
 namespace eq {
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int N> struct WordVec;
-template <> struct WordVec<1> {
-    static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* o) { o[0] = *p; }
+// Loop-invariant constants kept in VGPRs (opaque to the optimiser), so that
+// (p & mask) | bias compiles to one v_and_or_b32: on gfx9 a VOP3 instruction
+// takes no literal operands.
+struct UnpackConsts {
+    uint32_t nib_mask;  // 0x000f000f
+    uint32_t bf16_128;  // 0x43004300: bf16 0x43XX = 128 + XX for XX < 128
 };
-template <> struct WordVec<2> {
-    static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* o) {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(p);
-        o[0] = v[0]; o[1] = v[1];
-    }
-};
-template <> struct WordVec<4> {
-    static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* o) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
-        o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
-    }
-};
-template <> struct WordVec<8> {
-    static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* o) {
-        WordVec<4>::load(p, o);
-        WordVec<4>::load(p + 4, o + 4);
-    }
-};
+__device__ __forceinline__ UnpackConsts make_unpack_consts() {
+    UnpackConsts c;
+    asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(c.nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.bf16_128));
+    return c;
+}
 
 // 8 consecutive 4-bit codes (one word, LSB first) -> 8 bf16 values 128 + q,
 // in k order: pair i holds codes 2i (low half) and 2i+1 (high half).
-__device__ __forceinline__ bf16x8 unpack4_bf16_offset128(uint32_t w) {
+// 9 VALU ops: one shift, four byte permutes, four and-or.
+__device__ __forceinline__ bf16x8 unpack4_bf16_offset128(uint32_t w, const UnpackConsts& c) {
     const uint32_t t = w >> 4;
     u32x4 p;
     // byte 0 <- w.byte i (low nibble = code 2i), byte 2 <- t.byte i (low nibble = code 2i+1)
@@ -62,7 +63,7 @@ __device__ __forceinline__ bf16x8 unpack4_bf16_offset128(uint32_t w) {
     p[2] = __builtin_amdgcn_perm(t, w, 0x0c060c02u);
     p[3] = __builtin_amdgcn_perm(t, w, 0x0c070c03u);
 #pragma unroll
-    for (int i = 0; i < 4; i++) p[i] = (p[i] & 0x000f000fu) | 0x43004300u;  // bf16 0x43XX = 128 + X
+    for (int i = 0; i < 4; i++) p[i] = (p[i] & c.nib_mask) | c.bf16_128;
     return __builtin_bit_cast(bf16x8, p);
 }
 
@@ -83,114 +84,804 @@ __device__ __forceinline__ bf16x8 unpack8_bf16(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(bf16x8, p);
 }
 
-constexpr int kQmvMaxWaves = 16;
-constexpr int kQmvUnroll = 4;
+#ifndef EQ_QMV_WAVES
+#define EQ_QMV_WAVES 8
+#endif
+#ifndef EQ_QMV_UNROLL
+#define EQ_QMV_UNROLL 4
+#endif
+#ifndef EQ_QMV_SPANS_PER_WAVE
+#define EQ_QMV_SPANS_PER_WAVE 8
+#endif
+constexpr int kQmvMaxWaves = EQ_QMV_WAVES;            // waves per workgroup (upper bound)
+constexpr int kQmvUnroll = EQ_QMV_UNROLL;             // spans per load block
+constexpr int kQmvSpansPerWave = EQ_QMV_SPANS_PER_WAVE;  // target spans per wave
 
+template <int BITS, int GS>
+struct QmvGeom {
+    static constexpr int CPL = 128 / BITS;                  // codes per lane per span (16 bytes)
+    static constexpr int SPAN = 4 * CPL;                    // codes per row per span
+    static constexpr int P = SPAN > GS ? SPAN / GS : 1;     // quantization groups per span
+    static constexpr int MB = 16 / P;                       // A-operand rows per group block
+    static constexpr int STEPS = CPL / 8;                   // MFMAs per span
+    static constexpr int SPAN_WORDS = SPAN * BITS / 32;     // = 16
+};
+
+// Buffer resource (V#) of a raw byte range: loads through it are range-checked
+// by the hardware, and an offset at or past `bytes` reads as zero.  Buffer
+// loads are also ordered against scheduling barriers, which plain loads from
+// read-only pointers are not.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+// A wave-uniform 1 that the compiler cannot see through.  `if (opaque_one())`
+// puts the guarded code in a basic block of its own: instruction selection
+// and the machine scheduler work per block, so a block of prefetch loads
+// placed before it is issued before it (within one block the schedulers
+// would sink the loads down to their uses and serialise the pipeline).
+__device__ __forceinline__ int opaque_one() {
+    int v;
+    asm volatile("s_mov_b32 %0, 1" : "=s"(v));
+    return v;
+}
+
+// An offset past every buffer this file builds (all are < 2^31 bytes), leaving
+// room for the immediate offsets added to it.
+constexpr uint32_t kOutOfRange = 0xC0000000u;
+
+// Raw 16-bit parameter bits -> f32 (bf16 or f16 scales/biases).
+template <typename ST> __device__ __forceinline__ float param_bits_to_f32(uint32_t b);
+template <> __device__ __forceinline__ float param_bits_to_f32<BF16T>(uint32_t b) { return bf16_bits_to_f32(b); }
+template <> __device__ __forceinline__ float param_bits_to_f32<F16T>(uint32_t b) { return f16_bits_to_f32(b); }
+
+// Per-lane state of one wave's walk over its spans (byte offsets into the
+// buffers; span j adds j * the per-span stride).
+struct QmvLane {
+    __amdgpu_buffer_rsrc_t wr, xr, sr, br;
+    uint32_t woff;    // codes: row n0 + l%16, 16-byte chunk l/16 of span 0
+    uint32_t xoff;    // activations of this lane's A slots at span 0 (out of range for dead rows)
+    uint32_t xstep;   // activation bytes per span (0 for dead rows)
+    uint32_t soff;    // scales/biases of this lane's row
+    int r_p;          // this lane's result group within a span
+};
+
+// Scale/bias words of one block: the NU * SPAN / GS consecutive groups of a
+// row that the block's spans cover (at least one word).
+template <int BITS, int GS, int NU>
+struct QmvParamWords {
+    static constexpr int GROUPS = (NU * QmvGeom<BITS, GS>::SPAN) / GS > 0 ? (NU * QmvGeom<BITS, GS>::SPAN) / GS : 1;
+    static constexpr int WORDS = (GROUPS + 1) / 2;
+};
+
+// Registers of one block of NU spans.  With VEC the block's scales and biases
+// arrive as one vector load each (row and block starts aligned to the load),
+// otherwise as one 16-bit load per span.
+template <int BITS, int GS, int NU, bool VEC>
+struct QmvBlock {
+    static constexpr bool VECP = VEC && NU > 1;
+    static constexpr int PWORDS = VECP ? QmvParamWords<BITS, GS, NU>::WORDS : NU;
+    bf16x8 xa[NU][QmvGeom<BITS, GS>::STEPS];
+    u32x4 wd[NU];
+    uint32_t sw[PWORDS], bw[PWORDS];
+};
+
+// Loads `W` consecutive 32-bit words at byte offset `off` (16-, 8- or 4-byte loads).
+template <int W>
+__device__ __forceinline__ void load_words(uint32_t* d, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (W >= 4) {
+#pragma unroll
+        for (int i = 0; i < W / 4; i++) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+            d[4 * i] = v[0], d[4 * i + 1] = v[1], d[4 * i + 2] = v[2], d[4 * i + 3] = v[3];
+        }
+    } else if constexpr (W == 2) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        d[0] = v[0], d[1] = v[1];
+    } else {
+        d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    }
+}
+
+// Loads spans [j0, j0 + NU) (issue order scale/bias bits, activations, codes).
+// When a group is longer than a span (8-bit codes, group 128) j0 must be even
+// or NU == 1, so that group(j0 + u) = group(j0) + u * SPAN / GS.
+template <int BITS, int GS, int NU, bool VEC>
+__device__ __forceinline__ void qmv_load(QmvBlock<BITS, GS, NU, VEC>& b, const QmvLane& L, int j0) {
+    typedef QmvGeom<BITS, GS> Geo;
+    typedef QmvBlock<BITS, GS, NU, VEC> B;
+    if constexpr (B::VECP) {
+        // the block's groups of this lane's row (the lane's own group is picked later)
+        const uint32_t so = L.soff + uint32_t((j0 * Geo::SPAN) / GS) * 2u;
+        load_words<B::PWORDS>(b.sw, L.sr, so);
+        load_words<B::PWORDS>(b.bw, L.br, so);
+    } else {
+        const uint32_t so = L.soff + (uint32_t((j0 * Geo::SPAN) / GS) + uint32_t(L.r_p)) * 2u;
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            b.sw[u] = __builtin_amdgcn_raw_buffer_load_b16(L.sr, so + (u * Geo::SPAN) / GS * 2, 0, 0);
+            b.bw[u] = __builtin_amdgcn_raw_buffer_load_b16(L.br, so + (u * Geo::SPAN) / GS * 2, 0, 0);
+        }
+    }
+    const uint32_t xo = L.xoff + uint32_t(j0) * L.xstep;
+#pragma unroll
+    for (int u = 0; u < NU; u++)
+#pragma unroll
+        for (int t = 0; t < Geo::STEPS; t++)
+            b.xa[u][t] = __builtin_bit_cast(
+                bf16x8, __builtin_amdgcn_raw_buffer_load_b128(L.xr, xo + u * Geo::SPAN * 2 + 16 * t, 0, 0));
+    const uint32_t wo = L.woff + uint32_t(j0) * 64u;
+#pragma unroll
+    for (int u = 0; u < NU; u++) b.wd[u] = __builtin_amdgcn_raw_buffer_load_b128(L.wr, wo + u * 64, 0, 0);
+}
+
+// acc += s * (x . (128 + q)) + (b - 128 s) * sum(x) per span (4-bit); the 8-bit
+// codes are exact, so acc += s * (x . q) + b * sum(x).
+// Element e of a row of 16-bit parameters held in 32-bit words, as f32.
+template <typename ST, int WORDS>
+__device__ __forceinline__ float pick_param(const uint32_t* words, int e) {
+    uint32_t w = words[0];
+#pragma unroll
+    for (int i = 1; i < WORDS; i++) w = (e >> 1) == i ? words[i] : w;
+    return param_bits_to_f32<ST>((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// One span of one 16-row tile: the group-split MFMAs on the A operand xa
+// (activations) and the codes wd, then acc += s * t + b' * xs with the span's
+// scale s and bias b of this lane's result group:
+// 4-bit: t = x . (128 + q), b' = b - 128 s; 8-bit: t = x . q, b' = b.
 template <int BITS, int GS, typename ST, int MREG>
-__global__ __launch_bounds__(64 * kQmvMaxWaves) void qmv_mfma_kernel(
+__device__ __forceinline__ void qmv_span(f32x4& acc, const bf16x8* xa, const u32x4& wd, float sc, float bi,
+                                         const UnpackConsts& uc, bf16x8 ones) {
+    typedef QmvGeom<BITS, GS> Geo;
+    f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < Geo::STEPS; t++) {
+        bf16x8 bq;
+        if (BITS == 4)
+            bq = unpack4_bf16_offset128(wd[t], uc);
+        else
+            bq = unpack8_bf16(wd[2 * t], wd[2 * t + 1]);
+        t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], bq, t4, 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], ones, xs, 0, 0, 0);
+    }
+    const float beff = BITS == 4 ? fmaf(-128.f, sc, bi) : bi;
+#pragma unroll
+    for (int r = 0; r < MREG; r++) acc[r] = fmaf(sc, t4[r], fmaf(beff, xs[r], acc[r]));
+}
+
+// Scale and bias of span u of a block for this lane's result group r_p.
+template <int BITS, int GS, typename ST, int NU, bool VEC>
+__device__ __forceinline__ void qmv_params(const uint32_t* sw, const uint32_t* bw, int u, int r_p, float bias_on,
+                                           float& sc, float& bi) {
+    typedef QmvGeom<BITS, GS> Geo;
+    if constexpr (VEC && NU > 1) {
+        constexpr int PWORDS = QmvParamWords<BITS, GS, NU>::WORDS;
+        const int e = (u * Geo::SPAN) / GS + r_p;  // this lane's group, counted from the block's first
+        sc = pick_param<ST, PWORDS>(sw, e);
+        bi = pick_param<ST, PWORDS>(bw, e) * bias_on;
+    } else {
+        sc = param_bits_to_f32<ST>(sw[u] & 0xffffu);
+        bi = param_bits_to_f32<ST>(bw[u] & 0xffffu) * bias_on;
+    }
+}
+
+template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC>
+__device__ __forceinline__ void qmv_compute(f32x4& acc, const QmvBlock<BITS, GS, NU, VEC>& b, int r_p,
+                                            float bias_on, const UnpackConsts& uc, bf16x8 ones) {
+    // Loads issued before this block stay before it (no load may be sunk
+    // across a memory clobber).
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        float sc, bi;
+        qmv_params<BITS, GS, ST, NU, VEC>(b.sw, b.bw, u, r_p, bias_on, sc, bi);
+        qmv_span<BITS, GS, ST, MREG>(acc, b.xa[u], b.wd[u], sc, bi, uc, ones);
+    }
+}
+
+// MREG: result registers that can hold a live activation row (1 when M == 1).
+// Buffer sizes (M*K*2, N*K*bits/8, N*G*2 bytes) are below 2^31 (the launcher
+// splits N otherwise).
+//
+// Occupancy target 2 waves per SIMD: the two register blocks of the
+// double-buffered span pipeline must both stay live (the default target of
+// higher occupancy makes the scheduler serialise the prefetch instead).
+template <int BITS, int GS, typename ST, int MREG, bool VEC>
+__global__ __launch_bounds__(64 * kQmvMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_mfma_kernel(
     uint16_t* __restrict__ y, const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
-    const typename ST::storage* __restrict__ scales, const typename ST::storage* __restrict__ biases, int M,
-    int N, int K, int groups_per_wave) {
-    constexpr int CPL = GS / 4;             // codes per lane per group
-    constexpr int WPL = CPL * BITS / 32;    // words per lane per group
-    constexpr int STEPS = CPL / 8;          // MFMAs per group
-    constexpr int WPG = GS * BITS / 32;     // words per group per row
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases, int M, int N, int K, int ldy,
+    int spans_per_wave) {
+    typedef QmvGeom<BITS, GS> Geo;
+    constexpr int CPL = Geo::CPL, SPAN = Geo::SPAN, P = Geo::P, MB = Geo::MB;
+    constexpr int U = kQmvUnroll;
+    static_assert(U % 2 == 0, "blocks must start at even spans");
     __shared__ float red[kQmvMaxWaves][16][16];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int nwaves = blockDim.x >> 6;
     const int ln = lane & 15;
     const int kq = lane >> 4;
     const int n0 = blockIdx.x * 16;
     const int G = K / GS;
-    const int g_begin = wave * groups_per_wave;
-    const int g_end = min(G, g_begin + groups_per_wave);
+    const int S_full = K / SPAN;               // spans wholly inside the row
+    const int S = (K + SPAN - 1) / SPAN;       // including a ragged last span
+    const int j_begin = wave * spans_per_wave;
+    const int j_end = min(S, j_begin + spans_per_wave);
+    const int j_full_end = min(S_full, j_end);
+    const uint32_t row_bytes = uint32_t(K) * BITS / 8;
 
-    const uint32_t* wrow = w + int64_t(n0 + ln) * (int64_t(K) * BITS / 32) + kq * WPL;
-    const bool x_live = ln < M;
-    const uint16_t* xrow = x + int64_t(x_live ? ln : 0) * K + kq * CPL;
-    const typename ST::storage* srow = scales + int64_t(n0 + ln) * G;
-    const typename ST::storage* brow = biases ? biases + int64_t(n0 + ln) * G : nullptr;
+    // A operand: lane row ln is activation row ln % MB of group block ln / MB; it is
+    // live when that block is the group of this lane's k-slots (block kq * P / 4).
+    const int a_m = ln % MB;
+    const bool a_live = (ln / MB) == (kq * P / 4) && a_m < M;
+    // Result lanes: block kq holds result rows 4kq..4kq+3, all in group block kq * P / 4.
+    const int r_p = kq * P / 4;
 
+    QmvLane L;
+    L.wr = raw_rsrc(w, uint32_t(N) * row_bytes);
+    L.xr = raw_rsrc(x, uint32_t(M) * uint32_t(K) * 2u);
+    L.sr = raw_rsrc(scales, uint32_t(N) * uint32_t(G) * 2u);
+    L.br = biases ? raw_rsrc(biases, uint32_t(N) * uint32_t(G) * 2u) : L.sr;
+    L.woff = uint32_t(n0 + ln) * row_bytes + uint32_t(kq) * 16u;
+    L.xoff = a_live ? (uint32_t(a_m) * uint32_t(K) + uint32_t(kq * CPL)) * 2u : kOutOfRange;
+    L.xstep = a_live ? SPAN * 2 : 0;
+    L.soff = uint32_t(n0 + ln) * uint32_t(G) * 2u;
+    L.r_p = r_p;
+    const float bias_on = biases ? 1.f : 0.f;
+
+    const UnpackConsts uc = make_unpack_consts();
     u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
     const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_bits);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 
-    for (int g0 = g_begin; g0 < g_end; g0 += kQmvUnroll) {
-        uint32_t wd[kQmvUnroll][WPL];
-        bf16x8 xa[kQmvUnroll][STEPS];
-        float sc[kQmvUnroll], bi[kQmvUnroll];
-#pragma unroll
-        for (int u = 0; u < kQmvUnroll; u++) {
-            const int g = g0 + u;
-            if (g < g_end) {
-                WordVec<WPL>::load(wrow + int64_t(g) * WPG, wd[u]);
-                sc[u] = load_param<ST>(srow, g);
-                bi[u] = brow ? load_param<ST>(brow, g) : 0.f;
-#pragma unroll
-                for (int j = 0; j < STEPS; j++) {
-                    if (x_live)
-                        xa[u][j] = *reinterpret_cast<const bf16x8*>(xrow + g * GS + 8 * j);
-                    else
-                        xa[u][j] = bf16x8{};
-                }
-            }
+    // Full blocks, double-buffered: the loads of block i + 1 are in flight
+    // while block i is computed.  Each compute sits in a basic block of its
+    // own (opaque_one) so that the prefetch issued before it stays there.  The
+    // loop body handles a pair of blocks; every prefetch is unconditional (past
+    // the last block it re-reads the last block, which is still in L2).
+    const int nblk = max(0, (j_full_end - j_begin) / U);
+    if (nblk > 0) {
+        QmvBlock<BITS, GS, U, VEC> ba, bb;
+        qmv_load<BITS, GS, U, VEC>(ba, L, j_begin);
+        for (int i = 0; i + 1 < nblk; i += 2) {
+            qmv_load<BITS, GS, U, VEC>(bb, L, j_begin + (i + 1) * U);
+            if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, ba, r_p, bias_on, uc, ones);
+            qmv_load<BITS, GS, U, VEC>(ba, L, j_begin + min(i + 2, nblk - 1) * U);
+            if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, bb, r_p, bias_on, uc, ones);
         }
-#pragma unroll
-        for (int u = 0; u < kQmvUnroll; u++) {
-            if (g0 + u < g_end) {
-                f32x4 t = {0.f, 0.f, 0.f, 0.f};
-                f32x4 xs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < STEPS; j++) {
-                    bf16x8 bq;
-                    if (BITS == 4)
-                        bq = unpack4_bf16_offset128(wd[u][j]);
-                    else
-                        bq = unpack8_bf16(wd[u][2 * j], wd[u][2 * j + 1]);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[u][j], bq, t, 0, 0, 0);
-                    xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[u][j], ones, xs, 0, 0, 0);
-                }
-                const float beff = BITS == 4 ? bi[u] - 128.f * sc[u] : bi[u];
-#pragma unroll
-                for (int r = 0; r < MREG; r++) acc[r] = fmaf(sc[u], t[r], fmaf(beff, xs[r], acc[r]));
-            }
-        }
+        if (nblk & 1) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, ba, r_p, bias_on, uc, ones);  // block nblk - 1
+    }
+    // Remaining whole spans one at a time.
+    for (int j = j_begin + nblk * U; j < j_full_end; j++) {
+        QmvBlock<BITS, GS, 1, VEC> b1;
+        qmv_load<BITS, GS, 1, VEC>(b1, L, j);
+        qmv_compute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, r_p, bias_on, uc, ones);
+    }
+    // A ragged last span (K % SPAN != 0): chunks past the end of the row see
+    // zero activations (their codes belong to the next row, or read as zero
+    // past the buffer), and a group past the end has zero scale and bias.
+    if (j_end > S_full && S_full >= j_begin) {
+        const int j = S_full;
+        const bool chunk_in = j * SPAN + kq * CPL < K;
+        const bool g_in = j * SPAN + r_p * GS < K;
+        QmvLane T = L;
+        if (!chunk_in) T.xoff = kOutOfRange, T.xstep = 0;
+        if (!g_in) T.soff = kOutOfRange;
+        QmvBlock<BITS, GS, 1, VEC> b1;
+        qmv_load<BITS, GS, 1, VEC>(b1, T, j);
+        qmv_compute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, r_p, bias_on, uc, ones);
     }
 
-    // D layout: lane holds rows m = 4*kq + r of column n = ln.
+    // Result lane (n = ln, block kq) register r is row 4kq + r = (group block, m) with
+    // m = (4kq + r) % MB; fold the P group blocks (lane blocks 4/P apart) together.
 #pragma unroll
     for (int r = 0; r < MREG; r++) {
-        const int m = 4 * kq + r;
-        if (m < M) red[wave][m][ln] = acc[r];
+        if (P >= 4) acc[r] += __shfl_xor(acc[r], 16);
+        if (P >= 2) acc[r] += __shfl_xor(acc[r], 32);
+    }
+    if (r_p == 0) {
+#pragma unroll
+        for (int r = 0; r < MREG; r++) {
+            const int m = 4 * kq + r;
+            if (m < M) red[wave][m][ln] = acc[r];
+        }
     }
     __syncthreads();
     for (int t = threadIdx.x; t < 16 * M; t += blockDim.x) {
         const int m = t >> 4, n = t & 15;
         float v = 0.f;
         for (int i = 0; i < nwaves; i++) v += red[i][m][n];
-        y[int64_t(m) * N + n0 + n] = uint16_t(f32_to_bf16_bits(v));
+        y[int64_t(m) * ldy + n0 + n] = uint16_t(f32_to_bf16_bits(v));
     }
 }
 
-// Host-side launcher; returns false if this shape/dtype is not covered.
-template <int BITS, int GS, typename ST>
-static void launch_qmv_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b, int M,
-                         int N, int K, hipStream_t st) {
-    const int G = K / GS;
-    int waves = G / 4;
-    waves = waves < 1 ? 1 : (waves > kQmvMaxWaves ? kQmvMaxWaves : waves);
-    const int gpw = (G + waves - 1) / waves;
-    waves = (G + gpw - 1) / gpw;
+// ---------------------------------------------------------------------------
+// Persistent variant with activations in LDS.
+//
+// The grid holds about one workgroup per CU.  A workgroup first copies the
+// activations of every problem it serves into LDS, once, and then walks 16-row
+// tiles (tile, tile + gridDim.x, ...), possibly of several independent
+// problems (a grouped launch, e.g. the q/k/v projections of one token).  Its
+// waves split each tile's K into spans exactly as above, but the A operands
+// now come from LDS (ds_read, counted apart from the weight loads), so the
+// register blocks of the weight pipeline hold only codes and scale words and
+// the texture path carries almost nothing but the weight stream.  Per tile the
+// waves combine their partial sums through a double-buffered LDS slot (fixed
+// summation order, so results are reproducible).
+//
+// LDS layout (bytes): per staged activation matrix M rows of kpad bf16
+// (kpad = K rounded up to 64, zero-filled past K), 16-byte chunk c of row m
+// stored at chunk c ^ (m & 7) so that the rows of one A operand fall in
+// different banks; then a zero block read by dead A rows; then the reduction
+// slots.
+
+constexpr int kQmvMaxProblems = 8;
+
+struct QmvProblem {
+    const uint16_t* x;
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;   // may be null
+    uint16_t* y;
+    int N, K, ldy;
+    int spw;             // spans per wave
+    int tile0;           // first global tile of this problem
+    int x_lds;           // LDS byte offset of its activations
+    int kpad;            // activation row length in LDS (multiple of 64)
+};
+
+struct QmvBatch {
+    QmvProblem p[kQmvMaxProblems];
+    int count;               // problems
+    int M;                   // activation rows (all problems)
+    int total_tiles;
+    int nstage;              // distinct activation matrices to stage
+    int stage[kQmvMaxProblems];  // problem whose x each staged matrix is
+    int zero_lds, zero_bytes;
+    int red_lds;             // 2 x waves x M x 16 floats
+};
+
+// Registers of one block of NU spans of the LDS variant: codes and scale words.
+template <int BITS, int GS, int NU, bool VEC>
+struct QmvWBlock {
+    static constexpr int PWORDS = (VEC && NU > 1) ? QmvParamWords<BITS, GS, NU>::WORDS : NU;
+    u32x4 wd[NU];
+    uint32_t sw[PWORDS], bw[PWORDS];
+};
+
+struct QmvTileLane {
+    __amdgpu_buffer_rsrc_t wr, sr, br;
+    uint32_t woff, soff;  // this lane's code chunk / scale row within the tile, at span 0
+    int r_p;
+};
+
+template <int BITS, int GS, int NU, bool VEC>
+__device__ __forceinline__ void qmv_wload(QmvWBlock<BITS, GS, NU, VEC>& b, const QmvTileLane& L, int j0) {
+    typedef QmvGeom<BITS, GS> Geo;
+    if constexpr (VEC && NU > 1) {
+        const uint32_t so = L.soff + uint32_t((j0 * Geo::SPAN) / GS) * 2u;
+        load_words<QmvWBlock<BITS, GS, NU, VEC>::PWORDS>(b.sw, L.sr, so);
+        load_words<QmvWBlock<BITS, GS, NU, VEC>::PWORDS>(b.bw, L.br, so);
+    } else {
+        const uint32_t so = L.soff + (uint32_t((j0 * Geo::SPAN) / GS) + uint32_t(L.r_p)) * 2u;
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            b.sw[u] = __builtin_amdgcn_raw_buffer_load_b16(L.sr, so + (u * Geo::SPAN) / GS * 2, 0, 0);
+            b.bw[u] = __builtin_amdgcn_raw_buffer_load_b16(L.br, so + (u * Geo::SPAN) / GS * 2, 0, 0);
+        }
+    }
+    const uint32_t wo = L.woff + uint32_t(j0) * 64u;
+#pragma unroll
+    for (int u = 0; u < NU; u++) b.wd[u] = __builtin_amdgcn_raw_buffer_load_b128(L.wr, wo + u * 64, 0, 0);
+}
+
+// A operands of span j0 + u are read from LDS at xa_t + j0 * xstep + u * SPAN * 2
+// (dead rows have xstep 0 and xa_t in the zero block, which covers NU spans).
+template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC>
+__device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, GS, NU, VEC>& b, const char* smem,
+                                             const uint32_t* xa_t, uint32_t xstep, int j0, int r_p,
+                                             float bias_on, const UnpackConsts& uc, bf16x8 ones) {
+    typedef QmvGeom<BITS, GS> Geo;
+    asm volatile("" ::: "memory");
+    uint32_t xb[Geo::STEPS];
+#pragma unroll
+    for (int t = 0; t < Geo::STEPS; t++) xb[t] = xa_t[t] + uint32_t(j0) * xstep;
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        bf16x8 xa[Geo::STEPS];
+#pragma unroll
+        for (int t = 0; t < Geo::STEPS; t++)
+            xa[t] = *reinterpret_cast<const bf16x8*>(smem + xb[t] + u * Geo::SPAN * 2);
+        float sc, bi;
+        qmv_params<BITS, GS, ST, NU, VEC>(b.sw, b.bw, u, r_p, bias_on, sc, bi);
+        qmv_span<BITS, GS, ST, MREG>(acc, xa, b.wd[u], sc, bi, uc, ones);
+    }
+}
+
+#ifndef EQ_QMV_LDS_WAVES
+#define EQ_QMV_LDS_WAVES 4
+#endif
+constexpr int kQmvLdsWaves = EQ_QMV_LDS_WAVES;  // waves per workgroup of the LDS variant
+
+// Per-wave view of one tile: span range, buffers, offsets, A-operand addresses.
+template <int BITS, int GS>
+struct QmvTileView {
+    QmvTileLane L;
+    int n0, j_begin, j_end, j_full_end, nblk, S_full, K;
+    float bias_on;
+    uint32_t xa_t[QmvGeom<BITS, GS>::STEPS];
+    uint32_t xstep;
+};
+
+template <int BITS, int GS>
+__device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& batch, int pi, int tile, int wave,
+                                                              int ln, int kq, int a_m, bool a_live, int r_p) {
+    typedef QmvGeom<BITS, GS> Geo;
+    const QmvProblem& pr = batch.p[pi];
+    QmvTileView<BITS, GS> v;
+    const int N = pr.N, K = pr.K, G = K / GS;
+    v.K = K;
+    v.n0 = (tile - pr.tile0) * 16;
+    v.S_full = K / Geo::SPAN;
+    const int S = (K + Geo::SPAN - 1) / Geo::SPAN;
+    v.j_begin = wave * pr.spw;
+    v.j_end = min(S, v.j_begin + pr.spw);
+    v.j_full_end = min(v.S_full, v.j_end);
+    v.nblk = max(0, (v.j_full_end - v.j_begin) / kQmvUnroll);
+    const uint32_t row_bytes = uint32_t(K) * BITS / 8;
+    v.L.wr = raw_rsrc(pr.w, uint32_t(N) * row_bytes);
+    v.L.sr = raw_rsrc(pr.s, uint32_t(N) * uint32_t(G) * 2u);
+    v.L.br = pr.b ? raw_rsrc(pr.b, uint32_t(N) * uint32_t(G) * 2u) : v.L.sr;
+    v.L.woff = uint32_t(v.n0 + ln) * row_bytes + uint32_t(kq) * 16u;
+    v.L.soff = uint32_t(v.n0 + ln) * uint32_t(G) * 2u;
+    v.L.r_p = r_p;
+    v.bias_on = pr.b ? 1.f : 0.f;
+#pragma unroll
+    for (int t = 0; t < Geo::STEPS; t++)
+        v.xa_t[t] = a_live ? uint32_t(pr.x_lds + a_m * pr.kpad * 2 + (((kq * Geo::CPL / 8 + t) ^ (a_m & 7)) * 16))
+                           : uint32_t(batch.zero_lds);
+    v.xstep = a_live ? Geo::SPAN * 2 : 0;
+    return v;
+}
+
+template <int BITS, int GS, typename ST, int MREG, bool VEC>
+__global__ __launch_bounds__(64 * kQmvLdsWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
+    const QmvBatch batch) {
+    typedef QmvGeom<BITS, GS> Geo;
+    constexpr int CPL = Geo::CPL, SPAN = Geo::SPAN, P = Geo::P, MB = Geo::MB, STEPS = Geo::STEPS;
+    constexpr int U = kQmvUnroll;
+    static_assert(U % 2 == 0, "blocks must start at even spans");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int ln = lane & 15;
+    const int kq = lane >> 4;
+    const int M = batch.M;
+
+    // Stage the activations (zero past K), the zero block, then wait.  Eight
+    // chunks per thread are loaded before any is written, so the copy costs
+    // few round trips to L2.
+    for (int r = 0; r < batch.nstage; r++) {
+        const QmvProblem& pr = batch.p[batch.stage[r]];
+        const __amdgpu_buffer_rsrc_t xr = raw_rsrc(pr.x, uint32_t(M) * uint32_t(pr.K) * 2u);
+        const int cpr = pr.kpad / 8;  // 16-byte chunks per LDS row
+        const int total = M * cpr;
+        for (int c0 = threadIdx.x; c0 < total; c0 += 8 * blockDim.x) {
+            u32x4 v[8];
+            int dst[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int c = c0 + i * blockDim.x;
+                const int m = c / cpr, cc = c - m * cpr;
+                const bool in = c < total && cc * 8 < pr.K;
+                const uint32_t off = in ? (uint32_t(m) * uint32_t(pr.K) + uint32_t(cc) * 8u) * 2u : kOutOfRange;
+                v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+                dst[i] = c < total ? pr.x_lds + m * pr.kpad * 2 + ((cc ^ (m & 7)) * 16) : -1;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (dst[i] >= 0) *reinterpret_cast<u32x4*>(smem + dst[i]) = v[i];
+        }
+    }
+    for (int c = threadIdx.x; c < batch.zero_bytes / 16; c += blockDim.x)
+        *reinterpret_cast<u32x4*>(smem + batch.zero_lds + c * 16) = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+
+    const UnpackConsts uc = make_unpack_consts();
+    u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_bits);
+    // A operand row ln is activation row ln % MB of group block ln / MB; live when
+    // that block is the group of this lane's k-slots (block kq * P / 4).
+    const int a_m = ln % MB;
+    const bool a_live = (ln / MB) == (kq * P / 4) && a_m < M;
+    const int r_p = kq * P / 4;  // result group block of this lane
+    float* red = reinterpret_cast<float*>(smem + batch.red_lds);
+
+    int tile = blockIdx.x;
+    if (tile >= batch.total_tiles) return;
+    int pi = 0;
+    while (pi + 1 < batch.count && tile >= batch.p[pi + 1].tile0) pi++;
+    pi = __builtin_amdgcn_readfirstlane(pi);
+    QmvTileView<BITS, GS> V = qmv_tile_view<BITS, GS>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p);
+
+    QmvWBlock<BITS, GS, U, VEC> ba, bb;
+    bool pre = false;  // ba already holds (or is loading) this tile's first block
+    for (int iter = 0;; iter++) {
+        // The next tile of this workgroup: its first block is prefetched while
+        // this tile finishes, when this tile's block count is even.
+        const int ntile = tile + gridDim.x;
+        const bool has_next = ntile < batch.total_tiles;
+        int npi = pi;
+        while (has_next && npi + 1 < batch.count && ntile >= batch.p[npi + 1].tile0) npi++;
+        npi = __builtin_amdgcn_readfirstlane(npi);
+        QmvTileView<BITS, GS> Vn =
+            qmv_tile_view<BITS, GS>(batch, npi, has_next ? ntile : tile, wave, ln, kq, a_m, a_live, r_p);
+        const bool chain = has_next && Vn.nblk > 0;
+
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const int nblk = V.nblk;
+        if (nblk > 0 && !pre) qmv_wload<BITS, GS, U, VEC>(ba, V.L, V.j_begin);
+        bool pre_next = false;
+        if (nblk > 0 && (nblk & 1) == 0) {
+            for (int i = 0; i < nblk; i += 2) {
+                qmv_wload<BITS, GS, U, VEC>(bb, V.L, V.j_begin + (i + 1) * U);
+                if (opaque_one())
+                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ba, smem, V.xa_t, V.xstep, V.j_begin + i * U, r_p,
+                                                              V.bias_on, uc, ones);
+                // Next block of this tile, else the first block of the next
+                // tile, else a harmless re-read of this tile's last block.
+                const bool more = i + 2 < nblk;
+                const bool cross = !more && chain;
+                QmvTileLane Lp = cross ? Vn.L : V.L;
+                const int jp = more ? V.j_begin + (i + 2) * U : (cross ? Vn.j_begin : V.j_begin + (nblk - 1) * U);
+                qmv_wload<BITS, GS, U, VEC>(ba, Lp, jp);
+                if (opaque_one())
+                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, bb, smem, V.xa_t, V.xstep, V.j_begin + (i + 1) * U,
+                                                              r_p, V.bias_on, uc, ones);
+            }
+            pre_next = chain;
+        } else if (nblk > 0) {
+            for (int i = 0; i + 1 < nblk; i += 2) {
+                qmv_wload<BITS, GS, U, VEC>(bb, V.L, V.j_begin + (i + 1) * U);
+                if (opaque_one())
+                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ba, smem, V.xa_t, V.xstep, V.j_begin + i * U, r_p,
+                                                              V.bias_on, uc, ones);
+                qmv_wload<BITS, GS, U, VEC>(ba, V.L, V.j_begin + min(i + 2, nblk - 1) * U);
+                if (opaque_one())
+                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, bb, smem, V.xa_t, V.xstep, V.j_begin + (i + 1) * U,
+                                                              r_p, V.bias_on, uc, ones);
+            }
+            qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ba, smem, V.xa_t, V.xstep, V.j_begin + (nblk - 1) * U, r_p,
+                                                      V.bias_on, uc, ones);
+        }
+        for (int j = V.j_begin + nblk * U; j < V.j_full_end; j++) {
+            QmvWBlock<BITS, GS, 1, VEC> b1;
+            qmv_wload<BITS, GS, 1, VEC>(b1, V.L, j);
+            qmv_wcompute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, smem, V.xa_t, V.xstep, j, r_p, V.bias_on, uc, ones);
+        }
+        // Ragged last span: chunks past K see the zero block, groups past K
+        // have zero scale and bias.
+        if (V.j_end > V.S_full && V.S_full >= V.j_begin) {
+            const int j = V.S_full;
+            const bool chunk_in = j * SPAN + kq * CPL < V.K;
+            const bool g_in = j * SPAN + r_p * GS < V.K;
+            QmvTileLane T = V.L;
+            if (!g_in) T.soff = kOutOfRange;
+            uint32_t xt[STEPS];
+#pragma unroll
+            for (int t = 0; t < STEPS; t++)
+                xt[t] = chunk_in ? V.xa_t[t] : uint32_t(batch.zero_lds) - uint32_t(j) * V.xstep;
+            QmvWBlock<BITS, GS, 1, VEC> b1;
+            qmv_wload<BITS, GS, 1, VEC>(b1, T, j);
+            qmv_wcompute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, smem, xt, V.xstep, j, r_p, V.bias_on, uc, ones);
+        }
+
+        // Fold the P group blocks, then combine the waves through LDS.
+#pragma unroll
+        for (int r = 0; r < MREG; r++) {
+            if (P >= 4) acc[r] += __shfl_xor(acc[r], 16);
+            if (P >= 2) acc[r] += __shfl_xor(acc[r], 32);
+        }
+        float* slot = red + (iter & 1) * (nwaves * M * 16);
+        if (r_p == 0) {
+#pragma unroll
+            for (int r = 0; r < MREG; r++) {
+                const int m = 4 * kq + r;
+                if (m < M) slot[(wave * M + m) * 16 + ln] = acc[r];
+            }
+        }
+        __syncthreads();
+        const QmvProblem& pr = batch.p[pi];
+        for (int t = threadIdx.x; t < 16 * M; t += blockDim.x) {
+            const int m = t >> 4, n = t & 15;
+            float v = 0.f;
+            for (int i = 0; i < nwaves; i++) v += slot[(i * M + m) * 16 + n];
+            pr.y[int64_t(m) * pr.ldy + V.n0 + n] = uint16_t(f32_to_bf16_bits(v));
+        }
+        if (!has_next) break;
+        tile = ntile;
+        pi = npi;
+        V = Vn;
+        pre = pre_next;
+    }
+}
+
+template <int BITS, int GS, typename ST, bool VEC>
+static void launch_qmv_v(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                         int M, int N, int K, int ldy, int spw, int waves, hipStream_t st) {
+    typedef QmvGeom<BITS, GS> Geo;
     const dim3 grid(unsigned(N / 16)), block(unsigned(64 * waves));
-    typedef typename ST::storage S;
-    if (M == 1)
-        qmv_mfma_kernel<BITS, GS, ST, 1><<<grid, block, 0, st>>>(y, x, w, static_cast<const S*>(s),
-                                                                 static_cast<const S*>(b), M, N, K, gpw);
-    else
-        qmv_mfma_kernel<BITS, GS, ST, 4><<<grid, block, 0, st>>>(y, x, w, static_cast<const S*>(s),
-                                                                 static_cast<const S*>(b), M, N, K, gpw);
+    // One launch takes at most MB activation rows; larger M runs in row chunks
+    // (each chunk reads the weights again).
+    for (int m0 = 0; m0 < M; m0 += Geo::MB) {
+        const int mc = M - m0 < Geo::MB ? M - m0 : Geo::MB;
+        uint16_t* yc = y + int64_t(m0) * ldy;
+        const uint16_t* xc = x + int64_t(m0) * K;
+        if (mc == 1)
+            qmv_mfma_kernel<BITS, GS, ST, 1, VEC><<<grid, block, 0, st>>>(yc, xc, w, s, b, mc, N, K, ldy, spw);
+        else
+            qmv_mfma_kernel<BITS, GS, ST, 4, VEC><<<grid, block, 0, st>>>(yc, xc, w, s, b, mc, N, K, ldy, spw);
+    }
+}
+
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// LDS available to one workgroup on the current device (cached per device).
+static int device_lds_bytes() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 65536;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// One matrix-vector problem of a (possibly grouped) decode launch.
+struct QmvSpec {
+    const uint16_t* x;
+    const uint32_t* w;
+    const void* s;
+    const void* b;
+    uint16_t* y;
+    int N, K, ldy;
+};
+
+// Plans and launches the persistent LDS variant for `count` problems sharing
+// bits, group size, scale type and M (<= MB).  Returns false, launching
+// nothing, when the problems do not fit it (too many, LDS too small, buffers
+// of 2^31 bytes or more, N % 16 != 0).
+template <int BITS, int GS, typename ST>
+static bool launch_qmv_lds(const QmvSpec* specs, int count, int M, hipStream_t st) {
+    typedef QmvGeom<BITS, GS> Geo;
+    constexpr int W = kQmvLdsWaves, U = kQmvUnroll;
+    if (count < 1 || count > kQmvMaxProblems || M < 1 || M > Geo::MB) return false;
+    QmvBatch B{};
+    B.count = count;
+    B.M = M;
+    const int pbytes = QmvParamWords<BITS, GS, U>::WORDS * 4;
+    const int align = pbytes < 16 ? pbytes : 16;
+    bool vec = true;
+    int lds = 0, tiles = 0;
+    for (int i = 0; i < count; i++) {
+        const QmvSpec& q = specs[i];
+        QmvProblem& p = B.p[i];
+        const int64_t G = q.K / GS;
+        if (q.N % 16 != 0 || q.K % GS != 0 || q.K <= 0 || q.N <= 0) return false;
+        if (int64_t(q.N) * q.K * BITS / 8 >= (int64_t(1) << 31) || int64_t(M) * q.K * 2 >= (int64_t(1) << 31) ||
+            int64_t(q.N) * G * 2 >= (int64_t(1) << 31))
+            return false;
+        p.x = q.x, p.w = q.w, p.s = static_cast<const uint16_t*>(q.s), p.b = static_cast<const uint16_t*>(q.b);
+        p.y = q.y, p.N = q.N, p.K = q.K, p.ldy = q.ldy;
+        const int S = (q.K + Geo::SPAN - 1) / Geo::SPAN;
+        // spans per wave: a multiple of 2U, so that full waves have an even
+        // number of blocks (the first block of the next tile is then prefetched)
+        p.spw = ((S + W - 1) / W + 2 * U - 1) / (2 * U) * (2 * U);
+        p.tile0 = tiles;
+        tiles += q.N / 16;
+        p.kpad = (q.K + 63) / 64 * 64;
+        vec = vec && (G * 2) % align == 0 && aligned(q.s, align) && (q.b == nullptr || aligned(q.b, align));
+        // stage each distinct activation matrix once
+        p.x_lds = -1;
+        for (int j = 0; j < i; j++)
+            if (B.p[j].x == q.x && B.p[j].K == q.K) p.x_lds = B.p[j].x_lds;
+        if (p.x_lds < 0) {
+            p.x_lds = lds;
+            B.stage[B.nstage++] = i;
+            lds += M * p.kpad * 2;
+        }
+    }
+    B.total_tiles = tiles;
+    B.zero_lds = lds;
+    B.zero_bytes = (U * Geo::SPAN * 2 + 64 + 15) / 16 * 16;
+    lds += B.zero_bytes;
+    B.red_lds = lds;
+    lds += 2 * W * M * 16 * 4;
+    if (lds > device_lds_bytes()) return false;
+    const int grid = tiles < 2 * device_cu_count() ? tiles : 2 * device_cu_count();
+    auto go = [&](auto kernel) {
+        // (a refusal surfaces as a launch error)
+        if (lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      lds);
+        kernel<<<dim3(unsigned(grid)), dim3(64 * W), size_t(lds), st>>>(B);
+    };
+    if (M == 1) {
+        if (vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true>);
+        else go(qmv_lds_kernel<BITS, GS, ST, 1, false>);
+    } else {
+        if (vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true>);
+        else go(qmv_lds_kernel<BITS, GS, ST, 4, false>);
+    }
+    return true;
+}
+
+template <int BITS, int GS, typename ST>
+static void launch_qmv_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* sv, const void* bv, int M,
+                         int N, int K, hipStream_t st) {
+    typedef QmvGeom<BITS, GS> Geo;
+    // Persistent LDS variant, in chunks of at most MB activation rows; the rows
+    // it does not take (activations too large for LDS) go to the kernel above.
+    int m0 = 0;
+    for (; m0 < M; m0 += Geo::MB) {
+        const int mc = M - m0 < Geo::MB ? M - m0 : Geo::MB;
+        const QmvSpec q{x + int64_t(m0) * K, w, sv, bv, y + int64_t(m0) * N, N, K, N};
+        if (!launch_qmv_lds<BITS, GS, ST>(&q, 1, mc, st)) break;
+    }
+    if (m0 >= M) return;
+    x += int64_t(m0) * K;
+    y += int64_t(m0) * N;
+    M -= m0;
+    const uint16_t* s = static_cast<const uint16_t*>(sv);
+    const uint16_t* b = static_cast<const uint16_t*>(bv);
+    const int spans = (K + Geo::SPAN - 1) / Geo::SPAN;
+    // About kQmvSpansPerWave spans per wave, at most kQmvMaxWaves waves; spans
+    // per wave a multiple of the block length, so that every block starts at a
+    // multiple of kQmvUnroll (aligned scale loads; even spans, see qmv_load).
+    int waves = (spans + kQmvSpansPerWave - 1) / kQmvSpansPerWave;
+    waves = waves < 1 ? 1 : (waves > kQmvMaxWaves ? kQmvMaxWaves : waves);
+    const int spw = ((spans + waves - 1) / waves + kQmvUnroll - 1) / kQmvUnroll * kQmvUnroll;
+    waves = (spans + spw - 1) / spw;
+    // Vector scale/bias loads need rows and pointers aligned to the load size.
+    const int G = K / GS;
+    const int pbytes = QmvParamWords<BITS, GS, kQmvUnroll>::WORDS * 4;
+    const int align = pbytes < 16 ? pbytes : 16;
+    const bool vec = (G * 2) % align == 0 && aligned(s, align) && (b == nullptr || aligned(b, align));
+    // Buffer offsets are 32-bit: launch in row chunks of < 2^31 bytes of codes.
+    const int64_t row_bytes = int64_t(K) * BITS / 8;
+    int64_t rows_per_launch = ((int64_t(1) << 31) - 1) / row_bytes / 16 * 16;
+    if (rows_per_launch < 16) rows_per_launch = 16;
+    for (int64_t n0 = 0; n0 < N; n0 += rows_per_launch) {
+        const int nc = int(N - n0 < rows_per_launch ? N - n0 : rows_per_launch);
+        const uint32_t* wc = w + n0 * (row_bytes / 4);
+        const uint16_t* sc = s + n0 * G;
+        const uint16_t* bc = b ? b + n0 * G : nullptr;
+        // y rows are strided by N; a row chunk writes columns [n0, n0 + nc) of y.
+        if (vec)
+            launch_qmv_v<BITS, GS, ST, true>(y + n0, x, wc, sc, bc, M, nc, K, N, spw, waves, st);
+        else
+            launch_qmv_v<BITS, GS, ST, false>(y + n0, x, wc, sc, bc, M, nc, K, N, spw, waves, st);
+        if (N - n0 <= rows_per_launch) break;
+    }
 }
 
 template <int BITS, typename ST>
@@ -206,7 +897,7 @@ static bool launch_qmv_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t
 
 // Entry used by the dispatcher (api.hip).  Preconditions checked there:
 // x bf16, transpose, 1 <= M <= 16, N % 16 == 0, K % gs == 0, 16-byte aligned
-// x and weight rows, scale dtype bf16 or f16.
+// x and weight pointers, scale dtype bf16 or f16.
 bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, hipStream_t st) {
     if (bits == 4) {
