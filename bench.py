@@ -1,21 +1,26 @@
 """Benchmark of the quantized-linear hot path on one MI355X.
 
-Headline workload (M = 1): one step is the decode
-pass of a Llama-3-8B-shaped stack's linears -- q, k, v, o, gate, up, down
-(N x K = 4096x4096, 1024x4096, 1024x4096, 4096x4096, 14336x4096, 14336x4096,
-4096x14336) for each of 32 layers, 224 quantized matmuls at M = 1 with 4-bit,
-group-64 weights and bf16 activations/scales/biases.  Every layer has its
-own weights (3.93 GB in HBM), so the 256 MB Infinity Cache cannot serve
-repeats.  The step is captured once as a HIP graph and replayed; inputs are
-resident in HBM before the timed region starts.
+Headline workload (BASELINE.json configs[1] at M = 1): one step is the
+decode-time projections of a Llama-3-8B-shaped stack -- q, k, v, o, gate, up,
+down (N x K = 4096x4096, 1024x4096, 1024x4096, 4096x4096, 14336x4096,
+14336x4096, 4096x14336) for each of 32 layers: 224 quantized matmuls at M = 1
+with 4-bit, group-64 weights and bf16 activations/scales/biases.  Every layer
+has its own weights (3.93 GB in HBM), so the 256 MB Infinity Cache cannot
+serve repeats.  The projections are issued the way a decode step can issue
+them -- one grouped launch (eq_quantized_matmul_batched) for each set that
+shares an input: {q, k, v}, {o}, {gate, up}, {down}, i.e. 128 launches per
+step -- captured once as a HIP graph and replayed; inputs are resident in HBM
+before the timed region starts.
 
 value = algorithmic bytes of the step / step time, in GB/s
 (bytes per linear: N*K/2 packed codes + 4*N*K/64 scale+bias + 2*M*K + 2*M*N).
 
-Also reported (not the headline): per-shape qmv GB/s at M = 1 and 8,
-prefill qmm TFLOP/s, GGUF dequant/convert GB/s,
-the roofline record of the dominant kernel and the CPU baseline (the
-restated MLX CPU qmm loop from oracle/, timed on this host).
+Also reported (not the headline): the same step with one launch per
+projection (the drop-in eq_quantized_matmul path) and with all seven
+projections of a layer in one launch, M = 8, per-shape qmv, prefill qmm
+TFLOP/s, GGUF dequant/convert GB/s, the roofline
+record of the dominant kernel (qmv_lds_kernel) and the CPU baseline (the
+restated MLX CPU qmm loop of oracle/, timed on this host).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 """
@@ -32,14 +37,16 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBS = 8000.0
-BF16_MFMA_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 LAYERS = 32
 HIDDEN, FFN, KV = 4096, 14336, 1024
 LAYER_SHAPES = [  # (name, N, K)
     ("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
     ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN),
 ]
+DECODE_GROUPS = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]  # sets sharing an input
+ALL7 = [["q", "k", "v", "o", "gate", "up", "down"]]
 GS, BITS = 64, 4
 
 
@@ -65,83 +72,104 @@ class Linear:
         self.b = (-7.5 * self.s.float()).to(torch.bfloat16)
 
 
-def run_qmv(lin, x, y, bits=BITS, gs=GS):
+class Timer:
+    """Replays a captured HIP graph on its own stream and times it with HIP
+    events recorded on that same stream."""
+
+    def __init__(self, fn):
+        import torch
+
+        self.stream = torch.cuda.Stream()
+        self.graph = torch.cuda.CUDAGraph()
+        self.stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(self.stream):
+            fn(self.stream.cuda_stream)  # warm once outside capture
+            torch.cuda.synchronize()
+            with torch.cuda.graph(self.graph, stream=self.stream):
+                fn(self.stream.cuda_stream)
+        torch.cuda.synchronize()
+
+    def ms_per_replay(self, steps, warmup):
+        import torch
+
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                self.graph.replay()
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(self.stream)
+            for _ in range(steps):
+                self.graph.replay()
+            end.record(self.stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+
+def _lib():
     from eredu_amd import _native
 
-    _native.check(_native.lib().eq_quantized_matmul(
+    return _native
+
+
+def run_one(lin, x, y, stream, bits=BITS, gs=GS):
+    n = _lib()
+    n.check(n.lib().eq_quantized_matmul(
         y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(), x.shape[0], lin.N, lin.K,
-        True, gs, bits, b"affine", _native.EQ_DTYPE_BF16, _native.EQ_DTYPE_BF16, _stream()))
+        True, gs, bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, stream))
 
 
-def _stream():
-    import torch
-
-    return torch.cuda.current_stream().cuda_stream
-
-
-def capture(fn):
-    import torch
-
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        fn()  # warm the kernels once outside capture
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g, stream=s):
-            fn()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    return g
+def run_group(lins, xs, ys, stream, bits=BITS, gs=GS):
+    n = _lib()
+    arr = (n.QmmProblem * len(lins))()
+    for i, (lin, x, y) in enumerate(zip(lins, xs, ys)):
+        arr[i] = n.QmmProblem(y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(),
+                              lin.N, lin.K)
+    n.check(n.lib().eq_quantized_matmul_batched(arr, len(lins), xs[0].shape[0], True, gs, bits, b"affine",
+                                                n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, stream))
 
 
-def time_graph(g, steps, warmup):
-    import torch
-
-    for _ in range(warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        g.replay()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per replay
-
-
-def bench_decode_stack(layers, M, steps, warmup):
-    """The headline: all 7 linears of all layers at batch M, as one graph."""
+def decode_step_fn(layers, M, groups):
+    """Step of all layers' projections at batch M; groups=None issues one launch per
+    projection, else one grouped launch per listed set.  Returns (fn, launches)."""
     import torch
 
     xs = {K: torch.randn((M, K), device="cuda").to(torch.bfloat16) for K in (HIDDEN, FFN)}
-    ys = {N: torch.empty((M, N), device="cuda", dtype=torch.bfloat16) for N in (HIDDEN, FFN, KV)}
+    ys = {name: torch.empty((M, N), device="cuda", dtype=torch.bfloat16) for name, N, K in LAYER_SHAPES}
+    Ks = {name: K for name, N, K in LAYER_SHAPES}
 
-    def step():
+    def step(stream):
         for layer in layers:
-            for (name, N, K), lin in zip(LAYER_SHAPES, layer):
-                run_qmv(lin, xs[K], ys[N])
+            if groups is None:
+                for name, _, K in LAYER_SHAPES:
+                    run_one(layer[name], xs[K], ys[name], stream)
+            else:
+                for g in groups:
+                    run_group([layer[n] for n in g], [xs[Ks[n]] for n in g], [ys[n] for n in g], stream)
 
-    g = capture(step)
-    ms = time_graph(g, steps, warmup)
+    launches = len(layers) * (len(LAYER_SHAPES) if groups is None else len(groups))
+    return step, launches
+
+
+def bench_decode(layers, M, groups, steps, warmup):
+    step, launches = decode_step_fn(layers, M, groups)
+    ms = Timer(step).ms_per_replay(steps, warmup)
     nbytes = len(layers) * sum(qmv_bytes(M, N, K) for _, N, K in LAYER_SHAPES)
-    return ms, nbytes, len(layers) * len(LAYER_SHAPES)
+    return ms, nbytes, launches
 
 
 def bench_per_shape(layers, M, steps, warmup):
     import torch
 
     out = {}
-    for i, (name, N, K) in enumerate(LAYER_SHAPES):
-        if name in ("v", "up"):
-            continue  # same shapes as k and gate
+    for name, N, K in LAYER_SHAPES:
+        if name in ("v", "up", "o"):
+            continue  # same shapes as k, gate, q
         x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
         y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
-        g = capture(lambda: [run_qmv(layer[i], x, y) for layer in layers])
-        ms = time_graph(g, max(steps // 2, 10), warmup)
-        us = ms * 1e3 / len(layers)
+        t = Timer(lambda st: [run_one(layer[name], x, y, st) for layer in layers])
+        us = t.ms_per_replay(max(steps // 2, 10), warmup) * 1e3 / len(layers)
         gbs = qmv_bytes(M, N, K) / (us * 1e-6) / 1e9
-        out[f"{N}x{K}"] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        out[f"{N}x{K}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     return out
 
 
@@ -158,8 +186,8 @@ def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
             for M in Ms:
                 x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
                 y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
-                g = capture(lambda: [run_qmv(l, x, y, bits=bits) for l in lins])
-                ms = time_graph(g, max(steps // 4, 5), warmup) / len(lins)
+                t = Timer(lambda st: [run_one(l, x, y, st, bits=bits) for l in lins])
+                ms = t.ms_per_replay(max(steps // 4, 5), warmup) / len(lins)
                 tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
                 out[f"b{bits} M{M} {N}x{K}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
                                                 "frac_mfma": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
@@ -174,6 +202,7 @@ def bench_gguf(steps, warmup):
 
     from eredu_amd import gguf as G
 
+    n = _lib()
     rows, cols = 4096, 14336
     out = {}
     for ty in (G.GgmlType.Q4_0, G.GgmlType.Q8_0, G.GgmlType.Q4K):
@@ -181,28 +210,25 @@ def bench_gguf(steps, warmup):
         nraw = rows * cols // vals * nbytes
         copies = 3
         raws = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(copies)]
-        desc = G.TensorDescriptor("t", [cols, rows], ty, nraw)
         dense = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
         bits, gs = G.affine_config(ty)
         aw = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device="cuda")
         asb = torch.empty((rows, cols // gs), dtype=torch.float16, device="cuda")
         abb = torch.empty_like(asb)
-        from eredu_amd import _native
 
-        def deq():
+        def deq(st):
             for r in raws:
-                G.dequantize(desc, r, G.Endian.Little, G.DequantDefinition.Affine, torch.bfloat16, out=dense)
+                n.check(n.lib().eq_gguf_dequantize(dense.data_ptr(), r.data_ptr(), nraw, int(ty), rows, cols, 0,
+                                                   n.EQ_DEQUANT_AFFINE, n.EQ_DTYPE_BF16, st))
 
-        def conv():
+        def conv(st):
             for r in raws:
-                _native.check(_native.lib().eq_gguf_convert_affine(
-                    aw.data_ptr(), asb.data_ptr(), abb.data_ptr(), r.data_ptr(), nraw, int(ty), rows, cols, 0,
-                    _stream()))
+                n.check(n.lib().eq_gguf_convert_affine(aw.data_ptr(), asb.data_ptr(), abb.data_ptr(), r.data_ptr(),
+                                                       nraw, int(ty), rows, cols, 0, st))
 
         for label, fn, out_bytes in (("dequant_bf16", deq, rows * cols * 2),
                                      ("convert_affine_g32", conv, aw.numel() * 4 + 2 * asb.numel() * 2)):
-            g = capture(fn)
-            ms = time_graph(g, max(steps // 4, 5), warmup) / copies
+            ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / copies
             gbs = (nraw + out_bytes) / (ms * 1e-3) / 1e9
             out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
@@ -211,15 +237,31 @@ def bench_gguf(steps, warmup):
     return out
 
 
-def cpu_baseline(layer, budget_s=12.0):
-    """The restated MLX CPU quantized matmul (oracle/eq_oracle.c or_qmm_t_f32),
-    on the same packed inputs of one layer's 7 linears at M = 1."""
+def bench_decode_variants(layers, args):
+    """The decode step issued other ways: one launch per projection (the drop-in
+    path), all seven projections per launch, and the grouped step at M = 8."""
+    out = {}
+    steps = max(args.steps // 2, 5)
+    for key, M, groups, what in (("decode_M1_per_projection", 1, None, "one launch per projection (drop-in path)"),
+                                 ("decode_M1_all7_per_launch", 1, ALL7, "seven projections per launch"),
+                                 ("decode_M8_grouped", 8, DECODE_GROUPS, "grouped launches")):
+        log(f"[bench] decode step M={M}, {what}")
+        ms, nb, launches = bench_decode(layers, M, groups, steps, args.warmup)
+        out[key] = {"ms": round(ms, 4), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "launches": launches}
+    return out
+
+
+def cpu_baseline(layer, budget_s=20.0):
+    """The restated MLX CPU quantized matmul (oracle/eq_oracle.c or_qmm_t_f32), on the
+    same packed inputs of one layer's 7 projections at M = 1, single-threaded and
+    with one thread per host core (at most 16, the box's CPU share)."""
     import torch
 
     from oracle import oracle as orc
 
     host = []
-    for (name, N, K), lin in zip(LAYER_SHAPES, layer):
+    for name, N, K in LAYER_SHAPES:
+        lin = layer[name]
         host.append((N, K, lin.w.cpu().numpy().view(np.uint32), lin.s.view(torch.int16).cpu().numpy().view(np.uint16),
                      lin.b.view(torch.int16).cpu().numpy().view(np.uint16)))
     x = {K: np.ascontiguousarray(orc.f32_to_bf16_bits(np.random.default_rng(0).standard_normal((1, K), dtype=np.float32)))
@@ -233,58 +275,77 @@ def cpu_baseline(layer, budget_s=12.0):
                 orc.qmm_t_f32(x[K], orc.BF16, w, s, b, orc.BF16, 1, N, K, GS, BITS, threads=nthreads)
             reps += 1
             el = time.perf_counter() - t0
-            if el > budget_s / 2 or reps >= 50:
+            if el > budget_s / 2 or reps >= 200:
                 break
         nbytes = reps * sum(qmv_bytes(1, N, K) for N, K, *_ in host)
         res[nthreads] = (nbytes / el / 1e9, reps, el)
     return res, threads
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmv_lds_decode_M1_grouped.md")
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the headline kernel from the committed PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs of this same command, scaled by a copy-kernel
+    calibration); None if the summary is absent."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--quick", action="store_true", help="headline only (no qmm / gguf / per-shape sweeps)")
+    ap.add_argument("--quick", action="store_true", help="decode steps only (no qmm / gguf / per-shape sweeps)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="the headline step only (the run a kernel-trace profile of the roofline kernel uses)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build is single-GPU)",
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build runs on a single GPU "
+              f"only (one GPU's share of a sharded projection is the same kernel at a smaller N or K)",
               file=sys.stderr)
         sys.exit(2)
 
     import torch
 
-    from eredu_amd import _native
-
-    _native.lib()
+    _lib().lib()
     torch.cuda.set_device(0)
     gen = torch.Generator(device="cuda").manual_seed(0)
     log("[bench] allocating 32 layers of 4-bit weights")
-    layers = [[Linear(N, K, gen) for _, N, K in LAYER_SHAPES] for _ in range(LAYERS)]
+    layers = [{name: Linear(N, K, gen) for name, N, K in LAYER_SHAPES} for _ in range(LAYERS)]
     torch.cuda.synchronize()
 
-    log("[bench] decode stack M=1")
-    ms, nbytes, launches = bench_decode_stack(layers, 1, args.steps, args.warmup)
+    log("[bench] decode step M=1, grouped launches")
+    ms, nbytes, launches = bench_decode(layers, 1, DECODE_GROUPS, args.steps, args.warmup)
     value = nbytes / (ms * 1e-3) / 1e9
-    detail = {}
-    log("[bench] decode stack M=8")
-    ms8, nbytes8, _ = bench_decode_stack(layers, 8, max(args.steps // 2, 5), args.warmup)
-    detail["decode_stack_M8_GB/s"] = round(nbytes8 / (ms8 * 1e-3) / 1e9, 1)
+    detail = {"decode_M1_grouped": {"ms": round(ms, 4), "GB/s": round(value, 1), "launches": launches}}
+    if args.headline_only:
+        args.quick = args.no_cpu = True
+    else:
+        detail.update(bench_decode_variants(layers, args))
     if not args.quick:
         log("[bench] per-shape qmv")
-        detail["qmv_M1"] = bench_per_shape(layers, 1, args.steps, args.warmup)
-        detail["qmv_M8"] = bench_per_shape(layers, 8, args.steps, args.warmup)
+        detail["qmv_M1_per_shape"] = bench_per_shape(layers, 1, args.steps, args.warmup)
+        detail["qmv_M8_per_shape"] = bench_per_shape(layers, 8, args.steps, args.warmup)
 
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline")
         res, threads = cpu_baseline(layers[0])
-        v1 = res[1]
-        vt = res[threads]
+        v1, vt = res[1], res[threads]
         cpu = {"value": round(vt[0], 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"one layer's 7 linears (122.8 MB packed) at M=1, {vt[1]} passes in {vt[2]:.1f} s; "
-                         f"restated MLX CPU _qmm_t loop (oracle/eq_oracle.c or_qmm_t_f32), f32 accumulate",
+               "sample": f"one layer's 7 projections (122.8 MB packed) at M=1: {vt[1]} passes in {vt[2]:.1f} s on "
+                         f"{threads} threads ({v1[1]} passes in {v1[2]:.1f} s on 1 thread: "
+                         f"{v1[0]:.3f} GB/s); restated MLX CPU _qmm_t loop (oracle/eq_oracle.c or_qmm_t_f32), "
+                         f"f32 accumulate",
                "single_thread_GB/s": round(v1[0], 3)}
     del layers
     torch.cuda.empty_cache()
@@ -311,20 +372,22 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (random 4-bit codes, bf16 scales/biases, x ~ N(0,1) bf16)",
         "config": {
-            "workload": "decode qmv sweep: Llama-3-8B linears q,k,v,o,gate,up,down x 32 layers, M=1, "
-                        "4-bit group-64, bf16 activations/scales/biases, one HIP graph per step",
+            "workload": "decode qmv sweep (configs[1]): Llama-3-8B projections q,k,v,o,gate,up,down x 32 layers, "
+                        "M=1, 4-bit group-64, bf16 activations/scales/biases; one grouped launch per input-sharing "
+                        "set {q,k,v},{o},{gate,up},{down}; one HIP graph per step",
             "M": 1, "layers": LAYERS, "bits": BITS, "group_size": GS,
             "bytes_per_step": nbytes, "launches_per_step": launches,
         },
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "qmv_mfma_kernel<4,64,BF16T,1>",
+            "kernel": "qmv_lds_kernel<4,64,BF16T,1,true>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
+            "traffic_source": "profiles/qmv_lds_decode_M1_grouped.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
             "per_launch_bytes": int(per_launch_bytes),
             "avg_launch_us": round(avg_launch_us, 3),
         },

@@ -19,6 +19,7 @@ from .quantization import (
     dequantize,
     dequantize_with_mode,
     quantized_matmul,
+    quantized_matmul_batched,
     quantized_matmul_with_mode,
     quantized_packed_dimension,
 )
@@ -32,6 +33,7 @@ __all__ = [
     "dequantize",
     "dequantize_with_mode",
     "quantized_matmul",
+    "quantized_matmul_batched",
     "quantized_matmul_with_mode",
     "quantized_packed_dimension",
 ]

@@ -26,6 +26,17 @@ SIGNATURES = {
     "eq_gguf_dequantize": ([_vp, _vp, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _vp], _i32),
 }
 
+
+
+class QmmProblem(ctypes.Structure):
+    """eq_qmm_problem of include/eredu_hip.h."""
+
+    _fields_ = [("y", _vp), ("x", _vp), ("w", _vp), ("scales", _vp), ("biases", _vp), ("N", _i64), ("K", _i64)]
+
+
+SIGNATURES["eq_quantized_matmul_batched"] = (
+    [ctypes.POINTER(QmmProblem), _i32, _i64, _b, _i32, _i32, ctypes.c_char_p, _i32, _i32, _vp], _i32)
+
 _lib = None
 _lock = threading.Lock()
 

@@ -10,6 +10,7 @@
 // false, ragged N) runs the f32 kernels below.  There is no host fallback: a
 // shape no kernel takes is an error.
 #include <cstring>
+#include <vector>
 #include <type_traits>
 
 #include "eq_common.hpp"
@@ -30,8 +31,6 @@ int check_launch(const char* what) {
     return 0;
 }
 
-bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
-                     const void* s, const void* b, int M, int N, int K, hipStream_t st);
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, hipStream_t st);
 
@@ -268,6 +267,69 @@ extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, co
         return 1;
     }
     return check_launch("quantized_matmul (general)");
+}
+
+extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int count, int64_t M, bool transpose,
+                                           int group_size, int bits, const char* mode, int x_dtype, int scale_dtype,
+                                           eq_stream_t stream) {
+    clear_error();
+    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype)) {
+        set_error("invalid dtype code");
+        return 1;
+    }
+    if (count < 0 || M < 0 || (count > 0 && problems == nullptr)) {
+        set_error("invalid problem list");
+        return 1;
+    }
+    for (int i = 0; i < count; i++) {
+        const eq_qmm_problem& p = problems[i];
+        if (p.N <= 0 || p.K <= 0 || p.N > INT32_MAX || p.K > INT32_MAX) {
+            set_error("problem " + std::to_string(i) + ": N and K must be in [1, 2^31 - 1]");
+            return 1;
+        }
+        const int64_t packed_dim = transpose ? p.K : p.N;
+        if (packed_dim % group_size != 0) {
+            set_error("problem " + std::to_string(i) + ": the quantized dimension (" + std::to_string(packed_dim) +
+                      ") is not divisible by group_size " + std::to_string(group_size));
+            return 1;
+        }
+        if (!p.y || !p.x || !p.w || !p.scales) {
+            set_error("problem " + std::to_string(i) + ": null pointer argument");
+            return 1;
+        }
+    }
+    if (M == 0 || count == 0) return 0;
+    if (M > INT32_MAX) {
+        set_error("dimension exceeds 2^31 - 1");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    // Decode-shaped groups go to one grouped launch per kQmvMaxProblems problems.
+    bool grouped = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
+                   (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && M <= 16;
+    std::vector<QmvSpec> specs;
+    for (int i = 0; i < count && grouped; i++) {
+        const eq_qmm_problem& p = problems[i];
+        grouped = p.N % 16 == 0 && aligned(p.x, 16) && aligned(p.w, 16);
+        specs.push_back(QmvSpec{static_cast<const uint16_t*>(p.x), p.w, p.scales, p.biases, static_cast<uint16_t*>(p.y),
+                                int(p.N), int(p.K), int(p.N)});
+    }
+    if (grouped && launch_qmv_batched(bits, group_size, scale_dtype, specs.data(), count, int(M), st))
+        return check_launch("quantized_matmul_batched (qmv)");
+    // Otherwise one call per problem (same results: every problem runs the
+    // same kernels either way).
+    for (int i = 0; i < count; i++) {
+        const eq_qmm_problem& p = problems[i];
+        const int r = eq_quantized_matmul(p.y, p.x, p.w, p.scales, p.biases, M, p.N, p.K, transpose, group_size, bits,
+                                          mode, x_dtype, scale_dtype, stream);
+        if (r != 0) {
+            const std::string msg = "problem " + std::to_string(i) + ": " + eq_last_error();
+            set_error(msg);
+            return r;
+        }
+    }
+    return 0;
 }
 
 extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases, int64_t rows,

@@ -22,6 +22,25 @@ int check_launch(const char* what);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// One matrix-vector problem of a (possibly grouped) decode launch:
+// y[M, ldy] (columns [0, N)) = x[M, K] . W^T, W = [N, K] packed along K.
+struct QmvSpec {
+    const uint16_t* x;
+    const uint32_t* w;
+    const void* s;
+    const void* b;  // may be null
+    uint16_t* y;
+    int N, K, ldy;
+};
+
+// Decode (small-M) launchers of qmv.hip.  launch_qmv_mfma takes one problem;
+// launch_qmv_batched takes several sharing M, bits, group size and scale type
+// and returns false, launching nothing, if the grouped path cannot take them
+// all (the caller then issues them one by one).
+bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                     const void* s, const void* b, int M, int N, int K, hipStream_t st);
+bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st);
+
 // ---------------------------------------------------------------- device side
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -30,6 +30,7 @@
 //   acc += s * t + (b - 128 s) * xs         (f32, per span)
 // Waves combine through LDS; the result is rounded once to bf16.
 #include <atomic>
+#include <vector>
 
 #include "eq_common.hpp"
 
@@ -756,26 +757,23 @@ static int device_lds_bytes() {
     return v;
 }
 
-// One matrix-vector problem of a (possibly grouped) decode launch.
-struct QmvSpec {
-    const uint16_t* x;
-    const uint32_t* w;
-    const void* s;
-    const void* b;
-    uint16_t* y;
-    int N, K, ldy;
+// Launch plan of the persistent LDS variant.
+struct QmvLdsPlan {
+    QmvBatch B;
+    int lds, grid;
+    bool vec;
 };
 
-// Plans and launches the persistent LDS variant for `count` problems sharing
-// bits, group size, scale type and M (<= MB).  Returns false, launching
-// nothing, when the problems do not fit it (too many, LDS too small, buffers
-// of 2^31 bytes or more, N % 16 != 0).
+// Plans the persistent LDS variant for `count` problems sharing bits, group
+// size, scale type and M (<= MB).  Returns false when the problems do not fit
+// it (too many, LDS too small, buffers of 2^31 bytes or more, N % 16 != 0).
 template <int BITS, int GS, typename ST>
-static bool launch_qmv_lds(const QmvSpec* specs, int count, int M, hipStream_t st) {
+static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& plan) {
     typedef QmvGeom<BITS, GS> Geo;
     constexpr int W = kQmvLdsWaves, U = kQmvUnroll;
     if (count < 1 || count > kQmvMaxProblems || M < 1 || M > Geo::MB) return false;
-    QmvBatch B{};
+    QmvBatch& B = plan.B;
+    B = QmvBatch{};
     B.count = count;
     B.M = M;
     const int pbytes = QmvParamWords<BITS, GS, U>::WORDS * 4;
@@ -817,21 +815,62 @@ static bool launch_qmv_lds(const QmvSpec* specs, int count, int M, hipStream_t s
     B.red_lds = lds;
     lds += 2 * W * M * 16 * 4;
     if (lds > device_lds_bytes()) return false;
-    const int grid = tiles < 2 * device_cu_count() ? tiles : 2 * device_cu_count();
+    plan.lds = lds;
+    plan.vec = vec;
+    // Workgroups resident per CU: 8 waves (2 per SIMD, the register budget).
+    const int per_cu = 8 / W > 0 ? 8 / W : 1;
+    plan.grid = tiles < per_cu * device_cu_count() ? tiles : per_cu * device_cu_count();
+    return true;
+}
+
+template <int BITS, int GS, typename ST>
+static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
+    constexpr int W = kQmvLdsWaves;
     auto go = [&](auto kernel) {
         // (a refusal surfaces as a launch error)
-        if (lds > 65536)
+        if (plan.lds > 65536)
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      lds);
-        kernel<<<dim3(unsigned(grid)), dim3(64 * W), size_t(lds), st>>>(B);
+                                      plan.lds);
+        kernel<<<dim3(unsigned(plan.grid)), dim3(64 * W), size_t(plan.lds), st>>>(plan.B);
     };
-    if (M == 1) {
-        if (vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true>);
+    if (plan.B.M == 1) {
+        if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true>);
         else go(qmv_lds_kernel<BITS, GS, ST, 1, false>);
     } else {
-        if (vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true>);
+        if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true>);
         else go(qmv_lds_kernel<BITS, GS, ST, 4, false>);
     }
+}
+
+template <int BITS, int GS, typename ST>
+static bool launch_qmv_lds(const QmvSpec* specs, int count, int M, hipStream_t st) {
+    QmvLdsPlan plan;
+    if (!plan_qmv_lds<BITS, GS, ST>(specs, count, M, plan)) return false;
+    run_qmv_lds<BITS, GS, ST>(plan, st);
+    return true;
+}
+
+// Grouped decode launch: problems in groups of kQmvMaxProblems, activation
+// rows in chunks of MB; every launch is planned before any is issued.
+template <int BITS, int GS, typename ST>
+static bool launch_qmv_group_t(const QmvSpec* specs, int count, int M, hipStream_t st) {
+    typedef QmvGeom<BITS, GS> Geo;
+    std::vector<QmvLdsPlan> plans;
+    QmvSpec chunk[kQmvMaxProblems];
+    for (int m0 = 0; m0 < M; m0 += Geo::MB) {
+        const int mc = M - m0 < Geo::MB ? M - m0 : Geo::MB;
+        for (int i0 = 0; i0 < count; i0 += kQmvMaxProblems) {
+            const int n = count - i0 < kQmvMaxProblems ? count - i0 : kQmvMaxProblems;
+            for (int i = 0; i < n; i++) {
+                chunk[i] = specs[i0 + i];
+                chunk[i].x += int64_t(m0) * chunk[i].K;
+                chunk[i].y += int64_t(m0) * chunk[i].ldy;
+            }
+            plans.emplace_back();
+            if (!plan_qmv_lds<BITS, GS, ST>(chunk, n, mc, plans.back())) return false;
+        }
+    }
+    for (const QmvLdsPlan& plan : plans) run_qmv_lds<BITS, GS, ST>(plan, st);
     return true;
 }
 
@@ -906,6 +945,28 @@ bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint1
     } else if (bits == 8) {
         if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, st);
         if (scale_dtype == EQ_DTYPE_F16) return launch_qmv_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, st);
+    }
+    return false;
+}
+
+template <int BITS, typename ST>
+static bool launch_qmv_group_gs(int gs, const QmvSpec* specs, int count, int M, hipStream_t st) {
+    switch (gs) {
+    case 32: return launch_qmv_group_t<BITS, 32, ST>(specs, count, M, st);
+    case 64: return launch_qmv_group_t<BITS, 64, ST>(specs, count, M, st);
+    case 128: return launch_qmv_group_t<BITS, 128, ST>(specs, count, M, st);
+    default: return false;
+    }
+}
+
+// Preconditions as for launch_qmv_mfma, for every problem.
+bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st) {
+    if (bits == 4) {
+        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_group_gs<4, BF16T>(gs, specs, count, M, st);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmv_group_gs<4, F16T>(gs, specs, count, M, st);
+    } else if (bits == 8) {
+        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_group_gs<8, BF16T>(gs, specs, count, M, st);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmv_group_gs<8, F16T>(gs, specs, count, M, st);
     }
     return false;
 }

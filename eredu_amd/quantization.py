@@ -11,7 +11,7 @@ containers.
 from __future__ import annotations
 
 import enum
-from typing import Optional
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -93,32 +93,7 @@ def quantized_matmul_with_mode(
     mode.validate(group_size, bits)
     if mode is not QuantizationMode.Affine:
         raise EreduError("only affine quantization is implemented on the device path")
-    _require_device(x, w, scales, biases)
-    w = _words(w)
-    if w.dim() != 2 or scales.dim() != 2:
-        raise EreduError("w and scales must be 2-D")
-    if bits not in (2, 3, 4, 5, 6, 8):
-        raise EreduError(f"bits must be one of 2, 3, 4, 5, 6, 8, got {bits}")
-    if transpose:
-        N = w.shape[0]
-        K = w.shape[1] * 32 // bits
-    else:
-        K = w.shape[0]
-        N = w.shape[1] * 32 // bits
-    if x.shape[-1] != K:
-        raise EreduError(
-            f"shapes {tuple(x.shape)} and {tuple(w.shape)} are incompatible for quantized matmul "
-            f"(x's last dimension must be {K})"
-        )
-    packed_dim = K if transpose else N
-    if group_size <= 0 or packed_dim % group_size != 0:
-        raise EreduError(f"the quantized dimension {packed_dim} is not divisible by group_size {group_size}")
-    expect_scales = (w.shape[0], packed_dim // group_size)
-    if tuple(scales.shape) != expect_scales:
-        raise EreduError(f"scales has shape {tuple(scales.shape)}, expected {expect_scales}")
-    if biases is not None:
-        if tuple(biases.shape) != expect_scales or biases.dtype != scales.dtype:
-            raise EreduError("biases must match scales in shape and dtype")
+    N, K = _check_operands(x, w, scales, biases, transpose, group_size, bits)
     x_code = _dtype_code(x, "x")
     s_code = _dtype_code(scales, "scales")
     x2 = x.reshape(-1, K).contiguous()
@@ -149,6 +124,82 @@ def quantized_matmul(
     """Affine quantized matmul with safemlx's defaults (transpose=False, gs 64,
     bits 4; safemlx/src/ops/quantization.rs:165-184)."""
     return quantized_matmul_with_mode(x, w, scales, biases, transpose, group_size, bits, QuantizationMode.Affine)
+
+
+def _check_operands(x, w, scales, biases, transpose, group_size, bits):
+    """Shape/dtype rules of quantized_matmul_with_mode; returns (N, K)."""
+    _require_device(x, w, scales, biases)
+    _words(w)
+    if w.dim() != 2 or scales.dim() != 2:
+        raise EreduError("w and scales must be 2-D")
+    if bits not in (2, 3, 4, 5, 6, 8):
+        raise EreduError(f"bits must be one of 2, 3, 4, 5, 6, 8, got {bits}")
+    if transpose:
+        N, K = w.shape[0], w.shape[1] * 32 // bits
+    else:
+        K, N = w.shape[0], w.shape[1] * 32 // bits
+    if x.shape[-1] != K:
+        raise EreduError(
+            f"shapes {tuple(x.shape)} and {tuple(w.shape)} are incompatible for quantized matmul "
+            f"(x's last dimension must be {K})"
+        )
+    packed_dim = K if transpose else N
+    if group_size <= 0 or packed_dim % group_size != 0:
+        raise EreduError(f"the quantized dimension {packed_dim} is not divisible by group_size {group_size}")
+    expect_scales = (w.shape[0], packed_dim // group_size)
+    if tuple(scales.shape) != expect_scales:
+        raise EreduError(f"scales has shape {tuple(scales.shape)}, expected {expect_scales}")
+    if biases is not None and (tuple(biases.shape) != expect_scales or biases.dtype != scales.dtype):
+        raise EreduError("biases must match scales in shape and dtype")
+    return N, K
+
+
+def quantized_matmul_batched(
+    problems: Sequence[Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]],
+    transpose: bool = True,
+    group_size: int = DEFAULT_GROUP_SIZE,
+    bits: int = DEFAULT_BITS,
+    mode: QuantizationMode = QuantizationMode.Affine,
+) -> List[torch.Tensor]:
+    """Several independent quantized matmuls ``(x, w, scales, biases)`` that share
+    the encoding and the activation row count, e.g. the q/k/v projections of one
+    decoder layer (eredu-architectures/src/llama.rs:272-295).  Returns the same
+    tensors as one quantized_matmul_with_mode call per problem, bit for bit
+    (C ABI: eq_quantized_matmul_batched), from as few kernel launches as the
+    device path allows."""
+    mode.validate(group_size, bits)
+    if mode is not QuantizationMode.Affine:
+        raise EreduError("only affine quantization is implemented on the device path")
+    if not problems:
+        return []
+    x0, _, s0, _ = problems[0]
+    x_code, s_code = _dtype_code(x0, "x"), _dtype_code(s0, "scales")
+    keep, outs = [], []
+    arr = (_native.QmmProblem * len(problems))()
+    M = None
+    for i, (x, w, scales, biases) in enumerate(problems):
+        N, K = _check_operands(x, w, scales, biases, transpose, group_size, bits)
+        if x.dtype != x0.dtype or scales.dtype != s0.dtype:
+            raise EreduError("all problems of a batch must share the activation and scale dtypes")
+        x2 = x.reshape(-1, K).contiguous()
+        if M is None:
+            M = x2.shape[0]
+        elif x2.shape[0] != M:
+            raise EreduError("all problems of a batch must have the same number of activation rows")
+        w, scales = w.contiguous(), scales.contiguous()
+        biases = biases.contiguous() if biases is not None else None
+        y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+        keep += [x2, w, scales, biases]
+        outs.append((y, x.shape[:-1], N))
+        arr[i] = _native.QmmProblem(y.data_ptr(), x2.data_ptr(), w.data_ptr(), scales.data_ptr(),
+                                    biases.data_ptr() if biases is not None else None, N, K)
+    check(
+        _native.lib().eq_quantized_matmul_batched(
+            arr, len(problems), M, bool(transpose), int(group_size), int(bits), mode.value.encode(), x_code, s_code,
+            _stream(),
+        )
+    )
+    return [y.reshape(*lead, N) for y, lead, N in outs]
 
 
 def dequantize_with_mode(

@@ -69,6 +69,33 @@ int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
                         int group_size, int bits, const char* mode, int x_dtype,
                         int scale_dtype, eq_stream_t stream);
 
+/* One problem of a grouped quantized matmul: y[M, N] = x[M, K] . W^T (or . W). */
+typedef struct eq_qmm_problem {
+    void* y;
+    const void* x;
+    const uint32_t* w;
+    const void* scales;
+    const void* biases; /* may be NULL */
+    int64_t N;
+    int64_t K;
+} eq_qmm_problem;
+
+/*
+ * Grouped quantized matmul: `count` independent problems that share M,
+ * transpose, group_size, bits, mode and dtypes, with the results of `count`
+ * eq_quantized_matmul calls (bit for bit: each problem runs the same kernel
+ * code either way).  Decode-shaped groups (M <= 16, transpose, bf16 x) run as
+ * one persistent launch per 8 problems, which streams the weights of all of
+ * them back to back instead of paying a kernel launch per projection.
+ * No single counterpart in the reference's C ABI: it stands for the
+ * consecutive mlx_quantized_matmul calls (safemlx-sys/src/mlx-c/mlx/c/ops.h:809-819)
+ * that a decoder layer issues on one input, e.g. the q/k/v projections of
+ * eredu-architectures/src/llama.rs:272-295 or the gate/up pair of :414-423.
+ */
+int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int count, int64_t M, bool transpose,
+                                int group_size, int bits, const char* mode, int x_dtype, int scale_dtype,
+                                eq_stream_t stream);
+
 /*
  * Affine dequantize: out[r, c] = scale[r, c/gs] * q[r, c] + bias[r, c/gs],
  * computed in f32 (one multiply, one add) and written as out_dtype.

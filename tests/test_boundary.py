@@ -24,7 +24,7 @@ def declared_functions():
 
 def test_header_declares_the_boundary():
     assert declared_functions() == sorted(
-        ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_dequantize",
+        ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
          "eq_gguf_convert_affine", "eq_gguf_dequantize"]
     )
 

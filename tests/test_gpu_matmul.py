@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from eredu_amd import EreduError, QuantizedLinear, dequantize_with_mode, quantized_matmul, quantized_matmul_with_mode
+from eredu_amd import (EreduError, QuantizedLinear, dequantize_with_mode, quantized_matmul, quantized_matmul_batched,
+                       quantized_matmul_with_mode)
 from oracle import oracle as orc
 from tests.fixtures import (dev_bf16, dev_param, dev_words, host_bits16, host_f32, synthetic_linear,
                             synthetic_x)
@@ -162,3 +163,61 @@ def test_errors_surface_as_exceptions(cuda):
         quantized_matmul(x, w, s, s, transpose=True, group_size=48)
     with pytest.raises(EreduError, match="incompatible"):
         quantized_matmul(x[:, :64], w, s, s, transpose=True, group_size=48)
+
+
+def _batch_problems(specs, M, gs, bits, sdt=orc.BF16, seed=0, biases=True):
+    """(x, w, s, b) device tensors plus host copies for each (N, K) in specs;
+    problems with equal K share one activation tensor (as q/k/v do)."""
+    xs, probs, host = {}, [], []
+    for i, (N, K) in enumerate(specs):
+        if K not in xs:
+            xb = synthetic_x(M, K, seed + K)
+            xs[K] = (xb, dev_bf16(xb))
+        w, s, b = synthetic_linear(N, K, gs, bits, seed + 31 * i, scale_dtype=sdt)
+        bd = dev_param(b, sdt) if biases or i % 2 else None
+        probs.append((xs[K][1], dev_words(w), dev_param(s, sdt), bd))
+        host.append((xs[K][0], w, s, b if bd is not None else None, N, K))
+    return probs, host
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_batched_equals_separate_calls_bitwise(cuda, M):
+    # a decoder layer's projections: q, k, v, o, gate, up (x of K=4096) and down (K=14336), scaled down
+    specs = [(512, 1024), (128, 1024), (128, 1024), (512, 512), (1792, 1024), (1792, 1024), (1024, 3584)]
+    probs, host = _batch_problems(specs, M, 64, 4, seed=M, biases=False)
+    ys = quantized_matmul_batched(probs, transpose=True, group_size=64, bits=4)
+    torch.cuda.synchronize()
+    for (x, w, s, b), y, (xh, wh, sh, bh, N, K) in zip(probs, ys, host):
+        y1 = quantized_matmul_with_mode(x, w, s, b, True, 64, 4)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y1.view(torch.int16))
+        ref = orc.quantized_matmul_f64(xh, orc.BF16, wh, sh, bh, orc.BF16, True, 64, 4, N, K)
+        assert orc.matmul_within_tolerance(host_f32(y), ref, True)[0]
+
+
+@pytest.mark.parametrize("bits,gs,sdt", [(8, 32, orc.F16), (4, 128, orc.BF16), (4, 32, orc.F16)])
+def test_batched_more_than_one_launch_and_contract_grid(cuda, bits, gs, sdt):
+    # 11 problems (more than one grouped launch) with M = 5
+    specs = [(16 * (i + 1), 256 * (1 + i % 3)) for i in range(11)]
+    probs, host = _batch_problems(specs, 5, gs, bits, sdt=sdt, seed=bits + gs)
+    ys = quantized_matmul_batched(probs, transpose=True, group_size=gs, bits=bits)
+    torch.cuda.synchronize()
+    for y, (xh, wh, sh, bh, N, K) in zip(ys, host):
+        ref = orc.quantized_matmul_f64(xh, orc.BF16, wh, sh, bh, sdt, True, gs, bits, N, K)
+        assert orc.matmul_within_tolerance(host_f32(y), ref, True)[0]
+
+
+def test_batched_falls_back_per_problem(cuda):
+    # transpose=False and N % 16 != 0 are not decode-grouped; results still match
+    specs = [(40, 256), (48, 256)]
+    probs, host = _batch_problems(specs, 2, 32, 4, seed=5)
+    ys = quantized_matmul_batched(probs, transpose=True, group_size=32, bits=4)
+    torch.cuda.synchronize()
+    for y, (xh, wh, sh, bh, N, K) in zip(ys, host):
+        ref = orc.quantized_matmul_f64(xh, orc.BF16, wh, sh, bh, orc.BF16, True, 32, 4, N, K)
+        assert orc.matmul_within_tolerance(host_f32(y), ref, True)[0]
+    with pytest.raises(EreduError, match="same number of activation rows"):
+        x2 = torch.zeros(2, 256, dtype=torch.bfloat16, device="cuda")
+        x3 = torch.zeros(3, 256, dtype=torch.bfloat16, device="cuda")
+        quantized_matmul_batched([(x2, probs[0][1], probs[0][2], None), (x3, probs[0][1], probs[0][2], None)],
+                                 group_size=32)
