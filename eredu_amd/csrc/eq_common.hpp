@@ -47,6 +47,28 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Buffer resource (V#) of a raw byte range: loads through it are range-checked
+// by the hardware, and an offset at or past `bytes` reads as zero.  Buffer
+// loads are also ordered against scheduling barriers, which plain loads from
+// read-only pointers are not.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+// A wave-uniform 1 that the compiler cannot see through.  `if (opaque_one())`
+// puts the guarded code in a basic block of its own: instruction selection
+// and the machine scheduler work per block, so a block of prefetch loads
+// placed before it is issued before it (within one block the schedulers
+// would sink the loads down to their uses and serialise the pipeline).
+__device__ __forceinline__ int opaque_one() {
+    int v;
+    asm volatile("s_mov_b32 %0, 1" : "=s"(v));
+    return v;
+}
+
+// An offset past every buffer the kernels build (all are < 2^31 bytes), leaving
+// room for the immediate offsets added to it.
+constexpr uint32_t kOutOfRange = 0xC0000000u;
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
