@@ -69,6 +69,20 @@ __device__ __forceinline__ int opaque_one() {
 // room for the immediate offsets added to it.
 constexpr uint32_t kOutOfRange = 0xC0000000u;
 
+// Pulls every 64-byte line of a kernel's by-value argument block into the
+// scalar cache with independent loads and one wait.  The block is cold at
+// each dispatch; without this, code that indexes it with computed values
+// (a problem table walked per tile) pays one memory round trip per line, in
+// sequence, before its first useful load.
+template <typename T>
+__device__ __forceinline__ void prefetch_args(const T& args) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(&args);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < int(sizeof(T) + 63) / 64; i++) acc ^= p[16 * i];
+    asm volatile("" ::"s"(acc));
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {

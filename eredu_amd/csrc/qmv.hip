@@ -30,6 +30,7 @@
 //   acc += s * t + (b - 128 s) * xs         (f32, per span)
 // Waves combine through LDS; the result is rounded once to bf16.
 #include <atomic>
+#include <type_traits>
 #include <vector>
 
 #include "eq_common.hpp"
@@ -44,11 +45,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct UnpackConsts {
     uint32_t nib_mask;  // 0x000f000f
     uint32_t bf16_128;  // 0x43004300: bf16 0x43XX = 128 + XX for XX < 128
+    uint32_t c43;       // 0x43434343 (uniform)
 };
 __device__ __forceinline__ UnpackConsts make_unpack_consts() {
     UnpackConsts c;
     asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(c.nib_mask));
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.bf16_128));
+    asm volatile("s_mov_b32 %0, 0x43434343" : "=s"(c.c43));
     return c;
 }
 
@@ -83,6 +86,31 @@ __device__ __forceinline__ bf16x8 unpack8_bf16(uint32_t w0, uint32_t w1) {
         p[2 * h + 1] = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
     }
     return __builtin_bit_cast(bf16x8, p);
+}
+
+// 8 consecutive 4-bit codes -> 8 bf16 values 128 + q in the slot order
+// (c0, c2, c4, c6, c1, c3, c5, c7): 7 VALU ops (two masks, a shift, four byte
+// permutes against the constant 0x43 bytes).  The activations of the A
+// operand must be permuted the same way (qmv_permute_x8).
+__device__ __forceinline__ bf16x8 unpack4_bf16_offset128_perm(uint32_t w, uint32_t c43) {
+    const uint32_t lo = w & 0x0f0f0f0fu;         // bytes: c0 c2 c4 c6
+    const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // bytes: c1 c3 c5 c7
+    u32x4 p;
+    p[0] = __builtin_amdgcn_perm(c43, lo, 0x04010400u);  // [lo.b0, 43, lo.b1, 43]
+    p[1] = __builtin_amdgcn_perm(c43, lo, 0x04030402u);  // [lo.b2, 43, lo.b3, 43]
+    p[2] = __builtin_amdgcn_perm(c43, hi, 0x04010400u);
+    p[3] = __builtin_amdgcn_perm(c43, hi, 0x04030402u);
+    return __builtin_bit_cast(bf16x8, p);
+}
+
+// 8 activations [x0 .. x7] (16 bytes) -> [x0, x2, x4, x6, x1, x3, x5, x7].
+__device__ __forceinline__ u32x4 qmv_permute_x8(u32x4 v) {
+    u32x4 o;
+    o[0] = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
+    o[2] = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);
+    o[3] = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);
+    return o;
 }
 
 #ifndef EQ_QMV_WAVES
@@ -145,6 +173,30 @@ struct QmvBlock {
     uint32_t sw[PWORDS], bw[PWORDS];
 };
 
+// Reads every register of a block in an empty asm statement, which makes the
+// compiler wait for the block's loads.  A compute guarded by opaque_one()
+// is followed by `else qmv_retire(block)`: the else path never runs, but
+// without it the compiler's wait analysis sees a path on which the block's
+// loads are still in flight after the guard, and the next load into those
+// registers then waits for every outstanding load, prefetches included.
+__device__ __forceinline__ void qmv_retire_reg(const u32x4& v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void qmv_retire_reg(const bf16x8& v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void qmv_retire_reg(uint32_t v) { asm volatile("" ::"v"(v)); }
+template <int BITS, int GS, int NU, bool VEC>
+__device__ __forceinline__ void qmv_retire(const QmvBlock<BITS, GS, NU, VEC>& b) {
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        qmv_retire_reg(b.wd[u]);
+#pragma unroll
+        for (int t = 0; t < QmvGeom<BITS, GS>::STEPS; t++) qmv_retire_reg(b.xa[u][t]);
+    }
+#pragma unroll
+    for (int i = 0; i < QmvBlock<BITS, GS, NU, VEC>::PWORDS; i++) {
+        qmv_retire_reg(b.sw[i]);
+        qmv_retire_reg(b.bw[i]);
+    }
+}
+
 // Loads `W` consecutive 32-bit words at byte offset `off` (16-, 8- or 4-byte loads).
 template <int W>
 __device__ __forceinline__ void load_words(uint32_t* d, __amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -198,19 +250,31 @@ __device__ __forceinline__ void qmv_load(QmvBlock<BITS, GS, NU, VEC>& b, const Q
 // acc += s * (x . (128 + q)) + (b - 128 s) * sum(x) per span (4-bit); the 8-bit
 // codes are exact, so acc += s * (x . q) + b * sum(x).
 // Element e of a row of 16-bit parameters held in 32-bit words, as f32.
-template <typename ST, int WORDS>
-__device__ __forceinline__ float pick_param(const uint32_t* words, int e) {
-    uint32_t w = words[0];
-#pragma unroll
-    for (int i = 1; i < WORDS; i++) w = (e >> 1) == i ? words[i] : w;
-    return param_bits_to_f32<ST>((e & 1) ? (w >> 16) : (w & 0xffffu));
+// Group element e = base + r_p of the 16-bit parameters held in 32-bit words,
+// as f32, for a lane whose result group r_p lies in [0, P): base (a
+// compile-time multiple of P) fixes the word up to the choice among P/2
+// words, and r_p's low bit picks the half.
+template <typename ST, int P>
+__device__ __forceinline__ float pick_param(const uint32_t* words, int base, int r_p) {
+    uint32_t w;
+    if (P <= 1) {
+        w = words[base >> 1];
+        w = (base & 1) ? (w >> 16) : w;
+        return param_bits_to_f32<ST>(w & 0xffffu);
+    }
+    w = words[base >> 1];
+    if (P == 4) w = (r_p >> 1) ? words[(base >> 1) + 1] : w;
+    if constexpr (std::is_same<ST, BF16T>::value)  // bf16 bits of the chosen half into an f32's top half
+        return __uint_as_float(__builtin_amdgcn_perm(0u, w, (r_p & 1) ? 0x03020c0cu : 0x01000c0cu));
+    else
+        return param_bits_to_f32<ST>((w >> ((r_p & 1) * 16)) & 0xffffu);
 }
 
 // One span of one 16-row tile: the group-split MFMAs on the A operand xa
 // (activations) and the codes wd, then acc += s * t + b' * xs with the span's
 // scale s and bias b of this lane's result group:
 // 4-bit: t = x . (128 + q), b' = b - 128 s; 8-bit: t = x . q, b' = b.
-template <int BITS, int GS, typename ST, int MREG>
+template <int BITS, int GS, typename ST, int MREG, bool PERM = false>
 __device__ __forceinline__ void qmv_span(f32x4& acc, const bf16x8* xa, const u32x4& wd, float sc, float bi,
                                          const UnpackConsts& uc, bf16x8 ones) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -220,7 +284,7 @@ __device__ __forceinline__ void qmv_span(f32x4& acc, const bf16x8* xa, const u32
     for (int t = 0; t < Geo::STEPS; t++) {
         bf16x8 bq;
         if (BITS == 4)
-            bq = unpack4_bf16_offset128(wd[t], uc);
+            bq = PERM ? unpack4_bf16_offset128_perm(wd[t], uc.c43) : unpack4_bf16_offset128(wd[t], uc);
         else
             bq = unpack8_bf16(wd[2 * t], wd[2 * t + 1]);
         t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], bq, t4, 0, 0, 0);
@@ -237,10 +301,9 @@ __device__ __forceinline__ void qmv_params(const uint32_t* sw, const uint32_t* b
                                            float& sc, float& bi) {
     typedef QmvGeom<BITS, GS> Geo;
     if constexpr (VEC && NU > 1) {
-        constexpr int PWORDS = QmvParamWords<BITS, GS, NU>::WORDS;
-        const int e = (u * Geo::SPAN) / GS + r_p;  // this lane's group, counted from the block's first
-        sc = pick_param<ST, PWORDS>(sw, e);
-        bi = pick_param<ST, PWORDS>(bw, e) * bias_on;
+        // this lane's group, counted from the block's first: (u * SPAN) / GS + r_p
+        sc = pick_param<ST, Geo::P>(sw, (u * Geo::SPAN) / GS, r_p);
+        bi = pick_param<ST, Geo::P>(bw, (u * Geo::SPAN) / GS, r_p) * bias_on;
     } else {
         sc = param_bits_to_f32<ST>(sw[u] & 0xffffu);
         bi = param_bits_to_f32<ST>(bw[u] & 0xffffu) * bias_on;
@@ -329,8 +392,10 @@ __global__ __launch_bounds__(64 * kQmvMaxWaves) __attribute__((amdgpu_waves_per_
         for (int i = 0; i + 1 < nblk; i += 2) {
             qmv_load<BITS, GS, U, VEC>(bb, L, j_begin + (i + 1) * U);
             if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, ba, r_p, bias_on, uc, ones);
+            else qmv_retire(ba);
             qmv_load<BITS, GS, U, VEC>(ba, L, j_begin + min(i + 2, nblk - 1) * U);
             if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, bb, r_p, bias_on, uc, ones);
+            else qmv_retire(bb);
         }
         if (nblk & 1) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, ba, r_p, bias_on, uc, ones);  // block nblk - 1
     }
@@ -411,6 +476,7 @@ struct QmvProblem {
     int tile0;           // first global tile of this problem
     int x_lds;           // LDS byte offset of its activations
     int kpad;            // activation row length in LDS (multiple of 64)
+    float inv_cpr;       // 1 / (kpad / 8): row of a 16-byte LDS chunk by multiplication
 };
 
 struct QmvBatch {
@@ -431,6 +497,17 @@ struct QmvWBlock {
     u32x4 wd[NU];
     uint32_t sw[PWORDS], bw[PWORDS];
 };
+
+template <int BITS, int GS, int NU, bool VEC>
+__device__ __forceinline__ void qmv_retire(const QmvWBlock<BITS, GS, NU, VEC>& b) {
+#pragma unroll
+    for (int u = 0; u < NU; u++) qmv_retire_reg(b.wd[u]);
+#pragma unroll
+    for (int i = 0; i < QmvWBlock<BITS, GS, NU, VEC>::PWORDS; i++) {
+        qmv_retire_reg(b.sw[i]);
+        qmv_retire_reg(b.bw[i]);
+    }
+}
 
 struct QmvTileLane {
     __amdgpu_buffer_rsrc_t wr, sr, br;
@@ -458,6 +535,38 @@ __device__ __forceinline__ void qmv_wload(QmvWBlock<BITS, GS, NU, VEC>& b, const
     for (int u = 0; u < NU; u++) b.wd[u] = __builtin_amdgcn_raw_buffer_load_b128(L.wr, wo + u * 64, 0, 0);
 }
 
+// qmv_wload for the ring: the wave-uniform part of each offset (block j0)
+// goes into the scalar offset operand, so that issuing a block takes no
+// vector instruction.  A lane offset at kOutOfRange still reads zero.
+template <int W>
+__device__ __forceinline__ void load_words_s(uint32_t* d, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    if constexpr (W >= 4) {
+#pragma unroll
+        for (int i = 0; i < W / 4; i++) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * i, soff, 0);
+            d[4 * i] = v[0], d[4 * i + 1] = v[1], d[4 * i + 2] = v[2], d[4 * i + 3] = v[3];
+        }
+    } else if constexpr (W == 2) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+        d[0] = v[0], d[1] = v[1];
+    } else {
+        d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+}
+
+template <int BITS, int GS, int NU>
+__device__ __forceinline__ void qmv_wload_ring(QmvWBlock<BITS, GS, NU, true>& b, const QmvTileLane& L, int j0) {
+    typedef QmvGeom<BITS, GS> Geo;
+    static_assert(NU > 1, "vector parameter loads");
+    const uint32_t so = __builtin_amdgcn_readfirstlane(uint32_t((j0 * Geo::SPAN) / GS) * 2u);
+    load_words_s<QmvWBlock<BITS, GS, NU, true>::PWORDS>(b.sw, L.sr, L.soff, so);
+    load_words_s<QmvWBlock<BITS, GS, NU, true>::PWORDS>(b.bw, L.br, L.soff, so);
+    const uint32_t wo = __builtin_amdgcn_readfirstlane(uint32_t(j0) * 64u);
+#pragma unroll
+    for (int u = 0; u < NU; u++) b.wd[u] = __builtin_amdgcn_raw_buffer_load_b128(L.wr, L.woff + u * 64, wo, 0);
+}
+
 // A operands of span j0 + u are read from LDS at xa_t + j0 * xstep + u * SPAN * 2
 // (dead rows have xstep 0 and xa_t in the zero block, which covers NU spans).
 template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC>
@@ -477,14 +586,29 @@ __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, G
             xa[t] = *reinterpret_cast<const bf16x8*>(smem + xb[t] + u * Geo::SPAN * 2);
         float sc, bi;
         qmv_params<BITS, GS, ST, NU, VEC>(b.sw, b.bw, u, r_p, bias_on, sc, bi);
-        qmv_span<BITS, GS, ST, MREG>(acc, xa, b.wd[u], sc, bi, uc, ones);
+        qmv_span<BITS, GS, ST, MREG, BITS == 4>(acc, xa, b.wd[u], sc, bi, uc, ones);
     }
 }
 
 #ifndef EQ_QMV_LDS_WAVES
 #define EQ_QMV_LDS_WAVES 4
 #endif
-constexpr int kQmvLdsWaves = EQ_QMV_LDS_WAVES;  // waves per workgroup of the LDS variant
+#ifndef EQ_QMV_RING
+#define EQ_QMV_RING 2
+#endif
+constexpr int kQmvLdsMaxWaves = 8;              // waves per workgroup of the LDS variant, at most
+constexpr int kQmvLdsWaves = EQ_QMV_LDS_WAVES;  // the planner's choice
+
+// Register blocks in the load ring of the LDS variant: loads run RING - 1
+// blocks ahead of the block being computed.  Measured on MI355X (decode
+// shapes of an 8B model), two blocks and four waves per workgroup beat
+// deeper rings and eight waves: more requests in flight per CU only queue.
+// With 32-wide groups a block carries twice the scale words; rings deeper
+// than three would not fit the 256 registers of two waves per SIMD.
+template <int BITS, int GS>
+struct QmvRing {
+    static constexpr int D = (BITS == 4 && GS == 32 && EQ_QMV_RING > 3) ? 3 : EQ_QMV_RING;
+};
 
 // Per-wave view of one tile: span range, buffers, offsets, A-operand addresses.
 template <int BITS, int GS>
@@ -496,7 +620,11 @@ struct QmvTileView {
     uint32_t xstep;
 };
 
-template <int BITS, int GS>
+// TAIL = false: every problem's K is a multiple of U * SPAN, so a wave's
+// range is whole blocks; a wave without blocks in a tile gets one virtual
+// block instead (loads out of range read zero, activations from the zero
+// block), so that every tile takes at least one block from the ring.
+template <int BITS, int GS, bool TAIL>
 __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& batch, int pi, int tile, int wave,
                                                               int ln, int kq, int a_m, bool a_live, int r_p) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -524,52 +652,154 @@ __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& b
         v.xa_t[t] = a_live ? uint32_t(pr.x_lds + a_m * pr.kpad * 2 + (((kq * Geo::CPL / 8 + t) ^ (a_m & 7)) * 16))
                            : uint32_t(batch.zero_lds);
     v.xstep = a_live ? Geo::SPAN * 2 : 0;
+    if (!TAIL && v.nblk == 0) {
+        v.nblk = 1;
+        v.j_begin = v.j_end = v.j_full_end = 0;
+        v.S_full = 1 << 20;  // no ragged span
+        v.L.woff = v.L.soff = kOutOfRange;
+#pragma unroll
+        for (int t = 0; t < Geo::STEPS; t++) v.xa_t[t] = uint32_t(batch.zero_lds);
+        v.xstep = 0;
+    }
     return v;
 }
 
-template <int BITS, int GS, typename ST, int MREG, bool VEC>
-__global__ __launch_bounds__(64 * kQmvLdsWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
+// Problem of global tile t, searching on from problem pi (tiles only grow).
+__device__ __forceinline__ int qmv_problem_of(const QmvBatch& batch, int t, int pi) {
+    while (pi + 1 < batch.count && t >= batch.p[pi + 1].tile0) pi++;
+    return __builtin_amdgcn_readfirstlane(pi);
+}
+
+// The load side of a wave: the full blocks of its span range in each tile of
+// its workgroup (tile, tile + gridDim.x, ...), one after the other.  Once the
+// stream is exhausted its loads go out of range (they read zero and touch no
+// memory), so that the ring keeps issuing loads without a data-dependent
+// branch around them: a conditional load would make the compiler wait for
+// every load before the join.
+struct QmvStream {
+    QmvTileLane L;
+    int tile, pi, j, j_stop;
+    bool done;
+};
+
+template <int BITS, int GS, bool TAIL>
+__device__ __forceinline__ void qmv_stream_seek(const QmvBatch& batch, QmvStream& st, int tile, int wave, int ln,
+                                                int kq, int r_p) {
+    for (; tile < batch.total_tiles; tile += gridDim.x) {
+        st.pi = qmv_problem_of(batch, tile, st.pi);
+        const QmvTileView<BITS, GS> v = qmv_tile_view<BITS, GS, TAIL>(batch, st.pi, tile, wave, ln, kq, 0, false, r_p);
+        if (v.nblk > 0) {
+            st.L = v.L;
+            st.tile = tile;
+            st.j = v.j_begin;
+            st.j_stop = v.j_begin + v.nblk * kQmvUnroll;
+            return;
+        }
+    }
+    st.done = true;
+    st.j = 0;
+    st.L.woff = st.L.soff = kOutOfRange;
+}
+
+template <int BITS, int GS, bool TAIL>
+__device__ __forceinline__ void qmv_stream_next(const QmvBatch& batch, QmvStream& st, int wave, int ln, int kq,
+                                                int r_p) {
+    if (st.done) return;
+    if (st.j + kQmvUnroll < st.j_stop) {
+        st.j += kQmvUnroll;
+        return;
+    }
+    qmv_stream_seek<BITS, GS, TAIL>(batch, st, st.tile + gridDim.x, wave, ln, kq, r_p);
+}
+
+template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL>
+__global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
     const QmvBatch batch) {
     typedef QmvGeom<BITS, GS> Geo;
     constexpr int CPL = Geo::CPL, SPAN = Geo::SPAN, P = Geo::P, MB = Geo::MB, STEPS = Geo::STEPS;
     constexpr int U = kQmvUnroll;
+    constexpr int D = QmvRing<BITS, GS>::D;
     static_assert(U % 2 == 0, "blocks must start at even spans");
+    static_assert(D >= 2, "the ring needs two blocks");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nwaves = blockDim.x >> 6;
+    // The grid is launched with exactly kQmvLdsWaves waves per workgroup.
+    constexpr int NW = kQmvLdsWaves;
+    static_assert(NW >= 4, "the cross-wave sum assumes 16 * 16 <= 64 * NW threads");
+    const int nwaves = NW;
     const int ln = lane & 15;
     const int kq = lane >> 4;
     const int M = batch.M;
+    const int r_p = kq * P / 4;  // result group block of this lane
+    prefetch_args(batch);
+    if (int(blockIdx.x) >= batch.total_tiles) return;
 
-    // Stage the activations (zero past K), the zero block, then wait.  Eight
-    // chunks per thread are loaded before any is written, so the copy costs
-    // few round trips to L2.
-    for (int r = 0; r < batch.nstage; r++) {
+    // Activation staging, one round: eight 16-byte chunks per thread are loaded
+    // before any is written, so a round costs one trip to L2.  For 4-bit codes
+    // each 8-element chunk is stored as [x0, x2, x4, x6, x1, x3, x5, x7], the
+    // order in which unpack4_bf16_offset128_perm delivers the codes.
+    const int zero_lds = __builtin_amdgcn_readfirstlane(batch.zero_lds);
+    auto stage_load = [&](int r, int c0, u32x4* v, int* dst) __attribute__((always_inline)) {
         const QmvProblem& pr = batch.p[batch.stage[r]];
         const __amdgpu_buffer_rsrc_t xr = raw_rsrc(pr.x, uint32_t(M) * uint32_t(pr.K) * 2u);
-        const int cpr = pr.kpad / 8;  // 16-byte chunks per LDS row
+        const int K = pr.K, kpad = pr.kpad, x_lds = pr.x_lds;
+        const float inv_cpr = pr.inv_cpr;
+        const int cpr = kpad / 8;  // 16-byte chunks per LDS row
         const int total = M * cpr;
-        for (int c0 = threadIdx.x; c0 < total; c0 += 8 * blockDim.x) {
-            u32x4 v[8];
-            int dst[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int c = c0 + i * blockDim.x;
-                const int m = c / cpr, cc = c - m * cpr;
-                const bool in = c < total && cc * 8 < pr.K;
-                const uint32_t off = in ? (uint32_t(m) * uint32_t(pr.K) + uint32_t(cc) * 8u) * 2u : kOutOfRange;
-                v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
-                dst[i] = c < total ? pr.x_lds + m * pr.kpad * 2 + ((cc ^ (m & 7)) * 16) : -1;
-            }
+        for (int i = 0; i < 8; i++) {
+            const int c = c0 + i * 64 * NW;
+            // c / cpr exactly: c < 2^15 (the staged rows fit in LDS), so the
+            // product's error (below 2^-19) is far from the distance, at least
+            // 0.5 / cpr >= 2^-15, of (c + 0.5) / cpr to an integer
+            const int m = int((float(c) + 0.5f) * inv_cpr), cc = c - m * cpr;
+            const bool live = c < total;
+            const uint32_t off = (live & (cc * 8 < K)) ? (uint32_t(m) * uint32_t(K) + uint32_t(cc) * 8u) * 2u : kOutOfRange;
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+            // chunks past the end read zero and land in the zero block
+            dst[i] = live ? x_lds + m * kpad * 2 + ((cc ^ (m & 7)) * 16) : zero_lds;
+        }
+    };
+    auto stage_store = [&](const u32x4* v, const int* dst) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                if (dst[i] >= 0) *reinterpret_cast<u32x4*>(smem + dst[i]) = v[i];
+        for (int i = 0; i < 8; i++)
+            *reinterpret_cast<u32x4*>(smem + dst[i]) = BITS == 4 ? qmv_permute_x8(v[i]) : v[i];
+    };
+
+    // The first staging round, then the first D - 1 weight blocks, are
+    // requested before anything waits, so the L2 trip of the activations and
+    // the HBM trip of the weights overlap.
+    u32x4 xv[8];
+    int xdst[8];
+    stage_load(0, threadIdx.x, xv, xdst);
+    QmvStream ls;
+    ls.pi = qmv_problem_of(batch, blockIdx.x, 0);
+    ls.L = qmv_tile_view<BITS, GS, TAIL>(batch, ls.pi, blockIdx.x, wave, ln, kq, 0, false, r_p).L;
+    ls.tile = blockIdx.x;
+    ls.j = ls.j_stop = 0;
+    ls.done = false;
+    qmv_stream_seek<BITS, GS, TAIL>(batch, ls, blockIdx.x, wave, ln, kq, r_p);
+    QmvWBlock<BITS, GS, U, VEC> ring[D];
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) {
+        if constexpr (VEC) qmv_wload_ring<BITS, GS, U>(ring[d], ls.L, ls.j);
+        else qmv_wload<BITS, GS, U, VEC>(ring[d], ls.L, ls.j);
+        qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
+    }
+    stage_store(xv, xdst);
+    for (int r = 0; r < batch.nstage; r++) {
+        const QmvProblem& pr = batch.p[batch.stage[r]];
+        const int total = M * (pr.kpad / 8);
+        for (int c0 = int(threadIdx.x) + (r == 0 ? 8 * 64 * NW : 0); c0 < total; c0 += 8 * 64 * NW) {
+            stage_load(r, c0, xv, xdst);
+            stage_store(xv, xdst);
         }
     }
-    for (int c = threadIdx.x; c < batch.zero_bytes / 16; c += blockDim.x)
-        *reinterpret_cast<u32x4*>(smem + batch.zero_lds + c * 16) = u32x4{0u, 0u, 0u, 0u};
+    static_assert(U * SPAN * 2 + 64 <= 16 * 64 * NW, "one pass clears the zero block");
+    if (int(threadIdx.x) < batch.zero_bytes / 16)
+        *reinterpret_cast<u32x4*>(smem + zero_lds + threadIdx.x * 16) = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
 
     const UnpackConsts uc = make_unpack_consts();
@@ -579,67 +809,21 @@ __global__ __launch_bounds__(64 * kQmvLdsWaves) __attribute__((amdgpu_waves_per_
     // that block is the group of this lane's k-slots (block kq * P / 4).
     const int a_m = ln % MB;
     const bool a_live = (ln / MB) == (kq * P / 4) && a_m < M;
-    const int r_p = kq * P / 4;  // result group block of this lane
     float* red = reinterpret_cast<float*>(smem + batch.red_lds);
 
+    // The compute side walks the same tiles; per tile it takes its V.nblk
+    // blocks from the ring, then the spans that do not fill a block.
     int tile = blockIdx.x;
-    if (tile >= batch.total_tiles) return;
-    int pi = 0;
-    while (pi + 1 < batch.count && tile >= batch.p[pi + 1].tile0) pi++;
-    pi = __builtin_amdgcn_readfirstlane(pi);
-    QmvTileView<BITS, GS> V = qmv_tile_view<BITS, GS>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p);
+    int pi = qmv_problem_of(batch, tile, 0);
+    QmvTileView<BITS, GS> V = qmv_tile_view<BITS, GS, TAIL>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p);
+    int left = V.nblk, jc = V.j_begin, iter = 0;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 
-    QmvWBlock<BITS, GS, U, VEC> ba, bb;
-    bool pre = false;  // ba already holds (or is loading) this tile's first block
-    for (int iter = 0;; iter++) {
-        // The next tile of this workgroup: its first block is prefetched while
-        // this tile finishes, when this tile's block count is even.
-        const int ntile = tile + gridDim.x;
-        const bool has_next = ntile < batch.total_tiles;
-        int npi = pi;
-        while (has_next && npi + 1 < batch.count && ntile >= batch.p[npi + 1].tile0) npi++;
-        npi = __builtin_amdgcn_readfirstlane(npi);
-        QmvTileView<BITS, GS> Vn =
-            qmv_tile_view<BITS, GS>(batch, npi, has_next ? ntile : tile, wave, ln, kq, a_m, a_live, r_p);
-        const bool chain = has_next && Vn.nblk > 0;
-
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const int nblk = V.nblk;
-        if (nblk > 0 && !pre) qmv_wload<BITS, GS, U, VEC>(ba, V.L, V.j_begin);
-        bool pre_next = false;
-        if (nblk > 0 && (nblk & 1) == 0) {
-            for (int i = 0; i < nblk; i += 2) {
-                qmv_wload<BITS, GS, U, VEC>(bb, V.L, V.j_begin + (i + 1) * U);
-                if (opaque_one())
-                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ba, smem, V.xa_t, V.xstep, V.j_begin + i * U, r_p,
-                                                              V.bias_on, uc, ones);
-                // Next block of this tile, else the first block of the next
-                // tile, else a harmless re-read of this tile's last block.
-                const bool more = i + 2 < nblk;
-                const bool cross = !more && chain;
-                QmvTileLane Lp = cross ? Vn.L : V.L;
-                const int jp = more ? V.j_begin + (i + 2) * U : (cross ? Vn.j_begin : V.j_begin + (nblk - 1) * U);
-                qmv_wload<BITS, GS, U, VEC>(ba, Lp, jp);
-                if (opaque_one())
-                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, bb, smem, V.xa_t, V.xstep, V.j_begin + (i + 1) * U,
-                                                              r_p, V.bias_on, uc, ones);
-            }
-            pre_next = chain;
-        } else if (nblk > 0) {
-            for (int i = 0; i + 1 < nblk; i += 2) {
-                qmv_wload<BITS, GS, U, VEC>(bb, V.L, V.j_begin + (i + 1) * U);
-                if (opaque_one())
-                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ba, smem, V.xa_t, V.xstep, V.j_begin + i * U, r_p,
-                                                              V.bias_on, uc, ones);
-                qmv_wload<BITS, GS, U, VEC>(ba, V.L, V.j_begin + min(i + 2, nblk - 1) * U);
-                if (opaque_one())
-                    qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, bb, smem, V.xa_t, V.xstep, V.j_begin + (i + 1) * U,
-                                                              r_p, V.bias_on, uc, ones);
-            }
-            qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ba, smem, V.xa_t, V.xstep, V.j_begin + (nblk - 1) * U, r_p,
-                                                      V.bias_on, uc, ones);
-        }
-        for (int j = V.j_begin + nblk * U; j < V.j_full_end; j++) {
+    // Ends the current tile: leftover spans, the cross-wave sum, the store;
+    // then moves to the next tile.  False when the workgroup has no more.
+    auto finish = [&]() __attribute__((always_inline)) -> bool {
+        if constexpr (TAIL) {
+        for (int j = jc; j < V.j_full_end; j++) {
             QmvWBlock<BITS, GS, 1, VEC> b1;
             qmv_wload<BITS, GS, 1, VEC>(b1, V.L, j);
             qmv_wcompute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, smem, V.xa_t, V.xstep, j, r_p, V.bias_on, uc, ones);
@@ -660,8 +844,9 @@ __global__ __launch_bounds__(64 * kQmvLdsWaves) __attribute__((amdgpu_waves_per_
             qmv_wload<BITS, GS, 1, VEC>(b1, T, j);
             qmv_wcompute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, smem, xt, V.xstep, j, r_p, V.bias_on, uc, ones);
         }
-
-        // Fold the P group blocks, then combine the waves through LDS.
+        }
+        // Fold the P group blocks, then combine the waves through LDS (two
+        // slots: a wave may fill the next tile's slot while this one is read).
 #pragma unroll
         for (int r = 0; r < MREG; r++) {
             if (P >= 4) acc[r] += __shfl_xor(acc[r], 16);
@@ -676,18 +861,52 @@ __global__ __launch_bounds__(64 * kQmvLdsWaves) __attribute__((amdgpu_waves_per_
             }
         }
         __syncthreads();
-        const QmvProblem& pr = batch.p[pi];
-        for (int t = threadIdx.x; t < 16 * M; t += blockDim.x) {
-            const int m = t >> 4, n = t & 15;
+        // Straight-line on purpose (16 M <= 64 NW threads, NW unrolled): a loop
+        // holding a global store makes the compiler wait for every load in
+        // flight before entering it, prefetches included.
+        if (int(threadIdx.x) < 16 * M) {
+            const QmvProblem& pr = batch.p[pi];
+            const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
             float v = 0.f;
-            for (int i = 0; i < nwaves; i++) v += slot[(i * M + m) * 16 + n];
+#pragma unroll
+            for (int i = 0; i < NW; i++) v += slot[(i * M + m) * 16 + n];
             pr.y[int64_t(m) * pr.ldy + V.n0 + n] = uint16_t(f32_to_bf16_bits(v));
         }
-        if (!has_next) break;
-        tile = ntile;
-        pi = npi;
-        V = Vn;
-        pre = pre_next;
+        iter++;
+        acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        tile += gridDim.x;
+        if (tile >= batch.total_tiles) return false;
+        pi = qmv_problem_of(batch, tile, pi);
+        V = qmv_tile_view<BITS, GS, TAIL>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p);
+        left = V.nblk;
+        jc = V.j_begin;
+        return true;
+    };
+
+    while (left == 0)
+        if (!finish()) return;
+    for (;;) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            if constexpr (VEC) qmv_wload_ring<BITS, GS, U>(ring[(d + D - 1) % D], ls.L, ls.j);
+            else qmv_wload<BITS, GS, U, VEC>(ring[(d + D - 1) % D], ls.L, ls.j);
+            qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
+            if (opaque_one())
+                qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ring[d], smem, V.xa_t, V.xstep, jc, r_p, V.bias_on, uc,
+                                                          ones);
+            else
+                qmv_retire(ring[d]);
+            jc += U;
+            if (--left == 0) {
+                if constexpr (TAIL) {
+                    do {
+                        if (!finish()) return;
+                    } while (left == 0);
+                } else {
+                    if (!finish()) return;  // every tile has a block
+                }
+            }
+        }
     }
 }
 
@@ -739,8 +958,9 @@ static int device_lds_bytes() {
 // Launch plan of the persistent LDS variant.
 struct QmvLdsPlan {
     QmvBatch B;
-    int lds, grid;
+    int lds, grid, waves;
     bool vec;
+    bool tail;  // some K is not a multiple of a block (U spans)
 };
 
 // Plans the persistent LDS variant for `count` problems sharing bits, group
@@ -750,6 +970,7 @@ template <int BITS, int GS, typename ST>
 static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& plan) {
     typedef QmvGeom<BITS, GS> Geo;
     constexpr int W = kQmvLdsWaves, U = kQmvUnroll;
+    static_assert(W >= 1 && W <= kQmvLdsMaxWaves, "waves per workgroup");
     if (count < 1 || count > kQmvMaxProblems || M < 1 || M > Geo::MB) return false;
     QmvBatch& B = plan.B;
     B = QmvBatch{};
@@ -757,7 +978,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     B.M = M;
     const int pbytes = QmvParamWords<BITS, GS, U>::WORDS * 4;
     const int align = pbytes < 16 ? pbytes : 16;
-    bool vec = true;
+    bool vec = true, tail = false;
     int lds = 0, tiles = 0;
     for (int i = 0; i < count; i++) {
         const QmvSpec& q = specs[i];
@@ -770,12 +991,13 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
         p.x = q.x, p.w = q.w, p.s = static_cast<const uint16_t*>(q.s), p.b = static_cast<const uint16_t*>(q.b);
         p.y = q.y, p.N = q.N, p.K = q.K, p.ldy = q.ldy;
         const int S = (q.K + Geo::SPAN - 1) / Geo::SPAN;
-        // spans per wave: a multiple of 2U, so that full waves have an even
-        // number of blocks (the first block of the next tile is then prefetched)
-        p.spw = ((S + W - 1) / W + 2 * U - 1) / (2 * U) * (2 * U);
+        // spans per wave: a multiple of U (blocks start at multiples of U)
+        p.spw = ((S + W - 1) / W + U - 1) / U * U;
+        tail = tail || q.K % (U * Geo::SPAN) != 0;
         p.tile0 = tiles;
         tiles += q.N / 16;
         p.kpad = (q.K + 63) / 64 * 64;
+        p.inv_cpr = 1.0f / float(p.kpad / 8);
         vec = vec && (G * 2) % align == 0 && aligned(q.s, align) && (q.b == nullptr || aligned(q.b, align));
         // stage each distinct activation matrix once
         p.x_lds = -1;
@@ -796,28 +1018,31 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     if (lds > device_lds_bytes()) return false;
     plan.lds = lds;
     plan.vec = vec;
+    plan.tail = tail;
     // Workgroups resident per CU: 8 waves (2 per SIMD, the register budget).
     const int per_cu = 8 / W > 0 ? 8 / W : 1;
+    plan.waves = W;
     plan.grid = tiles < per_cu * device_cu_count() ? tiles : per_cu * device_cu_count();
     return true;
 }
 
 template <int BITS, int GS, typename ST>
 static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
-    constexpr int W = kQmvLdsWaves;
     auto go = [&](auto kernel) {
         // (a refusal surfaces as a launch error)
         if (plan.lds > 65536)
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                       plan.lds);
-        kernel<<<dim3(unsigned(plan.grid)), dim3(64 * W), size_t(plan.lds), st>>>(plan.B);
+        kernel<<<dim3(unsigned(plan.grid)), dim3(64 * plan.waves), size_t(plan.lds), st>>>(plan.B);
     };
     if (plan.B.M == 1) {
-        if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true>);
-        else go(qmv_lds_kernel<BITS, GS, ST, 1, false>);
+        if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 1, true, false>);
+        else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true, true>);
+        else go(qmv_lds_kernel<BITS, GS, ST, 1, false, true>);
     } else {
-        if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true>);
-        else go(qmv_lds_kernel<BITS, GS, ST, 4, false>);
+        if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 4, true, false>);
+        else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true, true>);
+        else go(qmv_lds_kernel<BITS, GS, ST, 4, false, true>);
     }
 }
 
