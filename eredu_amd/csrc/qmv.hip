@@ -29,6 +29,7 @@
 // the bias term and the removal of the +128 offset:
 //   acc += s * t + (b - 128 s) * xs         (f32, per span)
 // Waves combine through LDS; the result is rounded once to bf16.
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 #include <vector>
@@ -664,9 +665,12 @@ __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& b
     return v;
 }
 
-// Problem of global tile t, searching on from problem pi (tiles only grow).
-__device__ __forceinline__ int qmv_problem_of(const QmvBatch& batch, int t, int pi) {
-    while (pi + 1 < batch.count && t >= batch.p[pi + 1].tile0) pi++;
+// Problem of global tile t: the number of later problems whose first tile
+// is at or below t, counted without a loop (scalar compares and selects).
+__device__ __forceinline__ int qmv_problem_of(const QmvBatch& batch, int t, int /*hint*/) {
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < kQmvMaxProblems; i++) pi += (i < batch.count && t >= batch.p[i].tile0) ? 1 : 0;
     return __builtin_amdgcn_readfirstlane(pi);
 }
 
@@ -685,6 +689,22 @@ struct QmvStream {
 template <int BITS, int GS, bool TAIL>
 __device__ __forceinline__ void qmv_stream_seek(const QmvBatch& batch, QmvStream& st, int tile, int wave, int ln,
                                                 int kq, int r_p) {
+    if constexpr (!TAIL) {
+        // every tile has a block (real or virtual)
+        if (tile < batch.total_tiles) {
+            st.pi = qmv_problem_of(batch, tile, st.pi);
+            const QmvTileView<BITS, GS> v = qmv_tile_view<BITS, GS, TAIL>(batch, st.pi, tile, wave, ln, kq, 0, false, r_p);
+            st.L = v.L;
+            st.tile = tile;
+            st.j = v.j_begin;
+            st.j_stop = v.j_begin + v.nblk * kQmvUnroll;
+            return;
+        }
+        st.done = true;
+        st.j = 0;
+        st.L.woff = st.L.soff = kOutOfRange;
+        return;
+    }
     for (; tile < batch.total_tiles; tile += gridDim.x) {
         st.pi = qmv_problem_of(batch, tile, st.pi);
         const QmvTileView<BITS, GS> v = qmv_tile_view<BITS, GS, TAIL>(batch, st.pi, tile, wave, ln, kq, 0, false, r_p);
@@ -754,7 +774,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             // c / cpr exactly: c < 2^15 (the staged rows fit in LDS), so the
             // product's error (below 2^-19) is far from the distance, at least
             // 0.5 / cpr >= 2^-15, of (c + 0.5) / cpr to an integer
-            const int m = int((float(c) + 0.5f) * inv_cpr), cc = c - m * cpr;
+            const int m = MREG == 1 ? 0 : int((float(c) + 0.5f) * inv_cpr), cc = c - m * cpr;
             const bool live = c < total;
             const uint32_t off = (live & (cc * 8 < K)) ? (uint32_t(m) * uint32_t(K) + uint32_t(cc) * 8u) * 2u : kOutOfRange;
             v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
@@ -771,6 +791,9 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // The first staging round, then the first D - 1 weight blocks, are
     // requested before anything waits, so the L2 trip of the activations and
     // the HBM trip of the weights overlap.
+    // Order of the first requests: the activations, then the weight blocks.
+    // Loads complete in order, so the activations can be stored (and the
+    // workgroup synchronised) while the weights are still on their way.
     u32x4 xv[8];
     int xdst[8];
     stage_load(0, threadIdx.x, xv, xdst);
@@ -781,11 +804,15 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     ls.j = ls.j_stop = 0;
     ls.done = false;
     qmv_stream_seek<BITS, GS, TAIL>(batch, ls, blockIdx.x, wave, ln, kq, r_p);
-    QmvWBlock<BITS, GS, U, VEC> ring[D];
+    typedef QmvWBlock<BITS, GS, U, VEC> RingBlock;
+    RingBlock ring[D];
+    auto ring_load = [&](RingBlock& b) __attribute__((always_inline)) {
+        if constexpr (VEC) qmv_wload_ring<BITS, GS, U>(b, ls.L, ls.j);
+        else qmv_wload<BITS, GS, U, VEC>(b, ls.L, ls.j);
+    };
 #pragma unroll
     for (int d = 0; d < D - 1; d++) {
-        if constexpr (VEC) qmv_wload_ring<BITS, GS, U>(ring[d], ls.L, ls.j);
-        else qmv_wload<BITS, GS, U, VEC>(ring[d], ls.L, ls.j);
+        ring_load(ring[d]);
         qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
     }
     stage_store(xv, xdst);
@@ -860,6 +887,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
                 if (m < M) slot[(wave * M + m) * 16 + ln] = acc[r];
             }
         }
+        const int tile1 = tile + int(gridDim.x);
+        const bool has1 = tile1 < batch.total_tiles;
         __syncthreads();
         // Straight-line on purpose (16 M <= 64 NW threads, NW unrolled): a loop
         // holding a global store makes the compiler wait for every load in
@@ -874,8 +903,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         }
         iter++;
         acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        tile += gridDim.x;
-        if (tile >= batch.total_tiles) return false;
+        tile = tile1;
+        if (!has1) return false;
         pi = qmv_problem_of(batch, tile, pi);
         V = qmv_tile_view<BITS, GS, TAIL>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p);
         left = V.nblk;
@@ -883,19 +912,21 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         return true;
     };
 
-    while (left == 0)
-        if (!finish()) return;
+    if constexpr (TAIL) {
+        while (left == 0)
+            if (!finish()) return;
+    }
     for (;;) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
-            if constexpr (VEC) qmv_wload_ring<BITS, GS, U>(ring[(d + D - 1) % D], ls.L, ls.j);
-            else qmv_wload<BITS, GS, U, VEC>(ring[(d + D - 1) % D], ls.L, ls.j);
+            ring_load(ring[(d + D - 1) % D]);
             qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
-            if (opaque_one())
+            if (opaque_one()) {
                 qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ring[d], smem, V.xa_t, V.xstep, jc, r_p, V.bias_on, uc,
                                                           ones);
-            else
+            } else {
                 qmv_retire(ring[d]);
+            }
             jc += U;
             if (--left == 0) {
                 if constexpr (TAIL) {
@@ -1015,6 +1046,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     lds += B.zero_bytes;
     B.red_lds = lds;
     lds += 2 * W * M * 16 * 4;
+
     if (lds > device_lds_bytes()) return false;
     plan.lds = lds;
     plan.vec = vec;
