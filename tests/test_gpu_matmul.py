@@ -95,6 +95,20 @@ def test_qmm_f16_scales(cuda):
     run_case(64, 256, 512, 32, 4, sdt=orc.F16, seed=3)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("K", [64, 128, 192, 256, 320, 448])
+def test_qmm_pipeline_depths(cuda, bits, K):
+    # 1..7 chunks of 64 in one workgroup (too few to split K): every position
+    # of the three-slot load ring, including the wrap-around
+    run_case(40, 256, K, 64, bits, seed=K + bits)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_split_k(cuda, bits):
+    # 6 output tiles, 32 chunks: K split 8 ways, partial tiles summed in order
+    run_case(300, 512, 2048, 64, bits, seed=bits + 77)
+
+
 @pytest.mark.parametrize("xdt", [orc.F32, orc.F16])
 @pytest.mark.parametrize("M", [1, 33])
 def test_general_activation_dtypes(cuda, xdt, M):
