@@ -9,7 +9,9 @@
 // not 4-byte aligned, so a workgroup stages its 256 blocks through LDS with
 // 16-byte coalesced loads and each thread then decodes one block from LDS.
 // Q4_K superblocks (144 B) are 16-byte aligned and are read directly, one
-// thread per 32-value group.  Every product in these decoders is exact in f32
+// thread per 32-value group for the affine convert.  Dense output is written
+// by four lanes per 32-value block or group (8 values each), so that wave
+// stores are contiguous.  Every product in these decoders is exact in f32
 // (an 11-bit f16 significand times a code of at most 8 bits), so each output
 // carries exactly one rounding, as on the reference's CPU.
 #include "eq_common.hpp"
@@ -106,30 +108,29 @@ __global__ __launch_bounds__(256) void q8_0_to_affine(const uint8_t* __restrict_
     bias[blk] = uint16_t(f32_to_f16_bits(-128.0f * f16_bits_to_f32(d)));  // convert.rs:380
 }
 
-// Dense output: 32 consecutive values per thread.
+// Dense output: a block's (or Q4_K group's) 32 values are decoded by four
+// consecutive lanes, 8 values each, so that one wave store writes a
+// contiguous kilobyte (bf16) or two (f32).
 template <typename OUT>
-__device__ __forceinline__ void store32(typename OUT::storage* out, int64_t base, const float v[32]);
+__device__ __forceinline__ void store8(typename OUT::storage* out, int64_t base, const float v[8]);
 template <>
-__device__ __forceinline__ void store32<BF16T>(uint16_t* out, int64_t base, const float v[32]) {
-    uint4* o = reinterpret_cast<uint4*>(out + base);
+__device__ __forceinline__ void store8<BF16T>(uint16_t* out, int64_t base, const float v[8]) {
+    uint32_t p[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        uint32_t p[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            p[j] = f32_to_bf16_bits(v[8 * i + 2 * j]) | (f32_to_bf16_bits(v[8 * i + 2 * j + 1]) << 16);
-        o[i] = make_uint4(p[0], p[1], p[2], p[3]);
-    }
+    for (int j = 0; j < 4; j++) p[j] = f32_to_bf16_bits(v[2 * j]) | (f32_to_bf16_bits(v[2 * j + 1]) << 16);
+    *reinterpret_cast<uint4*>(out + base) = make_uint4(p[0], p[1], p[2], p[3]);
 }
 template <>
-__device__ __forceinline__ void store32<F32T>(float* out, int64_t base, const float v[32]) {
+__device__ __forceinline__ void store8<F32T>(float* out, int64_t base, const float v[8]) {
     float4* o = reinterpret_cast<float4*>(out + base);
-#pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
 // Q4_0 dense: affine route only (Q4_0 has no native decoder, format.rs:423-428):
-// w = f32(d) * code + f32(f16(-8 d)).
+// w = f32(d) * code + f32(f16(-8 d)).  Quarter c of a block holds values
+// [8c, 8c + 8): low nibbles of quant bytes [8c, 8c + 8) for c < 2, high
+// nibbles of bytes [8(c - 2), ...) for c >= 2 (convert.rs:355-358).
 template <bool BIG, typename OUT>
 __global__ __launch_bounds__(256) void q4_0_dense(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
                                                   typename OUT::storage* __restrict__ out) {
@@ -137,20 +138,22 @@ __global__ __launch_bounds__(256) void q4_0_dense(const uint8_t* __restrict__ ra
     const int64_t blk0 = int64_t(blockIdx.x) * kBlocksPerWG;
     const int nb = int(min<int64_t>(kBlocksPerWG, nblocks - blk0));
     stage_blocks<18>(lds, raw, blk0, nb, vec_ok);
-    const int t = threadIdx.x;
-    if (t >= nb) return;
-    uint32_t d, q[4];
-    q4_0_block<BIG>(lds + t * 9, d, q);
-    const float scale = f16_bits_to_f32(d);
-    const float bias = f16_bits_to_f32(f32_to_f16_bits(-8.0f * scale));
-    float v[32];
+    const int c = threadIdx.x & 3;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const uint32_t byte = (q[i >> 2] >> (8 * (i & 3))) & 0xffu;
-        v[i] = scale * float(byte & 15u) + bias;
-        v[16 + i] = scale * float(byte >> 4) + bias;
+    for (int k = 0; k < 4; k++) {
+        const int lb = k * 64 + (threadIdx.x >> 2);
+        if (lb >= nb) break;
+        const uint16_t* blk = lds + lb * 9;
+        const uint32_t d = BIG ? bswap16(blk[0]) : blk[0];
+        const float scale = f16_bits_to_f32(d);
+        const float bias = f16_bits_to_f32(f32_to_f16_bits(-8.0f * scale));
+        const int sh = (c >> 1) * 4;
+        const uint32_t q0 = lds_u32(blk + 1 + 4 * (c & 1)), q1 = lds_u32(blk + 3 + 4 * (c & 1));
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = scale * float(((i < 4 ? q0 : q1) >> (8 * (i & 3) + sh)) & 15u) + bias;
+        store8<OUT>(out, (blk0 + lb) * 32 + 8 * c, v);
     }
-    store32<OUT>(out, (blk0 + t) * 32, v);
 }
 
 // Q8_0 dense.  Affine route: f32(d) * (q ^ 0x80) + f32(f16(-128 d));
@@ -162,26 +165,27 @@ __global__ __launch_bounds__(256) void q8_0_dense(const uint8_t* __restrict__ ra
     const int64_t blk0 = int64_t(blockIdx.x) * kBlocksPerWG;
     const int nb = int(min<int64_t>(kBlocksPerWG, nblocks - blk0));
     stage_blocks<34>(lds, raw, blk0, nb, vec_ok);
-    const int t = threadIdx.x;
-    if (t >= nb) return;
-    const uint16_t* b = lds + t * 17;
-    const uint32_t dbits = BIG ? bswap16(b[0]) : b[0];
-    const float d = f16_bits_to_f32(dbits);
-    const float bias = f16_bits_to_f32(f32_to_f16_bits(-128.0f * d));
-    float v[32];
+    const int c = threadIdx.x & 3;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const uint32_t pair = b[1 + i];
+    for (int k = 0; k < 4; k++) {
+        const int lb = k * 64 + (threadIdx.x >> 2);
+        if (lb >= nb) break;
+        const uint16_t* blk = lds + lb * 17;
+        const uint32_t dbits = BIG ? bswap16(blk[0]) : blk[0];
+        const float d = f16_bits_to_f32(dbits);
+        const float bias = f16_bits_to_f32(f32_to_f16_bits(-128.0f * d));
+        const uint32_t q0 = lds_u32(blk + 1 + 4 * c), q1 = lds_u32(blk + 3 + 4 * c);
+        float v[8];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t byte = (pair >> (8 * h)) & 0xffu;
+        for (int i = 0; i < 8; i++) {
+            const uint32_t byte = ((i < 4 ? q0 : q1) >> (8 * (i & 3))) & 0xffu;
             if (NATIVE)
-                v[2 * i + h] = d * float(int8_t(byte));
+                v[i] = d * float(int8_t(byte));
             else
-                v[2 * i + h] = d * float(byte ^ 0x80u) + bias;
+                v[i] = d * float(byte ^ 0x80u) + bias;
         }
+        store8<OUT>(out, (blk0 + lb) * 32 + 8 * c, v);
     }
-    store32<OUT>(out, (blk0 + t) * 32, v);
 }
 
 // ------------------------------------------------------------------- Q4_K
@@ -191,6 +195,19 @@ struct Q4KGroup {
     uint32_t sc, m;
     uint32_t q[8];  // the 32 quant bytes holding this group's nibbles
 };
+
+// 6-bit scale and min of group g from the 12 scale bytes s[0..12) = bytes of
+// h[1], h[2], h[3] (scale_min, convert.rs:429-438).
+__device__ __forceinline__ void q4k_scale_min(const uint32_t h[4], int g, uint32_t& sc, uint32_t& m) {
+    auto sbyte = [&](int i) -> uint32_t { return (h[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu; };
+    if (g < 4) {
+        sc = sbyte(g) & 63u;
+        m = sbyte(g + 4) & 63u;
+    } else {
+        sc = (sbyte(g + 4) & 15u) | ((sbyte(g - 4) >> 6) << 4);
+        m = (sbyte(g + 4) >> 4) | ((sbyte(g) >> 6) << 4);
+    }
+}
 
 // One 32-value group g of a 144-byte superblock (convert.rs:439-465,
 // native_quantization.rs:3445-3469): header = d, dmin, 12 scale bytes; group g
@@ -219,15 +236,7 @@ __device__ __forceinline__ Q4KGroup load_q4k_group(const uint8_t* __restrict__ r
     const uint32_t mbits = BIG ? bswap16(h[0] >> 16) : (h[0] >> 16);
     r.d = f16_bits_to_f32(dbits);
     r.dmin = f16_bits_to_f32(mbits);
-    // 12 scale bytes s[0..12) = bytes of h[1], h[2], h[3]; scale_min, convert.rs:429-438
-    auto sbyte = [&](int i) -> uint32_t { return (h[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu; };
-    if (g < 4) {
-        r.sc = sbyte(g) & 63u;
-        r.m = sbyte(g + 4) & 63u;
-    } else {
-        r.sc = (sbyte(g + 4) & 15u) | ((sbyte(g - 4) >> 6) << 4);
-        r.m = (sbyte(g + 4) >> 4) | ((sbyte(g) >> 6) << 4);
-    }
+    q4k_scale_min(h, g, r.sc, r.m);
 #pragma unroll
     for (int i = 0; i < 8; i++) r.q[i] = q[i];
     return r;
@@ -252,29 +261,53 @@ __global__ __launch_bounds__(256) void q4k_to_affine(const uint8_t* __restrict__
     bias[idx] = uint16_t(f32_to_f16_bits(-r.dmin * float(r.m)));  // convert.rs:450
 }
 
+// Q4_K dense: thread idx decodes quarter c = idx % 4 (values [8c, 8c + 8),
+// quant bytes [8c, 8c + 8) of the group's 32) of group (idx / 4) % 8 of
+// superblock idx / 32.
 template <bool BIG, bool NATIVE, typename OUT>
-__global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw, int64_t ngroups, bool vec_ok,
+__global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw, int64_t nquarters, bool vec_ok,
                                                  typename OUT::storage* __restrict__ out) {
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= ngroups) return;
-    const int g = int(idx & 7);
-    const Q4KGroup r = load_q4k_group<BIG>(raw, idx >> 3, g, vec_ok);
+    if (idx >= nquarters) return;
+    const int c = int(idx & 3), g = int((idx >> 2) & 7);
+    // the superblock's 16-byte header (same address for its 32 lanes) and this
+    // quarter's 8 quant bytes
+    const uint8_t* p = raw + (idx >> 5) * 144;
+    const int qo = 16 + (g >> 1) * 32 + 8 * c;
+    uint32_t h[4], q0, q1;
+    if (vec_ok) {
+        const uint4 hv = *reinterpret_cast<const uint4*>(p);
+        const uint2 qv = *reinterpret_cast<const uint2*>(p + qo);
+        h[0] = hv.x, h[1] = hv.y, h[2] = hv.z, h[3] = hv.w;
+        q0 = qv.x, q1 = qv.y;
+    } else {
+        const uint16_t* p2 = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) h[i] = uint32_t(p2[2 * i]) | (uint32_t(p2[2 * i + 1]) << 16);
+        const uint16_t* q2 = reinterpret_cast<const uint16_t*>(p + qo);
+        q0 = uint32_t(q2[0]) | (uint32_t(q2[1]) << 16);
+        q1 = uint32_t(q2[2]) | (uint32_t(q2[3]) << 16);
+    }
+    uint32_t sc, m;
+    q4k_scale_min(h, g, sc, m);
+    const float d = f16_bits_to_f32(BIG ? bswap16(h[0] & 0xffffu) : (h[0] & 0xffffu));
+    const float dmin = f16_bits_to_f32(BIG ? bswap16(h[0] >> 16) : (h[0] >> 16));
     const int sh = (g & 1) * 4;
-    float v[32];
+    float v[8];
     if (NATIVE) {
         // d * sc * q - dmin * m, left to right (native_quantization.rs:3466)
-        const float ds = r.d * float(r.sc);
-        const float dm = r.dmin * float(r.m);
+        const float ds = d * float(sc);
+        const float dm = dmin * float(m);
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = ds * float((r.q[i >> 2] >> (8 * (i & 3) + sh)) & 15u) - dm;
+        for (int i = 0; i < 8; i++) v[i] = ds * float(((i < 4 ? q0 : q1) >> (8 * (i & 3) + sh)) & 15u) - dm;
     } else {
         // f32(f16(d sc)) * q + f32(f16(-dmin m)) (convert.rs:81-101 on the q45k output)
-        const float scale = f16_bits_to_f32(f32_to_f16_bits(r.d * float(r.sc)));
-        const float bias = f16_bits_to_f32(f32_to_f16_bits(-r.dmin * float(r.m)));
+        const float scale = f16_bits_to_f32(f32_to_f16_bits(d * float(sc)));
+        const float bias = f16_bits_to_f32(f32_to_f16_bits(-dmin * float(m)));
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = scale * float((r.q[i >> 2] >> (8 * (i & 3) + sh)) & 15u) + bias;
+        for (int i = 0; i < 8; i++) v[i] = scale * float(((i < 4 ? q0 : q1) >> (8 * (i & 3) + sh)) & 15u) + bias;
     }
-    store32<OUT>(out, idx * 32, v);
+    store8<OUT>(out, (idx >> 2) * 32 + 8 * c, v);
 }
 
 struct Geometry {
@@ -384,14 +417,14 @@ template <typename OUT>
 void launch_dense(int type, bool big, bool native, const uint8_t* raw, int64_t nblocks, bool vec_ok,
                   typename OUT::storage* out, hipStream_t st) {
     if (type == EQ_GGML_Q4_K) {
-        const int64_t ngroups = nblocks * 8;
-        const dim3 grid(unsigned((ngroups + 255) / 256));
+        const int64_t nq = nblocks * 32;  // 8 groups x 4 quarters per superblock
+        const dim3 grid(unsigned((nq + 255) / 256));
         if (big) {
-            if (native) q4k_dense<true, true, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
-            else q4k_dense<true, false, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
+            if (native) q4k_dense<true, true, OUT><<<grid, 256, 0, st>>>(raw, nq, vec_ok, out);
+            else q4k_dense<true, false, OUT><<<grid, 256, 0, st>>>(raw, nq, vec_ok, out);
         } else {
-            if (native) q4k_dense<false, true, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
-            else q4k_dense<false, false, OUT><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, out);
+            if (native) q4k_dense<false, true, OUT><<<grid, 256, 0, st>>>(raw, nq, vec_ok, out);
+            else q4k_dense<false, false, OUT><<<grid, 256, 0, st>>>(raw, nq, vec_ok, out);
         }
         return;
     }
