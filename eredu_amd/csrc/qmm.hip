@@ -4,10 +4,15 @@
 // y = x . W^T with W[n, k] = s[n, k/gs] * q[n, k] + b[n, k/gs]
 // (safemlx/src/ops/quantization.rs:190-226, QuantizedLinear's layout).
 //
-// Work layout.  A workgroup of 4 waves owns a 128 (m) x 256 (n) output tile
-// and walks K (or one split of it) in chunks of 64.  Wave w owns the 64
-// columns [64w, 64w + 64) and all 128 rows: 4 x 2 tiles of
-// v_mfma_f32_32x32x16_bf16 with f32 accumulators.
+// Work layout.  A workgroup of 8 waves owns a 128 (m) x 256 (n) output tile
+// and walks K (or one split of it) in chunks of 64.  The waves form two
+// K-groups of 4 that take alternate chunks (even, odd), each with its own
+// double-buffered activation tile in LDS, so that every SIMD runs two waves
+// (one's dequantization and memory waits overlap the other's MFMAs) while a
+// wave keeps a large output block; at the end the second K-group adds its
+// sums into the first through LDS.  Wave w of a K-group owns the 64 columns
+// [64w, 64w + 64) and all 128 rows: 4 x 2 tiles of v_mfma_f32_32x32x16_bf16
+// with f32 accumulators.
 //
 //  * Weights never touch LDS.  Each wave dequantizes only its own columns,
 //    straight from 16-byte loads into the B-operand registers: lane l reads
@@ -46,7 +51,7 @@ typedef uint32_t q_u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 q_bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 128, kBN = 256, kBK = 64;
-constexpr int kQmmThreads = 256;
+constexpr int kQmmThreads = 512;        // two K-groups of 4 waves
 constexpr int kLdsBuf = kBM * kBK * 2;  // bytes per activation buffer
 constexpr int kRing = 3;                // register slots of the load ring
 
@@ -122,9 +127,9 @@ struct QmmArgs {
 };
 
 template <int BITS, int GS, typename ST, bool SPLIT>
-__global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void qmm_mfma_kernel(
+__global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void qmm_mfma_kernel(
     const QmmArgs args) {
-    __shared__ __attribute__((aligned(16))) char lds[2 * kLdsBuf];
+    __shared__ __attribute__((aligned(16))) char lds_all[2 * 2 * kLdsBuf];  // [K-group][buffer]
     const int M = args.M, N = args.N, K = args.K;
 
     // Tile and split of this workgroup: the workgroups of one XCD (id % 8)
@@ -139,9 +144,13 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(1, 
     const int c_begin = split * args.cps, c_end = min(nchunks, c_begin + args.cps);
     const int nloc = c_end - c_begin;  // >= 1 (the planner leaves no split empty)
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = threadIdx.x & 63;
+    const int kgrp = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 8);  // K-group: chunks 2i + kgrp
+    const int tid = threadIdx.x & 255;                                         // thread within the K-group
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);                 // column quarter
     const int l32 = lane & 31, kb = lane >> 5;
+    char* lds = lds_all + kgrp * 2 * kLdsBuf;
+    const int steps = (nloc + 1) / 2;  // chunks per K-group (the second may have one fewer)
     const int G = K / GS;
 
     const __amdgpu_buffer_rsrc_t xr = raw_rsrc(args.x, uint32_t(M) * uint32_t(K) * 2u);
@@ -155,7 +164,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(1, 
     uint32_t a_goff[4], a_loff[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int q = tid + kQmmThreads * i, row = q >> 3, c = q & 7;
+        const int q = tid + 256 * i, row = q >> 3, c = q & 7;
         a_goff[i] = m0 + row < M ? (uint32_t(m0 + row) * uint32_t(K) + uint32_t(8 * c)) * 2u : kOutOfRange;
         a_loff[i] = uint32_t(row * (kBK * 2) + ((c ^ (row & 7)) << 4));
     }
@@ -170,9 +179,11 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(1, 
     // (a lane's 32 codes lie in one group: group sizes are multiples of 32 and
     // chunks start at multiples of 64, so its group is k0 / GS + 32 kb / GS)
 
-    // Loads of local chunk i (past the split's end: the last chunk again, in
-    // cache and never computed).
-    auto chunk_k0 = [&](int i) __attribute__((always_inline)) { return (c_begin + min(i, nloc - 1)) * kBK; };
+    // Loads of this K-group's chunk i, i.e. chunk 2i + kgrp of the split (past
+    // the split's end: the last chunk again, in cache and never computed).
+    auto chunk_k0 = [&](int i) __attribute__((always_inline)) {
+        return (c_begin + min(2 * i + kgrp, nloc - 1)) * kBK;
+    };
     auto load_a = [&](q_u32x4* r, int i) __attribute__((always_inline)) {
         const uint32_t ks = __builtin_amdgcn_readfirstlane(uint32_t(chunk_k0(i)) * 2u);
 #pragma unroll
@@ -253,14 +264,41 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(1, 
             const int i = i0 + r;
             load_a(areg, i + 1);
             load_b(ring[(r + 2) % kRing], i + 2);
-            if (opaque_one()) compute(ring[r], i & 1);
+            if (opaque_one() && 2 * i + kgrp < nloc) compute(ring[r], i & 1);
             else qmm_retire(ring[r]);
-            if (i + 1 >= nloc) goto done;
+            if (i + 1 >= steps) goto done;
             store_a(areg, (i + 1) & 1);
             __syncthreads();
         }
     }
 done:
+    // The second K-group's sums go to LDS (half the rows at a time: 64 KiB),
+    // the first adds them.  Layout: [wave][mi & 1][j][r][lane] floats.
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(lds_all);
+#pragma unroll
+        for (int mh = 0; mh < 2; mh++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int o = (((wave * 2 + mh) * 2 + j) * 16 + r) * 64 + lane;
+                    if (kgrp == 1) red[o] = acc[2 * half + mh][j][r];
+                }
+        __syncthreads();
+        if (kgrp == 0) {
+#pragma unroll
+            for (int mh = 0; mh < 2; mh++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        acc[2 * half + mh][j][r] += red[(((wave * 2 + mh) * 2 + j) * 16 + r) * 64 + lane];
+        }
+    }
+    if (kgrp == 1) return;
 
     // D layout of the 32x32 MFMA: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #pragma unroll
@@ -347,10 +385,11 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     a.M = M, a.N = N, a.K = K;
     a.mtiles = (M + kBM - 1) / kBM, a.ntiles = (N + kBN - 1) / kBN;
     const int tiles = a.mtiles * a.ntiles, nchunks = K / kBK;
-    // Split K so that the grid covers the CUs, at least 4 chunks per split.
+    // Split K so that the grid covers the CUs, at least 8 chunks per split (4
+    // per K-group).
     int splits = (qmm_cu_count() + tiles / 2) / tiles;
     splits = splits < 1 ? 1 : splits;
-    splits = splits > nchunks / 4 ? nchunks / 4 : splits;
+    splits = splits > nchunks / 8 ? nchunks / 8 : splits;
     splits = splits < 1 ? 1 : splits;
     if (splits > 1) {
         a.cps = (nchunks + splits - 1) / splits;
