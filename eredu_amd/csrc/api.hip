@@ -232,7 +232,7 @@ extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, co
                             w, scales, biases, int(M), int(N), int(K), st))
             return check_launch("quantized_matmul (qmv)");
     }
-    if (mfma_ok && M > 16 && N % 128 == 0 && K % 64 == 0) {
+    if (mfma_ok && M > 16 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8)) {
         if (launch_qmm_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
                             w, scales, biases, int(M), int(N), int(K), st))
             return check_launch("quantized_matmul (qmm)");

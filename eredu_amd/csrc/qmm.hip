@@ -241,7 +241,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
             for (int mi = 0; mi < 4; mi++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
-                    acc[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], __builtin_bit_cast(bf16x8, bq[j][t]),
+                    acc[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bq[j][t]), a[mi],
                                                                          acc[mi][j], 0, 0, 0);
         }
     };
@@ -272,21 +272,24 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         }
     }
 done:
-    // The second K-group's sums go to LDS (half the rows at a time: 64 KiB),
-    // the first adds them.  Layout: [wave][mi & 1][j][r][lane] floats.
+    // The second K-group's sums go to LDS (half the row blocks at a time:
+    // 64 KiB), the first adds them.  Layout: [wave][mi & 1][j][q][lane] x 16 B,
+    // q = the run of 4 accumulator registers.
 #pragma unroll
     for (int half = 0; half < 2; half++) {
         __syncthreads();
-        float* red = reinterpret_cast<float*>(lds_all);
+        f32x4* red = reinterpret_cast<f32x4*>(lds_all);
+        if (kgrp == 1) {
 #pragma unroll
-        for (int mh = 0; mh < 2; mh++)
+            for (int mh = 0; mh < 2; mh++)
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+                for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int o = (((wave * 2 + mh) * 2 + j) * 16 + r) * 64 + lane;
-                    if (kgrp == 1) red[o] = acc[2 * half + mh][j][r];
-                }
+                    for (int q = 0; q < 4; q++)
+                        red[(((wave * 2 + mh) * 2 + j) * 4 + q) * 64 + lane] =
+                            f32x4{acc[2 * half + mh][j][4 * q], acc[2 * half + mh][j][4 * q + 1],
+                                  acc[2 * half + mh][j][4 * q + 2], acc[2 * half + mh][j][4 * q + 3]};
+        }
         __syncthreads();
         if (kgrp == 0) {
 #pragma unroll
@@ -294,29 +297,39 @@ done:
 #pragma unroll
                 for (int j = 0; j < 2; j++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        acc[2 * half + mh][j][r] += red[(((wave * 2 + mh) * 2 + j) * 16 + r) * 64 + lane];
+                    for (int q = 0; q < 4; q++) {
+                        const f32x4 v = red[(((wave * 2 + mh) * 2 + j) * 4 + q) * 64 + lane];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[2 * half + mh][j][4 * q + e] += v[e];
+                    }
         }
     }
     if (kgrp == 1) return;
 
-    // D layout of the 32x32 MFMA: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    // The MFMA computed y^T blocks (weights as the first operand): register r
+    // of lane l holds row m = 32 mi + l % 32 and column n = 32 j + 8 (r / 4) +
+    // 4 (l / 32) + r % 4, so each run of 4 registers is 4 adjacent columns of
+    // one row.  Columns past N are whole waves (N % 128 == 0).
+    if (n0 + 64 * wave >= N) return;
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int mi = 0; mi < 4; mi++) {
+        const int m = m0 + 32 * mi + l32;
+        if (m < M) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + 64 * wave + 32 * j + l32;
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + 32 * mi + 8 * (r >> 2) + 4 * kb + (r & 3);
-                if (m < M && n < N) {
-                    if constexpr (SPLIT)
-                        args.ws[(int64_t(split) * M + m) * N + n] = acc[mi][j][r];
-                    else
-                        args.y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(acc[mi][j][r]));
+                for (int q = 0; q < 4; q++) {
+                    const int n = n0 + 64 * wave + 32 * j + 8 * q + 4 * kb;
+                    const f32x4 v = {acc[mi][j][4 * q], acc[mi][j][4 * q + 1], acc[mi][j][4 * q + 2], acc[mi][j][4 * q + 3]};
+                    if constexpr (SPLIT) {
+                        *reinterpret_cast<f32x4*>(args.ws + (int64_t(split) * M + m) * N + n) = v;
+                    } else {
+                        const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
+                        *reinterpret_cast<uint2*>(args.y + int64_t(m) * N + n) = make_uint2(lo, hi);
+                    }
                 }
-            }
         }
+    }
 }
 
 // y = bf16(sum over splits of the partial tiles), splits summed in order.
