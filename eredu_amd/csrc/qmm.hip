@@ -53,7 +53,7 @@ typedef __bf16 q_bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kBM = 128, kBN = 256, kBK = 64;
 constexpr int kQmmThreads = 512;        // two K-groups of 4 waves
 constexpr int kLdsBuf = kBM * kBK * 2;  // bytes per activation buffer
-constexpr int kRing = 3;                // register slots of the load ring
+constexpr int kRing = 3;                // slots of the load rings (codes in registers, activations in LDS)
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     const q_bf16x2 p = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};  // RNE (v_cvt_pk_bf16_f32)
@@ -88,25 +88,38 @@ __device__ __forceinline__ q_u32x4 dequant8<8>(const uint32_t* words, float s, f
     return r;
 }
 
-// One ring slot: this lane's codes and parameters (2 column blocks x 32 codes).
-template <int BITS>
+// One ring slot: this lane's codes (2 column blocks x 32 codes) and, unless
+// the parameters come in windows, the scale and bias of each block.
+template <int BITS, bool PARAMS>
 struct QmmSlot {
     static constexpr int WORDS = BITS;  // 32 codes * BITS / 32
     q_u32x4 w[2][WORDS / 4];
     uint32_t s[2], b[2];
 };
+template <int BITS>
+struct QmmSlot<BITS, false> {
+    static constexpr int WORDS = BITS;
+    q_u32x4 w[2][WORDS / 4];
+};
 
 // Reads every register of a slot in an empty asm statement (the never-taken
 // side of an opaque_one() guard): every path then retires the slot's loads,
 // which keeps the compiler's wait analysis exact at the join.
-template <int BITS>
-__device__ __forceinline__ void qmm_retire(const QmmSlot<BITS>& s) {
+template <int BITS, bool PARAMS>
+__device__ __forceinline__ void qmm_retire(const QmmSlot<BITS, PARAMS>& s) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
 #pragma unroll
-        for (int i = 0; i < QmmSlot<BITS>::WORDS / 4; i++) asm volatile("" ::"v"(s.w[j][i]));
-        asm volatile("" ::"v"(s.s[j]), "v"(s.b[j]));
+        for (int i = 0; i < QmmSlot<BITS, PARAMS>::WORDS / 4; i++) asm volatile("" ::"v"(s.w[j][i]));
+        if constexpr (PARAMS) asm volatile("" ::"v"(s.s[j]), "v"(s.b[j]));
     }
+}
+
+// s_waitcnt vmcnt(N), other counters untouched.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 template <typename ST>
@@ -126,10 +139,18 @@ struct QmmArgs {
     int M, N, K, mtiles, ntiles, splits, cps;  // cps: chunks per split
 };
 
-template <int BITS, int GS, typename ST, bool SPLIT>
+// PW (parameter windows, group size 64 with an even number of groups per row
+// and an even first chunk per split): instead of two 2-byte loads per column
+// block and step, which touch one cache line per row each, a lane loads the
+// scales and biases of 6 consecutive groups (3 steps of each K-group) with
+// one 12-byte load each.
+template <int BITS, int GS, typename ST, bool SPLIT, bool PW>
 __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void qmm_mfma_kernel(
     const QmmArgs args) {
-    __shared__ __attribute__((aligned(16))) char lds_all[2 * 2 * kLdsBuf];  // [K-group][buffer]
+    // Activation ring: three buffers per K-group.  Separate arrays, so that
+    // the compiler's LDS alias scopes tell the buffers apart and a read of one
+    // does not wait for the loads still landing in another.
+    __shared__ __attribute__((aligned(16))) char abuf0[2 * kLdsBuf], abuf1[2 * kLdsBuf], abuf2[2 * kLdsBuf];
     const int M = args.M, N = args.N, K = args.K;
 
     // Tile and split of this workgroup: the workgroups of one XCD (id % 8)
@@ -149,7 +170,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const int tid = threadIdx.x & 255;                                         // thread within the K-group
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);                 // column quarter
     const int l32 = lane & 31, kb = lane >> 5;
-    char* lds = lds_all + kgrp * 2 * kLdsBuf;
+    const int gofs = kgrp * kLdsBuf;  // this K-group's part of each ring buffer
     const int steps = (nloc + 1) / 2;  // chunks per K-group (the second may have one fewer)
     const int G = K / GS;
 
@@ -159,14 +180,16 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const __amdgpu_buffer_rsrc_t br = raw_rsrc(args.b ? args.b : args.s, args.b ? uint32_t(N) * uint32_t(G) * 2u : 0u);
 
     // Lane offsets (chunk 0); rows past M and columns past N read zero.
-    // Activations: thread tid copies the 16-byte chunks q = tid + 256 i
-    // (row q / 8, chunk q % 8) of each 128 x 64 tile.
-    uint32_t a_goff[4], a_loff[4];
+    // Activations go straight from memory to LDS: load i of wave w fills the
+    // 1 KiB (8 rows of 128 B) at (4 w + i) KiB of the 128 x 64 tile, lane l
+    // the 16 B at 16 l, i.e. row 8 (4 w + i) + l / 8, slot l % 8.  Slot p of
+    // row r holds the row's 16-byte chunk p ^ (r & 7), so the lane loads chunk
+    // (l % 8) ^ (l / 8).
+    uint32_t a_goff[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int q = tid + 256 * i, row = q >> 3, c = q & 7;
+        const int row = 8 * (4 * wave + i) + (lane >> 3), c = (lane & 7) ^ (lane >> 3);
         a_goff[i] = m0 + row < M ? (uint32_t(m0 + row) * uint32_t(K) + uint32_t(8 * c)) * 2u : kOutOfRange;
-        a_loff[i] = uint32_t(row * (kBK * 2) + ((c ^ (row & 7)) << 4));
     }
     // Weight rows of this lane: columns n0 + 64 wave + 32 j + l32, codes from 32 kb.
     uint32_t woff[2], soff[2];
@@ -174,7 +197,9 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     for (int j = 0; j < 2; j++) {
         const uint32_t n = uint32_t(n0 + 64 * wave + 32 * j + l32);
         woff[j] = int(n) < N ? n * uint32_t(K) * BITS / 8u + uint32_t(32 * kb) * BITS / 8u : kOutOfRange;
-        soff[j] = int(n) < N ? (n * uint32_t(G)) * 2u + uint32_t((32 * kb) / GS) * 2u : kOutOfRange;
+        // (windows: the row's parameters from the split's first group on)
+        soff[j] = int(n) < N ? (n * uint32_t(G)) * 2u + (PW ? uint32_t(c_begin) * 2u : uint32_t((32 * kb) / GS) * 2u)
+                             : kOutOfRange;
     }
     // (a lane's 32 codes lie in one group: group sizes are multiples of 32 and
     // chunks start at multiples of 64, so its group is k0 / GS + 32 kb / GS)
@@ -184,28 +209,52 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     auto chunk_k0 = [&](int i) __attribute__((always_inline)) {
         return (c_begin + min(2 * i + kgrp, nloc - 1)) * kBK;
     };
-    auto load_a = [&](q_u32x4* r, int i) __attribute__((always_inline)) {
+    auto load_a = [&](char* buf, int i) __attribute__((always_inline)) {
         const uint32_t ks = __builtin_amdgcn_readfirstlane(uint32_t(chunk_k0(i)) * 2u);
 #pragma unroll
-        for (int q = 0; q < 4; q++) r[q] = __builtin_amdgcn_raw_buffer_load_b128(xr, a_goff[q], ks, 0);
+        for (int q = 0; q < 4; q++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void*)(buf + gofs + (4 * wave + q) * 1024), 16,
+                a_goff[q], ks, 0, 0);
     };
-    auto load_b = [&](QmmSlot<BITS>& S, int i) __attribute__((always_inline)) {
+    typedef QmmSlot<BITS, !PW> Slot;
+    constexpr int NW = Slot::WORDS / 4;  // 16-byte code loads per column block
+    auto load_b = [&](Slot& S, int i) __attribute__((always_inline)) {
         const int k0 = chunk_k0(i);
         const uint32_t kw = __builtin_amdgcn_readfirstlane(uint32_t(k0) * BITS / 8u);
         const uint32_t kp = __builtin_amdgcn_readfirstlane(uint32_t(k0 / GS) * 2u);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
 #pragma unroll
-            for (int q = 0; q < QmmSlot<BITS>::WORDS / 4; q++)
-                S.w[j][q] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j] + 16 * q, kw, 0);
-            S.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], kp, 0);
-            S.b[j] = __builtin_amdgcn_raw_buffer_load_b16(br, soff[j], kp, 0);
+            for (int q = 0; q < NW; q++) S.w[j][q] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j] + 16 * q, kw, 0);
+            if constexpr (!PW) {
+                S.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], kp, 0);
+                S.b[j] = __builtin_amdgcn_raw_buffer_load_b16(br, soff[j], kp, 0);
+            }
         }
     };
-    auto store_a = [&](const q_u32x4* r, int buf) __attribute__((always_inline)) {
+    // Parameter window w (steps 3w .. 3w + 2, groups 6w .. 6w + 5 of the
+    // split): [slot][j][scale, bias][word]; step i reads word i % 3, half kgrp.
+    typedef uint32_t q_u32x3 __attribute__((ext_vector_type(3)));
+    q_u32x3 pwin[2][2][2];
+    auto load_pw = [&](q_u32x3 (&P)[2][2], int w) __attribute__((always_inline)) {
+        const uint32_t kq = __builtin_amdgcn_readfirstlane(uint32_t(6 * w) * 2u);
 #pragma unroll
-        for (int q = 0; q < 4; q++) *reinterpret_cast<q_u32x4*>(lds + buf * kLdsBuf + a_loff[q]) = r[q];
+        for (int j = 0; j < 2; j++) {
+            P[j][0] = __builtin_amdgcn_raw_buffer_load_b96(sr, soff[j], kq, 0);
+            P[j][1] = __builtin_amdgcn_raw_buffer_load_b96(br, soff[j], kq, 0);
+        }
     };
+    // Before a barrier: this wave's activation loads for the next step have
+    // landed (only the newest step's loads, codes then activations, may still
+    // be in flight; memory operations complete in order).  With windows, a
+    // step that also requested a window has 4 more loads in flight.
+    auto wait_a = [&](bool window_step) __attribute__((always_inline)) {
+        constexpr int n = 2 * NW + (PW ? 0 : 4) + 4;
+        if (PW && window_step) wait_vmcnt<n + 4>();
+        else wait_vmcnt<n>();
+    };
+    auto barrier = [&]() __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
 
     // A operand of this lane for step t and row block mi: row 32 mi + l32,
     // chunk (4 kb + t) ^ (row & 7) (row & 7 = l32 & 7 for every mi).
@@ -219,18 +268,19 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = f32x16{};
 
-    auto compute = [&](const QmmSlot<BITS>& S, int buf) __attribute__((always_inline)) {
+    auto compute = [&](const Slot& S, const char* buf, const uint32_t* sbits, const uint32_t* bbits)
+                       __attribute__((always_inline)) {
         asm volatile("" ::: "memory");
         q_u32x4 bq[2][4];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const float s = qmm_param<ST>(S.s[j]);
-            const float b = qmm_param<ST>(S.b[j]);
+            const float s = qmm_param<ST>(sbits[j]);
+            const float b = qmm_param<ST>(bbits[j]);
 #pragma unroll
             for (int t = 0; t < 4; t++)
                 bq[j][t] = dequant8<BITS>(reinterpret_cast<const uint32_t*>(&S.w[j][0]) + t * BITS / 4, s, b);
         }
-        const char* base = lds + buf * kLdsBuf;
+        const char* base = buf + gofs;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             bf16x8 a[4];
@@ -246,62 +296,77 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         }
     };
 
-    // Prologue: chunk 0's activations in LDS; codes of chunks 0 and 1 requested.
-    QmmSlot<BITS> ring[kRing];
-    q_u32x4 areg[4];
-    load_a(areg, 0);
+    // Prologue: codes and activations of chunks 0 and 1 requested.
+    Slot ring[kRing];
+    if constexpr (PW) load_pw(pwin[0], 0);
     load_b(ring[0], 0);
+    load_a(abuf0, 0);
     load_b(ring[1], 1);
-    store_a(areg, 0);
-    __syncthreads();
+    load_a(abuf1, 1);
+    wait_a(false);
+    barrier();
 
-    // Step i: request chunk i + 1's activations and chunk i + 2's codes,
-    // compute chunk i (LDS buffer i & 1), store chunk i + 1's activations into
-    // the other buffer, synchronise.
-    for (int i0 = 0;; i0 += kRing) {
+    // Step i: request chunk i + 2's codes and activations (into the buffer
+    // every wave finished reading before the last barrier) and, with windows,
+    // at i % 3 == 1 the next window; compute chunk i, wait for chunk i + 1's
+    // activations, synchronise.
+    constexpr int U = PW ? 2 * kRing : kRing;
+    for (int i0 = 0;; i0 += U) {
 #pragma unroll
-        for (int r = 0; r < kRing; r++) {
+        for (int r = 0; r < U; r++) {
             const int i = i0 + r;
-            load_a(areg, i + 1);
+            char* const bufs[3] = {abuf0, abuf1, abuf2};
+            const bool wstep = PW && r % 3 == 1;
+            if constexpr (PW)
+                if (wstep) load_pw(pwin[(r / 3 + 1) % 2], i / 3 + 1);
             load_b(ring[(r + 2) % kRing], i + 2);
-            if (opaque_one() && 2 * i + kgrp < nloc) compute(ring[r], i & 1);
-            else qmm_retire(ring[r]);
+            load_a(bufs[(r + 2) % 3], i + 2);
+            uint32_t sb[2], bb[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                if constexpr (PW) {
+                    sb[j] = pwin[(r / 3) % 2][j][0][r % 3] >> (16 * kgrp);
+                    bb[j] = pwin[(r / 3) % 2][j][1][r % 3] >> (16 * kgrp);
+                } else {
+                    sb[j] = ring[r % kRing].s[j];
+                    bb[j] = ring[r % kRing].b[j];
+                }
+            }
+            if (opaque_one() && 2 * i + kgrp < nloc) compute(ring[r % kRing], bufs[r % 3], sb, bb);
+            else qmm_retire(ring[r % kRing]);
             if (i + 1 >= steps) goto done;
-            store_a(areg, (i + 1) & 1);
-            __syncthreads();
+            wait_a(wstep);
+            barrier();
         }
     }
 done:
-    // The second K-group's sums go to LDS (half the row blocks at a time:
-    // 64 KiB), the first adds them.  Layout: [wave][mi & 1][j][q][lane] x 16 B,
-    // q = the run of 4 accumulator registers.
+    // Every load has landed (the ring buffers are reused below).
+    __builtin_amdgcn_s_waitcnt(0);
+    // The second K-group's sums go to LDS, one row block (32 KiB) at a time
+    // through alternating buffers, and the first adds them.  Layout:
+    // [wave][j][q][lane] x 16 B, q = the run of 4 accumulator registers.
+    __syncthreads();
 #pragma unroll
-    for (int half = 0; half < 2; half++) {
-        __syncthreads();
-        f32x4* red = reinterpret_cast<f32x4*>(lds_all);
+    for (int mi = 0; mi < 4; mi++) {
+        f32x4* red = reinterpret_cast<f32x4*>(mi == 1 ? abuf1 : mi == 2 ? abuf2 : abuf0);
         if (kgrp == 1) {
 #pragma unroll
-            for (int mh = 0; mh < 2; mh++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        red[(((wave * 2 + mh) * 2 + j) * 4 + q) * 64 + lane] =
-                            f32x4{acc[2 * half + mh][j][4 * q], acc[2 * half + mh][j][4 * q + 1],
-                                  acc[2 * half + mh][j][4 * q + 2], acc[2 * half + mh][j][4 * q + 3]};
+                for (int q = 0; q < 4; q++)
+                    red[((wave * 2 + j) * 4 + q) * 64 + lane] =
+                        f32x4{acc[mi][j][4 * q], acc[mi][j][4 * q + 1], acc[mi][j][4 * q + 2], acc[mi][j][4 * q + 3]};
         }
         __syncthreads();
         if (kgrp == 0) {
 #pragma unroll
-            for (int mh = 0; mh < 2; mh++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 v = red[((wave * 2 + j) * 4 + q) * 64 + lane];
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const f32x4 v = red[(((wave * 2 + mh) * 2 + j) * 4 + q) * 64 + lane];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) acc[2 * half + mh][j][4 * q + e] += v[e];
-                    }
+                    for (int e = 0; e < 4; e++) acc[mi][j][4 * q + e] += v[e];
+                }
         }
     }
     if (kgrp == 1) return;
@@ -406,17 +471,23 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     splits = splits < 1 ? 1 : splits;
     if (splits > 1) {
         a.cps = (nchunks + splits - 1) / splits;
+        a.cps += a.cps & 1;  // even, so that parameter windows stay 4-byte aligned
         splits = (nchunks + a.cps - 1) / a.cps;  // no empty split
         a.ws = qmm_workspace(size_t(splits) * size_t(M) * size_t(N) * 4u, st);
         if (!a.ws) splits = 1;
     }
     a.splits = splits;
+    if (splits == 1) a.cps = nchunks;
+    // parameter windows: group size 64, rows of an even number of groups
+    const bool pw = GS == 64 && (K / GS) % 2 == 0 && a.cps % 2 == 0;
+    const dim3 grid(unsigned(tiles * splits)), block(kQmmThreads);
     if (splits == 1) {
-        a.cps = nchunks;
-        qmm_mfma_kernel<BITS, GS, ST, false><<<dim3(unsigned(tiles)), dim3(kQmmThreads), 0, st>>>(a);
+        if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64><<<grid, block, 0, st>>>(a);
+        else qmm_mfma_kernel<BITS, GS, ST, false, false><<<grid, block, 0, st>>>(a);
         return;
     }
-    qmm_mfma_kernel<BITS, GS, ST, true><<<dim3(unsigned(tiles * splits)), dim3(kQmmThreads), 0, st>>>(a);
+    if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64><<<grid, block, 0, st>>>(a);
+    else qmm_mfma_kernel<BITS, GS, ST, true, false><<<grid, block, 0, st>>>(a);
     const int64_t mn = int64_t(M) * N;
     qmm_split_reduce<<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(y, a.ws, mn, splits,
                                                                                     aligned(y, 8));
