@@ -307,6 +307,10 @@ def main():
     ap.add_argument("--quick", action="store_true", help="decode steps only (no qmm / gguf / per-shape sweeps)")
     ap.add_argument("--headline-only", action="store_true",
                     help="the headline step only (the run a kernel-trace profile of the roofline kernel uses)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill qmm sweep, one JSON object of its figures (for kernel-trace profiles)")
+    ap.add_argument("--gguf-only", action="store_true",
+                    help="only the GGUF dequant/convert sweep, one JSON object of its figures")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build runs on a single GPU "
@@ -318,6 +322,16 @@ def main():
 
     _lib().lib()
     torch.cuda.set_device(0)
+    if args.prefill_only or args.gguf_only:
+        out = {}
+        if args.prefill_only:
+            log("[bench] qmm prefill")
+            out["qmm"] = bench_qmm(args.steps, args.warmup)
+        if args.gguf_only:
+            log("[bench] gguf")
+            out["gguf"] = bench_gguf(args.steps, args.warmup)
+        print(json.dumps(out), flush=True)
+        return
     gen = torch.Generator(device="cuda").manual_seed(0)
     log("[bench] allocating 32 layers of 4-bit weights")
     layers = [{name: Linear(N, K, gen) for name, N, K in LAYER_SHAPES} for _ in range(LAYERS)]
