@@ -237,6 +237,55 @@ def bench_gguf(steps, warmup):
     return out
 
 
+VOCAB, N_HEADS, N_KV_HEADS, CACHE_TOKENS = 128256, 32, 8, 1024
+
+
+def build_decoder(layers, gen):
+    """the Llama-3-8B-shaped stack around the 32 layers' packed
+    projections -- bf16 embeddings and norms, a 4-bit LM head, a bf16 KV cache
+    of CACHE_TOKENS random N(0, 1) rows per layer, Llama-3 RoPE (theta 5e5,
+    llama3 scaling) -- for the batch-1 decode step of eredu_amd.decode."""
+    import torch
+
+    from eredu_amd import decode as E
+
+    def q(l):
+        return E.QLinear(l.w, l.s, l.b, BITS, GS)
+
+    bf = torch.bfloat16
+    norm = lambda: (1.0 + 0.1 * torch.randn((HIDDEN,), device="cuda", generator=gen)).to(bf)
+    dec_layers = [E.DecoderLayer(norm(), norm(), *(q(L[p]) for p in ("q", "k", "v", "o", "gate", "up", "down")))
+                  for L in layers]
+    embed = torch.empty((VOCAB, HIDDEN), dtype=bf, device="cuda")
+    for r0 in range(0, VOCAB, 8192):
+        embed[r0:r0 + 8192] = torch.randn((min(8192, VOCAB - r0), HIDDEN), device="cuda", generator=gen).to(bf)
+    lm = Linear(VOCAB, HIDDEN, gen)
+    max_seq = CACHE_TOKENS + 1
+    caches = [[torch.randn((N_KV_HEADS, max_seq, 128), device="cuda", generator=gen).to(bf) for _ in layers]
+              for _ in range(2)]
+    freqs = E.llama3_rope_freqs(128, 500000.0, 8.0, 1.0, 4.0, 8192)
+    return E.LlamaDecoder(dec_layers, embed, norm(), q(lm), n_heads=N_HEADS, n_kv_heads=N_KV_HEADS, eps=1e-5,
+                          freqs=freqs, max_seq=max_seq, k_caches=caches[0], v_caches=caches[1])
+
+
+def bench_decode_step(layers, steps, warmup, gen):
+    """Full batch-1 decode step as one HIP graph: tok/s, and the
+    step's algorithmic bytes against 8 TB/s."""
+    dec = build_decoder(layers, gen)
+    pos = CACHE_TOKENS
+    ms = Timer(lambda st: dec.step(pos)).ms_per_replay(steps, warmup)
+    nbytes = dec.bytes_per_step(pos)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    roof = HBM_PEAK_GBS * 1e9 / nbytes
+    out = {"ms": round(ms, 4), "tok/s": round(1e3 / ms, 1), "bytes_per_token": nbytes, "GB/s": round(gbs, 1),
+           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "roofline_tok/s": round(roof, 1),
+           "launches": dec.launches_per_step(),
+           "workload": "batch 1, 32 layers, H 4096, 32 q / 8 kv heads x 128, FFN 14336, vocab 128256, 4-bit g64 "
+                       "linears incl. LM head, bf16 embeddings/norms, 1024-token bf16 KV cache, greedy argmax"}
+    del dec
+    return out
+
+
 def bench_decode_variants(layers, args):
     """The decode step issued other ways: one launch per projection (the drop-in
     path), all seven projections per launch, and the grouped step at M = 8."""
@@ -311,6 +360,8 @@ def main():
                     help="only the prefill qmm sweep, one JSON object of its figures (for kernel-trace profiles)")
     ap.add_argument("--gguf-only", action="store_true",
                     help="only the GGUF dequant/convert sweep, one JSON object of its figures")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the full decode step of configs[4], one JSON object of its figures")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build runs on a single GPU "
@@ -336,6 +387,10 @@ def main():
     log("[bench] allocating 32 layers of 4-bit weights")
     layers = [{name: Linear(N, K, gen) for name, N, K in LAYER_SHAPES} for _ in range(LAYERS)]
     torch.cuda.synchronize()
+    if args.decode_only:
+        log("[bench] full decode step (configs[4])")
+        print(json.dumps({"decode_step": bench_decode_step(layers, args.steps, args.warmup, gen)}), flush=True)
+        return
 
     log("[bench] decode step M=1, grouped launches")
     ms, nbytes, launches = bench_decode(layers, 1, DECODE_GROUPS, args.steps, args.warmup)
@@ -345,7 +400,11 @@ def main():
         args.quick = args.no_cpu = True
     else:
         detail.update(bench_decode_variants(layers, args))
+    step = None
     if not args.quick:
+        log("[bench] full decode step (configs[4])")
+        step = bench_decode_step(layers, args.steps, args.warmup, gen)
+        detail["decode_step_config5"] = step
         log("[bench] per-shape qmv")
         detail["qmv_M1_per_shape"] = bench_per_shape(layers, 1, args.steps, args.warmup)
         detail["qmv_M8_per_shape"] = bench_per_shape(layers, 8, args.steps, args.warmup)
@@ -408,6 +467,9 @@ def main():
         "cpu_baseline": cpu,
         "detail": detail,
     }
+    if step is not None:  # the metric's second figure: end-to-end decode of configs[4]
+        line["decode_tok_s"] = step["tok/s"]
+        line["decode_tok_s_frac_roofline"] = round(step["tok/s"] / step["roofline_tok/s"], 4)
     print(json.dumps(line), flush=True)
 
 

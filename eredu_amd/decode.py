@@ -1,0 +1,275 @@
+"""Batch-1 decode step of a Llama-shaped model on the HIP kernels.
+
+Mirrors the caller structure of the reference's decoder
+(eredu-architectures/src/llama.rs): ``Decoder::embed`` (:576-582), per layer
+``TransformerBlock::forward`` (:477-495) -- input RMSNorm, q/k/v projections,
+RoPE + KV-cache update + attention (``Attention::attend``, :296-330), output
+projection, residual add, post-attention RMSNorm, SwiGLU MLP (``Mlp``,
+:414-433), residual add -- then the final norm and ``Model::logits``
+(:649-658), and greedy selection of the next token.
+
+All seven projections per layer and the LM head go through the quantized
+matmul C ABI (q/k/v and gate/up as one grouped launch each, results
+bit-identical to separate calls); the rest through the decode entry points of
+``include/eredu_hip.h``.  Every buffer is allocated once, so a step can be
+captured in a HIP graph; the token id lives in device memory and the step
+reads it (embedding) and overwrites it (argmax), so graph replays generate
+successive tokens.  There is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native
+from ._native import check
+
+HEAD_DIM = 128
+
+
+def llama3_rope_freqs(dims: int, base: float, factor: float = 8.0, low_freq_factor: float = 1.0,
+                      high_freq_factor: float = 4.0, original_max_position_embeddings: int = 8192) -> np.ndarray:
+    """The rotary frequencies of Llama3Rope::new (eredu/src/backend/mlx/nn/rope.rs:105-186),
+    in f32 like the reference's arrays: base^(2i/dims), long wavelengths
+    (past orig / low_freq_factor) scaled by ``factor``, the band between
+    orig / high_freq_factor and orig / low_freq_factor interpolated.
+    ``factor = 1`` gives plain RoPE frequencies."""
+    f32 = np.float32
+    exps = np.arange(dims // 2, dtype=f32) * f32(2.0 / dims)
+    freqs = np.power(f32(base), exps).astype(f32)
+    old = f32(original_max_position_embeddings)
+    low_wl, high_wl = old / f32(low_freq_factor), old / f32(high_freq_factor)
+    wl = freqs * f32(2.0 * math.pi)
+    freqs = np.where(wl > low_wl, freqs * f32(factor), freqs).astype(f32)
+    medium = (wl > high_wl) & (wl < low_wl)
+    smooth = ((f32(1.0) / wl) * old - f32(low_freq_factor)) / f32(high_freq_factor - low_freq_factor)
+    freqs = np.where(medium, freqs / ((f32(1.0) - smooth) / f32(factor) + smooth), freqs).astype(f32)
+    return freqs
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _bf16(t: torch.Tensor, what: str) -> None:
+    if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+        raise _native.EreduError(f"{what} must be a contiguous bf16 CUDA tensor")
+
+
+def rms_norm(hidden: torch.Tensor, weight: torch.Tensor, eps: float,
+             residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``hidden += residual`` (in place, when given), then RMSNorm(hidden) * weight
+    (C ABI: eq_rms_norm)."""
+    for t, n in ((hidden, "hidden"), (weight, "weight")):
+        _bf16(t, n)
+    if residual is not None:
+        _bf16(residual, "residual")
+    dim = hidden.shape[-1]
+    out = torch.empty_like(hidden)
+    check(_native.lib().eq_rms_norm(out.data_ptr(), hidden.data_ptr(),
+                                    residual.data_ptr() if residual is not None else None, weight.data_ptr(),
+                                    hidden.numel() // dim, dim, float(eps), _native.EQ_DTYPE_BF16, _stream()))
+    return out
+
+
+def rope_attention_decode(q, k_new, v_new, k_cache, v_cache, freqs: torch.Tensor, pos: int, n_heads: int,
+                          n_kv_heads: int, scale: float) -> torch.Tensor:
+    """RoPE of q and k_new at ``pos``, cache update, grouped-query attention over
+    positions 0..pos (C ABI: eq_rope_attention_decode).  Caches are
+    [n_kv_heads, max_seq, 128] bf16 and are written at row ``pos``."""
+    for t, n in ((q, "q"), (k_new, "k_new"), (v_new, "v_new"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _bf16(t, n)
+    if freqs.dtype != torch.float32 or not freqs.is_cuda:
+        raise _native.EreduError("freqs must be a float32 CUDA tensor")
+    out = torch.empty((n_heads * HEAD_DIM,), dtype=torch.bfloat16, device=q.device)
+    check(_native.lib().eq_rope_attention_decode(
+        out.data_ptr(), q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        freqs.data_ptr(), int(pos), k_cache.shape[1], n_heads, n_kv_heads, HEAD_DIM, float(scale),
+        _native.EQ_DTYPE_BF16, _stream()))
+    return out
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up with the reference's bf16 roundings (C ABI: eq_silu_mul)."""
+    _bf16(gate, "gate")
+    _bf16(up, "up")
+    out = torch.empty_like(gate)
+    check(_native.lib().eq_silu_mul(out.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel(),
+                                    _native.EQ_DTYPE_BF16, _stream()))
+    return out
+
+
+def embedding(table: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """Rows of a bf16 table by int32 device token ids (C ABI: eq_embedding)."""
+    _bf16(table, "table")
+    if tokens.dtype != torch.int32 or not tokens.is_cuda:
+        raise _native.EreduError("tokens must be an int32 CUDA tensor")
+    out = torch.empty((tokens.numel(), table.shape[1]), dtype=torch.bfloat16, device=table.device)
+    check(_native.lib().eq_embedding(out.data_ptr(), table.data_ptr(), tokens.data_ptr(), tokens.numel(),
+                                     table.shape[0], table.shape[1], _native.EQ_DTYPE_BF16, _stream()))
+    return out
+
+
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """First index of the largest value per row, int32 (C ABI: eq_argmax)."""
+    _bf16(logits, "logits")
+    n = logits.shape[-1]
+    out = torch.empty((logits.numel() // n,), dtype=torch.int32, device=logits.device)
+    check(_native.lib().eq_argmax(out.data_ptr(), logits.data_ptr(), logits.numel() // n, n,
+                                  _native.EQ_DTYPE_BF16, _stream()))
+    return out
+
+
+@dataclass
+class QLinear:
+    """A packed projection W [N, K] (transpose = true): codes int32/uint32
+    [N, K * bits / 32], bf16 scales and biases [N, K / group_size]."""
+
+    w: torch.Tensor
+    scales: torch.Tensor
+    biases: Optional[torch.Tensor]
+    bits: int = 4
+    group_size: int = 64
+
+    @property
+    def N(self) -> int:
+        return self.w.shape[0]
+
+    @property
+    def K(self) -> int:
+        return self.w.shape[1] * 32 // self.bits
+
+
+@dataclass
+class DecoderLayer:
+    in_norm: torch.Tensor
+    post_norm: torch.Tensor
+    q: QLinear
+    k: QLinear
+    v: QLinear
+    o: QLinear
+    gate: QLinear
+    up: QLinear
+    down: QLinear
+
+
+class LlamaDecoder:
+    """Batch-1 greedy decode of a Llama-shaped model.  ``step(pos)`` embeds the
+    token in ``self.token``, runs every layer with the cache row ``pos`` as the
+    new position, and writes the argmax of the logits back into ``self.token``.
+    ``step`` enqueues on the current stream and allocates nothing."""
+
+    def __init__(self, layers: Sequence[DecoderLayer], embed: torch.Tensor, final_norm: torch.Tensor,
+                 lm_head: QLinear, *, n_heads: int, n_kv_heads: int, eps: float, freqs: np.ndarray, max_seq: int,
+                 k_caches: Optional[List[torch.Tensor]] = None, v_caches: Optional[List[torch.Tensor]] = None):
+        dev = embed.device
+        self.layers = list(layers)
+        self.embed, self.final_norm, self.lm_head = embed, final_norm, lm_head
+        self.n_heads, self.n_kv_heads, self.eps, self.max_seq = n_heads, n_kv_heads, float(eps), max_seq
+        self.hidden = embed.shape[1]
+        self.vocab = embed.shape[0]
+        self.scale = 1.0 / math.sqrt(HEAD_DIM)
+        self.freqs = torch.from_numpy(np.ascontiguousarray(freqs, dtype=np.float32)).to(dev)
+        L0 = self.layers[0]
+        self.ffn = L0.gate.N
+        H, bf = self.hidden, torch.bfloat16
+        if n_heads * HEAD_DIM != L0.q.N or n_kv_heads * HEAD_DIM != L0.k.N or L0.q.K != H:
+            raise _native.EreduError("projection shapes do not match the head geometry")
+        cache_shape = (n_kv_heads, max_seq, HEAD_DIM)
+        self.k_caches = k_caches if k_caches is not None else [torch.zeros(cache_shape, dtype=bf, device=dev)
+                                                                for _ in self.layers]
+        self.v_caches = v_caches if v_caches is not None else [torch.zeros(cache_shape, dtype=bf, device=dev)
+                                                                for _ in self.layers]
+        e = lambda n: torch.empty((n,), dtype=bf, device=dev)
+        self.x, self.h = e(H), e(H)
+        self.q, self.k, self.v = e(L0.q.N), e(L0.k.N), e(L0.v.N)
+        self.att, self.o = e(L0.q.N), e(H)
+        self.gate, self.up, self.act, self.down = e(self.ffn), e(self.ffn), e(self.ffn), e(H)
+        self.logits = e(lm_head.N)
+        self.token = torch.zeros((1,), dtype=torch.int32, device=dev)
+        # grouped problems (pointers fixed for the decoder's lifetime)
+        n = _native
+        self._qkv, self._gu = [], []
+        for Lr in self.layers:
+            qkv = (n.QmmProblem * 3)()
+            for i, (lin, y) in enumerate(((Lr.q, self.q), (Lr.k, self.k), (Lr.v, self.v))):
+                qkv[i] = self._problem(lin, self.h, y)
+            gu = (n.QmmProblem * 2)()
+            for i, (lin, y) in enumerate(((Lr.gate, self.gate), (Lr.up, self.up))):
+                gu[i] = self._problem(lin, self.h, y)
+            self._qkv.append(qkv)
+            self._gu.append(gu)
+
+    @staticmethod
+    def _problem(lin: QLinear, x: torch.Tensor, y: torch.Tensor):
+        return _native.QmmProblem(y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.scales.data_ptr(),
+                                  lin.biases.data_ptr() if lin.biases is not None else None, lin.N, lin.K)
+
+    def _group(self, probs, count: int, lin: QLinear, st: int) -> None:
+        n = _native
+        check(n.lib().eq_quantized_matmul_batched(probs, count, 1, True, lin.group_size, lin.bits, b"affine",
+                                                  n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, st))
+
+    def _linear(self, lin: QLinear, x: torch.Tensor, y: torch.Tensor, st: int) -> None:
+        n = _native
+        check(n.lib().eq_quantized_matmul(
+            y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.scales.data_ptr(),
+            lin.biases.data_ptr() if lin.biases is not None else None, 1, lin.N, lin.K, True, lin.group_size,
+            lin.bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, st))
+
+    def launches_per_step(self) -> int:
+        # embedding; per layer 2 norms, 4 projection launches, attention (2
+        # kernels), silu_mul; final norm, LM head, argmax
+        return 1 + len(self.layers) * 9 + 3
+
+    def step(self, pos: int) -> None:
+        if not 0 <= pos < self.max_seq:
+            raise _native.EreduError(f"position {pos} outside the cache of {self.max_seq}")
+        n, L = _native, _native.lib()
+        st = _stream()
+        bf = n.EQ_DTYPE_BF16
+        H, F = self.hidden, self.ffn
+        check(L.eq_embedding(self.x.data_ptr(), self.embed.data_ptr(), self.token.data_ptr(), 1, self.vocab, H, bf,
+                             st))
+        resid = None
+        for li, Lr in enumerate(self.layers):
+            check(L.eq_rms_norm(self.h.data_ptr(), self.x.data_ptr(), resid, Lr.in_norm.data_ptr(), 1, H, self.eps,
+                                bf, st))
+            self._group(self._qkv[li], 3, Lr.q, st)
+            check(L.eq_rope_attention_decode(
+                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                self.k_caches[li].data_ptr(), self.v_caches[li].data_ptr(), self.freqs.data_ptr(), pos, self.max_seq,
+                self.n_heads, self.n_kv_heads, HEAD_DIM, self.scale, bf, st))
+            self._linear(Lr.o, self.att, self.o, st)
+            check(L.eq_rms_norm(self.h.data_ptr(), self.x.data_ptr(), self.o.data_ptr(), Lr.post_norm.data_ptr(), 1,
+                                H, self.eps, bf, st))
+            self._group(self._gu[li], 2, Lr.gate, st)
+            check(L.eq_silu_mul(self.act.data_ptr(), self.gate.data_ptr(), self.up.data_ptr(), F, bf, st))
+            self._linear(Lr.down, self.act, self.down, st)
+            resid = self.down.data_ptr()
+        check(L.eq_rms_norm(self.h.data_ptr(), self.x.data_ptr(), resid, self.final_norm.data_ptr(), 1, H, self.eps,
+                            bf, st))
+        self._linear(self.lm_head, self.h, self.logits, st)
+        check(L.eq_argmax(self.token.data_ptr(), self.logits.data_ptr(), 1, self.lm_head.N, bf, st))
+
+    def bytes_per_step(self, pos: int) -> int:
+        """Algorithmic bytes of one step: packed projections (codes, scales,
+        biases, input and output vectors), the KV rows read and written,
+        norms, the embedding row and the logits."""
+        def lin_bytes(l: QLinear) -> int:
+            nb = 2 if l.biases is not None else 1
+            return l.N * l.K * l.bits // 8 + nb * 2 * l.N * (l.K // l.group_size) + 2 * l.K + 2 * l.N
+
+        total = sum(lin_bytes(getattr(Lr, p)) for Lr in self.layers
+                    for p in ("q", "k", "v", "o", "gate", "up", "down"))
+        total += lin_bytes(self.lm_head)
+        kv = 2 * self.n_kv_heads * HEAD_DIM * 2  # one row of K and of V
+        total += len(self.layers) * (kv * (pos + 1) + kv)  # rows 0..pos read, row pos written
+        total += len(self.layers) * 2 * self.hidden * 2 + self.hidden * 2  # norm weights
+        total += self.hidden * 2  # embedding row
+        return total

@@ -132,6 +132,53 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
                        int64_t rows, int64_t cols, int endian, int definition, int out_dtype,
                        eq_stream_t stream);
 
+/*
+ * Decode-step operations around the quantized projections of a Llama-shaped
+ * decoder at batch 1 (configs[4] of the measurement plan).  bf16 only
+ * (dtype must be EQ_DTYPE_BF16); no counterpart in the quantized-linear C ABI
+ * of the reference -- these replace the MLX calls a decoder layer makes
+ * between its projections.
+ */
+
+/* hidden[rows, dim] += residual (when residual is not NULL, each sum rounded
+ * to bf16, in place); out = hidden * rsqrt(mean(hidden^2) + eps) * weight.
+ * Replaces the block's residual adds and nn::RmsNorm (fast::rms_norm,
+ * safemlx/src/fast.rs:1119) in TransformerBlock::forward
+ * (eredu-architectures/src/llama.rs:477-495).  dim % 8 == 0, 16-byte aligned. */
+int eq_rms_norm(void* out, void* hidden, const void* residual, const void* weight, int64_t rows,
+                int64_t dim, float eps, int dtype, eq_stream_t stream);
+
+/* One decode position of grouped-query attention with a KV cache:
+ *   q [n_heads, 128], k_new / v_new [n_kv_heads, 128] (the projections' outputs);
+ *   q and k_new rotated by RoPE (half-split pairs, angle pos / freqs[i],
+ *   freqs[64] f32 = the Llama3Rope frequencies, eredu/src/backend/mlx/nn/rope.rs:105-186);
+ *   rotated k_new and v_new stored at row pos of k_cache / v_cache
+ *   [n_kv_heads, max_seq, 128];
+ *   out [n_heads, 128] = softmax(scale * q . K[0..pos]^T) . V[0..pos], head h
+ *   reading KV head h / (n_heads / n_kv_heads).
+ * Replaces Attention::attend (llama.rs:296-330): rotary forward, cache
+ * update_for_attention and fast::scaled_dot_product_attention.  head_dim must
+ * be 128 and n_heads / n_kv_heads at most 4.  Uses a library-owned workspace:
+ * the first call on a device must not be under stream capture. */
+int eq_rope_attention_decode(void* out, const void* q, const void* k_new, const void* v_new,
+                             void* k_cache, void* v_cache, const float* freqs, int64_t pos,
+                             int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
+                             int dtype, eq_stream_t stream);
+
+/* out[n] = silu(gate) * up, silu(x) = x * sigmoid(x), each op rounded to bf16
+ * (Mlp::hidden, llama.rs:414-422; eredu/src/backend/mlx/nn/layers.rs:21).
+ * n % 8 == 0, 16-byte aligned. */
+int eq_silu_mul(void* out, const void* gate, const void* up, int64_t n, int dtype, eq_stream_t stream);
+
+/* out[t, :] = table[tokens[t], :] (zeros for an id outside [0, vocab)); tokens
+ * is device memory (Decoder::embed, llama.rs:576-582). */
+int eq_embedding(void* out, const void* table, const int32_t* tokens, int64_t n_tokens, int64_t vocab,
+                 int64_t dim, int dtype, eq_stream_t stream);
+
+/* out[r] = first index of the largest value of logits[r, 0..n) (greedy
+ * decoding of the model's logits, llama.rs:649-658). */
+int eq_argmax(int32_t* out, const void* logits, int64_t rows, int64_t n, int dtype, eq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,7 +25,8 @@ def declared_functions():
 def test_header_declares_the_boundary():
     assert declared_functions() == sorted(
         ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
-         "eq_gguf_convert_affine", "eq_gguf_dequantize"]
+         "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
+         "eq_embedding", "eq_argmax"]
     )
 
 
@@ -143,3 +144,36 @@ def test_host_mirror_fails_loudly_without_gpu_tensors():
     s = torch.zeros(16, 1, dtype=torch.bfloat16)
     with pytest.raises(EreduError, match="GPU"):
         quantized_matmul(x, w, s, s, transpose=True)
+
+
+def _rejects(status, fragment):
+    assert status == 1
+    assert fragment in L.eq_last_error().decode()
+
+
+def test_decode_ops_reject_bad_arguments():
+    bf16, f32 = _native.EQ_DTYPE_BF16, _native.EQ_DTYPE_F32
+    # rms_norm: dtype, dim, alignment, null
+    _rejects(L.eq_rms_norm(16, 16, None, 16, 1, 4096, 1e-5, f32, None), "only bf16")
+    _rejects(L.eq_rms_norm(16, 16, None, 16, 1, 4095, 1e-5, bf16, None), "multiple of 8")
+    _rejects(L.eq_rms_norm(16, 18, None, 16, 1, 4096, 1e-5, bf16, None), "aligned")
+    _rejects(L.eq_rms_norm(None, 16, None, 16, 1, 4096, 1e-5, bf16, None), "null")
+    _rejects(L.eq_rms_norm(16, 16, None, 16, 1, 4096, -1.0, bf16, None), "eps")
+    # attention: head width, grouping, position range
+    att = lambda **k: L.eq_rope_attention_decode(16, 16, 16, 16, 16, 16, 16, k.get("pos", 10), k.get("max_seq", 64),
+                                                  k.get("h", 32), k.get("kv", 8), k.get("d", 128), 0.088,
+                                                  k.get("dt", bf16), None)
+    _rejects(att(d=64), "head_dim")
+    _rejects(att(h=33), "n_heads")
+    _rejects(att(h=64, kv=8), "n_heads")
+    _rejects(att(pos=64), "pos")
+    _rejects(att(pos=-1), "pos")
+    _rejects(att(dt=f32), "only bf16")
+    # silu_mul, embedding, argmax
+    _rejects(L.eq_silu_mul(16, 16, 16, 12, bf16, None), "multiple of 8")
+    _rejects(L.eq_embedding(16, 16, 16, 70000, 100, 64, bf16, None), "n_tokens")
+    _rejects(L.eq_embedding(16, 16, 16, 1, 100, 60, bf16, None), "dim")
+    _rejects(L.eq_argmax(16, 16, 1, 0, bf16, None), "0 < n")
+    # zero-size calls succeed without launching
+    assert L.eq_rms_norm(16, 16, None, 16, 0, 4096, 1e-5, bf16, None) == 0
+    assert L.eq_silu_mul(16, 16, 16, 0, bf16, None) == 0

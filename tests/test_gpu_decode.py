@@ -1,0 +1,230 @@
+"""Parity of the decode-step kernels (include/eredu_hip.h: eq_rms_norm,
+eq_rope_attention_decode, eq_silu_mul, eq_embedding, eq_argmax) and of a
+whole batch-1 decode step of a small Llama-shaped model with the oracle
+(oracle/decode_oracle.py), through the C ABI via eredu_amd.decode.
+
+Tolerances (written here): bf16 results that the reference rounds once from
+an exact value -- residual sums, embedding rows, stored values, argmax -- are
+bit-exact; results that pass through transcendental functions or an f32 sum
+of another order (RMSNorm output, rotated keys, silu) are within 1 bf16 ulp
+of the oracle; attention outputs and logits are within
+1e-2 * RMS(ref) + 1/2 ulp_bf16(ref) elementwise (the matmul rule), with the
+decode step's logits compared after two layers of bf16 roundings at
+2e-2 * RMS(ref).
+"""
+import numpy as np
+import pytest
+import torch
+
+from eredu_amd import decode as E
+from oracle import decode_oracle as D
+from oracle import oracle as orc
+from tests.fixtures import dev_bf16, dev_words, host_bits16, host_f32, synthetic_linear
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(x):
+    return orc.f32_to_bf16_bits(np.asarray(x, dtype=np.float32))
+
+
+def randn_bits(shape, seed, std=1.0):
+    return bits(np.random.default_rng(seed).standard_normal(shape) * std)
+
+
+def ulp_bf16(v):
+    a = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 1e-30)))
+    return np.where(a > 0, 2.0 ** (e - 7), 2.0 ** -133)
+
+
+def within_ulps(got_bits, ref_f64, n=1):
+    got = D.bits_to_f64(got_bits)
+    return np.all(np.abs(got - ref_f64) <= n * ulp_bf16(ref_f64) + 1e-30)
+
+
+@pytest.mark.parametrize("dim", [64, 512, 4096, 14336])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rms_norm(cuda, dim, with_residual):
+    print(f"[case] rms_norm dim={dim} residual={with_residual}", flush=True)
+    x = randn_bits(dim, dim)
+    w = bits(1.0 + 0.1 * np.random.default_rng(dim + 1).standard_normal(dim))
+    r = randn_bits(dim, dim + 2) if with_residual else None
+    xd, wd = dev_bf16(x), dev_bf16(w)
+    out = E.rms_norm(xd, wd, 1e-5, dev_bf16(r) if r is not None else None)
+    torch.cuda.synchronize()
+    hid_ref, out_ref = D.rms_norm_bf16(x, w, 1e-5, r)
+    assert np.array_equal(host_bits16(xd), hid_ref)  # residual sum: exact
+    ref = D.rms_norm(D.bits_to_f64(hid_ref), D.bits_to_f64(w), 1e-5)
+    assert within_ulps(host_bits16(out), ref, 1)
+
+
+@pytest.mark.parametrize("n_heads,n_kv", [(32, 8), (4, 1), (4, 4), (8, 4)])
+@pytest.mark.parametrize("pos", [0, 5, 31, 32, 33, 100, 1024])
+def test_rope_attention_decode(cuda, n_heads, n_kv, pos):
+    print(f"[case] attention heads={n_heads}/{n_kv} pos={pos}", flush=True)
+    max_seq = 1100
+    seed = pos * 7 + n_heads
+    q = randn_bits(n_heads * 128, seed)
+    kn = randn_bits(n_kv * 128, seed + 1)
+    vn = randn_bits(n_kv * 128, seed + 2)
+    kc = randn_bits((n_kv, max_seq, 128), seed + 3)
+    vc = randn_bits((n_kv, max_seq, 128), seed + 4)
+    freqs = D.llama3_rope_freqs(128, 500000.0)
+    scale = 1.0 / np.sqrt(128.0)
+    kcd, vcd = dev_bf16(kc), dev_bf16(vc)
+    out = E.rope_attention_decode(dev_bf16(q), dev_bf16(kn), dev_bf16(vn), kcd, vcd,
+                                  torch.from_numpy(freqs).cuda(), pos, n_heads, n_kv, scale)
+    torch.cuda.synchronize()
+    ref, kc_ref, vc_ref = D.attention_decode(q, kn, vn, kc, vc, freqs, pos, n_heads, n_kv, scale)
+    got_k, got_v = host_bits16(kcd), host_bits16(vcd)
+    assert np.array_equal(got_v, vc_ref)
+    mask = np.ones(max_seq, dtype=bool)
+    mask[pos] = False
+    assert np.array_equal(got_k[:, mask], kc[:, mask])
+    rot = D.rope(D.bits_to_f64(kn).reshape(n_kv, 128), pos, freqs)
+    assert within_ulps(got_k[:, pos], rot, 1)
+    # the oracle with the GPU's stored key (a 1-ulp rotation difference moves
+    # the scores a little; the output rule below absorbs it either way)
+    ok, worst, rms = orc.matmul_within_tolerance(host_f32(out).reshape(n_heads, 128), ref, out_is_bf16=True)
+    assert ok, f"max|err|/RMS = {worst:.3e}"
+
+
+def test_attention_matches_torch_sdpa(cuda):
+    """Cross-check with torch's own attention in f32 on the rotated inputs."""
+    n_heads, n_kv, pos, max_seq = 32, 8, 777, 1024
+    q = randn_bits(n_heads * 128, 11)
+    kn, vn = randn_bits(n_kv * 128, 12), randn_bits(n_kv * 128, 13)
+    kc, vc = randn_bits((n_kv, max_seq, 128), 14), randn_bits((n_kv, max_seq, 128), 15)
+    freqs = D.llama3_rope_freqs(128, 500000.0)
+    scale = 1.0 / np.sqrt(128.0)
+    kcd, vcd = dev_bf16(kc), dev_bf16(vc)
+    out = E.rope_attention_decode(dev_bf16(q), dev_bf16(kn), dev_bf16(vn), kcd, vcd, torch.from_numpy(freqs).cuda(),
+                                  pos, n_heads, n_kv, scale)
+    qr = torch.from_numpy(D.rope(D.bits_to_f64(q).reshape(n_heads, 128), pos, freqs)).float()
+    K = torch.from_numpy(D.bits_to_f64(host_bits16(kcd))[:, : pos + 1]).float()
+    V = torch.from_numpy(D.bits_to_f64(host_bits16(vcd))[:, : pos + 1]).float()
+    K = K.repeat_interleave(n_heads // n_kv, dim=0)
+    V = V.repeat_interleave(n_heads // n_kv, dim=0)
+    ref = torch.softmax((K @ qr.unsqueeze(-1)).squeeze(-1) * scale, dim=-1).unsqueeze(1) @ V
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(out).reshape(n_heads, 128), ref.squeeze(1).double().numpy(),
+                                               out_is_bf16=True)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("n", [8, 14336, 65536 + 8])
+def test_silu_mul(cuda, n):
+    print(f"[case] silu_mul n={n}", flush=True)
+    g = randn_bits(n, n, std=3.0)
+    u = randn_bits(n, n + 1)
+    out = E.silu_mul(dev_bf16(g), dev_bf16(u))
+    torch.cuda.synchronize()
+    ref_bits = D.silu_mul_bf16(g, u)
+    got = host_bits16(out)
+    # the three roundings are the reference's; the sigmoid's f32 exp may differ
+    # from the oracle's f64 one in the last place before rounding
+    assert within_ulps(got, D.bits_to_f64(ref_bits), 1)
+    assert np.mean(got == ref_bits) > 0.99
+
+
+def test_embedding_and_argmax(cuda):
+    vocab, dim = 1000, 256
+    table = randn_bits((vocab, dim), 3)
+    ids = np.array([0, 999, 17, -1, 1000, 5], dtype=np.int32)
+    out = E.embedding(dev_bf16(table), torch.from_numpy(ids).cuda())
+    got = host_bits16(out)
+    for t, i in enumerate(ids):
+        expect = table[i] if 0 <= i < vocab else np.zeros(dim, dtype=np.uint16)
+        assert np.array_equal(got[t], expect)
+    logits = randn_bits((3, 128256), 4)
+    logits[1, 5] = bits([100.0])[0]
+    logits[1, 70000] = bits([100.0])[0]  # tie: the first index wins
+    logits[2, 128255] = bits([1000.0])[0]
+    idx = E.argmax(dev_bf16(logits)).cpu().numpy()
+    ref = np.argmax(D.bits_to_f64(logits), axis=1)
+    assert list(idx) == list(ref) and idx[1] == 5 and idx[2] == 128255
+
+
+def tiny_model(seed=0, layers=2, n_heads=4, n_kv=2, ffn=1024, vocab=1024, max_seq=64):
+    H = n_heads * 128
+    rng = np.random.default_rng(seed)
+    host = {"hidden": H, "n_heads": n_heads, "n_kv_heads": n_kv, "eps": 1e-5,
+            "freqs": D.llama3_rope_freqs(128, 500000.0)}
+
+    def lin(N, K, s):
+        w, sc, b = synthetic_linear(N, K, 64, 4, s)
+        return {"w": w, "s": sc, "b": b, "bits": 4, "gs": 64}
+
+    host["embed"] = bits(rng.standard_normal((vocab, H)))
+    host["final_norm"] = bits(1.0 + 0.1 * rng.standard_normal(H))
+    host["layers"] = []
+    for li in range(layers):
+        s0 = seed * 100 + li * 10
+        host["layers"].append({
+            "in_norm": bits(1.0 + 0.1 * rng.standard_normal(H)), "post_norm": bits(1.0 + 0.1 * rng.standard_normal(H)),
+            "q": lin(n_heads * 128, H, s0), "k": lin(n_kv * 128, H, s0 + 1), "v": lin(n_kv * 128, H, s0 + 2),
+            "o": lin(H, n_heads * 128, s0 + 3), "gate": lin(ffn, H, s0 + 4), "up": lin(ffn, H, s0 + 5),
+            "down": lin(H, ffn, s0 + 6)})
+    host["lm_head"] = lin(vocab, H, seed * 100 + 99)
+    kcs = [randn_bits((n_kv, max_seq, 128), seed + 500 + i) for i in range(layers)]
+    vcs = [randn_bits((n_kv, max_seq, 128), seed + 600 + i) for i in range(layers)]
+
+    def qlin(d):
+        return E.QLinear(dev_words(d["w"]), dev_bf16(d["s"]), dev_bf16(d["b"]), d["bits"], d["gs"])
+
+    dev_layers = [E.DecoderLayer(dev_bf16(L["in_norm"]), dev_bf16(L["post_norm"]), *(qlin(L[p]) for p in
+                                 ("q", "k", "v", "o", "gate", "up", "down"))) for L in host["layers"]]
+    dec = E.LlamaDecoder(dev_layers, dev_bf16(host["embed"]), dev_bf16(host["final_norm"]), qlin(host["lm_head"]),
+                         n_heads=n_heads, n_kv_heads=n_kv, eps=1e-5, freqs=host["freqs"], max_seq=max_seq,
+                         k_caches=[dev_bf16(k) for k in kcs], v_caches=[dev_bf16(v) for v in vcs])
+    return host, dec, kcs, vcs
+
+
+def test_decode_step_end_to_end(cuda):
+    host, dec, kcs, vcs = tiny_model()
+    kcs = [k.copy() for k in kcs]
+    vcs = [v.copy() for v in vcs]
+    token = 7
+    dec.token.fill_(token)
+    for pos in (10, 11, 12):
+        print(f"[case] decode step pos={pos} token={token}", flush=True)
+        dec.step(pos)
+        torch.cuda.synchronize()
+        logits_ref, _ = D.decode_step(host, token, pos, kcs, vcs)
+        got = host_f32(dec.logits)
+        rms = np.sqrt(np.mean(logits_ref ** 2))
+        err = np.abs(got - logits_ref)
+        assert np.all(err <= 2e-2 * rms + 0.5 * ulp_bf16(logits_ref)), f"max|err|/RMS = {err.max() / rms:.3e}"
+        nxt = int(dec.token.cpu().numpy()[0])
+        assert logits_ref[nxt] >= logits_ref.max() - 4e-2 * rms  # greedy pick agrees up to near-ties
+        # the oracle continues from the GPU's token so the two stay in step
+        token = nxt
+
+
+def test_decode_step_graph_replay(cuda):
+    """The step captured in a HIP graph and replayed matches the eager step."""
+    _, dec, _, _ = tiny_model(seed=3)
+    _, dec2, _, _ = tiny_model(seed=3)
+    for d in (dec, dec2):
+        d.token.fill_(5)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        dec.step(20)  # first call outside capture (workspace)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            dec.step(21)
+        torch.cuda.synchronize()
+    dec2.step(20)
+    toks, toks2 = [], []
+    for _ in range(3):
+        with torch.cuda.stream(st):
+            g.replay()
+        torch.cuda.synchronize()
+        dec2.step(21)
+        torch.cuda.synchronize()
+        toks.append(int(dec.token.item()))
+        toks2.append(int(dec2.token.item()))
+        assert torch.equal(dec.logits, dec2.logits)
+    assert toks == toks2
