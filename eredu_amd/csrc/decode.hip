@@ -31,72 +31,109 @@ namespace {
 constexpr int kHeadDim = 128;  // head width of the attention fast path
 constexpr int kAttnChunk = 32; // cache positions per attention workgroup
 constexpr int kRowPad = kHeadDim + 8;  // LDS row of keys/values: 272 B, so 32 rows spread over 16 banks
+constexpr int kMaxChunks = 4096;       // positions up to kMaxChunks * kAttnChunk = 131072
 
 __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
 
-// Sum over a block of 1024 threads (16 waves); every thread gets the total.
-__device__ __forceinline__ float block_sum_1024(float v, float* red) {
+// Sum over the block (blockDim.x a multiple of 64, at most 1024); every
+// thread gets the same total (the waves' sums added in wave order).
+__device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     if (lane == 0) red[wave] = v;
     __syncthreads();
     float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) t += red[i];  // same order in every thread
-    __syncthreads();
+    for (int i = 0; i < nw; i++) t += red[i];
     return t;
 }
 
-// One row per workgroup of 1024 threads; dim % 8 == 0 (16-byte vectors).
+// bf16 pair sums a + b, each rounded to bf16 (the residual add).
+__device__ __forceinline__ uint4 add_bf16x8(uint4 a, const uint4 b) {
+    uint32_t* pa = reinterpret_cast<uint32_t*>(&a);
+    const uint32_t* pb = reinterpret_cast<const uint32_t*>(&b);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float lo = bf16_bits_to_f32(pa[i] & 0xffffu) + bf16_bits_to_f32(pb[i] & 0xffffu);
+        const float hi = bf16_bits_to_f32(pa[i] >> 16) + bf16_bits_to_f32(pb[i] >> 16);
+        pa[i] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    }
+    return a;
+}
+
+__device__ __forceinline__ float sumsq_bf16x8(const uint4 a) {
+    const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float lo = bf16_bits_to_f32(pa[i] & 0xffffu), hi = bf16_bits_to_f32(pa[i] >> 16);
+        ss = fmaf(lo, lo, ss);
+        ss = fmaf(hi, hi, ss);
+    }
+    return ss;
+}
+
+__device__ __forceinline__ uint4 norm_bf16x8(const uint4 a, const uint4 w, float inv) {
+    const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a);
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(&w);
+    uint4 o;
+    uint32_t* po = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float lo = bf16_bits_to_f32(pw[i] & 0xffffu) * (bf16_bits_to_f32(pa[i] & 0xffffu) * inv);
+        const float hi = bf16_bits_to_f32(pw[i] >> 16) * (bf16_bits_to_f32(pa[i] >> 16) * inv);
+        po[i] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    }
+    return o;
+}
+
+// One row per workgroup; dim % 8 == 0 (16-byte vectors).  VPT > 0: every
+// thread keeps its (at most VPT) vectors in registers between the two passes;
+// VPT == 0: any dim, the row is read again in the second pass.
+template <int VPT>
 __global__ __launch_bounds__(1024) void rms_norm_kernel(uint16_t* __restrict__ out, uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ residual,
                                                         const uint16_t* __restrict__ weight, int dim, float eps) {
     __shared__ float red[16];
     const int64_t row = blockIdx.x;
-    uint16_t* xr = x + row * dim;
-    const uint16_t* rr = residual ? residual + row * dim : nullptr;
-    uint16_t* orow = out + row * dim;
-    const int nvec = dim / 8;
+    uint4* xr = reinterpret_cast<uint4*>(x + row * dim);
+    const uint4* rr = residual ? reinterpret_cast<const uint4*>(residual + row * dim) : nullptr;
+    uint4* orow = reinterpret_cast<uint4*>(out + row * dim);
+    const uint4* wr = reinterpret_cast<const uint4*>(weight);
+    const int nvec = dim / 8, step = blockDim.x;
     float ss = 0.f;
-    for (int v = threadIdx.x; v < nvec; v += 1024) {
-        uint4 a = reinterpret_cast<const uint4*>(xr)[v];
-        if (rr) {
-            const uint4 b = reinterpret_cast<const uint4*>(rr)[v];
-            uint32_t* pa = reinterpret_cast<uint32_t*>(&a);
-            const uint32_t* pb = reinterpret_cast<const uint32_t*>(&b);
+    if constexpr (VPT > 0) {
+        uint4 a[VPT], w[VPT];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float lo = bf16_bits_to_f32(pa[i] & 0xffffu) + bf16_bits_to_f32(pb[i] & 0xffffu);
-                const float hi = bf16_bits_to_f32(pa[i] >> 16) + bf16_bits_to_f32(pb[i] >> 16);
-                pa[i] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+        for (int j = 0; j < VPT; j++) {
+            const int v = threadIdx.x + j * step;
+            if (v < nvec) {
+                a[j] = xr[v];
+                w[j] = wr[v];
+                if (rr) {
+                    a[j] = add_bf16x8(a[j], rr[v]);
+                    xr[v] = a[j];
+                }
+                ss += sumsq_bf16x8(a[j]);
             }
-            reinterpret_cast<uint4*>(xr)[v] = a;
         }
-        const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a);
+        const float inv = 1.0f / sqrtf(block_sum(ss, red) / float(dim) + eps);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float lo = bf16_bits_to_f32(pa[i] & 0xffffu), hi = bf16_bits_to_f32(pa[i] >> 16);
-            ss = fmaf(lo, lo, ss);
-            ss = fmaf(hi, hi, ss);
+        for (int j = 0; j < VPT; j++) {
+            const int v = threadIdx.x + j * step;
+            if (v < nvec) orow[v] = norm_bf16x8(a[j], w[j], inv);
         }
-    }
-    const float total = block_sum_1024(ss, red);
-    const float inv = 1.0f / sqrtf(total / float(dim) + eps);
-    for (int v = threadIdx.x; v < nvec; v += 1024) {
-        const uint4 a = reinterpret_cast<const uint4*>(xr)[v];  // this thread's own (updated) values
-        const uint4 w = reinterpret_cast<const uint4*>(weight)[v];
-        const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a);
-        const uint32_t* pw = reinterpret_cast<const uint32_t*>(&w);
-        uint4 o;
-        uint32_t* po = reinterpret_cast<uint32_t*>(&o);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float lo = bf16_bits_to_f32(pw[i] & 0xffffu) * (bf16_bits_to_f32(pa[i] & 0xffffu) * inv);
-            const float hi = bf16_bits_to_f32(pw[i] >> 16) * (bf16_bits_to_f32(pa[i] >> 16) * inv);
-            po[i] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    } else {
+        for (int v = threadIdx.x; v < nvec; v += step) {
+            uint4 a = xr[v];
+            if (rr) {
+                a = add_bf16x8(a, rr[v]);
+                xr[v] = a;
+            }
+            ss += sumsq_bf16x8(a);
         }
-        reinterpret_cast<uint4*>(orow)[v] = o;
+        const float inv = 1.0f / sqrtf(block_sum(ss, red) / float(dim) + eps);
+        for (int v = threadIdx.x; v < nvec; v += step) orow[v] = norm_bf16x8(xr[v], wr[v], inv);  // own values
     }
 }
 
@@ -135,34 +172,36 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(float* __restrict__ w
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float fpos = float(pos);
 
-    // queries of the group, rotated
+    // queries of the group, the new key (if this chunk holds pos) and the
+    // chunk's cached keys and values, all requested before any waits
     for (int i = tid; i < group * kHeadDim; i += 256)
         qs[i / kHeadDim][i % kHeadDim] = bf16_bits_to_f32(q[(int64_t(g) * group + i / kHeadDim) * kHeadDim + i % kHeadDim]);
     const bool has_new = pos >= p0 && pos < p0 + kAttnChunk;
     if (has_new && tid < kHeadDim) knew[tid] = bf16_bits_to_f32(k_new[int64_t(g) * kHeadDim + tid]);
-    __syncthreads();
-    for (int i = tid; i < group * (kHeadDim / 2); i += 256) rope_pair(qs[i / (kHeadDim / 2)], freqs, fpos, i % (kHeadDim / 2));
-    if (has_new && tid < kHeadDim / 2) rope_pair(knew, freqs, fpos, tid);
-    __syncthreads();
-
-    // keys and values of the chunk (16-byte pieces); position pos from the new ones
     uint16_t* kc = k_cache + int64_t(g) * max_seq * kHeadDim;
     uint16_t* vc = v_cache + int64_t(g) * max_seq * kHeadDim;
     for (int i = tid; i < np * (kHeadDim / 8); i += 256) {
         const int p = i / (kHeadDim / 8), v = i % (kHeadDim / 8);
-        uint4 kk, vv;
-        if (p0 + p == pos) {
-            uint32_t* pk = reinterpret_cast<uint32_t*>(&kk);
+        if (p0 + p == pos) continue;
+        reinterpret_cast<uint4*>(&ks[p][0])[v] = reinterpret_cast<const uint4*>(kc + int64_t(p0 + p) * kHeadDim)[v];
+        reinterpret_cast<uint4*>(&vs[p][0])[v] = reinterpret_cast<const uint4*>(vc + int64_t(p0 + p) * kHeadDim)[v];
+    }
+    __syncthreads();
+    for (int i = tid; i < group * (kHeadDim / 2); i += 256) rope_pair(qs[i / (kHeadDim / 2)], freqs, fpos, i % (kHeadDim / 2));
+    if (has_new && tid < kHeadDim / 2) rope_pair(knew, freqs, fpos, tid);
+    __syncthreads();
+    // position pos: the rotated new key (rounded to bf16) and the new value,
+    // into LDS and into the cache
+    if (has_new && tid < kHeadDim / 8) {
+        const int p = pos - p0, v = tid;
+        uint4 kk;
+        uint32_t* pk = reinterpret_cast<uint32_t*>(&kk);
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                pk[e] = f32_to_bf16_bits(knew[8 * v + 2 * e]) | (f32_to_bf16_bits(knew[8 * v + 2 * e + 1]) << 16);
-            vv = reinterpret_cast<const uint4*>(v_new + int64_t(g) * kHeadDim)[v];
-            reinterpret_cast<uint4*>(kc + int64_t(pos) * kHeadDim)[v] = kk;
-            reinterpret_cast<uint4*>(vc + int64_t(pos) * kHeadDim)[v] = vv;
-        } else {
-            kk = reinterpret_cast<const uint4*>(kc + int64_t(p0 + p) * kHeadDim)[v];
-            vv = reinterpret_cast<const uint4*>(vc + int64_t(p0 + p) * kHeadDim)[v];
-        }
+        for (int e = 0; e < 4; e++)
+            pk[e] = f32_to_bf16_bits(knew[8 * v + 2 * e]) | (f32_to_bf16_bits(knew[8 * v + 2 * e + 1]) << 16);
+        const uint4 vv = reinterpret_cast<const uint4*>(v_new + int64_t(g) * kHeadDim)[v];
+        reinterpret_cast<uint4*>(kc + int64_t(pos) * kHeadDim)[v] = kk;
+        reinterpret_cast<uint4*>(vc + int64_t(pos) * kHeadDim)[v] = vv;
         reinterpret_cast<uint4*>(&ks[p][0])[v] = kk;
         reinterpret_cast<uint4*>(&vs[p][0])[v] = vv;
     }
@@ -210,22 +249,44 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(float* __restrict__ w
     }
 }
 
-// One workgroup of 128 threads per query head: the chunks' partial states
-// merged in chunk order, divided by the total weight, rounded to bf16.
-__global__ __launch_bounds__(128) void attn_combine_kernel(uint16_t* __restrict__ out, const float* __restrict__ ws,
+// One workgroup of 256 threads per query head: the chunks' partial states
+// (max, weight sum, weighted values) merged -- their maxima and rescale
+// factors computed in parallel into LDS, then two halves of the threads sum
+// alternate chunks for each dimension with independent loads -- divided by
+// the total weight, rounded to bf16.
+__global__ __launch_bounds__(256) void attn_combine_kernel(uint16_t* __restrict__ out, const float* __restrict__ ws,
                                                            int nchunks) {
-    const int h = blockIdx.x, d = threadIdx.x;
+    __shared__ float fac[kMaxChunks];
+    __shared__ float red[4];
+    __shared__ float part[128];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* base = ws + int64_t(h) * nchunks * (kHeadDim + 2);
-    float mx = -INFINITY;
-    for (int c = 0; c < nchunks; c++) mx = fmaxf(mx, base[c * (kHeadDim + 2)]);
-    float l = 0.f, o = 0.f;
-    for (int c = 0; c < nchunks; c++) {
-        const float* p = base + c * (kHeadDim + 2);
-        const float f = expf(p[0] - mx);
-        l = fmaf(f, p[1], l);
-        o = fmaf(f, p[2 + d], o);
+    float m = -INFINITY;
+    for (int c = tid; c < nchunks; c += 256) m = fmaxf(m, base[c * (kHeadDim + 2)]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float l = 0.f;
+    for (int c = tid; c < nchunks; c += 256) {
+        const float f = expf(base[c * (kHeadDim + 2)] - mx);
+        fac[c] = f;
+        l = fmaf(f, base[c * (kHeadDim + 2) + 1], l);
     }
-    out[int64_t(h) * kHeadDim + d] = uint16_t(f32_to_bf16_bits(o / l));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+    if (lane == 0) red[wave] = l;
+    __syncthreads();
+    const float lsum = (red[0] + red[1]) + (red[2] + red[3]);
+    const int d = tid & (kHeadDim - 1), half = tid >> 7;
+    float o = 0.f;
+#pragma unroll 8
+    for (int c = half; c < nchunks; c += 2) o = fmaf(fac[c], base[c * (kHeadDim + 2) + 2 + d], o);
+    if (half == 1) part[d] = o;
+    __syncthreads();
+    if (half == 0) out[int64_t(h) * kHeadDim + d] = uint16_t(f32_to_bf16_bits((o + part[d]) / lsum));
 }
 
 // silu(gate) * up with the reference's roundings: sigmoid, the product with
@@ -270,29 +331,56 @@ __global__ __launch_bounds__(256) void embedding_kernel(uint16_t* __restrict__ o
     }
 }
 
-// First index of the largest value of each row (1024 threads per row).
+// First index of the largest value of each row (1024 threads per row):
+// each thread scans 16-byte pieces (8 values) of the row in index order,
+// four pieces in flight, then (value, index) pairs merge with ties to the
+// lower index.
+__device__ __forceinline__ void argmax_take(float v, int64_t i, float& best, int64_t& idx) {
+    if (v > best || (v == best && i < idx)) {
+        best = v;
+        idx = i;
+    }
+}
 __global__ __launch_bounds__(1024) void argmax_kernel(int32_t* __restrict__ out, const uint16_t* __restrict__ logits,
-                                                      int64_t n) {
+                                                      int64_t n, bool vec) {
     __shared__ float bv[16];
     __shared__ int64_t bi[16];
     const uint16_t* row = logits + int64_t(blockIdx.x) * n;
     float best = -INFINITY;
-    int64_t idx = n;  // none yet
-    for (int64_t i = threadIdx.x; i < n; i += 1024) {
-        const float v = bf16_bits_to_f32(row[i]);
-        if (v > best || idx == n) {
-            best = v;
-            idx = i;
+    int64_t idx = INT64_MAX;
+    int64_t tail = 0;
+    if (vec) {
+        const int64_t nv = n / 8;
+        const uint4* rv = reinterpret_cast<const uint4*>(row);
+        int64_t v = threadIdx.x;
+        for (; v + 3 * 1024 < nv; v += 4 * 1024) {
+            uint4 a[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) a[u] = rv[v + u * 1024];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a[u]);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    argmax_take(bf16_bits_to_f32((pa[e >> 1] >> (16 * (e & 1))) & 0xffffu), (v + u * 1024) * 8 + e,
+                                best, idx);
+            }
         }
+        for (; v < nv; v += 1024) {
+            const uint4 a = rv[v];
+            const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                argmax_take(bf16_bits_to_f32((pa[e >> 1] >> (16 * (e & 1))) & 0xffffu), v * 8 + e, best, idx);
+        }
+        tail = nv * 8;
     }
+    for (int64_t i = tail + threadIdx.x; i < n; i += 1024) argmax_take(bf16_bits_to_f32(row[i]), i, best, idx);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o);
         const int64_t oi = __shfl_xor(idx, o);
-        if (ov > best || (ov == best && oi < idx)) {
-            best = ov;
-            idx = oi;
-        }
+        argmax_take(ov, oi, best, idx);
     }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (lane == 0) {
@@ -303,11 +391,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int32_t* __restrict__ out,
     if (threadIdx.x == 0) {
         float b = bv[0];
         int64_t k = bi[0];
-        for (int w = 1; w < 16; w++)
-            if (bv[w] > b || (bv[w] == b && bi[w] < k)) {
-                b = bv[w];
-                k = bi[w];
-            }
+        for (int w = 1; w < 16; w++) argmax_take(bv[w], bi[w], b, k);
         out[blockIdx.x] = int32_t(k < n ? k : 0);
     }
 }
@@ -373,9 +457,18 @@ extern "C" int eq_rms_norm(void* out, void* x, const void* residual, const void*
     }
     if (rows == 0) return 0;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    rms_norm_kernel<<<dim3(unsigned(rows)), dim3(1024), 0, st>>>(
-        static_cast<uint16_t*>(out), static_cast<uint16_t*>(x), static_cast<const uint16_t*>(residual),
-        static_cast<const uint16_t*>(weight), int(dim), eps);
+    const int nvec = int(dim / 8);
+    const int block = nvec >= 1024 ? 1024 : (nvec + 63) / 64 * 64;
+    const int vpt = (nvec + block - 1) / block;
+    auto go = [&](auto kern) {
+        kern<<<dim3(unsigned(rows)), dim3(unsigned(block)), 0, st>>>(
+            static_cast<uint16_t*>(out), static_cast<uint16_t*>(x), static_cast<const uint16_t*>(residual),
+            static_cast<const uint16_t*>(weight), int(dim), eps);
+    };
+    if (vpt == 1) go(rms_norm_kernel<1>);
+    else if (vpt == 2) go(rms_norm_kernel<2>);
+    else if (vpt <= 4) go(rms_norm_kernel<4>);
+    else go(rms_norm_kernel<0>);
     return check_launch("eq_rms_norm");
 }
 
@@ -398,8 +491,8 @@ extern "C" int eq_rope_attention_decode(void* out, const void* q, const void* k_
         set_error("eq_rope_attention_decode: n_heads must be 1-4 times n_kv_heads");
         return 1;
     }
-    if (pos < 0 || max_seq <= 0 || pos >= max_seq || max_seq > (int64_t(1) << 24)) {
-        set_error("eq_rope_attention_decode: need 0 <= pos < max_seq <= 2^24");
+    if (pos < 0 || max_seq <= 0 || pos >= max_seq || pos >= int64_t(kMaxChunks) * kAttnChunk) {
+        set_error("eq_rope_attention_decode: need 0 <= pos < max_seq and pos < 131072");
         return 1;
     }
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(v_new, 16)) {
@@ -418,7 +511,7 @@ extern "C" int eq_rope_attention_decode(void* out, const void* q, const void* k_
         ws, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
         static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, int(pos), int(max_seq), n_heads,
         n_kv_heads, nchunks, scale);
-    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(kHeadDim), 0, st>>>(static_cast<uint16_t*>(out), ws, nchunks);
+    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, nchunks);
     return check_launch("eq_rope_attention_decode");
 }
 
@@ -478,6 +571,6 @@ extern "C" int eq_argmax(int32_t* out, const void* logits, int64_t rows, int64_t
     }
     if (rows == 0) return 0;
     argmax_kernel<<<dim3(unsigned(rows)), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        out, static_cast<const uint16_t*>(logits), n);
+        out, static_cast<const uint16_t*>(logits), n, n % 8 == 0 && aligned(logits, 16));
     return check_launch("eq_argmax");
 }

@@ -43,7 +43,7 @@ def within_ulps(got_bits, ref_f64, n=1):
     return np.all(np.abs(got - ref_f64) <= n * ulp_bf16(ref_f64) + 1e-30)
 
 
-@pytest.mark.parametrize("dim", [64, 512, 4096, 14336])
+@pytest.mark.parametrize("dim", [64, 512, 4096, 14336, 40000])
 @pytest.mark.parametrize("with_residual", [False, True])
 def test_rms_norm(cuda, dim, with_residual):
     print(f"[case] rms_norm dim={dim} residual={with_residual}", flush=True)
