@@ -240,7 +240,7 @@ def bench_gguf(steps, warmup):
 VOCAB, N_HEADS, N_KV_HEADS, CACHE_TOKENS = 128256, 32, 8, 1024
 
 
-def build_decoder(layers, gen):
+def build_decoder(layers, gen, fused=None):
     """the Llama-3-8B-shaped stack around the 32 layers' packed
     projections -- bf16 embeddings and norms, a 4-bit LM head, a bf16 KV cache
     of CACHE_TOKENS random N(0, 1) rows per layer, Llama-3 RoPE (theta 5e5,
@@ -265,24 +265,35 @@ def build_decoder(layers, gen):
               for _ in range(2)]
     freqs = E.llama3_rope_freqs(128, 500000.0, 8.0, 1.0, 4.0, 8192)
     return E.LlamaDecoder(dec_layers, embed, norm(), q(lm), n_heads=N_HEADS, n_kv_heads=N_KV_HEADS, eps=1e-5,
-                          freqs=freqs, max_seq=max_seq, k_caches=caches[0], v_caches=caches[1])
+                          freqs=freqs, max_seq=max_seq, k_caches=caches[0], v_caches=caches[1], fused=fused)
 
 
 def bench_decode_step(layers, steps, warmup, gen):
     """Full batch-1 decode step as one HIP graph: tok/s, and the
     step's algorithmic bytes against 8 TB/s."""
+    from eredu_amd import decode as E
+
     dec = build_decoder(layers, gen)
+    # the same model with the norms and SiLU-mul as launches of their own
+    other = E.LlamaDecoder(dec.layers, dec.embed, dec.final_norm, dec.lm_head, n_heads=N_HEADS, n_kv_heads=N_KV_HEADS,
+                           eps=1e-5, freqs=dec.freqs.cpu().numpy(), max_seq=dec.max_seq, k_caches=dec.k_caches,
+                           v_caches=dec.v_caches, fused=not dec.fused)
     pos = CACHE_TOKENS
-    ms = Timer(lambda st: dec.step(pos)).ms_per_replay(steps, warmup)
+    ms_a = Timer(lambda st: dec.step(pos)).ms_per_replay(steps, warmup)
+    ms_b = Timer(lambda st: other.step(pos)).ms_per_replay(steps, warmup)
+    if ms_b < ms_a:
+        dec, other, ms_a, ms_b = other, dec, ms_b, ms_a
+    ms = ms_a
     nbytes = dec.bytes_per_step(pos)
     gbs = nbytes / (ms * 1e-3) / 1e9
     roof = HBM_PEAK_GBS * 1e9 / nbytes
     out = {"ms": round(ms, 4), "tok/s": round(1e3 / ms, 1), "bytes_per_token": nbytes, "GB/s": round(gbs, 1),
            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "roofline_tok/s": round(roof, 1),
-           "launches": dec.launches_per_step(),
+           "launches": dec.launches_per_step(), "fused_prologues": dec.fused,
+           "other_variant_ms": round(ms_b, 4), "other_variant_launches": other.launches_per_step(),
            "workload": "batch 1, 32 layers, H 4096, 32 q / 8 kv heads x 128, FFN 14336, vocab 128256, 4-bit g64 "
                        "linears incl. LM head, bf16 embeddings/norms, 1024-token bf16 KV cache, greedy argmax"}
-    del dec
+    del dec, other
     return out
 
 

@@ -43,6 +43,19 @@ class QmmProblem(ctypes.Structure):
 SIGNATURES["eq_quantized_matmul_batched"] = (
     [ctypes.POINTER(QmmProblem), _i32, _i64, _b, _i32, _i32, ctypes.c_char_p, _i32, _i32, _vp], _i32)
 
+EQ_PROLOGUE_SILU_MUL, EQ_PROLOGUE_RMS_NORM = 1, 2
+
+
+class ActivationPrologue(ctypes.Structure):
+    """eq_activation_prologue of include/eredu_hip.h."""
+
+    _fields_ = [("kind", _i32), ("second", _vp), ("weight", _vp), ("hidden_out", _vp), ("eps", ctypes.c_float)]
+
+
+SIGNATURES["eq_quantized_matmul_batched_prologue"] = (
+    [ctypes.POINTER(QmmProblem), _i32, _i64, _b, _i32, _i32, ctypes.c_char_p, _i32, _i32,
+     ctypes.POINTER(ActivationPrologue), _vp], _i32)
+
 _lib = None
 _lock = threading.Lock()
 

@@ -332,6 +332,98 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
     return 0;
 }
 
+static bool ranges_overlap(const void* a, const void* b, int64_t bytes) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + uintptr_t(bytes) && y < x + uintptr_t(bytes);
+}
+
+extern "C" int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* problems, int count, int64_t M,
+                                                    bool transpose, int group_size, int bits, const char* mode,
+                                                    int x_dtype, int scale_dtype,
+                                                    const eq_activation_prologue* prologue, eq_stream_t stream) {
+    clear_error();
+    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    if (!prologue || (prologue->kind != EQ_PROLOGUE_SILU_MUL && prologue->kind != EQ_PROLOGUE_RMS_NORM)) {
+        set_error("prologue: kind must be EQ_PROLOGUE_SILU_MUL or EQ_PROLOGUE_RMS_NORM");
+        return 1;
+    }
+    const eq_activation_prologue& pr = *prologue;
+    if (count < 1 || count > 8 || !problems) {
+        set_error("prologue: 1 to 8 problems");
+        return 1;
+    }
+    if (M != 1 || !transpose || x_dtype != EQ_DTYPE_BF16 || scale_dtype != EQ_DTYPE_BF16 || group_size != 64 ||
+        (bits != 4 && bits != 8)) {
+        set_error("prologue: supported for M = 1, transpose = true, bf16 activations and scales, group size 64, "
+                  "4- or 8-bit codes");
+        return 1;
+    }
+    const void* x = problems[0].x;
+    const int64_t K = problems[0].K;
+    std::vector<QmvSpec> specs;
+    for (int i = 0; i < count; i++) {
+        const eq_qmm_problem& p = problems[i];
+        if (!p.y || !p.x || !p.w || !p.scales) {
+            set_error("problem " + std::to_string(i) + ": null pointer argument");
+            return 1;
+        }
+        if (p.x != x || p.K != K) {
+            set_error("prologue: all problems must share one input x");
+            return 1;
+        }
+        if (p.N <= 0 || p.N > INT32_MAX || p.N % 16 != 0 || !aligned(p.w, 16)) {
+            set_error("problem " + std::to_string(i) + ": N must be a positive multiple of 16, w 16-byte aligned");
+            return 1;
+        }
+        specs.push_back(QmvSpec{static_cast<const uint16_t*>(p.x), p.w, p.scales, p.biases, static_cast<uint16_t*>(p.y),
+                                int(p.N), int(p.K), int(p.N)});
+    }
+    if (K <= 0 || K % 64 != 0 || K > INT32_MAX || !aligned(x, 16)) {
+        set_error("prologue: K must be a positive multiple of 64 and x 16-byte aligned");
+        return 1;
+    }
+    const int64_t bytes = K * 2;
+    if (pr.kind == EQ_PROLOGUE_SILU_MUL) {
+        if (!pr.second || !aligned(pr.second, 16)) {
+            set_error("prologue: silu_mul needs a 16-byte aligned second input");
+            return 1;
+        }
+    } else {
+        if (K > 4096) {
+            set_error("prologue: rms_norm takes rows of at most 4096 values");
+            return 1;
+        }
+        if (!pr.weight || !aligned(pr.weight, 16) || (pr.second && !aligned(pr.second, 16)) ||
+            (pr.hidden_out && !aligned(pr.hidden_out, 16))) {
+            set_error("prologue: rms_norm needs a weight and 16-byte aligned vectors");
+            return 1;
+        }
+        if (!(pr.eps >= 0.f)) {
+            set_error("prologue: eps must be >= 0");
+            return 1;
+        }
+        if (pr.hidden_out && (ranges_overlap(pr.hidden_out, x, bytes) ||
+                              (pr.second && ranges_overlap(pr.hidden_out, pr.second, bytes)))) {
+            set_error("prologue: hidden_out must not overlap x or the residual (every workgroup reads them)");
+            return 1;
+        }
+    }
+    for (int i = 0; i < count; i++)
+        if (ranges_overlap(problems[i].y, x, bytes) ||
+            (pr.second && ranges_overlap(problems[i].y, pr.second, bytes))) {
+            set_error("prologue: outputs must not overlap the inputs");
+            return 1;
+        }
+    QmvPrologue q{pr.kind, static_cast<const uint16_t*>(pr.second), static_cast<const uint16_t*>(pr.weight),
+                  static_cast<uint16_t*>(pr.hidden_out), pr.eps};
+    if (!launch_qmv_prologue(bits, group_size, scale_dtype, specs.data(), count, q,
+                             reinterpret_cast<hipStream_t>(stream))) {
+        set_error("prologue: these problems do not fit one decode launch (at most 8, shared LDS budget)");
+        return 1;
+    }
+    return check_launch("quantized_matmul_batched_prologue");
+}
+
 extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases, int64_t rows,
                              int64_t cols, int group_size, int bits, const char* mode, int scale_dtype,
                              int out_dtype, eq_stream_t stream) {

@@ -308,9 +308,9 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t* __restrict__ ou
         for (int hh = 0; hh < 2; hh++) {
             const float x = bf16_bits_to_f32((pg[i] >> (16 * hh)) & 0xffffu);
             const float u = bf16_bits_to_f32((pu[i] >> (16 * hh)) & 0xffffu);
-            const float sg = bf16_round(1.0f / (1.0f + expf(-x)));
-            const float sl = bf16_round(x * sg);
-            r |= f32_to_bf16_bits(sl * u) << (16 * hh);
+            const float sg = silu_sigmoid_bf16(x);
+            const float sl = float(static_cast<__bf16>(x * sg));
+            r |= uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(sl * u))) << (16 * hh);
         }
         po[i] = r;
     }

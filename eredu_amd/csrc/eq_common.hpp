@@ -41,6 +41,20 @@ bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint1
                      const void* s, const void* b, int M, int N, int K, hipStream_t st);
 bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st);
 
+// Activation prologue of a decode launch: kind 1 = silu(x) * second,
+// kind 2 = RMSNorm(x + second) * weight (second may be null), x + second
+// written to hidden_out (may be null).  launch_qmv_prologue takes M = 1
+// problems sharing one input; false, launching nothing, when it cannot.
+struct QmvPrologue {
+    int kind;
+    const uint16_t* second;
+    const uint16_t* weight;
+    uint16_t* hidden_out;
+    float eps;
+};
+bool launch_qmv_prologue(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, const QmvPrologue& pro,
+                         hipStream_t st);
+
 // ---------------------------------------------------------------- device side
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -95,6 +109,15 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu)) return (x >> 16) | 0x40u;
     x += 0x7fffu + ((x >> 16) & 1u);
     return x >> 16;
+}
+
+// sigmoid(x) = 1 / (1 + e^-x) rounded to bf16 (the decoder's SiLU rounds it):
+// e^-x as 2^(-x log2 e) with v_exp_f32 and the reciprocal with v_rcp_f32 --
+// each within ~1 f32 ulp, far below the bf16 rounding that follows; the
+// rounding to bf16 is the hardware RNE conversion.
+__device__ __forceinline__ float silu_sigmoid_bf16(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * 1.44269504088896341f);
+    return float(static_cast<__bf16>(__builtin_amdgcn_rcpf(1.0f + e)));
 }
 
 // f32 -> IEEE binary16 bits with round-to-nearest-even, overflow to infinity

@@ -489,6 +489,13 @@ struct QmvBatch {
     int stage[kQmvMaxProblems];  // problem whose x each staged matrix is
     int zero_lds, zero_bytes;
     int red_lds;             // 2 x waves x M x 16 floats
+    // Activation prologue (M = 1, one staged input): 1 = silu(x) * pro_second,
+    // 2 = RMSNorm(x + pro_second) * pro_weight, the sum also written to
+    // pro_hidden_out by workgroup 0.  Applied while staging.
+    const uint16_t* pro_second;
+    const uint16_t* pro_weight;
+    uint16_t* pro_hidden_out;
+    float pro_eps;
 };
 
 // Registers of one block of NU spans of the LDS variant: codes and scale words.
@@ -732,7 +739,68 @@ __device__ __forceinline__ void qmv_stream_next(const QmvBatch& batch, QmvStream
     qmv_stream_seek<BITS, GS, TAIL>(batch, st, st.tile + gridDim.x, wave, ln, kq, r_p);
 }
 
-template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL>
+// silu(g) * u on 8 bf16 values with the decoder's roundings: sigmoid, the
+// product with g and the product with u each rounded to bf16
+// (eredu/src/backend/mlx/nn/layers.rs:21; Mlp::hidden,
+// eredu-architectures/src/llama.rs:414-422).
+__device__ __forceinline__ u32x4 qmv_silu_mul8(const u32x4 g, const u32x4 u) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t o = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float x = bf16_bits_to_f32((g[i] >> (16 * h)) & 0xffffu);
+            const float up = bf16_bits_to_f32((u[i] >> (16 * h)) & 0xffffu);
+            const float sg = silu_sigmoid_bf16(x);
+            const float sl = float(static_cast<__bf16>(x * sg));
+            o |= uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(sl * up))) << (16 * h);
+        }
+        r[i] = o;
+    }
+    return r;
+}
+
+// a + b on 8 bf16 values, each sum rounded to bf16 (the residual add).
+__device__ __forceinline__ u32x4 qmv_add8(const u32x4 a, const u32x4 b) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float lo = bf16_bits_to_f32(a[i] & 0xffffu) + bf16_bits_to_f32(b[i] & 0xffffu);
+        const float hi = bf16_bits_to_f32(a[i] >> 16) + bf16_bits_to_f32(b[i] >> 16);
+        r[i] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    }
+    return r;
+}
+
+__device__ __forceinline__ float qmv_sumsq8(const u32x4 a) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float lo = bf16_bits_to_f32(a[i] & 0xffffu), hi = bf16_bits_to_f32(a[i] >> 16);
+        ss = fmaf(lo, lo, ss);
+        ss = fmaf(hi, hi, ss);
+    }
+    return ss;
+}
+
+// w * (a * inv) on 8 bf16 values, rounded to bf16 (RMSNorm's scaling).
+__device__ __forceinline__ u32x4 qmv_norm8(const u32x4 a, const u32x4 w, float inv) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float lo = bf16_bits_to_f32(w[i] & 0xffffu) * (bf16_bits_to_f32(a[i] & 0xffffu) * inv);
+        const float hi = bf16_bits_to_f32(w[i] >> 16) * (bf16_bits_to_f32(a[i] >> 16) * inv);
+        r[i] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    }
+    return r;
+}
+
+// PRO: activation prologue (QmvBatch::pro_*), 0 none, 1 silu-mul, 2 RMSNorm.
+// With PRO = 2 the staged row (K <= 2 * 16 * 64 * NW values) is one round of
+// at most 2 chunks per thread, kept in registers across the workgroup's sum
+// of squares.
+template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL, int PRO = 0>
 __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
     const QmvBatch batch) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -761,15 +829,24 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // each 8-element chunk is stored as [x0, x2, x4, x6, x1, x3, x5, x7], the
     // order in which unpack4_bf16_offset128_perm delivers the codes.
     const int zero_lds = __builtin_amdgcn_readfirstlane(batch.zero_lds);
+    static_assert(PRO == 0 || MREG == 1, "activation prologues are for one activation row");
+    constexpr int NCH = PRO == 2 ? 2 : 8;  // chunks per thread and staging round
+    u32x4 x2v[PRO != 0 ? NCH : 1];         // second input (up, residual); with PRO = 2 also the norm weight
+    u32x4 nwv[PRO == 2 ? NCH : 1];
     auto stage_load = [&](int r, int c0, u32x4* v, int* dst) __attribute__((always_inline)) {
         const QmvProblem& pr = batch.p[batch.stage[r]];
         const __amdgpu_buffer_rsrc_t xr = raw_rsrc(pr.x, uint32_t(M) * uint32_t(pr.K) * 2u);
+        // (the prologue's inputs: with PRO = 2 a missing residual reads zero)
+        const __amdgpu_buffer_rsrc_t x2r =
+            raw_rsrc(PRO != 0 && batch.pro_second ? batch.pro_second : pr.x,
+                     PRO != 0 && batch.pro_second ? uint32_t(pr.K) * 2u : 0u);
+        const __amdgpu_buffer_rsrc_t nwr = raw_rsrc(PRO == 2 ? batch.pro_weight : pr.x, PRO == 2 ? uint32_t(pr.K) * 2u : 0u);
         const int K = pr.K, kpad = pr.kpad, x_lds = pr.x_lds;
         const float inv_cpr = pr.inv_cpr;
         const int cpr = kpad / 8;  // 16-byte chunks per LDS row
         const int total = M * cpr;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < NCH; i++) {
             const int c = c0 + i * 64 * NW;
             // c / cpr exactly: c < 2^15 (the staged rows fit in LDS), so the
             // product's error (below 2^-19) is far from the distance, at least
@@ -778,13 +855,43 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             const bool live = c < total;
             const uint32_t off = (live & (cc * 8 < K)) ? (uint32_t(m) * uint32_t(K) + uint32_t(cc) * 8u) * 2u : kOutOfRange;
             v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+            if constexpr (PRO != 0) x2v[i] = __builtin_amdgcn_raw_buffer_load_b128(x2r, off, 0, 0);
+            if constexpr (PRO == 2) nwv[i] = __builtin_amdgcn_raw_buffer_load_b128(nwr, off, 0, 0);
             // chunks past the end read zero and land in the zero block
             dst[i] = live ? x_lds + m * kpad * 2 + ((cc ^ (m & 7)) * 16) : zero_lds;
         }
     };
-    auto stage_store = [&](const u32x4* v, const int* dst) __attribute__((always_inline)) {
+    auto stage_store = [&](u32x4* v, const int* dst, int c0) __attribute__((always_inline)) {
+        if constexpr (PRO == 1) {
 #pragma unroll
-        for (int i = 0; i < 8; i++)
+            for (int i = 0; i < NCH; i++) v[i] = qmv_silu_mul8(v[i], x2v[i]);
+        } else if constexpr (PRO == 2) {
+            // hidden = x + residual (workgroup 0 writes it out), then the
+            // workgroup's sum of squares, then w * (hidden * inv)
+            float ss = 0.f;
+            const int K0 = batch.p[batch.stage[0]].K;
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                v[i] = qmv_add8(v[i], x2v[i]);
+                ss += qmv_sumsq8(v[i]);
+                const int c = c0 + i * 64 * NW;
+                if (blockIdx.x == 0 && batch.pro_hidden_out && c * 8 < K0)
+                    *reinterpret_cast<u32x4*>(batch.pro_hidden_out + c * 8) = v[i];
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+            float* pred = reinterpret_cast<float*>(smem + batch.red_lds);
+            if (lane == 0) pred[wave] = ss;
+            __syncthreads();
+            float tot = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) tot += pred[w];
+            const float inv = 1.0f / sqrtf(tot / float(K0) + batch.pro_eps);
+#pragma unroll
+            for (int i = 0; i < NCH; i++) v[i] = qmv_norm8(v[i], nwv[i], inv);
+        }
+#pragma unroll
+        for (int i = 0; i < NCH; i++)
             *reinterpret_cast<u32x4*>(smem + dst[i]) = BITS == 4 ? qmv_permute_x8(v[i]) : v[i];
     };
 
@@ -794,8 +901,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // Order of the first requests: the activations, then the weight blocks.
     // Loads complete in order, so the activations can be stored (and the
     // workgroup synchronised) while the weights are still on their way.
-    u32x4 xv[8];
-    int xdst[8];
+    u32x4 xv[NCH];
+    int xdst[NCH];
     stage_load(0, threadIdx.x, xv, xdst);
     QmvStream ls;
     ls.pi = qmv_problem_of(batch, blockIdx.x, 0);
@@ -815,13 +922,15 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         ring_load(ring[d]);
         qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
     }
-    stage_store(xv, xdst);
-    for (int r = 0; r < batch.nstage; r++) {
-        const QmvProblem& pr = batch.p[batch.stage[r]];
-        const int total = M * (pr.kpad / 8);
-        for (int c0 = int(threadIdx.x) + (r == 0 ? 8 * 64 * NW : 0); c0 < total; c0 += 8 * 64 * NW) {
-            stage_load(r, c0, xv, xdst);
-            stage_store(xv, xdst);
+    stage_store(xv, xdst, int(threadIdx.x));
+    if constexpr (PRO != 2) {  // (the planner keeps a normalized row to one round)
+        for (int r = 0; r < batch.nstage; r++) {
+            const QmvProblem& pr = batch.p[batch.stage[r]];
+            const int total = M * (pr.kpad / 8);
+            for (int c0 = int(threadIdx.x) + (r == 0 ? NCH * 64 * NW : 0); c0 < total; c0 += NCH * 64 * NW) {
+                stage_load(r, c0, xv, xdst);
+                stage_store(xv, xdst, c0);
+            }
         }
     }
     static_assert(U * SPAN * 2 + 64 <= 16 * 64 * NW, "one pass clears the zero block");
@@ -1196,6 +1305,45 @@ static bool launch_qmv_group_gs(int gs, const QmvSpec* specs, int count, int M, 
 }
 
 // Preconditions as for launch_qmv_mfma, for every problem.
+// One decode launch (M = 1) whose shared activation row gets a prologue
+// while it is staged (QmvBatch::pro_*).  False, launching nothing, when the
+// problems do not fit: more than kQmvMaxProblems, different inputs, N % 16,
+// RMSNorm rows longer than one staging round.
+template <int BITS, int GS, typename ST, int PRO>
+static bool launch_qmv_pro_t(const QmvSpec* specs, int count, const QmvPrologue& pro, hipStream_t st) {
+    QmvLdsPlan plan;
+    if (!plan_qmv_lds<BITS, GS, ST>(specs, count, 1, plan) || plan.B.nstage != 1) return false;
+    const int K = specs[0].K;
+    if (PRO == 2 && K > 2 * 8 * 64 * kQmvLdsWaves) return false;
+    plan.B.pro_second = pro.second;
+    plan.B.pro_weight = pro.weight;
+    plan.B.pro_hidden_out = pro.hidden_out;
+    plan.B.pro_eps = pro.eps;
+    auto go = [&](auto kernel) {
+        if (plan.lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      plan.lds);
+        kernel<<<dim3(unsigned(plan.grid)), dim3(64 * plan.waves), size_t(plan.lds), st>>>(plan.B);
+    };
+    if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 1, true, false, PRO>);
+    else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true, true, PRO>);
+    else go(qmv_lds_kernel<BITS, GS, ST, 1, false, true, PRO>);
+    return true;
+}
+
+bool launch_qmv_prologue(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, const QmvPrologue& pro,
+                         hipStream_t st) {
+    if (gs != 64 || scale_dtype != EQ_DTYPE_BF16 || count < 1) return false;
+    if (pro.kind == 1) {
+        if (bits == 4) return launch_qmv_pro_t<4, 64, BF16T, 1>(specs, count, pro, st);
+        if (bits == 8) return launch_qmv_pro_t<8, 64, BF16T, 1>(specs, count, pro, st);
+    } else if (pro.kind == 2) {
+        if (bits == 4) return launch_qmv_pro_t<4, 64, BF16T, 2>(specs, count, pro, st);
+        if (bits == 8) return launch_qmv_pro_t<8, 64, BF16T, 2>(specs, count, pro, st);
+    }
+    return false;
+}
+
 bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st) {
     if (bits == 4) {
         if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_group_gs<4, BF16T>(gs, specs, count, M, st);

@@ -162,11 +162,18 @@ class LlamaDecoder:
     """Batch-1 greedy decode of a Llama-shaped model.  ``step(pos)`` embeds the
     token in ``self.token``, runs every layer with the cache row ``pos`` as the
     new position, and writes the argmax of the logits back into ``self.token``.
-    ``step`` enqueues on the current stream and allocates nothing."""
+    ``step`` enqueues on the current stream and allocates nothing.
+
+    ``fused`` (default: when the shapes allow it) folds each residual add +
+    RMSNorm into the launch of the projections that consume it, and SiLU-mul
+    into the down projection's launch (eq_quantized_matmul_batched_prologue):
+    6 launches per layer instead of 9.  The hidden state then alternates
+    between two buffers (every workgroup of a launch reads the old one)."""
 
     def __init__(self, layers: Sequence[DecoderLayer], embed: torch.Tensor, final_norm: torch.Tensor,
                  lm_head: QLinear, *, n_heads: int, n_kv_heads: int, eps: float, freqs: np.ndarray, max_seq: int,
-                 k_caches: Optional[List[torch.Tensor]] = None, v_caches: Optional[List[torch.Tensor]] = None):
+                 k_caches: Optional[List[torch.Tensor]] = None, v_caches: Optional[List[torch.Tensor]] = None,
+                 fused: Optional[bool] = None):
         dev = embed.device
         self.layers = list(layers)
         self.embed, self.final_norm, self.lm_head = embed, final_norm, lm_head
@@ -192,6 +199,14 @@ class LlamaDecoder:
         self.gate, self.up, self.act, self.down = e(self.ffn), e(self.ffn), e(self.ffn), e(H)
         self.logits = e(lm_head.N)
         self.token = torch.zeros((1,), dtype=torch.int32, device=dev)
+        lins = [getattr(Lr, p) for Lr in self.layers for p in ("q", "k", "v", "o", "gate", "up", "down")]
+        can_fuse = (H <= 4096 and H % 64 == 0 and self.ffn % 64 == 0 and lm_head.N % 16 == 0 and
+                    all(l.group_size == 64 and l.bits in (4, 8) and l.N % 16 == 0 and l.scales.dtype == torch.bfloat16
+                        for l in lins + [lm_head]))
+        self.fused = can_fuse if fused is None else bool(fused)
+        if self.fused and not can_fuse:
+            raise _native.EreduError("fused decode needs hidden <= 4096, group size 64, 4/8-bit codes, bf16 scales")
+        self.x2 = e(H)  # the hidden state's second buffer (fused mode)
         # grouped problems (pointers fixed for the decoder's lifetime)
         n = _native
         self._qkv, self._gu = [], []
@@ -204,6 +219,34 @@ class LlamaDecoder:
                 gu[i] = self._problem(lin, self.h, y)
             self._qkv.append(qkv)
             self._gu.append(gu)
+        if self.fused:
+            # layer 0 reads the embedding row in x; afterwards q/k/v read x2
+            # (writing x) and gate/up read x (writing x2)
+            self._fqkv, self._fgu, self._fdown, self._pro_in, self._pro_post = [], [], [], [], []
+            for li, Lr in enumerate(self.layers):
+                src = self.x if li == 0 else self.x2
+                qkv = (n.QmmProblem * 3)()
+                for i, (lin, y) in enumerate(((Lr.q, self.q), (Lr.k, self.k), (Lr.v, self.v))):
+                    qkv[i] = self._problem(lin, src, y)
+                gu = (n.QmmProblem * 2)()
+                for i, (lin, y) in enumerate(((Lr.gate, self.gate), (Lr.up, self.up))):
+                    gu[i] = self._problem(lin, self.x, y)
+                down = (n.QmmProblem * 1)()
+                down[0] = self._problem(Lr.down, self.gate, self.down)
+                pin = n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, self.down.data_ptr() if li else None,
+                                           Lr.in_norm.data_ptr(), self.x.data_ptr() if li else None, self.eps)
+                ppost = n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, self.o.data_ptr(), Lr.post_norm.data_ptr(),
+                                             self.x2.data_ptr(), self.eps)
+                self._fqkv.append(qkv)
+                self._fgu.append(gu)
+                self._fdown.append(down)
+                self._pro_in.append(pin)
+                self._pro_post.append(ppost)
+            self._pro_silu = n.ActivationPrologue(n.EQ_PROLOGUE_SILU_MUL, self.up.data_ptr(), None, None, 0.0)
+            self._flm = (n.QmmProblem * 1)()
+            self._flm[0] = self._problem(lm_head, self.x2, self.logits)
+            self._pro_final = n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, self.down.data_ptr(),
+                                                   final_norm.data_ptr(), None, self.eps)
 
     @staticmethod
     def _problem(lin: QLinear, x: torch.Tensor, y: torch.Tensor):
@@ -224,14 +267,42 @@ class LlamaDecoder:
 
     def launches_per_step(self) -> int:
         # embedding; per layer 2 norms, 4 projection launches, attention (2
-        # kernels), silu_mul; final norm, LM head, argmax
+        # kernels), silu_mul; final norm, LM head, argmax (fused: the norms
+        # and silu_mul ride in the projections' launches)
+        if self.fused:
+            return 1 + len(self.layers) * 6 + 2
         return 1 + len(self.layers) * 9 + 3
+
+    def _pro(self, probs, count: int, lin: QLinear, pro, st: int) -> None:
+        n = _native
+        check(n.lib().eq_quantized_matmul_batched_prologue(probs, count, 1, True, lin.group_size, lin.bits, b"affine",
+                                                           n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, ctypes.byref(pro), st))
+
+    def _step_fused(self, pos: int, st: int) -> None:
+        n, L = _native, _native.lib()
+        bf = n.EQ_DTYPE_BF16
+        check(L.eq_embedding(self.x.data_ptr(), self.embed.data_ptr(), self.token.data_ptr(), 1, self.vocab,
+                             self.hidden, bf, st))
+        for li, Lr in enumerate(self.layers):
+            self._pro(self._fqkv[li], 3, Lr.q, self._pro_in[li], st)
+            check(L.eq_rope_attention_decode(
+                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                self.k_caches[li].data_ptr(), self.v_caches[li].data_ptr(), self.freqs.data_ptr(), pos, self.max_seq,
+                self.n_heads, self.n_kv_heads, HEAD_DIM, self.scale, bf, st))
+            self._linear(Lr.o, self.att, self.o, st)
+            self._pro(self._fgu[li], 2, Lr.gate, self._pro_post[li], st)
+            self._pro(self._fdown[li], 1, Lr.down, self._pro_silu, st)
+        self._pro(self._flm, 1, self.lm_head, self._pro_final, st)
+        check(L.eq_argmax(self.token.data_ptr(), self.logits.data_ptr(), 1, self.lm_head.N, bf, st))
 
     def step(self, pos: int) -> None:
         if not 0 <= pos < self.max_seq:
             raise _native.EreduError(f"position {pos} outside the cache of {self.max_seq}")
         n, L = _native, _native.lib()
         st = _stream()
+        if self.fused:
+            self._step_fused(pos, st)
+            return
         bf = n.EQ_DTYPE_BF16
         H, F = self.hidden, self.ffn
         check(L.eq_embedding(self.x.data_ptr(), self.embed.data_ptr(), self.token.data_ptr(), 1, self.vocab, H, bf,

@@ -132,6 +132,38 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
                        int64_t rows, int64_t cols, int endian, int definition, int out_dtype,
                        eq_stream_t stream);
 
+/* Activation prologues of eq_quantized_matmul_batched_prologue. */
+enum eq_prologue_kind { EQ_PROLOGUE_SILU_MUL = 1, EQ_PROLOGUE_RMS_NORM = 2 };
+
+typedef struct eq_activation_prologue {
+    int kind;            /* enum eq_prologue_kind */
+    const void* second;  /* SILU_MUL: up (x is the gate); RMS_NORM: residual added to x (may be NULL) */
+    const void* weight;  /* RMS_NORM: norm weight [K] */
+    void* hidden_out;    /* RMS_NORM: x + residual [K] (may be NULL; must not overlap x or the residual) */
+    float eps;           /* RMS_NORM */
+} eq_activation_prologue;
+
+/*
+ * eq_quantized_matmul_batched with the shared input row transformed first:
+ *   SILU_MUL:  x' = silu(x) * second            (Mlp::hidden before down_proj,
+ *              eredu-architectures/src/llama.rs:414-422)
+ *   RMS_NORM:  h = x + second (rounded to bf16, stored to hidden_out),
+ *              x' = h * rsqrt(mean(h^2) + eps) * weight
+ *              (the residual add and pre-norm of TransformerBlock::forward,
+ *              llama.rs:477-495)
+ * then y_i = x' . W_i^T.  Results equal eq_silu_mul / eq_rms_norm followed by
+ * eq_quantized_matmul_batched (RMS_NORM up to the order of the sum of
+ * squares).  No counterpart in the reference's C ABI: it folds the MLX ops a
+ * decoder layer runs before its projections into their launch.  Supported:
+ * M = 1, 1-8 problems sharing x, transpose = true, bf16 x and scales, group
+ * size 64, 4/8-bit, N % 16 == 0, K % 64 == 0, K <= 4096 for RMS_NORM;
+ * anything else is rejected (use the separate entry points).
+ */
+int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* problems, int count, int64_t M,
+                                         bool transpose, int group_size, int bits, const char* mode,
+                                         int x_dtype, int scale_dtype,
+                                         const eq_activation_prologue* prologue, eq_stream_t stream);
+
 /*
  * Decode-step operations around the quantized projections of a Llama-shaped
  * decoder at batch 1 (configs[4] of the measurement plan).  bf16 only

@@ -145,7 +145,7 @@ def test_embedding_and_argmax(cuda):
     assert list(idx) == list(ref) and idx[1] == 5 and idx[2] == 128255
 
 
-def tiny_model(seed=0, layers=2, n_heads=4, n_kv=2, ffn=1024, vocab=1024, max_seq=64):
+def tiny_model(seed=0, layers=2, n_heads=4, n_kv=2, ffn=1024, vocab=1024, max_seq=64, fused=None):
     H = n_heads * 128
     rng = np.random.default_rng(seed)
     host = {"hidden": H, "n_heads": n_heads, "n_kv_heads": n_kv, "eps": 1e-5,
@@ -176,12 +176,14 @@ def tiny_model(seed=0, layers=2, n_heads=4, n_kv=2, ffn=1024, vocab=1024, max_se
                                  ("q", "k", "v", "o", "gate", "up", "down"))) for L in host["layers"]]
     dec = E.LlamaDecoder(dev_layers, dev_bf16(host["embed"]), dev_bf16(host["final_norm"]), qlin(host["lm_head"]),
                          n_heads=n_heads, n_kv_heads=n_kv, eps=1e-5, freqs=host["freqs"], max_seq=max_seq,
-                         k_caches=[dev_bf16(k) for k in kcs], v_caches=[dev_bf16(v) for v in vcs])
+                         k_caches=[dev_bf16(k) for k in kcs], v_caches=[dev_bf16(v) for v in vcs], fused=fused)
     return host, dec, kcs, vcs
 
 
-def test_decode_step_end_to_end(cuda):
-    host, dec, kcs, vcs = tiny_model()
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_step_end_to_end(cuda, fused):
+    host, dec, kcs, vcs = tiny_model(fused=fused)
+    assert dec.fused == fused
     kcs = [k.copy() for k in kcs]
     vcs = [v.copy() for v in vcs]
     token = 7
@@ -201,10 +203,11 @@ def test_decode_step_end_to_end(cuda):
         token = nxt
 
 
-def test_decode_step_graph_replay(cuda):
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_step_graph_replay(cuda, fused):
     """The step captured in a HIP graph and replayed matches the eager step."""
-    _, dec, _, _ = tiny_model(seed=3)
-    _, dec2, _, _ = tiny_model(seed=3)
+    _, dec, _, _ = tiny_model(seed=3, fused=fused)
+    _, dec2, _, _ = tiny_model(seed=3, fused=fused)
     for d in (dec, dec2):
         d.token.fill_(5)
     st = torch.cuda.Stream()
@@ -228,3 +231,101 @@ def test_decode_step_graph_replay(cuda):
         toks2.append(int(dec2.token.item()))
         assert torch.equal(dec.logits, dec2.logits)
     assert toks == toks2
+
+
+def _prologue_call(problems, lins, pro):
+    from eredu_amd import _native as n
+
+    arr = (n.QmmProblem * len(problems))()
+    for i, (x, lin, y) in enumerate(problems):
+        arr[i] = n.QmmProblem(y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.scales.data_ptr(),
+                              lin.biases.data_ptr(), lin.N, lin.K)
+    import ctypes
+    n.check(n.lib().eq_quantized_matmul_batched_prologue(arr, len(problems), 1, True, 64, lins[0].bits, b"affine",
+                                                         n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, ctypes.byref(pro), None))
+
+
+def _qlin(N, K, seed, bits=4):
+    w, s, b = synthetic_linear(N, K, 64, bits, seed)
+    return E.QLinear(dev_words(w), dev_bf16(s), dev_bf16(b), bits, 64), (w, s, b)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("K", [1024, 14336])
+def test_prologue_silu_mul(cuda, bits, K):
+    """down_proj(silu(gate) * up) in one launch equals eq_silu_mul then the matmul, bit for bit."""
+    from eredu_amd import _native as n
+
+    print(f"[case] prologue silu_mul bits={bits} K={K}", flush=True)
+    lin, (w, s, b) = _qlin(4096, K, K + bits, bits)
+    g, u = dev_bf16(randn_bits(K, 1, std=2.0)), dev_bf16(randn_bits(K, 2))
+    y = torch.empty(4096, dtype=torch.bfloat16, device="cuda")
+    _prologue_call([(g, lin, y)], [lin], n.ActivationPrologue(n.EQ_PROLOGUE_SILU_MUL, u.data_ptr(), None, None, 0.0))
+    act = E.silu_mul(g, u)
+    y2 = torch.empty_like(y)
+    _prologue_call_plain = n.lib().eq_quantized_matmul(y2.data_ptr(), act.data_ptr(), lin.w.data_ptr(),
+                                                        lin.scales.data_ptr(), lin.biases.data_ptr(), 1, 4096, K, True,
+                                                        64, bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, None)
+    n.check(_prologue_call_plain)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    ref = orc.quantized_matmul_f64(host_bits16(act), orc.BF16, w, s, b, orc.BF16, True, 64, bits, 4096, K)
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(y).reshape(1, -1), ref, out_is_bf16=True)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("K", [512, 4096])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_prologue_rms_norm(cuda, K, with_residual):
+    """q/k/v of RMSNorm(x + r) in one launch: hidden_out bit-exact, the
+    normalized row within 1 ulp of eq_rms_norm's (sum order), outputs within
+    the matmul rule of the oracle on the oracle's normalized row."""
+    from eredu_amd import _native as n
+
+    print(f"[case] prologue rms_norm K={K} residual={with_residual}", flush=True)
+    shapes = [(K, K), (K // 4, K), (K // 4, K)]
+    lins = [_qlin(N, K_, 100 + i) for i, (N, K_) in enumerate(shapes)]
+    xb, rb = randn_bits(K, 7), randn_bits(K, 8)
+    wb = bits(1.0 + 0.1 * np.random.default_rng(9).standard_normal(K))
+    x, r, nw = dev_bf16(xb), dev_bf16(rb), dev_bf16(wb)
+    hid = torch.empty(K, dtype=torch.bfloat16, device="cuda")
+    ys = [torch.empty(N, dtype=torch.bfloat16, device="cuda") for N, _ in shapes]
+    pro = n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, r.data_ptr() if with_residual else None, nw.data_ptr(),
+                               hid.data_ptr() if with_residual else None, 1e-5)
+    _prologue_call([(x, l, y) for (l, _), y in zip(lins, ys)], [l for l, _ in lins], pro)
+    torch.cuda.synchronize()
+    hid_ref, h_ref = D.rms_norm_bf16(xb, wb, 1e-5, rb if with_residual else None)
+    if with_residual:
+        assert np.array_equal(host_bits16(hid), hid_ref)
+    assert np.array_equal(host_bits16(x), xb)  # the input row is not modified
+    for (lin, (w, s, b)), y, (N, K_) in zip(lins, ys, shapes):
+        ref = orc.quantized_matmul_f64(h_ref, orc.BF16, w, s, b, orc.BF16, True, 64, 4, N, K_)
+        ok, worst, _ = orc.matmul_within_tolerance(host_f32(y).reshape(1, -1), ref, out_is_bf16=True)
+        assert ok, worst
+
+
+def test_prologue_rejects_unsupported(cuda):
+    from eredu_amd import _native as n
+    import ctypes
+
+    lin, _ = _qlin(512, 8192, 5)
+    x = dev_bf16(randn_bits(8192, 1))
+    y = torch.empty(512, dtype=torch.bfloat16, device="cuda")
+    arr = (n.QmmProblem * 1)()
+    arr[0] = n.QmmProblem(y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.scales.data_ptr(), lin.biases.data_ptr(),
+                          512, 8192)
+    call = lambda pro, M=1: n.lib().eq_quantized_matmul_batched_prologue(arr, 1, M, True, 64, 4, b"affine",
+                                                                         n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16,
+                                                                         ctypes.byref(pro), None)
+    wv = dev_bf16(randn_bits(8192, 2))
+    assert call(n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, None, wv.data_ptr(), None, 1e-5)) == 1
+    assert "4096" in n.lib().eq_last_error().decode()
+    assert call(n.ActivationPrologue(7, None, None, None, 0.0)) == 1
+    assert call(n.ActivationPrologue(n.EQ_PROLOGUE_SILU_MUL, wv.data_ptr(), None, None, 0.0), M=2) == 1
+    # the hidden output may not alias the input it is computed from
+    lin2, _ = _qlin(512, 4096, 6)
+    x2 = dev_bf16(randn_bits(4096, 3))
+    arr[0] = n.QmmProblem(y.data_ptr(), x2.data_ptr(), lin2.w.data_ptr(), lin2.scales.data_ptr(),
+                          lin2.biases.data_ptr(), 512, 4096)
+    assert call(n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, None, wv.data_ptr(), x2.data_ptr(), 1e-5)) == 1
+    assert "overlap" in n.lib().eq_last_error().decode()
