@@ -463,9 +463,10 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     a.M = M, a.N = N, a.K = K;
     a.mtiles = (M + kBM - 1) / kBM, a.ntiles = (N + kBN - 1) / kBN;
     const int tiles = a.mtiles * a.ntiles, nchunks = K / kBK;
-    // Split K so that the grid covers the CUs, at least 8 chunks per split (4
-    // per K-group).
-    int splits = (qmm_cu_count() + tiles / 2) / tiles;
+    // Split K so that the grid fills the CUs without exceeding them (one
+    // workgroup per CU: a second round of workgroups would double the time),
+    // at least 8 chunks per split (4 per K-group).
+    int splits = qmm_cu_count() / tiles;
     splits = splits < 1 ? 1 : splits;
     splits = splits > nchunks / 8 ? nchunks / 8 : splits;
     splits = splits < 1 ? 1 : splits;
