@@ -183,12 +183,14 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // Activations go straight from memory to LDS: load i of wave w fills the
     // 1 KiB (8 rows of 128 B) at (4 w + i) KiB of the 128 x 64 tile, lane l
     // the 16 B at 16 l, i.e. row 8 (4 w + i) + l / 8, slot l % 8.  Slot p of
-    // row r holds the row's 16-byte chunk p ^ (r & 7), so the lane loads chunk
-    // (l % 8) ^ (l / 8).
+    // row r holds the row's 16-byte chunk p ^ ((r / 2) & 7), so the lane loads
+    // chunk (l % 8) ^ ((row / 2) & 7).  (A 16-lane group of an A-operand read
+    // takes rows r .. r + 15 at one chunk; 64 banks of 4 bytes span two rows,
+    // so the rows of one parity must land in 8 different 16-byte bank groups.)
     uint32_t a_goff[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int row = 8 * (4 * wave + i) + (lane >> 3), c = (lane & 7) ^ (lane >> 3);
+        const int row = 8 * (4 * wave + i) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
         a_goff[i] = m0 + row < M ? (uint32_t(m0 + row) * uint32_t(K) + uint32_t(8 * c)) * 2u : kOutOfRange;
     }
     // Weight rows of this lane: columns n0 + 64 wave + 32 j + l32, codes from 32 kb.
@@ -257,10 +259,10 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     auto barrier = [&]() __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
 
     // A operand of this lane for step t and row block mi: row 32 mi + l32,
-    // chunk (4 kb + t) ^ (row & 7) (row & 7 = l32 & 7 for every mi).
+    // chunk 4 kb + t in slot (4 kb + t) ^ ((row / 2) & 7) (the same for every mi).
     uint32_t aoff[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) aoff[t] = uint32_t(l32 * (kBK * 2) + (((4 * kb + t) ^ (l32 & 7)) << 4));
+    for (int t = 0; t < 4; t++) aoff[t] = uint32_t(l32 * (kBK * 2) + (((4 * kb + t) ^ ((l32 >> 1) & 7)) << 4));
 
     f32x16 acc[4][2];
 #pragma unroll
