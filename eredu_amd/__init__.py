@@ -6,7 +6,7 @@ hand-written HIP kernels behind a C ABI (``include/eredu_hip.h``), with a
 host-side mirror of the reference's operator API:
 
 * :mod:`eredu_amd.quantization` -- safemlx ``quantized_matmul[_with_mode]``,
-  ``dequantize[_with_mode]``, ``QuantizedLinear``.
+  ``dequantize[_with_mode]``, ``quantize[_with_mode]``, ``QuantizedLinear``.
 * :mod:`eredu_amd.gguf` -- eredu-gguf ``convert_affine`` / ``AffineTensor``
   and dense dequantization.
 """
@@ -22,6 +22,8 @@ from .quantization import (
     quantized_matmul_batched,
     quantized_matmul_with_mode,
     quantized_packed_dimension,
+    quantize,
+    quantize_with_mode,
 )
 
 __all__ = [
@@ -36,4 +38,6 @@ __all__ = [
     "quantized_matmul_batched",
     "quantized_matmul_with_mode",
     "quantized_packed_dimension",
+    "quantize",
+    "quantize_with_mode",
 ]

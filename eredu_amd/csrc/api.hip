@@ -188,6 +188,54 @@ int check_gs_bits(int group_size, int bits) {
 
 using namespace eq;
 
+// Affine group quantizer (the MLX quantize that safemlx::ops::quantize_with_mode
+// calls, safemlx/src/ops/quantization.rs:100-159), one thread per group of
+// `gs` values along a row: min and max; scale = (max - min) / (2^bits - 1)
+// (at least 1e-7), signed toward the larger magnitude; the edge value
+// (min or max) made exactly representable (scale = edge / rint(edge /
+// scale)); bias = edge; scale and bias stored in the input's dtype and the
+// codes q = clamp(rint((w - bias) / scale), 0, 2^bits - 1) computed with the
+// stored values, packed LSB-first.
+template <int BITS, typename T>
+__global__ __launch_bounds__(256) void quantize_kernel(uint32_t* __restrict__ wq, typename T::storage* __restrict__ sc,
+                                                       typename T::storage* __restrict__ bi,
+                                                       const typename T::storage* __restrict__ w, int64_t groups,
+                                                       int gs) {
+    const int64_t gidx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (gidx >= groups) return;
+    const typename T::storage* v = w + gidx * gs;
+    constexpr int n_bins = (1 << BITS) - 1;
+    float mn = load_param<T>(v, 0), mx = mn;
+    for (int i = 1; i < gs; i++) {
+        const float x = load_param<T>(v, i);
+        mn = x < mn ? x : mn;
+        mx = x > mx ? x : mx;
+    }
+    float scale = (mx - mn) / float(n_bins);
+    if (scale < 1e-7f) scale = 1e-7f;
+    const bool neg = fabsf(mn) > fabsf(mx);
+    scale = neg ? scale : -scale;
+    const float edge = neg ? mn : mx;
+    const float q0 = rintf(edge / scale);
+    if (q0 != 0.0f) scale = edge / q0;
+    store_out<T>(sc, gidx, scale);
+    store_out<T>(bi, gidx, edge);
+    const float s_st = load_param<T>(sc, gidx), b_st = load_param<T>(bi, gidx);
+    uint32_t* dst = wq + gidx * (gs * BITS / 32);
+    for (int w0 = 0; w0 < gs * BITS / 32; w0++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 32 / BITS; e++) {
+            const float x = load_param<T>(v, w0 * (32 / BITS) + e);
+            float q = s_st != 0.0f ? rintf((x - b_st) / s_st) : 0.0f;
+            q = q >= 0.0f ? q : 0.0f;
+            q = q > float(n_bins) ? float(n_bins) : q;
+            word |= uint32_t(q) << (BITS * e);
+        }
+        dst[w0] = word;
+    }
+}
+
 extern "C" const char* eq_last_error(void) { return g_last_error.c_str(); }
 
 extern "C" int eq_version(void) { return 100; }
@@ -422,6 +470,43 @@ extern "C" int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* proble
         return 1;
     }
     return check_launch("quantized_matmul_batched_prologue");
+}
+
+extern "C" int eq_quantize(uint32_t* w_out, void* scales, void* biases, const void* w, int64_t rows, int64_t cols,
+                           int group_size, int bits, const char* mode, int dtype, eq_stream_t stream) {
+    clear_error();
+    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    if (!valid_dtype(dtype)) {
+        set_error("invalid dtype code");
+        return 1;
+    }
+    if (rows < 0 || cols < 0 || (cols % group_size) != 0) {
+        set_error("cols must be a non-negative multiple of group_size");
+        return 1;
+    }
+    if (rows == 0 || cols == 0) return 0;
+    if (!w_out || !scales || !biases || !w) {
+        set_error("null pointer argument");
+        return 1;
+    }
+    const int64_t groups = rows * (cols / group_size);
+    if ((groups + 255) / 256 > INT32_MAX) {
+        set_error("tensor too large");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(unsigned((groups + 255) / 256));
+    with_bits(bits, [&](auto bc) {
+        constexpr int B = decltype(bc)::value;
+        with_dtype(dtype, [&](auto tt) {
+            typedef decltype(tt) T;
+            quantize_kernel<B, T><<<grid, 256, 0, st>>>(w_out, static_cast<typename T::storage*>(scales),
+                                                        static_cast<typename T::storage*>(biases),
+                                                        static_cast<const typename T::storage*>(w), groups,
+                                                        group_size);
+        });
+    });
+    return check_launch("quantize");
 }
 
 extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases, int64_t rows,

@@ -202,6 +202,41 @@ def quantized_matmul_batched(
     return [y.reshape(*lead, N) for y, lead, N in outs]
 
 
+def quantize_with_mode(
+    w: torch.Tensor,
+    group_size: int,
+    bits: int,
+    mode: QuantizationMode = QuantizationMode.Affine,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(codes u32-as-int32 [rows, cols * bits / 32], scales, biases) of the
+    affine quantization of w [..., cols] along its last axis, scales and
+    biases in w's dtype (safemlx/src/ops/quantization.rs:100-159; C ABI:
+    eq_quantize)."""
+    mode.validate(group_size, bits)
+    if mode is not QuantizationMode.Affine:
+        raise EreduError("only affine quantization is implemented on the device path")
+    _require_device(w)
+    cols = w.shape[-1]
+    if cols % group_size != 0:
+        raise EreduError(f"the last dimension ({cols}) is not divisible by group_size {group_size}")
+    w2 = w.reshape(-1, cols).contiguous()
+    rows = w2.shape[0]
+    wq = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device=w.device)
+    scales = torch.empty((rows, cols // group_size), dtype=w.dtype, device=w.device)
+    biases = torch.empty_like(scales)
+    check(
+        _native.lib().eq_quantize(wq.data_ptr(), scales.data_ptr(), biases.data_ptr(), w2.data_ptr(), rows, cols,
+                                  int(group_size), int(bits), mode.value.encode(), _dtype_code(w2, "w"), _stream())
+    )
+    lead = tuple(w.shape[:-1])
+    return (wq.reshape(*lead, -1), scales.reshape(*lead, -1), biases.reshape(*lead, -1))
+
+
+def quantize(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS):
+    """Affine quantize with the reference's defaults (quantization.rs:100-117)."""
+    return quantize_with_mode(w, group_size, bits, QuantizationMode.Affine)
+
+
 def dequantize_with_mode(
     w: torch.Tensor,
     scales: torch.Tensor,

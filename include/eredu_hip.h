@@ -132,6 +132,19 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
                        int64_t rows, int64_t cols, int endian, int definition, int out_dtype,
                        eq_stream_t stream);
 
+/*
+ * Affine group quantization of w [rows, cols] (dtype: f32, f16 or bf16) along
+ * its rows: codes [rows, cols * bits / 32] u32 packed LSB-first, scales and
+ * biases [rows, cols / group_size] in w's dtype, with MLX's affine rule --
+ * scale = (max - min) / (2^bits - 1) signed toward the larger magnitude, the
+ * edge value made exactly representable, bias = edge, codes rounded from the
+ * stored scale and bias.  Replaces mlx_quantize (ops.h:801-808) under
+ * safemlx::ops::quantize_with_mode (safemlx/src/ops/quantization.rs:100-159).
+ * bits in {2, 4, 8}; group_size in {32, 64, 128}.
+ */
+int eq_quantize(uint32_t* w_out, void* scales, void* biases, const void* w, int64_t rows, int64_t cols,
+                int group_size, int bits, const char* mode, int dtype, eq_stream_t stream);
+
 /* Activation prologues of eq_quantized_matmul_batched_prologue. */
 enum eq_prologue_kind { EQ_PROLOGUE_SILU_MUL = 1, EQ_PROLOGUE_RMS_NORM = 2 };
 

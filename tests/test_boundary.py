@@ -26,7 +26,7 @@ def test_header_declares_the_boundary():
     assert declared_functions() == sorted(
         ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
-         "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue"]
+         "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize"]
     )
 
 
@@ -177,3 +177,13 @@ def test_decode_ops_reject_bad_arguments():
     # zero-size calls succeed without launching
     assert L.eq_rms_norm(16, 16, None, 16, 0, 4096, 1e-5, bf16, None) == 0
     assert L.eq_silu_mul(16, 16, 16, 0, bf16, None) == 0
+
+
+def test_quantize_rejects_bad_arguments():
+    bf16 = _native.EQ_DTYPE_BF16
+    _rejects(L.eq_quantize(16, 16, 16, 16, 4, 100, 64, 4, b"affine", bf16, None), "multiple of group_size")
+    _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 48, 4, b"affine", bf16, None), "group")
+    _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 64, 5, b"affine", bf16, None), "bits")
+    _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 64, 4, b"affine", 9, None), "dtype")
+    _rejects(L.eq_quantize(None, 16, 16, 16, 4, 128, 64, 4, b"affine", bf16, None), "null")
+    assert L.eq_quantize(16, 16, 16, 16, 0, 128, 64, 4, b"affine", bf16, None) == 0
