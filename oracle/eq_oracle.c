@@ -24,7 +24,8 @@
  *                                    the converted tensor; closed form.
  *   or_qmm_f32                       pinned: fp64 numpy closed form (tolerance),
  *                                    pure-Python brute force on tiny shapes.
- *   or_quantize_affine               parity unpinned: input generator only
+ *   or_quantize_affine               parity unpinned: input generator and the
+ *                                    checker of the device quantizer
  *                                    (MLX v0.32.0 quantize is not available);
  *                                    bounded by test_quantize_dequantize's
  *                                    max|w - w_hat| <= 127/2^bits rule.
