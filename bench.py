@@ -232,6 +232,20 @@ def bench_gguf(steps, warmup):
             gbs = (nraw + out_bytes) / (ms * 1e-3) / 1e9
             out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        if ty in (G.GgmlType.Q8_0, G.GgmlType.Q4K):
+            # batch-1 linear straight from the blocks: y [1, 4096] = x [1, 14336] . W^T
+            x = torch.randn((1, cols), device="cuda").to(torch.bfloat16)
+            y = torch.empty((1, rows), dtype=torch.bfloat16, device="cuda")
+
+            def lin(st):
+                for r in raws:
+                    n.check(n.lib().eq_gguf_linear(y.data_ptr(), x.data_ptr(), r.data_ptr(), nraw, int(ty), 1, rows,
+                                                   cols, 0, n.EQ_DTYPE_BF16, st))
+
+            ms = Timer(lin).ms_per_replay(max(steps // 4, 5), warmup) / copies
+            gbs = (nraw + cols * 2 + rows * 2) / (ms * 1e-3) / 1e9
+            out[f"{ty.name} linear_M1"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         del raws
         torch.cuda.empty_cache()
     return out

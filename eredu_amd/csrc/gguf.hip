@@ -310,6 +310,156 @@ __global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw
     store8<OUT>(out, (idx >> 2) * 32 + 8 * c, v);
 }
 
+// ------------------------------------------------- native linear (M small)
+//
+// NativeQuantizedTensor::linear with transpose = true
+// (safemlx/src/native_quantization.rs:741-772, its CPU stream at :858-913):
+// y[m, n] = sum_k x[m, k] W[n, k], W decoded by the native definition (Q4_K:
+// d sc q - dmin m; Q8_0: d q), accumulated in f32, y in bf16.  No affine
+// expansion: each wave takes one output row n at a time and walks its
+// blocks, its lanes splitting them; the per-group factors are applied to
+// sums of x q and of x (d sc sum(x q) - dmin m sum(x)).  kLinRows activation
+// rows per launch.
+constexpr int kLinRows = 8;
+
+__device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float* f) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(&v);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = bf16_bits_to_f32(p[i] & 0xffffu);
+        f[2 * i + 1] = bf16_bits_to_f32(p[i] >> 16);
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Q4_K: a lane takes one 16-byte quant chunk (32 codes: 16 of group 2p in
+// the low nibbles, 16 of group 2p + 1 in the high) and its superblock's
+// 16-byte header (d, dmin, the 12 scale/min bytes).  Rows are whole
+// superblocks of 144 = 9 x 16 bytes, so both loads are aligned.
+template <bool BIG>
+__global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
+                                                  const uint8_t* __restrict__ raw, int M, int N, int K) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nsb = K / 256, nch = nsb * 8;
+    for (int n = blockIdx.x * 4 + wave; n < N; n += gridDim.x * 4) {
+        const uint8_t* row = raw + int64_t(n) * nsb * 144;
+        float acc[kLinRows];
+#pragma unroll
+        for (int m = 0; m < kLinRows; m++) acc[m] = 0.f;
+        for (int c = lane; c < nch; c += 64) {
+            const int sb = c >> 3, q = c & 7, p = q >> 1;
+            const uint4 hv = *reinterpret_cast<const uint4*>(row + sb * 144);
+            const uint4 qv = *reinterpret_cast<const uint4*>(row + sb * 144 + 16 + q * 16);
+            const uint32_t h[4] = {hv.x, hv.y, hv.z, hv.w};
+            uint32_t sc0, m0, sc1, m1;
+            q4k_scale_min(h, 2 * p, sc0, m0);
+            q4k_scale_min(h, 2 * p + 1, sc1, m1);
+            const float d = f16_bits_to_f32(BIG ? bswap16(h[0] & 0xffffu) : (h[0] & 0xffffu));
+            const float dmin = f16_bits_to_f32(BIG ? bswap16(h[0] >> 16) : (h[0] >> 16));
+            const float ds0 = d * float(sc0), dm0 = dmin * float(m0);
+            const float ds1 = d * float(sc1), dm1 = dmin * float(m1);
+            const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+            const int k0 = sb * 256 + 2 * p * 32 + (q & 1) * 16;  // group 2p; group 2p + 1 at k0 + 32
+#pragma unroll
+            for (int m = 0; m < kLinRows; m++) {
+                if (m >= M) break;
+                const uint4* xa = reinterpret_cast<const uint4*>(x + int64_t(m) * K + k0);
+                const uint4* xb = reinterpret_cast<const uint4*>(x + int64_t(m) * K + k0 + 32);
+                float fa[16], fb[16];
+                bf16x8_to_f32(xa[0], fa);
+                bf16x8_to_f32(xa[1], fa + 8);
+                bf16x8_to_f32(xb[0], fb);
+                bf16x8_to_f32(xb[1], fb + 8);
+                float sxq0 = 0.f, sx0 = 0.f, sxq1 = 0.f, sx1 = 0.f;
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const uint32_t byte = (qw[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                    sxq0 = fmaf(fa[j], float(byte & 15u), sxq0);
+                    sx0 += fa[j];
+                    sxq1 = fmaf(fb[j], float(byte >> 4), sxq1);
+                    sx1 += fb[j];
+                }
+                acc[m] += (ds0 * sxq0 - dm0 * sx0) + (ds1 * sxq1 - dm1 * sx1);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < kLinRows; m++) {
+            if (m >= M) break;
+            const float v = wave_sum(acc[m]);
+            if (lane == 0) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(v));
+        }
+    }
+}
+
+// Q8_0: 34-byte blocks are not 4-byte aligned, so a wave first copies a run
+// of up to 256 blocks of its row into LDS (16-byte loads when the run is
+// 16-byte aligned, else 2-byte loads), then each lane takes whole blocks.
+template <bool BIG>
+__global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
+                                                   const uint8_t* __restrict__ raw, int M, int N, int K) {
+    constexpr int kRun = 256;
+    __shared__ uint16_t lds[4][kRun * 17];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = K / 32;
+    uint16_t* mine = lds[wave];
+    for (int n = blockIdx.x * 4 + wave; n < N; n += gridDim.x * 4) {
+        float acc[kLinRows];
+#pragma unroll
+        for (int m = 0; m < kLinRows; m++) acc[m] = 0.f;
+        for (int b0 = 0; b0 < nb; b0 += kRun) {
+            const int cnt = min(kRun, nb - b0);
+            const uint8_t* src = raw + (int64_t(n) * nb + b0) * 34;
+            __builtin_amdgcn_wave_barrier();
+            if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0 && (cnt * 34) % 16 == 0) {
+                for (int i = lane; i < cnt * 34 / 16; i += 64)
+                    reinterpret_cast<uint4*>(mine)[i] = reinterpret_cast<const uint4*>(src)[i];
+            } else {
+                for (int i = lane; i < cnt * 17; i += 64) mine[i] = reinterpret_cast<const uint16_t*>(src)[i];
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS stores have landed
+            __builtin_amdgcn_wave_barrier();
+            for (int lb = lane; lb < cnt; lb += 64) {
+                const uint16_t* blk = mine + lb * 17;
+                const float d = f16_bits_to_f32(BIG ? bswap16(blk[0]) : blk[0]);
+                uint32_t qw[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) qw[i] = lds_u32(blk + 1 + 2 * i);
+                const int k0 = (b0 + lb) * 32;
+#pragma unroll
+                for (int m = 0; m < kLinRows; m++) {
+                    if (m >= M) break;
+                    const uint4* xa = reinterpret_cast<const uint4*>(x + int64_t(m) * K + k0);
+                    float s = 0.f;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        float f[8];
+                        bf16x8_to_f32(xa[v], f);
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const int e = v * 8 + j;
+                            const int8_t qb = int8_t((qw[e >> 2] >> (8 * (e & 3))) & 0xffu);
+                            s = fmaf(f[j], float(qb), s);
+                        }
+                    }
+                    acc[m] = fmaf(d, s, acc[m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < kLinRows; m++) {
+            if (m >= M) break;
+            const float v = wave_sum(acc[m]);
+            if (lane == 0) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(v));
+        }
+    }
+}
+
 struct Geometry {
     int values, bytes, bits;
 };
@@ -471,4 +621,50 @@ extern "C" int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len
     else
         launch_dense<F32T>(ggml_type, big, native, raw, nblocks, vec_ok, static_cast<float*>(out), st);
     return check_launch("gguf dequantize");
+}
+
+extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
+                              int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream) {
+    clear_error();
+    if (ggml_type != EQ_GGML_Q4_K && ggml_type != EQ_GGML_Q8_0) {
+        set_error("native GGUF linear covers Q4_K and Q8_0");
+        return 1;
+    }
+    Geometry geo;
+    int64_t nblocks;
+    if (validate(raw, raw_len, ggml_type, N, K, endian, geo, nblocks)) return 1;
+    if (x_dtype != EQ_DTYPE_BF16) {
+        set_error("native GGUF linear takes bf16 activations");
+        return 1;
+    }
+    if (M < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
+        set_error("dimension exceeds 2^31 - 1");
+        return 1;
+    }
+    if (M == 0) return 0;
+    if (!y || !x) {
+        set_error("null pointer argument");
+        return 1;
+    }
+    if (!aligned(x, 16) || (ggml_type == EQ_GGML_Q4_K && !aligned(raw, 16))) {
+        set_error("x (and a Q4_K payload) must be 16-byte aligned");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool big = endian == EQ_ENDIAN_BIG;
+    const int rows_per_wg = 4;
+    const unsigned grid = unsigned(N < 1024 * rows_per_wg ? (N + rows_per_wg - 1) / rows_per_wg : 1024);
+    for (int64_t m0 = 0; m0 < M; m0 += kLinRows) {
+        const int mc = int(M - m0 < kLinRows ? M - m0 : kLinRows);
+        uint16_t* yy = static_cast<uint16_t*>(y) + m0 * N;
+        const uint16_t* xx = static_cast<const uint16_t*>(x) + m0 * K;
+        if (ggml_type == EQ_GGML_Q4_K) {
+            if (big) q4k_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
+            else q4k_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
+        } else {
+            if (big) q8_0_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
+            else q8_0_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
+        }
+    }
+    return check_launch("gguf linear");
 }

@@ -161,3 +161,27 @@ def dequantize(
         )
     )
     return out
+
+
+def linear(x: torch.Tensor, desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little) -> torch.Tensor:
+    """y = x . W^T with W the GGUF tensor of ``desc`` decoded by the native
+    definition, straight from its Q4_K or Q8_0 blocks (no affine expansion):
+    NativeQuantizedTensor::linear with transpose = true
+    (safemlx/src/native_quantization.rs:741-772); C ABI eq_gguf_linear.
+    x is bf16 [..., K] on the GPU; W's MLX shape is [N, K]."""
+    ty = GgmlType(desc.ggml_type)
+    _check_raw(desc, raw)
+    shape, N, K = _rows_cols(desc)
+    if len(shape) != 2:
+        raise EreduError(f"tensor '{desc.name}': native linear expects a single logical matrix")
+    if x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[-1] != K:
+        raise EreduError(f"native linear expected a bf16 CUDA input with trailing dimension {K}")
+    x2 = x.reshape(-1, K).contiguous()
+    y = torch.empty((x2.shape[0], N), dtype=torch.bfloat16, device=x.device)
+    check(
+        _native.lib().eq_gguf_linear(
+            y.data_ptr(), x2.data_ptr(), raw.contiguous().data_ptr(), raw.numel(), int(ty), x2.shape[0], N, K,
+            int(endian), _native.EQ_DTYPE_BF16, torch.cuda.current_stream().cuda_stream,
+        )
+    )
+    return y.reshape(*x.shape[:-1], N)

@@ -133,6 +133,18 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
                        eq_stream_t stream);
 
 /*
+ * Native GGUF linear: y[M, N] = x[M, K] . W^T with W the GGUF tensor (MLX
+ * shape [N, K], raw Q4_K or Q8_0 blocks as stored, raw_len bytes) decoded by
+ * the native definition (Q4_K: d*sc*q - dmin*m, Q8_0: d*q) without an affine
+ * expansion; f32 accumulation, bf16 x and y.  Replaces
+ * NativeQuantizedTensor::linear with transpose = true
+ * (safemlx/src/native_quantization.rs:741-772), whose CUDA/CPU builds decode
+ * on the host (:846-913).  x 16-byte aligned; a Q4_K payload 16-byte aligned.
+ */
+int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
+                   int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream);
+
+/*
  * Affine group quantization of w [rows, cols] (dtype: f32, f16 or bf16) along
  * its rows: codes [rows, cols * bits / 32] u32 packed LSB-first, scales and
  * biases [rows, cols / group_size] in w's dtype, with MLX's affine rule --

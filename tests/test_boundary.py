@@ -26,7 +26,8 @@ def test_header_declares_the_boundary():
     assert declared_functions() == sorted(
         ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
-         "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize"]
+         "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
+         "eq_gguf_linear"]
     )
 
 
@@ -187,3 +188,13 @@ def test_quantize_rejects_bad_arguments():
     _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 64, 4, b"affine", 9, None), "dtype")
     _rejects(L.eq_quantize(None, 16, 16, 16, 4, 128, 64, 4, b"affine", bf16, None), "null")
     assert L.eq_quantize(16, 16, 16, 16, 0, 128, 64, 4, b"affine", bf16, None) == 0
+
+
+def test_gguf_linear_rejects_bad_arguments():
+    bf16 = _native.EQ_DTYPE_BF16
+    # Q4_0 is not a native-linear type; payload length must match; bf16 only
+    _rejects(L.eq_gguf_linear(16, 16, 16, 18 * 8, 2, 1, 2, 128, 0, bf16, None), "Q4_K and Q8_0")
+    _rejects(L.eq_gguf_linear(16, 16, 16, 100, 12, 1, 2, 256, 0, bf16, None), "payload length")
+    _rejects(L.eq_gguf_linear(16, 16, 16, 2 * 144, 12, 1, 2, 256, 0, _native.EQ_DTYPE_F32, None), "bf16")
+    _rejects(L.eq_gguf_linear(16, 18, 16, 2 * 144, 12, 1, 2, 256, 0, bf16, None), "aligned")
+    assert L.eq_gguf_linear(16, 16, 16, 2 * 144, 12, 0, 2, 256, 0, bf16, None) == 0

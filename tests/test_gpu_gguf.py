@@ -171,3 +171,58 @@ def test_errors(cuda):
         G.convert_affine(G.TensorDescriptor("x", [64, 1], ty, 18 * 4), raw[:36])
     with pytest.raises(EreduError, match="group size"):
         G.convert_affine(G.TensorDescriptor("x", [48, 1], ty, 18 * 4), raw)
+
+
+# ----------------------------------------------------------- native linear
+# y = x . W^T straight from the blocks; reference: the oracle's native dense
+# decode (bit-exact with the device's, tested above) multiplied in fp64.
+# Tolerance: the matmul rule |y - y_ref| <= 1e-2 RMS(y_ref) + 1/2 ulp_bf16.
+
+def swap_f16_headers(ty, raw):
+    """Byte-swap every block's f16 d (and Q4_K's dmin), the fields the endian
+    switch applies to."""
+    _, nbytes = ty.block_and_bytes()
+    b = raw.reshape(-1, nbytes).copy()
+    heads = [0, 2] if ty == G.GgmlType.Q4K else [0]
+    for h in heads:
+        b[:, [h, h + 1]] = b[:, [h + 1, h]]
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("ty", [G.GgmlType.Q4K, G.GgmlType.Q8_0])
+@pytest.mark.parametrize("M", [1, 3, 8, 11])
+@pytest.mark.parametrize("endian", [G.Endian.Little, G.Endian.Big])
+def test_native_linear(cuda, ty, M, endian):
+    N, K = 384, 4096 if ty == G.GgmlType.Q4K else 4160  # Q8_0: 130 blocks per row, rows not 16-byte aligned
+    print(f"[case] native linear {ty.name} M={M} N={N} K={K} endian={endian.name}", flush=True)
+    vals, _ = ty.block_and_bytes()
+    raw = synthetic_blocks(int(ty), N * K // vals, seed=M + int(ty))
+    if endian == G.Endian.Big:
+        raw = swap_f16_headers(ty, raw)  # same block values, stored big-endian
+    desc = desc_for(ty, N, K)
+    rng = np.random.default_rng(M)
+    xb = orc.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    y = G.linear(x, desc, dev_u8(raw), endian)
+    torch.cuda.synchronize()
+    W = orc.gguf_dequant_f32(int(ty), raw, int(G.DequantDefinition.Native),
+                             big_endian=endian == G.Endian.Big).reshape(N, K).astype(np.float64)
+    y_ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ W.T
+    got = (host_bits16(y).astype(np.uint32) << 16).view(np.float32)
+    ok, worst, _ = orc.matmul_within_tolerance(got, y_ref, out_is_bf16=True)
+    assert ok, f"max|err|/RMS = {worst:.3e}"
+
+
+def test_native_linear_llama_shapes(cuda):
+    """The decode shapes of a Q4_K checkpoint: q (4096 x 4096) and down (4096 x 14336)."""
+    for N, K in [(4096, 4096), (4096, 14336)]:
+        ty = G.GgmlType.Q4K
+        raw = synthetic_blocks(int(ty), N * K // 256, seed=N + K)
+        xb = orc.f32_to_bf16_bits(np.random.default_rng(K).standard_normal((1, K)).astype(np.float32))
+        x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+        y = G.linear(x, desc_for(ty, N, K), dev_u8(raw))
+        W = orc.gguf_dequant_f32(int(ty), raw, int(G.DequantDefinition.Native)).reshape(N, K).astype(np.float64)
+        y_ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ W.T
+        got = (host_bits16(y).astype(np.uint32) << 16).view(np.float32)
+        ok, worst, _ = orc.matmul_within_tolerance(got, y_ref, out_is_bf16=True)
+        assert ok, f"{N}x{K}: max|err|/RMS = {worst:.3e}"
