@@ -316,10 +316,9 @@ __global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw
 // (safemlx/src/native_quantization.rs:741-772, its CPU stream at :858-913):
 // y[m, n] = sum_k x[m, k] W[n, k], W decoded by the native definition (Q4_K:
 // d sc q - dmin m; Q8_0: d q), accumulated in f32, y in bf16.  No affine
-// expansion: each wave takes one output row n at a time and walks its
-// blocks, its lanes splitting them; the per-group factors are applied to
-// sums of x q and of x (d sc sum(x q) - dmin m sum(x)).  kLinRows activation
-// rows per launch.
+// expansion: the blocks are read once, straight from the payload, and the
+// per-group factors are applied to sums of x q and of x (d sc sum(x q) -
+// dmin m sum(x)).  kLinRows activation rows per launch.
 constexpr int kLinRows = 8;
 
 __device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float* f) {
@@ -331,68 +330,184 @@ __device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float* f) {
     }
 }
 
+// 16-byte streaming load: the weight blocks are read once, so they are not
+// kept in the caches the activation rows are re-read from.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// An empty asm that makes v opaque to the optimizer: values derived from it
+// are recomputed after this point instead of hoisted and kept live, and loads
+// whose address depends on it are not issued before it.
+__device__ __forceinline__ void opaque(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void opaque(int& v) { asm volatile("" : "+v"(v)); }
+
+// a.x b.x + a.y b.y + c over bf16 pairs (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// Two 4-bit codes n0, n1 as the bf16 pair (128 + n0, 128 + n1): 128 = 0x4300
+// has a unit ulp, so OR-ing n into the mantissa is exact.
+constexpr uint32_t kNibbleMagic = 0x43004300u;
+constexpr uint32_t kBf16Ones = 0x3f803f80u;
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
 }
 
-// Q4_K: a lane takes one 16-byte quant chunk (32 codes: 16 of group 2p in
-// the low nibbles, 16 of group 2p + 1 in the high) and its superblock's
-// 16-byte header (d, dmin, the 12 scale/min bytes).  Rows are whole
-// superblocks of 144 = 9 x 16 bytes, so both loads are aligned.
-template <bool BIG>
+// Workgroup layout of the linear kernels: 256 lanes in T teams of S = 256 / T
+// lanes; a team takes kTeamRows consecutive rows and splits their columns into
+// chunks c = s, s + S, ... (s = the lane's index in the team), so the
+// activation values of a chunk are loaded once for all of the team's rows.
+// T is picked on the host so that S is about the number of chunks per row.
+constexpr int kTeamRows = 4;
+
+// A lane's partial sums, one per (activation row m, team row r).  With one
+// activation row (MANY = false) they live in registers; with 2..kLinRows in
+// the workgroup's LDS, one word per lane and pair (consecutive lanes in
+// consecutive words, so no bank conflicts), which lets the loop over
+// activation rows stay rolled with one row's values live at a time.
+template <bool MANY>
+struct LinAcc {
+    float v[kTeamRows];
+    __device__ __forceinline__ LinAcc(float*) {}
+    __device__ __forceinline__ float& at(int, int r) { return v[r]; }
+};
+template <>
+struct LinAcc<true> {
+    float* base;
+    __device__ __forceinline__ LinAcc(float* lds) : base(lds + threadIdx.x) {}
+    __device__ __forceinline__ float& at(int m, int r) { return base[(m * kTeamRows + r) * 256]; }
+};
+
+// Sum of the team's lanes' partials for each (activation row, team row):
+// waves reduce by shuffles, lane 0 of each wave writes red, then one lane per
+// pair adds the team's waves and writes y.  Ends with a barrier so red can be
+// reused.
+template <int T, bool MANY>
+__device__ __forceinline__ void team_reduce(LinAcc<MANY>& acc, float* red, uint16_t* __restrict__ y, int M, int N,
+                                            int row0) {
+    constexpr int S = 256 / T, WPT = S / 64;  // waves per team
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll 1
+    for (int m = 0; m < (MANY ? M : 1); m++) {
+#pragma unroll
+        for (int r = 0; r < kTeamRows; r++) {
+            const float v = wave_sum(acc.at(m, r));
+            if (lane == 0) red[wave * kLinRows * kTeamRows + m * kTeamRows + r] = v;
+        }
+    }
+    __syncthreads();
+    const int per_team = M * kTeamRows;
+    if (tid < T * per_team) {
+        const int team = tid / per_team, j = tid % per_team, m = j / kTeamRows, r = j % kTeamRows;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPT; w++) v += red[(team * WPT + w) * kLinRows * kTeamRows + m * kTeamRows + r];
+        const int n = row0 + team * kTeamRows + r;
+        if (n < N) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(v));
+    }
+    __syncthreads();
+}
+
+// Q4_K: a chunk is one 16-byte run of codes (16 of group 2p in the low
+// nibbles, 16 of group 2p + 1 in the high) plus its superblock's 16-byte
+// header (d, dmin, the 12 scale/min bytes); rows are whole superblocks of
+// 144 = 9 x 16 bytes, so both loads are aligned.  Per row and chunk:
+// d sc sum(x q) - dmin m sum(x) for each group, sum(x) shared by the rows;
+// sum(x q) by bf16 dot products with the codes as 128 + q.  (Chunks of a
+// whole group pair, 32 code bytes, halve the scale decoding but measured
+// slower: fewer waves in flight.)
+template <bool BIG, int T, bool MANY>
 __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
                                                   const uint8_t* __restrict__ raw, int M, int N, int K) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int S = 256 / T;
+    __shared__ float red[4 * kLinRows * kTeamRows];
+    __shared__ float lacc[MANY ? kLinRows * kTeamRows * 256 : 1];
+    const int s = threadIdx.x % S, team = threadIdx.x / S;
     const int nsb = K / 256, nch = nsb * 8;
-    for (int n = blockIdx.x * 4 + wave; n < N; n += gridDim.x * 4) {
-        const uint8_t* row = raw + int64_t(n) * nsb * 144;
-        float acc[kLinRows];
+    const int64_t row_bytes = int64_t(nsb) * 144;
+    for (int row0 = blockIdx.x * T * kTeamRows; row0 < N; row0 += gridDim.x * T * kTeamRows) {
+        const int r0 = row0 + team * kTeamRows;
+        LinAcc<MANY> acc(lacc);
+#pragma unroll 1
+        for (int m = 0; m < (MANY ? M : 1); m++)
 #pragma unroll
-        for (int m = 0; m < kLinRows; m++) acc[m] = 0.f;
-        for (int c = lane; c < nch; c += 64) {
+            for (int r = 0; r < kTeamRows; r++) acc.at(m, r) = 0.f;
+#pragma unroll 1
+        for (int c = s; c < nch; c += S) {
             const int sb = c >> 3, q = c & 7, p = q >> 1;
-            const uint4 hv = *reinterpret_cast<const uint4*>(row + sb * 144);
-            const uint4 qv = *reinterpret_cast<const uint4*>(row + sb * 144 + 16 + q * 16);
-            const uint32_t h[4] = {hv.x, hv.y, hv.z, hv.w};
-            uint32_t sc0, m0, sc1, m1;
-            q4k_scale_min(h, 2 * p, sc0, m0);
-            q4k_scale_min(h, 2 * p + 1, sc1, m1);
-            const float d = f16_bits_to_f32(BIG ? bswap16(h[0] & 0xffffu) : (h[0] & 0xffffu));
-            const float dmin = f16_bits_to_f32(BIG ? bswap16(h[0] >> 16) : (h[0] >> 16));
-            const float ds0 = d * float(sc0), dm0 = dmin * float(m0);
-            const float ds1 = d * float(sc1), dm1 = dmin * float(m1);
-            const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+            uint4 hv[kTeamRows], qv[kTeamRows];
+#pragma unroll
+            for (int r = 0; r < kTeamRows; r++) {
+                const int n = min(r0 + r, N - 1);  // rows past N read row N - 1; their sums are not stored
+                const uint8_t* blk = raw + int64_t(n) * row_bytes + sb * 144;
+                hv[r] = load_stream16(blk);
+                qv[r] = load_stream16(blk + 16 + q * 16);
+            }
+            float ds[kTeamRows][2], dm[kTeamRows][2];
+#pragma unroll
+            for (int r = 0; r < kTeamRows; r++) {
+                const uint32_t h[4] = {hv[r].x, hv[r].y, hv[r].z, hv[r].w};
+                uint32_t sc0, m0, sc1, m1;
+                q4k_scale_min(h, 2 * p, sc0, m0);
+                q4k_scale_min(h, 2 * p + 1, sc1, m1);
+                const float d = f16_bits_to_f32(BIG ? bswap16(h[0] & 0xffffu) : (h[0] & 0xffffu));
+                const float dmin = f16_bits_to_f32(BIG ? bswap16(h[0] >> 16) : (h[0] >> 16));
+                ds[r][0] = d * float(sc0), dm[r][0] = dmin * float(m0);
+                ds[r][1] = d * float(sc1), dm[r][1] = dmin * float(m1);
+            }
             const int k0 = sb * 256 + 2 * p * 32 + (q & 1) * 16;  // group 2p; group 2p + 1 at k0 + 32
+#pragma unroll 1
+            for (int m = 0; m < (MANY ? M : 1); m++) {
+                int kk = k0;
+                if (MANY) {  // the codes are re-extracted per activation row, not kept live
+                    opaque(kk);
 #pragma unroll
-            for (int m = 0; m < kLinRows; m++) {
-                if (m >= M) break;
-                const uint4* xa = reinterpret_cast<const uint4*>(x + int64_t(m) * K + k0);
-                const uint4* xb = reinterpret_cast<const uint4*>(x + int64_t(m) * K + k0 + 32);
-                float fa[16], fb[16];
-                bf16x8_to_f32(xa[0], fa);
-                bf16x8_to_f32(xa[1], fa + 8);
-                bf16x8_to_f32(xb[0], fb);
-                bf16x8_to_f32(xb[1], fb + 8);
-                float sxq0 = 0.f, sx0 = 0.f, sxq1 = 0.f, sx1 = 0.f;
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const uint32_t byte = (qw[j >> 2] >> (8 * (j & 3))) & 0xffu;
-                    sxq0 = fmaf(fa[j], float(byte & 15u), sxq0);
-                    sx0 += fa[j];
-                    sxq1 = fmaf(fb[j], float(byte >> 4), sxq1);
-                    sx1 += fb[j];
+                    for (int r = 0; r < kTeamRows; r++) opaque(qv[r].x), opaque(qv[r].y), opaque(qv[r].z), opaque(qv[r].w);
                 }
-                acc[m] += (ds0 * sxq0 - dm0 * sx0) + (ds1 * sxq1 - dm1 * sx1);
+                // x words: xw[0..7] = group 2p values (x0, x1) .. (x14, x15), xw[8..15] group 2p + 1
+                const uint4* xa = reinterpret_cast<const uint4*>(x + int64_t(m) * K + kk);
+                const uint4* xb = reinterpret_cast<const uint4*>(x + int64_t(m) * K + kk + 32);
+                const uint4 xv[4] = {xa[0], xa[1], xb[0], xb[1]};
+                uint32_t xw[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    xw[4 * i] = xv[i].x, xw[4 * i + 1] = xv[i].y, xw[4 * i + 2] = xv[i].z, xw[4 * i + 3] = xv[i].w;
+                }
+                float sx0 = 0.f, sx1 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    sx0 = dot2_bf16(xw[i], kBf16Ones, sx0);
+                    sx1 = dot2_bf16(xw[8 + i], kBf16Ones, sx1);
+                }
+#pragma unroll
+                for (int r = 0; r < kTeamRows; r++) {
+                    const uint32_t qw[4] = {qv[r].x, qv[r].y, qv[r].z, qv[r].w};
+                    // sum x (128 + q) per group; byte j holds code j of group 2p
+                    // (low nibble) and of group 2p + 1 (high nibble)
+                    float e0 = 0.f, e1 = 0.f;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const uint32_t lo2 = __builtin_amdgcn_perm(0u, qw[t], 0x0c010c00u);  // bytes 0, 1 -> halves
+                        const uint32_t hi2 = __builtin_amdgcn_perm(0u, qw[t], 0x0c030c02u);  // bytes 2, 3 -> halves
+                        e0 = dot2_bf16(xw[2 * t], (lo2 & 0x000f000fu) | kNibbleMagic, e0);
+                        e0 = dot2_bf16(xw[2 * t + 1], (hi2 & 0x000f000fu) | kNibbleMagic, e0);
+                        e1 = dot2_bf16(xw[8 + 2 * t], ((lo2 >> 4) & 0x000f000fu) | kNibbleMagic, e1);
+                        e1 = dot2_bf16(xw[8 + 2 * t + 1], ((hi2 >> 4) & 0x000f000fu) | kNibbleMagic, e1);
+                    }
+                    const float sxq0 = e0 - 128.f * sx0, sxq1 = e1 - 128.f * sx1;
+                    acc.at(m, r) += (ds[r][0] * sxq0 - dm[r][0] * sx0) + (ds[r][1] * sxq1 - dm[r][1] * sx1);
+                }
             }
         }
-#pragma unroll
-        for (int m = 0; m < kLinRows; m++) {
-            if (m >= M) break;
-            const float v = wave_sum(acc[m]);
-            if (lane == 0) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(v));
-        }
+        team_reduce<T, MANY>(acc, red, y, M, N, row0);
     }
 }
 
@@ -430,24 +545,32 @@ __global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, con
                 uint32_t qw[8];
 #pragma unroll
                 for (int i = 0; i < 8; i++) qw[i] = lds_u32(blk + 1 + 2 * i);
+                // codes as q + 128 (sign bit flipped: one unsigned byte convert
+                // each), sum x q = sum x (q + 128) - 128 sum x
+#pragma unroll
+                for (int i = 0; i < 8; i++) qw[i] ^= 0x80808080u;
                 const int k0 = (b0 + lb) * 32;
 #pragma unroll
                 for (int m = 0; m < kLinRows; m++) {
                     if (m >= M) break;
                     const uint4* xa = reinterpret_cast<const uint4*>(x + int64_t(m) * K + k0);
-                    float s = 0.f;
+                    float s = 0.f, sx = 0.f;
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
+                        const uint4 xv = xa[v];
+                        sx = dot2_bf16(xv.x, kBf16Ones, sx);
+                        sx = dot2_bf16(xv.y, kBf16Ones, sx);
+                        sx = dot2_bf16(xv.z, kBf16Ones, sx);
+                        sx = dot2_bf16(xv.w, kBf16Ones, sx);
                         float f[8];
-                        bf16x8_to_f32(xa[v], f);
+                        bf16x8_to_f32(xv, f);
 #pragma unroll
                         for (int j = 0; j < 8; j++) {
                             const int e = v * 8 + j;
-                            const int8_t qb = int8_t((qw[e >> 2] >> (8 * (e & 3))) & 0xffu);
-                            s = fmaf(f[j], float(qb), s);
+                            s = fmaf(f[j], float((qw[e >> 2] >> (8 * (e & 3))) & 0xffu), s);
                         }
                     }
-                    acc[m] = fmaf(d, s, acc[m]);
+                    acc[m] = fmaf(d, s - 128.f * sx, acc[m]);
                 }
             }
         }
@@ -652,19 +775,32 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool big = endian == EQ_ENDIAN_BIG;
-    const int rows_per_wg = 4;
-    const unsigned grid = unsigned(N < 1024 * rows_per_wg ? (N + rows_per_wg - 1) / rows_per_wg : 1024);
+    // Q4_K: 32-code chunks per row -> teams per workgroup; Q8_0: a wave per row
+    const int64_t nch = K / 32;
+    const int teams = nch <= 64 ? 4 : nch <= 128 ? 2 : 1;
+    const int64_t rows_per_wg = ggml_type == EQ_GGML_Q4_K ? int64_t(teams) * kTeamRows : 4;
+    const int64_t wgs = (N + rows_per_wg - 1) / rows_per_wg;
+    const unsigned grid = unsigned(wgs < 8192 ? wgs : 8192);
     for (int64_t m0 = 0; m0 < M; m0 += kLinRows) {
         const int mc = int(M - m0 < kLinRows ? M - m0 : kLinRows);
         uint16_t* yy = static_cast<uint16_t*>(y) + m0 * N;
         const uint16_t* xx = static_cast<const uint16_t*>(x) + m0 * K;
+        const int n = int(N), k = int(K);
+#define EQ_LIN_MANY(KERNEL, T, MANY)                                                        \
+    (big ? KERNEL<true, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k)               \
+         : KERNEL<false, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k))
+#define EQ_LIN_T(KERNEL, T) (mc == 1 ? EQ_LIN_MANY(KERNEL, T, false) : EQ_LIN_MANY(KERNEL, T, true))
+#define EQ_LIN(KERNEL) \
+    (teams == 4 ? EQ_LIN_T(KERNEL, 4) : teams == 2 ? EQ_LIN_T(KERNEL, 2) : EQ_LIN_T(KERNEL, 1))
         if (ggml_type == EQ_GGML_Q4_K) {
-            if (big) q4k_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
-            else q4k_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
+            EQ_LIN(q4k_linear);
         } else {
-            if (big) q8_0_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
-            else q8_0_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, int(N), int(K));
+            if (big) q8_0_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k);
+            else q8_0_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k);
         }
+#undef EQ_LIN_MANY
+#undef EQ_LIN_T
+#undef EQ_LIN
     }
     return check_launch("gguf linear");
 }

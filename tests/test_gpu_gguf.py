@@ -189,11 +189,19 @@ def swap_f16_headers(ty, raw):
     return b.reshape(-1)
 
 
-@pytest.mark.parametrize("ty", [G.GgmlType.Q4K, G.GgmlType.Q8_0])
-@pytest.mark.parametrize("M", [1, 3, 8, 11])
+# (type, K): Q4_K with 64 and 128 16-byte chunks per row (4 and 2 teams per
+# workgroup; the Llama shapes below take 1); Q8_0 rows of 130 and 129 blocks, whose runs are not whole
+# 16-byte words (the 2-byte staging path; the Llama shapes below take the
+# 16-byte one).  N = 390 leaves a partial workgroup of rows; M = 11 takes two
+# launches (8 + 3).
+LINEAR_CASES = [(G.GgmlType.Q4K, 2048), (G.GgmlType.Q4K, 4096), (G.GgmlType.Q8_0, 4160), (G.GgmlType.Q8_0, 4128)]
+
+
+@pytest.mark.parametrize("ty,K", LINEAR_CASES, ids=[f"{t.name}-K{k}" for t, k in LINEAR_CASES])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 11])
 @pytest.mark.parametrize("endian", [G.Endian.Little, G.Endian.Big])
-def test_native_linear(cuda, ty, M, endian):
-    N, K = 384, 4096 if ty == G.GgmlType.Q4K else 4160  # Q8_0: 130 blocks per row, rows not 16-byte aligned
+def test_native_linear(cuda, ty, K, M, endian):
+    N = 390
     print(f"[case] native linear {ty.name} M={M} N={N} K={K} endian={endian.name}", flush=True)
     vals, _ = ty.block_and_bytes()
     raw = synthetic_blocks(int(ty), N * K // vals, seed=M + int(ty))
@@ -213,11 +221,12 @@ def test_native_linear(cuda, ty, M, endian):
     assert ok, f"max|err|/RMS = {worst:.3e}"
 
 
-def test_native_linear_llama_shapes(cuda):
-    """The decode shapes of a Q4_K checkpoint: q (4096 x 4096) and down (4096 x 14336)."""
+@pytest.mark.parametrize("ty", [G.GgmlType.Q4K, G.GgmlType.Q8_0])
+def test_native_linear_llama_shapes(cuda, ty):
+    """Decode shapes of a Llama-3-8B checkpoint: q (4096 x 4096), down (4096 x 14336; one team per workgroup)."""
+    vals, _ = ty.block_and_bytes()
     for N, K in [(4096, 4096), (4096, 14336)]:
-        ty = G.GgmlType.Q4K
-        raw = synthetic_blocks(int(ty), N * K // 256, seed=N + K)
+        raw = synthetic_blocks(int(ty), N * K // vals, seed=N + K)
         xb = orc.f32_to_bf16_bits(np.random.default_rng(K).standard_normal((1, K)).astype(np.float32))
         x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
         y = G.linear(x, desc_for(ty, N, K), dev_u8(raw))
