@@ -251,6 +251,44 @@ def bench_gguf(steps, warmup):
     return out
 
 
+def bench_gather(steps, warmup):
+    """Routed-expert decode through gather_qmm (the eredu MoE call, x [routes,
+    1, K], lhs = arange, rhs = expert of each route): a Mixtral-8x7B-shaped
+    bank of 8 experts, 4-bit g64 bf16, 2 routes per token, for the gate/up
+    shape (14336 x 4096) and the down shape (4096 x 14336); a replay runs 4
+    tokens over disjoint expert pairs.  Bytes per call = the two selected
+    experts' codes + scales + biases + x + y."""
+    import torch
+
+    n = _lib()
+    E, routes, gs, bits = 8, 2, GS, BITS
+    out = {}
+    for label, N, K in (("gate_up_14336x4096", 14336, 4096), ("down_4096x14336", 4096, 14336)):
+        w = torch.randint(-2**31, 2**31 - 1, (E, N, K * bits // 32), dtype=torch.int32, device="cuda")
+        s = (0.01 * torch.rand((E, N, K // gs), device="cuda")).to(torch.bfloat16)
+        b = (-0.08 * torch.rand((E, N, K // gs), device="cuda")).to(torch.bfloat16)
+        x = torch.randn((routes, 1, K), device="cuda").to(torch.bfloat16)
+        y = torch.empty((routes, 1, N), dtype=torch.bfloat16, device="cuda")
+        lhs = torch.arange(routes, dtype=torch.int32, device="cuda")
+        # four tokens' routes per replay, each pair on experts not read by the others
+        rhs = [torch.tensor([2 * i + 1, 2 * i], dtype=torch.int32, device="cuda") for i in range(E // 2)]
+
+        def fn(st):
+            for r in rhs:
+                n.check(n.lib().eq_gather_qmm(y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(),
+                                              lhs.data_ptr(), r.data_ptr(), routes, routes, E, 1, N, K, True, gs,
+                                              bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, True, st))
+
+        ms = Timer(fn).ms_per_replay(max(steps // 4, 20), warmup) / len(rhs)
+        nbytes = routes * (N * K * bits // 8 + 2 * N * (K // gs) * 2) + routes * (K + N) * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[label] = {"us": round(ms * 1e3, 2), "MB": round(nbytes / 1e6, 2), "GB/s": round(gbs, 1),
+                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del w, s, b
+        torch.cuda.empty_cache()
+    return out
+
+
 VOCAB, N_HEADS, N_KV_HEADS, CACHE_TOKENS = 128256, 32, 8, 1024
 
 
@@ -385,6 +423,8 @@ def main():
                     help="only the prefill qmm sweep, one JSON object of its figures (for kernel-trace profiles)")
     ap.add_argument("--gguf-only", action="store_true",
                     help="only the GGUF dequant/convert sweep, one JSON object of its figures")
+    ap.add_argument("--gather-only", action="store_true",
+                    help="only the routed-expert gather_qmm decode figures, one JSON object")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the full decode step of configs[4], one JSON object of its figures")
     args = ap.parse_args()
@@ -398,7 +438,7 @@ def main():
 
     _lib().lib()
     torch.cuda.set_device(0)
-    if args.prefill_only or args.gguf_only:
+    if args.prefill_only or args.gguf_only or args.gather_only:
         out = {}
         if args.prefill_only:
             log("[bench] qmm prefill")
@@ -406,6 +446,9 @@ def main():
         if args.gguf_only:
             log("[bench] gguf")
             out["gguf"] = bench_gguf(args.steps, args.warmup)
+        if args.gather_only:
+            log("[bench] gather_qmm routed-expert decode")
+            out["gather_qmm"] = bench_gather(args.steps, args.warmup)
         print(json.dumps(out), flush=True)
         return
     gen = torch.Generator(device="cuda").manual_seed(0)
@@ -452,6 +495,8 @@ def main():
         detail["qmm"] = bench_qmm(args.steps, args.warmup)
         log("[bench] gguf")
         detail["gguf"] = bench_gguf(args.steps, args.warmup)
+        log("[bench] gather_qmm routed-expert decode")
+        detail["gather_qmm"] = bench_gather(args.steps, args.warmup)
 
     per_launch_bytes = nbytes / launches
     avg_launch_us = ms * 1e3 / launches

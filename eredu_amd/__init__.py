@@ -18,6 +18,8 @@ from .quantization import (
     QuantizedLinear,
     dequantize,
     dequantize_with_mode,
+    gather_qmm,
+    gather_qmm_with_mode,
     quantized_matmul,
     quantized_matmul_batched,
     quantized_matmul_with_mode,
@@ -34,6 +36,8 @@ __all__ = [
     "QuantizedLinear",
     "dequantize",
     "dequantize_with_mode",
+    "gather_qmm",
+    "gather_qmm_with_mode",
     "quantized_matmul",
     "quantized_matmul_batched",
     "quantized_matmul_with_mode",

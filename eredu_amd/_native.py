@@ -25,6 +25,8 @@ SIGNATURES = {
     "eq_gguf_convert_affine": ([_vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i32, _vp], _i32),
     "eq_gguf_dequantize": ([_vp, _vp, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _vp], _i32),
     "eq_gguf_linear": ([_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i32, _i32, _vp], _i32),
+    "eq_gather_qmm": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _b, _i32, _i32,
+                       ctypes.c_char_p, _i32, _i32, _b, _vp], _i32),
     "eq_quantize": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, ctypes.c_char_p, _i32, _vp], _i32),
     "eq_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _i32, _vp], _i32),
     "eq_rope_attention_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, ctypes.c_float,

@@ -38,51 +38,20 @@ namespace {
 
 // ------------------------------------------------------------ general kernels
 
-// LSB-first code c of a packed row (bits in {2, 4, 8} never straddle words).
-template <int BITS>
-__device__ __forceinline__ uint32_t code_at(const uint32_t* row, int64_t c) {
-    constexpr int PACK = 32 / BITS;
-    return (row[c / PACK] >> ((c % PACK) * BITS)) & ((1u << BITS) - 1u);
-}
-
-constexpr int kGenRowsPerWG = 4;
-constexpr int kGenMChunk = 8;
-
-// transpose = true: one wave per output feature n, lanes stride over K;
-// activations in chunks of 8 rows.  f32 arithmetic throughout.
+// transpose = true: one wave per output feature n (qmm_t_rows), activations
+// in chunks of 8 rows.
 template <int BITS, typename XT, typename ST>
 __global__ __launch_bounds__(64 * kGenRowsPerWG) void qmm_t_general(
     typename XT::storage* __restrict__ y, const typename XT::storage* __restrict__ x,
     const uint32_t* __restrict__ w, const typename ST::storage* __restrict__ s,
     const typename ST::storage* __restrict__ b, int64_t M, int64_t N, int64_t K, int gs) {
-    const int lane = threadIdx.x & 63;
     const int64_t n = int64_t(blockIdx.x) * kGenRowsPerWG + (threadIdx.x >> 6);
     if (n >= N) return;
-    const int64_t G = K / gs;
-    const uint32_t* row = w + n * (K * BITS / 32);
-    for (int64_t m0 = 0; m0 < M; m0 += kGenMChunk) {
-        float acc[kGenMChunk];
-#pragma unroll
-        for (int i = 0; i < kGenMChunk; i++) acc[i] = 0.f;
-        for (int64_t k = lane; k < K; k += 64) {
-            const int64_t g = k / gs;
-            const float wv = load_param<ST>(s, n * G + g) * float(code_at<BITS>(row, k)) +
-                             (b ? load_param<ST>(b, n * G + g) : 0.f);
-#pragma unroll
-            for (int i = 0; i < kGenMChunk; i++)
-                if (m0 + i < M) acc[i] = fmaf(load_param<XT>(x, (m0 + i) * K + k), wv, acc[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < kGenMChunk; i++) {
-            float v = acc[i];
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0 && m0 + i < M) store_out<XT>(y, (m0 + i) * N + n, v);
-        }
-    }
+    qmm_t_rows<BITS, XT, ST>(y, x, w, s, b, M, N, K, gs, n, threadIdx.x & 63);
 }
 
 // transpose = false: W is [K, N] packed along N.  One thread per output
-// column n and chunk of 8 activation rows, walking K.
+// column n and chunk of 8 activation rows (qmm_n_cols).
 template <int BITS, typename XT, typename ST>
 __global__ __launch_bounds__(256) void qmm_n_general(typename XT::storage* __restrict__ y,
                                                      const typename XT::storage* __restrict__ x,
@@ -91,23 +60,8 @@ __global__ __launch_bounds__(256) void qmm_n_general(typename XT::storage* __res
                                                      const typename ST::storage* __restrict__ b, int64_t M,
                                                      int64_t N, int64_t K, int gs) {
     const int64_t n = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t m0 = int64_t(blockIdx.y) * kGenMChunk;
     if (n >= N) return;
-    const int64_t G = N / gs;
-    float acc[kGenMChunk];
-#pragma unroll
-    for (int i = 0; i < kGenMChunk; i++) acc[i] = 0.f;
-    for (int64_t k = 0; k < K; k++) {
-        const uint32_t* row = w + k * (N * BITS / 32);
-        const float wv = load_param<ST>(s, k * G + n / gs) * float(code_at<BITS>(row, n)) +
-                         (b ? load_param<ST>(b, k * G + n / gs) : 0.f);
-#pragma unroll
-        for (int i = 0; i < kGenMChunk; i++)
-            if (m0 + i < M) acc[i] = fmaf(load_param<XT>(x, (m0 + i) * K + k), wv, acc[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < kGenMChunk; i++)
-        if (m0 + i < M) store_out<XT>(y, (m0 + i) * N + n, acc[i]);
+    qmm_n_cols<BITS, XT, ST>(y, x, w, s, b, M, N, K, gs, n, int64_t(blockIdx.y) * kGenMChunk);
 }
 
 // out[r, c] = f32(s) * q + f32(b), one rounding each (convert.rs:81-101).
@@ -136,52 +90,6 @@ __global__ __launch_bounds__(256) void dequant_kernel(typename OT::storage* __re
 }
 
 // --------------------------------------------------------------- dispatch
-
-template <typename F>
-bool with_dtype(int dt, F&& f) {
-    switch (dt) {
-    case EQ_DTYPE_F32: f(F32T{}); return true;
-    case EQ_DTYPE_F16: f(F16T{}); return true;
-    case EQ_DTYPE_BF16: f(BF16T{}); return true;
-    default: return false;
-    }
-}
-
-template <typename F>
-bool with_bits(int bits, F&& f) {
-    switch (bits) {
-    case 2: f(std::integral_constant<int, 2>{}); return true;
-    case 4: f(std::integral_constant<int, 4>{}); return true;
-    case 8: f(std::integral_constant<int, 8>{}); return true;
-    default: return false;
-    }
-}
-
-bool valid_dtype(int d) { return d == EQ_DTYPE_F32 || d == EQ_DTYPE_F16 || d == EQ_DTYPE_BF16; }
-
-int check_mode(const char* mode) {
-    if (mode == nullptr || std::strcmp(mode, "affine") == 0) return 0;
-    if (std::strcmp(mode, "mxfp4") == 0) {
-        set_error("quantization mode 'mxfp4' is not implemented on this device path (affine only)");
-        return 1;
-    }
-    set_error(std::string("invalid quantization mode '") + mode + "'");
-    return 1;
-}
-
-// Group size / bits rules of the affine contract (eredu-checkpoint/src/lib.rs:69-123,
-// safemlx/src/ops/quantization.rs:62-64); this library implements gs 32/64/128, bits 2/4/8.
-int check_gs_bits(int group_size, int bits) {
-    if (bits != 2 && bits != 4 && bits != 8) {
-        set_error("bits must be 2, 4 or 8 on this device path, got " + std::to_string(bits));
-        return 1;
-    }
-    if (group_size != 32 && group_size != 64 && group_size != 128) {
-        set_error("group_size must be 32, 64 or 128, got " + std::to_string(group_size));
-        return 1;
-    }
-    return 0;
-}
 
 }  // namespace
 }  // namespace eq

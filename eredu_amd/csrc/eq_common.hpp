@@ -4,7 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "../../include/eredu_hip.h"
 
@@ -153,6 +155,54 @@ struct BF16T { typedef uint16_t storage; };
 struct F16T { typedef uint16_t storage; };
 struct F32T { typedef float storage; };
 
+// --------------------------------------------------------------- dispatch
+
+template <typename F>
+inline bool with_dtype(int dt, F&& f) {
+    switch (dt) {
+    case EQ_DTYPE_F32: f(F32T{}); return true;
+    case EQ_DTYPE_F16: f(F16T{}); return true;
+    case EQ_DTYPE_BF16: f(BF16T{}); return true;
+    default: return false;
+    }
+}
+
+template <typename F>
+inline bool with_bits(int bits, F&& f) {
+    switch (bits) {
+    case 2: f(std::integral_constant<int, 2>{}); return true;
+    case 4: f(std::integral_constant<int, 4>{}); return true;
+    case 8: f(std::integral_constant<int, 8>{}); return true;
+    default: return false;
+    }
+}
+
+inline bool valid_dtype(int d) { return d == EQ_DTYPE_F32 || d == EQ_DTYPE_F16 || d == EQ_DTYPE_BF16; }
+
+inline int check_mode(const char* mode) {
+    if (mode == nullptr || std::strcmp(mode, "affine") == 0) return 0;
+    if (std::strcmp(mode, "mxfp4") == 0) {
+        set_error("quantization mode 'mxfp4' is not implemented on this device path (affine only)");
+        return 1;
+    }
+    set_error(std::string("invalid quantization mode '") + mode + "'");
+    return 1;
+}
+
+// Group size / bits rules of the affine contract (eredu-checkpoint/src/lib.rs:69-123,
+// safemlx/src/ops/quantization.rs:62-64); this library implements gs 32/64/128, bits 2/4/8.
+inline int check_gs_bits(int group_size, int bits) {
+    if (bits != 2 && bits != 4 && bits != 8) {
+        set_error("bits must be 2, 4 or 8 on this device path, got " + std::to_string(bits));
+        return 1;
+    }
+    if (group_size != 32 && group_size != 64 && group_size != 128) {
+        set_error("group_size must be 32, 64 or 128, got " + std::to_string(group_size));
+        return 1;
+    }
+    return 0;
+}
+
 template <typename T> __device__ __forceinline__ float load_param(const typename T::storage* p, int64_t i);
 template <> __device__ __forceinline__ float load_param<BF16T>(const uint16_t* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
 template <> __device__ __forceinline__ float load_param<F16T>(const uint16_t* p, int64_t i) { return f16_bits_to_f32(p[i]); }
@@ -162,5 +212,111 @@ template <typename T> __device__ __forceinline__ void store_out(typename T::stor
 template <> __device__ __forceinline__ void store_out<BF16T>(uint16_t* p, int64_t i, float v) { p[i] = static_cast<uint16_t>(f32_to_bf16_bits(v)); }
 template <> __device__ __forceinline__ void store_out<F16T>(uint16_t* p, int64_t i, float v) { p[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
 template <> __device__ __forceinline__ void store_out<F32T>(float* p, int64_t i, float v) { p[i] = v; }
+
+// ------------------------------------------------------ small vector helpers
+
+// 16-byte streaming load: the weight blocks are read once, so they are not
+// kept in the caches the activation rows are re-read from.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float* f) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(&v);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = bf16_bits_to_f32(p[i] & 0xffffu);
+        f[2 * i + 1] = bf16_bits_to_f32(p[i] >> 16);
+    }
+}
+
+// a.x b.x + a.y b.y + c over bf16 pairs (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// Two 4-bit codes n0, n1 as the bf16 pair (128 + n0, 128 + n1): 128 = 0x4300
+// has a unit ulp, so OR-ing n into the mantissa is exact.
+constexpr uint32_t kNibbleMagic = 0x43004300u;
+constexpr uint32_t kBf16Ones = 0x3f803f80u;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+
+// ------------------------------------------------------------ general bodies
+
+// LSB-first code c of a packed row (bits in {2, 4, 8} never straddle words).
+template <int BITS>
+__device__ __forceinline__ uint32_t code_at(const uint32_t* row, int64_t c) {
+    constexpr int PACK = 32 / BITS;
+    return (row[c / PACK] >> ((c % PACK) * BITS)) & ((1u << BITS) - 1u);
+}
+
+constexpr int kGenRowsPerWG = 4;
+constexpr int kGenMChunk = 8;
+
+// transpose = true, output feature n by one wave (lane = 0..63): lanes stride
+// over K, activations in chunks of kGenMChunk rows, f32 arithmetic
+// throughout, y[m, n] written by lane 0.
+template <int BITS, typename XT, typename ST>
+__device__ __forceinline__ void qmm_t_rows(typename XT::storage* __restrict__ y,
+                                           const typename XT::storage* __restrict__ x, const uint32_t* __restrict__ w,
+                                           const typename ST::storage* __restrict__ s,
+                                           const typename ST::storage* __restrict__ b, int64_t M, int64_t N,
+                                           int64_t K, int gs, int64_t n, int lane) {
+    const int64_t G = K / gs;
+    const uint32_t* row = w + n * (K * BITS / 32);
+    for (int64_t m0 = 0; m0 < M; m0 += kGenMChunk) {
+        float acc[kGenMChunk];
+#pragma unroll
+        for (int i = 0; i < kGenMChunk; i++) acc[i] = 0.f;
+        for (int64_t k = lane; k < K; k += 64) {
+            const int64_t g = k / gs;
+            const float wv = load_param<ST>(s, n * G + g) * float(code_at<BITS>(row, k)) +
+                             (b ? load_param<ST>(b, n * G + g) : 0.f);
+#pragma unroll
+            for (int i = 0; i < kGenMChunk; i++)
+                if (m0 + i < M) acc[i] = fmaf(load_param<XT>(x, (m0 + i) * K + k), wv, acc[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kGenMChunk; i++) {
+            float v = acc[i];
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0 && m0 + i < M) store_out<XT>(y, (m0 + i) * N + n, v);
+        }
+    }
+}
+
+// transpose = false (W [K, N] packed along N): output column n for the
+// activation rows m0 .. m0 + kGenMChunk - 1, walking K.
+template <int BITS, typename XT, typename ST>
+__device__ __forceinline__ void qmm_n_cols(typename XT::storage* __restrict__ y,
+                                           const typename XT::storage* __restrict__ x, const uint32_t* __restrict__ w,
+                                           const typename ST::storage* __restrict__ s,
+                                           const typename ST::storage* __restrict__ b, int64_t M, int64_t N,
+                                           int64_t K, int gs, int64_t n, int64_t m0) {
+    const int64_t G = N / gs;
+    float acc[kGenMChunk];
+#pragma unroll
+    for (int i = 0; i < kGenMChunk; i++) acc[i] = 0.f;
+    for (int64_t k = 0; k < K; k++) {
+        const uint32_t* row = w + k * (N * BITS / 32);
+        const float wv = load_param<ST>(s, k * G + n / gs) * float(code_at<BITS>(row, n)) +
+                         (b ? load_param<ST>(b, k * G + n / gs) : 0.f);
+#pragma unroll
+        for (int i = 0; i < kGenMChunk; i++)
+            if (m0 + i < M) acc[i] = fmaf(load_param<XT>(x, (m0 + i) * K + k), wv, acc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kGenMChunk; i++)
+        if (m0 + i < M) store_out<XT>(y, (m0 + i) * N + n, acc[i]);
+}
 
 }  // namespace eq

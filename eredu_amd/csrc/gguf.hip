@@ -321,45 +321,12 @@ __global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw
 // dmin m sum(x)).  kLinRows activation rows per launch.
 constexpr int kLinRows = 8;
 
-__device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float* f) {
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(&v);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        f[2 * i] = bf16_bits_to_f32(p[i] & 0xffffu);
-        f[2 * i + 1] = bf16_bits_to_f32(p[i] >> 16);
-    }
-}
-
-// 16-byte streaming load: the weight blocks are read once, so they are not
-// kept in the caches the activation rows are re-read from.
-__device__ __forceinline__ uint4 load_stream16(const void* p) {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 // An empty asm that makes v opaque to the optimizer: values derived from it
 // are recomputed after this point instead of hoisted and kept live, and loads
 // whose address depends on it are not issued before it.
 __device__ __forceinline__ void opaque(uint32_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void opaque(int& v) { asm volatile("" : "+v"(v)); }
-
-// a.x b.x + a.y b.y + c over bf16 pairs (v_dot2c_f32_bf16).
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-}
-
-// Two 4-bit codes n0, n1 as the bf16 pair (128 + n0, 128 + n1): 128 = 0x4300
-// has a unit ulp, so OR-ing n into the mantissa is exact.
-constexpr uint32_t kNibbleMagic = 0x43004300u;
-constexpr uint32_t kBf16Ones = 0x3f803f80u;
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
 
 // Workgroup layout of the linear kernels: 256 lanes in T teams of S = 256 / T
 // lanes; a team takes kTeamRows consecutive rows and splits their columns into

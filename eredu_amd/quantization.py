@@ -202,6 +202,101 @@ def quantized_matmul_batched(
     return [y.reshape(*lead, N) for y, lead, N in outs]
 
 
+def gather_qmm_with_mode(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    biases: Optional[torch.Tensor],
+    lhs_indices: Optional[torch.Tensor],
+    rhs_indices: Optional[torch.Tensor],
+    transpose: bool,
+    group_size: int,
+    bits: int,
+    sorted_indices: bool,
+    mode: QuantizationMode = QuantizationMode.Affine,
+) -> torch.Tensor:
+    """Gathered quantized matmul (safemlx/src/ops/quantization.rs:338-379; C ABI:
+    eq_gather_qmm), the routed-expert primitive of
+    eredu/src/backend/mlx/nn/moe.rs:121-139.
+
+    x [..., M, K]; w [..., N, K*bits/32] (transpose) or [..., K, N*bits/32];
+    scales/biases [..., rows, packed_dim/gs].  lhs_indices index x's batch
+    elements (flattened), rhs_indices w's; an absent array is arange over
+    that operand's batch shape.  The two broadcast to the output batch shape;
+    y [*batch, M, N] with y[b] = quantized_matmul(x[lhs[b]], w[rhs[b]]).
+    The indices are read on the device: an out-of-range index gives zero
+    output rows.  sorted_indices is a hint and does not change the result.
+    """
+    mode.validate(group_size, bits)
+    if mode is not QuantizationMode.Affine:
+        raise EreduError("only affine quantization is implemented on the device path")
+    _require_device(x, w, scales, biases, lhs_indices, rhs_indices)
+    _words(w)
+    if x.dim() < 2 or w.dim() < 2 or scales.dim() != w.dim():
+        raise EreduError("x and w need at least 2 dimensions, scales as many as w")
+    xb_shape, wb_shape = tuple(x.shape[:-2]), tuple(w.shape[:-2])
+    if tuple(scales.shape[:-2]) != wb_shape or (biases is not None and tuple(biases.shape[:-2]) != wb_shape):
+        raise EreduError("scales and biases must have w's batch dimensions")
+    x_batches = 1
+    for d in xb_shape:
+        x_batches *= d
+    w_batches = 1
+    for d in wb_shape:
+        w_batches *= d
+    w2 = w.reshape(-1, *w.shape[-2:])
+    s2 = scales.reshape(-1, *scales.shape[-2:])
+    b2 = biases.reshape(-1, *biases.shape[-2:]) if biases is not None else None
+    N, K = _check_operands(x, w2[0], s2[0], b2[0] if b2 is not None else None, transpose, group_size, bits)
+    M = x.shape[-2]
+    dev = x.device
+    if lhs_indices is None:
+        lhs_indices = torch.arange(x_batches, device=dev, dtype=torch.int32).reshape(xb_shape)
+    if rhs_indices is None:
+        rhs_indices = torch.arange(w_batches, device=dev, dtype=torch.int32).reshape(wb_shape)
+    for name, idx in (("lhs_indices", lhs_indices), ("rhs_indices", rhs_indices)):
+        if idx.dtype.is_floating_point or idx.dtype.is_complex or idx.dtype == torch.bool:
+            raise EreduError(f"{name} must be an integer array, got {idx.dtype}")
+    try:
+        batch_shape = torch.broadcast_shapes(lhs_indices.shape, rhs_indices.shape)
+    except RuntimeError as e:
+        raise EreduError(f"lhs_indices {tuple(lhs_indices.shape)} and rhs_indices "
+                         f"{tuple(rhs_indices.shape)} do not broadcast") from e
+    lhs = lhs_indices.to(torch.int32).broadcast_to(batch_shape).contiguous().reshape(-1)
+    rhs = rhs_indices.to(torch.int32).broadcast_to(batch_shape).contiguous().reshape(-1)
+    batch = lhs.numel()
+    x3 = x.reshape(x_batches, M, K).contiguous()
+    w2, s2 = w2.contiguous(), s2.contiguous()
+    b2 = b2.contiguous() if b2 is not None else None
+    y = torch.empty((batch, M, N), dtype=x.dtype, device=dev)
+    check(
+        _native.lib().eq_gather_qmm(
+            y.data_ptr(), x3.data_ptr(), w2.data_ptr(), s2.data_ptr(), b2.data_ptr() if b2 is not None else None,
+            lhs.data_ptr(), rhs.data_ptr(), batch, x_batches, w_batches, M, N, K, bool(transpose),
+            int(group_size), int(bits), mode.value.encode(), _dtype_code(x, "x"), _dtype_code(scales, "scales"),
+            bool(sorted_indices), _stream(),
+        )
+    )
+    return y.reshape(*batch_shape, M, N)
+
+
+def gather_qmm(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    biases: Optional[torch.Tensor] = None,
+    lhs_indices: Optional[torch.Tensor] = None,
+    rhs_indices: Optional[torch.Tensor] = None,
+    transpose: bool = True,
+    group_size: int = DEFAULT_GROUP_SIZE,
+    bits: int = DEFAULT_BITS,
+    sorted_indices: bool = False,
+) -> torch.Tensor:
+    """gather_qmm with safemlx's defaults (transpose=True, gs 64, bits 4,
+    affine; safemlx/src/ops/quantization.rs:297-334)."""
+    return gather_qmm_with_mode(x, w, scales, biases, lhs_indices, rhs_indices, transpose, group_size, bits,
+                                sorted_indices, QuantizationMode.Affine)
+
+
 def quantize_with_mode(
     w: torch.Tensor,
     group_size: int,

@@ -145,6 +145,25 @@ int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, 
                    int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream);
 
 /*
+ * Gathered quantized matmul (routed experts): for b in [0, batch),
+ *   y[b] = x[lhs[b]] . dequant(w[rhs[b]])^T   (transpose)
+ *   y[b] = x[lhs[b]] . dequant(w[rhs[b]])     (!transpose)
+ * x [x_batches, M, K], w / scales / biases [w_batches, N, K*bits/32 | K/gs]
+ * (transpose) or [w_batches, K, N*bits/32 | N/gs], y [batch, M, N].  The int32
+ * index arrays live on the device; a null lhs_indices means b (x_batches ==
+ * batch) or 0 (x_batches == 1), likewise rhs_indices.  A batch whose index is
+ * out of range gets zero output rows.  sorted_indices is an ordering hint and
+ * does not change the result.  Replaces mlx_gather_qmm
+ * (safemlx-sys/src/bindings.rs:3309) under safemlx::ops::gather_qmm_with_mode
+ * (safemlx/src/ops/quantization.rs:298-379), as called by eredu's routed
+ * experts (eredu/src/backend/mlx/nn/moe.rs:121-139).
+ */
+int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                  const int32_t* lhs_indices, const int32_t* rhs_indices, int64_t batch, int64_t x_batches,
+                  int64_t w_batches, int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
+                  const char* mode, int x_dtype, int scale_dtype, bool sorted_indices, eq_stream_t stream);
+
+/*
  * Affine group quantization of w [rows, cols] (dtype: f32, f16 or bf16) along
  * its rows: codes [rows, cols * bits / 32] u32 packed LSB-first, scales and
  * biases [rows, cols / group_size] in w's dtype, with MLX's affine rule --

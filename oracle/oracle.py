@@ -10,8 +10,11 @@ Two layers:
   byte-level restatement of ``eredu-gguf/src/convert.rs`` and the native
   decoders of ``safemlx/src/native_quantization.rs``, f16/bf16 rounding, an
   input quantizer and the restated MLX CPU ``_qmm_t`` loop (CPU baseline).
-* numpy: the fp64 closed form of ``quantized_matmul`` (the matmul oracle) and
-  bf16 helpers.
+* numpy: the fp64 closed form of ``quantized_matmul`` (the matmul oracle),
+  ``gather_qmm_f64`` (index broadcasting around it; pinned in
+  tests/test_oracle_gather.py by a closed form: expert e dequantizing to the
+  constant e + 1 gives y[b] = (rhs[b] + 1) * sum(x[lhs[b]]), which a swapped,
+  mis-broadcast or dropped index fails) and bf16 helpers.
 
 Parity status per function is listed in the header of ``eq_oracle.c``; every
 function here that is not a thin wrapper names what pins it.
@@ -190,6 +193,31 @@ def quantized_matmul_f64(x, x_dtype, w, scales, biases, scale_dtype, transpose, 
         return x64 @ W.T
     W = affine_dequant_f64(w, scales, biases, scale_dtype, K, N, group_size, bits)
     return x64 @ W
+
+
+def gather_qmm_f64(x, x_dtype, w, scales, biases, scale_dtype, lhs, rhs, transpose, group_size, bits, N, K):
+    """fp64 gather_qmm (MLX's gather_qmm under safemlx::ops::gather_qmm_with_mode,
+    safemlx/src/ops/quantization.rs:298-379): x [Bx, M, K] (stored bits or
+    f32), w / scales / biases [Bw, ...]; lhs and rhs (integer arrays, or None
+    for arange over x's / w's batches) broadcast together to the output batch
+    shape; y[b] = quantized_matmul(x[lhs[b]], w[rhs[b]]).  Returns f64
+    [*batch, M, N]; a batch with an index out of range is all zeros (the
+    device path's rule; MLX leaves it undefined)."""
+    x = np.asarray(x)
+    Bx, Bw = x.shape[0], np.asarray(w).shape[0]
+    lhs = np.arange(Bx) if lhs is None else np.asarray(lhs)
+    rhs = np.arange(Bw) if rhs is None else np.asarray(rhs)
+    shape = np.broadcast_shapes(lhs.shape, rhs.shape)
+    li = np.broadcast_to(lhs, shape).reshape(-1)
+    ri = np.broadcast_to(rhs, shape).reshape(-1)
+    M = x.shape[1]
+    y = np.zeros((li.size, M, N))
+    for b, (i, e) in enumerate(zip(li, ri)):
+        if not (0 <= i < Bx and 0 <= e < Bw):
+            continue
+        y[b] = quantized_matmul_f64(x[i], x_dtype, w[e], scales[e], None if biases is None else biases[e],
+                                    scale_dtype, transpose, group_size, bits, N, K)
+    return y.reshape(*shape, M, N)
 
 
 def qmm_t_f32(x, x_dtype, w, scales, biases, scale_dtype, M, N, K, gs, bits, threads=1) -> np.ndarray:

@@ -27,7 +27,7 @@ def test_header_declares_the_boundary():
         ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
          "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
-         "eq_gguf_linear"]
+         "eq_gguf_linear", "eq_gather_qmm"]
     )
 
 
@@ -198,3 +198,30 @@ def test_gguf_linear_rejects_bad_arguments():
     _rejects(L.eq_gguf_linear(16, 16, 16, 2 * 144, 12, 1, 2, 256, 0, _native.EQ_DTYPE_F32, None), "bf16")
     _rejects(L.eq_gguf_linear(16, 18, 16, 2 * 144, 12, 1, 2, 256, 0, bf16, None), "aligned")
     assert L.eq_gguf_linear(16, 16, 16, 2 * 144, 12, 0, 2, 256, 0, bf16, None) == 0
+
+
+def test_gather_qmm_rejects_bad_arguments():
+    bf16 = _native.EQ_DTYPE_BF16
+    # (y, x, w, scales, biases, lhs, rhs, batch, x_batches, w_batches, M, N, K, transpose, gs, bits, mode,
+    #  x_dtype, scale_dtype, sorted, stream)
+    args = [16, 16, 16, 16, None, 16, 16, 4, 4, 8, 1, 32, 128, True, 64, 4, b"affine", bf16, bf16, False, None]
+
+    def call(**kw):
+        a = list(args)
+        names = ["y", "x", "w", "s", "b", "lhs", "rhs", "batch", "xb", "wb", "M", "N", "K", "t", "gs", "bits",
+                 "mode", "xd", "sd", "sorted", "st"]
+        for k, v in kw.items():
+            a[names.index(k)] = v
+        return L.eq_gather_qmm(*a)
+
+    _rejects(call(gs=48), "group_size")
+    _rejects(call(bits=3), "bits")
+    _rejects(call(mode=b"mxfp4"), "mxfp4")
+    _rejects(call(xd=7), "dtype")
+    _rejects(call(K=96), "divisible")
+    _rejects(call(wb=0), "w_batches")
+    _rejects(call(lhs=None, xb=3), "lhs_indices")     # 3 x batches for 4 outputs, no indices
+    _rejects(call(rhs=None, wb=8), "rhs_indices")
+    _rejects(call(w=None), "null")
+    _rejects(call(t=False, N=128, M=8 * 65535 + 1), "rows per batch")
+    assert call(batch=0) == 0 and call(M=0) == 0      # nothing to do, nothing launched
