@@ -89,10 +89,24 @@ def quantized_matmul_with_mode(
     transpose=True : w [N, K*bits/32], scales/biases [N, K/gs], y = x @ W^T.
     transpose=False: w [K, N*bits/32], scales/biases [K, N/gs], y = x @ W.
     x [..., K] -> y [..., N] in x's dtype.
+
+    With batch dimensions on w (w [..., rows, cols], as the quantized KV
+    attention of eredu/src/backend/mlx/nn/tensor.rs:76-150 passes them), x is
+    [..., M, K] and the two batch shapes broadcast: y[b] = x[b] @ W[b] (MLX's
+    rule), computed by eq_gather_qmm with the broadcast batch indices.
     """
     mode.validate(group_size, bits)
     if mode is not QuantizationMode.Affine:
         raise EreduError("only affine quantization is implemented on the device path")
+    if w.dim() > 2:
+        if x.dim() < 2:
+            raise EreduError("with batched weights, x must be at least [M, K]")
+        try:
+            torch.broadcast_shapes(tuple(x.shape[:-2]), tuple(w.shape[:-2]))
+        except RuntimeError as e:
+            raise EreduError(f"batch dimensions of x {tuple(x.shape[:-2])} and w {tuple(w.shape[:-2])} "
+                             f"do not broadcast") from e
+        return gather_qmm_with_mode(x, w, scales, biases, None, None, transpose, group_size, bits, False, mode)
     N, K = _check_operands(x, w, scales, biases, transpose, group_size, bits)
     x_code = _dtype_code(x, "x")
     s_code = _dtype_code(scales, "scales")

@@ -161,3 +161,59 @@ def _mxfp4():
     from eredu_amd import QuantizationMode
 
     return QuantizationMode("mxfp4")
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 32)])
+def test_batched_quantized_matmul_kv_attention(cuda, bits, gs):
+    """The quantized KV attention of eredu/src/backend/mlx/nn/tensor.rs:76-150
+    at one decode position: queries [1, n_kv, n_rep, 1, D] against keys and
+    values [1, n_kv, 1, T, D*bits/32] through quantized_matmul's batch
+    broadcasting (scores with transpose = true, then softmax, then the values
+    with transpose = false); each product against gather_qmm_f64 with the
+    broadcast indices, and the whole attention against an f64 softmax."""
+    from eredu_amd import quantized_matmul
+
+    n_kv, n_rep, T, D = 2, 4, 256, 128
+    print(f"[case] quantized KV attention bits={bits} gs={gs} T={T}", flush=True)
+    keys = expert_bank(n_kv, T, D, gs, bits, orc.BF16, 51, transpose=True)       # [n_kv, T, D*bits/32]
+    vals = expert_bank(n_kv, D, T, gs, bits, orc.BF16, 61, transpose=False)      # [n_kv, T, D*bits/32]
+    q_host, qd = activations(n_kv * n_rep, 1, D, orc.BF16, 71)
+    lhs = np.arange(n_kv * n_rep).reshape(1, n_kv, n_rep)
+    rhs = np.arange(n_kv).reshape(1, n_kv, 1)
+
+    def dev(bank):
+        w, s, b = bank
+        shape = (1, n_kv, 1)
+        return (dev_words(w).reshape(*shape, *w.shape[1:]), dev_bf16(s).reshape(*shape, *s.shape[1:]),
+                dev_bf16(b).reshape(*shape, *b.shape[1:]))
+
+    kw, ks, kb = dev(keys)
+    vw, vs, vb = dev(vals)
+    q5 = qd.reshape(1, n_kv, n_rep, 1, D)
+    scores = quantized_matmul(q5, kw, ks, kb, transpose=True, group_size=gs, bits=bits)
+    assert tuple(scores.shape) == (1, n_kv, n_rep, 1, T)
+    s_ref = orc.gather_qmm_f64(q_host, orc.BF16, *keys, orc.BF16, lhs, rhs, True, gs, bits, T, D)
+    check(scores, s_ref, out_is_bf16=True)
+
+    probs = torch.softmax(scores.float() / np.sqrt(D), dim=-1).to(torch.bfloat16)
+    out = quantized_matmul(probs, vw, vs, vb, transpose=False, group_size=gs, bits=bits)
+    assert tuple(out.shape) == (1, n_kv, n_rep, 1, D)
+    p_host = host_f32(probs).reshape(n_kv * n_rep, 1, T)
+    p_bits = orc.f32_to_bf16_bits(p_host)
+    o_ref = orc.gather_qmm_f64(p_bits, orc.BF16, *vals, orc.BF16, lhs, rhs, False, gs, bits, D, T)
+    check(out, o_ref, out_is_bf16=True)
+
+    # the composition against an f64 attention over the dequantized caches;
+    # tolerance 2e-2 RMS: the bf16 roundings of the scores and probabilities
+    # (2^-9 relative each) come on top of the two products' own 1e-2 rule
+    Kd = [orc.affine_dequant_f64(keys[0][h], keys[1][h], keys[2][h], orc.BF16, T, D, gs, bits) for h in range(n_kv)]
+    Vd = [orc.affine_dequant_f64(vals[0][h], vals[1][h], vals[2][h], orc.BF16, T, D, gs, bits) for h in range(n_kv)]
+    q64 = orc.bf16_bits_to_f32(q_host).astype(np.float64).reshape(n_kv, n_rep, D)
+    att = np.empty((n_kv, n_rep, D))
+    for h in range(n_kv):
+        sc = q64[h] @ Kd[h].T / np.sqrt(D)
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        att[h] = (p / p.sum(axis=1, keepdims=True)) @ Vd[h]
+    got = host_f32(out).reshape(n_kv, n_rep, D)
+    rms = np.sqrt(np.mean(att ** 2))
+    assert np.max(np.abs(got - att)) <= 2e-2 * rms, np.max(np.abs(got - att)) / rms
