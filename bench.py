@@ -251,6 +251,57 @@ def bench_gguf(steps, warmup):
     return out
 
 
+def bench_qmm_n(steps, warmup):
+    """transpose = false at M = 1 (x . W, W [K, N] packed along N; the
+    safemlx default layout): N x K = 4096 x 4096 and 14336 x 4096, 4 weight
+    copies rotating per replay; and the values product of the quantized KV
+    attention at one decode position (32 query heads over 8 KV heads, 1024
+    cached tokens, D = 128: gather_qmm batches through quantized_matmul's
+    broadcasting)."""
+    import torch
+
+    n = _lib()
+    out = {}
+    for N, K in ((4096, 4096), (14336, 4096)):
+        copies = 4
+        ws = [torch.randint(-2**31, 2**31 - 1, (K, N * BITS // 32), dtype=torch.int32, device="cuda")
+              for _ in range(copies)]
+        s = (0.01 * torch.rand((K, N // GS), device="cuda")).to(torch.bfloat16)
+        b = (-0.08 * torch.rand((K, N // GS), device="cuda")).to(torch.bfloat16)
+        x = torch.randn((1, K), device="cuda").to(torch.bfloat16)
+        y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+
+        def fn(st):
+            for w in ws:
+                n.check(n.lib().eq_quantized_matmul(y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(),
+                                                    b.data_ptr(), 1, N, K, False, GS, BITS, b"affine",
+                                                    n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, st))
+
+        ms = Timer(fn).ms_per_replay(max(steps // 4, 20), warmup) / copies
+        gbs = qmv_bytes(1, N, K) / (ms * 1e-3) / 1e9
+        out[f"x.W_{N}x{K}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del ws
+    # values product of the quantized KV attention: probs [1, 8, 4, 1, T] . values [1, 8, 1, T, D]
+    n_kv, n_rep, T, D = 8, 4, 1024, 128
+    vw = torch.randint(-2**31, 2**31 - 1, (n_kv, T, D * BITS // 32), dtype=torch.int32, device="cuda")
+    vs = (0.01 * torch.rand((n_kv, T, D // GS), device="cuda")).to(torch.bfloat16)
+    vb = (-0.08 * torch.rand((n_kv, T, D // GS), device="cuda")).to(torch.bfloat16)
+    probs = torch.softmax(torch.randn((n_kv * n_rep, 1, T), device="cuda"), -1).to(torch.bfloat16)
+    yv = torch.empty((n_kv * n_rep, 1, D), dtype=torch.bfloat16, device="cuda")
+    lhs = torch.arange(n_kv * n_rep, dtype=torch.int32, device="cuda")
+    rhs = torch.arange(n_kv, dtype=torch.int32, device="cuda").repeat_interleave(n_rep)
+
+    def fv(st):
+        n.check(n.lib().eq_gather_qmm(yv.data_ptr(), probs.data_ptr(), vw.data_ptr(), vs.data_ptr(), vb.data_ptr(),
+                                      lhs.data_ptr(), rhs.data_ptr(), n_kv * n_rep, n_kv * n_rep, n_kv, 1, D, T,
+                                      False, GS, BITS, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, True, st))
+
+    ms = Timer(fv).ms_per_replay(max(steps // 4, 20), warmup)
+    out[f"kv_values_{n_kv}x{T}x{D}_rep{n_rep}"] = {"us": round(ms * 1e3, 2),
+                                                   "MB_values": round(n_kv * T * D * (BITS / 8 + 4 / GS) / 1e6, 3)}
+    return out
+
+
 def bench_gather(steps, warmup):
     """Routed-expert decode through gather_qmm (the eredu MoE call, x [routes,
     1, K], lhs = arange, rhs = expert of each route): a Mixtral-8x7B-shaped
@@ -424,7 +475,7 @@ def main():
     ap.add_argument("--gguf-only", action="store_true",
                     help="only the GGUF dequant/convert sweep, one JSON object of its figures")
     ap.add_argument("--gather-only", action="store_true",
-                    help="only the routed-expert gather_qmm decode figures, one JSON object")
+                    help="only the gather_qmm and transpose = false figures, one JSON object")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the full decode step of configs[4], one JSON object of its figures")
     args = ap.parse_args()
@@ -449,6 +500,8 @@ def main():
         if args.gather_only:
             log("[bench] gather_qmm routed-expert decode")
             out["gather_qmm"] = bench_gather(args.steps, args.warmup)
+            log("[bench] transpose = false (qmm_n)")
+            out["qmm_n"] = bench_qmm_n(args.steps, args.warmup)
         print(json.dumps(out), flush=True)
         return
     gen = torch.Generator(device="cuda").manual_seed(0)
@@ -497,6 +550,8 @@ def main():
         detail["gguf"] = bench_gguf(args.steps, args.warmup)
         log("[bench] gather_qmm routed-expert decode")
         detail["gather_qmm"] = bench_gather(args.steps, args.warmup)
+        log("[bench] transpose = false (qmm_n)")
+        detail["qmm_n"] = bench_qmm_n(args.steps, args.warmup)
 
     per_launch_bytes = nbytes / launches
     avg_launch_us = ms * 1e3 / launches

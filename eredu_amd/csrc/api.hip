@@ -193,6 +193,12 @@ extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, co
                             w, scales, biases, int(M), int(N), int(K), st))
             return check_launch("quantized_matmul (qmm)");
     }
+    if (!transpose && x_dtype == EQ_DTYPE_BF16 && M <= 8) {
+        const GatherIdx one{nullptr, nullptr, 1, 1};
+        if (launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w,
+                               scales, biases, one, 1, int(M), int(N), int(K), group_size, st))
+            return check_launch("quantized_matmul (qmm_n)");
+    }
 
     bool launched = false;
     with_bits(bits, [&](auto bc) {

@@ -250,6 +250,36 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 
+// ------------------------------------------------------------ gather / batch
+
+// Batch indirection of gather_qmm (and of batched transpose = false launches):
+// output batch b reads x batch lhs[b] and weight batch rhs[b].
+struct GatherIdx {
+    const int32_t* lhs;  // null: batch b reads x batch b (or 0 when x has one)
+    const int32_t* rhs;  // null: batch b reads w batch b (or 0 when w has one)
+    int64_t x_batches, w_batches;
+};
+
+// The operand batches of output batch b; false if an index is out of range.
+__device__ __forceinline__ bool gather_batch(const GatherIdx& g, int64_t b, int64_t& xb, int64_t& wb) {
+    xb = g.lhs ? int64_t(g.lhs[b]) : (g.x_batches == 1 ? 0 : b);
+    wb = g.rhs ? int64_t(g.rhs[b]) : (g.w_batches == 1 ? 0 : b);
+    return xb >= 0 && xb < g.x_batches && wb >= 0 && wb < g.w_batches;
+}
+
+// Split-K partial sums: a per-device f32 buffer of at least `bytes`, grown
+// (never while `st` is capturing) and kept until the process ends; null if it
+// cannot be provided.  Launches that use it on one device are stream-ordered.
+float* qmm_workspace(size_t bytes, hipStream_t st);
+
+// x . W for W [K, N] packed along N (transpose = false), M <= 8 activation
+// rows per batch, bf16 x and y, bf16/f16 scales, 4- or 8-bit codes; batches
+// through g (y [batch, M, N]).  False (nothing launched) for other
+// combinations.
+bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
+                        const void* b, const GatherIdx& g, int64_t batch, int M, int N, int K, int gs,
+                        hipStream_t st);
+
 // ------------------------------------------------------------ general bodies
 
 // LSB-first code c of a packed row (bits in {2, 4, 8} never straddle words).

@@ -18,24 +18,12 @@
 // loaded once for 4 rows); 4-bit sums run on v_dot2c_f32_bf16 with codes as
 // the exact bf16 values 128 + q.  Everything else: the general kernels'
 // bodies (one wave per output feature, or one thread per output column),
-// offset per batch.
+// offset per batch; transpose = false with M <= 8, bf16 x and 4/8-bit codes
+// takes qmm_n_small (qmm_n.hip) with these indices.
 #include "eq_common.hpp"
 
 namespace eq {
 namespace {
-
-struct GatherIdx {
-    const int32_t* lhs;  // null: batch b reads x batch b (or 0 when x has one)
-    const int32_t* rhs;  // null: batch b reads w batch b (or 0 when w has one)
-    int64_t x_batches, w_batches;
-};
-
-// The operand batches of output batch b; false if an index is out of range.
-__device__ __forceinline__ bool gather_batch(const GatherIdx& g, int64_t b, int64_t& xb, int64_t& wb) {
-    xb = g.lhs ? int64_t(g.lhs[b]) : (g.x_batches == 1 ? 0 : b);
-    wb = g.rhs ? int64_t(g.rhs[b]) : (g.w_batches == 1 ? 0 : b);
-    return xb >= 0 && xb < g.x_batches && wb >= 0 && wb < g.w_batches;
-}
 
 // grid (ceil(N / kGenRowsPerWG), batches of this launch); b = b0 + blockIdx.y.
 template <int BITS, typename XT, typename ST>
@@ -269,6 +257,10 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
 
     const bool fast = transpose && M == 1 && x_dtype == EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F32 &&
                       (bits == 4 || bits == 8) && aligned(x, 16) && aligned(w, 16);
+    if (!transpose && M <= 8 && x_dtype == EQ_DTYPE_BF16 &&
+        launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales,
+                           biases, g, batch, int(M), int(N), int(K), group_size, st))
+        return check_launch("gather_qmm (qmm_n)");
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const unsigned nb = unsigned(batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY);
         if (fast) {

@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void qmm_split_reduce(uint16_t* __restrict__ y
 
 // Per-device f32 workspace for split K, grown on demand outside stream
 // capture (a capturing caller whose workspace is too small gets no split).
-static float* qmm_workspace(size_t bytes, hipStream_t st) {
+float* qmm_workspace(size_t bytes, hipStream_t st) {
     static std::mutex mu;
     static float* ptr[64] = {};
     static size_t cap[64] = {};

@@ -127,6 +127,25 @@ def test_transpose_false(cuda, M):
     run_case(M, 128, 192, 64, 4, transpose=False, seed=M)
 
 
+# transpose = false, bf16 x: M = 1 takes qmm_n_m1 (N = 64 / 128 / 384 / 4096:
+# 4, 4, 8, 16 lanes across the columns), M = 2..8 qmm_n_small (16 / 32 / 64
+# word columns per workgroup); K = 96 runs one K split, 1024 and 4096 several
+# (partial sums through the workspace); M = 9 takes the general kernel.
+@pytest.mark.parametrize("N,K", [(64, 96), (384, 1024), (4096, 4096), (128, 4096)])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 9])
+def test_transpose_false_small_m(cuda, N, K, M):
+    run_case(M, N, K, 64, 4, transpose=False, seed=N + K + M)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("sdt", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("M", [1, 3])
+def test_transpose_false_contract_grid(cuda, bits, gs, sdt, M):
+    # M = 1 takes qmm_n_m1 (16-byte words per lane), M = 3 qmm_n_small
+    run_case(M, 256, 2048, gs, bits, sdt=sdt, transpose=False, seed=bits * gs + M, biases=(gs != 32))
+
+
 def test_ragged_n_and_no_biases(cuda):
     run_case(2, 40, 256, 32, 4, seed=9, biases=False)   # N % 16 != 0 -> general kernel
     run_case(2, 64, 256, 32, 4, seed=10, biases=False)  # qmv without biases
