@@ -6,9 +6,12 @@ hand-written HIP kernels behind a C ABI (``include/eredu_hip.h``), with a
 host-side mirror of the reference's operator API:
 
 * :mod:`eredu_amd.quantization` -- safemlx ``quantized_matmul[_with_mode]``,
-  ``dequantize[_with_mode]``, ``quantize[_with_mode]``, ``QuantizedLinear``.
-* :mod:`eredu_amd.gguf` -- eredu-gguf ``convert_affine`` / ``AffineTensor``
-  and dense dequantization.
+  ``gather_qmm[_with_mode]``, ``dequantize[_with_mode]``,
+  ``quantize[_with_mode]``, ``QuantizedLinear``.
+* :mod:`eredu_amd.gguf` -- eredu-gguf ``convert_affine`` / ``AffineTensor``,
+  dense dequantization and the native Q4_K / Q8_0 linear.
+* :mod:`eredu_amd.checkpoint` -- MLX-LM quantized SafeTensors checkpoints.
+* :mod:`eredu_amd.decode` -- the Llama decode step around the projections.
 """
 from ._native import EreduError
 from .quantization import (
