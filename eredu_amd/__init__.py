@@ -11,6 +11,8 @@ host-side mirror of the reference's operator API:
 * :mod:`eredu_amd.gguf` -- eredu-gguf ``convert_affine`` / ``AffineTensor``,
   dense dequantization and the native Q4_K / Q8_0 linear.
 * :mod:`eredu_amd.checkpoint` -- MLX-LM quantized SafeTensors checkpoints.
+* :mod:`eredu_amd.gguf_file` -- GGUF container reader/writer and the
+  streaming load into the device-side convert.
 * :mod:`eredu_amd.decode` -- the Llama decode step around the projections.
 """
 from ._native import EreduError
