@@ -337,6 +337,31 @@ def bench_gather(steps, warmup):
                       "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         del w, s, b
         torch.cuda.empty_cache()
+    # prefill: many routes over sorted experts -- grouped MFMA GEMM (sorted hint)
+    # against the per-route kernel (no hint); TFLOP/s = 2 routes N K / time
+    for label, E, routes, N, K in (("prefill_mixtral_8x_1024routes_14336x4096", 8, 1024, 14336, 4096),
+                                   ("prefill_qwen3moe_128x_4096routes_768x2048", 128, 4096, 768, 2048)):
+        w = torch.randint(-2**31, 2**31 - 1, (E, N, K * bits // 32), dtype=torch.int32, device="cuda")
+        s = (0.01 * torch.rand((E, N, K // gs), device="cuda")).to(torch.bfloat16)
+        b = (-0.08 * torch.rand((E, N, K // gs), device="cuda")).to(torch.bfloat16)
+        x = torch.randn((routes, 1, K), device="cuda").to(torch.bfloat16)
+        y = torch.empty((routes, 1, N), dtype=torch.bfloat16, device="cuda")
+        lhs = torch.arange(routes, dtype=torch.int32, device="cuda")
+        g = torch.Generator(device="cuda").manual_seed(5)
+        rhs = torch.sort(torch.randint(0, E, (routes,), device="cuda", generator=g, dtype=torch.int32)).values
+        res = {}
+        for hint in (True, False):
+            def fg(st, hint=hint):
+                n.check(n.lib().eq_gather_qmm(y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(),
+                                              lhs.data_ptr(), rhs.data_ptr(), routes, routes, E, 1, N, K, True, gs,
+                                              bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, hint, st))
+
+            ms = Timer(fg).ms_per_replay(max(steps // 4, 10), warmup)
+            tf = 2.0 * routes * N * K / (ms * 1e-3) / 1e12
+            res["grouped" if hint else "per_route"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1)}
+        out[label] = res
+        del w, s, b
+        torch.cuda.empty_cache()
     return out
 
 

@@ -272,6 +272,18 @@ __device__ __forceinline__ bool gather_batch(const GatherIdx& g, int64_t b, int6
 // cannot be provided.  Launches that use it on one device are stream-ordered.
 float* qmm_workspace(size_t bytes, hipStream_t st);
 
+// Routed experts over sorted expert indices (gather_qmm with sorted_indices,
+// transpose, one activation row per route, bf16 x, 4/8-bit, bf16/f16
+// scales): y [batch, N] zeroed, rows x[lhs[b]] gathered into the workspace,
+// a device-built list of (expert, 128-row tile) entries, and one MFMA qmm
+// launch over the list, so each expert's weights are read once per 128
+// routes instead of once per route.  N a multiple of 128, K of 64, x and w
+// 16-byte aligned, y 8-byte aligned.  False (nothing launched) when the
+// workspace cannot be provided or the combination has no kernel.
+bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                        const void* s, const void* b, const int32_t* lhs, const int32_t* rhs, int batch,
+                        int64_t x_batches, int experts, int N, int K, hipStream_t st);
+
 // x . W for W [K, N] packed along N (transpose = false), M <= 8 activation
 // rows per batch, bf16 x and y, bf16/f16 scales, 4- or 8-bit codes; batches
 // through g (y [batch, M, N]).  False (nothing launched) for other

@@ -214,7 +214,10 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
                              int64_t w_batches, int64_t M, int64_t N, int64_t K, bool transpose, int group_size,
                              int bits, const char* mode, int x_dtype, int scale_dtype, bool sorted_indices,
                              eq_stream_t stream) {
-    (void)sorted_indices;  // an ordering hint; the results do not depend on it
+    // sorted_indices: an ordering hint.  With it (and many routes) the
+    // grouped MFMA path runs; its results equal the other paths' within the
+    // matmul rule for sorted indices (unsorted indices under the hint give
+    // wrong rows, as in MLX, but every access stays in bounds).
     clear_error();
     if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
     if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype)) {
@@ -255,6 +258,16 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const GatherIdx g{lhs_indices, rhs_indices, x_batches, w_batches};
 
+    // many routes over sorted experts: one MFMA GEMM per expert's rows
+    const bool grouped = transpose && M == 1 && sorted_indices && rhs_indices && x_dtype == EQ_DTYPE_BF16 &&
+                         scale_dtype != EQ_DTYPE_F32 && (bits == 4 || bits == 8) && batch >= 64 &&
+                         batch >= 2 * w_batches && batch <= INT32_MAX && w_batches <= INT32_MAX && N % 128 == 0 &&
+                         K % 64 == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 8) &&
+                         int64_t(N) * K * bits / 8 < (int64_t(1) << 31) && batch * K * 2 < (int64_t(1) << 31);
+    if (grouped && launch_qmm_grouped(bits, group_size, scale_dtype, static_cast<uint16_t*>(y),
+                                      static_cast<const uint16_t*>(x), w, scales, biases, lhs_indices, rhs_indices,
+                                      int(batch), x_batches, int(w_batches), int(N), int(K), st))
+        return check_launch("gather_qmm (grouped qmm)");
     const bool fast = transpose && M == 1 && x_dtype == EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F32 &&
                       (bits == 4 || bits == 8) && aligned(x, 16) && aligned(w, 16);
     if (!transpose && M <= 8 && x_dtype == EQ_DTYPE_BF16 &&

@@ -137,6 +137,12 @@ struct QmmArgs {
     const uint16_t* s;
     const uint16_t* b;  // may be null
     int M, N, K, mtiles, ntiles, splits, cps;  // cps: chunks per split
+    // Grouped (routed experts, no split K): row tile tm of the grid is entry
+    // groups[tm] = {expert, first row, rows, row offset} of a device-built
+    // list; x and y rows [first, first + rows) belong to the expert, whose
+    // weights, scales and biases follow the previous expert's.  An expert
+    // below zero marks an unused entry.  Null: one plain problem.
+    const int4* groups;
 };
 
 // PW (parameter windows, group size 64 with an even number of groups per row
@@ -151,7 +157,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // the compiler's LDS alias scopes tell the buffers apart and a read of one
     // does not wait for the loads still landing in another.
     __shared__ __attribute__((aligned(16))) char abuf0[2 * kLdsBuf], abuf1[2 * kLdsBuf], abuf2[2 * kLdsBuf];
-    const int M = args.M, N = args.N, K = args.K;
+    const int N = args.N, K = args.K, G = K / GS;
+    int M = args.M;
 
     // Tile and split of this workgroup: the workgroups of one XCD (id % 8)
     // take a contiguous run of row-major tiles, i.e. few row blocks of x.
@@ -160,7 +167,24 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
     const int split = bid % args.splits, tile = bid / args.splits;
     const int tm = tile / args.ntiles, tn = tile % args.ntiles;
-    const int m0 = tm * kBM, n0 = tn * kBN;
+    int m0 = tm * kBM;
+    const int n0 = tn * kBN;
+    const uint16_t* xp = args.x;
+    const uint32_t* wp = args.w;
+    const uint16_t* sp = args.s;
+    const uint16_t* bp = args.b;
+    uint16_t* yp = args.y;
+    if (args.groups) {
+        const int4 gd = args.groups[tm];
+        if (gd.x < 0) return;  // unused entry: the whole workgroup leaves before any barrier
+        xp += int64_t(gd.y) * K;
+        yp += int64_t(gd.y) * N;
+        M = gd.z;
+        m0 = gd.w;
+        wp += int64_t(gd.x) * N * (K * BITS / 32);
+        sp += int64_t(gd.x) * N * G;
+        if (bp) bp += int64_t(gd.x) * N * G;
+    }
     const int nchunks = K / kBK;
     const int c_begin = split * args.cps, c_end = min(nchunks, c_begin + args.cps);
     const int nloc = c_end - c_begin;  // >= 1 (the planner leaves no split empty)
@@ -172,12 +196,11 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const int l32 = lane & 31, kb = lane >> 5;
     const int gofs = kgrp * kLdsBuf;  // this K-group's part of each ring buffer
     const int steps = (nloc + 1) / 2;  // chunks per K-group (the second may have one fewer)
-    const int G = K / GS;
 
-    const __amdgpu_buffer_rsrc_t xr = raw_rsrc(args.x, uint32_t(M) * uint32_t(K) * 2u);
-    const __amdgpu_buffer_rsrc_t wr = raw_rsrc(args.w, uint32_t(N) * uint32_t(K) * BITS / 8u);
-    const __amdgpu_buffer_rsrc_t sr = raw_rsrc(args.s, uint32_t(N) * uint32_t(G) * 2u);
-    const __amdgpu_buffer_rsrc_t br = raw_rsrc(args.b ? args.b : args.s, args.b ? uint32_t(N) * uint32_t(G) * 2u : 0u);
+    const __amdgpu_buffer_rsrc_t xr = raw_rsrc(xp, uint32_t(M) * uint32_t(K) * 2u);
+    const __amdgpu_buffer_rsrc_t wr = raw_rsrc(wp, uint32_t(N) * uint32_t(K) * BITS / 8u);
+    const __amdgpu_buffer_rsrc_t sr = raw_rsrc(sp, uint32_t(N) * uint32_t(G) * 2u);
+    const __amdgpu_buffer_rsrc_t br = raw_rsrc(bp ? bp : sp, bp ? uint32_t(N) * uint32_t(G) * 2u : 0u);
 
     // Lane offsets (chunk 0); rows past M and columns past N read zero.
     // Activations go straight from memory to LDS: load i of wave w fills the
@@ -392,7 +415,7 @@ done:
                         *reinterpret_cast<f32x4*>(args.ws + (int64_t(split) * M + m) * N + n) = v;
                     } else {
                         const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
-                        *reinterpret_cast<uint2*>(args.y + int64_t(m) * N + n) = make_uint2(lo, hi);
+                        *reinterpret_cast<uint2*>(yp + int64_t(m) * N + n) = make_uint2(lo, hi);
                     }
                 }
         }
@@ -505,6 +528,132 @@ static bool launch_qmm_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t
     case 128: launch_qmm_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, st); return true;
     default: return false;
     }
+}
+
+// ------------------------------------------------------- grouped (experts)
+
+// First index i of a[0, n) with a[i] >= v (a sorted ascending; for unsorted
+// input the result is still in [0, n]).
+__device__ __forceinline__ int lower_bound_i32(const int32_t* __restrict__ a, int n, int v) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (a[mid] < v) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Sorted expert indices -> the grouped tile list: expert e owns rows
+// [lower_bound(e), lower_bound(e + 1)) and takes ceil(rows / kBM) entries
+// {e, first, rows, kBM t}.  One workgroup of 1024 threads, experts in passes
+// of 1024 with a block scan of the entry counts; entries at or past `cap`
+// are dropped and the list's remaining entries are marked unused.
+__global__ __launch_bounds__(1024) void qmm_group_tiles(int4* __restrict__ out, const int32_t* __restrict__ rhs,
+                                                        int batch, int experts, int cap) {
+    __shared__ int scan[1024];
+    __shared__ int carry;
+    const int tid = threadIdx.x;
+    if (tid == 0) carry = 0;
+    __syncthreads();
+    for (int e0 = 0; e0 < experts; e0 += 1024) {
+        const int e = e0 + tid;
+        int first = 0, rows = 0;
+        if (e < experts) {
+            first = lower_bound_i32(rhs, batch, e);
+            const int end = lower_bound_i32(rhs, batch, e + 1);
+            rows = end > first ? end - first : 0;
+        }
+        const int nt = (rows + kBM - 1) / kBM;
+        scan[tid] = nt;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {  // inclusive scan
+            const int v = tid >= o ? scan[tid - o] : 0;
+            __syncthreads();
+            scan[tid] += v;
+            __syncthreads();
+        }
+        const int base = carry + scan[tid] - nt;
+        for (int t = 0; t < nt; t++)
+            if (base + t < cap) out[base + t] = make_int4(e, first, rows, t * kBM);
+        __syncthreads();
+        if (tid == 1023) carry += scan[1023];
+        __syncthreads();
+    }
+    for (int i = carry + tid; i < cap; i += 1024) out[i] = make_int4(-1, 0, 0, 0);
+}
+
+// xg[b] = x[lhs[b]] (K bf16 per row, 16-byte copies); an out-of-range index
+// gives a zero row.  One workgroup per row.
+__global__ __launch_bounds__(256) void qmm_gather_rows(uint16_t* __restrict__ xg, const uint16_t* __restrict__ x,
+                                                       const int32_t* __restrict__ lhs, int64_t x_batches, int K) {
+    const int64_t b = blockIdx.x;
+    const int64_t src = lhs ? int64_t(lhs[b]) : (x_batches == 1 ? 0 : b);
+    uint4* dst = reinterpret_cast<uint4*>(xg + b * K);
+    const bool ok = src >= 0 && src < x_batches;
+    const uint4* from = reinterpret_cast<const uint4*>(x + (ok ? src : 0) * K);
+    for (int i = threadIdx.x; i < K / 8; i += 256) dst[i] = ok ? from[i] : make_uint4(0, 0, 0, 0);
+}
+
+// y = 0 (n bf16 values, n a multiple of 4, y 8-byte aligned).
+__global__ __launch_bounds__(256) void qmm_zero(uint16_t* __restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4; i < n; i += int64_t(gridDim.x) * 1024)
+        *reinterpret_cast<uint2*>(y + i) = make_uint2(0, 0);
+}
+
+template <int BITS, int GS, typename ST>
+static bool launch_qmm_grouped_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
+                                 const int32_t* lhs, const int32_t* rhs, int batch, int64_t x_batches, int experts,
+                                 int N, int K, hipStream_t st) {
+    const int cap = experts + (batch + kBM - 1) / kBM;  // sum over experts of ceil(rows / kBM)
+    const size_t xg_bytes = (size_t(batch) * size_t(K) * 2u + 255u) & ~size_t(255);
+    float* ws = qmm_workspace(xg_bytes + size_t(cap) * sizeof(int4), st);
+    if (!ws) return false;
+    uint16_t* xg = reinterpret_cast<uint16_t*>(ws);
+    int4* list = reinterpret_cast<int4*>(reinterpret_cast<char*>(ws) + xg_bytes);
+    const int64_t yn = int64_t(batch) * N;
+    qmm_zero<<<dim3(unsigned(yn / 1024 < 4096 ? yn / 1024 + 1 : 4096)), dim3(256), 0, st>>>(y, yn);
+    qmm_gather_rows<<<dim3(unsigned(batch)), dim3(256), 0, st>>>(xg, x, lhs, x_batches, K);
+    qmm_group_tiles<<<dim3(1), dim3(1024), 0, st>>>(list, rhs, batch, experts, cap);
+    QmmArgs a{};
+    a.y = y, a.x = xg, a.w = w, a.s = static_cast<const uint16_t*>(s), a.b = static_cast<const uint16_t*>(b);
+    a.M = batch, a.N = N, a.K = K;
+    a.mtiles = cap, a.ntiles = (N + kBN - 1) / kBN, a.splits = 1, a.cps = K / kBK;
+    a.groups = list;
+    const bool pw = GS == 64 && (K / GS) % 2 == 0 && a.cps % 2 == 0;
+    const dim3 grid(unsigned(a.mtiles * a.ntiles)), block(kQmmThreads);
+    if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64><<<grid, block, 0, st>>>(a);
+    else qmm_mfma_kernel<BITS, GS, ST, false, false><<<grid, block, 0, st>>>(a);
+    return true;
+}
+
+template <int BITS, typename ST>
+static bool launch_qmm_grouped_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
+                                  const void* b, const int32_t* lhs, const int32_t* rhs, int batch,
+                                  int64_t x_batches, int experts, int N, int K, hipStream_t st) {
+    switch (gs) {
+    case 32: return launch_qmm_grouped_t<BITS, 32, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+    case 64: return launch_qmm_grouped_t<BITS, 64, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+    case 128: return launch_qmm_grouped_t<BITS, 128, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+    default: return false;
+    }
+}
+
+bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                        const void* s, const void* b, const int32_t* lhs, const int32_t* rhs, int batch,
+                        int64_t x_batches, int experts, int N, int K, hipStream_t st) {
+    if (bits == 4) {
+        if (scale_dtype == EQ_DTYPE_BF16)
+            return launch_qmm_grouped_gs<4, BF16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+        if (scale_dtype == EQ_DTYPE_F16)
+            return launch_qmm_grouped_gs<4, F16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+    } else if (bits == 8) {
+        if (scale_dtype == EQ_DTYPE_BF16)
+            return launch_qmm_grouped_gs<8, BF16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+        if (scale_dtype == EQ_DTYPE_F16)
+            return launch_qmm_grouped_gs<8, F16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+    }
+    return false;
 }
 
 // Preconditions checked by the dispatcher (api.hip): x bf16, transpose,

@@ -239,7 +239,9 @@ def gather_qmm_with_mode(
     that operand's batch shape.  The two broadcast to the output batch shape;
     y [*batch, M, N] with y[b] = quantized_matmul(x[lhs[b]], w[rhs[b]]).
     The indices are read on the device: an out-of-range index gives zero
-    output rows.  sorted_indices is a hint and does not change the result.
+    output rows.  sorted_indices promises ascending rhs_indices (MLX's
+    meaning): with it, many single-row routes run as one MFMA GEMM per
+    expert (results equal within the matmul rule).
     """
     mode.validate(group_size, bits)
     if mode is not QuantizationMode.Affine:

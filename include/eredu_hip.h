@@ -152,8 +152,11 @@ int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, 
  * (transpose) or [w_batches, K, N*bits/32 | N/gs], y [batch, M, N].  The int32
  * index arrays live on the device; a null lhs_indices means b (x_batches ==
  * batch) or 0 (x_batches == 1), likewise rhs_indices.  A batch whose index is
- * out of range gets zero output rows.  sorted_indices is an ordering hint and
- * does not change the result.  Replaces mlx_gather_qmm
+ * out of range gets zero output rows.  sorted_indices promises rhs_indices in
+ * ascending order (MLX's meaning); with it and many routes per expert
+ * (transpose, M = 1, bf16 x, 4/8-bit) each expert's routes run as one MFMA
+ * GEMM -- same results within the matmul rule; unsorted indices under the
+ * promise give wrong rows (never an out-of-bounds access).  Replaces mlx_gather_qmm
  * (safemlx-sys/src/bindings.rs:3309) under safemlx::ops::gather_qmm_with_mode
  * (safemlx/src/ops/quantization.rs:298-379), as called by eredu's routed
  * experts (eredu/src/backend/mlx/nn/moe.rs:121-139).

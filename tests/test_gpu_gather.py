@@ -217,3 +217,54 @@ def test_batched_quantized_matmul_kv_attention(cuda, bits, gs):
     got = host_f32(out).reshape(n_kv, n_rep, D)
     rms = np.sqrt(np.mean(att ** 2))
     assert np.max(np.abs(got - att)) <= 2e-2 * rms, np.max(np.abs(got - att)) / rms
+
+
+# ------------------------------------------------ grouped (sorted, many routes)
+# sorted_indices with >= 64 routes and >= 2 routes per expert: the routes of
+# an expert run as one MFMA GEMM (qmm_mfma_kernel over a device-built tile
+# list).  Same tolerance rule; experts with 0, 1..127 and > 128 routes.
+
+def sorted_routes(E, R, seed, lo=0, hi=None):
+    rng = np.random.default_rng(seed)
+    hi = E if hi is None else hi
+    # skewed: expert 1 gets many routes (several 128-row tiles), expert E-1 none
+    r = np.concatenate([np.full(R // 3, 1), rng.integers(lo, hi - 1, R - R // 3)])
+    return np.sort(r)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("sdt", [orc.BF16, orc.F16])
+def test_grouped_routes(cuda, bits, gs, sdt):
+    E, R = 6, 420
+    rhs = sorted_routes(E, R, seed=bits + gs)
+    run(E, 384, 512, gs, bits, np.arange(R), rhs, Bx=R, sdt=sdt, seed=bits * gs + 7, sorted_indices=True,
+        biases=(gs != 32))
+
+
+def test_grouped_routes_out_of_range_and_shared_rows(cuda):
+    """Sorted expert ids with -1 at the front and 99 at the back (zero rows),
+    one lhs out of range (zero row), lhs repeating rows (a token routed to
+    several experts)."""
+    E, R = 4, 200
+    rhs = np.concatenate([[-1, -1], sorted_routes(E, R - 5, seed=3), [99, 99, 99]])
+    lhs = np.arange(R) // 2
+    lhs[10] = 10_000
+    run(E, 256, 256, 64, 4, lhs, rhs, Bx=R // 2, seed=13, sorted_indices=True)
+
+
+def test_grouped_and_per_route_paths_on_a_mixtral_like_layout(cuda):
+    """8 experts of 1024 x 4096, 256 sorted routes: the grouped GEMM (sorted
+    hint) and the per-route kernel (no hint) each within the matmul rule of
+    the fp64 oracle (two bf16 results may differ by one ulp of each other)."""
+    E, R, N, K = 8, 256, 1024, 4096
+    w, s, b = expert_bank(E, N, K, 64, 4, orc.BF16, 77)
+    x_host, xd = activations(R, 1, K, orc.BF16, 78)
+    rhs_np = sorted_routes(E, R, seed=79)
+    rhs = torch.as_tensor(rhs_np, dtype=torch.int32).cuda()
+    lhs = torch.arange(R, dtype=torch.int32).cuda()
+    args = (xd, dev_words(w), dev_bf16(s), dev_bf16(b), lhs, rhs)
+    y_ref = orc.gather_qmm_f64(x_host, orc.BF16, w, s, b, orc.BF16, np.arange(R), rhs_np, True, 64, 4, N, K)
+    for hint in (True, False):
+        y = gather_qmm(*args, sorted_indices=hint)
+        check(y, y_ref, out_is_bf16=True)
