@@ -9,7 +9,8 @@ header, each offset aligned, shapes divisible by the GGML block, ranges
 inside the file and not overlapping.  ``write_gguf`` is the deterministic
 writer of eredu-gguf/src/writer.rs (test inputs, conversion output).
 
-``stream_convert_affine`` is the streaming read of SURVEY's format row: the
+``stream_convert_affine`` streams a checkpoint onto the GPU (the role of
+eredu-gguf/src/catalog.rs:435-660's converted-tensor iteration): the
 raw blocks of each Q4_0 / Q8_0 / Q4_K tensor go file -> pinned host buffer
 -> HBM on a copy stream while the previous tensor is converted to the MLX
 affine triple by ``eq_gguf_convert_affine`` on the compute stream (two
