@@ -365,6 +365,41 @@ def bench_gather(steps, warmup):
     return out
 
 
+def bench_affine_codec(steps, warmup):
+    """Affine dequantize (eq_dequantize: codes + scales + biases -> bf16) and
+    quantize (eq_quantize: bf16 -> codes + scales + biases) of a 4096 x 14336
+    matrix, 4-bit g64 bf16; GB/s of bytes read + written, 3 copies rotating."""
+    import torch
+
+    n = _lib()
+    rows, cols, copies = 4096, 14336, 3
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    lins = [Linear(rows, cols, gen) for _ in range(copies)]
+    dense = [torch.randn((rows, cols), device="cuda", generator=gen).to(torch.bfloat16) * 0.02 for _ in range(copies)]
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
+    wq = torch.empty((rows, cols * BITS // 32), dtype=torch.int32, device="cuda")
+    sq = torch.empty((rows, cols // GS), dtype=torch.bfloat16, device="cuda")
+    bq = torch.empty_like(sq)
+    packed = rows * cols * BITS // 8 + 2 * 2 * rows * (cols // GS)
+    res = {}
+
+    def deq(st):
+        for lin in lins:
+            n.check(n.lib().eq_dequantize(out.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(), rows,
+                                          cols, GS, BITS, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, st))
+
+    def quant(st):
+        for d in dense:
+            n.check(n.lib().eq_quantize(wq.data_ptr(), sq.data_ptr(), bq.data_ptr(), d.data_ptr(), rows, cols, GS,
+                                        BITS, b"affine", n.EQ_DTYPE_BF16, st))
+
+    for label, fn in (("dequantize_bf16", deq), ("quantize_bf16", quant)):
+        ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / copies
+        gbs = (packed + rows * cols * 2) / (ms * 1e-3) / 1e9
+        res[label] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    return res
+
+
 def bench_gguf_stream():
     """GGUF file -> HBM affine triples (gguf_file.stream_convert_affine): a
     file of 8 Q4_K tensors of 4096 x 14336 (264 MB, synthetic blocks) in the
@@ -580,6 +615,8 @@ def main():
             out["gguf"] = bench_gguf(args.steps, args.warmup)
             log("[bench] gguf streaming load")
             out["gguf_stream"] = bench_gguf_stream()
+            log("[bench] affine dequantize / quantize")
+            out["affine_codec"] = bench_affine_codec(args.steps, args.warmup)
         if args.gather_only:
             log("[bench] gather_qmm routed-expert decode")
             out["gather_qmm"] = bench_gather(args.steps, args.warmup)
@@ -633,6 +670,8 @@ def main():
         detail["gguf"] = bench_gguf(args.steps, args.warmup)
         log("[bench] gguf streaming load")
         detail["gguf_stream"] = bench_gguf_stream()
+        log("[bench] affine dequantize / quantize")
+        detail["affine_codec"] = bench_affine_codec(args.steps, args.warmup)
         log("[bench] gather_qmm routed-expert decode")
         detail["gather_qmm"] = bench_gather(args.steps, args.warmup)
         log("[bench] transpose = false (qmm_n)")

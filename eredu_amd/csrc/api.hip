@@ -65,27 +65,44 @@ __global__ __launch_bounds__(256) void qmm_n_general(typename XT::storage* __res
 }
 
 // out[r, c] = f32(s) * q + f32(b), one rounding each (convert.rs:81-101).
-template <int BITS, typename ST, typename OT>
+// One thread per code word; its PACK codes share a group (gs >= 32 >= PACK).
+// VEC (out 16-byte aligned): the word's outputs leave as 8- or 16-byte
+// stores instead of PACK scalar ones.
+template <int BITS, typename ST, typename OT, bool VEC>
 __global__ __launch_bounds__(256) void dequant_kernel(typename OT::storage* __restrict__ out,
                                                       const uint32_t* __restrict__ w,
                                                       const typename ST::storage* __restrict__ s,
                                                       const typename ST::storage* __restrict__ b, int64_t rows,
                                                       int64_t cols, int gs) {
     constexpr int PACK = 32 / BITS;
+    typedef typename OT::storage OS;
     const int64_t words = rows * cols / PACK;
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= words) return;
     const uint32_t word = w[i];
     const int64_t base = i * PACK;  // element index of the word's first code
     const int64_t r = base / cols, c0 = base % cols;
-    const int64_t G = cols / gs;
+    const int64_t g = r * (cols / gs) + c0 / gs;
+    const float sc = load_param<ST>(s, g);
+    const float bi = b ? load_param<ST>(b, g) : 0.f;
+    OS v[PACK];
 #pragma unroll
-    for (int p = 0; p < PACK; p++) {
-        const int64_t g = r * G + (c0 + p) / gs;
-        const float sc = load_param<ST>(s, g);
-        const float bi = b ? load_param<ST>(b, g) : 0.f;
-        const float prod = sc * float((word >> (p * BITS)) & ((1u << BITS) - 1u));
-        store_out<OT>(out, base + p, __fadd_rn(prod, bi));
+    for (int p = 0; p < PACK; p++)
+        v[p] = to_storage<OT>(__fadd_rn(sc * float((word >> (p * BITS)) & ((1u << BITS) - 1u)), bi));
+    if constexpr (VEC) {
+        constexpr int BYTES = PACK * int(sizeof(OS));
+        if constexpr (BYTES % 16 == 0) {
+#pragma unroll
+            for (int q = 0; q < BYTES / 16; q++)
+                reinterpret_cast<uint4*>(out + base)[q] = reinterpret_cast<const uint4*>(v)[q];
+        } else {
+#pragma unroll
+            for (int q = 0; q < BYTES / 8; q++)
+                reinterpret_cast<uint2*>(out + base)[q] = reinterpret_cast<const uint2*>(v)[q];
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < PACK; p++) out[base + p] = v[p];
     }
 }
 
@@ -141,6 +158,72 @@ __global__ __launch_bounds__(256) void quantize_kernel(uint32_t* __restrict__ wq
             word |= uint32_t(q) << (BITS * e);
         }
         dst[w0] = word;
+    }
+}
+
+// quantize_kernel with the group held in registers: one thread per group of
+// GS values, loaded with 16-byte loads (w 16-byte aligned), the same
+// arithmetic in the same order (bit-identical results), codes stored as
+// 16- or 8-byte words (wq 16-byte aligned).
+template <int BITS, typename T, int GS>
+__global__ __launch_bounds__(256) void quantize_vec_kernel(uint32_t* __restrict__ wq,
+                                                           typename T::storage* __restrict__ sc,
+                                                           typename T::storage* __restrict__ bi,
+                                                           const typename T::storage* __restrict__ w, int64_t groups) {
+    typedef typename T::storage S;
+    constexpr int PER16 = 16 / int(sizeof(S)), WORDS = GS * BITS / 32, PACK = 32 / BITS;
+    const int64_t gidx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (gidx >= groups) return;
+    float x[GS];
+    const uint4* src = reinterpret_cast<const uint4*>(w + gidx * GS);
+#pragma unroll
+    for (int q = 0; q < GS / PER16; q++) {
+        const uint4 u = src[q];
+        const S* e = reinterpret_cast<const S*>(&u);
+#pragma unroll
+        for (int j = 0; j < PER16; j++) {
+            if constexpr (sizeof(S) == 4) x[q * PER16 + j] = __builtin_bit_cast(float, e[j]);
+            else x[q * PER16 + j] = load_param<T>(e, j);
+        }
+    }
+    constexpr int n_bins = (1 << BITS) - 1;
+    float mn = x[0], mx = mn;
+#pragma unroll
+    for (int i = 1; i < GS; i++) {
+        mn = x[i] < mn ? x[i] : mn;
+        mx = x[i] > mx ? x[i] : mx;
+    }
+    float scale = (mx - mn) / float(n_bins);
+    if (scale < 1e-7f) scale = 1e-7f;
+    const bool neg = fabsf(mn) > fabsf(mx);
+    scale = neg ? scale : -scale;
+    const float edge = neg ? mn : mx;
+    const float q0 = rintf(edge / scale);
+    if (q0 != 0.0f) scale = edge / q0;
+    const S s_bits = to_storage<T>(scale), b_bits = to_storage<T>(edge);
+    sc[gidx] = s_bits;
+    bi[gidx] = b_bits;
+    const float s_st = load_param<T>(&s_bits, 0), b_st = load_param<T>(&b_bits, 0);
+    uint32_t words[WORDS];
+#pragma unroll
+    for (int w0 = 0; w0 < WORDS; w0++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < PACK; e++) {
+            float q = s_st != 0.0f ? rintf((x[w0 * PACK + e] - b_st) / s_st) : 0.0f;
+            q = q >= 0.0f ? q : 0.0f;
+            q = q > float(n_bins) ? float(n_bins) : q;
+            word |= uint32_t(q) << (BITS * e);
+        }
+        words[w0] = word;
+    }
+    uint32_t* dst = wq + gidx * WORDS;
+    if constexpr (WORDS % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < WORDS / 4; q++) reinterpret_cast<uint4*>(dst)[q] = reinterpret_cast<const uint4*>(words)[q];
+    } else {
+#pragma unroll
+        for (int q = 0; q < WORDS / 2; q++) reinterpret_cast<uint2*>(dst)[q] = reinterpret_cast<const uint2*>(words)[q];
     }
 }
 
@@ -414,10 +497,17 @@ extern "C" int eq_quantize(uint32_t* w_out, void* scales, void* biases, const vo
         constexpr int B = decltype(bc)::value;
         with_dtype(dtype, [&](auto tt) {
             typedef decltype(tt) T;
-            quantize_kernel<B, T><<<grid, 256, 0, st>>>(w_out, static_cast<typename T::storage*>(scales),
-                                                        static_cast<typename T::storage*>(biases),
-                                                        static_cast<const typename T::storage*>(w), groups,
-                                                        group_size);
+            typedef typename T::storage S;
+            S* sp = static_cast<S*>(scales);
+            S* bp = static_cast<S*>(biases);
+            const S* wp = static_cast<const S*>(w);
+            if (aligned(w, 16) && aligned(w_out, 16)) {
+                if (group_size == 32) quantize_vec_kernel<B, T, 32><<<grid, 256, 0, st>>>(w_out, sp, bp, wp, groups);
+                else if (group_size == 64) quantize_vec_kernel<B, T, 64><<<grid, 256, 0, st>>>(w_out, sp, bp, wp, groups);
+                else quantize_vec_kernel<B, T, 128><<<grid, 256, 0, st>>>(w_out, sp, bp, wp, groups);
+            } else {
+                quantize_kernel<B, T><<<grid, 256, 0, st>>>(w_out, sp, bp, wp, groups, group_size);
+            }
         });
     });
     return check_launch("quantize");
@@ -450,9 +540,16 @@ extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, c
             typedef decltype(stt) ST;
             with_dtype(out_dtype, [&](auto ot) {
                 typedef decltype(ot) OT;
-                dequant_kernel<B, ST, OT><<<grid, 256, 0, st>>>(
-                    static_cast<typename OT::storage*>(out), w, static_cast<const typename ST::storage*>(scales),
-                    static_cast<const typename ST::storage*>(biases), rows, cols, group_size);
+                typedef typename OT::storage OS;
+                typedef typename ST::storage SS;
+                if (aligned(out, 16))
+                    dequant_kernel<B, ST, OT, true><<<grid, 256, 0, st>>>(
+                        static_cast<OS*>(out), w, static_cast<const SS*>(scales), static_cast<const SS*>(biases), rows,
+                        cols, group_size);
+                else
+                    dequant_kernel<B, ST, OT, false><<<grid, 256, 0, st>>>(
+                        static_cast<OS*>(out), w, static_cast<const SS*>(scales), static_cast<const SS*>(biases), rows,
+                        cols, group_size);
             });
         });
     });

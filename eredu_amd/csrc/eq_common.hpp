@@ -213,6 +213,12 @@ template <> __device__ __forceinline__ void store_out<BF16T>(uint16_t* p, int64_
 template <> __device__ __forceinline__ void store_out<F16T>(uint16_t* p, int64_t i, float v) { p[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
 template <> __device__ __forceinline__ void store_out<F32T>(float* p, int64_t i, float v) { p[i] = v; }
 
+// The storage bits store_out writes (RNE to the output type).
+template <typename T> __device__ __forceinline__ typename T::storage to_storage(float v);
+template <> __device__ __forceinline__ uint16_t to_storage<BF16T>(float v) { return static_cast<uint16_t>(f32_to_bf16_bits(v)); }
+template <> __device__ __forceinline__ uint16_t to_storage<F16T>(float v) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v)); }
+template <> __device__ __forceinline__ float to_storage<F32T>(float v) { return v; }
+
 // ------------------------------------------------------ small vector helpers
 
 // 16-byte streaming load: the weight blocks are read once, so they are not

@@ -54,3 +54,28 @@ def test_quantize_leading_dims_and_defaults(cuda):
     assert tuple(wq.shape) == (2, 3, 32) and tuple(s.shape) == (2, 3, 4) and s.dtype == torch.bfloat16
     wq2, s2, b2 = quantize(w.reshape(6, 256))
     assert torch.equal(wq.reshape(6, 32), wq2) and torch.equal(s.reshape(6, 4), s2)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_unaligned_buffers_take_the_scalar_kernels(cuda, bits):
+    """Input / output pointers off 16-byte alignment run the one-value-per-step
+    kernels; their results equal the vector kernels' bit for bit."""
+    from eredu_amd import _native as n
+
+    rows, cols, gs = 9, 256, 64
+    rng = np.random.default_rng(bits)
+    w = torch.from_numpy((rng.standard_normal(rows * cols) * 0.02).astype(np.float32)).to(torch.bfloat16)
+    buf = torch.empty(rows * cols + 1, dtype=torch.bfloat16, device="cuda")
+    buf[1:] = w.cuda()
+    w_off = buf[1:].view(rows, cols)  # 2 bytes past a 16-byte boundary
+    assert w_off.data_ptr() % 16 != 0
+    q0, s0, b0 = quantize_with_mode(w.cuda().view(rows, cols), gs, bits)
+    q1, s1, b1 = quantize_with_mode(w_off, gs, bits)
+    assert torch.equal(q0, q1) and torch.equal(s0.view(torch.int16), s1.view(torch.int16))
+    assert torch.equal(b0.view(torch.int16), b1.view(torch.int16))
+    out = torch.empty(rows * cols + 1, dtype=torch.bfloat16, device="cuda")
+    d0 = dequantize(q0, s0, b0, group_size=gs, bits=bits)
+    n.check(n.lib().eq_dequantize(out.data_ptr() + 2, q0.data_ptr(), s0.data_ptr(), b0.data_ptr(), rows, cols, gs,
+                                  bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, 0))
+    torch.cuda.synchronize()
+    assert torch.equal(out[1:].view(rows, cols).view(torch.int16), d0.view(torch.int16))
