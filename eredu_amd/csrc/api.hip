@@ -94,11 +94,11 @@ __global__ __launch_bounds__(256) void dequant_kernel(typename OT::storage* __re
         if constexpr (BYTES % 16 == 0) {
 #pragma unroll
             for (int q = 0; q < BYTES / 16; q++)
-                reinterpret_cast<uint4*>(out + base)[q] = reinterpret_cast<const uint4*>(v)[q];
+                store_stream16(reinterpret_cast<uint4*>(out + base) + q, reinterpret_cast<const uint4*>(v)[q]);
         } else {
 #pragma unroll
             for (int q = 0; q < BYTES / 8; q++)
-                reinterpret_cast<uint2*>(out + base)[q] = reinterpret_cast<const uint2*>(v)[q];
+                store_stream8(reinterpret_cast<uint2*>(out + base) + q, reinterpret_cast<const uint2*>(v)[q]);
         }
     } else {
 #pragma unroll

@@ -118,13 +118,14 @@ __device__ __forceinline__ void store8<BF16T>(uint16_t* out, int64_t base, const
     uint32_t p[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) p[j] = f32_to_bf16_bits(v[2 * j]) | (f32_to_bf16_bits(v[2 * j + 1]) << 16);
-    *reinterpret_cast<uint4*>(out + base) = make_uint4(p[0], p[1], p[2], p[3]);
+    store_stream16(out + base, make_uint4(p[0], p[1], p[2], p[3]));
 }
 template <>
 __device__ __forceinline__ void store8<F32T>(float* out, int64_t base, const float v[8]) {
-    float4* o = reinterpret_cast<float4*>(out + base);
-    o[0] = make_float4(v[0], v[1], v[2], v[3]);
-    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    store_stream16(out + base, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                          __float_as_uint(v[3])));
+    store_stream16(out + base + 4, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                              __float_as_uint(v[7])));
 }
 
 // Q4_0 dense: affine route only (Q4_0 has no native decoder, format.rs:423-428):
