@@ -150,7 +150,7 @@ def quantize_tensor(weight: torch.Tensor, quantization: WeightQuantization
     """Packed uint32 codes, scales and biases of one floating-point weight of
     rank >= 2, grouped along its last axis (leading dimensions, an expert
     bank's included, kept; quantization.rs:169-224), on the GPU with
-    eq_quantize (affine; gs 32/64/128 and bits 2/4/8 on this device path)."""
+    eq_quantize (affine; bits 2, 3, 4, 5, 6 or 8, group size 16 or a multiple of 32)."""
     quantization.validate()
     if weight.dim() < 2 or not weight.dtype.is_floating_point:
         raise EreduError(f"expected a floating-point weight with at least two dimensions, got shape "

@@ -106,6 +106,41 @@ __global__ __launch_bounds__(256) void dequant_kernel(typename OT::storage* __re
     }
 }
 
+// 3-, 5- and 6-bit codes (an LSB-first bit stream, eredu-gguf/src/convert.rs:413-427):
+// one thread per CPT codes -- 32 (BITS words) for 3 and 5 bits, 16 (3 words)
+// for 6 bits.  A packed row holds whole words, so cols is a multiple of CPT
+// and a thread's codes lie in one row; at group size 16 they span two groups.
+template <int BITS, typename ST, typename OT>
+__global__ __launch_bounds__(256) void dequant_odd_kernel(typename OT::storage* __restrict__ out,
+                                                          const uint32_t* __restrict__ w,
+                                                          const typename ST::storage* __restrict__ s,
+                                                          const typename ST::storage* __restrict__ b, int64_t rows,
+                                                          int64_t cols, int gs) {
+    constexpr int CPT = BITS == 6 ? 16 : 32, WPT = CPT * BITS / 32;
+    const int64_t units = rows * cols / CPT;
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= units) return;
+    uint32_t wd[WPT + 1];
+#pragma unroll
+    for (int j = 0; j < WPT; j++) wd[j] = w[i * WPT + j];
+    wd[WPT] = 0u;
+    const int64_t base = i * CPT;
+    const int64_t r = base / cols, c0 = base % cols;
+    const int64_t g0 = r * (cols / gs);
+#pragma unroll
+    for (int p = 0; p < CPT; p++) {
+        constexpr uint32_t mask = (1u << BITS) - 1u;
+        const int bit = p * BITS, wi = bit >> 5, sh = bit & 31;
+        uint32_t q = wd[wi] >> sh;
+        if (sh + BITS > 32) q |= wd[wi + 1] << (32 - sh);
+        q &= mask;
+        const int64_t g = g0 + (c0 + p) / gs;
+        const float sc = load_param<ST>(s, g);
+        const float bi = b ? load_param<ST>(b, g) : 0.f;
+        out[base + p] = to_storage<OT>(__fadd_rn(sc * float(q), bi));
+    }
+}
+
 // --------------------------------------------------------------- dispatch
 
 }  // namespace
@@ -158,6 +193,57 @@ __global__ __launch_bounds__(256) void quantize_kernel(uint32_t* __restrict__ wq
             word |= uint32_t(q) << (BITS * e);
         }
         dst[w0] = word;
+    }
+}
+
+// quantize_kernel for 3-, 5- and 6-bit codes: one thread per unit of `gpu`
+// consecutive groups (2 when one group's codes do not fill whole words, group
+// size 16 at 3 or 5 bits), the same arithmetic per group, codes appended to an
+// LSB-first bit stream (eredu-gguf/src/convert.rs:413-427 `pack`).
+template <int BITS, typename T>
+__global__ __launch_bounds__(256) void quantize_odd_kernel(uint32_t* __restrict__ wq,
+                                                           typename T::storage* __restrict__ sc,
+                                                           typename T::storage* __restrict__ bi,
+                                                           const typename T::storage* __restrict__ w, int64_t units,
+                                                           int gs, int gpu) {
+    const int64_t unit = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (unit >= units) return;
+    constexpr int n_bins = (1 << BITS) - 1;
+    uint32_t* dst = wq + unit * (int64_t(gs) * gpu * BITS / 32);
+    uint64_t acc = 0;
+    int nacc = 0, wo = 0;
+    for (int gi = 0; gi < gpu; gi++) {
+        const int64_t gidx = unit * gpu + gi;
+        const typename T::storage* v = w + gidx * gs;
+        float mn = load_param<T>(v, 0), mx = mn;
+        for (int i = 1; i < gs; i++) {
+            const float x = load_param<T>(v, i);
+            mn = x < mn ? x : mn;
+            mx = x > mx ? x : mx;
+        }
+        float scale = (mx - mn) / float(n_bins);
+        if (scale < 1e-7f) scale = 1e-7f;
+        const bool neg = fabsf(mn) > fabsf(mx);
+        scale = neg ? scale : -scale;
+        const float edge = neg ? mn : mx;
+        const float q0 = rintf(edge / scale);
+        if (q0 != 0.0f) scale = edge / q0;
+        store_out<T>(sc, gidx, scale);
+        store_out<T>(bi, gidx, edge);
+        const float s_st = load_param<T>(sc, gidx), b_st = load_param<T>(bi, gidx);
+        for (int i = 0; i < gs; i++) {
+            const float x = load_param<T>(v, i);
+            float q = s_st != 0.0f ? rintf((x - b_st) / s_st) : 0.0f;
+            q = q >= 0.0f ? q : 0.0f;
+            q = q > float(n_bins) ? float(n_bins) : q;
+            acc |= uint64_t(uint32_t(q)) << nacc;
+            nacc += BITS;
+            if (nacc >= 32) {
+                dst[wo++] = uint32_t(acc);
+                acc >>= 32;
+                nacc -= 32;
+            }
+        }
     }
 }
 
@@ -252,6 +338,7 @@ extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, co
                   std::to_string(group_size));
         return 1;
     }
+    if (!check_packed_row(packed_dim, bits)) return 1;
     if (!y || !x || !w || !scales) {
         set_error("null pointer argument");
         return 1;
@@ -337,6 +424,10 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
         if (packed_dim % group_size != 0) {
             set_error("problem " + std::to_string(i) + ": the quantized dimension (" + std::to_string(packed_dim) +
                       ") is not divisible by group_size " + std::to_string(group_size));
+            return 1;
+        }
+        if (!check_packed_row(packed_dim, bits)) {
+            set_error("problem " + std::to_string(i) + ": " + eq_last_error());
             return 1;
         }
         if (!p.y || !p.x || !p.w || !p.scales) {
@@ -481,6 +572,7 @@ extern "C" int eq_quantize(uint32_t* w_out, void* scales, void* biases, const vo
         set_error("cols must be a non-negative multiple of group_size");
         return 1;
     }
+    if (!check_packed_row(cols, bits)) return 1;
     if (rows == 0 || cols == 0) return 0;
     if (!w_out || !scales || !biases || !w) {
         set_error("null pointer argument");
@@ -501,7 +593,13 @@ extern "C" int eq_quantize(uint32_t* w_out, void* scales, void* biases, const vo
             S* sp = static_cast<S*>(scales);
             S* bp = static_cast<S*>(biases);
             const S* wp = static_cast<const S*>(w);
-            if (aligned(w, 16) && aligned(w_out, 16)) {
+            if constexpr (32 % B != 0) {
+                // a unit of whole words: one group, or two at group size 16
+                const int gpu = (int64_t(group_size) * B) % 32 == 0 ? 1 : 2;
+                const int64_t units = groups / gpu;
+                quantize_odd_kernel<B, T><<<dim3(unsigned((units + 255) / 256)), 256, 0, st>>>(w_out, sp, bp, wp, units,
+                                                                                             group_size, gpu);
+            } else if (aligned(w, 16) && aligned(w_out, 16) && fast_group_size(group_size)) {
                 if (group_size == 32) quantize_vec_kernel<B, T, 32><<<grid, 256, 0, st>>>(w_out, sp, bp, wp, groups);
                 else if (group_size == 64) quantize_vec_kernel<B, T, 64><<<grid, 256, 0, st>>>(w_out, sp, bp, wp, groups);
                 else quantize_vec_kernel<B, T, 128><<<grid, 256, 0, st>>>(w_out, sp, bp, wp, groups);
@@ -526,6 +624,7 @@ extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, c
         set_error("cols must be a non-negative multiple of group_size");
         return 1;
     }
+    if (!check_packed_row(cols, bits)) return 1;
     if (rows == 0 || cols == 0) return 0;
     if (!out || !w || !scales) {
         set_error("null pointer argument");
@@ -542,7 +641,13 @@ extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, c
                 typedef decltype(ot) OT;
                 typedef typename OT::storage OS;
                 typedef typename ST::storage SS;
-                if (aligned(out, 16))
+                if constexpr (32 % B != 0) {
+                    constexpr int CPT = B == 6 ? 16 : 32;
+                    const int64_t units = rows * cols / CPT;
+                    dequant_odd_kernel<B, ST, OT><<<dim3(unsigned((units + 255) / 256)), 256, 0, st>>>(
+                        static_cast<OS*>(out), w, static_cast<const SS*>(scales), static_cast<const SS*>(biases), rows,
+                        cols, group_size);
+                } else if (aligned(out, 16))
                     dequant_kernel<B, ST, OT, true><<<grid, 256, 0, st>>>(
                         static_cast<OS*>(out), w, static_cast<const SS*>(scales), static_cast<const SS*>(biases), rows,
                         cols, group_size);

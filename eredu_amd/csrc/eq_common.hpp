@@ -171,7 +171,10 @@ template <typename F>
 inline bool with_bits(int bits, F&& f) {
     switch (bits) {
     case 2: f(std::integral_constant<int, 2>{}); return true;
+    case 3: f(std::integral_constant<int, 3>{}); return true;
     case 4: f(std::integral_constant<int, 4>{}); return true;
+    case 5: f(std::integral_constant<int, 5>{}); return true;
+    case 6: f(std::integral_constant<int, 6>{}); return true;
     case 8: f(std::integral_constant<int, 8>{}); return true;
     default: return false;
     }
@@ -189,18 +192,34 @@ inline int check_mode(const char* mode) {
     return 1;
 }
 
-// Group size / bits rules of the affine contract (eredu-checkpoint/src/lib.rs:69-123,
-// safemlx/src/ops/quantization.rs:62-64); this library implements gs 32/64/128, bits 2/4/8.
+// Group size / bits rules of the affine contract (eredu-checkpoint/src/lib.rs:103-122,
+// safemlx/src/ops/quantization.rs:62-64): bits 2, 3, 4, 5, 6 or 8; group size 16
+// or a positive multiple of 32.  The fast kernels take bits 4 / 8 at group
+// sizes 32, 64 and 128; every other combination runs on the general kernels.
 inline int check_gs_bits(int group_size, int bits) {
-    if (bits != 2 && bits != 4 && bits != 8) {
-        set_error("bits must be 2, 4 or 8 on this device path, got " + std::to_string(bits));
+    if (bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8) {
+        set_error("bits must be one of 2, 3, 4, 5, 6 or 8, got " + std::to_string(bits));
         return 1;
     }
-    if (group_size != 32 && group_size != 64 && group_size != 128) {
-        set_error("group_size must be 32, 64 or 128, got " + std::to_string(group_size));
+    if (group_size != 16 && (group_size <= 0 || group_size % 32 != 0)) {
+        set_error("group_size must be 16 or a positive multiple of 32, got " + std::to_string(group_size));
         return 1;
     }
     return 0;
+}
+
+// Group sizes the fast (templated) kernels are built for.
+inline bool fast_group_size(int gs) { return gs == 32 || gs == 64 || gs == 128; }
+
+// A packed row of `dim` codes must fill whole u32 words (quantized_packed_dimension
+// is dim * bits / 32); false, with the error set, otherwise.
+inline bool check_packed_row(int64_t dim, int bits) {
+    if ((dim * bits) % 32 != 0) {
+        set_error("a packed row of " + std::to_string(dim) + " " + std::to_string(bits) +
+                  "-bit codes does not fill whole 32-bit words");
+        return false;
+    }
+    return true;
 }
 
 template <typename T> __device__ __forceinline__ float load_param(const typename T::storage* p, int64_t i);
@@ -313,11 +332,21 @@ bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* 
 
 // ------------------------------------------------------------ general bodies
 
-// LSB-first code c of a packed row (bits in {2, 4, 8} never straddle words).
+// LSB-first code c of a packed row (codes of 2, 4 or 8 bits never straddle words).
 template <int BITS>
 __device__ __forceinline__ uint32_t code_at(const uint32_t* row, int64_t c) {
-    constexpr int PACK = 32 / BITS;
-    return (row[c / PACK] >> ((c % PACK) * BITS)) & ((1u << BITS) - 1u);
+    if constexpr (32 % BITS == 0) {
+        constexpr int PACK = 32 / BITS;
+        return (row[c / PACK] >> ((c % PACK) * BITS)) & ((1u << BITS) - 1u);
+    } else {
+        // 3-, 5- and 6-bit codes: an LSB-first bit stream whose codes may
+        // straddle two words (eredu-gguf/src/convert.rs:413-427 `pack`)
+        const int64_t bit = c * BITS;
+        const int sh = int(bit & 31);
+        uint32_t v = row[bit >> 5] >> sh;
+        if (sh + BITS > 32) v |= row[(bit >> 5) + 1] << (32 - sh);
+        return v & ((1u << BITS) - 1u);
+    }
 }
 
 constexpr int kGenRowsPerWG = 4;

@@ -234,6 +234,7 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
                   std::to_string(group_size));
         return 1;
     }
+    if (!check_packed_row(packed_dim, bits)) return 1;
     if (!lhs_indices && x_batches != batch && x_batches != 1) {
         set_error("without lhs_indices, x must have one batch or as many as the output");
         return 1;
@@ -269,7 +270,7 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
                                       int(batch), x_batches, int(w_batches), int(N), int(K), st))
         return check_launch("gather_qmm (grouped qmm)");
     const bool fast = transpose && M == 1 && x_dtype == EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F32 &&
-                      (bits == 4 || bits == 8) && aligned(x, 16) && aligned(w, 16);
+                      (bits == 4 || bits == 8) && fast_group_size(group_size) && aligned(x, 16) && aligned(w, 16);
     if (!transpose && M <= 8 && x_dtype == EQ_DTYPE_BF16 &&
         launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales,
                            biases, g, batch, int(M), int(N), int(K), group_size, st))

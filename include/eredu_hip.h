@@ -62,7 +62,10 @@ int eq_version(void);
  *   the u32 words (eredu-gguf/src/convert.rs:87-99,413-427).
  * x is [M, K] of x_dtype (leading batch dims flattened into M), y is [M, N] of
  * x_dtype.  biases may be NULL (treated as zero).  mode must be "affine" (or
- * NULL).  bits in {2, 4, 8}; group_size in {32, 64, 128}.  Accumulation is f32.
+ * NULL).  bits in {2, 3, 4, 5, 6, 8} (3/5/6-bit codes form an LSB-first bit
+ * stream and may straddle words; a packed row holds whole words); group_size
+ * 16 or a positive multiple of 32 (eredu-checkpoint/src/lib.rs:103-122).
+ * Accumulation is f32.
  */
 int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                         const void* biases, int64_t M, int64_t N, int64_t K, bool transpose,
@@ -174,7 +177,7 @@ int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
  * edge value made exactly representable, bias = edge, codes rounded from the
  * stored scale and bias.  Replaces mlx_quantize (ops.h:801-808) under
  * safemlx::ops::quantize_with_mode (safemlx/src/ops/quantization.rs:100-159).
- * bits in {2, 4, 8}; group_size in {32, 64, 128}.
+ * bits and group_size as for eq_quantized_matmul.
  */
 int eq_quantize(uint32_t* w_out, void* scales, void* biases, const void* w, int64_t rows, int64_t cols,
                 int group_size, int bits, const char* mode, int dtype, eq_stream_t stream);

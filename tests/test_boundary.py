@@ -63,8 +63,10 @@ def call_qmm(**kw):
 @pytest.mark.parametrize(
     "kw,needle",
     [
-        (dict(gs=48), "group_size must be 32, 64 or 128"),
-        (dict(bits=3), "bits must be 2, 4 or 8"),
+        (dict(gs=48), "group_size must be 16 or a positive multiple of 32"),
+        (dict(bits=7), "bits must be one of 2, 3, 4, 5, 6 or 8"),
+        (dict(bits=3, gs=16, K=16), "does not fill whole 32-bit words"),
+        (dict(bits=5, gs=16, transpose=False, N=16), "does not fill whole 32-bit words"),
         (dict(K=96), "not divisible by group_size"),
         (dict(transpose=False, N=40), "not divisible by group_size"),
         (dict(mode=b"mxfp4"), "mxfp4"),
@@ -91,7 +93,7 @@ def test_error_message_is_thread_local():
 
     def other():
         seen["before"] = L.eq_last_error().decode()
-        call_qmm(bits=3)
+        call_qmm(bits=7)
         seen["after"] = L.eq_last_error().decode()
 
     t = threading.Thread(target=other)
@@ -184,7 +186,8 @@ def test_quantize_rejects_bad_arguments():
     bf16 = _native.EQ_DTYPE_BF16
     _rejects(L.eq_quantize(16, 16, 16, 16, 4, 100, 64, 4, b"affine", bf16, None), "multiple of group_size")
     _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 48, 4, b"affine", bf16, None), "group")
-    _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 64, 5, b"affine", bf16, None), "bits")
+    _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 64, 7, b"affine", bf16, None), "bits")
+    _rejects(L.eq_quantize(16, 16, 16, 16, 4, 16, 16, 3, b"affine", bf16, None), "whole 32-bit words")
     _rejects(L.eq_quantize(16, 16, 16, 16, 4, 128, 64, 4, b"affine", 9, None), "dtype")
     _rejects(L.eq_quantize(None, 16, 16, 16, 4, 128, 64, 4, b"affine", bf16, None), "null")
     assert L.eq_quantize(16, 16, 16, 16, 0, 128, 64, 4, b"affine", bf16, None) == 0
@@ -215,7 +218,8 @@ def test_gather_qmm_rejects_bad_arguments():
         return L.eq_gather_qmm(*a)
 
     _rejects(call(gs=48), "group_size")
-    _rejects(call(bits=3), "bits")
+    _rejects(call(bits=7), "bits")
+    _rejects(call(bits=3, gs=16, K=16), "whole 32-bit words")
     _rejects(call(mode=b"mxfp4"), "mxfp4")
     _rejects(call(xd=7), "dtype")
     _rejects(call(K=96), "divisible")

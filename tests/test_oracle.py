@@ -313,3 +313,61 @@ def test_tolerance_rule_rejects_planted_errors():
     x_rev = x[:, ::-1].copy()
     y_rev = orc.quantized_matmul_f64(x_rev, orc.BF16, w, s, b, orc.BF16, True, gs, bits, N, K)
     assert not orc.matmul_within_tolerance(y_rev, y, True)[0]
+
+
+def _pack_bitstream(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Rows of codes as one Python integer each, code i at bit i * bits
+    (eredu-gguf/src/convert.rs:413-427: LSB-first, a code may straddle two
+    words), cut into 32-bit words."""
+    rows, cols = codes.shape
+    words = cols * bits // 32
+    out = np.zeros((rows, words), dtype=np.uint32)
+    for r in range(rows):
+        stream = 0
+        for i, c in enumerate(codes[r]):
+            stream |= int(c) << (i * bits)
+        for j in range(words):
+            out[r, j] = (stream >> (32 * j)) & 0xFFFFFFFF
+    return out
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_unpack_matches_the_reference_bit_stream(bits):
+    """Both oracle unpackers (numpy and C) read the reference packer's bit
+    stream back, including 3-, 5- and 6-bit codes that straddle words."""
+    rng = np.random.default_rng(bits)
+    rows, cols = 3, 96
+    codes = rng.integers(0, 1 << bits, size=(rows, cols), dtype=np.uint32)
+    codes[0, :] = (1 << bits) - 1  # all ones: every straddling bit is set
+    w = _pack_bitstream(codes, bits)
+    assert np.array_equal(orc.unpack_codes(w, cols, bits), codes)
+    ones = np.ones((rows, cols // 16), dtype=np.float32)
+    zeros = np.zeros_like(ones)
+    assert np.array_equal(orc.affine_dequant_f32(w, ones, zeros, orc.F32, rows, cols, 16, bits),
+                          codes.astype(np.float32))
+
+
+@pytest.mark.parametrize("bits", [3, 5, 6])
+@pytest.mark.parametrize("gs", [16, 32])
+def test_quantize_odd_widths_round_trip(bits, gs):
+    """The oracle quantizer at 3/5/6 bits packs a stream the reference's
+    packer would produce from its codes, and meets the round-trip bound."""
+    rng = np.random.default_rng(bits * 100 + gs)
+    rows, cols = 5, 96
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    wq, s, b = orc.quantize_affine(w, gs, bits, orc.F32)
+    assert wq.shape == (rows, cols * bits // 32)
+    codes = orc.unpack_codes(wq, cols, bits)
+    assert np.array_equal(_pack_bitstream(codes, bits), wq)
+    w_hat = orc.affine_dequant_f32(wq, s, b, orc.F32, rows, cols, gs, bits)
+    # MLX's edge rule: the group's larger-magnitude extreme is the bias and
+    # dequantizes exactly; the opposite extreme may clamp, so the bound is one
+    # step rather than half of one
+    g = w.reshape(rows, cols // gs, gs)
+    mn, mx = g.min(axis=2), g.max(axis=2)
+    edge = np.where(np.abs(mn) > np.abs(mx), mn, mx)
+    assert np.array_equal(b, edge)
+    at_edge = g == edge[:, :, None]
+    assert np.array_equal(w_hat.reshape(g.shape)[at_edge], g[at_edge])
+    step = np.repeat(np.abs(s), gs, axis=1)
+    assert np.all(np.abs(w_hat - w) <= step * (1 + 1e-5))
