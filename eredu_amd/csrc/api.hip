@@ -2,13 +2,16 @@
 // (any activation/scale dtype, any layout) quantized matmul and dequantize
 // kernels that back the shapes the matrix-core paths do not take.
 //
-// Dispatch of eq_quantized_matmul (transpose = true, bf16 activations,
-// bits 4/8, bf16/f16 scales):
-//   M <= 16  -> qmv_mfma (qmv.hip), the decode path
-//   M  > 16  -> qmm_mfma (qmm.hip), the prefill path (N % 128 == 0)
-// Everything else (f32/f16 activations, f32 scales, bits 2, transpose =
-// false, ragged N) runs the f32 kernels below.  There is no host fallback: a
-// shape no kernel takes is an error.
+// Dispatch of eq_quantized_matmul:
+//   transpose, bf16 x, bits 4/8, bf16/f16 scales, group size 32/64/128:
+//     M <= 16  -> qmv (qmv.hip), the decode path (N % 16 == 0)
+//     M  > 16  -> qmm_mfma (qmm.hip), the prefill path (N % 128 == 0, K % 64 == 0)
+//   transpose = false, bf16 x, bits 4/8, M <= 8 -> qmm_n (qmm_n.hip)
+// Everything else -- f32/f16 activations, f32 scales, bits 2/3/5/6 (3/5/6-bit
+// codes form an LSB-first bit stream), group size 16 or a multiple of 32
+// other than 32/64/128, the remaining transpose = false shapes, ragged N --
+// runs the f32 kernels below.  There is no host fallback: a shape no kernel
+// takes is an error.
 #include <cstring>
 #include <vector>
 #include <type_traits>
@@ -30,9 +33,6 @@ int check_launch(const char* what) {
     }
     return 0;
 }
-
-bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
-                     const void* s, const void* b, int M, int N, int K, hipStream_t st);
 
 namespace {
 
@@ -317,10 +317,12 @@ extern "C" const char* eq_last_error(void) { return g_last_error.c_str(); }
 
 extern "C" int eq_version(void) { return 100; }
 
-extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
-                                   int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
-                                   const char* mode, int x_dtype, int scale_dtype, eq_stream_t stream) {
-    clear_error();
+// eq_quantized_matmul with the scratch memory of split-K launches taken from
+// `ws` (null: the library workspace).
+static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                                 int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
+                                 const char* mode, int x_dtype, int scale_dtype, const WsSource* ws,
+                                 eq_stream_t stream) {
     if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
     if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype)) {
         set_error("invalid dtype code");
@@ -360,13 +362,13 @@ extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, co
     }
     if (mfma_ok && M > 16 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8)) {
         if (launch_qmm_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
-                            w, scales, biases, int(M), int(N), int(K), st))
+                            w, scales, biases, int(M), int(N), int(K), ws, st))
             return check_launch("quantized_matmul (qmm)");
     }
     if (!transpose && x_dtype == EQ_DTYPE_BF16 && M <= 8) {
         const GatherIdx one{nullptr, nullptr, 1, 1};
         if (launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w,
-                               scales, biases, one, 1, int(M), int(N), int(K), group_size, st))
+                               scales, biases, one, 1, int(M), int(N), int(K), group_size, ws, st))
             return check_launch("quantized_matmul (qmm_n)");
     }
 
@@ -385,10 +387,15 @@ extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, co
                         static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
                         static_cast<const SS*>(biases), M, N, K, group_size);
                 } else {
-                    const dim3 grid(unsigned((N + 255) / 256), unsigned((M + kGenMChunk - 1) / kGenMChunk));
-                    qmm_n_general<B, XT, ST><<<grid, 256, 0, st>>>(
-                        static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
-                        static_cast<const SS*>(biases), M, N, K, group_size);
+                    // grid.y is at most 65535: activation rows in pieces of 65535 * kGenMChunk
+                    const int64_t piece = int64_t(kMaxGridY) * kGenMChunk;
+                    for (int64_t m0 = 0; m0 < M; m0 += piece) {
+                        const int64_t mc = M - m0 < piece ? M - m0 : piece;
+                        const dim3 grid(unsigned((N + 255) / 256), unsigned((mc + kGenMChunk - 1) / kGenMChunk));
+                        qmm_n_general<B, XT, ST><<<grid, 256, 0, st>>>(
+                            static_cast<XS*>(y) + m0 * N, static_cast<const XS*>(x) + m0 * K, w,
+                            static_cast<const SS*>(scales), static_cast<const SS*>(biases), mc, N, K, group_size);
+                    }
                 }
                 launched = true;
             });
@@ -399,6 +406,14 @@ extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, co
         return 1;
     }
     return check_launch("quantized_matmul (general)");
+}
+
+extern "C" int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                                   int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
+                                   const char* mode, int x_dtype, int scale_dtype, eq_stream_t stream) {
+    clear_error();
+    return quantized_matmul_impl(y, x, w, scales, biases, M, N, K, transpose, group_size, bits, mode, x_dtype,
+                                 scale_dtype, nullptr, stream);
 }
 
 extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int count, int64_t M, bool transpose,
@@ -468,9 +483,16 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
     return 0;
 }
 
-static bool ranges_overlap(const void* a, const void* b, int64_t bytes) {
-    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
-    return x < y + uintptr_t(bytes) && y < x + uintptr_t(bytes);
+// A device byte range [p, p + bytes).
+struct ByteRange {
+    const void* p;
+    int64_t bytes;
+};
+
+static bool ranges_overlap(const ByteRange& a, const ByteRange& b) {
+    if (!a.p || !b.p || a.bytes <= 0 || b.bytes <= 0) return false;
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a.p), y = reinterpret_cast<uintptr_t>(b.p);
+    return x < y + uintptr_t(b.bytes) && y < x + uintptr_t(a.bytes);
 }
 
 extern "C" int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* problems, int count, int64_t M,
@@ -538,18 +560,35 @@ extern "C" int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* proble
             set_error("prologue: eps must be >= 0");
             return 1;
         }
-        if (pr.hidden_out && (ranges_overlap(pr.hidden_out, x, bytes) ||
-                              (pr.second && ranges_overlap(pr.hidden_out, pr.second, bytes)))) {
-            set_error("prologue: hidden_out must not overlap x or the residual (every workgroup reads them)");
-            return 1;
-        }
     }
-    for (int i = 0; i < count; i++)
-        if (ranges_overlap(problems[i].y, x, bytes) ||
-            (pr.second && ranges_overlap(problems[i].y, pr.second, bytes))) {
-            set_error("prologue: outputs must not overlap the inputs");
-            return 1;
-        }
+    // Every workgroup reads x, the second input, the norm weight and the
+    // weights of every problem while others write y_i and hidden_out: no
+    // written range may overlap a read one or another written one.
+    std::vector<ByteRange> reads{{x, bytes}, {pr.second, bytes}};
+    if (pr.kind == EQ_PROLOGUE_RMS_NORM) reads.push_back({pr.weight, bytes});
+    std::vector<ByteRange> writes;
+    for (int i = 0; i < count; i++) {
+        const eq_qmm_problem& p = problems[i];
+        const int64_t G = K / group_size;
+        reads.push_back({p.w, p.N * K * bits / 8});
+        reads.push_back({p.scales, p.N * G * 2});
+        reads.push_back({p.biases, p.N * G * 2});
+        writes.push_back({p.y, p.N * 2});
+    }
+    if (pr.kind == EQ_PROLOGUE_RMS_NORM) writes.push_back({pr.hidden_out, bytes});
+    for (size_t i = 0; i < writes.size(); i++) {
+        for (const ByteRange& r : reads)
+            if (ranges_overlap(writes[i], r)) {
+                set_error("prologue: an output (y or hidden_out) overlaps an input (x, the second input, the norm "
+                          "weight or a problem's weights, scales or biases)");
+                return 1;
+            }
+        for (size_t j = i + 1; j < writes.size(); j++)
+            if (ranges_overlap(writes[i], writes[j])) {
+                set_error("prologue: outputs (y of each problem, hidden_out) must not overlap each other");
+                return 1;
+            }
+    }
     QmvPrologue q{pr.kind, static_cast<const uint16_t*>(pr.second), static_cast<const uint16_t*>(pr.weight),
                   static_cast<uint16_t*>(pr.hidden_out), pr.eps};
     if (!launch_qmv_prologue(bits, group_size, scale_dtype, specs.data(), count, q,

@@ -396,32 +396,6 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int32_t* __restrict__ out,
     }
 }
 
-// Per-device f32 workspace of the attention partials, grown outside stream
-// capture (a capturing call whose workspace is too small fails).
-float* attn_workspace(size_t bytes, hipStream_t st) {
-    static std::mutex mu;
-    static float* ptr[64] = {};
-    static size_t cap[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    if (cap[dev] >= bytes) return ptr[dev];
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    if (ptr[dev]) {
-        if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-        (void)hipFree(ptr[dev]);
-        ptr[dev] = nullptr;
-        cap[dev] = 0;
-    }
-    void* p = nullptr;
-    const size_t want = bytes < (size_t(4) << 20) ? (size_t(4) << 20) : bytes;
-    if (hipMalloc(&p, want) != hipSuccess) return nullptr;
-    ptr[dev] = static_cast<float*>(p);
-    cap[dev] = want;
-    return ptr[dev];
-}
-
 bool bf16_only(int dtype, const char* what) {
     if (dtype != EQ_DTYPE_BF16) {
         set_error(std::string(what) + ": only bf16 is implemented");
@@ -502,9 +476,10 @@ extern "C" int eq_rope_attention_decode(void* out, const void* q, const void* k_
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int nchunks = int((pos + kAttnChunk) / kAttnChunk);
     const size_t ws_bytes = size_t(n_heads) * size_t(nchunks) * (kHeadDim + 2) * sizeof(float);
-    float* ws = attn_workspace(ws_bytes, st);
+    float* ws = static_cast<float*>(ws_acquire(nullptr, ws_bytes, st));
     if (!ws) {
-        set_error("eq_rope_attention_decode: no workspace (first call must not be under stream capture)");
+        set_error("eq_rope_attention_decode: no workspace (its stream's workspace cannot grow while capturing: "
+                  "make one call of at least this position on the stream before capturing)");
         return 1;
     }
     attn_partial_kernel<<<dim3(unsigned(n_kv_heads), unsigned(nchunks)), dim3(256), 0, st>>>(

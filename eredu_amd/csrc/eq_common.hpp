@@ -305,10 +305,19 @@ __device__ __forceinline__ bool gather_batch(const GatherIdx& g, int64_t b, int6
     return xb >= 0 && xb < g.x_batches && wb >= 0 && wb < g.w_batches;
 }
 
-// Split-K partial sums: a per-device f32 buffer of at least `bytes`, grown
-// (never while `st` is capturing) and kept until the process ends; null if it
-// cannot be provided.  Launches that use it on one device are stream-ordered.
-float* qmm_workspace(size_t bytes, hipStream_t st);
+// Where a launch's scratch memory comes from: a fixed region (ptr, cap) that
+// the caller owns, or, for a null WsSource*, the library's workspace of the
+// current device and `st` (workspace.hip: grow-only, never freed while the
+// process runs, one buffer per stream).
+struct WsSource {
+    void* ptr;
+    size_t cap;
+};
+
+// At least `bytes` of device scratch, 256-byte aligned, or null when none can
+// be provided (fixed region too small, or the library buffer would have to
+// grow while `st` is capturing).  Launches that use it are ordered on `st`.
+void* ws_acquire(const WsSource* src, size_t bytes, hipStream_t st);
 
 // Routed experts over sorted expert indices (gather_qmm with sorted_indices,
 // transpose, one activation row per route, bf16 x, 4/8-bit, bf16/f16
@@ -322,13 +331,21 @@ bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const ui
                         const void* s, const void* b, const int32_t* lhs, const int32_t* rhs, int batch,
                         int64_t x_batches, int experts, int N, int K, hipStream_t st);
 
+// Prefill qmm (qmm.hip): M > 16, x bf16, transpose, 4/8-bit, bf16/f16 scales,
+// N % 128 == 0, K % 64 == 0, 16-byte aligned x and w, 8-byte aligned y.  Any
+// buffer size: launches are split so that every buffer offset fits 32 bits.
+// Split K takes its partial tiles from `ws` (null: the library workspace);
+// without room for them the launch runs unsplit.
+bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                     const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st);
+
 // x . W for W [K, N] packed along N (transpose = false), M <= 8 activation
 // rows per batch, bf16 x and y, bf16/f16 scales, 4- or 8-bit codes; batches
 // through g (y [batch, M, N]).  False (nothing launched) for other
 // combinations.
 bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
                         const void* b, const GatherIdx& g, int64_t batch, int M, int N, int K, int gs,
-                        hipStream_t st);
+                        const WsSource* ws, hipStream_t st);
 
 // ------------------------------------------------------------ general bodies
 
@@ -351,6 +368,7 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t* row, int64_t c) {
 
 constexpr int kGenRowsPerWG = 4;
 constexpr int kGenMChunk = 8;
+constexpr int64_t kMaxGridY = 65535;  // largest grid y / z dimension of a launch
 
 // transpose = true, output feature n by one wave (lane = 0..63): lanes stride
 // over K, activations in chunks of kGenMChunk rows, f32 arithmetic

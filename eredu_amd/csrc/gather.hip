@@ -202,7 +202,6 @@ void launch_gather_qmv_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t
     else launch_gather_qmv<BITS, 128, ST>(y, x, w, s, bz, g, b0, nb, N, K, st);
 }
 
-constexpr int64_t kMaxGridY = 65535;  // batches per launch (grid y / z)
 
 }  // namespace
 }  // namespace eq
@@ -273,7 +272,7 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
                       (bits == 4 || bits == 8) && fast_group_size(group_size) && aligned(x, 16) && aligned(w, 16);
     if (!transpose && M <= 8 && x_dtype == EQ_DTYPE_BF16 &&
         launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales,
-                           biases, g, batch, int(M), int(N), int(K), group_size, st))
+                           biases, g, batch, int(M), int(N), int(K), group_size, nullptr, st))
         return check_launch("gather_qmm (qmm_n)");
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const unsigned nb = unsigned(batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY);

@@ -136,7 +136,7 @@ struct QmmArgs {
     const uint32_t* w;
     const uint16_t* s;
     const uint16_t* b;  // may be null
-    int M, N, K, mtiles, ntiles, splits, cps;  // cps: chunks per split
+    int M, N, K, ldy, mtiles, ntiles, splits, cps;  // cps: chunks per split; ldy: y row stride
     // Grouped (routed experts, no split K): row tile tm of the grid is entry
     // groups[tm] = {expert, first row, rows, row offset} of a device-built
     // list; x and y rows [first, first + rows) belong to the expert, whose
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         const int4 gd = args.groups[tm];
         if (gd.x < 0) return;  // unused entry: the whole workgroup leaves before any barrier
         xp += int64_t(gd.y) * K;
-        yp += int64_t(gd.y) * N;
+        yp += int64_t(gd.y) * args.ldy;
         M = gd.z;
         m0 = gd.w;
         wp += int64_t(gd.x) * N * (K * BITS / 32);
@@ -198,7 +198,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const int steps = (nloc + 1) / 2;  // chunks per K-group (the second may have one fewer)
 
     const __amdgpu_buffer_rsrc_t xr = raw_rsrc(xp, uint32_t(M) * uint32_t(K) * 2u);
-    const __amdgpu_buffer_rsrc_t wr = raw_rsrc(wp, uint32_t(N) * uint32_t(K) * BITS / 8u);
+    const uint32_t row_bytes = uint32_t(K) * BITS / 8u;  // (the launcher keeps N * row_bytes below 2^31)
+    const __amdgpu_buffer_rsrc_t wr = raw_rsrc(wp, uint32_t(N) * row_bytes);
     const __amdgpu_buffer_rsrc_t sr = raw_rsrc(sp, uint32_t(N) * uint32_t(G) * 2u);
     const __amdgpu_buffer_rsrc_t br = raw_rsrc(bp ? bp : sp, bp ? uint32_t(N) * uint32_t(G) * 2u : 0u);
 
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const uint32_t n = uint32_t(n0 + 64 * wave + 32 * j + l32);
-        woff[j] = int(n) < N ? n * uint32_t(K) * BITS / 8u + uint32_t(32 * kb) * BITS / 8u : kOutOfRange;
+        woff[j] = int(n) < N ? n * row_bytes + uint32_t(32 * kb) * BITS / 8u : kOutOfRange;
         // (windows: the row's parameters from the split's first group on)
         soff[j] = int(n) < N ? (n * uint32_t(G)) * 2u + (PW ? uint32_t(c_begin) * 2u : uint32_t((32 * kb) / GS) * 2u)
                              : kOutOfRange;
@@ -415,7 +416,7 @@ done:
                         *reinterpret_cast<f32x4*>(args.ws + (int64_t(split) * M + m) * N + n) = v;
                     } else {
                         const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
-                        *reinterpret_cast<uint2*>(yp + int64_t(m) * N + n) = make_uint2(lo, hi);
+                        *reinterpret_cast<uint2*>(yp + int64_t(m) * args.ldy + n) = make_uint2(lo, hi);
                     }
                 }
         }
@@ -446,32 +447,6 @@ __global__ __launch_bounds__(256) void qmm_split_reduce(uint16_t* __restrict__ y
     }
 }
 
-// Per-device f32 workspace for split K, grown on demand outside stream
-// capture (a capturing caller whose workspace is too small gets no split).
-float* qmm_workspace(size_t bytes, hipStream_t st) {
-    static std::mutex mu;
-    static float* ptr[64] = {};
-    static size_t cap[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    if (cap[dev] >= bytes) return ptr[dev];
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    // the old buffer may still be in use by queued work: synchronise first
-    if (ptr[dev]) {
-        if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-        (void)hipFree(ptr[dev]);
-        ptr[dev] = nullptr;
-        cap[dev] = 0;
-    }
-    void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-    ptr[dev] = static_cast<float*>(p);
-    cap[dev] = bytes;
-    return ptr[dev];
-}
-
 // Compute units of the current device.
 static int qmm_cu_count() {
     int dev = 0, v = 0;
@@ -480,18 +455,19 @@ static int qmm_cu_count() {
     return v;
 }
 
+// One launch (plus the split reduction): every buffer below 2^31 bytes.
 template <int BITS, int GS, typename ST>
-static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b, int M,
-                         int N, int K, hipStream_t st) {
+static void launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
+                             int M, int N, int K, bool may_split, const WsSource* src, hipStream_t st) {
     QmmArgs a{};
     a.y = y, a.x = x, a.w = w, a.s = static_cast<const uint16_t*>(s), a.b = static_cast<const uint16_t*>(b);
-    a.M = M, a.N = N, a.K = K;
+    a.M = M, a.N = N, a.K = K, a.ldy = ldy;
     a.mtiles = (M + kBM - 1) / kBM, a.ntiles = (N + kBN - 1) / kBN;
     const int tiles = a.mtiles * a.ntiles, nchunks = K / kBK;
     // Split K so that the grid fills the CUs without exceeding them (one
     // workgroup per CU: a second round of workgroups would double the time),
     // at least 8 chunks per split (4 per K-group).
-    int splits = qmm_cu_count() / tiles;
+    int splits = may_split ? qmm_cu_count() / tiles : 1;
     splits = splits < 1 ? 1 : splits;
     splits = splits > nchunks / 8 ? nchunks / 8 : splits;
     splits = splits < 1 ? 1 : splits;
@@ -499,8 +475,22 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
         a.cps = (nchunks + splits - 1) / splits;
         a.cps += a.cps & 1;  // even, so that parameter windows stay 4-byte aligned
         splits = (nchunks + a.cps - 1) / a.cps;  // no empty split
-        a.ws = qmm_workspace(size_t(splits) * size_t(M) * size_t(N) * 4u, st);
-        if (!a.ws) splits = 1;
+        // a fixed scratch region may hold fewer splits than planned
+        const size_t per_split = size_t(M) * size_t(N) * 4u;
+        if (src && splits > 1 && size_t(splits) * per_split > src->cap) {
+            const int fit = int(src->cap / per_split);
+            if (fit >= 2) {
+                a.cps = (nchunks + fit - 1) / fit;
+                a.cps += a.cps & 1;
+                splits = (nchunks + a.cps - 1) / a.cps;
+            } else {
+                splits = 1;
+            }
+        }
+        if (splits > 1) {
+            a.ws = static_cast<float*>(ws_acquire(src, size_t(splits) * per_split, st));
+            if (!a.ws) splits = 1;
+        }
     }
     a.splits = splits;
     if (splits == 1) a.cps = nchunks;
@@ -514,18 +504,44 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     }
     if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64><<<grid, block, 0, st>>>(a);
     else qmm_mfma_kernel<BITS, GS, ST, true, false><<<grid, block, 0, st>>>(a);
-    const int64_t mn = int64_t(M) * N;
+    const int64_t mn = int64_t(M) * N;  // (split only when y is one whole piece: ldy == N)
     qmm_split_reduce<<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(y, a.ws, mn, splits,
                                                                                     aligned(y, 8));
 }
 
+// Buffer offsets in the kernel are 32-bit: a weight matrix of 2^31 bytes or
+// more runs in row pieces (multiples of the 256-column tile), an activation
+// matrix that large in row pieces (multiples of the 128-row tile).
+template <int BITS, int GS, typename ST>
+static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b, int M,
+                         int N, int K, const WsSource* src, hipStream_t st) {
+    const int64_t limit = (int64_t(1) << 31) - 1;
+    const int64_t row_bytes = int64_t(K) * BITS / 8;
+    const int64_t G = K / GS;
+    int64_t n_piece = limit / row_bytes / kBN * kBN;
+    int64_t m_piece = limit / (int64_t(K) * 2) / kBM * kBM;
+    n_piece = n_piece < kBN ? kBN : n_piece;
+    m_piece = m_piece < kBM ? kBM : m_piece;
+    const bool whole = n_piece >= N && m_piece >= M;
+    for (int64_t m0 = 0; m0 < M; m0 += m_piece) {
+        const int mc = int(M - m0 < m_piece ? M - m0 : m_piece);
+        for (int64_t n0 = 0; n0 < N; n0 += n_piece) {
+            const int nc = int(N - n0 < n_piece ? N - n0 : n_piece);
+            const uint16_t* sp = static_cast<const uint16_t*>(s) + n0 * G;
+            const uint16_t* bp = b ? static_cast<const uint16_t*>(b) + n0 * G : nullptr;
+            launch_qmm_piece<BITS, GS, ST>(y + m0 * N + n0, N, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp, mc, nc,
+                                           K, whole, src, st);
+        }
+    }
+}
+
 template <int BITS, typename ST>
 static bool launch_qmm_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
-                          int M, int N, int K, hipStream_t st) {
+                          int M, int N, int K, const WsSource* src, hipStream_t st) {
     switch (gs) {
-    case 32: launch_qmm_t<BITS, 32, ST>(y, x, w, s, b, M, N, K, st); return true;
-    case 64: launch_qmm_t<BITS, 64, ST>(y, x, w, s, b, M, N, K, st); return true;
-    case 128: launch_qmm_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, st); return true;
+    case 32: launch_qmm_t<BITS, 32, ST>(y, x, w, s, b, M, N, K, src, st); return true;
+    case 64: launch_qmm_t<BITS, 64, ST>(y, x, w, s, b, M, N, K, src, st); return true;
+    case 128: launch_qmm_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, src, st); return true;
     default: return false;
     }
 }
@@ -606,8 +622,10 @@ static bool launch_qmm_grouped_t(uint16_t* y, const uint16_t* x, const uint32_t*
                                  const int32_t* lhs, const int32_t* rhs, int batch, int64_t x_batches, int experts,
                                  int N, int K, hipStream_t st) {
     const int cap = experts + (batch + kBM - 1) / kBM;  // sum over experts of ceil(rows / kBM)
+    // one launch with 32-bit offsets: each expert's codes and the gathered rows below 2^31 bytes
+    if (int64_t(N) * K * BITS / 8 >= (int64_t(1) << 31) || int64_t(batch) * K * 2 >= (int64_t(1) << 31)) return false;
     const size_t xg_bytes = (size_t(batch) * size_t(K) * 2u + 255u) & ~size_t(255);
-    float* ws = qmm_workspace(xg_bytes + size_t(cap) * sizeof(int4), st);
+    void* ws = ws_acquire(nullptr, xg_bytes + size_t(cap) * sizeof(int4), st);
     if (!ws) return false;
     uint16_t* xg = reinterpret_cast<uint16_t*>(ws);
     int4* list = reinterpret_cast<int4*>(reinterpret_cast<char*>(ws) + xg_bytes);
@@ -617,7 +635,7 @@ static bool launch_qmm_grouped_t(uint16_t* y, const uint16_t* x, const uint32_t*
     qmm_group_tiles<<<dim3(1), dim3(1024), 0, st>>>(list, rhs, batch, experts, cap);
     QmmArgs a{};
     a.y = y, a.x = xg, a.w = w, a.s = static_cast<const uint16_t*>(s), a.b = static_cast<const uint16_t*>(b);
-    a.M = batch, a.N = N, a.K = K;
+    a.M = batch, a.N = N, a.K = K, a.ldy = N;
     a.mtiles = cap, a.ntiles = (N + kBN - 1) / kBN, a.splits = 1, a.cps = K / kBK;
     a.groups = list;
     const bool pw = GS == 64 && (K / GS) % 2 == 0 && a.cps % 2 == 0;
@@ -656,17 +674,14 @@ bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const ui
     return false;
 }
 
-// Preconditions checked by the dispatcher (api.hip): x bf16, transpose,
-// K % 64 == 0 and K % gs == 0, 16-byte aligned x and w, scale dtype bf16 or
-// f16, buffers below 2^31 bytes.
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
-                     const void* s, const void* b, int M, int N, int K, hipStream_t st) {
+                     const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st) {
     if (bits == 4) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<4, BF16T>(gs, y, x, w, s, b, M, N, K, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<4, F16T>(gs, y, x, w, s, b, M, N, K, st);
+        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<4, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<4, F16T>(gs, y, x, w, s, b, M, N, K, ws, st);
     } else if (bits == 8) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, st);
+        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, ws, st);
     }
     return false;
 }

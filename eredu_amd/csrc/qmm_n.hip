@@ -294,7 +294,7 @@ void pick_splits(int64_t tiles, int K, int kp, int min_rows, int64_t target, int
 
 bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
                         const void* b, const GatherIdx& g, int64_t batch, int M, int N, int K, int gs,
-                        hipStream_t st) {
+                        const WsSource* src, hipStream_t st) {
     if ((bits != 4 && bits != 8) || (scale_dtype != EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F16) || M < 1 ||
         M > 8 || batch < 1 || gs < 32)
         return false;
@@ -324,8 +324,19 @@ bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* 
         pick_splits(tiles, K, kp, 4, 1024, splits, kchunk);
     }
     float* ws = nullptr;
+    if (splits > 1 && src && size_t(splits) * size_t(mn) * 4u > src->cap) {
+        // a fixed scratch region holds fewer splits: re-plan for what fits
+        const int64_t fit = int64_t(src->cap / (size_t(mn) * 4u));
+        if (fit >= 2) {
+            kchunk = int((K + fit - 1) / fit);
+            splits = int((K + kchunk - 1) / kchunk);
+        } else {
+            splits = 1;
+            kchunk = K;
+        }
+    }
     if (splits > 1) {
-        ws = qmm_workspace(size_t(splits) * size_t(mn) * 4u, st);
+        ws = static_cast<float*>(ws_acquire(src, size_t(splits) * size_t(mn) * 4u, st));
         if (!ws) {
             splits = 1;
             kchunk = K;

@@ -13,8 +13,10 @@ matmul C ABI (q/k/v and gate/up as one grouped launch each, results
 bit-identical to separate calls); the rest through the decode entry points of
 ``include/eredu_hip.h``.  Every buffer is allocated once, so a step can be
 captured in a HIP graph; the token id lives in device memory and the step
-reads it (embedding) and overwrites it (argmax), so graph replays generate
-successive tokens.  There is no CPU fallback.
+reads it (embedding) and overwrites it (argmax).  The position is an argument
+of the step that the capture records: one graph replays one position (it
+re-reads cache rows 0..pos and rewrites row pos), so autoregressive decoding
+captures one graph per position.  There is no CPU fallback.
 """
 from __future__ import annotations
 
