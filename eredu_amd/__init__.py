@@ -8,8 +8,11 @@ host-side mirror of the reference's operator API:
 * :mod:`eredu_amd.quantization` -- safemlx ``quantized_matmul[_with_mode]``,
   ``gather_qmm[_with_mode]``, ``dequantize[_with_mode]``,
   ``quantize[_with_mode]``, ``QuantizedLinear``.
-* :mod:`eredu_amd.gguf` -- eredu-gguf ``convert_affine`` / ``AffineTensor``,
-  dense dequantization and the native Q4_K / Q8_0 linear.
+* :mod:`eredu_amd.gguf` -- eredu-gguf ``conversion_kind`` routing, ``convert``,
+  ``convert_affine`` / ``AffineTensor``, ``NativeTensor`` (blocks kept as
+  stored), dense dequantization and the native Q4_K / Q8_0 linear.
+* :mod:`eredu_amd.nn` -- the linear-layer dispatch (``LinearSpec`` ->
+  dense ``Linear`` or ``QuantizedLinear`` for affine / MXFP4 / native GGUF).
 * :mod:`eredu_amd.checkpoint` -- MLX-LM quantized SafeTensors checkpoints.
 * :mod:`eredu_amd.gguf_file` -- GGUF container reader/writer and the
   streaming load into the device-side convert.
@@ -20,6 +23,7 @@ from .quantization import (
     DEFAULT_BITS,
     DEFAULT_GROUP_SIZE,
     QuantizationMode,
+    QuantizedEmbedding,
     QuantizedLinear,
     dequantize,
     dequantize_with_mode,
@@ -38,6 +42,7 @@ __all__ = [
     "DEFAULT_BITS",
     "DEFAULT_GROUP_SIZE",
     "QuantizationMode",
+    "QuantizedEmbedding",
     "QuantizedLinear",
     "dequantize",
     "dequantize_with_mode",

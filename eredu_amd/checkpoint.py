@@ -30,13 +30,48 @@ _INDEX = "model.safetensors.index.json"
 class WeightQuantization:
     """Stored weight encoding (eredu-checkpoint/src/lib.rs:69-123,140-250):
     affine (group_size 16 or a positive multiple of 32; bits 2, 3, 4, 5, 6
-    or 8) or MXFP4 (fixed group 32, 4 bits, no biases)."""
+    or 8), MXFP4 (fixed group 32, 4 bits, no biases), or checkpoint-native
+    GGML blocks (``mode`` "gguf" with ``ggml_type`` and ``endian``; group_size
+    and bits then hold the block geometry, values and bytes per block, as
+    WeightQuantization::GgufIQuant reports them)."""
 
     group_size: int = 64
     bits: int = 4
     mode: str = "affine"
+    ggml_type: Optional[int] = None
+    endian: int = 0
+
+    @staticmethod
+    def Affine(group_size: int = 64, bits: int = 4) -> "WeightQuantization":
+        q = WeightQuantization(group_size, bits, "affine")
+        q.validate()
+        return q
+
+    @staticmethod
+    def MxFp4() -> "WeightQuantization":
+        return WeightQuantization(32, 4, "mxfp4")
+
+    @staticmethod
+    def GgufIQuant(ggml_type: int, endian: int = 0) -> "WeightQuantization":
+        """Native GGML blocks of ``ggml_type`` in a file of byte order ``endian``."""
+        from .gguf import ggml_type_from_code
+
+        ty = ggml_type_from_code(int(ggml_type))
+        values, nbytes = ty.block_and_bytes()
+        return WeightQuantization(values, nbytes, "gguf", int(ty), int(endian))
+
+    def gguf_iquant(self):
+        """(ggml_type, endian) for native GGML blocks, else None (lib.rs:190-196)."""
+        return (self.ggml_type, self.endian) if self.mode == "gguf" else None
 
     def validate(self) -> None:
+        if self.mode == "gguf":
+            from .gguf import ggml_type_from_code
+
+            if self.ggml_type is None:
+                raise EreduError("native GGUF quantization needs a GGML type")
+            ggml_type_from_code(self.ggml_type).block_and_bytes()
+            return
         if self.mode == "mxfp4":
             if (self.group_size, self.bits) != (32, 4):
                 raise EreduError(f"mxfp4 metadata must be group_size 32, bits 4, got {self.group_size}, {self.bits}")
@@ -53,7 +88,9 @@ class WeightQuantization:
         return self.mode == "affine"
 
     def to_json(self) -> dict:
-        """MLX spelling: {"group_size", "bits", "mode"}."""
+        """MLX spelling: {"group_size", "bits", "mode"} (affine and MXFP4 only)."""
+        if self.mode == "gguf":
+            raise EreduError("native GGUF quantization has no MLX checkpoint metadata")
         return {"group_size": self.group_size, "bits": self.bits, "mode": self.mode}
 
     @staticmethod
@@ -61,7 +98,10 @@ class WeightQuantization:
         """An omitted mode means affine (lib.rs:207-214)."""
         if not isinstance(value, dict) or "group_size" not in value or "bits" not in value:
             raise EreduError(f"invalid quantization metadata {value!r}")
-        q = WeightQuantization(int(value["group_size"]), int(value["bits"]), str(value.get("mode", "affine")))
+        mode = str(value.get("mode", "affine"))
+        if mode not in ("affine", "mxfp4"):
+            raise EreduError(f"unknown quantization mode {mode!r}")
+        q = WeightQuantization(int(value["group_size"]), int(value["bits"]), mode)
         q.validate()
         return q
 

@@ -20,24 +20,121 @@ from ._native import EreduError, check
 
 
 class GgmlType(enum.IntEnum):
-    """Codes of eredu-gguf/src/format.rs:297-330 handled on the device."""
+    """GGML tensor type codes (eredu-gguf/src/format.rs:295-365).  The device
+    path converts and executes Q4_0, Q8_0 and Q4_K; the rest are named so that
+    routing (``conversion_kind``) covers every code the container holds."""
 
+    F32 = 0
+    F16 = 1
     Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
     Q8_0 = 8
+    Q2K = 10
+    Q3K = 11
     Q4K = 12
+    Q5K = 13
+    Q6K = 14
+    IQ2XXS = 16
+    IQ2XS = 17
+    IQ3XXS = 18
+    IQ1S = 19
+    IQ4NL = 20
+    IQ3S = 21
+    IQ2S = 22
+    IQ4XS = 23
+    I8 = 24
+    I16 = 25
+    I32 = 26
+    I64 = 27
+    F64 = 28
+    IQ1M = 29
+    BF16 = 30
+    MXFP4 = 39
 
     def block_and_bytes(self):
-        """(values per block, bytes per block), format.rs:368-400."""
-        return {GgmlType.Q4_0: (32, 18), GgmlType.Q8_0: (32, 34), GgmlType.Q4K: (256, 144)}[self]
+        """(values per block, bytes per block), format.rs:366-400."""
+        return _BLOCK_AND_BYTES[self]
+
+    def is_iq(self) -> bool:
+        """The nine on-disk IQ encodings (format.rs:403-416)."""
+        return self in _IQ_TYPES
 
     def has_native_execution(self) -> bool:
-        """format.rs:423-428: Q4_K and Q8_0 stay native in eredu; Q4_0 does not."""
-        return self in (GgmlType.Q4K, GgmlType.Q8_0)
+        """format.rs:423-428: encodings that stay in their blocks when converted
+        (Q4_K, Q5_K, Q6_K, Q5_1, Q8_0 and the IQ types)."""
+        return self in (GgmlType.Q4K, GgmlType.Q5K, GgmlType.Q6K, GgmlType.Q5_1, GgmlType.Q8_0) or self.is_iq()
+
+    def has_device_kernels(self) -> bool:
+        """Encodings this library converts and dequantizes (Q4_0, Q8_0, Q4_K)."""
+        return self in (GgmlType.Q4_0, GgmlType.Q8_0, GgmlType.Q4K)
+
+    def has_device_linear(self) -> bool:
+        """Encodings this library multiplies straight from their blocks (eq_gguf_linear)."""
+        return self in (GgmlType.Q8_0, GgmlType.Q4K)
+
+
+_BLOCK_AND_BYTES = {
+    GgmlType.F32: (1, 4), GgmlType.F16: (1, 2), GgmlType.BF16: (1, 2), GgmlType.I16: (1, 2), GgmlType.I8: (1, 1),
+    GgmlType.I32: (1, 4), GgmlType.I64: (1, 8), GgmlType.F64: (1, 8),
+    GgmlType.Q4_0: (32, 18), GgmlType.Q4_1: (32, 20), GgmlType.Q5_0: (32, 22), GgmlType.Q5_1: (32, 24),
+    GgmlType.Q8_0: (32, 34), GgmlType.Q2K: (256, 84), GgmlType.Q3K: (256, 110), GgmlType.Q4K: (256, 144),
+    GgmlType.Q5K: (256, 176), GgmlType.Q6K: (256, 210), GgmlType.IQ2XXS: (256, 66), GgmlType.IQ2XS: (256, 74),
+    GgmlType.IQ3XXS: (256, 98), GgmlType.IQ1S: (256, 50), GgmlType.IQ4NL: (32, 18), GgmlType.IQ3S: (256, 110),
+    GgmlType.IQ2S: (256, 82), GgmlType.IQ4XS: (256, 136), GgmlType.IQ1M: (256, 56), GgmlType.MXFP4: (32, 17),
+}
+_IQ_TYPES = (GgmlType.IQ2XXS, GgmlType.IQ2XS, GgmlType.IQ3XXS, GgmlType.IQ1S, GgmlType.IQ4NL, GgmlType.IQ3S,
+             GgmlType.IQ2S, GgmlType.IQ4XS, GgmlType.IQ1M)
+_DENSE_DTYPES = {GgmlType.F32: torch.float32, GgmlType.F16: torch.float16, GgmlType.BF16: torch.bfloat16,
+                 GgmlType.I8: torch.int8, GgmlType.I16: torch.int16, GgmlType.I32: torch.int32,
+                 GgmlType.I64: torch.int64, GgmlType.F64: torch.float64}
+
+
+def ggml_type_from_code(code: int) -> GgmlType:
+    """GgmlType::from_code; a code outside the table is UnsupportedTensorType."""
+    try:
+        return GgmlType(code)
+    except ValueError:
+        raise EreduError(f"unsupported GGML tensor type {code}") from None
 
 
 def affine_config(ty: GgmlType):
-    """(bits, group_size) of the affine form, convert.rs:142-152."""
-    return {GgmlType.Q4_0: (4, 32), GgmlType.Q8_0: (8, 32), GgmlType.Q4K: (4, 32)}[ty]
+    """(bits, group_size) of the affine form (convert.rs:142-152), or None."""
+    return {GgmlType.Q2K: (2, 16), GgmlType.Q3K: (3, 16), GgmlType.Q4_0: (4, 32), GgmlType.Q4_1: (4, 32),
+            GgmlType.Q4K: (4, 32), GgmlType.Q5_0: (5, 32), GgmlType.Q5_1: (5, 32), GgmlType.Q5K: (5, 32),
+            GgmlType.Q6K: (6, 16), GgmlType.Q8_0: (8, 32)}.get(GgmlType(ty))
+
+
+@dataclasses.dataclass(frozen=True)
+class ConversionKind:
+    """How eredu-gguf converts a tensor (convert.rs:104-140): ``kind`` is
+    "dense" (with ``dtype``), "native" (kept in its GGML blocks, the
+    reference's ConversionKind::IQuant), "mxfp4", or "affine" (with ``bits``
+    and ``group_size``)."""
+
+    kind: str
+    dtype: Optional[torch.dtype] = None
+    bits: int = 0
+    group_size: int = 0
+
+
+def conversion_kind(ty: GgmlType, endian: "Endian") -> ConversionKind:
+    """Routing of convert.rs:125-140: dense types stay dense; IQ types and,
+    in little-endian files, the natively executable encodings (Q4_K, Q8_0,
+    ...) stay in their blocks; MXFP4 has its own form; everything else with
+    an affine geometry is expanded to the affine triple."""
+    ty = GgmlType(ty)
+    if ty in _DENSE_DTYPES:
+        return ConversionKind("dense", dtype=_DENSE_DTYPES[ty])
+    if ty.is_iq() or (Endian(endian) == Endian.Little and ty.has_native_execution()):
+        return ConversionKind("native")
+    if ty == GgmlType.MXFP4:
+        return ConversionKind("mxfp4")
+    cfg = affine_config(ty)
+    if cfg is None:
+        raise EreduError(f"unsupported GGML tensor type {int(ty)}")
+    return ConversionKind("affine", bits=cfg[0], group_size=cfg[1])
 
 
 class Endian(enum.IntEnum):
@@ -101,6 +198,13 @@ def _rows_cols(desc: TensorDescriptor):
     return shape, rows, cols
 
 
+def _device_type(desc: TensorDescriptor) -> GgmlType:
+    ty = ggml_type_from_code(int(desc.ggml_type))
+    if not ty.has_device_kernels():
+        raise EreduError(f"tensor '{desc.name}': GGML type {int(ty)} has no device kernels (Q4_0, Q8_0, Q4_K)")
+    return ty
+
+
 def _check_raw(desc: TensorDescriptor, raw: torch.Tensor) -> None:
     if raw.dtype != torch.uint8 or not raw.is_cuda:
         raise EreduError("raw GGUF payload must be a uint8 tensor on the GPU")
@@ -111,7 +215,7 @@ def _check_raw(desc: TensorDescriptor, raw: torch.Tensor) -> None:
 def convert_affine(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little) -> AffineTensor:
     """GGML blocks -> MLX affine triple, byte-identical to
     eredu_gguf::convert_affine (convert.rs:318-465); C ABI eq_gguf_convert_affine."""
-    ty = GgmlType(desc.ggml_type)
+    ty = _device_type(desc)
     _check_raw(desc, raw)
     shape, rows, cols = _rows_cols(desc)
     bits, gs = affine_config(ty)
@@ -144,7 +248,7 @@ def dequantize(
 ) -> torch.Tensor:
     """Dense dequant of GGML blocks (bf16 = round-to-nearest-even image of the
     reference's f32 values); C ABI eq_gguf_dequantize."""
-    ty = GgmlType(desc.ggml_type)
+    ty = _device_type(desc)
     _check_raw(desc, raw)
     shape, rows, cols = _rows_cols(desc)
     if dtype not in (torch.bfloat16, torch.float32):
@@ -169,7 +273,9 @@ def linear(x: torch.Tensor, desc: TensorDescriptor, raw: torch.Tensor, endian: E
     NativeQuantizedTensor::linear with transpose = true
     (safemlx/src/native_quantization.rs:741-772); C ABI eq_gguf_linear.
     x is bf16 [..., K] on the GPU; W's MLX shape is [N, K]."""
-    ty = GgmlType(desc.ggml_type)
+    ty = _device_type(desc)
+    if not ty.has_device_linear():
+        raise EreduError(f"tensor '{desc.name}': no native linear for GGML type {int(ty)} (Q4_K and Q8_0 only)")
     _check_raw(desc, raw)
     shape, N, K = _rows_cols(desc)
     if len(shape) != 2:
@@ -185,3 +291,83 @@ def linear(x: torch.Tensor, desc: TensorDescriptor, raw: torch.Tensor, endian: E
         )
     )
     return y.reshape(*x.shape[:-1], N)
+
+
+@dataclasses.dataclass
+class NativeTensor:
+    """A GGML tensor kept in its checkpoint-native blocks on the device: the
+    reference's IQuantTensor (convert.rs:26-56) as safemlx hands it to
+    NativeQuantizedTensor (safemlx/src/native_quantization.rs:741-772).
+    ``shape`` is the logical MLX shape, ``data`` the raw blocks (uint8, GPU)."""
+
+    name: str
+    shape: List[int]
+    ggml_type: GgmlType
+    endian: Endian
+    data: torch.Tensor
+
+    def descriptor(self) -> TensorDescriptor:
+        return TensorDescriptor(self.name, list(reversed(self.shape)), self.ggml_type, self.data.numel())
+
+    def packed_shape(self) -> List[int]:
+        """Rows of packed block bytes (convert.rs:176-194 iquant_packed_shape)."""
+        values, nbytes = GgmlType(self.ggml_type).block_and_bytes()
+        if not self.shape or self.shape[-1] % values != 0:
+            raise EreduError(f"tensor '{self.name}': row width is not divisible by block length {values}")
+        return list(self.shape[:-1]) + [self.shape[-1] // values * nbytes]
+
+    def dequantize_f32(self) -> torch.Tensor:
+        """IQuantTensor::dequantize_f32 (convert.rs:43-56): for the non-IQ
+        encodings the affine route, convert_affine then AffineTensor::dequantize."""
+        return dequantize(self.descriptor(), self.data, self.endian, DequantDefinition.Affine, torch.float32)
+
+    def dequantize(self, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        """NativeQuantizedTensor::dequantize: the native decoders
+        (safemlx/src/native_quantization.rs:3417-3542)."""
+        return dequantize(self.descriptor(), self.data, self.endian, DequantDefinition.Native, dtype)
+
+    def linear(self, x: torch.Tensor, transpose: bool = True) -> torch.Tensor:
+        """NativeQuantizedTensor::linear (native_quantization.rs:741-772): y = x . W^T
+        from the blocks (transpose = true, the only form QuantizedLinear uses)."""
+        if not transpose:
+            raise EreduError("native GGUF linear is implemented for transpose = true")
+        return linear(x, self.descriptor(), self.data, self.endian)
+
+
+@dataclasses.dataclass
+class DenseTensor:
+    """A dense GGUF tensor (convert.rs:19-24) on the device, in its MLX shape."""
+
+    name: str
+    array: torch.Tensor
+
+
+def convert(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little):
+    """eredu_gguf's convert (convert.rs:276-313) on device payloads, routed by
+    ``conversion_kind``: a DenseTensor (dense types), a NativeTensor (blocks
+    kept as stored: little-endian Q4_K / Q8_0), or an AffineTensor (Q4_0 in
+    either byte order, big-endian Q4_K / Q8_0).  Encodings without device
+    kernels, and MXFP4, are refused with the type named."""
+    if raw.dtype != torch.uint8 or not raw.is_cuda:
+        raise EreduError("raw GGUF payload must be a uint8 tensor on the GPU")
+    if raw.numel() != desc.byte_len:
+        raise EreduError(f"tensor '{desc.name}': payload length does not match descriptor")
+    ty = ggml_type_from_code(int(desc.ggml_type))
+    kind = conversion_kind(ty, endian)
+    if kind.kind == "dense":
+        width = ty.block_and_bytes()[1]
+        if Endian(endian) == Endian.Big and width > 1:  # normalize_dense (convert.rs:216-233): swap each element
+            raw = raw.view(-1, width).flip(-1).contiguous().view(-1)
+        return DenseTensor(desc.name, raw.view(kind.dtype).reshape(desc.mlx_shape()))
+    if kind.kind == "native":
+        if not ty.has_device_linear():
+            raise EreduError(f"tensor '{desc.name}': GGML type {int(ty)} stays native in eredu, and this library "
+                             f"executes only Q4_K and Q8_0 blocks")
+        shape = desc.mlx_shape()
+        values, _ = ty.block_and_bytes()
+        if not shape or shape[-1] % values != 0:
+            raise EreduError(f"tensor '{desc.name}': row width is not divisible by block length {values}")
+        return NativeTensor(desc.name, shape, ty, Endian(endian), raw)
+    if kind.kind == "mxfp4":
+        raise EreduError(f"tensor '{desc.name}': MXFP4 blocks are not converted on the device")
+    return convert_affine(desc, raw, endian)

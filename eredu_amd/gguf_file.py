@@ -9,13 +9,17 @@ header, each offset aligned, shapes divisible by the GGML block, ranges
 inside the file and not overlapping.  ``write_gguf`` is the deterministic
 writer of eredu-gguf/src/writer.rs (test inputs, conversion output).
 
-``stream_convert_affine`` streams a checkpoint onto the GPU (the role of
+``stream_convert`` streams a checkpoint onto the GPU (the role of
 eredu-gguf/src/catalog.rs:435-660's converted-tensor iteration): the
-raw blocks of each Q4_0 / Q8_0 / Q4_K tensor go file -> pinned host buffer
--> HBM on a copy stream while the previous tensor is converted to the MLX
-affine triple by ``eq_gguf_convert_affine`` on the compute stream (two
+raw blocks of each tensor go file -> pinned host buffer -> HBM on a copy
+stream while the previous tensor is converted on the compute stream (two
 pinned staging buffers, ordered by events), so file reads, PCIe copies and
-conversion overlap.  Dense F32 / F16 / BF16 tensors are copied as they are.
+conversion overlap.  Tensors are routed as eredu routes them
+(eredu-gguf/src/convert.rs:125-140): little-endian Q4_K / Q8_0 stay in their
+blocks (executed by the native linear), Q4_0 and big-endian Q4_K / Q8_0 are
+expanded to the MLX affine triple by ``eq_gguf_convert_affine``, dense
+tensors are copied as they are.  ``stream_convert_affine`` expands every
+quantized tensor (the explicit convert_affine of portable backends).
 """
 from __future__ import annotations
 
@@ -35,7 +39,7 @@ BLOCK_GEOMETRY: Dict[int, Tuple[int, int]] = {
     2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34),
     10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210),
     16: (256, 66), 17: (256, 74), 18: (256, 98), 19: (256, 50), 20: (32, 18), 21: (256, 110),
-    22: (256, 82), 23: (256, 136), 29: (256, 56),
+    22: (256, 82), 23: (256, 136), 29: (256, 56), 39: (32, 17),
 }
 F32, F16, BF16, Q4_0, Q8_0, Q4_K = 0, 1, 30, 2, 8, 12
 
@@ -331,16 +335,42 @@ def write_gguf(out: BinaryIO, metadata: Dict[str, MetadataValue],
         out.write(data)
 
 
-def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, staging_bytes: int = 256 << 20):
-    """Loads a GGUF file's tensors into HBM, converting Q4_0 / Q8_0 / Q4_K
-    blocks to the MLX affine triple on the GPU as they arrive.
+def stream_convert(path: str, names: Optional[Sequence[str]] = None, staging_bytes: int = 256 << 20):
+    """Loads a GGUF file's tensors into HBM, converting each on the GPU as it
+    arrives the way eredu loads a checkpoint (eredu-gguf/src/convert.rs:276-313
+    routed by conversion_kind, :125-140; safemlx/src/ops/gguf.rs:421-528):
 
-    Returns {name: AffineTensor (device weight/scales/biases) | torch.Tensor
-    (dense F32 / F16 / BF16, MLX shape)}.  Two pinned staging buffers of
-    ``staging_bytes`` alternate: while tensor i is copied to the device and
-    converted, tensor i + 1 is read from the file into the other buffer;
-    events order each buffer's reuse after its copy.  A tensor larger than a
-    buffer goes through a device staging tensor in buffer-sized pieces."""
+    * dense F32 / F16 / BF16 (and the integer dense types) -> ``gguf.DenseTensor``,
+    * little-endian Q4_K / Q8_0 -> ``gguf.NativeTensor`` (blocks kept as stored,
+      executed by the native linear),
+    * Q4_0, and big-endian Q4_K / Q8_0 -> ``gguf.AffineTensor``.
+
+    Returns {name: tensor}.  Two pinned staging buffers of ``staging_bytes``
+    alternate: while tensor i is copied to the device and converted, tensor
+    i + 1 is read from the file into the other buffer; events order each
+    buffer's reuse after its copy.  A tensor larger than a buffer goes
+    through in buffer-sized pieces."""
+    from . import gguf as G
+
+    return _stream(path, names, staging_bytes, lambda desc, raw, endian: G.convert(desc, raw, endian))
+
+
+def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, staging_bytes: int = 256 << 20):
+    """stream_convert with every Q4_0 / Q8_0 / Q4_K tensor expanded to the
+    MLX affine triple (the explicit eredu_gguf::convert_affine,
+    convert.rs:318-465, which portable backends use); dense tensors as in
+    stream_convert.  Returns {name: AffineTensor | torch.Tensor (dense)}."""
+    from . import gguf as G
+
+    def conv(desc, raw, endian):
+        if G.conversion_kind(desc.ggml_type, endian).kind == "dense":
+            return G.convert(desc, raw, endian).array
+        return G.convert_affine(desc, raw, endian)
+
+    return _stream(path, names, staging_bytes, conv)
+
+
+def _stream(path: str, names: Optional[Sequence[str]], staging_bytes: int, conv):
     import torch
 
     from . import gguf as G
@@ -352,6 +382,11 @@ def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, stag
         missing = set(names) - {t.name for t in wanted}
         if missing:
             raise EreduError(f"tensors not present: {sorted(missing)}")
+    for t in wanted:  # refuse before anything is read
+        ty = G.ggml_type_from_code(t.ggml_type)
+        kind = G.conversion_kind(ty, endian)
+        if kind.kind != "dense" and not ty.has_device_kernels():
+            raise EreduError(f"tensor {t.name!r}: GGML type {t.ggml_type} has no device conversion")
     dev = torch.device("cuda")
     copy_stream = torch.cuda.Stream()
     compute = torch.cuda.current_stream()
@@ -364,8 +399,6 @@ def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, stag
     slot = 0
     try:
         for t in wanted:
-            if t.ggml_type not in (Q4_0, Q8_0, Q4_K, F32, F16, BF16):
-                raise EreduError(f"tensor {t.name!r}: GGML type {t.ggml_type} has no device conversion")
             # allocated on the copy stream that fills it; record_stream below
             # keeps the allocator from handing it to a later copy while the
             # conversion on the compute stream still reads it
@@ -386,15 +419,8 @@ def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, stag
                 slot ^= 1
             compute.wait_stream(copy_stream)
             raw_dev.record_stream(compute)
-            shape = t.mlx_shape
-            if t.ggml_type in (F32, F16, BF16):
-                dt = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[t.ggml_type]
-                if reader.endian == "big":
-                    raise EreduError(f"tensor {t.name!r}: big-endian dense tensors are not converted on the device")
-                out[t.name] = raw_dev.view(dt).reshape(shape)
-                continue
-            desc = G.TensorDescriptor(t.name, list(t.dimensions), G.GgmlType(t.ggml_type), t.byte_len)
-            out[t.name] = G.convert_affine(desc, raw_dev, endian)
+            desc = G.TensorDescriptor(t.name, list(t.dimensions), G.ggml_type_from_code(t.ggml_type), t.byte_len)
+            out[t.name] = conv(desc, raw_dev, endian)
         torch.cuda.synchronize()
     finally:
         reader.close()

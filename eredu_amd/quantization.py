@@ -398,18 +398,33 @@ def dequantize(
 
 
 class QuantizedLinear:
-    """Affine quantized linear layer (safemlx/src/nn/quantized.rs:582-615,787-835):
-    forward = quantized_matmul(x, weight, scales, biases, transpose=True) + bias."""
+    """Quantized linear layer (safemlx/src/nn/quantized.rs:582-615,787-835).
+
+    Holds either the affine triple -- ``weight`` (packed u32 codes [N, K * bits
+    / 32]), ``scales``, ``biases`` -- or checkpoint-native GGML blocks: a
+    ``native`` tensor (gguf.NativeTensor), or raw block rows in ``weight``
+    (uint8 [N, K / block_values * block_bytes]) with ``native_format`` set.
+    ``forward`` dispatches as the reference's does: native -> the native GGUF
+    linear; native_format -> the same on the block rows; otherwise
+    quantized_matmul(x, weight, scales, biases, transpose=True); then the
+    optional dense ``bias`` is added."""
+
+    DEFAULT_GROUP_SIZE = DEFAULT_GROUP_SIZE
+    DEFAULT_BITS = DEFAULT_BITS
 
     def __init__(
         self,
         weight: torch.Tensor,
-        scales: torch.Tensor,
+        scales: Optional[torch.Tensor],
         biases: Optional[torch.Tensor],
         group_size: int = DEFAULT_GROUP_SIZE,
         bits: int = DEFAULT_BITS,
         bias: Optional[torch.Tensor] = None,
         mode: QuantizationMode = QuantizationMode.Affine,
+        native=None,
+        native_format=None,
+        native_endian: int = 0,
+        native_columns: int = 0,
     ):
         self.weight = weight
         self.scales = scales
@@ -418,6 +433,87 @@ class QuantizedLinear:
         self.bits = bits
         self.bias = bias
         self.mode = mode
+        self.native = native
+        self.native_format = native_format
+        self.native_endian = native_endian
+        self.native_columns = native_columns
+
+    # -- construction (quantized.rs:505-580, 621-780) ------------------------
+
+    @classmethod
+    def unloaded(cls, input_dims: int, output_dims: int, group_size: int, bits: int, bias: bool,
+                 device=None) -> "QuantizedLinear":
+        """Placeholder layer carrying only shapes, to be filled by load_parameters
+        (quantized.rs:621-640)."""
+        return cls.unloaded_with_mode(input_dims, output_dims, group_size, bits, QuantizationMode.Affine, bias,
+                                      device)
+
+    @classmethod
+    def unloaded_with_mode(cls, input_dims: int, output_dims: int, group_size: int, bits: int,
+                           mode: QuantizationMode, bias: bool, device=None) -> "QuantizedLinear":
+        """quantized.rs:643-706: u32 weight [out, packed], scales [out, in / gs]
+        in f32 (u8 for MXFP4), f32 biases when the mode has them, f32 bias."""
+        mode.validate(group_size, bits)
+        dev = torch.device("cuda") if device is None else device
+        scale_dtype = torch.uint8 if mode is QuantizationMode.MxFp4 else torch.float32
+        weight = torch.zeros((output_dims, quantized_packed_dimension(input_dims, bits)), dtype=torch.int32,
+                             device=dev)
+        scales = torch.zeros((output_dims, input_dims // group_size), dtype=scale_dtype, device=dev)
+        biases = (torch.zeros((output_dims, input_dims // group_size), dtype=torch.float32, device=dev)
+                  if mode.has_biases() else None)
+        b = torch.zeros((output_dims,), dtype=torch.float32, device=dev) if bias else None
+        return cls(weight, scales, biases, group_size, bits, b, mode)
+
+    @classmethod
+    def unloaded_iq(cls, input_dims: int, output_dims: int, ggml_type, endian, bias: bool,
+                    device=None) -> "QuantizedLinear":
+        """A layer backed by checkpoint-native GGML block rows (quantized.rs:709-750):
+        weight uint8 [out, in / block_values * block_bytes], group_size and bits
+        holding the block geometry, scales a [1] placeholder, no biases."""
+        from . import gguf as G
+
+        ty = G.ggml_type_from_code(int(ggml_type))
+        if not ty.has_native_execution():
+            raise EreduError(f"{ty.name} is not an IQ type")
+        values, nbytes = ty.block_and_bytes()
+        if input_dims <= 0 or input_dims % values != 0:
+            raise EreduError(f"IQ linear width {input_dims} is not divisible by {values}")
+        dev = torch.device("cuda") if device is None else device
+        weight = torch.zeros((output_dims, input_dims // values * nbytes), dtype=torch.uint8, device=dev)
+        b = torch.zeros((output_dims,), dtype=torch.float32, device=dev) if bias else None
+        return cls(weight, torch.zeros((1,), dtype=torch.float32, device=dev), None, values, nbytes, b,
+                   QuantizationMode.Affine, None, ty, int(endian), input_dims)
+
+    @classmethod
+    def from_native(cls, native, bias: Optional[torch.Tensor] = None) -> "QuantizedLinear":
+        """A layer whose weight is a gguf.NativeTensor (the ``native`` field)."""
+        values, nbytes = native.ggml_type.block_and_bytes()
+        return cls(native.data.view(native.shape[0], -1), None, None, values, nbytes, bias, QuantizationMode.Affine,
+                   native)
+
+    @classmethod
+    def try_from_linear(cls, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                        group_size: Optional[int] = None, bits: Optional[int] = None) -> "QuantizedLinear":
+        """Quantizes a dense [out, in] weight (quantized.rs:765-780, defaults 64 / 4)."""
+        gs = DEFAULT_GROUP_SIZE if group_size is None else group_size
+        b = DEFAULT_BITS if bits is None else bits
+        w, s, bi = quantize_with_mode(weight, gs, b, QuantizationMode.Affine)
+        return cls(w, s, bi, gs, b, bias, QuantizationMode.Affine)
+
+    def load_parameters(self, params: dict) -> None:
+        """Replaces placeholders by loaded tensors (``weight``, ``scales``,
+        ``biases``, ``bias``), each of the placeholder's shape."""
+        for name in ("weight", "scales", "biases", "bias"):
+            if name not in params:
+                continue
+            cur, new = getattr(self, name), params[name]
+            if cur is None:
+                raise EreduError(f"layer has no parameter {name!r}")
+            if tuple(new.shape) != tuple(cur.shape):
+                raise EreduError(f"parameter {name!r}: shape {tuple(new.shape)}, expected {tuple(cur.shape)}")
+            setattr(self, name, new)
+
+    # -- geometry and forward -------------------------------------------------
 
     @property
     def output_dims(self) -> int:
@@ -425,14 +521,83 @@ class QuantizedLinear:
 
     @property
     def input_dims(self) -> int:
+        if self.native is not None:
+            return self.native.shape[-1]
+        if self.native_format is not None:
+            return self.native_columns
         return self.weight.shape[1] * 32 // self.bits
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        y = quantized_matmul_with_mode(
-            x, self.weight, self.scales, self.biases, True, self.group_size, self.bits, self.mode
-        )
+        if self.native is not None:
+            y = self.native.linear(x, True)
+        elif self.native_format is not None:
+            from . import gguf as G
+
+            nt = G.NativeTensor("<native blocks>", [self.weight.shape[0], self.native_columns], self.native_format,
+                                G.Endian(self.native_endian), self.weight.contiguous().view(-1))
+            y = nt.linear(x, True)
+        else:
+            y = quantized_matmul_with_mode(
+                x, self.weight, self.scales, self.biases, True, self.group_size, self.bits, self.mode
+            )
         if self.bias is not None:
             y = y + self.bias
         return y
 
     __call__ = forward
+
+
+class QuantizedEmbedding:
+    """Quantized token embedding (safemlx/src/nn/quantized.rs:200-435):
+    ``forward`` gathers the rows of the ids (codes, scales, biases) and
+    dequantizes them (dequantize_with_mode, output in the scales' dtype), or,
+    for native GGML block rows, decodes the gathered blocks with the native
+    definition; ``as_linear`` is the tied output projection
+    (quantized_matmul with transpose = true, or the native linear)."""
+
+    DEFAULT_GROUP_SIZE = DEFAULT_GROUP_SIZE
+    DEFAULT_BITS = DEFAULT_BITS
+
+    def __init__(self, weight: torch.Tensor, scales: Optional[torch.Tensor], biases: Optional[torch.Tensor],
+                 group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS,
+                 mode: QuantizationMode = QuantizationMode.Affine, native=None):
+        self.weight, self.scales, self.biases = weight, scales, biases
+        self.group_size, self.bits, self.mode = group_size, bits, mode
+        self.native = native
+
+    @classmethod
+    def try_from_embedding(cls, table: torch.Tensor, group_size: Optional[int] = None,
+                           bits: Optional[int] = None) -> "QuantizedEmbedding":
+        gs = DEFAULT_GROUP_SIZE if group_size is None else group_size
+        b = DEFAULT_BITS if bits is None else bits
+        w, s, bi = quantize_with_mode(table, gs, b, QuantizationMode.Affine)
+        return cls(w, s, bi, gs, b)
+
+    @classmethod
+    def from_native(cls, native) -> "QuantizedEmbedding":
+        values, nbytes = native.ggml_type.block_and_bytes()
+        return cls(native.data.view(native.shape[0], -1), None, None, values, nbytes, QuantizationMode.Affine, native)
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        flat = ids.reshape(-1).to(torch.int64)
+        if self.native is not None:
+            from . import gguf as G
+
+            nt = self.native
+            rows = nt.data.view(nt.shape[0], -1).index_select(0, flat).contiguous().view(-1)
+            sub = G.NativeTensor(nt.name, [flat.numel(), nt.shape[-1]], nt.ggml_type, nt.endian, rows)
+            out = sub.dequantize(torch.bfloat16)
+        else:
+            w = self.weight.index_select(0, flat)
+            s = self.scales.index_select(0, flat)
+            b = self.biases.index_select(0, flat) if self.biases is not None else None
+            out = dequantize_with_mode(w, s, b, self.group_size, self.bits, self.mode)
+        return out.reshape(*ids.shape, -1)
+
+    __call__ = forward
+
+    def as_linear(self, x: torch.Tensor) -> torch.Tensor:
+        if self.native is not None:
+            return self.native.linear(x, True)
+        return quantized_matmul_with_mode(x, self.weight, self.scales, self.biases, True, self.group_size, self.bits,
+                                          self.mode)
