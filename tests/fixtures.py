@@ -140,3 +140,26 @@ def host_f32(t) -> np.ndarray:
     if t.dtype == torch.bfloat16:
         return (host_bits16(t).astype(np.uint32) << 16).view(np.float32)
     return t.float().cpu().numpy()
+
+
+def device_random_linear(N: int, K: int, group_size: int, bits: int, seed: int):
+    """A packed projection drawn directly on the GPU (random codes; bf16 scales
+    in [0.004, 0.008) and biases -s * (2^bits - 1) / 2, the magnitudes a
+    N(0, 0.02) weight quantizes to) for shapes too large for the host
+    quantizer: (w int32 [N, K*bits/32], scales, biases) device tensors."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randint(-(2**31), 2**31 - 1, (N, K * bits // 32), dtype=torch.int32, device="cuda", generator=g)
+    s = (torch.rand((N, K // group_size), device="cuda", generator=g) * 0.004 + 0.004).to(torch.bfloat16)
+    b = (-0.5 * ((1 << bits) - 1) * s.float()).to(torch.bfloat16)
+    return w, s, b
+
+
+def host_rows(w, s, b, rows):
+    """Host copies (u32 words, bf16 bits) of the given output rows of a device projection."""
+    import torch
+
+    idx = torch.as_tensor(np.asarray(rows, dtype=np.int64), device=w.device)
+    wr = w.index_select(0, idx).cpu().numpy().view(np.uint32)
+    return wr, host_bits16(s.index_select(0, idx)), host_bits16(b.index_select(0, idx))
