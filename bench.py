@@ -48,6 +48,14 @@ LAYER_SHAPES = [  # (name, N, K)
 DECODE_GROUPS = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]  # sets sharing an input
 ALL7 = [["q", "k", "v", "o", "gate", "up", "down"]]
 GS, BITS = 64, 4
+# Every timed buffer set rotates at least this many distinct bytes, so that the
+# 256 MB Infinity Cache cannot serve a repeat from cache.
+ROTATE_BYTES = 300_000_000
+
+
+def rotation(bytes_per_copy, minimum=2):
+    """Copies of a buffer set needed to rotate ROTATE_BYTES."""
+    return max(minimum, -(-ROTATE_BYTES // int(bytes_per_copy)))
 
 
 def qmv_bytes(M, N, K, bits=BITS, gs=GS):
@@ -158,23 +166,34 @@ def bench_decode(layers, M, groups, steps, warmup):
 
 
 def bench_per_shape(layers, M, steps, warmup):
+    """One eq_quantized_matmul launch per call, per distinct Llama shape; the
+    layers' weights rotate, topped up with more copies of a shape whose 32
+    layers hold less than ROTATE_BYTES (k/v)."""
     import torch
 
     out = {}
+    gen = torch.Generator(device="cuda").manual_seed(7)
     for name, N, K in LAYER_SHAPES:
         if name in ("v", "up", "o"):
             continue  # same shapes as k, gate, q
+        lins = [layer[name] for layer in layers]
+        extra = rotation(qmv_bytes(M, N, K), len(lins)) - len(lins)
+        lins += [Linear(N, K, gen) for _ in range(extra)]
         x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
         y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
-        t = Timer(lambda st: [run_one(layer[name], x, y, st) for layer in layers])
-        us = t.ms_per_replay(max(steps // 2, 10), warmup) * 1e3 / len(layers)
+        t = Timer(lambda st: [run_one(lin, x, y, st) for lin in lins])
+        us = t.ms_per_replay(max(steps // 2, 10), warmup) * 1e3 / len(lins)
         gbs = qmv_bytes(M, N, K) / (us * 1e-6) / 1e9
-        out[f"{N}x{K}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        out[f"{N}x{K}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                           "copies": len(lins)}
+        del lins
+        torch.cuda.empty_cache()
     return out
 
 
 def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
-    """Prefill qmm TFLOP/s at the Llama shapes; weights rotate over 4 copies."""
+    """Prefill qmm TFLOP/s at the Llama shapes; the weights rotate
+    over at least ROTATE_BYTES (and at least 4 copies)."""
     import torch
 
     gen = torch.Generator(device="cuda").manual_seed(1)
@@ -182,7 +201,7 @@ def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
     for bits in bits_list:
         for (name, N, K) in [("q/o", HIDDEN, HIDDEN), ("k/v", KV, HIDDEN), ("gate/up", FFN, HIDDEN),
                              ("down", HIDDEN, FFN)]:
-            lins = [Linear(N, K, gen, bits=bits) for _ in range(4)]
+            lins = [Linear(N, K, gen, bits=bits) for _ in range(rotation(qmv_bytes(0, N, K, bits), 4))]
             for M in Ms:
                 x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
                 y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
@@ -208,30 +227,34 @@ def bench_gguf(steps, warmup):
     for ty in (G.GgmlType.Q4_0, G.GgmlType.Q8_0, G.GgmlType.Q4K):
         vals, nbytes = ty.block_and_bytes()
         nraw = rows * cols // vals * nbytes
-        copies = 3
-        raws = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(copies)]
-        dense = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
         bits, gs = G.affine_config(ty)
-        aw = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device="cuda")
-        asb = torch.empty((rows, cols // gs), dtype=torch.float16, device="cuda")
-        abb = torch.empty_like(asb)
+        conv_bytes = rows * cols * bits // 8 + 2 * 2 * rows * (cols // gs)
+        # each copy is a distinct input and its own output, rotating >= ROTATE_BYTES
+        copies = rotation(nraw + rows * cols * 2)
+        raws = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(rotation(nraw))]
+        dense = [torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
+        cc = rotation(nraw + conv_bytes)
+        aw = [torch.empty((rows, cols * bits // 32), dtype=torch.int32, device="cuda") for _ in range(cc)]
+        asb = [torch.empty((rows, cols // gs), dtype=torch.float16, device="cuda") for _ in range(cc)]
+        abb = [torch.empty((rows, cols // gs), dtype=torch.float16, device="cuda") for _ in range(cc)]
 
         def deq(st):
-            for r in raws:
-                n.check(n.lib().eq_gguf_dequantize(dense.data_ptr(), r.data_ptr(), nraw, int(ty), rows, cols, 0,
-                                                   n.EQ_DEQUANT_AFFINE, n.EQ_DTYPE_BF16, st))
+            for i in range(copies):
+                n.check(n.lib().eq_gguf_dequantize(dense[i].data_ptr(), raws[i].data_ptr(), nraw, int(ty), rows, cols,
+                                                   0, n.EQ_DEQUANT_AFFINE, n.EQ_DTYPE_BF16, st))
 
         def conv(st):
-            for r in raws:
-                n.check(n.lib().eq_gguf_convert_affine(aw.data_ptr(), asb.data_ptr(), abb.data_ptr(), r.data_ptr(),
-                                                       nraw, int(ty), rows, cols, 0, st))
+            for i in range(cc):
+                n.check(n.lib().eq_gguf_convert_affine(aw[i].data_ptr(), asb[i].data_ptr(), abb[i].data_ptr(),
+                                                       raws[i].data_ptr(), nraw, int(ty), rows, cols, 0, st))
 
-        for label, fn, out_bytes in (("dequant_bf16", deq, rows * cols * 2),
-                                     ("convert_affine_g32", conv, aw.numel() * 4 + 2 * asb.numel() * 2)):
-            ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / copies
+        for label, fn, out_bytes, k in (("dequant_bf16", deq, rows * cols * 2, copies),
+                                        ("convert_affine_g32", conv, conv_bytes, cc)):
+            ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / k
             gbs = (nraw + out_bytes) / (ms * 1e-3) / 1e9
             out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-                                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": k}
+        del dense, aw, asb, abb
         if ty in (G.GgmlType.Q8_0, G.GgmlType.Q4K):
             # batch-1 linear straight from the blocks: y [1, 4096] = x [1, 14336] . W^T
             x = torch.randn((1, cols), device="cuda").to(torch.bfloat16)
@@ -242,10 +265,10 @@ def bench_gguf(steps, warmup):
                     n.check(n.lib().eq_gguf_linear(y.data_ptr(), x.data_ptr(), r.data_ptr(), nraw, int(ty), 1, rows,
                                                    cols, 0, n.EQ_DTYPE_BF16, st))
 
-            ms = Timer(lin).ms_per_replay(max(steps // 4, 5), warmup) / copies
+            ms = Timer(lin).ms_per_replay(max(steps // 4, 5), warmup) / len(raws)
             gbs = (nraw + cols * 2 + rows * 2) / (ms * 1e-3) / 1e9
             out[f"{ty.name} linear_M1"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-                                           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                                           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": len(raws)}
         del raws
         torch.cuda.empty_cache()
     return out
@@ -253,8 +276,8 @@ def bench_gguf(steps, warmup):
 
 def bench_qmm_n(steps, warmup):
     """transpose = false at M = 1 (x . W, W [K, N] packed along N; the
-    safemlx default layout): N x K = 4096 x 4096 and 14336 x 4096, 4 weight
-    copies rotating per replay; and the values product of the quantized KV
+    safemlx default layout): N x K = 4096 x 4096 and 14336 x 4096, weight
+    copies rotating >= ROTATE_BYTES per replay; and the values product of the quantized KV
     attention at one decode position (32 query heads over 8 KV heads, 1024
     cached tokens, D = 128: gather_qmm batches through quantized_matmul's
     broadcasting)."""
@@ -263,7 +286,7 @@ def bench_qmm_n(steps, warmup):
     n = _lib()
     out = {}
     for N, K in ((4096, 4096), (14336, 4096)):
-        copies = 4
+        copies = rotation(qmv_bytes(1, N, K))
         ws = [torch.randint(-2**31, 2**31 - 1, (K, N * BITS // 32), dtype=torch.int32, device="cuda")
               for _ in range(copies)]
         s = (0.01 * torch.rand((K, N // GS), device="cuda")).to(torch.bfloat16)
@@ -279,7 +302,8 @@ def bench_qmm_n(steps, warmup):
 
         ms = Timer(fn).ms_per_replay(max(steps // 4, 20), warmup) / copies
         gbs = qmv_bytes(1, N, K) / (ms * 1e-3) / 1e9
-        out[f"x.W_{N}x{K}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        out[f"x.W_{N}x{K}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                               "copies": copies}
         del ws
     # values product of the quantized KV attention: probs [1, 8, 4, 1, T] . values [1, 8, 1, T, D]
     n_kv, n_rep, T, D = 8, 4, 1024, 128
@@ -368,35 +392,35 @@ def bench_gather(steps, warmup):
 def bench_affine_codec(steps, warmup):
     """Affine dequantize (eq_dequantize: codes + scales + biases -> bf16) and
     quantize (eq_quantize: bf16 -> codes + scales + biases) of a 4096 x 14336
-    matrix, 4-bit g64 bf16; GB/s of bytes read + written, 3 copies rotating."""
+    matrix, 4-bit g64 bf16; GB/s of bytes read + written; each copy is a
+    distinct input and output, rotating >= ROTATE_BYTES."""
     import torch
 
     n = _lib()
-    rows, cols, copies = 4096, 14336, 3
+    rows, cols = 4096, 14336
+    packed = rows * cols * BITS // 8 + 2 * 2 * rows * (cols // GS)
+    copies = rotation(packed + rows * cols * 2)
     gen = torch.Generator(device="cuda").manual_seed(3)
     lins = [Linear(rows, cols, gen) for _ in range(copies)]
     dense = [torch.randn((rows, cols), device="cuda", generator=gen).to(torch.bfloat16) * 0.02 for _ in range(copies)]
-    out = torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda")
-    wq = torch.empty((rows, cols * BITS // 32), dtype=torch.int32, device="cuda")
-    sq = torch.empty((rows, cols // GS), dtype=torch.bfloat16, device="cuda")
-    bq = torch.empty_like(sq)
-    packed = rows * cols * BITS // 8 + 2 * 2 * rows * (cols // GS)
+    outs = [torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
     res = {}
 
     def deq(st):
-        for lin in lins:
-            n.check(n.lib().eq_dequantize(out.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(), rows,
+        for lin, o in zip(lins, outs):
+            n.check(n.lib().eq_dequantize(o.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(), rows,
                                           cols, GS, BITS, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, st))
 
     def quant(st):
-        for d in dense:
-            n.check(n.lib().eq_quantize(wq.data_ptr(), sq.data_ptr(), bq.data_ptr(), d.data_ptr(), rows, cols, GS,
-                                        BITS, b"affine", n.EQ_DTYPE_BF16, st))
+        for d, lin in zip(dense, lins):  # (written into the copies' own packed buffers)
+            n.check(n.lib().eq_quantize(lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(), d.data_ptr(), rows, cols,
+                                        GS, BITS, b"affine", n.EQ_DTYPE_BF16, st))
 
     for label, fn in (("dequantize_bf16", deq), ("quantize_bf16", quant)):
         ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / copies
         gbs = (packed + rows * cols * 2) / (ms * 1e-3) / 1e9
-        res[label] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        res[label] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                      "copies": copies}
     return res
 
 
@@ -530,6 +554,23 @@ def bench_decode_variants(layers, args):
     return out
 
 
+def host_cpu():
+    """The host CPU as lscpu names it (model, sockets, cores, threads)."""
+    import subprocess
+
+    info = {}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)"):
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info["affinity_cpus"] = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    return info
+
+
 def cpu_baseline(layer, budget_s=20.0):
     """The restated MLX CPU quantized matmul (oracle/eq_oracle.c or_qmm_t_f32), on the
     same packed inputs of one layer's 7 projections at M = 1, single-threaded and
@@ -545,7 +586,10 @@ def cpu_baseline(layer, budget_s=20.0):
                      lin.b.view(torch.int16).cpu().numpy().view(np.uint16)))
     x = {K: np.ascontiguousarray(orc.f32_to_bf16_bits(np.random.default_rng(0).standard_normal((1, K), dtype=np.float32)))
          for K in (HIDDEN, FFN)}
-    threads = max(1, min(16, os.cpu_count() or 1))
+    # one thread per host core the process may use, at most 16: the GPU box's
+    # CPU share for one GPU (its nproc reports the whole host)
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(16, avail))
     res = {}
     for nthreads in sorted({1, threads}):
         reps, t0 = 0, time.perf_counter()
@@ -660,7 +704,9 @@ def main():
                          f"{threads} threads ({v1[1]} passes in {v1[2]:.1f} s on 1 thread: "
                          f"{v1[0]:.3f} GB/s); restated MLX CPU _qmm_t loop (oracle/eq_oracle.c or_qmm_t_f32), "
                          f"f32 accumulate",
-               "single_thread_GB/s": round(v1[0], 3)}
+               "single_thread_GB/s": round(v1[0], 3), "host": host_cpu(),
+               "threads_note": "threads = min(16, CPUs in this process's affinity): 16 is the GPU box's CPU share "
+                               "per GPU"}
     del layers
     torch.cuda.empty_cache()
     if not args.quick:
@@ -716,6 +762,11 @@ def main():
         "cpu_baseline": cpu,
         "detail": detail,
     }
+    dropin = detail.get("decode_M1_per_projection")
+    if dropin:  # the path unchanged eredu callers take: one eq_quantized_matmul per projection
+        line["roofline"]["dropin_per_projection"] = {"GB/s": dropin["GB/s"],
+                                                     "frac": round(dropin["GB/s"] / HBM_PEAK_GBS, 4),
+                                                     "launches": dropin["launches"]}
     if step is not None:  # the metric's second figure: end-to-end decode of configs[4]
         line["decode_tok_s"] = step["tok/s"]
         line["decode_tok_s_frac_roofline"] = round(step["tok/s"] / step["roofline_tok/s"], 4)
