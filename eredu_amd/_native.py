@@ -31,6 +31,8 @@ SIGNATURES = {
     "eq_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _i32, _vp], _i32),
     "eq_rope_attention_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, ctypes.c_float,
                                   _i32, _vp], _i32),
+    "eq_rope_attention_decode_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32,
+                                          ctypes.c_float, _i32, _vp], _i32),
     "eq_silu_mul": ([_vp, _vp, _vp, _i64, _i32, _vp], _i32),
     "eq_embedding": ([_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp], _i32),
     "eq_argmax": ([_vp, _vp, _i64, _i64, _i32, _vp], _i32),

@@ -446,48 +446,130 @@ extern "C" int eq_rms_norm(void* out, void* x, const void* residual, const void*
     return check_launch("eq_rms_norm");
 }
 
+// Validation shared by the two attention entry points; the number of
+// position chunks on success.
+static bool attention_args_ok(const char* name, const void* out, const void* q, const void* k_new,
+                              const void* v_new, const void* k_cache, const void* v_cache, const float* freqs,
+                              int64_t pos, int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, int dtype) {
+    const std::string who(name);
+    if (!bf16_only(dtype, name)) return false;
+    if (!out || !q || !k_new || !v_new || !k_cache || !v_cache || !freqs) {
+        set_error(who + ": null pointer argument");
+        return false;
+    }
+    if (head_dim != kHeadDim) {
+        set_error(who + ": head_dim must be 128");
+        return false;
+    }
+    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads / n_kv_heads > 4 ||
+        n_kv_heads > 65535) {
+        set_error(who + ": n_heads must be 1-4 times n_kv_heads");
+        return false;
+    }
+    if (pos < 0 || max_seq <= 0 || pos >= max_seq || pos >= int64_t(kMaxChunks) * kAttnChunk) {
+        set_error(who + ": need 0 <= pos < max_seq and pos < 131072");
+        return false;
+    }
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(v_new, 16)) {
+        set_error(who + ": cache and value pointers must be 16-byte aligned");
+        return false;
+    }
+    return true;
+}
+
+// The two attention passes: per-chunk partial softmax states into ws, then
+// their combination per query head.
+static void launch_attention(float* ws, void* out, const void* q, const void* k_new, const void* v_new, void* k_cache,
+                             void* v_cache, const float* freqs, int64_t pos, int64_t max_seq, int n_heads,
+                             int n_kv_heads, int nchunks, float scale, hipStream_t st) {
+    attn_partial_kernel<<<dim3(unsigned(n_kv_heads), unsigned(nchunks)), dim3(256), 0, st>>>(
+        ws, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
+        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, int(pos), int(max_seq), n_heads,
+        n_kv_heads, nchunks, scale);
+    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, nchunks);
+}
+
+static size_t attention_scratch_bytes(int64_t pos, int n_heads, int& nchunks) {
+    nchunks = int((pos + kAttnChunk) / kAttnChunk);
+    return size_t(n_heads) * size_t(nchunks) * (kHeadDim + 2) * sizeof(float);
+}
+
 extern "C" int eq_rope_attention_decode(void* out, const void* q, const void* k_new, const void* v_new,
                                         void* k_cache, void* v_cache, const float* freqs, int64_t pos,
                                         int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
                                         int dtype, eq_stream_t stream) {
     clear_error();
-    if (!bf16_only(dtype, "eq_rope_attention_decode")) return 1;
-    if (!out || !q || !k_new || !v_new || !k_cache || !v_cache || !freqs) {
-        set_error("eq_rope_attention_decode: null pointer argument");
+    if (!attention_args_ok("eq_rope_attention_decode", out, q, k_new, v_new, k_cache, v_cache, freqs, pos, max_seq,
+                           n_heads, n_kv_heads, head_dim, dtype))
         return 1;
-    }
-    if (head_dim != kHeadDim) {
-        set_error("eq_rope_attention_decode: head_dim must be 128");
-        return 1;
-    }
-    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads / n_kv_heads > 4 ||
-        n_kv_heads > 65535) {
-        set_error("eq_rope_attention_decode: n_heads must be 1-4 times n_kv_heads");
-        return 1;
-    }
-    if (pos < 0 || max_seq <= 0 || pos >= max_seq || pos >= int64_t(kMaxChunks) * kAttnChunk) {
-        set_error("eq_rope_attention_decode: need 0 <= pos < max_seq and pos < 131072");
-        return 1;
-    }
-    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(v_new, 16)) {
-        set_error("eq_rope_attention_decode: cache and value pointers must be 16-byte aligned");
-        return 1;
-    }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const int nchunks = int((pos + kAttnChunk) / kAttnChunk);
-    const size_t ws_bytes = size_t(n_heads) * size_t(nchunks) * (kHeadDim + 2) * sizeof(float);
+    int nchunks = 0;
+    const size_t ws_bytes = attention_scratch_bytes(pos, n_heads, nchunks);
     float* ws = static_cast<float*>(ws_acquire(nullptr, ws_bytes, st));
     if (!ws) {
         set_error("eq_rope_attention_decode: no workspace (its stream's workspace cannot grow while capturing: "
                   "make one call of at least this position on the stream before capturing)");
         return 1;
     }
-    attn_partial_kernel<<<dim3(unsigned(n_kv_heads), unsigned(nchunks)), dim3(256), 0, st>>>(
-        ws, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
-        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, int(pos), int(max_seq), n_heads,
-        n_kv_heads, nchunks, scale);
-    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, nchunks);
+    launch_attention(ws, out, q, k_new, v_new, k_cache, v_cache, freqs, pos, max_seq, n_heads, n_kv_heads, nchunks,
+                     scale, st);
     return check_launch("eq_rope_attention_decode");
+}
+
+// ---------------------------------------------------- allocation-free variant
+
+// Scratch of eq_rope_attention_decode_noalloc: the attention partials
+// (n_heads * chunks * 520 bytes).  Every GPU the library runs on holds its own
+// copy until the process ends.  The array's name is a host-side stand-in in
+// host code; the device address comes from attention_scratch_address().
+constexpr size_t kAttnScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) char scratch[kAttnScratchBytes];
+
+// Device address of `scratch` on the current device, resolved on the first
+// call on each device (with that device current) and kept.
+static void* attention_scratch_address() {
+    static std::mutex mu;
+    static void* addr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("eq_rope_attention_decode_noalloc: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error(std::string("eq_rope_attention_decode_noalloc: scratch address lookup failed: ") +
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
+extern "C" int eq_rope_attention_decode_noalloc(void* out, const void* q, const void* k_new, const void* v_new,
+                                                void* k_cache, void* v_cache, const float* freqs, int64_t pos,
+                                                int64_t max_seq, int n_heads, int n_kv_heads, int head_dim,
+                                                float scale, int dtype, eq_stream_t stream) {
+    clear_error();
+    if (!attention_args_ok("eq_rope_attention_decode_noalloc", out, q, k_new, v_new, k_cache, v_cache, freqs, pos,
+                           max_seq, n_heads, n_kv_heads, head_dim, dtype))
+        return 1;
+    int nchunks = 0;
+    const size_t ws_bytes = attention_scratch_bytes(pos, n_heads, nchunks);
+    if (ws_bytes > kAttnScratchBytes) {
+        set_error("eq_rope_attention_decode_noalloc: n_heads * (pos / 32 + 1) * 520 = " + std::to_string(ws_bytes) +
+                  " bytes of scratch, more than the " + std::to_string(kAttnScratchBytes) +
+                  " this entry point holds (use eq_rope_attention_decode)");
+        return 1;
+    }
+    void* ws = attention_scratch_address();
+    if (!ws) return 1;
+    launch_attention(static_cast<float*>(ws), out, q, k_new, v_new, k_cache, v_cache, freqs, pos, max_seq, n_heads,
+                     n_kv_heads, nchunks, scale, reinterpret_cast<hipStream_t>(stream));
+    return check_launch("eq_rope_attention_decode_noalloc");
 }
 
 extern "C" int eq_silu_mul(void* out, const void* gate, const void* up, int64_t n, int dtype, eq_stream_t stream) {

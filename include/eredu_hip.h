@@ -240,12 +240,31 @@ int eq_rms_norm(void* out, void* hidden, const void* residual, const void* weigh
  *   reading KV head h / (n_heads / n_kv_heads).
  * Replaces Attention::attend (llama.rs:296-330): rotary forward, cache
  * update_for_attention and fast::scaled_dot_product_attention.  head_dim must
- * be 128 and n_heads / n_kv_heads at most 4.  Uses a library-owned workspace:
- * the first call on a device must not be under stream capture. */
+ * be 128 and n_heads / n_kv_heads at most 4.  The attention partials live in
+ * the library workspace of `stream` (grow-only, never freed while the process
+ * runs); it cannot grow while `stream` is capturing, so a capture needs an
+ * earlier call at least this large on that stream (else the call fails), or
+ * eq_rope_attention_decode_noalloc. */
 int eq_rope_attention_decode(void* out, const void* q, const void* k_new, const void* v_new,
                              void* k_cache, void* v_cache, const float* freqs, int64_t pos,
                              int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
                              int dtype, eq_stream_t stream);
+
+/* eq_rope_attention_decode without any device allocation: no counterpart in
+ * the reference.  For callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments, validation and results (the same kernels); the
+ * attention partials live in a library-owned static device array of 8 MiB
+ * per GPU, held until the process ends, instead of the stream's workspace.
+ * A call needing more than that -- n_heads * (pos / 32 + 1) * 520 bytes, e.g.
+ * 32 heads at pos >= 16128 -- is rejected with a message.  Every call on one
+ * GPU shares that GPU's array: calls that overlap in time on one GPU (two
+ * streams, or two processes' graphs) race and must be serialised by the
+ * caller.  The first call on each device resolves the array's address. */
+int eq_rope_attention_decode_noalloc(void* out, const void* q, const void* k_new, const void* v_new,
+                                     void* k_cache, void* v_cache, const float* freqs, int64_t pos,
+                                     int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
+                                     int dtype, eq_stream_t stream);
 
 /* out[n] = silu(gate) * up, silu(x) = x * sigmoid(x), each op rounded to bf16
  * (Mlp::hidden, llama.rs:414-422; eredu/src/backend/mlx/nn/layers.rs:21).

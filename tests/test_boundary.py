@@ -27,7 +27,7 @@ def test_header_declares_the_boundary():
         ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
          "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
-         "eq_gguf_linear", "eq_gather_qmm"]
+         "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc"]
     )
 
 
