@@ -405,6 +405,59 @@ bool bf16_only(int dtype, const char* what) {
 }
 
 }  // namespace
+// Multi-workgroup argmax of one row per blockIdx.y: workgroup blockIdx.x
+// scans its slice (a multiple of 8 values, 16-byte pieces), reduces to its
+// first largest value, and folds it into the row's 64-bit key with an atomic
+// maximum -- key = (order-preserving image of the value) << 32 | (2^32 - 1 -
+// index), so the largest value wins and, among equal values, the lowest
+// index.  The last workgroup of the row (arrival counter) reads and clears the
+// key and writes the index.  NaNs are skipped as argmax_take skips them; a
+// row with nothing but NaNs gives index 0.
+__global__ __launch_bounds__(256) void argmax_wide_kernel(int32_t* __restrict__ out,
+                                                          const uint16_t* __restrict__ logits, int64_t n, int slice,
+                                                          unsigned* __restrict__ counters,
+                                                          unsigned long long* __restrict__ keys) {
+    __shared__ float bv[4];
+    __shared__ int64_t bi[4];
+    __shared__ unsigned ticket;
+    const int64_t row = blockIdx.y;
+    const uint16_t* r = logits + row * n;
+    const int64_t lo = int64_t(blockIdx.x) * slice, hi = lo + slice < n ? lo + slice : n;
+    float best = -INFINITY;
+    int64_t idx = INT64_MAX;
+    const uint4* rv = reinterpret_cast<const uint4*>(r);
+    for (int64_t v = lo / 8 + threadIdx.x; v < hi / 8; v += 256) {
+        const uint4 a = rv[v];
+        const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a);
+#pragma unroll
+        for (int e = 0; e < 8; e++) argmax_take(bf16_bits_to_f32((pa[e >> 1] >> (16 * (e & 1))) & 0xffffu), v * 8 + e, best, idx);
+    }
+    for (int64_t i = hi / 8 * 8 + threadIdx.x; i < hi; i += 256) argmax_take(bf16_bits_to_f32(r[i]), i, best, idx);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int64_t oi = __shfl_xor(idx, o);
+        argmax_take(ov, oi, best, idx);
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) bv[wave] = best, bi[wave] = idx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) argmax_take(bv[w], bi[w], best, idx);
+        if (idx < n) {
+            const uint32_t b = __float_as_uint(best);
+            const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+            const unsigned long long key = (static_cast<unsigned long long>(ord) << 32) | (0xFFFFFFFFu - uint32_t(idx));
+            __hip_atomic_fetch_max(keys + row, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (!last_arriver(counters + row, gridDim.x, &ticket)) return;
+    if (threadIdx.x == 0) {
+        const unsigned long long key = __hip_atomic_exchange(keys + row, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        out[row] = key ? int32_t(0xFFFFFFFFu - uint32_t(key & 0xFFFFFFFFull)) : 0;
+    }
+}
+
 }  // namespace eq
 
 using namespace eq;
@@ -627,7 +680,22 @@ extern "C" int eq_argmax(int32_t* out, const void* logits, int64_t rows, int64_t
         return 1;
     }
     if (rows == 0) return 0;
-    argmax_kernel<<<dim3(unsigned(rows)), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        out, static_cast<const uint16_t*>(logits), n, n % 8 == 0 && aligned(logits, 16));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    // Long rows: several workgroups per row (a key and a counter per row in
+    // the stream's arrival counters); otherwise -- or when the counters
+    // cannot be provided (first use under capture) -- one workgroup per row.
+    constexpr int kMaxWideRows = kWsCounters / 4;
+    if (n >= 16384 && n % 8 == 0 && aligned(logits, 16) && rows <= kMaxWideRows) {
+        if (unsigned* c = ws_counters(nullptr, st)) {
+            const int slice = int(((n + 63) / 64 + 2047) / 2048 * 2048);  // at most 64 slices, multiples of 2048
+            const int groups = int((n + slice - 1) / slice);
+            unsigned long long* keys = reinterpret_cast<unsigned long long*>(c + kWsCounters / 2);
+            argmax_wide_kernel<<<dim3(unsigned(groups), unsigned(rows)), dim3(256), 0, st>>>(
+                out, static_cast<const uint16_t*>(logits), n, slice, c, keys);
+            return check_launch("eq_argmax");
+        }
+    }
+    argmax_kernel<<<dim3(unsigned(rows)), dim3(1024), 0, st>>>(out, static_cast<const uint16_t*>(logits), n,
+                                                              n % 8 == 0 && aligned(logits, 16));
     return check_launch("eq_argmax");
 }

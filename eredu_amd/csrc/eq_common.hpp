@@ -85,6 +85,35 @@ __device__ __forceinline__ int opaque_one() {
 // room for the immediate offsets added to it.
 constexpr uint32_t kOutOfRange = 0xC0000000u;
 
+// ------------------------------------------------- cross-workgroup hand-off
+//
+// Each XCD has its own L2, and those caches are not kept coherent with each
+// other for ordinary loads and stores; device-scope atomics are.  A kernel
+// whose workgroups combine results within one launch does it through
+// device-scope atomics and an arrival counter (last_arriver).  Measured on
+// MI355X, such a hand-off (store completion, the counter's round trip, the
+// last workgroup's reads) costs more than a kernel boundary in a HIP graph,
+// so the kernels here use it only where the combined data is a few words.
+
+// s_waitcnt vmcnt(0): every vector memory operation of this wave, stores
+// included, has completed.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Counts this workgroup at `counter` after all its threads' device-scope
+// stores have completed; true in the workgroup that arrives last of
+// `expected`, which also resets the counter to zero for the next launch.
+// Every workgroup must call it exactly once (it has two barriers), with the
+// same `ticket` slot of LDS.
+__device__ __forceinline__ bool last_arriver(unsigned* counter, unsigned expected, unsigned* ticket) {
+    wait_vmem_all();
+    __syncthreads();
+    if (threadIdx.x == 0) *ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const bool last = *ticket == expected - 1;
+    if (last && threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return last;
+}
+
 // Pulls every 64-byte line of a kernel's by-value argument block into the
 // scalar cache with independent loads and one wait.  The block is cold at
 // each dispatch; without this, code that indexes it with computed values
@@ -312,12 +341,23 @@ __device__ __forceinline__ bool gather_batch(const GatherIdx& g, int64_t b, int6
 struct WsSource {
     void* ptr;
     size_t cap;
+    unsigned* counters;  // kWsCounters zeroed 32-bit words that kernels leave zeroed
 };
+
+// Arrival counters of one stream (or fixed region): last-arriver kernels
+// count their workgroups here and reset each counter they used, so the words
+// are zero between launches.
+constexpr int kWsCounters = 16384;
 
 // At least `bytes` of device scratch, 256-byte aligned, or null when none can
 // be provided (fixed region too small, or the library buffer would have to
 // grow while `st` is capturing).  Launches that use it are ordered on `st`.
 void* ws_acquire(const WsSource* src, size_t bytes, hipStream_t st);
+
+// The kWsCounters arrival counters of `src` (null: the library's, one
+// zero-filled buffer per device and stream, used for nothing else), or null
+// when they cannot be provided (first use while `st` is capturing).
+unsigned* ws_counters(const WsSource* src, hipStream_t st);
 
 // Routed experts over sorted expert indices (gather_qmm with sorted_indices,
 // transpose, one activation row per route, bf16 x, 4/8-bit, bf16/f16

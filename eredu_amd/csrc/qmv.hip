@@ -604,6 +604,9 @@ __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, G
 #ifndef EQ_QMV_RING
 #define EQ_QMV_RING 2
 #endif
+#ifndef EQ_QMV_WAVES_PER_CU
+#define EQ_QMV_WAVES_PER_CU 8
+#endif
 constexpr int kQmvLdsMaxWaves = 8;              // waves per workgroup of the LDS variant, at most
 constexpr int kQmvLdsWaves = EQ_QMV_LDS_WAVES;  // the planner's choice
 
@@ -1160,10 +1163,11 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     plan.lds = lds;
     plan.vec = vec;
     plan.tail = tail;
-    // Workgroups resident per CU: 8 waves (2 per SIMD, the register budget).
-    const int per_cu = 8 / W > 0 ? 8 / W : 1;
+    // Workgroups resident per CU: EQ_QMV_WAVES_PER_CU waves.
+    const int per_cu = EQ_QMV_WAVES_PER_CU / W > 0 ? EQ_QMV_WAVES_PER_CU / W : 1;
     plan.waves = W;
-    plan.grid = tiles < per_cu * device_cu_count() ? tiles : per_cu * device_cu_count();
+    const int cap = per_cu * device_cu_count();
+    plan.grid = tiles < cap ? tiles : cap;
     return true;
 }
 

@@ -14,6 +14,11 @@
 //    plan without scratch, or fails with a message).
 //  * a fixed region named by the caller (the allocation-free entry points):
 //    never grown; a request beyond its size gets nothing.
+//
+// Kernels that hand results between workgroups of one launch also need
+// arrival counters that start at zero: one small zero-filled buffer per
+// (device, stream), separate from the workspace (whose contents other
+// kernels overwrite), which every such kernel leaves zeroed when it ends.
 #include <map>
 #include <mutex>
 #include <utility>
@@ -33,6 +38,10 @@ struct OwnedBuffer {
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, OwnedBuffer>& owned_buffers() {
     static auto* m = new std::map<std::pair<int, hipStream_t>, OwnedBuffer>();  // lives until exit
+    return *m;
+}
+std::map<std::pair<int, hipStream_t>, unsigned*>& counter_buffers() {
+    static auto* m = new std::map<std::pair<int, hipStream_t>, unsigned*>();  // lives until exit
     return *m;
 }
 std::vector<void*>& retired_buffers() {
@@ -65,6 +74,31 @@ void* ws_acquire(const WsSource* src, size_t bytes, hipStream_t st) {
     buf.ptr = p;
     buf.cap = want;
     return p;
+}
+
+unsigned* ws_counters(const WsSource* src, hipStream_t st) {
+    if (src) return src->counters;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    unsigned*& c = counter_buffers()[std::make_pair(dev, st)];
+    if (c) return c;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, size_t(kWsCounters) * sizeof(unsigned)) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    // zeroed once, in stream order before any kernel of `st` counts in it;
+    // every kernel leaves its counters at zero again
+    if (hipMemsetAsync(p, 0, size_t(kWsCounters) * sizeof(unsigned), st) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(p);
+        return nullptr;
+    }
+    c = static_cast<unsigned*>(p);
+    return c;
 }
 
 }  // namespace eq

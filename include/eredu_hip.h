@@ -277,7 +277,11 @@ int eq_embedding(void* out, const void* table, const int32_t* tokens, int64_t n_
                  int64_t dim, int dtype, eq_stream_t stream);
 
 /* out[r] = first index of the largest value of logits[r, 0..n) (greedy
- * decoding of the model's logits, llama.rs:649-658). */
+ * decoding of the model's logits, llama.rs:649-658); NaNs are skipped (a row
+ * of NaNs gives 0).  Rows of 16384 or more 16-byte aligned values (up to 4096
+ * rows) are split over several workgroups that meet at arrival counters of
+ * `stream` (allocated on the stream's first such call; under capture before
+ * that, one workgroup per row is used). */
 int eq_argmax(int32_t* out, const void* logits, int64_t rows, int64_t n, int dtype, eq_stream_t stream);
 
 #ifdef __cplusplus

@@ -329,3 +329,23 @@ def test_prologue_rejects_unsupported(cuda):
                           lin2.biases.data_ptr(), 512, 4096)
     assert call(n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, None, wv.data_ptr(), x2.data_ptr(), 1e-5)) == 1
     assert "overlap" in n.lib().eq_last_error().decode()
+
+
+@pytest.mark.parametrize("n", [16384, 128256, 200000, 1000])
+def test_argmax_wide_rows_ties_and_nans(cuda, n):
+    """Rows long enough to be split over workgroups (and one short row that is
+    not): ties resolve to the first index across workgroup boundaries, NaNs are
+    skipped, a row of NaNs gives 0, -inf counts as a value."""
+    print(f"[case] argmax n={n}", flush=True)
+    rows = 5
+    x = randn_bits((rows, n), n)
+    big = bits([50.0])[0]
+    x[0, n - 1] = big                      # the last element
+    x[1, 3] = big
+    x[1, n // 2 + 3] = big                 # a tie in a later workgroup: the first wins
+    x[2, :] = 0x7FC0                       # all NaN
+    x[3, :] = bits([-np.inf])[0]           # all -inf: index 0
+    x[4, 7] = 0x7FC0                       # a NaN before the maximum is skipped
+    x[4, n - 2] = big
+    got = E.argmax(dev_bf16(x)).cpu().numpy()
+    assert list(got) == [n - 1, 3, 0, 0, n - 2]
