@@ -14,6 +14,8 @@
 // stores are contiguous.  Every product in these decoders is exact in f32
 // (an 11-bit f16 significand times a code of at most 8 bits), so each output
 // carries exactly one rounding, as on the reference's CPU.
+#include <atomic>
+
 #include "eq_common.hpp"
 
 namespace eq {
@@ -479,6 +481,255 @@ __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, cons
     }
 }
 
+// ------------------------------------------- native Q4_K linear on MFMA
+//
+// The same product as q4k_linear for up to 8 activation rows per launch, on
+// v_mfma_f32_16x16x32_bf16.  A workgroup takes a tile of 16 weight rows and
+// its W waves split each row's superblocks into contiguous ranges.  Per
+// superblock, lane (n = lane % 16, kq = lane / 16) loads the 16-byte header
+// of tile row n (d, dmin, the 12 scale/min bytes) and code chunks kq and
+// kq + 4, 16 bytes each (bytes 16 kq and 64 + 16 kq of the 128 code bytes).
+// Chunk 2p + h holds values 16 h .. 16 h + 15 of groups 2p (low nibbles) and
+// 2p + 1 (high nibbles), so lane kq sees groups 2a, 2a + 1 (chunk kq) and
+// 4 + 2a, 5 + 2a (chunk kq + 4), a = kq / 2, values 16 (kq % 2) .. + 15.
+//
+// Eight MFMA steps per superblock.  Step s takes chunk cc = s / 4, nibble
+// plane o = s % 2 and bytes 8 hb .. 8 hb + 7 (hb = (s / 2) % 2): eight codes of
+// group 4 cc + 2a + o as bf16 128 + q, in byte order (B operand).  The four
+// lane blocks of one step cover two groups (a = 0, 1), so the A operand
+// splits its 16 rows as (a, m), row 8a + m = activation row m, non-zero only
+// in the lane blocks of its own a (other lanes read a zero block of LDS).
+// Result lane (n, kq) then holds rows 4kq .. 4kq + 3 = (a = kq / 2,
+// m = 4 (kq % 2) + i) of the step's group: one accumulator per (cc, o).  Per
+// group and row:
+//   sum x (d sc q - dmin m) = d sc (t - 128 xs) - dmin m xs,
+// t = sum x (128 + q) from the MFMAs, xs = sum x over the group, computed once
+// per workgroup while the activations are staged into LDS.
+//
+// LDS: activation row m at m * xstride (xstride = 2K + 16, so the rows of one
+// A read fall in different banks), then xs [M][K / 32] f32, then a zero
+// block, then the cross-wave partial sums.
+// Launch shapes (waves per workgroup W, superblocks in the load ring D; loads
+// run D - 1 superblocks ahead), measured on MI355X at the decode shapes of an
+// 8B model with payloads rotating past the caches: rows of 56 superblocks
+// (K = 14336) run best with W = 8, D = 2; rows of 16 (K = 4096) with W = 4,
+// D = 4 (more workgroups per CU, each wave a longer run).  A 16-row tile is
+// the whole grid's unit, so the short rows want the smaller workgroups.
+constexpr int kQ4kMaxWaves = 8;
+constexpr int kQ4kMaxRows = 8;           // activation rows per launch
+constexpr int kQ4kZeroBytes = 512;       // zero block: the largest step offset (336) plus a read
+
+typedef uint32_t q4k_u32x4 __attribute__((ext_vector_type(4)));
+
+struct Q4kMfmaArgs {
+    uint16_t* y;
+    const uint16_t* x;
+    const uint8_t* raw;
+    int M, N, K;  // M <= kQ4kMaxRows; y [M, ldy] (columns [0, N)), x [M, K]
+    int ldy;
+    int sbw;      // superblocks per wave
+    int xstride;  // LDS bytes per staged activation row
+    int xs_lds, zero_lds, red_lds;
+};
+
+// One superblock of one lane: the header and its two code chunks.
+struct Q4kSb {
+    q4k_u32x4 h, c0, c1;
+};
+
+// Eight codes of one nibble plane (o = 0 low, 1 high) of bytes b0 .. b7
+// (words w0, w1) as bf16 128 + q, in byte order: mask, then byte permutes
+// against the constant 0x43 bytes (0x43XX = 128 + XX as bf16).
+__device__ __forceinline__ bf16x8 q4k_plane8(uint32_t w0, uint32_t w1, int o) {
+    const uint32_t c43 = 0x43434343u;
+    const uint32_t l0 = (o ? w0 >> 4 : w0) & 0x0f0f0f0fu;
+    const uint32_t l1 = (o ? w1 >> 4 : w1) & 0x0f0f0f0fu;
+    q4k_u32x4 p;
+    p[0] = __builtin_amdgcn_perm(c43, l0, 0x04010400u);  // [b0, 43, b1, 43]
+    p[1] = __builtin_amdgcn_perm(c43, l0, 0x04030402u);  // [b2, 43, b3, 43]
+    p[2] = __builtin_amdgcn_perm(c43, l1, 0x04010400u);
+    p[3] = __builtin_amdgcn_perm(c43, l1, 0x04030402u);
+    return __builtin_bit_cast(bf16x8, p);
+}
+
+__device__ __forceinline__ void q4k_retire(const Q4kSb& b) { asm volatile("" ::"v"(b.h), "v"(b.c0), "v"(b.c1)); }
+
+// MREG: result registers per lane that can hold a live activation row (1 when M == 1, else 4).
+template <bool BIG, int MREG, int W, int D>
+__global__ __launch_bounds__(64 * W) void q4k_mfma_linear(const Q4kMfmaArgs args) {
+    static_assert(D >= 2, "the ring needs two superblocks");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ln = lane & 15, kq = lane >> 4, a = kq >> 1;
+    const int M = args.M, N = args.N, K = args.K;
+    const int n0 = blockIdx.x * 16;
+    const int nsb = K / 256, G = K / 32;
+    const uint32_t row_bytes = uint32_t(nsb) * 144u;
+
+    // This wave's superblocks [sb0, sb0 + cnt).
+    const int sb0 = min(nsb, wave * args.sbw);
+    const int cnt = min(nsb, sb0 + args.sbw) - sb0;
+
+    // Weight loads: rows past N read zero (offsets out of range, fixed step 0).
+    const bool row_live = n0 + ln < N;
+    const __amdgpu_buffer_rsrc_t wr = raw_rsrc(args.raw, uint32_t(N) * row_bytes);
+    const uint32_t hoff = row_live ? uint32_t(n0 + ln) * row_bytes : kOutOfRange;
+    const uint32_t hstep = row_live ? 144u : 0u;
+    auto load_sb = [&](Q4kSb& b, int j) __attribute__((always_inline)) {
+        // superblocks past the wave's range read zero
+        const uint32_t o = j < cnt ? hoff + uint32_t(sb0 + j) * hstep : kOutOfRange;
+        b.h = __builtin_bit_cast(q4k_u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0));
+        b.c0 = __builtin_bit_cast(q4k_u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o + 16u + 16u * kq, 0, 0));
+        b.c1 = __builtin_bit_cast(q4k_u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o + 80u + 16u * kq, 0, 0));
+    };
+
+    // Stage x (natural order, row m at m * xstride) and the group sums xs.
+    // A round takes NCH 16-byte chunks per thread; four consecutive threads
+    // hold the four chunks of one group.  The first round's loads go out
+    // before the first D - 1 superblocks of the ring, the stores after them:
+    // loads complete in order, so the stores wait for the activations only.
+    constexpr int NCH = 4;
+    const __amdgpu_buffer_rsrc_t xr = raw_rsrc(args.x, uint32_t(M) * uint32_t(K) * 2u);
+    const int cpr = K / 8, total = M * cpr;
+    auto stage_load = [&](int c0, q4k_u32x4* v) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const int c = c0 + i * 64 * W + int(threadIdx.x);
+            const int m = c < total ? c / cpr : 0, cc = c - m * cpr;
+            const uint32_t off = c < total ? (uint32_t(m) * uint32_t(K) + uint32_t(cc) * 8u) * 2u : kOutOfRange;
+            v[i] = __builtin_bit_cast(q4k_u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        }
+    };
+    auto stage_store = [&](int c0, const q4k_u32x4* v) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const int c = c0 + i * 64 * W + int(threadIdx.x);
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) s += bf16_bits_to_f32(v[i][e] & 0xffffu) + bf16_bits_to_f32(v[i][e] >> 16);
+            s += __shfl_xor(s, 1);
+            s += __shfl_xor(s, 2);
+            if (c < total) {
+                const int m = c / cpr, cc = c - m * cpr;
+                *reinterpret_cast<q4k_u32x4*>(smem + m * args.xstride + cc * 16) = v[i];
+                if ((cc & 3) == 0) reinterpret_cast<float*>(smem + args.xs_lds)[m * G + (cc >> 2)] = s;
+            }
+        }
+    };
+    q4k_u32x4 xv[NCH];
+    stage_load(0, xv);
+    Q4kSb ring[D];
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) load_sb(ring[d], d);
+    stage_store(0, xv);
+    for (int c0 = NCH * 64 * W; c0 < total; c0 += NCH * 64 * W) {  // wave-uniform trip count
+        stage_load(c0, xv);
+        stage_store(c0, xv);
+    }
+    if (int(threadIdx.x) < kQ4kZeroBytes / 16)
+        *reinterpret_cast<q4k_u32x4*>(smem + args.zero_lds + threadIdx.x * 16) = q4k_u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+
+    // A operand: lane row ln = (ln / 8, m = ln % 8), live in the lane blocks of
+    // its own a; its 16-byte read for step s of superblock sb is at
+    // xa + 512 sb + 256 cc + 64 o + 16 hb.
+    const int a_m = ln & 7;
+    const bool a_live = (ln >> 3) == a && a_m < M;
+    const uint32_t xa = a_live ? uint32_t(a_m * args.xstride + 128 * a + 32 * (kq & 1)) : uint32_t(args.zero_lds);
+    const uint32_t xstep = a_live ? 512u : 0u;
+    // Group sums of this lane's result rows m_i = 4 (kq % 2) + i (rows past M read row 0:
+    // their results are not stored): groups 4cc + 2a + o of superblock sb at
+    // xsb[i] + 32 sb + 16 cc + 4 o.
+    uint32_t xsb[MREG];
+#pragma unroll
+    for (int i = 0; i < MREG; i++) {
+        const int m = 4 * (kq & 1) + i;
+        xsb[i] = uint32_t(args.xs_lds + ((m < M ? m : 0) * G + 2 * a) * 4);
+    }
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Q4kSb& b, int j) __attribute__((always_inline)) {
+        const int sb = sb0 + j;
+        // activations first: the LDS reads overlap the unpacking
+        const uint32_t xb = xa + uint32_t(sb) * xstep;
+        bf16x8 av[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            av[s] = *reinterpret_cast<const bf16x8*>(smem + xb + 256 * (s >> 2) + 64 * (s & 1) + 16 * ((s >> 1) & 1));
+        float xs[MREG][4];
+#pragma unroll
+        for (int i = 0; i < MREG; i++) {
+            const float* p = reinterpret_cast<const float*>(smem + xsb[i] + 32u * uint32_t(sb));
+            xs[i][0] = p[0], xs[i][1] = p[1], xs[i][2] = p[4], xs[i][3] = p[5];  // (cc, o) = (0,0) (0,1) (1,0) (1,1)
+        }
+        f32x4 t[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) t[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int cc = s >> 2, o = s & 1, hb = (s >> 1) & 1;
+            const q4k_u32x4& cw = cc ? b.c1 : b.c0;
+            const bf16x8 bq = q4k_plane8(cw[2 * hb], cw[2 * hb + 1], o);
+            t[2 * cc + o] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[s], bq, t[2 * cc + o], 0, 0, 0);
+        }
+        // Factors of groups 2a + o (bytes 2a + o of the scale words h1, h2) and
+        // 4 + 2a + o (low 6 bits from h3, top 2 from h1 / h2): scale_min of
+        // convert.rs:429-438.
+        const uint32_t h0 = b.h[0];
+        const float d = f16_bits_to_f32(BIG ? bswap16(h0 & 0xffffu) : (h0 & 0xffffu));
+        const float dmin = f16_bits_to_f32(BIG ? bswap16(h0 >> 16) : (h0 >> 16));
+        const uint32_t H1 = b.h[1] >> (16 * a), H2 = b.h[2] >> (16 * a), H3 = b.h[3] >> (16 * a);
+#pragma unroll
+        for (int o = 0; o < 2; o++) {
+            const uint32_t s1 = H1 >> (8 * o), s2 = H2 >> (8 * o), s3 = H3 >> (8 * o);
+            const uint32_t sc0 = s1 & 63u, mn0 = s2 & 63u;
+            const uint32_t sc1 = (s3 & 15u) | (((s1 >> 6) & 3u) << 4);
+            const uint32_t mn1 = ((s3 >> 4) & 15u) | (((s2 >> 6) & 3u) << 4);
+            const float ds0 = d * float(sc0), ds1 = d * float(sc1);
+            const float be0 = fmaf(-128.f, ds0, -dmin * float(mn0));
+            const float be1 = fmaf(-128.f, ds1, -dmin * float(mn1));
+#pragma unroll
+            for (int i = 0; i < MREG; i++) {
+                acc[i] = fmaf(ds0, t[o][i], fmaf(be0, xs[i][o], acc[i]));
+                acc[i] = fmaf(ds1, t[2 + o][i], fmaf(be1, xs[i][2 + o], acc[i]));
+            }
+        }
+    };
+
+    // The ring: loads run D - 1 superblocks ahead; each compute sits in a
+    // basic block of its own, so the loads issued before it stay there.
+    for (int j = 0; j < cnt; j += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            load_sb(ring[(d + D - 1) % D], j + d + D - 1);
+            if (j + d < cnt) compute(ring[d], j + d);
+            else q4k_retire(ring[d]);
+        }
+    }
+
+    // Fold the two a halves (lane blocks kq and kq ^ 2 hold the same rows),
+    // then sum the waves through LDS in a fixed order.
+#pragma unroll
+    for (int i = 0; i < MREG; i++) acc[i] += __shfl_xor(acc[i], 32);
+    float* red = reinterpret_cast<float*>(smem + args.red_lds);
+    if (kq < 2) {
+#pragma unroll
+        for (int i = 0; i < MREG; i++) {
+            const int m = 4 * kq + i;
+            if (m < M) red[(wave * kQ4kMaxRows + m) * 16 + ln] = acc[i];
+        }
+    }
+    __syncthreads();
+    if (int(threadIdx.x) < 16 * M) {
+        const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) v += red[(w * kQ4kMaxRows + m) * 16 + n];
+        if (n0 + n < N) args.y[int64_t(m) * args.ldy + n0 + n] = uint16_t(f32_to_bf16_bits(v));
+    }
+}
+
 // Q8_0: 34-byte blocks are not 4-byte aligned, so a wave first copies a run
 // of up to 256 blocks of its row into LDS (16-byte loads when the run is
 // 16-byte aligned, else 2-byte loads), then each lane takes whole blocks.
@@ -683,6 +934,84 @@ void launch_dense(int type, bool big, bool native, const uint8_t* raw, int64_t n
         }
     }
 }
+
+// LDS layout of q4k_mfma_linear for mc activation rows of length K; returns
+// the total bytes.
+int64_t q4k_mfma_layout(int64_t K, int mc, Q4kMfmaArgs& a) {
+    const int64_t xstride = 2 * K + 16;
+    int64_t off = mc * xstride;
+    a.xstride = int(xstride);
+    a.xs_lds = int(off);
+    off += int64_t(mc) * (K / 32) * 4;
+    a.zero_lds = int(off);
+    off += kQ4kZeroBytes;
+    a.red_lds = int(off);
+    off += int64_t(kQ4kMaxWaves) * kQ4kMaxRows * 16 * 4;
+    return off;
+}
+
+// LDS available to one workgroup on the current device (cached per device).
+int lds_limit() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 65536;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// Native Q4_K linear on MFMA: activation rows in chunks of at most
+// kQ4kMaxRows (fewer when their staged rows would not fit in LDS), weight rows
+// in chunks of < 2^31 payload bytes (32-bit buffer offsets).  False, launching
+// nothing, when even one activation row does not fit in LDS.
+bool launch_q4k_mfma(uint16_t* y, const uint16_t* x, const uint8_t* raw, int64_t M, int64_t N, int64_t K, bool big,
+                     hipStream_t st) {
+    Q4kMfmaArgs a{};
+    int mcap = kQ4kMaxRows;
+    while (mcap > 0 && q4k_mfma_layout(K, mcap, a) > lds_limit()) mcap--;
+    if (mcap == 0) return false;
+    const int64_t nsb = K / 256, row_bytes = nsb * 144;
+    int64_t rows_cap = ((int64_t(1) << 31) - 1) / row_bytes / 16 * 16;
+    if (rows_cap < 16) return false;
+    for (int64_t m0 = 0; m0 < M; m0 += mcap) {
+        const int mc = int(M - m0 < mcap ? M - m0 : mcap);
+        const int lds = int(q4k_mfma_layout(K, mc, a));
+        for (int64_t n0 = 0; n0 < N; n0 += rows_cap) {
+            const int64_t nc = N - n0 < rows_cap ? N - n0 : rows_cap;
+            a.y = y + m0 * N + n0;
+            a.x = x + m0 * K;
+            a.raw = raw + n0 * row_bytes;
+            a.M = mc, a.N = int(nc), a.K = int(K), a.ldy = int(N);
+            const bool wide = nsb >= 32;  // W = 8, D = 2; else W = 4, D = 4
+            const int W = wide ? 8 : 4;
+            a.sbw = int((nsb + W - 1) / W);
+            auto go = [&](auto kernel) {
+                // (a refusal surfaces as a launch error)
+                if (lds > 65536)
+                    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+                kernel<<<dim3(unsigned((nc + 15) / 16)), dim3(64 * W), size_t(lds), st>>>(a);
+            };
+            auto pick = [&](auto big_tag) {
+                constexpr bool B = decltype(big_tag)::value;
+                if (wide) {
+                    if (mc == 1) go(q4k_mfma_linear<B, 1, 8, 2>);
+                    else go(q4k_mfma_linear<B, 4, 8, 2>);
+                } else {
+                    if (mc == 1) go(q4k_mfma_linear<B, 1, 4, 4>);
+                    else go(q4k_mfma_linear<B, 4, 4, 4>);
+                }
+            };
+            if (big) pick(std::true_type{});
+            else pick(std::false_type{});
+        }
+    }
+    return true;
+}
 }  // namespace
 
 extern "C" int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t rows,
@@ -743,6 +1072,9 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool big = endian == EQ_ENDIAN_BIG;
+    if (ggml_type == EQ_GGML_Q4_K &&
+        launch_q4k_mfma(static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), raw, M, N, K, big, st))
+        return check_launch("gguf linear");
     // Q4_K: 32-code chunks per row -> teams per workgroup; Q8_0: a wave per row
     const int64_t nch = K / 32;
     const int teams = nch <= 64 ? 4 : nch <= 128 ? 2 : 1;

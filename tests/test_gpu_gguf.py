@@ -189,12 +189,14 @@ def swap_f16_headers(ty, raw):
     return b.reshape(-1)
 
 
-# (type, K): Q4_K with 64 and 128 16-byte chunks per row (4 and 2 teams per
-# workgroup; the Llama shapes below take 1); Q8_0 rows of 130 and 129 blocks, whose runs are not whole
-# 16-byte words (the 2-byte staging path; the Llama shapes below take the
-# 16-byte one).  N = 390 leaves a partial workgroup of rows; M = 11 takes two
-# launches (8 + 3).
-LINEAR_CASES = [(G.GgmlType.Q4K, 2048), (G.GgmlType.Q4K, 4096), (G.GgmlType.Q8_0, 4160), (G.GgmlType.Q8_0, 4128)]
+# (type, K): Q4_K rows of 5, 13 and 16 superblocks (the MFMA kernel's four
+# waves per tile take 2/2/1/0, 4/4/4/1 and 4 each, against a four-deep load
+# ring) and of 33 (eight waves: 5 each, the last one none, against a two-deep
+# ring); Q8_0 rows of 130 and 129 blocks, whose runs are not whole 16-byte
+# words (the 2-byte staging path; the Llama shapes below take the 16-byte one).
+# N = 390 leaves a partial tile of rows; M = 11 takes two launches (8 + 3).
+LINEAR_CASES = [(G.GgmlType.Q4K, 1280), (G.GgmlType.Q4K, 3328), (G.GgmlType.Q4K, 4096), (G.GgmlType.Q4K, 8448),
+                (G.GgmlType.Q8_0, 4160), (G.GgmlType.Q8_0, 4128)]
 
 
 @pytest.mark.parametrize("ty,K", LINEAR_CASES, ids=[f"{t.name}-K{k}" for t, k in LINEAR_CASES])
@@ -223,7 +225,8 @@ def test_native_linear(cuda, ty, K, M, endian):
 
 @pytest.mark.parametrize("ty", [G.GgmlType.Q4K, G.GgmlType.Q8_0])
 def test_native_linear_llama_shapes(cuda, ty):
-    """Decode shapes of a Llama-3-8B checkpoint: q (4096 x 4096), down (4096 x 14336; one team per workgroup)."""
+    """Decode shapes of a Llama-3-8B checkpoint: q (4096 x 4096), down (4096 x 14336; 7 superblocks per wave of
+    the Q4_K MFMA kernel's eight, three turns of its two-deep load ring and one more)."""
     vals, _ = ty.block_and_bytes()
     for N, K in [(4096, 4096), (4096, 14336)]:
         raw = synthetic_blocks(int(ty), N * K // vals, seed=N + K)
@@ -235,3 +238,21 @@ def test_native_linear_llama_shapes(cuda, ty):
         got = (host_bits16(y).astype(np.uint32) << 16).view(np.float32)
         ok, worst, _ = orc.matmul_within_tolerance(got, y_ref, out_is_bf16=True)
         assert ok, f"{N}x{K}: max|err|/RMS = {worst:.3e}"
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_native_q4k_linear_long_rows(cuda, M):
+    """Q4_K rows of 84480 values: one staged activation row (169 KB) exceeds a
+    workgroup's LDS, so the VALU kernel q4k_linear takes the product."""
+    ty, N, K = G.GgmlType.Q4K, 20, 256 * 330
+    print(f"[case] native linear long rows M={M} N={N} K={K}", flush=True)
+    vals, _ = ty.block_and_bytes()
+    raw = synthetic_blocks(int(ty), N * K // vals, seed=K + M)
+    xb = orc.f32_to_bf16_bits(np.random.default_rng(M).standard_normal((M, K)).astype(np.float32))
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    y = G.linear(x, desc_for(ty, N, K), dev_u8(raw))
+    W = orc.gguf_dequant_f32(int(ty), raw, int(G.DequantDefinition.Native)).reshape(N, K).astype(np.float64)
+    y_ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ W.T
+    got = (host_bits16(y).astype(np.uint32) << 16).view(np.float32)
+    ok, worst, _ = orc.matmul_within_tolerance(got, y_ref, out_is_bf16=True)
+    assert ok, f"max|err|/RMS = {worst:.3e}"
