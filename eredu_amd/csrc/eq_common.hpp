@@ -22,6 +22,9 @@ void clear_error();
 // Checks the launch status of the kernels just enqueued.
 int check_launch(const char* what);
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cu_count();
+
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // One matrix-vector problem of a (possibly grouped) decode launch:
@@ -98,6 +101,13 @@ constexpr uint32_t kOutOfRange = 0xC0000000u;
 // s_waitcnt vmcnt(0): every vector memory operation of this wave, stores
 // included, has completed.
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Workgroup barrier for LDS hand-offs that leaves global loads in flight:
+// this wave's LDS operations complete (lgkmcnt(0)), then s_barrier.
+// __syncthreads() also carries a workgroup-scope fence, which the compiler
+// implements by waiting for every outstanding memory operation (vmcnt(0)),
+// prefetches included.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Counts this workgroup at `counter` after all its threads' device-scope
 // stores have completed; true in the workgroup that arrives last of

@@ -1071,19 +1071,6 @@ static void launch_qmv_v(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     }
 }
 
-// Compute units of the current device (cached per device).
-static int device_cu_count() {
-    static std::atomic<int> cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int v = cache[dev].load(std::memory_order_relaxed);
-    if (v <= 0) {
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cache[dev].store(v, std::memory_order_relaxed);
-    }
-    return v;
-}
-
 // LDS available to one workgroup on the current device (cached per device).
 static int device_lds_bytes() {
     static std::atomic<int> cache[64];

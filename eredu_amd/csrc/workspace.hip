@@ -19,6 +19,7 @@
 // arrival counters that start at zero: one small zero-filled buffer per
 // (device, stream), separate from the workspace (whose contents other
 // kernels overwrite), which every such kernel leaves zeroed when it ends.
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -50,6 +51,18 @@ std::vector<void*>& retired_buffers() {
 }
 
 }  // namespace
+
+int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
 
 void* ws_acquire(const WsSource* src, size_t bytes, hipStream_t st) {
     if (bytes == 0) bytes = 256;

@@ -127,11 +127,13 @@ def test_transpose_false(cuda, M):
     run_case(M, 128, 192, 64, 4, transpose=False, seed=M)
 
 
-# transpose = false, bf16 x: M = 1 takes qmm_n_m1 (N = 64 / 128 / 384 / 4096:
-# 4, 4, 8, 16 lanes across the columns), M = 2..8 qmm_n_small (16 / 32 / 64
-# word columns per workgroup); K = 96 runs one K split, 1024 and 4096 several
-# (partial sums through the workspace); M = 9 takes the general kernel.
-@pytest.mark.parametrize("N,K", [(64, 96), (384, 1024), (4096, 4096), (128, 4096)])
+# transpose = false, bf16 x: M = 1 takes qmm_n_m1 (128-column tiles: N = 64
+# fills half of one, 384 three, 4096 thirty-two; K = 96 is two row runs of 64
+# and 32, the others 8 to 56 runs of 64 to 256 rows, added by the last
+# workgroup of each tile), M = 2..8 qmm_n_small (16 / 32 / 64 word columns per
+# workgroup; partial sums through the workspace); M = 9 takes the general
+# kernel.
+@pytest.mark.parametrize("N,K", [(64, 96), (384, 1024), (4096, 4096), (128, 4096), (1024, 14336)])
 @pytest.mark.parametrize("M", [1, 2, 5, 8, 9])
 def test_transpose_false_small_m(cuda, N, K, M):
     run_case(M, N, K, 64, 4, transpose=False, seed=N + K + M)
