@@ -365,6 +365,10 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
                             w, scales, biases, int(M), int(N), int(K), ws, st))
             return check_launch("quantized_matmul (qmm)");
     }
+    if (transpose && x_dtype == EQ_DTYPE_BF16 && M <= 16 &&
+        launch_qmv_any(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w,
+                       scales, biases, int(M), int(N), int(K), st))
+        return check_launch("quantized_matmul (qmv_any)");
     if (!transpose && x_dtype == EQ_DTYPE_BF16 && M <= 8) {
         const GatherIdx one{nullptr, nullptr, 1, 1};
         if (launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w,

@@ -45,6 +45,11 @@ struct QmvSpec {
 bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, hipStream_t st);
 bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st);
+// Decode for the other widths (qmv_any.hip): transpose, bf16 x, M <= 16, bits
+// 2..8, group 16 or a multiple of 32, K a multiple of 32; false, launching
+// nothing, when it does not take the problem.
+bool launch_qmv_any(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                    const void* s, const void* b, int M, int N, int K, hipStream_t st);
 
 // Activation prologue of a decode launch: kind 1 = silu(x) * second,
 // kind 2 = RMSNorm(x + second) * weight (second may be null), x + second

@@ -39,6 +39,29 @@ def test_matmul_widths(cuda, bits, gs, transpose, M):
     assert ok, worst
 
 
+# qmv_any (transpose, bf16 x, M <= 16): N = 4100 rows take the persistent
+# workgroups (4 rows each, at most 4 per CU) through a second pass; M = 7 and
+# 16 take launches of 4 activation rows; K = 14336 holds one activation row per
+# launch in LDS; f16 scales without biases on a subset.
+@pytest.mark.parametrize("bits,gs,sdt,biases", [(3, 64, orc.BF16, True), (5, 32, orc.F16, False),
+                                                (6, 16, orc.BF16, True), (2, 128, orc.F16, True),
+                                                (8, 256, orc.BF16, False), (4, 16, orc.BF16, True)])
+@pytest.mark.parametrize("M,N,K", [(1, 4100, 2048), (7, 4100, 2048), (16, 520, 2048), (3, 260, 14336)])
+def test_any_width_decode_shapes(cuda, bits, gs, sdt, biases, M, N, K):
+    print(f"[case] qmv_any bits={bits} gs={gs} M={M} N={N} K={K}", flush=True)
+    w, s, b = synthetic_linear(N, K, gs, bits, seed=bits * 13 + gs + M + N, scale_dtype=sdt)
+    if not biases:
+        b = None
+    xb = synthetic_x(M, K, seed=bits + gs + M)
+    y = quantized_matmul_with_mode(dev_bf16(xb), dev_words(w), dev_param(s, sdt),
+                                   dev_param(b, sdt) if b is not None else None, True, gs, bits)
+    torch.cuda.synchronize()
+    ref = orc.quantized_matmul_f64(xb, orc.BF16, w, s, b, sdt, True, gs, bits, N, K)
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(y), ref, out_is_bf16=True)
+    assert y.shape == (M, N)
+    assert ok, worst
+
+
 @pytest.mark.parametrize("bits,gs", WIDTHS)
 @pytest.mark.parametrize("sdt", [orc.BF16, orc.F16, orc.F32])
 def test_dequantize_widths_bit_exact(cuda, bits, gs, sdt):
