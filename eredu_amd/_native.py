@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-EQ_DTYPE_F32, EQ_DTYPE_F16, EQ_DTYPE_BF16 = 0, 1, 2
+EQ_DTYPE_F32, EQ_DTYPE_F16, EQ_DTYPE_BF16, EQ_DTYPE_U8 = 0, 1, 2, 3
 EQ_ENDIAN_LITTLE, EQ_ENDIAN_BIG = 0, 1
 EQ_DEQUANT_AFFINE, EQ_DEQUANT_NATIVE = 0, 1
 
@@ -23,6 +23,7 @@ SIGNATURES = {
     "eq_quantized_matmul": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _b, _i32, _i32, ctypes.c_char_p, _i32, _i32, _vp], _i32),
     "eq_dequantize": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, ctypes.c_char_p, _i32, _i32, _vp], _i32),
     "eq_gguf_convert_affine": ([_vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i32, _vp], _i32),
+    "eq_gguf_convert_mxfp4": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _i32),
     "eq_gguf_dequantize": ([_vp, _vp, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _vp], _i32),
     "eq_gguf_linear": ([_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i32, _i32, _vp], _i32),
     "eq_gather_qmm": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _b, _i32, _i32,

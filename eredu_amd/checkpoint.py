@@ -190,7 +190,8 @@ def quantize_tensor(weight: torch.Tensor, quantization: WeightQuantization
     """Packed uint32 codes, scales and biases of one floating-point weight of
     rank >= 2, grouped along its last axis (leading dimensions, an expert
     bank's included, kept; quantization.rs:169-224), on the GPU with
-    eq_quantize (affine; bits 2, 3, 4, 5, 6 or 8, group size 16 or a multiple of 32)."""
+    eq_quantize: affine (bits 2, 3, 4, 5, 6 or 8, group size 16 or a multiple
+    of 32) or MXFP4 (uint8 E8M0 scales, biases None; quantization.rs:226-233)."""
     quantization.validate()
     if weight.dim() < 2 or not weight.dtype.is_floating_point:
         raise EreduError(f"expected a floating-point weight with at least two dimensions, got shape "
@@ -198,12 +199,13 @@ def quantize_tensor(weight: torch.Tensor, quantization: WeightQuantization
     cols = weight.shape[-1]
     if cols % quantization.group_size != 0 or cols % 32 != 0:
         raise EreduError(f"input dimension {cols} must be divisible by group_size {quantization.group_size} and 32")
-    if quantization.mode != "affine":
-        raise EreduError("only affine quantization is implemented on the device path")
+    if quantization.mode not in ("affine", "mxfp4"):
+        raise EreduError("checkpoint-native GGML blocks cannot be produced by dense quantization")
+    mode = QuantizationMode.MxFp4 if quantization.mode == "mxfp4" else QuantizationMode.Affine
     dev = weight if weight.is_cuda else weight.cuda()
     if dev.dtype == torch.float64:
         raise EreduError("float64 weights are not supported (f32, f16 or bf16)")
-    wq, s, b = quantize_with_mode(dev, quantization.group_size, quantization.bits, QuantizationMode.Affine)
+    wq, s, b = quantize_with_mode(dev, quantization.group_size, quantization.bits, mode)
     return wq.view(torch.uint32), s, b
 
 
@@ -321,8 +323,8 @@ def load_quantized_checkpoint(model_dir: str, device: str = "cuda"
     """Loads an MLX-LM checkpoint onto the GPU: every ``p.weight`` with a
     ``p.scales`` sibling becomes ``QuantizedLinear`` (key ``p``; codes,
     scales, biases resident in HBM), every other tensor is returned as is.
-    The encoding comes from config.json; quantized tensors without affine
-    metadata are refused."""
+    The encoding (affine or MXFP4) comes from config.json; quantized tensors
+    without such metadata are refused."""
     from safetensors import safe_open
 
     quant = checkpoint_quantization_metadata(_config(model_dir))
@@ -338,8 +340,8 @@ def load_quantized_checkpoint(model_dir: str, device: str = "cuda"
         prefix = name[: -len(".scales")]
         if prefix + ".weight" not in tensors:
             raise EreduError(f"{name} has no {prefix}.weight")
-        if quant is None or quant.mode != "affine":
-            raise EreduError(f"{prefix} is quantized but config.json has no affine quantization metadata")
+        if quant is None or quant.mode not in ("affine", "mxfp4"):
+            raise EreduError(f"{prefix} is quantized but config.json has no affine or MXFP4 quantization metadata")
         w = tensors.pop(prefix + ".weight")
         s = tensors.pop(name)
         b = tensors.pop(prefix + ".biases", None)
@@ -349,8 +351,11 @@ def load_quantized_checkpoint(model_dir: str, device: str = "cuda"
         if tuple(s.shape) != (w.shape[0], K // quant.group_size) or (b is not None and b.shape != s.shape):
             raise EreduError(f"{prefix}: scales/biases {tuple(s.shape)} do not match weight {tuple(w.shape)} "
                              f"at group_size {quant.group_size}, bits {quant.bits}")
+        mode = QuantizationMode.MxFp4 if quant.mode == "mxfp4" else QuantizationMode.Affine
+        if mode is QuantizationMode.MxFp4 and (b is not None or s.dtype != torch.uint8):
+            raise EreduError(f"{prefix}: MXFP4 layers carry uint8 scales and no biases")
         bias = tensors.pop(prefix + ".bias", None)
         linears[prefix] = QuantizedLinear(w.view(torch.int32).to(device), s.to(device),
                                           None if b is None else b.to(device), quant.group_size, quant.bits,
-                                          None if bias is None else bias.to(device))
+                                          None if bias is None else bias.to(device), mode)
     return linears, tensors, quant

@@ -323,8 +323,11 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
                                  int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
                                  const char* mode, int x_dtype, int scale_dtype, const WsSource* ws,
                                  eq_stream_t stream) {
-    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
-    if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype)) {
+    QuantMode qm;
+    if (parse_mode(mode, qm)) return 1;
+    if (qm == kModeMxFp4 ? check_mxfp4(group_size, bits, scale_dtype, biases) : check_gs_bits(group_size, bits))
+        return 1;
+    if (!valid_dtype(x_dtype) || (qm == kModeAffine && !valid_dtype(scale_dtype))) {
         set_error("invalid dtype code");
         return 1;
     }
@@ -351,6 +354,10 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
         return 1;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (qm == kModeMxFp4) {
+        const GatherIdx one{nullptr, nullptr, 1, 1};
+        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), one, 1, M, N, K, transpose, x_dtype, st);
+    }
 
     const bool mfma_ok = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
                          (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && aligned(x, 16) &&
@@ -424,8 +431,13 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
                                            int group_size, int bits, const char* mode, int x_dtype, int scale_dtype,
                                            eq_stream_t stream) {
     clear_error();
-    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
-    if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype)) {
+    QuantMode qm;
+    if (parse_mode(mode, qm)) return 1;
+    if (qm == kModeMxFp4 ? (group_size != 32 || bits != 4) : check_gs_bits(group_size, bits) != 0) {
+        if (qm == kModeMxFp4) check_mxfp4(group_size, bits, scale_dtype, nullptr);
+        return 1;
+    }
+    if (!valid_dtype(x_dtype) || !(qm == kModeAffine ? valid_dtype(scale_dtype) : scale_dtype == EQ_DTYPE_U8)) {
         set_error("invalid dtype code");
         return 1;
     }
@@ -461,7 +473,7 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     // Decode-shaped groups go to one grouped launch per kQmvMaxProblems problems.
-    bool grouped = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
+    bool grouped = qm == kModeAffine && transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
                    (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && M <= 16;
     std::vector<QmvSpec> specs;
     for (int i = 0; i < count && grouped; i++) {
@@ -606,7 +618,28 @@ extern "C" int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* proble
 extern "C" int eq_quantize(uint32_t* w_out, void* scales, void* biases, const void* w, int64_t rows, int64_t cols,
                            int group_size, int bits, const char* mode, int dtype, eq_stream_t stream) {
     clear_error();
-    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    QuantMode qm;
+    if (parse_mode(mode, qm)) return 1;
+    if (qm == kModeMxFp4) {
+        // E2M1 codes and E8M0 scale bytes, no biases (the biases argument must be null)
+        if (check_mxfp4(group_size, bits, EQ_DTYPE_U8, biases)) return 1;
+        if (!valid_dtype(dtype)) {
+            set_error("invalid dtype code");
+            return 1;
+        }
+        if (rows < 0 || cols < 0 || cols % 32 != 0) {
+            set_error("cols must be a non-negative multiple of group_size");
+            return 1;
+        }
+        if (rows == 0 || cols == 0) return 0;
+        if (!w_out || !scales || !w) {
+            set_error("null pointer argument");
+            return 1;
+        }
+        return mxfp4_quantize(w_out, static_cast<uint8_t*>(scales), w, rows, cols, dtype,
+                              reinterpret_cast<hipStream_t>(stream));
+    }
+    if (check_gs_bits(group_size, bits)) return 1;
     if (!valid_dtype(dtype)) {
         set_error("invalid dtype code");
         return 1;
@@ -658,7 +691,27 @@ extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, c
                              int64_t cols, int group_size, int bits, const char* mode, int scale_dtype,
                              int out_dtype, eq_stream_t stream) {
     clear_error();
-    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    QuantMode qm;
+    if (parse_mode(mode, qm)) return 1;
+    if (qm == kModeMxFp4) {
+        if (check_mxfp4(group_size, bits, scale_dtype, biases)) return 1;
+        if (!valid_dtype(out_dtype)) {
+            set_error("invalid dtype code");
+            return 1;
+        }
+        if (rows < 0 || cols < 0 || cols % 32 != 0) {
+            set_error("cols must be a non-negative multiple of group_size");
+            return 1;
+        }
+        if (rows == 0 || cols == 0) return 0;
+        if (!out || !w || !scales) {
+            set_error("null pointer argument");
+            return 1;
+        }
+        return mxfp4_dequantize(out, w, static_cast<const uint8_t*>(scales), rows, cols, out_dtype,
+                                reinterpret_cast<hipStream_t>(stream));
+    }
+    if (check_gs_bits(group_size, bits)) return 1;
     if (!valid_dtype(scale_dtype) || !valid_dtype(out_dtype)) {
         set_error("invalid dtype code");
         return 1;

@@ -50,6 +50,9 @@ bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs,
 // nothing, when it does not take the problem.
 bool launch_qmv_any(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                     const void* s, const void* b, int M, int N, int K, hipStream_t st);
+// The same kernel for MXFP4 codes (E8M0 scale bytes, no biases).
+bool launch_qmv_any_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, int M, int N, int K,
+                          hipStream_t st);
 
 // Activation prologue of a decode launch: kind 1 = silu(x) * second,
 // kind 2 = RMSNorm(x + second) * weight (second may be null), x + second
@@ -225,16 +228,61 @@ inline bool with_bits(int bits, F&& f) {
 }
 
 inline bool valid_dtype(int d) { return d == EQ_DTYPE_F32 || d == EQ_DTYPE_F16 || d == EQ_DTYPE_BF16; }
+inline bool valid_scale_dtype(int d) { return valid_dtype(d) || d == EQ_DTYPE_U8; }
 
-inline int check_mode(const char* mode) {
-    if (mode == nullptr || std::strcmp(mode, "affine") == 0) return 0;
+enum QuantMode { kModeAffine = 0, kModeMxFp4 = 1 };
+
+// "affine" (or null) / "mxfp4"; anything else is an error.
+inline int parse_mode(const char* mode, QuantMode& out) {
+    if (mode == nullptr || std::strcmp(mode, "affine") == 0) {
+        out = kModeAffine;
+        return 0;
+    }
     if (std::strcmp(mode, "mxfp4") == 0) {
-        set_error("quantization mode 'mxfp4' is not implemented on this device path (affine only)");
-        return 1;
+        out = kModeMxFp4;
+        return 0;
     }
     set_error(std::string("invalid quantization mode '") + mode + "'");
     return 1;
 }
+
+// Entry points that take the affine encoding only.
+inline int check_mode(const char* mode) {
+    QuantMode m;
+    if (parse_mode(mode, m)) return 1;
+    if (m == kModeMxFp4) {
+        set_error("quantization mode 'mxfp4' is not supported by this entry point (affine only)");
+        return 1;
+    }
+    return 0;
+}
+
+// MXFP4's fixed geometry (safemlx/src/ops/quantization.rs:37-45): group size
+// 32, 4-bit codes, u8 scales, no biases.
+inline int check_mxfp4(int group_size, int bits, int scale_dtype, const void* biases) {
+    if (group_size != 32 || bits != 4) {
+        set_error("MXFP4 requires group_size=32 and bits=4, got group_size=" + std::to_string(group_size) +
+                  " bits=" + std::to_string(bits));
+        return 1;
+    }
+    if (scale_dtype != EQ_DTYPE_U8) {
+        set_error("MXFP4 scales are E8M0 bytes (EQ_DTYPE_U8)");
+        return 1;
+    }
+    if (biases != nullptr) {
+        set_error("MXFP4 has no biases");
+        return 1;
+    }
+    return 0;
+}
+
+// MXFP4 host entry points (mxfp4.hip); arguments validated by the callers
+// (geometry by check_mxfp4, pointers, shapes).
+int mxfp4_quantize(uint32_t* w_out, uint8_t* scales, const void* w, int64_t rows, int64_t cols, int dtype,
+                   hipStream_t st);
+int mxfp4_dequantize(void* out, const uint32_t* w, const uint8_t* scales, int64_t rows, int64_t cols, int out_dtype,
+                     hipStream_t st);
+
 
 // Group size / bits rules of the affine contract (eredu-checkpoint/src/lib.rs:103-122,
 // safemlx/src/ops/quantization.rs:62-64): bits 2, 3, 4, 5, 6 or 8; group size 16
@@ -320,6 +368,23 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
+// MXFP4 (safemlx QuantizationMode::MxFp4, safemlx/src/ops/quantization.rs:16-46;
+// the OCP microscaling FP4 format): E2M1 codes -- bit 3 sign, bits 2-1
+// exponent, bit 0 mantissa; magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6 -- packed 8
+// per u32 LSB-first like 4-bit affine codes, and one E8M0 scale byte per 32
+// values: 2^(e - 127), e = 255 is NaN.
+__device__ __forceinline__ float e2m1_to_f32(uint32_t c) {
+    const uint32_t m = c & 7u;
+    // m >= 2: 2^(m/2 - 1) * (1 + (m & 1) / 2) as f32 bits; m = 1: 0.5; m = 0: 0
+    uint32_t bits = ((126u + (m >> 1)) << 23) | ((m & 1u) << 22);
+    bits = m >= 2u ? bits : (m == 1u ? 0x3F000000u : 0u);
+    return __uint_as_float(bits | ((c & 8u) << 28));
+}
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+    e &= 0xffu;
+    return __uint_as_float(e == 255u ? 0x7FC00000u : (e == 0u ? 0x00400000u : e << 23));
+}
+
 // Two 4-bit codes n0, n1 as the bf16 pair (128 + n0, 128 + n1): 128 = 0x4300
 // has a unit ulp, so OR-ing n into the mantissa is exact.
 constexpr uint32_t kNibbleMagic = 0x43004300u;
@@ -341,6 +406,12 @@ struct GatherIdx {
     const int32_t* rhs;  // null: batch b reads w batch b (or 0 when w has one)
     int64_t x_batches, w_batches;
 };
+
+// MXFP4 matmul (mxfp4.hip): y[b] = x[lhs(b)] . dequant(w[rhs(b)])^T (or
+// without the transpose) for every output batch b of `batch`; the plain
+// matmul is batch 1 with no indices.  Validated by the callers.
+int mxfp4_matmul(void* y, const void* x, const uint32_t* w, const uint8_t* scales, const GatherIdx& g,
+                 int64_t batch, int64_t M, int64_t N, int64_t K, bool transpose, int x_dtype, hipStream_t st);
 
 // The operand batches of output batch b; false if an index is out of range.
 __device__ __forceinline__ bool gather_batch(const GatherIdx& g, int64_t b, int64_t& xb, int64_t& wb) {

@@ -218,8 +218,11 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
     // matmul rule for sorted indices (unsorted indices under the hint give
     // wrong rows, as in MLX, but every access stays in bounds).
     clear_error();
-    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
-    if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype)) {
+    QuantMode qm;
+    if (parse_mode(mode, qm)) return 1;
+    if (qm == kModeMxFp4 ? check_mxfp4(group_size, bits, scale_dtype, biases) : check_gs_bits(group_size, bits))
+        return 1;
+    if (!valid_dtype(x_dtype) || (qm == kModeAffine && !valid_dtype(scale_dtype))) {
         set_error("invalid dtype code");
         return 1;
     }
@@ -257,6 +260,8 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const GatherIdx g{lhs_indices, rhs_indices, x_batches, w_batches};
+    if (qm == kModeMxFp4)
+        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), g, batch, M, N, K, transpose, x_dtype, st);
 
     // many routes over sorted experts: one MFMA GEMM per expert's rows
     const bool grouped = transpose && M == 1 && sorted_indices && rhs_indices && x_dtype == EQ_DTYPE_BF16 &&

@@ -1014,6 +1014,59 @@ bool launch_q4k_mfma(uint16_t* y, const uint16_t* x, const uint8_t* raw, int64_t
 }
 }  // namespace
 
+namespace eq {
+namespace {
+// GGML type 39 (MXFP4) -> MLX MXFP4 (eredu-gguf/src/convert.rs:247-276): block
+// = 1 E8M0 byte + 16 code bytes, low nibbles values 0..15, high nibbles
+// 16..31; out: the scale byte and 4 words of 8 codes each, LSB-first.  One
+// thread per block (byte loads: 17-byte blocks are not aligned).
+__global__ __launch_bounds__(256) void mxfp4_from_ggml(uint32_t* __restrict__ w, uint8_t* __restrict__ s,
+                                                      const uint8_t* __restrict__ raw, int64_t nblocks) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint8_t* b = raw + i * 17;
+    s[i] = b[0];
+    uint32_t lo[2] = {0u, 0u}, hi[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t q = b[1 + j];
+        lo[j >> 3] |= (q & 15u) << (4 * (j & 7));
+        hi[j >> 3] |= (q >> 4) << (4 * (j & 7));
+    }
+    w[i * 4 + 0] = lo[0];
+    w[i * 4 + 1] = lo[1];
+    w[i * 4 + 2] = hi[0];
+    w[i * 4 + 3] = hi[1];
+}
+}  // namespace
+}  // namespace eq
+
+extern "C" int eq_gguf_convert_mxfp4(uint32_t* weights, uint8_t* scales, const uint8_t* raw, int64_t raw_len,
+                                     int64_t rows, int64_t cols, eq_stream_t stream) {
+    clear_error();
+    if (rows < 0 || cols < 0 || cols % 32 != 0) {
+        set_error("MXFP4 row width is not divisible by 32");
+        return 1;
+    }
+    const int64_t nblocks = rows * (cols / 32);
+    if (raw_len != nblocks * 17) {
+        set_error("payload length does not match descriptor");
+        return 1;
+    }
+    if (nblocks == 0) return 0;
+    if (!weights || !scales || !raw) {
+        set_error("null pointer argument");
+        return 1;
+    }
+    if ((nblocks + 255) / 256 > INT32_MAX) {
+        set_error("tensor too large");
+        return 1;
+    }
+    mxfp4_from_ggml<<<dim3(unsigned((nblocks + 255) / 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        weights, scales, raw, nblocks);
+    return check_launch("gguf convert (mxfp4)");
+}
+
 extern "C" int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t rows,
                                   int64_t cols, int endian, int definition, int out_dtype, eq_stream_t stream) {
     clear_error();

@@ -59,6 +59,34 @@ template <typename ST> __device__ __forceinline__ float any_param(uint32_t v);
 template <> __device__ __forceinline__ float any_param<BF16T>(uint32_t v) { return bf16_bits_to_f32(v & 0xffffu); }
 template <> __device__ __forceinline__ float any_param<F16T>(uint32_t v) { return f16_bits_to_f32(v & 0xffffu); }
 
+// MXFP4: 8 E2M1 codes of a word (nibble i = code i) as bf16 pairs (c0, c2),
+// (c4, c6), (c1, c3), (c5, c7): the magnitudes (3 bits) index byte tables of
+// the bf16 images with v_perm, the sign bit is OR-ed into the high byte.
+__device__ __forceinline__ void e2m1_pairs8(uint32_t w, uint32_t* p) {
+    const uint32_t TL0 = 0xC0800000u, TL1 = 0xC0804000u;  // low bytes of bf16(0, .5, 1, 1.5 | 2, 3, 4, 6)
+    const uint32_t TH0 = 0x3F3F3F00u, TH1 = 0x40404040u;  // high bytes
+    const uint32_t ie = w & 0x07070707u, io = (w >> 4) & 0x07070707u;  // magnitudes of even / odd nibbles
+    const uint32_t le = __builtin_amdgcn_perm(TL1, TL0, ie);
+    const uint32_t he = __builtin_amdgcn_perm(TH1, TH0, ie) | ((w << 4) & 0x80808080u);
+    const uint32_t lo = __builtin_amdgcn_perm(TL1, TL0, io);
+    const uint32_t ho = __builtin_amdgcn_perm(TH1, TH0, io) | (w & 0x80808080u);
+    p[0] = __builtin_amdgcn_perm(he, le, 0x05010400u);  // (c0, c2)
+    p[1] = __builtin_amdgcn_perm(he, le, 0x07030602u);  // (c4, c6)
+    p[2] = __builtin_amdgcn_perm(ho, lo, 0x05010400u);  // (c1, c3)
+    p[3] = __builtin_amdgcn_perm(ho, lo, 0x07030602u);  // (c5, c7)
+}
+
+// 8 activations [x0 .. x7] as the pairs (x0, x2), (x4, x6), (x1, x3), (x5, x7)
+// that meet e2m1_pairs8's code pairs.
+__device__ __forceinline__ qa_u32x4 mx_permute_x8(qa_u32x4 d) {
+    qa_u32x4 t;
+    t[0] = __builtin_amdgcn_perm(d[1], d[0], 0x05040100u);
+    t[1] = __builtin_amdgcn_perm(d[3], d[2], 0x05040100u);
+    t[2] = __builtin_amdgcn_perm(d[1], d[0], 0x07060302u);
+    t[3] = __builtin_amdgcn_perm(d[3], d[2], 0x07060302u);
+    return t;
+}
+
 // Loads the BITS words of segment `off` (byte offset) into wv.
 template <int BITS>
 __device__ __forceinline__ void load_segment(uint32_t* wv, __amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -84,9 +112,12 @@ __device__ __forceinline__ void load_segment(uint32_t* wv, __amdgpu_buffer_rsrc_
 }
 
 // GS16: group size 16 (two groups per segment); otherwise a segment lies in
-// one group (group size a multiple of 32).
-template <int BITS, typename ST, int MC, bool GS16>
+// one group (group size a multiple of 32).  MX: MXFP4 (BITS 4, group 32,
+// E8M0 scale bytes, no biases): codes decode to E2M1 bf16 pairs, activations
+// are staged in the pairs' order, y = sum over groups of 2^(e - 127) x . v.
+template <int BITS, typename ST, int MC, bool GS16, bool MX = false>
 __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArgs a) {
+    static_assert(!MX || (BITS == 4 && !GS16), "MXFP4 is 4-bit, group 32");
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -109,7 +140,7 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
             for (int i = 0; i < 4; i++) sum += bf16_bits_to_f32(v[i] & 0xffffu) + bf16_bits_to_f32(v[i] >> 16);
             sum += __shfl_xor(sum, 1);
             if (live) {
-                *reinterpret_cast<qa_u32x4*>(smem + m * K * 2 + any_chunk_slot(q) * 16) = v;
+                *reinterpret_cast<qa_u32x4*>(smem + m * K * 2 + any_chunk_slot(q) * 16) = MX ? mx_permute_x8(v) : v;
                 if ((q & 1) == 0) xs16[m * (K / 16) + (q >> 1)] = sum;
             }
         }
@@ -118,7 +149,7 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
 
     const uint32_t row_bytes = uint32_t(K) * BITS / 8;
     const __amdgpu_buffer_rsrc_t wr = raw_rsrc(a.w, uint32_t(N) * row_bytes);
-    const __amdgpu_buffer_rsrc_t sr = raw_rsrc(a.s, uint32_t(N) * uint32_t(G) * 2u);
+    const __amdgpu_buffer_rsrc_t sr = raw_rsrc(a.s, uint32_t(N) * uint32_t(G) * (MX ? 1u : 2u));
     const __amdgpu_buffer_rsrc_t br = raw_rsrc(a.b ? a.b : a.s, a.b ? uint32_t(N) * uint32_t(G) * 2u : 0u);
     constexpr uint32_t kMagic = 0x43004300u;  // bf16 (128, 128)
 
@@ -131,8 +162,10 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
             uint32_t wv[BITS];
             load_segment<BITS>(wv, wr, uint32_t(n) * row_bytes + uint32_t(j) * (4u * BITS));
             // parameters of the segment's group(s)
-            float s0, b0, s1 = 0.f, b1 = 0.f;
-            if constexpr (GS16) {
+            float s0, b0 = 0.f, s1 = 0.f, b1 = 0.f;
+            if constexpr (MX) {
+                s0 = e8m0_to_f32(__builtin_amdgcn_raw_buffer_load_b8(sr, uint32_t(n) * uint32_t(G) + uint32_t(j), 0, 0));
+            } else if constexpr (GS16) {
                 const uint32_t po = (uint32_t(n) * uint32_t(G) + 2u * uint32_t(j)) * 2u;
                 const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b32(sr, po, 0, 0);
                 const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b32(br, po, 0, 0);
@@ -145,7 +178,10 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
             }
             // code pairs as bf16 (128 + q0, 128 + q1)
             uint32_t pk[16];
-            if constexpr (BITS < 8) {
+            if constexpr (MX) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) e2m1_pairs8(wv[r], pk + 4 * r);
+            } else if constexpr (BITS < 8) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) pk[i] = seg_code<BITS>(wv, 2 * i) | (seg_code<BITS>(wv, 2 * i + 1) << 16) | kMagic;
             }
@@ -161,7 +197,13 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
                 }
                 const float xa = xs16[m * (K / 16) + 2 * j], xb = xs16[m * (K / 16) + 2 * j + 1];
                 float t0 = 0.f, t1 = 0.f;  // sum x q over values 0..15 and 16..31 of the segment
-                if constexpr (BITS < 8) {
+                if constexpr (MX) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        t0 = dot2_bf16(xw[i], pk[i], t0);
+                        t1 = dot2_bf16(xw[8 + i], pk[8 + i], t1);
+                    }
+                } else if constexpr (BITS < 8) {
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
                         t0 = dot2_bf16(xw[i], pk[i], t0);
@@ -178,7 +220,9 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
                         t = fmaf(bf16_bits_to_f32(xw[i] >> 16), float(q1), t);
                     }
                 }
-                if constexpr (GS16) {
+                if constexpr (MX) {
+                    acc[m] = fmaf(s0, t0 + t1, acc[m]);
+                } else if constexpr (GS16) {
                     acc[m] += fmaf(s0, t0, b0 * xa) + fmaf(s1, t1, b1 * xb);
                 } else {
                     acc[m] += fmaf(s0, t0 + t1, b0 * (xa + xb));
@@ -243,6 +287,25 @@ bool launch_qmv_any(int bits, int gs, int scale_dtype, uint16_t* y, const uint16
         case 6: with_st(std::integral_constant<int, 6>{}); break;
         default: with_st(std::integral_constant<int, 8>{}); break;
         }
+    }
+    return true;
+}
+
+bool launch_qmv_any_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, int M, int N, int K,
+                          hipStream_t st) {
+    if (M < 1 || M > 16 || K % 32 != 0 || !aligned(x, 16) || !aligned(w, 4)) return false;
+    if (int64_t(N) * K / 2 >= (int64_t(1) << 31) || int64_t(kAnyMaxM) * K * 2 >= (int64_t(1) << 31)) return false;
+    const int mc_max = any_lds_bytes(kAnyMaxM, K) <= 65536 ? kAnyMaxM : (any_lds_bytes(1, K) <= 65536 ? 1 : 0);
+    if (mc_max == 0) return false;
+    const int64_t rows_wg = kAnyWaves;
+    const int64_t grid = (N + rows_wg - 1) / rows_wg < int64_t(device_cu_count()) * 4 ? (N + rows_wg - 1) / rows_wg
+                                                                                      : int64_t(device_cu_count()) * 4;
+    for (int m0 = 0; m0 < M; m0 += mc_max) {
+        const int mc = M - m0 < mc_max ? M - m0 : mc_max;
+        QmvAnyArgs a{y + int64_t(m0) * N, x + int64_t(m0) * K, w, s, nullptr, mc, N, K, 32, mc * K * 2};
+        const size_t lds = size_t(any_lds_bytes(mc, K));
+        if (mc == 1) qmv_any_kernel<4, BF16T, 1, false, true><<<dim3(unsigned(grid)), dim3(64 * kAnyWaves), lds, st>>>(a);
+        else qmv_any_kernel<4, BF16T, kAnyMaxM, false, true><<<dim3(unsigned(grid)), dim3(64 * kAnyWaves), lds, st>>>(a);
     }
     return true;
 }

@@ -335,6 +335,56 @@ class NativeTensor:
 
 
 @dataclasses.dataclass
+class MxFp4Tensor:
+    """convert.rs:73-79: E2M1 codes packed 8 per u32 (LSB first) and one E8M0
+    scale byte per 32 values, both on the GPU (int32 / uint8 tensors)."""
+
+    weight_shape: List[int]
+    scale_shape: List[int]
+    weights: torch.Tensor
+    scales: torch.Tensor
+
+    def dequantize(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """2^(e - 127) * e2m1(code) per value, written as ``dtype``."""
+        from .quantization import QuantizationMode, dequantize_with_mode
+
+        rows = self.scales.numel() // self.scale_shape[-1] if self.scale_shape else 1
+        out = dequantize_with_mode(self.weights.view(rows, -1), self.scales.view(rows, -1), None, 32, 4,
+                                   QuantizationMode.MxFp4, dtype=dtype)
+        return out.view(*self.weight_shape[:-1], -1)
+
+
+def convert_mxfp4(desc: TensorDescriptor, raw: torch.Tensor) -> MxFp4Tensor:
+    """Type-39 blocks -> MLX MXFP4 pair, byte-identical to the reference's
+    mxfp4 conversion (convert.rs:197-212 shapes, 247-276 packing); either byte
+    order (single bytes only).  C ABI eq_gguf_convert_mxfp4."""
+    if int(desc.ggml_type) != int(GgmlType.MXFP4):
+        raise EreduError(f"tensor '{desc.name}': not an MXFP4 tensor")
+    _check_raw(desc, raw)
+    shape = desc.mlx_shape()
+    if not shape:
+        raise EreduError(f"tensor '{desc.name}': MXFP4 scalar is invalid")
+    cols = shape[-1]
+    if cols % 32 != 0:
+        raise EreduError(f"tensor '{desc.name}': MXFP4 row width is not divisible by 32")
+    rows = 1
+    for d in shape[:-1]:
+        rows *= d
+    dev = raw.device
+    weights = torch.empty((rows, cols // 8), dtype=torch.int32, device=dev)
+    scales = torch.empty((rows, cols // 32), dtype=torch.uint8, device=dev)
+    check(
+        _native.lib().eq_gguf_convert_mxfp4(
+            weights.data_ptr(), scales.data_ptr(), raw.contiguous().data_ptr(), raw.numel(), rows, cols,
+            torch.cuda.current_stream().cuda_stream,
+        )
+    )
+    weight_shape = shape[:-1] + [cols // 8]
+    scale_shape = shape[:-1] + [cols // 32]
+    return MxFp4Tensor(weight_shape, scale_shape, weights.view(*weight_shape), scales.view(*scale_shape))
+
+
+@dataclasses.dataclass
 class DenseTensor:
     """A dense GGUF tensor (convert.rs:19-24) on the device, in its MLX shape."""
 
@@ -345,9 +395,9 @@ class DenseTensor:
 def convert(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little):
     """eredu_gguf's convert (convert.rs:276-313) on device payloads, routed by
     ``conversion_kind``: a DenseTensor (dense types), a NativeTensor (blocks
-    kept as stored: little-endian Q4_K / Q8_0), or an AffineTensor (Q4_0 in
-    either byte order, big-endian Q4_K / Q8_0).  Encodings without device
-    kernels, and MXFP4, are refused with the type named."""
+    kept as stored: little-endian Q4_K / Q8_0), an MxFp4Tensor (type 39), or
+    an AffineTensor (Q4_0 in either byte order, big-endian Q4_K / Q8_0).
+    Encodings without device kernels are refused with the type named."""
     if raw.dtype != torch.uint8 or not raw.is_cuda:
         raise EreduError("raw GGUF payload must be a uint8 tensor on the GPU")
     if raw.numel() != desc.byte_len:
@@ -369,5 +419,5 @@ def convert(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.L
             raise EreduError(f"tensor '{desc.name}': row width is not divisible by block length {values}")
         return NativeTensor(desc.name, shape, ty, Endian(endian), raw)
     if kind.kind == "mxfp4":
-        raise EreduError(f"tensor '{desc.name}': MXFP4 blocks are not converted on the device")
+        return convert_mxfp4(desc, raw)
     return convert_affine(desc, raw, endian)

@@ -67,6 +67,21 @@ def _require_device(*tensors: Optional[torch.Tensor]) -> None:
             raise EreduError("all arrays must live on the GPU (the library has no host path)")
 
 
+def _scale_code(scales: torch.Tensor, mode: "QuantizationMode") -> int:
+    """Affine scales are float32/float16/bfloat16; MXFP4 scales are E8M0
+    bytes (uint8, quantized.rs:240-244)."""
+    if mode is QuantizationMode.MxFp4:
+        if scales.dtype != torch.uint8:
+            raise EreduError(f"MXFP4 scales must be uint8 E8M0 bytes, got {scales.dtype}")
+        return _native.EQ_DTYPE_U8
+    return _dtype_code(scales, "scales")
+
+
+def _check_biases(biases: Optional[torch.Tensor], mode: "QuantizationMode") -> None:
+    if mode is QuantizationMode.MxFp4 and biases is not None:
+        raise EreduError("MXFP4 has no biases")
+
+
 def _words(w: torch.Tensor) -> torch.Tensor:
     if w.dtype not in _WORD_DTYPES:
         raise EreduError(f"quantized weights must be packed u32 words, got {w.dtype}")
@@ -96,8 +111,7 @@ def quantized_matmul_with_mode(
     rule), computed by eq_gather_qmm with the broadcast batch indices.
     """
     mode.validate(group_size, bits)
-    if mode is not QuantizationMode.Affine:
-        raise EreduError("only affine quantization is implemented on the device path")
+    _check_biases(biases, mode)
     if w.dim() > 2:
         if x.dim() < 2:
             raise EreduError("with batched weights, x must be at least [M, K]")
@@ -109,7 +123,7 @@ def quantized_matmul_with_mode(
         return gather_qmm_with_mode(x, w, scales, biases, None, None, transpose, group_size, bits, False, mode)
     N, K = _check_operands(x, w, scales, biases, transpose, group_size, bits)
     x_code = _dtype_code(x, "x")
-    s_code = _dtype_code(scales, "scales")
+    s_code = _scale_code(scales, mode)
     x2 = x.reshape(-1, K).contiguous()
     M = x2.shape[0]
     w = w.contiguous()
@@ -182,16 +196,15 @@ def quantized_matmul_batched(
     (C ABI: eq_quantized_matmul_batched), from as few kernel launches as the
     device path allows."""
     mode.validate(group_size, bits)
-    if mode is not QuantizationMode.Affine:
-        raise EreduError("only affine quantization is implemented on the device path")
     if not problems:
         return []
     x0, _, s0, _ = problems[0]
-    x_code, s_code = _dtype_code(x0, "x"), _dtype_code(s0, "scales")
+    x_code, s_code = _dtype_code(x0, "x"), _scale_code(s0, mode)
     keep, outs = [], []
     arr = (_native.QmmProblem * len(problems))()
     M = None
     for i, (x, w, scales, biases) in enumerate(problems):
+        _check_biases(biases, mode)
         N, K = _check_operands(x, w, scales, biases, transpose, group_size, bits)
         if x.dtype != x0.dtype or scales.dtype != s0.dtype:
             raise EreduError("all problems of a batch must share the activation and scale dtypes")
@@ -244,8 +257,7 @@ def gather_qmm_with_mode(
     expert (results equal within the matmul rule).
     """
     mode.validate(group_size, bits)
-    if mode is not QuantizationMode.Affine:
-        raise EreduError("only affine quantization is implemented on the device path")
+    _check_biases(biases, mode)
     _require_device(x, w, scales, biases, lhs_indices, rhs_indices)
     _words(w)
     if x.dim() < 2 or w.dim() < 2 or scales.dim() != w.dim():
@@ -288,7 +300,7 @@ def gather_qmm_with_mode(
         _native.lib().eq_gather_qmm(
             y.data_ptr(), x3.data_ptr(), w2.data_ptr(), s2.data_ptr(), b2.data_ptr() if b2 is not None else None,
             lhs.data_ptr(), rhs.data_ptr(), batch, x_batches, w_batches, M, N, K, bool(transpose),
-            int(group_size), int(bits), mode.value.encode(), _dtype_code(x, "x"), _dtype_code(scales, "scales"),
+            int(group_size), int(bits), mode.value.encode(), _dtype_code(x, "x"), _scale_code(scales, mode),
             bool(sorted_indices), _stream(),
         )
     )
@@ -318,14 +330,13 @@ def quantize_with_mode(
     group_size: int,
     bits: int,
     mode: QuantizationMode = QuantizationMode.Affine,
-) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """(codes u32-as-int32 [rows, cols * bits / 32], scales, biases) of the
-    affine quantization of w [..., cols] along its last axis, scales and
-    biases in w's dtype (safemlx/src/ops/quantization.rs:100-159; C ABI:
-    eq_quantize)."""
+    quantization of w [..., cols] along its last axis
+    (safemlx/src/ops/quantization.rs:119-159; C ABI: eq_quantize).  Affine:
+    scales and biases in w's dtype.  MXFP4: E2M1 codes, uint8 E8M0 scales
+    and no biases (None), as QuantizedArrays.biases is for that mode."""
     mode.validate(group_size, bits)
-    if mode is not QuantizationMode.Affine:
-        raise EreduError("only affine quantization is implemented on the device path")
     _require_device(w)
     cols = w.shape[-1]
     if cols % group_size != 0:
@@ -333,14 +344,17 @@ def quantize_with_mode(
     w2 = w.reshape(-1, cols).contiguous()
     rows = w2.shape[0]
     wq = torch.empty((rows, cols * bits // 32), dtype=torch.int32, device=w.device)
-    scales = torch.empty((rows, cols // group_size), dtype=w.dtype, device=w.device)
-    biases = torch.empty_like(scales)
+    mx = mode is QuantizationMode.MxFp4
+    scales = torch.empty((rows, cols // group_size), dtype=torch.uint8 if mx else w.dtype, device=w.device)
+    biases = None if mx else torch.empty_like(scales)
     check(
-        _native.lib().eq_quantize(wq.data_ptr(), scales.data_ptr(), biases.data_ptr(), w2.data_ptr(), rows, cols,
-                                  int(group_size), int(bits), mode.value.encode(), _dtype_code(w2, "w"), _stream())
+        _native.lib().eq_quantize(wq.data_ptr(), scales.data_ptr(), biases.data_ptr() if biases is not None else None,
+                                  w2.data_ptr(), rows, cols, int(group_size), int(bits), mode.value.encode(),
+                                  _dtype_code(w2, "w"), _stream())
     )
     lead = tuple(w.shape[:-1])
-    return (wq.reshape(*lead, -1), scales.reshape(*lead, -1), biases.reshape(*lead, -1))
+    return (wq.reshape(*lead, -1), scales.reshape(*lead, -1),
+            biases.reshape(*lead, -1) if biases is not None else None)
 
 
 def quantize(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS):
@@ -358,10 +372,11 @@ def dequantize_with_mode(
     dtype: Optional[torch.dtype] = None,
 ) -> torch.Tensor:
     """w_hat = scales * q + biases in the scales' dtype unless ``dtype`` is given
-    (safemlx/src/ops/quantization.rs:256-289; C ABI: eq_dequantize)."""
+    (safemlx/src/ops/quantization.rs:256-289; C ABI: eq_dequantize).  MXFP4:
+    w_hat = 2^(e - 127) * e2m1(q), no biases; the scales being bytes, the
+    default output is bfloat16 (MLX's default for its floating-point modes)."""
     mode.validate(group_size, bits)
-    if mode is not QuantizationMode.Affine:
-        raise EreduError("only affine quantization is implemented on the device path")
+    _check_biases(biases, mode)
     _require_device(w, scales, biases)
     w = _words(w).contiguous()
     if w.dim() != 2:
@@ -372,15 +387,17 @@ def dequantize_with_mode(
         raise EreduError(f"scales has shape {tuple(scales.shape)}, expected {(rows, cols // group_size)}")
     if biases is not None and (tuple(biases.shape) != tuple(scales.shape) or biases.dtype != scales.dtype):
         raise EreduError("biases must match scales in shape and dtype")
-    out_dtype = dtype or scales.dtype
+    s_code = _scale_code(scales, mode)
+    out_dtype = dtype or (torch.bfloat16 if mode is QuantizationMode.MxFp4 else scales.dtype)
+    if out_dtype not in _DTYPE_CODE:
+        raise EreduError(f"output dtype must be float32, float16 or bfloat16, got {out_dtype}")
     out = torch.empty((rows, cols), dtype=out_dtype, device=w.device)
     scales = scales.contiguous()
     biases = biases.contiguous() if biases is not None else None
     check(
         _native.lib().eq_dequantize(
             out.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr() if biases is not None else None,
-            rows, cols, int(group_size), int(bits), mode.value.encode(), _dtype_code(scales, "scales"),
-            _DTYPE_CODE[out_dtype], _stream(),
+            rows, cols, int(group_size), int(bits), mode.value.encode(), s_code, _DTYPE_CODE[out_dtype], _stream(),
         )
     )
     return out

@@ -28,7 +28,7 @@ extern "C" {
 typedef struct ihipStream_t* eq_stream_t;
 
 /* Element types of activations, scales/biases and dense outputs. */
-enum eq_dtype { EQ_DTYPE_F32 = 0, EQ_DTYPE_F16 = 1, EQ_DTYPE_BF16 = 2 };
+enum eq_dtype { EQ_DTYPE_F32 = 0, EQ_DTYPE_F16 = 1, EQ_DTYPE_BF16 = 2, EQ_DTYPE_U8 = 3 /* MXFP4 scales */ };
 
 /* GGML block types handled on the device (codes of eredu-gguf/src/format.rs:297-330). */
 enum eq_ggml_type { EQ_GGML_Q4_0 = 2, EQ_GGML_Q8_0 = 8, EQ_GGML_Q4_K = 12 };
@@ -122,6 +122,17 @@ int eq_dequantize(void* out, const uint32_t* w, const void* scales, const void* 
 int eq_gguf_convert_affine(uint32_t* weights, uint16_t* scales, uint16_t* biases,
                            const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t rows,
                            int64_t cols, int endian, eq_stream_t stream);
+
+/*
+ * GGML type 39 (MXFP4) blocks of a [rows, cols] tensor -> MLX's MXFP4 pair:
+ * weights [rows, cols / 8] u32 (E2M1 codes, 8 per word LSB-first) and scales
+ * [rows, cols / 32] E8M0 bytes.  A block is the scale byte and 16 code bytes
+ * (low nibbles values 0..15, high nibbles 16..31); no value changes.
+ * Replaces the MXFP4 branch of eredu_gguf::convert (eredu-gguf/src/convert.rs:
+ * 241, 247-276).  cols must be a multiple of 32, raw_len = rows * cols / 32 * 17.
+ */
+int eq_gguf_convert_mxfp4(uint32_t* weights, uint8_t* scales, const uint8_t* raw, int64_t raw_len, int64_t rows,
+                          int64_t cols, eq_stream_t stream);
 
 /*
  * GGML blocks -> dense [rows, cols] of out_dtype (EQ_DTYPE_BF16 or EQ_DTYPE_F32),

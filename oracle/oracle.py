@@ -245,6 +245,93 @@ def quantize_affine(wf32: np.ndarray, group_size: int, bits: int, scale_dtype: i
     return wq, s, b
 
 
+# ------------------------------------------------------------------ MXFP4
+
+# E2M1 magnitudes of codes 0..7 (OCP Microscaling Formats v1.0, sec. 5.3.3:
+# 1 sign, 2 exponent bits with bias 1, 1 mantissa bit, exponent 0 subnormal);
+# code bit 3 is the sign.  Pinned in tests/test_oracle_mxfp4.py by decoding
+# the bit fields.
+E2M1_MAGNITUDES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def e2m1_decode(codes: np.ndarray) -> np.ndarray:
+    c = np.asarray(codes, dtype=np.uint32)
+    return np.where(c & 8, -1.0, 1.0) * E2M1_MAGNITUDES[c & 7]
+
+
+def e8m0_decode(e: np.ndarray) -> np.ndarray:
+    """2^(e - 127); 255 is NaN (OCP MX v1.0 sec. 5.4).  Pinned by the
+    reference's decode test (eredu/src/backend/mlx/nn/fp8.rs:1670-1678:
+    127, 128, 126 -> 1, 2, 0.5) and np.ldexp."""
+    e = np.asarray(e, dtype=np.int64)
+    out = np.ldexp(1.0, e - 127)
+    return np.where(e == 255, np.nan, out)
+
+
+def mxfp4_convert_ggml(raw: np.ndarray, rows: int, cols: int):
+    """GGML type-39 blocks -> (u32 weights [rows, cols/8], u8 scales [rows,
+    cols/32]) as eredu-gguf/src/convert.rs:247-276: each 17-byte block is the
+    scale byte and 16 code bytes, low nibbles values 0..15, high nibbles
+    16..31, packed 8 codes per word LSB-first.  Pinned by the golden vector of
+    eredu-gguf/tests/mxfp4.rs:5-60."""
+    blocks = np.asarray(raw, dtype=np.uint8).reshape(-1, 17)
+    assert blocks.shape[0] == rows * (cols // 32)
+    q = blocks[:, 1:].astype(np.uint32)
+    values = np.concatenate([q & 15, q >> 4], axis=1)  # [blocks, 32]
+    words = (values.reshape(-1, 4, 8) << (np.arange(8, dtype=np.uint32) * 4)).sum(axis=2).astype(np.uint32)
+    return words.reshape(rows, cols // 8), blocks[:, 0].reshape(rows, cols // 32).copy()
+
+
+def mxfp4_dequant_f64(w, scales, rows, cols) -> np.ndarray:
+    """2^(e - 127) * e2m1(q) per value (exact in f64 and in f32 for e >= 1)."""
+    q = unpack_codes(np.asarray(w).reshape(rows, -1), cols, 4).reshape(rows, cols // 32, 32)
+    s = e8m0_decode(np.asarray(scales).reshape(rows, cols // 32))
+    return (e2m1_decode(q) * s[:, :, None]).reshape(rows, cols)
+
+
+def mxfp4_quantize(wf32: np.ndarray):
+    """(u32 codes, u8 scales) of w [rows, cols] in groups of 32 along the last
+    axis, by the OCP MX v1.0 rule (sec. 6.3) with the exponent chosen so that
+    nothing saturates: the scale is the smallest power of two 2^e, e in
+    [-127, 127], with amax / 2^e <= 6; every value is w / 2^e rounded to the
+    nearest E2M1 value, ties to the even code, sign bit set for w < 0; a
+    group with a NaN or an infinity gets scale byte 255 (NaN) and magnitude
+    codes 0, an all-zero group byte 0.  Found by
+    search over exponents and over the 8 magnitudes (no closed form is
+    shared with the device code).  MLX's own mxfp4 quantizer is not in this
+    image: parity of this rule with MLX is unpinned."""
+    w = np.ascontiguousarray(wf32, dtype=np.float32).astype(np.float64)
+    rows, cols = w.shape
+    g = w.reshape(rows, cols // 32, 32)
+    amax = np.abs(g).max(axis=2)
+    bad = ~np.isfinite(g).all(axis=2)
+    exps = np.arange(-127, 128)
+    fits = amax[:, :, None] <= 6.0 * np.ldexp(1.0, exps)[None, None, :]
+    e = exps[np.argmax(fits, axis=2)]  # the first (smallest) exponent that fits
+    e = np.where(amax > 0, e, -127)
+    sbyte = np.where(bad, 255, e + 127).astype(np.uint8)
+    a = np.abs(np.where(bad[:, :, None], 0.0, g)) / np.ldexp(1.0, e)[:, :, None]
+    dist = np.abs(a[..., None] - E2M1_MAGNITUDES)  # [rows, groups, 32, 8]
+    best = dist.min(axis=3, keepdims=True)
+    cand = dist == best
+    # ties: the even code (codes 0..7 alternate even/odd mantissa bits)
+    even = cand & (np.arange(8) % 2 == 0)
+    m = np.where(even.any(axis=3), np.argmax(even, axis=3), np.argmax(cand, axis=3)).astype(np.uint32)
+    # the sign bit follows w < 0 (so small negatives become -0, NaN and -0.0 stay +)
+    codes = (m | np.where(g < 0, 8, 0).astype(np.uint32)).reshape(rows, cols)
+    words = (codes.reshape(rows, -1, 8) << (np.arange(8, dtype=np.uint32) * 4)).sum(axis=2).astype(np.uint32)
+    return words, sbyte
+
+
+def mxfp4_matmul_f64(x, x_dtype, w, scales, transpose, N, K):
+    """fp64 closed form of the MXFP4 quantized_matmul
+    (safemlx/src/ops/quantization.rs:190-226, mode "mxfp4")."""
+    x64 = scalar_to_f64(np.asarray(x), x_dtype).reshape(-1, K)
+    if transpose:
+        return x64 @ mxfp4_dequant_f64(w, scales, N, K).T
+    return x64 @ mxfp4_dequant_f64(w, scales, K, N)
+
+
 # ------------------------------------------------------------------ parity rule
 
 def bf16_half_ulp(y: np.ndarray) -> np.ndarray:

@@ -27,7 +27,7 @@ def test_header_declares_the_boundary():
         ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
          "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
-         "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc"]
+         "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc", "eq_gguf_convert_mxfp4"]
     )
 
 
@@ -69,7 +69,8 @@ def call_qmm(**kw):
         (dict(bits=5, gs=16, transpose=False, N=16), "does not fill whole 32-bit words"),
         (dict(K=96), "not divisible by group_size"),
         (dict(transpose=False, N=40), "not divisible by group_size"),
-        (dict(mode=b"mxfp4"), "mxfp4"),
+        (dict(mode=b"mxfp4"), "MXFP4 requires group_size=32 and bits=4"),
+        (dict(mode=b"mxfp4", gs=32, sd=2), "E8M0 bytes"),
         (dict(mode=b"nf4"), "invalid quantization mode"),
         (dict(xd=7), "invalid dtype"),
         (dict(N=0), "invalid shape"),
@@ -125,6 +126,15 @@ def test_gguf_convert_rejects(args, needle):
     rc = L.eq_gguf_convert_affine(ptr, ptr, ptr, ptr, a["raw_len"], a["ty"], a["rows"], a["cols"], a["endian"], None)
     assert rc != 0
     assert needle in L.eq_last_error().decode()
+
+
+def test_gguf_convert_mxfp4_rejects():
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    _rejects(L.eq_gguf_convert_mxfp4(p, p, p, 17, 1, 48, None), "not divisible by 32")
+    _rejects(L.eq_gguf_convert_mxfp4(p, p, p, 18, 1, 32, None), "payload length")
+    _rejects(L.eq_gguf_convert_mxfp4(None, p, p, 17, 1, 32, None), "null")
+    assert L.eq_gguf_convert_mxfp4(None, None, None, 0, 0, 32, None) == 0  # nothing to convert
 
 
 def test_gguf_dequant_rejects_bad_definition_and_dtype():
@@ -220,7 +230,8 @@ def test_gather_qmm_rejects_bad_arguments():
     _rejects(call(gs=48), "group_size")
     _rejects(call(bits=7), "bits")
     _rejects(call(bits=3, gs=16, K=16), "whole 32-bit words")
-    _rejects(call(mode=b"mxfp4"), "mxfp4")
+    _rejects(call(mode=b"mxfp4"), "MXFP4 requires group_size=32 and bits=4")
+    _rejects(call(mode=b"mxfp4", gs=32, sd=3, b=16), "no biases")
     _rejects(call(xd=7), "dtype")
     _rejects(call(K=96), "divisible")
     _rejects(call(wb=0), "w_batches")

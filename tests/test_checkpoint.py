@@ -114,5 +114,13 @@ def test_loader_refuses_quantized_tensors_without_metadata(tmp_path):
 
     save_file({"p.weight": torch.zeros(4, 8, dtype=torch.int32), "p.scales": torch.zeros(4, 1)},
               str(tmp_path / "model.safetensors"))
-    with pytest.raises(EreduError, match="no affine quantization metadata"):
+    with pytest.raises(EreduError, match="no affine or MXFP4 quantization metadata"):
         C.load_quantized_checkpoint(str(tmp_path))
+
+
+def test_gguf_blocks_cannot_be_produced_by_dense_quantization():
+    """quantization.rs:226-233: GgufIQuant has no dense quantizer (raised before any device work)."""
+    import torch
+
+    with pytest.raises(EreduError, match="cannot be produced by dense quantization"):
+        C.quantize_tensor(torch.ones(2, 256), C.WeightQuantization.GgufIQuant(12))

@@ -63,14 +63,34 @@ def test_rank_three_expert_bank(cuda):
     assert tuple(wq.shape) == (3, 8, 8) and tuple(s.shape) == (3, 8, 2) and tuple(b.shape) == (3, 8, 2)
 
 
-def test_device_path_refuses_mxfp4_and_cleans_up(cuda, tmp_path):
-    src = tmp_path / "source"
+def test_mxfp4_checkpoint_round_trip(cuda, tmp_path):
+    """An MXFP4 checkpoint: weight + uint8 scales, no biases, both metadata
+    keys; loaded layers run the MXFP4 matmul (quantization.rs:226-233)."""
+    from eredu_amd import QuantizationMode, quantized_matmul_with_mode
+
+    src, out = tmp_path / "source", tmp_path / "out"
     src.mkdir()
-    save_file({"m.proj.weight": torch.ones(2, 64)}, str(src / "model.safetensors"))
-    opts = C.CheckpointQuantizationOptions(quantization=C.WeightQuantization(32, 4, "mxfp4"))
-    with pytest.raises(EreduError, match="affine"):
-        C.quantize_checkpoint(str(src), str(tmp_path / "out"), opts)
-    assert not (tmp_path / "out").exists()
+    g = torch.Generator().manual_seed(4)
+    dense = {"m.proj.weight": (0.05 * torch.randn(256, 512, generator=g)).to(torch.bfloat16),
+             "m.norm.weight": torch.ones(512, dtype=torch.bfloat16)}
+    save_file(dense, str(src / "model.safetensors"))
+    mx = C.WeightQuantization(32, 4, "mxfp4")
+    C.quantize_checkpoint(str(src), str(out), C.CheckpointQuantizationOptions(quantization=mx))
+    saved = load_file(str(out / "model.safetensors"))
+    assert sorted(saved) == ["m.norm.weight", "m.proj.scales", "m.proj.weight"]
+    assert saved["m.proj.scales"].dtype == torch.uint8 and tuple(saved["m.proj.scales"].shape) == (256, 16)
+    with open(out / "config.json") as f:
+        assert json.load(f)["quantization"] == {"group_size": 32, "bits": 4, "mode": "mxfp4"}
+    linears, rest, quant = C.load_quantized_checkpoint(str(out))
+    assert quant == mx and list(rest) == ["m.norm.weight"]
+    lin = linears["m.proj"]
+    assert lin.mode is QuantizationMode.MxFp4 and lin.biases is None
+    x = torch.randn(3, 512, generator=g).to(torch.bfloat16).cuda()
+    wq, s, b = C.quantize_tensor(dense["m.proj.weight"], mx)
+    assert b is None
+    y2 = quantized_matmul_with_mode(x, wq.view(torch.int32), s, None, True, 32, 4, QuantizationMode.MxFp4)
+    assert torch.equal(lin(x).view(torch.int16), y2.view(torch.int16))
+
 
 
 @pytest.mark.parametrize("bits,gs", [(4, 64), (8, 32)])

@@ -153,7 +153,7 @@ def test_mirror_rejects_bad_arguments(cuda):
         gather_qmm(xd, W, S, B, None, torch.zeros(2).cuda())
     with pytest.raises(EreduError, match="batch dimensions"):
         gather_qmm(xd, W, S[:1], B)
-    with pytest.raises(EreduError, match="affine"):
+    with pytest.raises(EreduError, match="no biases"):
         gather_qmm_with_mode(xd, W, S, B, None, None, True, 32, 4, False, mode=_mxfp4())
 
 
