@@ -356,7 +356,8 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (qm == kModeMxFp4) {
         const GatherIdx one{nullptr, nullptr, 1, 1};
-        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), one, 1, M, N, K, transpose, x_dtype, st);
+        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), one, 1, M, N, K, transpose, x_dtype, false, ws,
+                            st);
     }
 
     const bool mfma_ok = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
@@ -382,6 +383,10 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
                                scales, biases, one, 1, int(M), int(N), int(K), group_size, ws, st))
             return check_launch("quantized_matmul (qmm_n)");
     }
+    if (!transpose && x_dtype == EQ_DTYPE_BF16 && M > 8 && M <= kQmmNRowsMax &&
+        launch_qmm_n_rows(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales,
+                          biases, M, int(N), int(K), group_size, ws, st))
+        return check_launch("quantized_matmul (qmm_n rows)");
 
     bool launched = false;
     with_bits(bits, [&](auto bc) {

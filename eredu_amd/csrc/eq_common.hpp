@@ -201,6 +201,8 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
 struct BF16T { typedef uint16_t storage; };
 struct F16T { typedef uint16_t storage; };
 struct F32T { typedef float storage; };
+// MXFP4 scales: E8M0 bytes (load_param gives 2^(e - 127)).
+struct E8M0T { typedef uint8_t storage; };
 
 // --------------------------------------------------------------- dispatch
 
@@ -384,6 +386,20 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
     e &= 0xffu;
     return __uint_as_float(e == 255u ? 0x7FC00000u : (e == 0u ? 0x00400000u : e << 23));
 }
+template <> __device__ __forceinline__ float load_param<E8M0T>(const uint8_t* p, int64_t i) { return e8m0_to_f32(p[i]); }
+
+// The 8 E2M1 codes of a word (LSB-first) times `scale`, as 4 bf16 pairs in
+// code order (c0, c1), (c2, c3), ...: v_cvt_scalef32_pk_bf16_fp4, which reads
+// only the exponent field of `scale` (2^(field - 127), field 255 giving NaN).
+// With scale = e8m0_to_f32(e) that is 2^(e - 127) for every byte e, byte 0's
+// subnormal image included; the products are exact in bf16 (two significant
+// bits) down to its subnormals.
+__device__ __forceinline__ void e2m1x8_to_bf16(uint32_t w, float scale, uint32_t* p) {
+    p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
+    p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
+    p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
+    p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
+}
 
 // Two 4-bit codes n0, n1 as the bf16 pair (128 + n0, 128 + n1): 128 = 0x4300
 // has a unit ulp, so OR-ing n into the mantissa is exact.
@@ -409,9 +425,13 @@ struct GatherIdx {
 
 // MXFP4 matmul (mxfp4.hip): y[b] = x[lhs(b)] . dequant(w[rhs(b)])^T (or
 // without the transpose) for every output batch b of `batch`; the plain
-// matmul is batch 1 with no indices.  Validated by the callers.
+// matmul is batch 1 with no indices.  sorted: ascending rhs indices promised
+// (gather_qmm's hint).  Split-K scratch from `ws` (null: the library
+// workspace).  Validated by the callers.
+struct WsSource;
 int mxfp4_matmul(void* y, const void* x, const uint32_t* w, const uint8_t* scales, const GatherIdx& g,
-                 int64_t batch, int64_t M, int64_t N, int64_t K, bool transpose, int x_dtype, hipStream_t st);
+                 int64_t batch, int64_t M, int64_t N, int64_t K, bool transpose, int x_dtype, bool sorted,
+                 const WsSource* ws, hipStream_t st);
 
 // The operand batches of output batch b; false if an index is out of range.
 __device__ __forceinline__ bool gather_batch(const GatherIdx& g, int64_t b, int64_t& xb, int64_t& wb) {
@@ -465,13 +485,33 @@ bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const ui
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st);
 
+// The same two launchers for MXFP4 codes (E8M0 scale bytes, no biases).
+bool launch_qmm_mfma_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, int M, int N, int K,
+                           const WsSource* ws, hipStream_t st);
+bool launch_qmm_grouped_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s,
+                              const int32_t* lhs, const int32_t* rhs, int batch, int64_t x_batches, int experts, int N,
+                              int K, hipStream_t st);
+
+// Routed-expert decode for MXFP4 (gather.hip's per-route kernel): transpose,
+// M = 1, bf16 x, 16-byte aligned x and w; batches b0 .. b0 + nb of g.
+void launch_gather_qmv_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, const GatherIdx& g,
+                             int64_t b0, unsigned nb, int N, int K, hipStream_t st);
+
 // x . W for W [K, N] packed along N (transpose = false), M <= 8 activation
-// rows per batch, bf16 x and y, bf16/f16 scales, 4- or 8-bit codes; batches
-// through g (y [batch, M, N]).  False (nothing launched) for other
-// combinations.
+// rows per batch, bf16 x and y, bf16/f16 scales, 4- or 8-bit codes, or MXFP4
+// (scale_dtype EQ_DTYPE_U8, bits 4, gs 32, b null); batches through g (y
+// [batch, M, N]).  False (nothing launched) for other combinations.
 bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
                         const void* b, const GatherIdx& g, int64_t batch, int M, int N, int K, int gs,
                         const WsSource* ws, hipStream_t st);
+
+// The same for one product of any M (batch 1, no indices): launches of 8
+// activation rows per batch (the rows as M / 8 batches over one weight
+// matrix), then the remaining rows.  Each launch reads W once, so the codes
+// are read ceil(M / 8) times: for the small M of transpose = false callers.
+constexpr int64_t kQmmNRowsMax = int64_t(1) << 20;
+bool launch_qmm_n_rows(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
+                       const void* b, int64_t M, int N, int K, int gs, const WsSource* ws, hipStream_t st);
 
 // ------------------------------------------------------------ general bodies
 

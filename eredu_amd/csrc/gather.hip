@@ -82,6 +82,8 @@ __device__ __forceinline__ void unpack4_pairs(uint32_t w, uint32_t* p) {
 // grid (ceil(N / (4 T)), batches of this launch); 256 lanes.  Chunk c of a
 // row = 16 bytes of codes = CPC codes inside one group (CPC <= GS).  Per
 // row and chunk: scale * sum(x q) + bias * sum(x), sum(x) shared by the rows.
+// MXFP4 (ST = E8M0T): the chunk is one group of 32 E2M1 codes, decoded to
+// bf16 with the scale folded in (e2m1x8_to_bf16), no bias.
 template <int BITS, int GS, typename ST, int T>
 __global__ __launch_bounds__(256) void gather_qmv(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
                                                   const uint32_t* __restrict__ w,
@@ -119,7 +121,27 @@ __global__ __launch_bounds__(256) void gather_qmv(uint16_t* __restrict__ y, cons
                 bi[r] = br ? load_param<ST>(br, int64_t(n) * G + grp) : 0.f;
             }
             const uint4* xa = reinterpret_cast<const uint4*>(xr + int64_t(c) * CPC);
-            if constexpr (BITS == 4) {
+            if constexpr (__is_same(ST, E8M0T)) {
+                uint32_t xw[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint4 v = xa[i];
+                    xw[4 * i] = v.x, xw[4 * i + 1] = v.y, xw[4 * i + 2] = v.z, xw[4 * i + 3] = v.w;
+                }
+#pragma unroll
+                for (int r = 0; r < kGqRows; r++) {
+                    const uint32_t qw[4] = {qv[r].x, qv[r].y, qv[r].z, qv[r].w};
+                    float e = 0.f;  // sum x 2^(s - 127) e2m1(q)
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        uint32_t p[4];
+                        e2m1x8_to_bf16(qw[t], sc[r], p);
+#pragma unroll
+                        for (int j = 0; j < 4; j++) e = dot2_bf16(xw[4 * t + j], p[j], e);
+                    }
+                    acc[r] += e;
+                }
+            } else if constexpr (BITS == 4) {
                 uint32_t xw[16];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -202,8 +224,13 @@ void launch_gather_qmv_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t
     else launch_gather_qmv<BITS, 128, ST>(y, x, w, s, bz, g, b0, nb, N, K, st);
 }
 
-
 }  // namespace
+
+void launch_gather_qmv_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, const GatherIdx& g,
+                             int64_t b0, unsigned nb, int N, int K, hipStream_t st) {
+    launch_gather_qmv<4, 32, E8M0T>(y, x, w, s, nullptr, g, b0, nb, N, K, st);
+}
+
 }  // namespace eq
 
 using namespace eq;
@@ -261,7 +288,8 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const GatherIdx g{lhs_indices, rhs_indices, x_batches, w_batches};
     if (qm == kModeMxFp4)
-        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), g, batch, M, N, K, transpose, x_dtype, st);
+        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), g, batch, M, N, K, transpose, x_dtype,
+                            sorted_indices, nullptr, st);
 
     // many routes over sorted experts: one MFMA GEMM per expert's rows
     const bool grouped = transpose && M == 1 && sorted_indices && rhs_indices && x_dtype == EQ_DTYPE_BF16 &&

@@ -207,13 +207,44 @@ int mxfp4_dequantize(void* out, const uint32_t* w, const uint8_t* scales, int64_
 }
 
 int mxfp4_matmul(void* y, const void* x, const uint32_t* w, const uint8_t* scales, const GatherIdx& g,
-                 int64_t batch, int64_t M, int64_t N, int64_t K, bool transpose, int x_dtype, hipStream_t st) {
+                 int64_t batch, int64_t M, int64_t N, int64_t K, bool transpose, int x_dtype, bool sorted,
+                 const WsSource* ws, hipStream_t st) {
     if (M == 0 || batch == 0) return 0;
+    uint16_t* yb = static_cast<uint16_t*>(y);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    const bool plain = batch == 1 && g.lhs == nullptr && g.rhs == nullptr;
+    const bool bf16_t = transpose && x_dtype == EQ_DTYPE_BF16;
+    const bool mfma_ok = bf16_t && aligned(x, 16) && aligned(w, 16);
+    // prefill (and M > 4, where the decode kernel's passes of 4 rows, each
+    // reading W again, cost more than one MFMA tile of 128 rows): the MFMA qmm
+    if (mfma_ok && plain && M > 4 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8) &&
+        launch_qmm_mfma_mxfp4(yb, xb, w, scales, int(M), int(N), int(K), ws, st))
+        return check_launch("quantized_matmul (mxfp4 qmm)");
     // the decode shape: the any-width decode kernel with E2M1 codes
-    if (transpose && batch == 1 && g.lhs == nullptr && g.rhs == nullptr && x_dtype == EQ_DTYPE_BF16 && M <= 16 &&
-        launch_qmv_any_mxfp4(static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales, int(M), int(N),
-                             int(K), st))
+    if (bf16_t && plain && M <= 16 && launch_qmv_any_mxfp4(yb, xb, w, scales, int(M), int(N), int(K), st))
         return check_launch("quantized_matmul (mxfp4 decode)");
+    // many routes over sorted experts: one MFMA GEMM per expert's rows
+    if (mfma_ok && M == 1 && sorted && g.rhs && batch >= 64 && batch >= 2 * g.w_batches && batch <= INT32_MAX &&
+        g.w_batches <= INT32_MAX && N % 128 == 0 && K % 64 == 0 && aligned(y, 8) &&
+        int64_t(N) * K / 2 < (int64_t(1) << 31) && batch * K * 2 < (int64_t(1) << 31) &&
+        launch_qmm_grouped_mxfp4(yb, xb, w, scales, g.lhs, g.rhs, int(batch), g.x_batches, int(g.w_batches), int(N),
+                                 int(K), st))
+        return check_launch("gather_qmm (mxfp4 grouped qmm)");
+    // transpose = false, few rows: the split-K VALU kernel of the affine path
+    if (!transpose && x_dtype == EQ_DTYPE_BF16 && M <= 8 &&
+        launch_qmm_n_small(4, EQ_DTYPE_U8, yb, xb, w, scales, nullptr, g, batch, int(M), int(N), int(K), 32, ws, st))
+        return check_launch("quantized_matmul (mxfp4 qmm_n)");
+    if (!transpose && x_dtype == EQ_DTYPE_BF16 && plain && M > 8 && M <= kQmmNRowsMax &&
+        launch_qmm_n_rows(4, EQ_DTYPE_U8, yb, xb, w, scales, nullptr, M, int(N), int(K), 32, ws, st))
+        return check_launch("quantized_matmul (mxfp4 qmm_n rows)");
+    // routed-expert decode: one activation row per route
+    if (mfma_ok && M == 1) {
+        for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
+            const unsigned nb = unsigned(batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY);
+            launch_gather_qmv_mxfp4(yb, xb, w, scales, g, b0, nb, int(N), int(K), st);
+        }
+        return check_launch("gather_qmm (mxfp4 qmv)");
+    }
     if ((N + kMxRows - 1) / kMxRows > INT32_MAX || (N / 8) * M / 256 >= INT32_MAX) {
         set_error("dimension too large for the MXFP4 kernels");
         return 1;

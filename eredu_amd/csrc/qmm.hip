@@ -41,6 +41,9 @@
 //    not depend on timing) and rounds once to bf16.
 //  * Tiles are assigned so that the workgroups one XCD receives cover few
 //    row blocks of x (which then stay in that XCD's L2).
+//  * MXFP4 (scale type E8M0T: group 32, E8M0 scale bytes, no biases): the
+//    same tiles and pipeline; each lane's 32 codes become B operands through
+//    v_cvt_scalef32_pk_bf16_fp4 with the group's scale folded in (exact).
 #include <mutex>
 
 #include "eq_common.hpp"
@@ -157,6 +160,9 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // the compiler's LDS alias scopes tell the buffers apart and a read of one
     // does not wait for the loads still landing in another.
     __shared__ __attribute__((aligned(16))) char abuf0[2 * kLdsBuf], abuf1[2 * kLdsBuf], abuf2[2 * kLdsBuf];
+    constexpr bool MX = __is_same(ST, E8M0T);
+    constexpr uint32_t PB = MX ? 1u : 2u;  // bytes per scale / bias
+    static_assert(!MX || (BITS == 4 && GS == 32 && !PW), "MXFP4: 4-bit codes, group 32");
     const int N = args.N, K = args.K, G = K / GS;
     int M = args.M;
 
@@ -171,8 +177,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const int n0 = tn * kBN;
     const uint16_t* xp = args.x;
     const uint32_t* wp = args.w;
-    const uint16_t* sp = args.s;
-    const uint16_t* bp = args.b;
+    const char* sp = reinterpret_cast<const char*>(args.s);
+    const char* bp = reinterpret_cast<const char*>(args.b);
     uint16_t* yp = args.y;
     if (args.groups) {
         const int4 gd = args.groups[tm];
@@ -182,8 +188,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         M = gd.z;
         m0 = gd.w;
         wp += int64_t(gd.x) * N * (K * BITS / 32);
-        sp += int64_t(gd.x) * N * G;
-        if (bp) bp += int64_t(gd.x) * N * G;
+        sp += int64_t(gd.x) * N * G * PB;
+        if (bp) bp += int64_t(gd.x) * N * G * PB;
     }
     const int nchunks = K / kBK;
     const int c_begin = split * args.cps, c_end = min(nchunks, c_begin + args.cps);
@@ -200,8 +206,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const __amdgpu_buffer_rsrc_t xr = raw_rsrc(xp, uint32_t(M) * uint32_t(K) * 2u);
     const uint32_t row_bytes = uint32_t(K) * BITS / 8u;  // (the launcher keeps N * row_bytes below 2^31)
     const __amdgpu_buffer_rsrc_t wr = raw_rsrc(wp, uint32_t(N) * row_bytes);
-    const __amdgpu_buffer_rsrc_t sr = raw_rsrc(sp, uint32_t(N) * uint32_t(G) * 2u);
-    const __amdgpu_buffer_rsrc_t br = raw_rsrc(bp ? bp : sp, bp ? uint32_t(N) * uint32_t(G) * 2u : 0u);
+    const __amdgpu_buffer_rsrc_t sr = raw_rsrc(sp, uint32_t(N) * uint32_t(G) * PB);
+    const __amdgpu_buffer_rsrc_t br = raw_rsrc(bp ? bp : sp, bp ? uint32_t(N) * uint32_t(G) * PB : 0u);
 
     // Lane offsets (chunk 0); rows past M and columns past N read zero.
     // Activations go straight from memory to LDS: load i of wave w fills the
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         const uint32_t n = uint32_t(n0 + 64 * wave + 32 * j + l32);
         woff[j] = int(n) < N ? n * row_bytes + uint32_t(32 * kb) * BITS / 8u : kOutOfRange;
         // (windows: the row's parameters from the split's first group on)
-        soff[j] = int(n) < N ? (n * uint32_t(G)) * 2u + (PW ? uint32_t(c_begin) * 2u : uint32_t((32 * kb) / GS) * 2u)
+        soff[j] = int(n) < N ? (n * uint32_t(G)) * PB + (PW ? uint32_t(c_begin) * 2u : uint32_t((32 * kb) / GS) * PB)
                              : kOutOfRange;
     }
     // (a lane's 32 codes lie in one group: group sizes are multiples of 32 and
@@ -248,12 +254,15 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     auto load_b = [&](Slot& S, int i) __attribute__((always_inline)) {
         const int k0 = chunk_k0(i);
         const uint32_t kw = __builtin_amdgcn_readfirstlane(uint32_t(k0) * BITS / 8u);
-        const uint32_t kp = __builtin_amdgcn_readfirstlane(uint32_t(k0 / GS) * 2u);
+        const uint32_t kp = __builtin_amdgcn_readfirstlane(uint32_t(k0 / GS) * PB);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
 #pragma unroll
             for (int q = 0; q < NW; q++) S.w[j][q] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j] + 16 * q, kw, 0);
-            if constexpr (!PW) {
+            if constexpr (MX) {
+                S.s[j] = __builtin_amdgcn_raw_buffer_load_b8(sr, soff[j], kp, 0);
+                S.b[j] = 0u;
+            } else if constexpr (!PW) {
                 S.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], kp, 0);
                 S.b[j] = __builtin_amdgcn_raw_buffer_load_b16(br, soff[j], kp, 0);
             }
@@ -274,9 +283,11 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // Before a barrier: this wave's activation loads for the next step have
     // landed (only the newest step's loads, codes then activations, may still
     // be in flight; memory operations complete in order).  With windows, a
-    // step that also requested a window has 4 more loads in flight.
+    // step that also requested a window has 4 more loads in flight.  (Per
+    // step: 2 NW code loads, 4 parameter loads -- 2 for MXFP4, none with
+    // windows -- and 4 activation loads.)
     auto wait_a = [&](bool window_step) __attribute__((always_inline)) {
-        constexpr int n = 2 * NW + (PW ? 0 : 4) + 4;
+        constexpr int n = 2 * NW + (MX ? 2 : PW ? 0 : 4) + 4;
         if (PW && window_step) wait_vmcnt<n + 4>();
         else wait_vmcnt<n>();
     };
@@ -300,11 +311,21 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         q_u32x4 bq[2][4];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const float s = qmm_param<ST>(sbits[j]);
-            const float b = qmm_param<ST>(bbits[j]);
+            if constexpr (MX) {
+                const float s = e8m0_to_f32(sbits[j]);
 #pragma unroll
-            for (int t = 0; t < 4; t++)
-                bq[j][t] = dequant8<BITS>(reinterpret_cast<const uint32_t*>(&S.w[j][0]) + t * BITS / 4, s, b);
+                for (int t = 0; t < 4; t++) {
+                    uint32_t p[4];
+                    e2m1x8_to_bf16(S.w[j][0][t], s, p);
+                    bq[j][t] = q_u32x4{p[0], p[1], p[2], p[3]};
+                }
+            } else {
+                const float s = qmm_param<ST>(sbits[j]);
+                const float b = qmm_param<ST>(bbits[j]);
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    bq[j][t] = dequant8<BITS>(reinterpret_cast<const uint32_t*>(&S.w[j][0]) + t * BITS / 4, s, b);
+            }
         }
         const char* base = buf + gofs;
 #pragma unroll
@@ -527,8 +548,9 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
         const int mc = int(M - m0 < m_piece ? M - m0 : m_piece);
         for (int64_t n0 = 0; n0 < N; n0 += n_piece) {
             const int nc = int(N - n0 < n_piece ? N - n0 : n_piece);
-            const uint16_t* sp = static_cast<const uint16_t*>(s) + n0 * G;
-            const uint16_t* bp = b ? static_cast<const uint16_t*>(b) + n0 * G : nullptr;
+            constexpr int64_t PB = __is_same(ST, E8M0T) ? 1 : 2;
+            const char* sp = static_cast<const char*>(s) + n0 * G * PB;
+            const char* bp = b ? static_cast<const char*>(b) + n0 * G * PB : nullptr;
             launch_qmm_piece<BITS, GS, ST>(y + m0 * N + n0, N, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp, mc, nc,
                                            K, whole, src, st);
         }
@@ -672,6 +694,18 @@ bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const ui
             return launch_qmm_grouped_gs<8, F16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
     }
     return false;
+}
+
+bool launch_qmm_mfma_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, int M, int N, int K,
+                           const WsSource* ws, hipStream_t st) {
+    launch_qmm_t<4, 32, E8M0T>(y, x, w, s, nullptr, M, N, K, ws, st);
+    return true;
+}
+
+bool launch_qmm_grouped_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s,
+                              const int32_t* lhs, const int32_t* rhs, int batch, int64_t x_batches, int experts, int N,
+                              int K, hipStream_t st) {
+    return launch_qmm_grouped_t<4, 32, E8M0T>(y, x, w, s, nullptr, lhs, rhs, batch, x_batches, experts, N, K, st);
 }
 
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,

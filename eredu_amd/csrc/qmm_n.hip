@@ -27,6 +27,8 @@ template <> __device__ __forceinline__ float param_bits<F32T>(uint32_t v) { retu
 // KP, ... of its K split [kb, ke) (blockIdx.y); consecutive lanes read
 // consecutive words of a row.  The phases are summed through LDS; with more
 // than one split the sums go to ws[split][batch][M][N] for qmm_n_finish.
+// MXFP4 (ST = E8M0T, no biases): the codes convert to their E2M1 values
+// (v_cvt_scalef32_pk_f32_fp4 at scale 1) and x s carries 2^(e - 127).
 template <int BITS, typename ST, bool MANY, int TW>
 __global__ __launch_bounds__(256) void qmm_n_small(uint16_t* __restrict__ y, float* __restrict__ ws,
                                                    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
@@ -61,7 +63,14 @@ __global__ __launch_bounds__(256) void qmm_n_small(uint16_t* __restrict__ y, flo
             const float sc = load_param<ST>(sr, int64_t(k) * G);
             const float bi = br ? load_param<ST>(br, int64_t(k) * G) : 0.f;
             float q[CPW];
-            if constexpr (BITS == 4) {
+            if constexpr (__is_same(ST, E8M0T)) {
+                const auto v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 0);
+                const auto v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 1);
+                const auto v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2);
+                const auto v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 3);
+                q[0] = v0[0], q[1] = v0[1], q[2] = v1[0], q[3] = v1[1];
+                q[4] = v2[0], q[5] = v2[1], q[6] = v3[0], q[7] = v3[1];
+            } else if constexpr (BITS == 4) {
                 const uint32_t lo = word & 0x0f0f0f0fu, hi = (word >> 4) & 0x0f0f0f0fu;  // codes 0,2,4,6 / 1,3,5,7
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -704,10 +713,13 @@ bool launch_qmm_n_m1(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, 
 bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
                         const void* b, const GatherIdx& g, int64_t batch, int M, int N, int K, int gs,
                         const WsSource* src, hipStream_t st) {
-    if ((bits != 4 && bits != 8) || (scale_dtype != EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F16) || M < 1 ||
-        M > 8 || batch < 1 || gs < 32)
+    if ((bits != 4 && bits != 8) ||
+        (scale_dtype != EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F16 && scale_dtype != EQ_DTYPE_U8) || M < 1 ||
+        M > 8 || batch < 1 || gs < 32 || (scale_dtype == EQ_DTYPE_U8 && (bits != 4 || gs != 32 || b)))
         return false;
-    if (M == 1 && launch_qmm_n_m1(bits, scale_dtype, y, x, w, s, b, g, batch, N, K, gs, src, st)) return true;
+    if (M == 1 && scale_dtype != EQ_DTYPE_U8 &&
+        launch_qmm_n_m1(bits, scale_dtype, y, x, w, s, b, g, batch, N, K, gs, src, st))
+        return true;
     const int64_t mn = batch * M * int64_t(N);
     int tl = 0, kp = 0, splits = 1, kchunk = K;
     int64_t tiles = 0;
@@ -738,7 +750,9 @@ bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* 
         }
     }
 #define EQ_N_DISPATCH(BITS, ST) launch_n_bits<BITS, ST>(y, ws, x, w, s, b, g, batch, M, N, K, gs, splits, kchunk, tl, st)
-    if (bits == 4) {
+    if (scale_dtype == EQ_DTYPE_U8) {
+        EQ_N_DISPATCH(4, E8M0T);
+    } else if (bits == 4) {
         if (scale_dtype == EQ_DTYPE_BF16) EQ_N_DISPATCH(4, BF16T);
         else EQ_N_DISPATCH(4, F16T);
     } else {
@@ -748,6 +762,24 @@ bool launch_qmm_n_small(int bits, int scale_dtype, uint16_t* y, const uint16_t* 
 #undef EQ_N_DISPATCH
     if (splits > 1)
         qmm_n_finish<<<dim3(unsigned((mn * 8 + 255) / 256)), dim3(256), 0, st>>>(y, ws, mn, splits);
+    return true;
+}
+
+bool launch_qmm_n_rows(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
+                       const void* b, int64_t M, int N, int K, int gs, const WsSource* src, hipStream_t st) {
+    if (M < 1) return false;
+    const int64_t full = M / 8, rest = M % 8;
+    if (full > 0) {
+        // the rows as `full` batches of 8 over one weight matrix
+        const GatherIdx g{nullptr, nullptr, full, 1};
+        if (!launch_qmm_n_small(bits, scale_dtype, y, x, w, s, b, g, full, 8, N, K, gs, src, st)) return false;
+    }
+    if (rest > 0) {
+        const GatherIdx g{nullptr, nullptr, 1, 1};
+        if (!launch_qmm_n_small(bits, scale_dtype, y + full * 8 * N, x + full * 8 * K, w, s, b, g, 1, int(rest), N, K,
+                                gs, src, st))
+            return false;
+    }
     return true;
 }
 

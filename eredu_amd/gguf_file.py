@@ -343,6 +343,7 @@ def stream_convert(path: str, names: Optional[Sequence[str]] = None, staging_byt
     * dense F32 / F16 / BF16 (and the integer dense types) -> ``gguf.DenseTensor``,
     * little-endian Q4_K / Q8_0 -> ``gguf.NativeTensor`` (blocks kept as stored,
       executed by the native linear),
+    * MXFP4 (type 39) -> ``gguf.MxFp4Tensor`` (E2M1 codes + E8M0 scale bytes),
     * Q4_0, and big-endian Q4_K / Q8_0 -> ``gguf.AffineTensor``.
 
     Returns {name: tensor}.  Two pinned staging buffers of ``staging_bytes``
@@ -352,7 +353,7 @@ def stream_convert(path: str, names: Optional[Sequence[str]] = None, staging_byt
     through in buffer-sized pieces."""
     from . import gguf as G
 
-    return _stream(path, names, staging_bytes, lambda desc, raw, endian: G.convert(desc, raw, endian))
+    return _stream(path, names, staging_bytes, lambda desc, raw, endian: G.convert(desc, raw, endian), True)
 
 
 def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, staging_bytes: int = 256 << 20):
@@ -370,7 +371,7 @@ def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, stag
     return _stream(path, names, staging_bytes, conv)
 
 
-def _stream(path: str, names: Optional[Sequence[str]], staging_bytes: int, conv):
+def _stream(path: str, names: Optional[Sequence[str]], staging_bytes: int, conv, mxfp4: bool = False):
     import torch
 
     from . import gguf as G
@@ -385,7 +386,7 @@ def _stream(path: str, names: Optional[Sequence[str]], staging_bytes: int, conv)
     for t in wanted:  # refuse before anything is read
         ty = G.ggml_type_from_code(t.ggml_type)
         kind = G.conversion_kind(ty, endian)
-        if kind.kind != "dense" and not ty.has_device_kernels():
+        if kind.kind != "dense" and not ty.has_device_kernels() and not (mxfp4 and kind.kind == "mxfp4"):
             raise EreduError(f"tensor {t.name!r}: GGML type {t.ggml_type} has no device conversion")
     dev = torch.device("cuda")
     copy_stream = torch.cuda.Stream()

@@ -49,7 +49,7 @@ const char* eq_last_error(void);
 int eq_version(void);
 
 /*
- * Group-wise affine quantized matmul.
+ * Group-wise quantized matmul (affine or MXFP4).
  * Replaces mlx_quantized_matmul (safemlx-sys/src/mlx-c/mlx/c/ops.h:809-819) as
  * called by safemlx::ops::quantized_matmul_with_mode
  * (safemlx/src/ops/quantization.rs:190-226).
@@ -61,10 +61,14 @@ int eq_version(void);
  *   W[r, c] = scale[r, c/gs] * q[r, c] + bias[r, c/gs], q read LSB-first from
  *   the u32 words (eredu-gguf/src/convert.rs:87-99,413-427).
  * x is [M, K] of x_dtype (leading batch dims flattened into M), y is [M, N] of
- * x_dtype.  biases may be NULL (treated as zero).  mode must be "affine" (or
- * NULL).  bits in {2, 3, 4, 5, 6, 8} (3/5/6-bit codes form an LSB-first bit
- * stream and may straddle words; a packed row holds whole words); group_size
- * 16 or a positive multiple of 32 (eredu-checkpoint/src/lib.rs:103-122).
+ * x_dtype.  biases may be NULL (treated as zero).  mode "affine" (or NULL):
+ * bits in {2, 3, 4, 5, 6, 8} (3/5/6-bit codes form an LSB-first bit stream
+ * and may straddle words; a packed row holds whole words); group_size 16 or a
+ * positive multiple of 32 (eredu-checkpoint/src/lib.rs:103-122).
+ * mode "mxfp4" (safemlx/src/ops/quantization.rs:16-46): group_size 32, bits
+ * 4, scale_dtype EQ_DTYPE_U8 (E8M0 bytes, 2^(e - 127), 255 = NaN), biases
+ * NULL; W[r, c] = 2^(e[r, c/32] - 127) * e2m1(q[r, c]) with the E2M1 code
+ * bit 3 = sign, magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6.
  * Accumulation is f32.
  */
 int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
@@ -101,7 +105,9 @@ int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int count, int64
 
 /*
  * Affine dequantize: out[r, c] = scale[r, c/gs] * q[r, c] + bias[r, c/gs],
- * computed in f32 (one multiply, one add) and written as out_dtype.
+ * computed in f32 (one multiply, one add) and written as out_dtype; "mxfp4":
+ * out[r, c] = 2^(e[r, c/32] - 127) * e2m1(q[r, c]) (scale_dtype EQ_DTYPE_U8,
+ * biases NULL).
  * Replaces mlx_dequantize (safemlx-sys/src/mlx-c/mlx/c/ops.h:359-369) as called
  * by safemlx::ops::dequantize_with_mode (safemlx/src/ops/quantization.rs:256-289).
  * w is [rows, cols*bits/32] u32; scales/biases [rows, cols/gs]; biases may be NULL.
@@ -188,7 +194,12 @@ int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
  * edge value made exactly representable, bias = edge, codes rounded from the
  * stored scale and bias.  Replaces mlx_quantize (ops.h:801-808) under
  * safemlx::ops::quantize_with_mode (safemlx/src/ops/quantization.rs:100-159).
- * bits and group_size as for eq_quantized_matmul.
+ * bits and group_size as for eq_quantized_matmul.  "mxfp4" (group 32, bits
+ * 4, biases NULL): scales are u8 E8M0 bytes, the smallest power of two 2^e,
+ * e in [-127, 127], with max|w| / 2^e <= 6 (a group with a NaN or infinity:
+ * 255, an all-zero group: 0), and each code the nearest E2M1 value of
+ * w / 2^e, ties to the even code, sign bit set for w < 0 (the OCP
+ * microscaling rule; MLX's own quantizer is not available to check against).
  */
 int eq_quantize(uint32_t* w_out, void* scales, void* biases, const void* w, int64_t rows, int64_t cols,
                 int group_size, int bits, const char* mode, int dtype, eq_stream_t stream);

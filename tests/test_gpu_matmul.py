@@ -131,11 +131,17 @@ def test_transpose_false(cuda, M):
 # fills half of one, 384 three, 4096 thirty-two; K = 96 is two row runs of 64
 # and 32, the others 8 to 56 runs of 64 to 256 rows, added by the last
 # workgroup of each tile), M = 2..8 qmm_n_small (16 / 32 / 64 word columns per
-# workgroup; partial sums through the workspace); M = 9 takes the general
-# kernel.
+# workgroup; partial sums through the workspace); M > 8 runs qmm_n_small on
+# 8-row batches over the one weight matrix plus a launch for the rest.
 @pytest.mark.parametrize("N,K", [(64, 96), (384, 1024), (4096, 4096), (128, 4096), (1024, 14336)])
 @pytest.mark.parametrize("M", [1, 2, 5, 8, 9])
 def test_transpose_false_small_m(cuda, N, K, M):
+    run_case(M, N, K, 64, 4, transpose=False, seed=N + K + M)
+
+
+@pytest.mark.parametrize("N,K", [(384, 1024), (4096, 4096)])
+@pytest.mark.parametrize("M", [16, 23, 64])
+def test_transpose_false_row_chunks(cuda, N, K, M):
     run_case(M, N, K, 64, 4, transpose=False, seed=N + K + M)
 
 

@@ -89,7 +89,8 @@ def test_dequantize_matches_oracle(cuda, out):
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan)
     if out == torch.float32:
-        exp = ref.astype(np.float32).astype(np.float64)
+        with np.errstate(over="ignore"):  # 6 * 2^127 overflows to inf, as on the device
+            exp = ref.astype(np.float32).astype(np.float64)
     else:
         exp = torch.from_numpy(ref).to(out).double().numpy()
     assert np.array_equal(got[~nan], exp[~nan])
@@ -141,14 +142,20 @@ def x_of(M, K, xdt, seed):
 MATMUL_CASES = [
     # (M, N, K, x dtype, transpose)
     (1, 4096, 4096, orc.BF16, True),     # the decode kernel
-    (5, 1024, 2048, orc.BF16, True),     # decode kernel, two activation passes
-    (16, 512, 1024, orc.BF16, True),
+    (4, 1024, 2048, orc.BF16, True),     # decode kernel, four activation rows
+    (5, 1000, 2048, orc.BF16, True),     # decode kernel, two passes (N % 128 != 0)
+    (16, 512, 1024, orc.BF16, True),     # the MFMA qmm from M = 5 on
     (1, 300, 14336, orc.BF16, True),     # a long row: the decode kernel's single-row LDS case
-    (37, 256, 512, orc.BF16, True),      # the general kernel
+    (37, 256, 512, orc.BF16, True),      # the MFMA qmm (N % 128 == 0, K % 64 == 0)
+    (300, 1024, 2048, orc.BF16, True),   # MFMA qmm, K split over workgroups
+    (130, 384, 4160, orc.BF16, True),    # MFMA qmm, ragged row tile, odd chunk count
+    (37, 200, 512, orc.BF16, True),      # the general kernel (N % 128 != 0)
     (7, 258, 1024, orc.F32, True),
     (3, 130, 160, orc.F16, True),
-    (1, 4096, 1024, orc.BF16, False),
-    (9, 512, 256, orc.F32, False),
+    (1, 4096, 1024, orc.BF16, False),    # split-K VALU kernel (M <= 8, bf16)
+    (8, 512, 2048, orc.BF16, False),
+    (12, 256, 512, orc.BF16, False),     # 8-row launches plus the rest (M > 8)
+    (9, 512, 256, orc.F32, False),       # the general kernel (f32 x)
     (4, 96, 64, orc.F16, False),
 ]
 
@@ -187,6 +194,35 @@ def test_gather_matches_oracle(cuda, transpose, sorted_hint):
             assert np.all(got[b] == 0.0)
             continue
         ref = orc.mxfp4_matmul_f64(xb[lhs[b]], orc.BF16, wq[rhs[b]], sc[rhs[b]], transpose, N, K)
+        assert orc.matmul_within_tolerance(got[b], ref, True)[0], b
+
+
+@pytest.mark.parametrize("B,E,sorted_hint", [(6, 4, False), (40, 4, True), (160, 8, True)])
+def test_routed_decode_matches_oracle(cuda, B, E, sorted_hint):
+    """One activation row per route (moe.rs:121-139): the per-route kernel, and
+    for many sorted routes the grouped MFMA qmm (an out-of-range expert gives a
+    zero row either way)."""
+    print(f"[case] mxfp4 routed decode B={B} E={E} sorted={sorted_hint}", flush=True)
+    N, K = 512, 1024
+    banks = [random_mx(N, K, 60 + e) for e in range(E)]
+    wq = np.stack([b[0] for b in banks])
+    sc = np.stack([b[1] for b in banks])
+    xb = synthetic_x(B, K, 19).reshape(B, 1, K)
+    rng = np.random.default_rng(B)
+    rhs = rng.integers(0, E, size=B).astype(np.int32)
+    rhs[-1] = E + 3
+    if sorted_hint:
+        rhs = np.sort(rhs)
+    lhs = np.arange(B, dtype=np.int32)
+    y = gather_qmm_with_mode(dev_bf16(xb), dev_words(wq), dev_u8(sc), None, torch.from_numpy(lhs).cuda(),
+                             torch.from_numpy(rhs).cuda(), True, 32, 4, sorted_hint, MX)
+    torch.cuda.synchronize()
+    got = host_f32(y)
+    for b in range(B):
+        if rhs[b] >= E:
+            assert np.all(got[b] == 0.0), b
+            continue
+        ref = orc.mxfp4_matmul_f64(xb[b], orc.BF16, wq[rhs[b]], sc[rhs[b]], True, N, K)
         assert orc.matmul_within_tolerance(got[b], ref, True)[0], b
 
 
@@ -250,3 +286,31 @@ def test_gguf_random_blocks(cuda):
     with pytest.raises(EreduError, match="divisible by 32"):
         G.convert(G.TensorDescriptor("bad", [48], G.GgmlType.MXFP4, 17), dev_u8(raw[:17]))
     assert math.isfinite(float(deq.abs().max()))
+
+
+def test_streamed_gguf_mxfp4_layer(cuda, tmp_path):
+    """A type-39 tensor in a GGUF file streams to an MxFp4Tensor (both byte
+    orders: single bytes), and a QuantizedLinear over it computes the MXFP4
+    matmul (safemlx/src/ops/gguf.rs:498-525 hands MLX the same pair)."""
+    from eredu_amd import QuantizedLinear
+    from eredu_amd import gguf_file as F
+
+    N, K = 256, 512
+    rng = np.random.default_rng(23)
+    raw = rng.integers(0, 256, size=N * K // 32 * 17, dtype=np.uint8)
+    raw[0::17] = rng.integers(118, 128, size=N * K // 32)
+    for endian in ("little", "big"):
+        path = tmp_path / f"mx_{endian}.gguf"
+        with open(path, "wb") as f:
+            F.write_gguf(f, {}, [("blk.0.ffn_gate_exps.weight", [K, N], 39, raw.tobytes())], endian=endian)
+        t = F.stream_convert(str(path), staging_bytes=4096)["blk.0.ffn_gate_exps.weight"]
+        assert isinstance(t, G.MxFp4Tensor) and t.weight_shape == [N, K // 8] and t.scale_shape == [N, K // 32]
+        rw, rs = orc.mxfp4_convert_ggml(raw, N, K)
+        assert np.array_equal(t.weights.cpu().numpy().view(np.uint32), rw)
+        layer = QuantizedLinear(t.weights, t.scales, None, 32, 4, mode=MX)
+        xb = synthetic_x(3, K, 29)
+        y = layer(dev_bf16(xb))
+        ref = orc.mxfp4_matmul_f64(xb, orc.BF16, rw, rs, True, N, K)
+        assert orc.matmul_within_tolerance(host_f32(y), ref, True)[0]
+    with pytest.raises(EreduError, match="no device conversion"):
+        F.stream_convert_affine(str(tmp_path / "mx_little.gguf"))
