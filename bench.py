@@ -18,7 +18,8 @@ value = algorithmic bytes of the step / step time, in GB/s
 Also reported (not the headline): the same step with one launch per
 projection (the drop-in eq_quantized_matmul path) and with all seven
 projections of a layer in one launch, M = 8, per-shape qmv, prefill qmm
-TFLOP/s, GGUF dequant/convert GB/s, the roofline
+TFLOP/s, GGUF dequant/convert GB/s, the MXFP4
+mode (decode, prefill, routed experts, codec, GGUF type 39), the roofline
 record of the dominant kernel (qmv_lds_kernel) and the CPU baseline (the
 restated MLX CPU qmm loop of oracle/, timed on this host).
 
@@ -424,6 +425,116 @@ def bench_affine_codec(steps, warmup):
     return res
 
 
+def bench_mxfp4(steps, warmup):
+    """MXFP4 mode (E2M1 codes, one E8M0 scale byte per 32 values, no biases):
+    decode (M = 1) and prefill (M = 512) quantized_matmul, the routed-expert
+    decode of a Mixtral-shaped bank (2 routes per token), transpose = false
+    at M = 1, dequantize / quantize, and GGUF type-39 conversion.  Weight
+    copies rotate >= ROTATE_BYTES per replay (the prefill leg: 4 copies).
+    Bytes per linear: N*K/2 codes + N*K/32 scale bytes + 2*M*K + 2*M*N."""
+    import torch
+
+    n = _lib()
+    u8 = n.EQ_DTYPE_U8
+    out = {}
+
+    def mx_bytes(M, N, K):
+        return N * K // 2 + N * K // 32 + 2 * M * K + 2 * M * N
+
+    def mx_weights(rows, cols, count):
+        ws = [torch.randint(-2**31, 2**31 - 1, (rows, cols // 8), dtype=torch.int32, device="cuda")
+              for _ in range(count)]
+        ss = [torch.randint(118, 128, (rows, cols // 32), dtype=torch.uint8, device="cuda") for _ in range(count)]
+        return ws, ss
+
+    for label, M, N, K, transpose in (("decode_M1_4096x4096", 1, 4096, 4096, True),
+                                      ("decode_M1_14336x4096", 1, 14336, 4096, True),
+                                      ("decode_M1_4096x14336", 1, 4096, 14336, True),
+                                      ("prefill_M512_4096x4096", 512, 4096, 4096, True),
+                                      ("prefill_M512_14336x4096", 512, 14336, 4096, True),
+                                      ("xW_M1_4096x4096", 1, 4096, 4096, False)):
+        rows, cols = (N, K) if transpose else (K, N)
+        copies = rotation(mx_bytes(M, N, K)) if M == 1 else 4
+        ws, ss = mx_weights(rows, cols, copies)
+        x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+
+        def fn(st):
+            for w, sc in zip(ws, ss):
+                n.check(n.lib().eq_quantized_matmul(y.data_ptr(), x.data_ptr(), w.data_ptr(), sc.data_ptr(), None, M,
+                                                    N, K, transpose, 32, 4, b"mxfp4", n.EQ_DTYPE_BF16, u8, st))
+
+        ms = Timer(fn).ms_per_replay(max(steps // 4, 10), warmup) / copies
+        rec = {"us": round(ms * 1e3, 2), "copies": copies}
+        if M == 1:
+            gbs = mx_bytes(M, N, K) / (ms * 1e-3) / 1e9
+            rec.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        else:
+            tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            rec.update({"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)})
+        out[label] = rec
+        del ws, ss
+        torch.cuda.empty_cache()
+
+    # routed experts: 8 experts, 2 routes per token, 4 tokens per replay on disjoint pairs
+    E, routes = 8, 2
+    for label, N, K in (("routed_gate_up_14336x4096", 14336, 4096), ("routed_down_4096x14336", 4096, 14336)):
+        w = torch.randint(-2**31, 2**31 - 1, (E, N, K // 8), dtype=torch.int32, device="cuda")
+        sc = torch.randint(118, 128, (E, N, K // 32), dtype=torch.uint8, device="cuda")
+        x = torch.randn((routes, 1, K), device="cuda").to(torch.bfloat16)
+        y = torch.empty((routes, 1, N), dtype=torch.bfloat16, device="cuda")
+        lhs = torch.arange(routes, dtype=torch.int32, device="cuda")
+        rhs = [torch.tensor([2 * i + 1, 2 * i], dtype=torch.int32, device="cuda") for i in range(E // 2)]
+
+        def fr(st):
+            for r in rhs:
+                n.check(n.lib().eq_gather_qmm(y.data_ptr(), x.data_ptr(), w.data_ptr(), sc.data_ptr(), None,
+                                              lhs.data_ptr(), r.data_ptr(), routes, routes, E, 1, N, K, True, 32, 4,
+                                              b"mxfp4", n.EQ_DTYPE_BF16, u8, True, st))
+
+        ms = Timer(fr).ms_per_replay(max(steps // 4, 20), warmup) / len(rhs)
+        nbytes = routes * (N * K // 2 + N * K // 32) + routes * (K + N) * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[label] = {"us": round(ms * 1e3, 2), "MB": round(nbytes / 1e6, 2), "GB/s": round(gbs, 1),
+                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del w, sc
+        torch.cuda.empty_cache()
+
+    # codec: 4096 x 14336 dequantize (-> bf16), quantize (bf16 ->), GGUF type-39 blocks -> MLX pair
+    rows, cols = 4096, 14336
+    packed = rows * cols // 2 + rows * cols // 32
+    copies = rotation(packed + rows * cols * 2)
+    ws, ss = mx_weights(rows, cols, copies)
+    dense = [torch.randn((rows, cols), device="cuda").to(torch.bfloat16) for _ in range(copies)]
+    nraw = rows * cols // 32 * 17
+    cc = rotation(nraw + packed)
+    raws = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(cc)]
+    cw, cs = mx_weights(rows, cols, cc)
+
+    def deq(st):
+        for w, sc, o in zip(ws, ss, dense):
+            n.check(n.lib().eq_dequantize(o.data_ptr(), w.data_ptr(), sc.data_ptr(), None, rows, cols, 32, 4,
+                                          b"mxfp4", u8, n.EQ_DTYPE_BF16, st))
+
+    def quant(st):
+        for d, w, sc in zip(dense, ws, ss):
+            n.check(n.lib().eq_quantize(w.data_ptr(), sc.data_ptr(), None, d.data_ptr(), rows, cols, 32, 4,
+                                        b"mxfp4", n.EQ_DTYPE_BF16, st))
+
+    def conv(st):
+        for r, w, sc in zip(raws, cw, cs):
+            n.check(n.lib().eq_gguf_convert_mxfp4(w.data_ptr(), sc.data_ptr(), r.data_ptr(), nraw, rows, cols, st))
+
+    for label, fn, nb, k in (("dequantize_bf16", deq, packed + rows * cols * 2, copies),
+                             ("quantize_bf16", quant, packed + rows * cols * 2, copies),
+                             ("gguf_convert_type39", conv, nraw + packed, cc)):
+        ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / k
+        gbs = nb / (ms * 1e-3) / 1e9
+        out[label] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                      "copies": k}
+    return out
+
+
 def bench_gguf_stream():
     """GGUF file -> HBM affine triples (gguf_file.stream_convert_affine): a
     file of 8 Q4_K tensors of 4096 x 14336 (264 MB, synthetic blocks) in the
@@ -638,6 +749,8 @@ def main():
                     help="only the gather_qmm and transpose = false figures, one JSON object")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the full decode step of configs[4], one JSON object of its figures")
+    ap.add_argument("--mxfp4-only", action="store_true",
+                    help="only the MXFP4-mode figures, one JSON object")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build runs on a single GPU "
@@ -649,8 +762,11 @@ def main():
 
     _lib().lib()
     torch.cuda.set_device(0)
-    if args.prefill_only or args.gguf_only or args.gather_only:
+    if args.prefill_only or args.gguf_only or args.gather_only or args.mxfp4_only:
         out = {}
+        if args.mxfp4_only:
+            log("[bench] mxfp4 mode")
+            out["mxfp4"] = bench_mxfp4(args.steps, args.warmup)
         if args.prefill_only:
             log("[bench] qmm prefill")
             out["qmm"] = bench_qmm(args.steps, args.warmup)
@@ -722,6 +838,8 @@ def main():
         detail["gather_qmm"] = bench_gather(args.steps, args.warmup)
         log("[bench] transpose = false (qmm_n)")
         detail["qmm_n"] = bench_qmm_n(args.steps, args.warmup)
+        log("[bench] mxfp4 mode")
+        detail["mxfp4"] = bench_mxfp4(args.steps, args.warmup)
 
     per_launch_bytes = nbytes / launches
     avg_launch_us = ms * 1e3 / launches

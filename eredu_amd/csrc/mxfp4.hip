@@ -90,6 +90,45 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(typename OT::storage
     for (int c = 0; c < 8; c++) store_out<OT>(out, i * 8 + c, e2m1_to_f32((word >> (4 * c)) & 15u) * s);
 }
 
+// One thread per code word (8 values; consecutive lanes, consecutive words)
+// with 16-byte streaming stores: the codes convert in hardware
+// (v_cvt_scalef32_pk_{bf16,f32}_fp4 with the scale's f32 image, exact); f16
+// outputs round from the exact f32 values.  out 16-byte aligned.
+template <typename OT>
+__global__ __launch_bounds__(256) void mxfp4_dequant_vec_kernel(typename OT::storage* __restrict__ out,
+                                                                const uint32_t* __restrict__ w,
+                                                                const uint8_t* __restrict__ sc, int64_t words) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= words) return;
+    const uint32_t q = w[i];
+    const float s = e8m0_to_f32(sc[i >> 2]);
+    uint4* dst = reinterpret_cast<uint4*>(out + i * 8);
+    if constexpr (__is_same(OT, BF16T)) {
+        uint32_t p[4];
+        e2m1x8_to_bf16(q, s, p);
+        store_stream16(dst, make_uint4(p[0], p[1], p[2], p[3]));
+    } else {
+        const auto a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, s, 0);
+        const auto b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, s, 1);
+        const auto c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, s, 2);
+        const auto d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(q, s, 3);
+        const float v[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+        if constexpr (__is_same(OT, F32T)) {
+            store_stream16(dst, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                           __float_as_uint(v[3])));
+            store_stream16(dst + 1, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                               __float_as_uint(v[7])));
+        } else {
+            uint32_t h[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                h[k] = uint32_t(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * k]))) |
+                       (uint32_t(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * k + 1]))) << 16);
+            store_stream16(dst, make_uint4(h[0], h[1], h[2], h[3]));
+        }
+    }
+}
+
 constexpr int kMxRows = 4;  // weight rows (waves) per workgroup of the transposed kernel
 constexpr int kMxM = 4;     // activation rows per pass
 
@@ -198,10 +237,13 @@ int mxfp4_dequantize(void* out, const uint32_t* w, const uint8_t* scales, int64_
         set_error("tensor too large");
         return 1;
     }
+    const bool vec = aligned(out, 16);
     const dim3 grid(unsigned((words + 255) / 256));
     with_dtype(out_dtype, [&](auto ot) {
         typedef decltype(ot) OT;
-        mxfp4_dequant_kernel<OT><<<grid, 256, 0, st>>>(static_cast<typename OT::storage*>(out), w, scales, words);
+        typedef typename OT::storage OS;
+        if (vec) mxfp4_dequant_vec_kernel<OT><<<grid, 256, 0, st>>>(static_cast<OS*>(out), w, scales, words);
+        else mxfp4_dequant_kernel<OT><<<grid, 256, 0, st>>>(static_cast<OS*>(out), w, scales, words);
     });
     return check_launch("dequantize (mxfp4)");
 }

@@ -59,34 +59,6 @@ template <typename ST> __device__ __forceinline__ float any_param(uint32_t v);
 template <> __device__ __forceinline__ float any_param<BF16T>(uint32_t v) { return bf16_bits_to_f32(v & 0xffffu); }
 template <> __device__ __forceinline__ float any_param<F16T>(uint32_t v) { return f16_bits_to_f32(v & 0xffffu); }
 
-// MXFP4: 8 E2M1 codes of a word (nibble i = code i) as bf16 pairs (c0, c2),
-// (c4, c6), (c1, c3), (c5, c7): the magnitudes (3 bits) index byte tables of
-// the bf16 images with v_perm, the sign bit is OR-ed into the high byte.
-__device__ __forceinline__ void e2m1_pairs8(uint32_t w, uint32_t* p) {
-    const uint32_t TL0 = 0xC0800000u, TL1 = 0xC0804000u;  // low bytes of bf16(0, .5, 1, 1.5 | 2, 3, 4, 6)
-    const uint32_t TH0 = 0x3F3F3F00u, TH1 = 0x40404040u;  // high bytes
-    const uint32_t ie = w & 0x07070707u, io = (w >> 4) & 0x07070707u;  // magnitudes of even / odd nibbles
-    const uint32_t le = __builtin_amdgcn_perm(TL1, TL0, ie);
-    const uint32_t he = __builtin_amdgcn_perm(TH1, TH0, ie) | ((w << 4) & 0x80808080u);
-    const uint32_t lo = __builtin_amdgcn_perm(TL1, TL0, io);
-    const uint32_t ho = __builtin_amdgcn_perm(TH1, TH0, io) | (w & 0x80808080u);
-    p[0] = __builtin_amdgcn_perm(he, le, 0x05010400u);  // (c0, c2)
-    p[1] = __builtin_amdgcn_perm(he, le, 0x07030602u);  // (c4, c6)
-    p[2] = __builtin_amdgcn_perm(ho, lo, 0x05010400u);  // (c1, c3)
-    p[3] = __builtin_amdgcn_perm(ho, lo, 0x07030602u);  // (c5, c7)
-}
-
-// 8 activations [x0 .. x7] as the pairs (x0, x2), (x4, x6), (x1, x3), (x5, x7)
-// that meet e2m1_pairs8's code pairs.
-__device__ __forceinline__ qa_u32x4 mx_permute_x8(qa_u32x4 d) {
-    qa_u32x4 t;
-    t[0] = __builtin_amdgcn_perm(d[1], d[0], 0x05040100u);
-    t[1] = __builtin_amdgcn_perm(d[3], d[2], 0x05040100u);
-    t[2] = __builtin_amdgcn_perm(d[1], d[0], 0x07060302u);
-    t[3] = __builtin_amdgcn_perm(d[3], d[2], 0x07060302u);
-    return t;
-}
-
 // Loads the BITS words of segment `off` (byte offset) into wv.
 template <int BITS>
 __device__ __forceinline__ void load_segment(uint32_t* wv, __amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -113,8 +85,8 @@ __device__ __forceinline__ void load_segment(uint32_t* wv, __amdgpu_buffer_rsrc_
 
 // GS16: group size 16 (two groups per segment); otherwise a segment lies in
 // one group (group size a multiple of 32).  MX: MXFP4 (BITS 4, group 32,
-// E8M0 scale bytes, no biases): codes decode to E2M1 bf16 pairs, activations
-// are staged in the pairs' order, y = sum over groups of 2^(e - 127) x . v.
+// E8M0 scale bytes, no biases): the codes convert in hardware to bf16 pairs
+// with the group's scale folded in (e2m1x8_to_bf16), y = sum x . v.
 template <int BITS, typename ST, int MC, bool GS16, bool MX = false>
 __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArgs a) {
     static_assert(!MX || (BITS == 4 && !GS16), "MXFP4 is 4-bit, group 32");
@@ -140,7 +112,7 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
             for (int i = 0; i < 4; i++) sum += bf16_bits_to_f32(v[i] & 0xffffu) + bf16_bits_to_f32(v[i] >> 16);
             sum += __shfl_xor(sum, 1);
             if (live) {
-                *reinterpret_cast<qa_u32x4*>(smem + m * K * 2 + any_chunk_slot(q) * 16) = MX ? mx_permute_x8(v) : v;
+                *reinterpret_cast<qa_u32x4*>(smem + m * K * 2 + any_chunk_slot(q) * 16) = v;
                 if ((q & 1) == 0) xs16[m * (K / 16) + (q >> 1)] = sum;
             }
         }
@@ -180,7 +152,7 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
             uint32_t pk[16];
             if constexpr (MX) {
 #pragma unroll
-                for (int r = 0; r < 4; r++) e2m1_pairs8(wv[r], pk + 4 * r);
+                for (int r = 0; r < 4; r++) e2m1x8_to_bf16(wv[r], s0, pk + 4 * r);
             } else if constexpr (BITS < 8) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) pk[i] = seg_code<BITS>(wv, 2 * i) | (seg_code<BITS>(wv, 2 * i + 1) << 16) | kMagic;
@@ -221,7 +193,7 @@ __global__ __launch_bounds__(64 * kAnyWaves) void qmv_any_kernel(const QmvAnyArg
                     }
                 }
                 if constexpr (MX) {
-                    acc[m] = fmaf(s0, t0 + t1, acc[m]);
+                    acc[m] += t0 + t1;
                 } else if constexpr (GS16) {
                     acc[m] += fmaf(s0, t0, b0 * xa) + fmaf(s1, t1, b1 * xb);
                 } else {

@@ -96,6 +96,28 @@ def test_dequantize_matches_oracle(cuda, out):
     assert np.array_equal(got[~nan], exp[~nan])
 
 
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16, torch.float16])
+def test_dequantize_unaligned_output_takes_the_scalar_kernel(cuda, out):
+    """An output 2 bytes past a 16-byte boundary runs the per-word kernel;
+    its values equal the 16-byte-store kernel's bit for bit."""
+    from eredu_amd import _native as n
+
+    rows, cols = 7, 128
+    wq, sc = random_mx(rows, cols, 31)
+    w, s = dev_words(wq), dev_u8(sc)
+    ref = dequantize_with_mode(w, s, None, 32, 4, MX, dtype=out)
+    code = {torch.float32: n.EQ_DTYPE_F32, torch.bfloat16: n.EQ_DTYPE_BF16, torch.float16: n.EQ_DTYPE_F16}[out]
+    buf = torch.zeros(rows * cols + 8, dtype=out, device="cuda")
+    shifted = buf[1:1 + rows * cols]
+    n.check(n.lib().eq_dequantize(shifted.data_ptr(), w.data_ptr(), s.data_ptr(), None, rows, cols, 32, 4, b"mxfp4",
+                                  n.EQ_DTYPE_U8, code, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    got, exp = shifted.view(rows, cols), ref
+    assert torch.equal(torch.isnan(got), torch.isnan(exp))
+    ok = ~torch.isnan(exp)
+    assert torch.equal(got[ok], exp[ok])
+
+
 def test_dequantize_default_dtype_is_bf16(cuda):
     wq = torch.zeros((2, 4), dtype=torch.int32, device="cuda")
     sc = torch.full((2, 1), 127, dtype=torch.uint8, device="cuda")
