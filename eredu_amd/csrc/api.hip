@@ -68,7 +68,10 @@ __global__ __launch_bounds__(256) void qmm_n_general(typename XT::storage* __res
 // One thread per code word; its PACK codes share a group (gs >= 32 >= PACK).
 // VEC (out 16-byte aligned): the word's outputs leave as 8- or 16-byte
 // stores instead of PACK scalar ones.
-template <int BITS, typename ST, typename OT, bool VEC>
+// GS: the group size when it is a compile-time power of two (32, 64, 128),
+// else 0 and `gs` holds it.  Rows hold whole groups, so the group of element
+// e (row-major) is e / gs.
+template <int BITS, typename ST, typename OT, bool VEC, int GS = 0>
 __global__ __launch_bounds__(256) void dequant_kernel(typename OT::storage* __restrict__ out,
                                                       const uint32_t* __restrict__ w,
                                                       const typename ST::storage* __restrict__ s,
@@ -81,8 +84,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(typename OT::storage* __re
     if (i >= words) return;
     const uint32_t word = w[i];
     const int64_t base = i * PACK;  // element index of the word's first code
-    const int64_t r = base / cols, c0 = base % cols;
-    const int64_t g = r * (cols / gs) + c0 / gs;
+    const int64_t g = GS ? base / GS : base / gs;
     const float sc = load_param<ST>(s, g);
     const float bi = b ? load_param<ST>(b, g) : 0.f;
     OS v[PACK];
@@ -748,11 +750,16 @@ extern "C" int eq_dequantize(void* out, const uint32_t* w, const void* scales, c
                     dequant_odd_kernel<B, ST, OT><<<dim3(unsigned((units + 255) / 256)), 256, 0, st>>>(
                         static_cast<OS*>(out), w, static_cast<const SS*>(scales), static_cast<const SS*>(biases), rows,
                         cols, group_size);
-                } else if (aligned(out, 16))
-                    dequant_kernel<B, ST, OT, true><<<grid, 256, 0, st>>>(
-                        static_cast<OS*>(out), w, static_cast<const SS*>(scales), static_cast<const SS*>(biases), rows,
-                        cols, group_size);
-                else
+                } else if (aligned(out, 16)) {
+                    auto go = [&](auto kernel) {
+                        kernel<<<grid, 256, 0, st>>>(static_cast<OS*>(out), w, static_cast<const SS*>(scales),
+                                                     static_cast<const SS*>(biases), rows, cols, group_size);
+                    };
+                    if (group_size == 32) go(dequant_kernel<B, ST, OT, true, 32>);
+                    else if (group_size == 64) go(dequant_kernel<B, ST, OT, true, 64>);
+                    else if (group_size == 128) go(dequant_kernel<B, ST, OT, true, 128>);
+                    else go(dequant_kernel<B, ST, OT, true>);
+                } else
                     dequant_kernel<B, ST, OT, false><<<grid, 256, 0, st>>>(
                         static_cast<OS*>(out), w, static_cast<const SS*>(scales), static_cast<const SS*>(biases), rows,
                         cols, group_size);
