@@ -583,6 +583,27 @@ class QuantizedEmbedding:
         self.native = native
 
     @classmethod
+    def unloaded(cls, embedding_count: int, dimensions: int, group_size: int, bits: int,
+                 device=None) -> "QuantizedEmbedding":
+        """Placeholder table carrying only shapes (quantized.rs:211-227)."""
+        return cls.unloaded_with_mode(embedding_count, dimensions, group_size, bits, QuantizationMode.Affine, device)
+
+    @classmethod
+    def unloaded_with_mode(cls, embedding_count: int, dimensions: int, group_size: int, bits: int,
+                           mode: QuantizationMode, device=None) -> "QuantizedEmbedding":
+        """quantized.rs:229-280: u32 codes [count, packed], scales [count,
+        dims / gs] in f32 (u8 for MXFP4), f32 biases when the mode has them."""
+        mode.validate(group_size, bits)
+        dev = torch.device("cuda") if device is None else device
+        scale_dtype = torch.uint8 if mode is QuantizationMode.MxFp4 else torch.float32
+        weight = torch.zeros((embedding_count, quantized_packed_dimension(dimensions, bits)), dtype=torch.int32,
+                             device=dev)
+        scales = torch.zeros((embedding_count, dimensions // group_size), dtype=scale_dtype, device=dev)
+        biases = (torch.zeros((embedding_count, dimensions // group_size), dtype=torch.float32, device=dev)
+                  if mode.has_biases() else None)
+        return cls(weight, scales, biases, group_size, bits, mode)
+
+    @classmethod
     def try_from_embedding(cls, table: torch.Tensor, group_size: Optional[int] = None,
                            bits: Optional[int] = None) -> "QuantizedEmbedding":
         gs = DEFAULT_GROUP_SIZE if group_size is None else group_size

@@ -336,3 +336,40 @@ def test_streamed_gguf_mxfp4_layer(cuda, tmp_path):
         assert orc.matmul_within_tolerance(host_f32(y), ref, True)[0]
     with pytest.raises(EreduError, match="no device conversion"):
         F.stream_convert_affine(str(tmp_path / "mx_little.gguf"))
+
+
+def test_quantized_embedding_mxfp4(cuda):
+    """QuantizedEmbedding over an MXFP4 table (safemlx/src/nn/quantized.rs:
+    359-435 with mode MxFp4): forward = the ids' rows dequantized (bf16,
+    bit-exact against the oracle), as_linear = the MXFP4 matmul."""
+    from eredu_amd import QuantizedEmbedding
+
+    vocab, dim = 300, 256
+    wq, sc = random_mx(vocab, dim, 71)
+    emb = QuantizedEmbedding(dev_words(wq), dev_u8(sc), None, 32, 4, MX)
+    ids = torch.tensor([[0, 299, 17], [17, 5, 128]], device="cuda")
+    out = emb(ids)
+    assert tuple(out.shape) == (2, 3, dim) and out.dtype == torch.bfloat16
+    ref = orc.mxfp4_dequant_f64(wq, sc, vocab, dim)[ids.cpu().numpy().reshape(-1)]
+    exp = torch.from_numpy(ref).to(torch.bfloat16).reshape(2, 3, dim)
+    assert torch.equal(out.cpu().view(torch.int16), exp.view(torch.int16))
+    xb = synthetic_x(2, dim, 72)
+    y = emb.as_linear(dev_bf16(xb))
+    yref = orc.mxfp4_matmul_f64(xb, orc.BF16, wq, sc, True, vocab, dim)
+    assert orc.matmul_within_tolerance(host_f32(y), yref, True)[0]
+
+
+def test_reference_mxfp4_modules_have_no_quantization_biases(cuda):
+    """safemlx/src/nn/quantized.rs:906-939: an MXFP4 QuantizedLinear (64 -> 8,
+    with a dense bias) and QuantizedEmbedding (16 x 64) built unloaded run
+    and carry no quantization biases."""
+    from eredu_amd import QuantizedEmbedding, QuantizedLinear
+
+    linear = QuantizedLinear.unloaded_with_mode(64, 8, 32, 4, MX, bias=True)
+    assert linear.biases is None and linear.bias is not None and linear.scales.dtype == torch.uint8
+    out = linear(torch.ones((2, 64), dtype=torch.float32, device="cuda"))
+    assert tuple(out.shape) == (2, 8)
+    emb = QuantizedEmbedding.unloaded_with_mode(16, 64, 32, 4, MX)
+    assert emb.biases is None
+    tokens = torch.tensor([[0, 3], [7, 15]], dtype=torch.int32, device="cuda")
+    assert tuple(emb(tokens).shape) == (2, 2, 64)
