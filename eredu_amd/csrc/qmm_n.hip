@@ -342,8 +342,10 @@ __global__ __launch_bounds__(256) void qmm_n_m1(const QmmN1Args a) {
 //    below; the run's sums of hi + lo and of x[k] b[k, g] are kept per group.
 // The loads of the next two chunks are in flight while a chunk is computed.
 //
-// Wave w owns slices 2w and 2w + 1 (one group).  ds_read_b64_tr_b4 transposes
-// a 16 x 16 block of nibbles within each 16-lane group: lane (g, i) names row
+// The 8 waves of a workgroup own one 16-column slice each (with 4 waves, two
+// adjacent slices of one group; 8 measured 3-6 % faster on MI355X).
+// ds_read_b64_tr_b4 transposes a 16 x 16 block of nibbles within each
+// 16-lane group: lane (g, i) names row
 // 16g + i of a 64-row block at the slice's 8 bytes and receives column i's
 // codes of rows 16g .. 16g + 15.  Its first word is the B operand of one MFMA
 // (rows 16g + 0..7 for lane block g), its second of the next (rows
@@ -352,6 +354,11 @@ __global__ __launch_bounds__(256) void qmm_n_m1(const QmmN1Args a) {
 // 1 = lo, the other rows zero, so C rows 0 + 1 = sum_k xs (128 + q), and
 //   y[n] = C0 + C1 - 128 sum_k (hi + lo) + sum_k x b.
 // Runs of one tile are combined as in qmm_n_m1.
+#ifndef EQ_QNM_WAVES
+#define EQ_QNM_WAVES 8
+#endif
+constexpr int kQnmWaves = EQ_QNM_WAVES;              // waves per workgroup: 8 / kQnmWaves slices each
+constexpr int kQnmThreads = 64 * kQnmWaves;
 constexpr int kQnmCols = 128;                        // columns per tile
 constexpr int kQnmRows = 256;                        // rows per chunk
 constexpr int kQnmWStride = 80;                      // LDS bytes per code row
@@ -372,15 +379,16 @@ __device__ __forceinline__ bf16x8 qnm_unpack(uint32_t w) {
 }
 
 template <typename ST, int GS>
-__global__ __launch_bounds__(256) void qmm_n_m1_mfma(const QmmN1Args a) {
+__global__ __launch_bounds__(kQnmThreads) void qmm_n_m1_mfma(const QmmN1Args a) {
     typedef typename ST::storage SS;
     typedef int qn_v2i __attribute__((ext_vector_type(2)));
+    constexpr int NT = kQnmThreads, NW = kQnmWaves, SPW = 8 / NW;  // threads, waves, slices per wave
     constexpr int C = kQnmCols, RC = kQnmRows, NG = C >= GS ? C / GS : 1;
-    constexpr int E = RC * NG / 256;  // staged elements per thread and chunk
-    static_assert(E >= 1 && NG <= 4, "group sizes 32, 64, 128");
+    constexpr int E = (RC * NG + NT - 1) / NT;  // staged elements per thread and chunk
+    static_assert(NG <= 4 && (NW == 4 || NW == 8), "group sizes 32, 64, 128; 4 or 8 waves");
     __shared__ __attribute__((aligned(16))) char wl[2][kQnmWBytes];
     __shared__ __attribute__((aligned(16))) char al[2][kQnmABytes];
-    __shared__ float sums[2][4][NG];  // [sum of hi + lo, sum of x b][wave][group]
+    __shared__ float sums[2][NW][NG];  // [sum of hi + lo, sum of x b][wave][group]
     __shared__ float colv[C];
     __shared__ unsigned ticket;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -406,29 +414,30 @@ __global__ __launch_bounds__(256) void qmm_n_m1_mfma(const QmmN1Args a) {
     const __amdgpu_buffer_rsrc_t sr = raw_rsrc(sp, uint32_t(K) * uint32_t(G) * uint32_t(sizeof(SS)));
     const __amdgpu_buffer_rsrc_t br = raw_rsrc(bp, a.b ? uint32_t(K) * uint32_t(G) * uint32_t(sizeof(SS)) : 0u);
 
-    // Code copy: thread t moves 16 bytes (32 columns) of rows t / 4 + 64 j.
+    // Code copy: thread t moves 16 bytes (32 columns) of rows t / 4 + (NT / 4) j.
+    constexpr int CPR = RC / (NT / 4);  // copies per thread and chunk
     const int cr = tid >> 2, cb = (tid & 3) * 16;
     const bool ccol = n0 + 2 * cb < N;
     auto load_codes = [&](qn_u32x4* v, int c) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < RC / 64; j++) {
-            const int r = c * RC + cr + 64 * j;
+        for (int j = 0; j < CPR; j++) {
+            const int r = c * RC + cr + (NT / 4) * j;
             const uint32_t off = (ccol && r < rows) ? uint32_t(kb + r) * row_bytes + uint32_t(n0 / 2 + cb) : kOutOfRange;
             v[j] = __builtin_bit_cast(qn_u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
         }
     };
     auto store_codes = [&](const qn_u32x4* v, int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < RC / 64; j++)
-            *reinterpret_cast<qn_u32x4*>(&wl[buf][(cr + 64 * j) * kQnmWStride + cb]) = v[j];
+        for (int j = 0; j < CPR; j++)
+            *reinterpret_cast<qn_u32x4*>(&wl[buf][(cr + (NT / 4) * j) * kQnmWStride + cb]) = v[j];
     };
-    // Staging: element e = tid + 256 i is (row e / NG of the chunk, group e % NG).
+    // Staging: element e = tid + NT i is (row e / NG of the chunk, group e % NG).
     auto load_stage = [&](uint32_t* xv, uint32_t* sv, uint32_t* bv, int c) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < E; i++) {
-            const int e = tid + 256 * i;
+            const int e = tid + NT * i;
             const int r = c * RC + e / NG, gi = e % NG;
-            const bool live = r < rows && g0 + gi < G;
+            const bool live = e < RC * NG && r < rows && g0 + gi < G;
             const uint32_t xo = live ? uint32_t(kb + r) * 2u : kOutOfRange;
             const uint32_t po =
                 live ? (uint32_t(kb + r) * uint32_t(G) + uint32_t(g0 + gi)) * uint32_t(sizeof(SS)) : kOutOfRange;
@@ -447,7 +456,8 @@ __global__ __launch_bounds__(256) void qmm_n_m1_mfma(const QmmN1Args a) {
                            __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < E; i++) {
-            const int e = tid + 256 * i;
+            const int e = tid + NT * i;
+            if (RC * NG % NT != 0 && e >= RC * NG) break;  // (the last round covers part of the threads)
             const int rr = e / NG, gi = e % NG;
             // dead elements read zero: every term below is zero for them
             const float x1 = bf16_bits_to_f32(xv[i]);
@@ -466,7 +476,7 @@ __global__ __launch_bounds__(256) void qmm_n_m1_mfma(const QmmN1Args a) {
     // Two chunks' loads are in flight while a chunk is computed: register sets
     // 0 and 1 take the even and odd chunks (the loop is unrolled by two so that
     // no set is ever copied).
-    qn_u32x4 cv0[RC / 64], cv1[RC / 64];
+    qn_u32x4 cv0[CPR], cv1[CPR];
     uint32_t xv0[E], sv0[E], bv0[E], xv1[E], sv1[E], bv1[E];
     load_stage(xv0, sv0, bv0, 0);  // (L2) first, so that the staging does not wait for the codes
     load_codes(cv0, 0);
@@ -475,9 +485,11 @@ __global__ __launch_bounds__(256) void qmm_n_m1_mfma(const QmmN1Args a) {
 
     // A operand: lane row m = lane % 16 (0 = hi, 1 = lo, others zero), lane block g.
     const int g = lane >> 4, m = lane & 15;
-    const int gi_w = (n0 + 32 * wave) / GS - g0;  // this wave's group in the tile
+    const int gi_w = (n0 + (C / NW) * wave) / GS - g0;  // this wave's group in the tile
     const uint32_t a_off = m < 2 ? uint32_t(((gi_w * 2 + m) * RC + 16 * g) * 2) : 0u;
-    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    f32x4 acc[SPW];
+#pragma unroll
+    for (int s2 = 0; s2 < SPW; s2++) acc[s2] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto compute = [&](int c, int buf) __attribute__((always_inline)) {
         const int crows = rows - c * RC;
 #pragma unroll
@@ -487,8 +499,8 @@ __global__ __launch_bounds__(256) void qmm_n_m1_mfma(const QmmN1Args a) {
             const bf16x8 aa = m < 2 ? *reinterpret_cast<const bf16x8*>(al[buf] + a_off + rd * 128) : za;
             const bf16x8 ab = m < 2 ? *reinterpret_cast<const bf16x8*>(al[buf] + a_off + rd * 128 + 16) : za;
 #pragma unroll
-            for (int s2 = 0; s2 < 2; s2++) {
-                const int sl = 2 * wave + s2;
+            for (int s2 = 0; s2 < SPW; s2++) {
+                const int sl = SPW * wave + s2;
                 const qn_v2i v = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
                     (__attribute__((address_space(3))) qn_v2i*)(&wl[buf][(64 * rd + 16 * g + m) * kQnmWStride + sl * 8]));
                 acc[s2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aa, qnm_unpack(uint32_t(v.x)), acc[s2], 0, 0, 0);
@@ -526,10 +538,10 @@ __global__ __launch_bounds__(256) void qmm_n_m1_mfma(const QmmN1Args a) {
     if (lane < 16) {
         float sx = 0.f, sb = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; w++) sx += sums[0][w][gi_w], sb += sums[1][w][gi_w];
+        for (int w = 0; w < NW; w++) sx += sums[0][w][gi_w], sb += sums[1][w][gi_w];
         const float corr = fmaf(-128.f, sx, sb);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) colv[(2 * wave + s2) * 16 + lane] = (acc[s2][0] + acc[s2][1]) + corr;
+        for (int s2 = 0; s2 < SPW; s2++) colv[(SPW * wave + s2) * 16 + lane] = (acc[s2][0] + acc[s2][1]) + corr;
     }
     __syncthreads();
     const int n = n0 + tid;
@@ -678,28 +690,28 @@ bool launch_qmm_n_m1(int bits, int scale_dtype, uint16_t* y, const uint16_t* x, 
             else if (fit < per_launch) per_launch = fit;
         }
     }
-    auto go = [&](auto kernel) {
+    auto go = [&](auto kernel, int threads) {
         for (int64_t b0 = 0; b0 < batch; b0 += per_launch) {
             const unsigned nb = unsigned(batch - b0 < per_launch ? batch - b0 : per_launch);
             a.b0 = b0;
-            kernel<<<dim3(unsigned(ctiles * splits), 1, nb), dim3(256), 0, st>>>(a);
+            kernel<<<dim3(unsigned(ctiles * splits), 1, nb), dim3(threads), 0, st>>>(a);
         }
     };
     auto with_gs = [&](auto st_tag) {
         typedef decltype(st_tag) T;
-        if (gs == 32) go(qmm_n_m1_mfma<T, 32>);
-        else if (gs == 64) go(qmm_n_m1_mfma<T, 64>);
-        else go(qmm_n_m1_mfma<T, 128>);
+        if (gs == 32) go(qmm_n_m1_mfma<T, 32>, kQnmThreads);
+        else if (gs == 64) go(qmm_n_m1_mfma<T, 64>, kQnmThreads);
+        else go(qmm_n_m1_mfma<T, 128>, kQnmThreads);
     };
     if (mfma) {
         if (scale_dtype == EQ_DTYPE_BF16) with_gs(BF16T{});
         else with_gs(F16T{});
     } else if (bits == 4) {
-        if (scale_dtype == EQ_DTYPE_BF16) go(qmm_n_m1<4, BF16T>);
-        else go(qmm_n_m1<4, F16T>);
+        if (scale_dtype == EQ_DTYPE_BF16) go(qmm_n_m1<4, BF16T>, 256);
+        else go(qmm_n_m1<4, F16T>, 256);
     } else {
-        if (scale_dtype == EQ_DTYPE_BF16) go(qmm_n_m1<8, BF16T>);
-        else go(qmm_n_m1<8, F16T>);
+        if (scale_dtype == EQ_DTYPE_BF16) go(qmm_n_m1<8, BF16T>, 256);
+        else go(qmm_n_m1<8, F16T>, 256);
     }
     if (splits > 1 && !a.counters) {
         const int64_t mn = batch * int64_t(N);
