@@ -1,9 +1,10 @@
 // GGML block dequant and convert on gfx950.
 //
-// Restates, per block and bit for bit, eredu-gguf/src/convert.rs:318-465
-// (convert_affine for Q4_0 / Q8_0 / Q4_K), AffineTensor::dequantize
-// (convert.rs:81-101) and the native decoders of
-// safemlx/src/native_quantization.rs:3445-3469 (Q4_K) and :3539-3542 (Q8_0).
+// Restates, per block and bit for bit, eredu-gguf/src/convert.rs:318-564
+// (convert_affine for Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_0 / Q2_K / Q3_K / Q4_K /
+// Q5_K / Q6_K), AffineTensor::dequantize (convert.rs:81-101) and the native
+// decoders of safemlx/src/native_quantization.rs:3445-3469 (Q4_K), :3499-3509
+// (Q5_1) and :3539-3542 (Q8_0).
 //
 // All kernels are HBM-bound byte work.  Q4_0 (18 B) and Q8_0 (34 B) blocks are
 // not 4-byte aligned, so a workgroup stages its 256 blocks through LDS with
@@ -39,12 +40,13 @@ __device__ __forceinline__ uint32_t hi_nibbles(uint32_t x) { return lo_nibbles(x
 // Full workgroups on a 16-byte-aligned payload use 16-byte loads; a ragged
 // tail uses 2-byte loads (block sizes here are even), so nothing past the
 // payload is ever read.
-template <int BYTES>
+template <int BYTES, int NB = kBlocksPerWG>
 __device__ __forceinline__ void stage_blocks(uint16_t* lds, const uint8_t* raw, int64_t blk0, int nb,
                                              bool vec_ok) {
+    static_assert(NB * BYTES % 16 == 0, "a workgroup's blocks must start 16-byte aligned");
     const uint8_t* src = raw + blk0 * BYTES;
-    if (vec_ok && nb == kBlocksPerWG) {
-        constexpr int kVec = kBlocksPerWG * BYTES / 16;
+    if (vec_ok && nb == NB) {
+        constexpr int kVec = NB * BYTES / 16;
         const uint4* s4 = reinterpret_cast<const uint4*>(src);
         uint4* d4 = reinterpret_cast<uint4*>(lds);
         for (int i = threadIdx.x; i < kVec; i += blockDim.x) d4[i] = s4[i];
@@ -311,6 +313,193 @@ __global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw
         for (int i = 0; i < 8; i++) v[i] = scale * float(((i < 4 ? q0 : q1) >> (8 * (i & 3) + sh)) & 15u) + bias;
     }
     store8<OUT>(out, (idx >> 2) * 32 + 8 * c, v);
+}
+
+// --------------------------- Q4_1 / Q5_0 / Q5_1 / Q2_K / Q3_K / Q5_K / Q6_K
+//
+// Blocks of 20 / 22 / 24 / 84 / 110 / 176 / 210 bytes, staged through LDS
+// like Q4_0.  The unit of work is 32 consecutive values: a whole block of
+// the 32-value types, an eighth of a 256-value superblock.  A unit packs to
+// exactly `bits` u32 words and holds one (group 32) or two (group 16)
+// affine groups, so each thread of the convert writes whole words and whole
+// groups, and each quarter-lane of the dense decode writes 8 values of one
+// group.
+
+template <int T>
+struct KQuant;
+template <> struct KQuant<EQ_GGML_Q4_1> { static constexpr int bytes = 20, units = 1, bits = 4, gs = 32; };
+template <> struct KQuant<EQ_GGML_Q5_0> { static constexpr int bytes = 22, units = 1, bits = 5, gs = 32; };
+template <> struct KQuant<EQ_GGML_Q5_1> { static constexpr int bytes = 24, units = 1, bits = 5, gs = 32; };
+template <> struct KQuant<EQ_GGML_Q2_K> { static constexpr int bytes = 84, units = 8, bits = 2, gs = 16; };
+template <> struct KQuant<EQ_GGML_Q3_K> { static constexpr int bytes = 110, units = 8, bits = 3, gs = 16; };
+template <> struct KQuant<EQ_GGML_Q5_K> { static constexpr int bytes = 176, units = 8, bits = 5, gs = 32; };
+template <> struct KQuant<EQ_GGML_Q6_K> { static constexpr int bytes = 210, units = 8, bits = 6, gs = 16; };
+
+// f16 field at byte offset o of a block in LDS.
+template <bool BIG>
+__device__ __forceinline__ uint32_t lds_half(const uint8_t* b, int o) {
+    return BIG ? (uint32_t(b[o]) << 8) | b[o + 1] : uint32_t(b[o]) | (uint32_t(b[o + 1]) << 8);
+}
+
+// Code of value i (0..31) of unit u of a block.
+template <int T, bool BIG>
+__device__ __forceinline__ uint32_t kq_code(const uint8_t* b, int u, int i) {
+    if constexpr (T == EQ_GGML_Q4_1) {
+        // low nibbles of bytes 4..20 are values 0..15, high nibbles 16..31 (convert.rs:367-370)
+        return (b[4 + (i & 15)] >> ((i >> 4) * 4)) & 15u;
+    } else if constexpr (T == EQ_GGML_Q5_0 || T == EQ_GGML_Q5_1) {
+        // nibble as Q4_1 plus bit i of the u32 at 2 (Q5_0) or 4 (Q5_1) (convert.rs:553-562)
+        constexpr int qh = T == EQ_GGML_Q5_0 ? 2 : 4, qs = qh + 4;
+        const uint32_t lo = (b[qs + (i & 15)] >> ((i >> 4) * 4)) & 15u;
+        const uint32_t hi = (b[qh + (BIG ? 3 - (i >> 3) : (i >> 3))] >> (i & 7)) & 1u;
+        return lo | (hi << 4);
+    } else if constexpr (T == EQ_GGML_Q2_K) {
+        // group g = 2u + i/16 takes 2 bits at shift 2 (g % 8) / 2 of byte
+        // 16 + (g / 8) 32 + (g % 2) 16 + i % 16 (convert.rs:501-505)
+        return (b[16 + (u >> 2) * 32 + i] >> ((u & 3) * 2)) & 3u;
+    } else if constexpr (T == EQ_GGML_Q3_K) {
+        // as Q2_K at byte 32, plus bit g / 2 = u of hm[i] as bit 2 (convert.rs:531-539)
+        const uint32_t lo = (b[32 + (u >> 2) * 32 + i] >> ((u & 3) * 2)) & 3u;
+        return lo | (((uint32_t(b[i]) >> u) & 1u) << 2);
+    } else if constexpr (T == EQ_GGML_Q5_K) {
+        // unit = group g: nibble g % 2 of qs[(g / 2) 32 + i] at 48, bit g of qh[i] at 16 (convert.rs:453-461)
+        const uint32_t lo = (b[48 + (u >> 1) * 32 + i] >> ((u & 1) * 4)) & 15u;
+        return lo | (((uint32_t(b[16 + i]) >> u) & 1u) << 4);
+    } else {
+        // Q6_K: unit u is value run k = u % 4 of half h = u / 4: nibble k / 2 of
+        // ql[h 64 + (k % 2) 32 + i], bits 2k..2k+1 of qh[128 + h 32 + i] (convert.rs:472-477)
+        const int h = u >> 2, k = u & 3;
+        const uint32_t lo = (b[h * 64 + (k & 1) * 32 + i] >> ((k >> 1) * 4)) & 15u;
+        return lo | (((uint32_t(b[128 + h * 32 + i]) >> (2 * k)) & 3u) << 4);
+    }
+}
+
+// 6-bit scale and min of group g from the 12 scale bytes at s (scale_min,
+// convert.rs:429-438), as q4k_scale_min but from LDS bytes.
+__device__ __forceinline__ void scale_min_bytes(const uint8_t* s, int g, uint32_t& sc, uint32_t& m) {
+    if (g < 4) {
+        sc = s[g] & 63u;
+        m = s[g + 4] & 63u;
+    } else {
+        sc = (s[g + 4] & 15u) | ((uint32_t(s[g - 4]) >> 6) << 4);
+        m = (uint32_t(s[g + 4]) >> 4) | ((uint32_t(s[g]) >> 6) << 4);
+    }
+}
+
+// f16 bits of the scale and the bias of group g of a block.
+template <int T, bool BIG>
+__device__ __forceinline__ void kq_group(const uint8_t* b, int g, uint32_t& sb, uint32_t& bb) {
+    if constexpr (T == EQ_GGML_Q4_1 || T == EQ_GGML_Q5_1) {
+        sb = lds_half<BIG>(b, 0);  // d and m as stored (convert.rs:364-365, 548-551)
+        bb = lds_half<BIG>(b, 2);
+    } else if constexpr (T == EQ_GGML_Q5_0) {
+        sb = lds_half<BIG>(b, 0);
+        bb = f32_to_f16_bits(-16.0f * f16_bits_to_f32(sb));  // convert.rs:549
+    } else if constexpr (T == EQ_GGML_Q2_K) {
+        const float d = f16_bits_to_f32(lds_half<BIG>(b, 80)), dm = f16_bits_to_f32(lds_half<BIG>(b, 82));
+        sb = f32_to_f16_bits(d * float(b[g] & 15u));  // convert.rs:496-499
+        bb = f32_to_f16_bits(-dm * float(uint32_t(b[g]) >> 4));
+    } else if constexpr (T == EQ_GGML_Q3_K) {
+        // 6-bit code: low 4 bits from byte 96 + g % 8 (nibble g / 8), high 2 bits
+        // from byte 104 + g % 4 (bits 2 (g / 4)) (convert.rs:514-520)
+        const uint32_t enc = ((uint32_t(b[96 + (g & 7)]) >> (4 * (g >> 3))) & 15u) |
+                             (((uint32_t(b[104 + (g & 3)]) >> (2 * (g >> 2))) & 3u) << 4);
+        const float sc = f16_bits_to_f32(lds_half<BIG>(b, 108)) * float(int(enc) - 32);
+        sb = f32_to_f16_bits(sc);  // convert.rs:524-526
+        bb = f32_to_f16_bits(-4.0f * sc);
+    } else if constexpr (T == EQ_GGML_Q5_K) {
+        uint32_t sc, m;
+        scale_min_bytes(b + 4, g, sc, m);
+        sb = f32_to_f16_bits(f16_bits_to_f32(lds_half<BIG>(b, 0)) * float(sc));  // convert.rs:449-450
+        bb = f32_to_f16_bits(-f16_bits_to_f32(lds_half<BIG>(b, 2)) * float(m));
+    } else {
+        // Q6_K: int8 scale byte 192 + g, d at 208 (convert.rs:469, 479-482)
+        const float sc = f16_bits_to_f32(lds_half<BIG>(b, 208)) * float(int8_t(b[192 + g]));
+        sb = f32_to_f16_bits(sc);
+        bb = f32_to_f16_bits(-32.0f * sc);
+    }
+}
+
+// Stores the `BITS` words of one unit at w (w is 4 * BITS-byte aligned times
+// the unit index from a 16-byte-aligned base).
+template <int BITS>
+__device__ __forceinline__ void store_unit(uint32_t* w, const uint32_t* wd) {
+    if constexpr (BITS == 4) {
+        *reinterpret_cast<uint4*>(w) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    } else if constexpr (BITS == 2 || BITS == 6) {
+#pragma unroll
+        for (int j = 0; j < BITS; j += 2) *reinterpret_cast<uint2*>(w + j) = make_uint2(wd[j], wd[j + 1]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < BITS; j++) w[j] = wd[j];
+    }
+}
+
+template <int T, bool BIG>
+__global__ __launch_bounds__(256) void kq_to_affine(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
+                                                    uint32_t* __restrict__ w, uint16_t* __restrict__ s,
+                                                    uint16_t* __restrict__ bias) {
+    using P = KQuant<T>;
+    constexpr int NB = 256 / P::units, G = 32 / P::gs;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[NB * P::bytes / 2];
+    const int64_t blk0 = int64_t(blockIdx.x) * NB;
+    const int nb = int(min<int64_t>(NB, nblocks - blk0));
+    stage_blocks<P::bytes, NB>(lds, raw, blk0, nb, vec_ok);
+    const int lb = threadIdx.x / P::units, u = threadIdx.x % P::units;
+    if (lb >= nb) return;
+    const uint8_t* b = reinterpret_cast<const uint8_t*>(lds) + lb * P::bytes;
+    // LSB-first pack of the unit's 32 codes (convert.rs:413-427); offsets are
+    // constants once the loop is unrolled
+    uint32_t wd[P::bits];
+#pragma unroll
+    for (int j = 0; j < P::bits; j++) wd[j] = 0;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const uint32_t c = kq_code<T, BIG>(b, u, i);
+        const int off = i * P::bits, sh = off & 31;
+        wd[off >> 5] |= c << sh;
+        if (sh + P::bits > 32) wd[(off >> 5) + 1] |= c >> (32 - sh);
+    }
+    const int64_t unit = (blk0 + lb) * P::units + u;
+    store_unit<P::bits>(w + unit * P::bits, wd);
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        uint32_t sb, bb;
+        kq_group<T, BIG>(b, u * G + j, sb, bb);
+        s[unit * G + j] = uint16_t(sb);
+        bias[unit * G + j] = uint16_t(bb);
+    }
+}
+
+// Dense decode by the affine route, f32(scale) * code + f32(bias)
+// (convert.rs:81-101); for these types it is also the native definition
+// (Q5_1's native decoder d * q + m uses the same unrounded d and m,
+// native_quantization.rs:3499-3509).  Lane quarter c of unit lu decodes values
+// [8c, 8c + 8).
+template <int T, bool BIG, typename OUT>
+__global__ __launch_bounds__(256) void kq_dense(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
+                                                typename OUT::storage* __restrict__ out) {
+    using P = KQuant<T>;
+    constexpr int NB = 256 / P::units;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[NB * P::bytes / 2];
+    const int64_t blk0 = int64_t(blockIdx.x) * NB;
+    const int nb = int(min<int64_t>(NB, nblocks - blk0));
+    stage_blocks<P::bytes, NB>(lds, raw, blk0, nb, vec_ok);
+    const int c = threadIdx.x & 3;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int lu = k * 64 + (threadIdx.x >> 2);
+        const int lb = lu / P::units, u = lu % P::units;
+        if (lb >= nb) break;
+        const uint8_t* b = reinterpret_cast<const uint8_t*>(lds) + lb * P::bytes;
+        uint32_t sb, bb;
+        kq_group<T, BIG>(b, (u * 32 + 8 * c) / P::gs, sb, bb);
+        const float scale = f16_bits_to_f32(sb), bv = f16_bits_to_f32(bb);
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = scale * float(kq_code<T, BIG>(b, u, 8 * c + i)) + bv;
+        store8<OUT>(out, ((blk0 + lb) * P::units + u) * 32 + 8 * c, v);
+    }
 }
 
 // ------------------------------------------------- native linear (M small)
@@ -803,14 +992,21 @@ __global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, con
 }
 
 struct Geometry {
-    int values, bytes, bits;
+    int values, bytes, bits, gs;
 };
 
 bool geometry(int type, Geometry& g) {
     switch (type) {  // eredu-gguf/src/format.rs:368-400, convert.rs:142-152
-    case EQ_GGML_Q4_0: g = {32, 18, 4}; return true;
-    case EQ_GGML_Q8_0: g = {32, 34, 8}; return true;
-    case EQ_GGML_Q4_K: g = {256, 144, 4}; return true;
+    case EQ_GGML_Q4_0: g = {32, 18, 4, 32}; return true;
+    case EQ_GGML_Q4_1: g = {32, 20, 4, 32}; return true;
+    case EQ_GGML_Q5_0: g = {32, 22, 5, 32}; return true;
+    case EQ_GGML_Q5_1: g = {32, 24, 5, 32}; return true;
+    case EQ_GGML_Q8_0: g = {32, 34, 8, 32}; return true;
+    case EQ_GGML_Q2_K: g = {256, 84, 2, 16}; return true;
+    case EQ_GGML_Q3_K: g = {256, 110, 3, 16}; return true;
+    case EQ_GGML_Q4_K: g = {256, 144, 4, 32}; return true;
+    case EQ_GGML_Q5_K: g = {256, 176, 5, 32}; return true;
+    case EQ_GGML_Q6_K: g = {256, 210, 6, 16}; return true;
     default: return false;
     }
 }
@@ -819,7 +1015,8 @@ bool geometry(int type, Geometry& g) {
 int validate(const uint8_t* raw, int64_t raw_len, int type, int64_t rows, int64_t cols, int endian,
              Geometry& geo, int64_t& nblocks) {
     if (!geometry(type, geo)) {
-        set_error("unsupported GGML tensor type " + std::to_string(type) + " (device path covers Q4_0, Q8_0, Q4_K)");
+        set_error("unsupported GGML tensor type " + std::to_string(type) +
+                  " (device path covers Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)");
         return 1;
     }
     if (endian != EQ_ENDIAN_LITTLE && endian != EQ_ENDIAN_BIG) {
@@ -830,8 +1027,8 @@ int validate(const uint8_t* raw, int64_t raw_len, int type, int64_t rows, int64_
         set_error("quantized scalar is invalid: rows and cols must be positive");
         return 1;
     }
-    if (cols % 32 != 0) {
-        set_error("last dimension is not divisible by group size 32");
+    if (cols % geo.gs != 0) {
+        set_error("last dimension is not divisible by group size " + std::to_string(geo.gs));
         return 1;
     }
     if (cols % geo.values != 0) {
@@ -854,6 +1051,29 @@ int validate(const uint8_t* raw, int64_t raw_len, int type, int64_t rows, int64_
         return 1;
     }
     return 0;
+}
+
+// Calls f(type tag, byte-order tag) for the types of KQuant; false, calling
+// nothing, for the others.
+template <typename F>
+bool with_kq(int type, bool big, F&& f) {
+    auto go = [&](auto t) {
+        if (big)
+            f(t, std::true_type{});
+        else
+            f(t, std::false_type{});
+        return true;
+    };
+    switch (type) {
+    case EQ_GGML_Q4_1: return go(std::integral_constant<int, EQ_GGML_Q4_1>{});
+    case EQ_GGML_Q5_0: return go(std::integral_constant<int, EQ_GGML_Q5_0>{});
+    case EQ_GGML_Q5_1: return go(std::integral_constant<int, EQ_GGML_Q5_1>{});
+    case EQ_GGML_Q2_K: return go(std::integral_constant<int, EQ_GGML_Q2_K>{});
+    case EQ_GGML_Q3_K: return go(std::integral_constant<int, EQ_GGML_Q3_K>{});
+    case EQ_GGML_Q5_K: return go(std::integral_constant<int, EQ_GGML_Q5_K>{});
+    case EQ_GGML_Q6_K: return go(std::integral_constant<int, EQ_GGML_Q6_K>{});
+    default: return false;
+    }
 }
 
 }  // namespace
@@ -880,6 +1100,13 @@ extern "C" int eq_gguf_convert_affine(uint32_t* weights, uint16_t* scales, uint1
     const bool vec_ok = aligned(raw, 16);
     const bool big = endian == EQ_ENDIAN_BIG;
     uint4* w4 = reinterpret_cast<uint4*>(weights);
+    if (with_kq(ggml_type, big, [&](auto t, auto b) {
+            constexpr int T = decltype(t)::value;
+            constexpr int NB = 256 / KQuant<T>::units;
+            kq_to_affine<T, decltype(b)::value><<<dim3(unsigned((nblocks + NB - 1) / NB)), 256, 0, st>>>(
+                raw, nblocks, vec_ok, weights, scales, biases);
+        }))
+        return check_launch("gguf convert_affine");
     if (ggml_type == EQ_GGML_Q4_K) {
         const int64_t ngroups = nblocks * 8;
         const dim3 grid(unsigned((ngroups + 255) / 256));
@@ -908,6 +1135,13 @@ namespace {
 template <typename OUT>
 void launch_dense(int type, bool big, bool native, const uint8_t* raw, int64_t nblocks, bool vec_ok,
                   typename OUT::storage* out, hipStream_t st) {
+    if (with_kq(type, big, [&](auto t, auto b) {
+            constexpr int T = decltype(t)::value;
+            constexpr int NB = 256 / KQuant<T>::units;
+            kq_dense<T, decltype(b)::value, OUT><<<dim3(unsigned((nblocks + NB - 1) / NB)), 256, 0, st>>>(
+                raw, nblocks, vec_ok, out);
+        }))
+        return;
     if (type == EQ_GGML_Q4_K) {
         const int64_t nq = nblocks * 32;  // 8 groups x 4 quarters per superblock
         const dim3 grid(unsigned((nq + 255) / 256));

@@ -2,7 +2,8 @@
 
 Follows ``eredu-gguf/src/convert.rs`` (``convert_affine``, ``AffineTensor``)
 and ``eredu-gguf/src/format.rs`` (``GgmlType``, ``TensorDescriptor``,
-``Endian``) for the block types the device path covers: Q4_0, Q8_0 and Q4_K.
+``Endian``) for the block types the device path covers: Q4_0, Q4_1, Q5_0,
+Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K (every type with an affine form).
 The raw block payload is a uint8 tensor on the GPU (what a loader copies to
 the device); outputs are GPU tensors.  Conversion and dequantization run in
 the HIP library; there is no host path.
@@ -21,8 +22,9 @@ from ._native import EreduError, check
 
 class GgmlType(enum.IntEnum):
     """GGML tensor type codes (eredu-gguf/src/format.rs:295-365).  The device
-    path converts and executes Q4_0, Q8_0 and Q4_K; the rest are named so that
-    routing (``conversion_kind``) covers every code the container holds."""
+    path converts and dequantizes every type with an affine form and executes
+    Q4_K and Q8_0 blocks natively; the rest are named so that routing
+    (``conversion_kind``) covers every code the container holds."""
 
     F32 = 0
     F16 = 1
@@ -67,8 +69,9 @@ class GgmlType(enum.IntEnum):
         return self in (GgmlType.Q4K, GgmlType.Q5K, GgmlType.Q6K, GgmlType.Q5_1, GgmlType.Q8_0) or self.is_iq()
 
     def has_device_kernels(self) -> bool:
-        """Encodings this library converts and dequantizes (Q4_0, Q8_0, Q4_K)."""
-        return self in (GgmlType.Q4_0, GgmlType.Q8_0, GgmlType.Q4K)
+        """Encodings this library converts and dequantizes: those with an
+        affine form (convert.rs:142-152)."""
+        return affine_config(self) is not None
 
     def has_device_linear(self) -> bool:
         """Encodings this library multiplies straight from their blocks (eq_gguf_linear)."""
@@ -201,7 +204,8 @@ def _rows_cols(desc: TensorDescriptor):
 def _device_type(desc: TensorDescriptor) -> GgmlType:
     ty = ggml_type_from_code(int(desc.ggml_type))
     if not ty.has_device_kernels():
-        raise EreduError(f"tensor '{desc.name}': GGML type {int(ty)} has no device kernels (Q4_0, Q8_0, Q4_K)")
+        raise EreduError(f"tensor '{desc.name}': GGML type {int(ty)} has no device kernels "
+                         f"(types with an affine form only)")
     return ty
 
 
@@ -214,7 +218,7 @@ def _check_raw(desc: TensorDescriptor, raw: torch.Tensor) -> None:
 
 def convert_affine(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little) -> AffineTensor:
     """GGML blocks -> MLX affine triple, byte-identical to
-    eredu_gguf::convert_affine (convert.rs:318-465); C ABI eq_gguf_convert_affine."""
+    eredu_gguf::convert_affine (convert.rs:318-564); C ABI eq_gguf_convert_affine."""
     ty = _device_type(desc)
     _check_raw(desc, raw)
     shape, rows, cols = _rows_cols(desc)
@@ -396,8 +400,9 @@ def convert(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.L
     """eredu_gguf's convert (convert.rs:276-313) on device payloads, routed by
     ``conversion_kind``: a DenseTensor (dense types), a NativeTensor (blocks
     kept as stored: little-endian Q4_K / Q8_0), an MxFp4Tensor (type 39), or
-    an AffineTensor (Q4_0 in either byte order, big-endian Q4_K / Q8_0).
-    Encodings without device kernels are refused with the type named."""
+    an AffineTensor (Q4_0, Q4_1, Q5_0, Q2_K, Q3_K in either byte order; the
+    natively executed types in big-endian files).  Encodings without device
+    kernels are refused with the type named."""
     if raw.dtype != torch.uint8 or not raw.is_cuda:
         raise EreduError("raw GGUF payload must be a uint8 tensor on the GPU")
     if raw.numel() != desc.byte_len:

@@ -31,15 +31,21 @@ typedef struct ihipStream_t* eq_stream_t;
 enum eq_dtype { EQ_DTYPE_F32 = 0, EQ_DTYPE_F16 = 1, EQ_DTYPE_BF16 = 2, EQ_DTYPE_U8 = 3 /* MXFP4 scales */ };
 
 /* GGML block types handled on the device (codes of eredu-gguf/src/format.rs:297-330). */
-enum eq_ggml_type { EQ_GGML_Q4_0 = 2, EQ_GGML_Q8_0 = 8, EQ_GGML_Q4_K = 12 };
+enum eq_ggml_type {
+    EQ_GGML_Q4_0 = 2, EQ_GGML_Q4_1 = 3, EQ_GGML_Q5_0 = 6, EQ_GGML_Q5_1 = 7, EQ_GGML_Q8_0 = 8,
+    EQ_GGML_Q2_K = 10, EQ_GGML_Q3_K = 11, EQ_GGML_Q4_K = 12, EQ_GGML_Q5_K = 13, EQ_GGML_Q6_K = 14
+};
 
 /* Byte order of multi-byte block fields (eredu-gguf/src/format.rs:5-23 Endian). */
 enum eq_endian { EQ_ENDIAN_LITTLE = 0, EQ_ENDIAN_BIG = 1 };
 
 /* Which dense-dequant definition to follow for GGML blocks:
  * AFFINE = convert_affine then AffineTensor::dequantize (eredu-gguf/src/convert.rs:43-56,81-101);
- * NATIVE = the checkpoint-native decoders (safemlx/src/native_quantization.rs:3445-3469,3539-3542).
- * The two differ only for Q4_K (f16 rounding of d*sc and -dmin*m). */
+ * NATIVE = the checkpoint-native decoders (safemlx/src/native_quantization.rs:3445-3469,
+ * 3499-3509,3539-3542), the affine route for types without one (Q5_K and Q6_K dequantize
+ * through IQuantTensor::dequantize_f32, native_quantization.rs:792-830).
+ * The two differ only for Q4_K (f16 rounding of d*sc and -dmin*m) and for Q8_0 when
+ * -128 d overflows f16. */
 enum eq_dequant_definition { EQ_DEQUANT_AFFINE = 0, EQ_DEQUANT_NATIVE = 1 };
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -118,12 +124,14 @@ int eq_dequantize(void* out, const uint32_t* w, const void* scales, const void* 
 
 /*
  * GGML blocks -> MLX affine (u32 codes, f16 scale bits, f16 bias bits),
- * byte-identical to eredu_gguf::convert_affine (eredu-gguf/src/convert.rs:318-465)
- * for Q4_0 (bits 4), Q8_0 (bits 8) and Q4_K (bits 4), all group 32.
- * `rows` x `cols` is the MLX shape (GGUF dims reversed, format.rs:449-452);
- * raw holds rows*cols/block_values blocks (raw_len bytes, checked like
- * convert.rs:319-324).  Outputs: weights [rows, cols*bits/32],
- * scales/biases [rows, cols/32].
+ * byte-identical to eredu_gguf::convert_affine (eredu-gguf/src/convert.rs:318-564)
+ * with (bits, group size) of convert.rs:142-152: Q2_K (2, 16), Q3_K (3, 16),
+ * Q4_0 / Q4_1 / Q4_K (4, 32), Q5_0 / Q5_1 / Q5_K (5, 32), Q6_K (6, 16),
+ * Q8_0 (8, 32).  `rows` x `cols` is the MLX shape (GGUF dims reversed,
+ * format.rs:449-452); cols is a multiple of the block length (32, or 256 for
+ * the K types); raw holds rows*cols/block_values blocks (raw_len bytes,
+ * checked like convert.rs:319-324).  Outputs: weights [rows, cols*bits/32],
+ * scales/biases [rows, cols/group_size].
  */
 int eq_gguf_convert_affine(uint32_t* weights, uint16_t* scales, uint16_t* biases,
                            const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t rows,

@@ -13,10 +13,17 @@
  *                                    f16 patterns and 2^20 random f32s.
  *   or_f32_to_bf16                   pinned: torch bfloat16 RNE conversion.
  *   or_gguf_convert_affine           pinned: mlx-v0.32.0.oracle fixture rows
- *                                    (Q4_0, Q8_0, Q4_K byte-exact) and the
- *                                    boundary blocks of eredu-gguf/tests/oracle.rs.
+ *                                    (Q4_0, Q4_1, Q8_0, Q2_K, Q3_K, Q4_K,
+ *                                    Q5_K, Q6_K byte-exact), the boundary
+ *                                    blocks and Q5_0/Q5_1 repack tests of
+ *                                    eredu-gguf/tests/oracle.rs, and closed
+ *                                    forms from ggml's published decoders
+ *                                    (tests/test_oracle_kquants.py).
  *   or_gguf_dequant_f32 (affine)     pinned: fixture "dequantized" column
- *                                    (exact after f16 rounding).
+ *                                    (exact after f16 rounding; Q6_K within
+ *                                    the reference test's tolerance and exact
+ *                                    under MLX's two-rounding f16 arithmetic),
+ *                                    the Q5_0/Q5_1 rows' f16 weights (exact).
  *   or_gguf_dequant_f32 (native)     pinned: closed form d*sc*q - dmin*m in
  *                                    f64, and the <=1e-6 native-vs-affine
  *                                    tests' sample blocks.
@@ -111,11 +118,20 @@ static float load_scalar(const void* p, int dtype, int64_t i) {
 
 /* ----------------------------------------------------------- GGUF types */
 
-enum { OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q4_K = 12 };
+enum {
+    OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8,
+    OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14
+};
 
 static uint16_t rd16(const uint8_t* b, int big_endian) {
     /* eredu-gguf/src/format.rs:12-17 Endian::u16 */
     return big_endian ? (uint16_t)((b[0] << 8) | b[1]) : (uint16_t)(b[0] | (b[1] << 8));
+}
+
+static uint32_t rd32(const uint8_t* b, int big_endian) {
+    /* eredu-gguf/src/format.rs:18-23 Endian::u32 (the Q5_0/Q5_1 high-bit word) */
+    return big_endian ? ((uint32_t)b[0] << 24) | ((uint32_t)b[1] << 16) | ((uint32_t)b[2] << 8) | b[3]
+                      : (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) | ((uint32_t)b[3] << 24);
 }
 
 /* LSB-first bit packing of `n` codes of `bits` each into u32 words
@@ -144,24 +160,160 @@ static void q4k_scale_min(const uint8_t* s, int i, uint8_t* sc, uint8_t* m) {
 int or_gguf_block_geometry(int type, int* values, int* bytes) {
     switch (type) {
     case OR_Q4_0: *values = 32; *bytes = 18; return 0;
+    case OR_Q4_1: *values = 32; *bytes = 20; return 0;
+    case OR_Q5_0: *values = 32; *bytes = 22; return 0;
+    case OR_Q5_1: *values = 32; *bytes = 24; return 0;
     case OR_Q8_0: *values = 32; *bytes = 34; return 0;
+    case OR_Q2_K: *values = 256; *bytes = 84; return 0;
+    case OR_Q3_K: *values = 256; *bytes = 110; return 0;
     case OR_Q4_K: *values = 256; *bytes = 144; return 0;
+    case OR_Q5_K: *values = 256; *bytes = 176; return 0;
+    case OR_Q6_K: *values = 256; *bytes = 210; return 0;
+    default: return 1;
+    }
+}
+
+/* (bits, group size) of the affine form (eredu-gguf/src/convert.rs:142-152). */
+int or_gguf_affine_config(int type, int* bits, int* gs) {
+    switch (type) {
+    case OR_Q2_K: *bits = 2; *gs = 16; return 0;
+    case OR_Q3_K: *bits = 3; *gs = 16; return 0;
+    case OR_Q4_0: case OR_Q4_1: case OR_Q4_K: *bits = 4; *gs = 32; return 0;
+    case OR_Q5_0: case OR_Q5_1: case OR_Q5_K: *bits = 5; *gs = 32; return 0;
+    case OR_Q6_K: *bits = 6; *gs = 16; return 0;
+    case OR_Q8_0: *bits = 8; *gs = 32; return 0;
     default: return 1;
     }
 }
 
 /*
- * GGML blocks -> MLX affine (u32 codes, f16 scales, f16 biases), group 32.
+ * One block of the types added after Q4_0/Q8_0/Q4_K: its codes (in value
+ * order) and the f16 scale/bias bits of each group.  The whole block is then
+ * packed as one LSB-first stream; every group of these types ends on a word
+ * boundary except Q3_K's, and convert.rs packs Q3_K per block too.
+ *   Q4_1  convert.rs:362-373  scale = d, bias = m (raw halves), nibbles at 4
+ *   Q5_0  convert.rs:544-564  scale = d, bias = f16(-16 d), qh u32 at 2, qs at 6
+ *   Q5_1  convert.rs:544-564  scale = d, bias = m, qh u32 at 4, qs at 8
+ *   Q5_K  convert.rs:439-465  as Q4_K + bit g of qh[i] (b[16..48]) as bit 4,
+ *                             qs at 48
+ *   Q6_K  convert.rs:467-489  two 128-value halves: ql (64 B), qh (32 B),
+ *                             int8 scales at 192 + 8 half; d at 208;
+ *                             scale = f16(d sc), bias = f16(-32 d sc)
+ *   Q2_K  convert.rs:491-508  scale byte g: low nibble * d, high nibble * dmin
+ *                             (bias negated); d at 80, dmin at 82
+ *   Q3_K  convert.rs:510-542  6-bit signed scales (enc - 32) from 12 bytes at 96,
+ *                             bias = f16(-4 d sc); high bit from hm; d at 108
+ */
+static void kquant_block(int type, int be, const uint8_t* p, uint8_t* codes, uint16_t* s, uint16_t* b) {
+    if (type == OR_Q4_1) {
+        s[0] = rd16(p, be);
+        b[0] = rd16(p + 2, be);
+        for (int i = 0; i < 16; i++) {
+            codes[i] = p[4 + i] & 15;
+            codes[16 + i] = p[4 + i] >> 4;
+        }
+    } else if (type == OR_Q5_0 || type == OR_Q5_1) {
+        const int q50 = type == OR_Q5_0;
+        uint16_t d = rd16(p, be);
+        s[0] = d;
+        b[0] = q50 ? or_f32_to_f16(-16.0f * or_f16_to_f32(d)) : rd16(p + 2, be);
+        uint32_t qh = rd32(p + (q50 ? 2 : 4), be);
+        const uint8_t* qs = p + (q50 ? 6 : 8);
+        for (int j = 0; j < 16; j++) {
+            codes[j] = (uint8_t)((qs[j] & 15) | (((qh >> j) & 1) << 4));
+            codes[j + 16] = (uint8_t)((qs[j] >> 4) | (((qh >> (j + 16)) & 1) << 4));
+        }
+    } else if (type == OR_Q5_K) {
+        float d = or_f16_to_f32(rd16(p, be));
+        float dm = or_f16_to_f32(rd16(p + 2, be));
+        const uint8_t* qh = p + 16;
+        const uint8_t* qs = p + 48;
+        for (int g = 0; g < 8; g++) {
+            uint8_t sc, m;
+            q4k_scale_min(p + 4, g, &sc, &m);
+            s[g] = or_f32_to_f16(d * (float)sc);
+            b[g] = or_f32_to_f16(-dm * (float)m);
+            for (int i = 0; i < 32; i++) {
+                uint8_t q = qs[(g / 2) * 32 + i];
+                uint8_t lo = (g % 2 == 0) ? (q & 15) : (q >> 4);
+                codes[g * 32 + i] = (uint8_t)(lo | ((qh[i] >> g) & 1) << 4);
+            }
+        }
+    } else if (type == OR_Q6_K) {
+        float d = or_f16_to_f32(rd16(p + 208, be));
+        for (int half = 0; half < 2; half++) {
+            const uint8_t* ql = p + half * 64;
+            const uint8_t* qh = p + 128 + half * 32;
+            uint8_t* v = codes + half * 128;
+            for (int i = 0; i < 32; i++) {
+                v[i] = (uint8_t)((ql[i] & 15) | ((qh[i] & 3) << 4));
+                v[i + 32] = (uint8_t)((ql[i + 32] & 15) | (((qh[i] >> 2) & 3) << 4));
+                v[i + 64] = (uint8_t)((ql[i] >> 4) | (((qh[i] >> 4) & 3) << 4));
+                v[i + 96] = (uint8_t)((ql[i + 32] >> 4) | (((qh[i] >> 6) & 3) << 4));
+            }
+            for (int g = 0; g < 8; g++) {
+                float sc = d * (float)(int8_t)p[192 + half * 8 + g];
+                s[half * 8 + g] = or_f32_to_f16(sc);
+                b[half * 8 + g] = or_f32_to_f16(-32.0f * sc);
+            }
+        }
+    } else if (type == OR_Q2_K) {
+        float d = or_f16_to_f32(rd16(p + 80, be));
+        float dm = or_f16_to_f32(rd16(p + 82, be));
+        for (int g = 0; g < 16; g++) {
+            s[g] = or_f32_to_f16(d * (float)(p[g] & 15));
+            b[g] = or_f32_to_f16(-dm * (float)(p[g] >> 4));
+            int qo = (g / 8) * 32 + (g % 2) * 16, shift = ((g % 8) / 2) * 2;
+            for (int i = 0; i < 16; i++) codes[g * 16 + i] = (p[16 + qo + i] >> shift) & 3;
+        }
+    } else { /* OR_Q3_K */
+        const uint8_t* hm = p;
+        const uint8_t* qs = p + 32;
+        const uint8_t* src = p + 96;
+        uint8_t enc[16];
+        for (int i = 0; i < 4; i++) {
+            enc[i] = (uint8_t)((src[i] & 15) | ((src[8 + i] & 3) << 4));
+            enc[4 + i] = (uint8_t)((src[4 + i] & 15) | (((src[8 + i] >> 2) & 3) << 4));
+            enc[8 + i] = (uint8_t)((src[i] >> 4) | (((src[8 + i] >> 4) & 3) << 4));
+            enc[12 + i] = (uint8_t)((src[4 + i] >> 4) | (((src[8 + i] >> 6) & 3) << 4));
+        }
+        float d = or_f16_to_f32(rd16(p + 108, be));
+        for (int g = 0; g < 16; g++) {
+            float sc = d * (float)((int)enc[g] - 32);
+            s[g] = or_f32_to_f16(sc);
+            b[g] = or_f32_to_f16(-4.0f * sc);
+            int qo = (g / 8) * 32 + (g % 2) * 16, shift = ((g % 8) / 2) * 2;
+            for (int i = 0; i < 16; i++)
+                codes[g * 16 + i] = (uint8_t)(((qs[qo + i] >> shift) & 3) |
+                                              ((hm[(g % 2) * 16 + i] >> (g / 2)) & 1) << 2);
+        }
+    }
+}
+
+/*
+ * GGML blocks -> MLX affine (u32 codes, f16 scales, f16 biases).
  * eredu-gguf/src/convert.rs:318-404 (`convert_affine`/`affine`):
  *   Q4_0  :349-361   scale = d, bias = f16(-8 d), codes lo nibbles then hi
  *   Q8_0  :377-385   scale = d, bias = f16(-128 d), codes = byte ^ 0x80, 8-bit
  *   Q4_K  :439-465   scale = f16(d sc), bias = f16(-dmin m), 8 groups of 32
- * Outputs per block: Q4_0 4 words/1 group, Q8_0 8 words/1 group,
- * Q4_K 32 words/8 groups.  Returns 0, or 1 for an unsupported type.
+ *   the others in kquant_block above.
+ * Outputs per block: values * bits / 32 words and values / group size groups
+ * (or_gguf_affine_config).  Returns 0, or 1 for an unsupported type.
  */
 int or_gguf_convert_affine(int type, int big_endian, const uint8_t* raw, int64_t nblocks,
                            uint32_t* w, uint16_t* s, uint16_t* b) {
-    uint8_t codes[32];
+    uint8_t codes[256];
+    int values, bytes, bits, gs;
+    if (or_gguf_block_geometry(type, &values, &bytes) || or_gguf_affine_config(type, &bits, &gs)) return 1;
+    if (type != OR_Q4_0 && type != OR_Q8_0 && type != OR_Q4_K) {
+        const int wpb = values * bits / 32, gpb = values / gs;
+        for (int64_t blk = 0; blk < nblocks; blk++) {
+            kquant_block(type, big_endian, raw + blk * bytes, codes, s + blk * gpb, b + blk * gpb);
+            memset(w + blk * wpb, 0, sizeof(uint32_t) * wpb);
+            pack_codes(codes, values, bits, w + blk * wpb);
+        }
+        return 0;
+    }
     for (int64_t blk = 0; blk < nblocks; blk++) {
         if (type == OR_Q4_0) {
             const uint8_t* p = raw + blk * 18;
@@ -241,9 +393,12 @@ void or_affine_dequant_f32(const uint32_t* w, const void* scales, const void* bi
  *   (eredu-gguf/src/convert.rs:43-56,81-101).
  * definition 1 ("native route"): safemlx/src/native_quantization.rs
  *   :3445-3469 decode_q4k_block   w = d*sc*q - dmin*m  (f32, left to right)
+ *   :3499-3509 decode_q5_1_block  w = d*q + m (equal to the affine route:
+ *                                 scale and bias are d and m unrounded)
  *   :3539-3542 decode_q8_0_block  w = d*int8(q)
- *   Q4_0 has no native decoder (format.rs:423-428); both definitions use the
- *   affine route for it.
+ *   Q4_0, Q4_1, Q5_0, Q2_K and Q3_K have no native form (format.rs:423-428)
+ *   and Q5_K / Q6_K dequantize through the affine form; both definitions use
+ *   the affine route for them.
  */
 int or_gguf_dequant_f32(int type, int big_endian, int definition, const uint8_t* raw, int64_t nblocks,
                         float* out) {
@@ -274,16 +429,32 @@ int or_gguf_dequant_f32(int type, int big_endian, int definition, const uint8_t*
         }
         return 0;
     }
-    int groups_per_block = values / 32;
-    int bits = type == OR_Q8_0 ? 8 : 4;
-    int words_per_block = values * bits / 32;
-    uint32_t* w = (uint32_t*)malloc(sizeof(uint32_t) * words_per_block);
-    uint16_t s[8], b[8];
+    if (definition == 1 && type == OR_Q5_1) {
+        for (int64_t blk = 0; blk < nblocks; blk++) {
+            const uint8_t* p = raw + blk * 24;
+            float d = or_f16_to_f32(rd16(p, big_endian));
+            float m = or_f16_to_f32(rd16(p + 2, big_endian));
+            uint32_t high = rd32(p + 4, big_endian);
+            for (int i = 0; i < 32; i++) {
+                uint8_t packed = p[8 + i % 16];
+                uint32_t q = (uint32_t)(i < 16 ? (packed & 15) : (packed >> 4)) | (((high >> i) & 1) << 4);
+                out[blk * 32 + i] = d * (float)q + m;
+            }
+        }
+        return 0;
+    }
+    /* Every other (type, definition): the affine route.  Q5_K and Q6_K have
+     * no CPU decoder of their own in the reference; their native dequantize
+     * is IQuantTensor::dequantize_f32 = convert_affine + dequantize
+     * (safemlx/src/native_quantization.rs:792-830, convert.rs:43-56). */
+    int bits, gs;
+    or_gguf_affine_config(type, &bits, &gs);
+    uint32_t w[64];
+    uint16_t s[16], b[16];
     for (int64_t blk = 0; blk < nblocks; blk++) {
         or_gguf_convert_affine(type, big_endian, raw + blk * bytes, 1, w, s, b);
-        or_affine_dequant_f32(w, s, b, OR_F16, groups_per_block, 32, 32, bits, out + blk * values);
+        or_affine_dequant_f32(w, s, b, OR_F16, 1, values, gs, bits, out + blk * values);
     }
-    free(w);
     return 0;
 }
 

@@ -31,9 +31,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "libeq_oracle.so")
 
 F32, F16, BF16 = 0, 1, 2
-Q4_0, Q8_0, Q4_K = 2, 8, 12
-BLOCK_GEOMETRY = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144)}  # format.rs:368-400
-AFFINE_CONFIG = {Q4_0: (4, 32), Q8_0: (8, 32), Q4_K: (4, 32)}  # convert.rs:142-152
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 2, 3, 6, 7, 8
+Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 10, 11, 12, 13, 14
+BLOCK_GEOMETRY = {Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q8_0: (32, 34),
+                  Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176),
+                  Q6_K: (256, 210)}  # format.rs:368-400
+AFFINE_CONFIG = {Q4_0: (4, 32), Q4_1: (4, 32), Q5_0: (5, 32), Q5_1: (5, 32), Q8_0: (8, 32),
+                 Q2_K: (2, 16), Q3_K: (3, 16), Q4_K: (4, 32), Q5_K: (5, 32), Q6_K: (6, 16)}  # convert.rs:142-152
+GGUF_TYPES = tuple(BLOCK_GEOMETRY)
 
 _lib = None
 
@@ -130,7 +135,8 @@ def gguf_convert_affine(ggml_type: int, raw: np.ndarray, big_endian: bool = Fals
 
 def gguf_dequant_f32(ggml_type: int, raw: np.ndarray, definition: int = 0, big_endian: bool = False) -> np.ndarray:
     """Dense f32 dequant; definition 0 = affine route (convert.rs:81-101),
-    1 = native decoder (native_quantization.rs:3445-3469, 3539-3542)."""
+    1 = native decoder (native_quantization.rs:3445-3469, 3499-3509,
+    3539-3542) where the type has one, else the affine route."""
     values, nbytes = BLOCK_GEOMETRY[ggml_type]
     raw = np.ascontiguousarray(raw, dtype=np.uint8)
     nblocks = raw.size // nbytes

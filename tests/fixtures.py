@@ -45,10 +45,31 @@ def f16_bits(v: np.ndarray) -> np.ndarray:
     return np.asarray(v, dtype=np.float32).astype(np.float16).view(np.uint16)
 
 
+# (block bytes, offsets of the f16 scale-like fields drawn |N(0, 0.01)|, offsets
+# of the f16 offset fields drawn N(0, 0.01)) of the block types added after
+# Q4_0 / Q8_0 / Q4_K (eredu-gguf/src/convert.rs:362-564).
+KQUANT_HEADERS = {
+    3: (20, (0,), (2,)),      # Q4_1: d, m
+    6: (22, (0,), ()),        # Q5_0: d
+    7: (24, (0,), (2,)),      # Q5_1: d, m
+    10: (84, (80, 82), ()),   # Q2_K: d, dmin
+    11: (110, (108,), ()),    # Q3_K: d
+    13: (176, (0, 2), ()),    # Q5_K: d, dmin
+    14: (210, (208,), ()),    # Q6_K: d
+}
+
+
 def synthetic_blocks(ggml_type: int, nblocks: int, seed: int) -> np.ndarray:
     """GGML blocks with uniform random quant bytes and f16 d/dmin = f16(|N(0, 0.01)|)
-    (the config-4 distribution)."""
+    (the config-4 distribution; Q4_1 / Q5_1 offsets m = f16(N(0, 0.01)))."""
     rng = np.random.default_rng(seed)
+    if ggml_type in KQUANT_HEADERS:
+        nbytes, pos, signed = KQUANT_HEADERS[ggml_type]
+        b = rng.integers(0, 256, size=(nblocks, nbytes), dtype=np.uint8)
+        for off in pos + signed:
+            v = rng.normal(0, 0.01, nblocks)
+            b[:, off:off + 2] = f16_bits(v if off in signed else np.abs(v)).view(np.uint8).reshape(nblocks, 2)
+        return np.ascontiguousarray(b.reshape(-1))
     if ggml_type == 2:  # Q4_0
         b = rng.integers(0, 256, size=(nblocks, 18), dtype=np.uint8)
         b[:, 0:2] = f16_bits(np.abs(rng.normal(0, 0.01, nblocks))).view(np.uint8).reshape(nblocks, 2)

@@ -108,8 +108,10 @@ def test_error_message_is_thread_local():
 @pytest.mark.parametrize(
     "args,needle",
     [
-        (dict(ty=3), "unsupported GGML tensor type"),
+        (dict(ty=16), "unsupported GGML tensor type"),
+        (dict(ty=39), "unsupported GGML tensor type"),
         (dict(cols=48), "not divisible by group size 32"),
+        (dict(cols=264, ty=14), "not divisible by group size 16"),
         (dict(cols=288, ty=12), "not divisible by block length 256"),
         (dict(raw_len=17), "payload length does not match descriptor"),
         (dict(endian=5), "invalid endian"),
