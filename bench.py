@@ -217,7 +217,9 @@ def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
 
 
 def bench_gguf(steps, warmup):
-    """GGUF 4096x14336 dequant (bf16) and convert (affine) GB/s."""
+    """GGUF 4096x14336 dequant (bf16) and convert (affine) GB/s,
+    for every block type with an affine form (Q4_0 / Q8_0 / Q4_K first, the
+    configs' types)."""
     import torch
 
     from eredu_amd import gguf as G
@@ -225,7 +227,8 @@ def bench_gguf(steps, warmup):
     n = _lib()
     rows, cols = 4096, 14336
     out = {}
-    for ty in (G.GgmlType.Q4_0, G.GgmlType.Q8_0, G.GgmlType.Q4K):
+    T = G.GgmlType
+    for ty in (T.Q4_0, T.Q8_0, T.Q4K, T.Q4_1, T.Q5_0, T.Q5_1, T.Q2K, T.Q3K, T.Q5K, T.Q6K):
         vals, nbytes = ty.block_and_bytes()
         nraw = rows * cols // vals * nbytes
         bits, gs = G.affine_config(ty)
@@ -250,7 +253,7 @@ def bench_gguf(steps, warmup):
                                                        raws[i].data_ptr(), nraw, int(ty), rows, cols, 0, st))
 
         for label, fn, out_bytes, k in (("dequant_bf16", deq, rows * cols * 2, copies),
-                                        ("convert_affine_g32", conv, conv_bytes, cc)):
+                                        (f"convert_affine_g{gs}", conv, conv_bytes, cc)):
             ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / k
             gbs = (nraw + out_bytes) / (ms * 1e-3) / 1e9
             out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),

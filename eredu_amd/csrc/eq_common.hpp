@@ -171,30 +171,18 @@ __device__ __forceinline__ float silu_sigmoid_bf16(float x) {
 
 // f32 -> IEEE binary16 bits with round-to-nearest-even, overflow to infinity
 // and NaN quieted with the top payload bits kept: the rounding of the `half`
-// crate's f16::from_f32 that eredu-gguf/src/convert.rs:409-411 uses.  Done in
-// integer arithmetic so the result does not depend on the hardware mode bits.
+// crate's f16::from_f32 that eredu-gguf/src/convert.rs:409-411 uses.  Finite
+// and infinite inputs take the hardware conversion (v_cvt_f16_f32 under the
+// default round-to-nearest-even mode with f16 subnormals kept); NaN takes the
+// crate's bit pattern, which the hardware does not promise.  The empty asm
+// keeps f the rounded f32 it is: without it the compiler folds a product into
+// the conversion (v_fma_mix with a +0 addend), rounding once instead of twice
+// and turning a -0 product into +0.
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
-    uint32_t x = __float_as_uint(f);
-    uint32_t sign = (x >> 16) & 0x8000u;
-    uint32_t exp = (x >> 23) & 0xffu;
-    uint32_t man = x & 0x7fffffu;
-    if (exp == 0xffu) return sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u);
-    int e = static_cast<int>(exp) - 112;  // rebias 127 -> 15
-    if (e >= 0x1f) return sign | 0x7c00u;
-    if (e <= 0) {
-        if (e < -10) return sign;
-        uint32_t m = man | 0x800000u;
-        uint32_t shift = static_cast<uint32_t>(14 - e);
-        uint32_t h = m >> shift;
-        uint32_t rem = m & ((1u << shift) - 1u);
-        uint32_t halfway = 1u << (shift - 1u);
-        if (rem > halfway || (rem == halfway && (h & 1u))) h += 1u;
-        return sign | h;
-    }
-    uint32_t h = (static_cast<uint32_t>(e) << 10) | (man >> 13);
-    uint32_t rem = man & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
-    return sign | h;
+    const uint32_t x = __float_as_uint(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return ((x >> 16) & 0x8000u) | 0x7e00u | ((x & 0x7fffffu) >> 13);
+    asm volatile("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
 // Scalar parameter loads for each scale/activation element type.
@@ -362,6 +350,15 @@ __device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float* f) {
         f[2 * i] = bf16_bits_to_f32(p[i] & 0xffffu);
         f[2 * i + 1] = bf16_bits_to_f32(p[i] >> 16);
     }
+}
+
+// Two f32 -> one word of bf16 (a low, b high), round to nearest even, in one
+// v_cvt_pk_bf16_f32; equal to f32_to_bf16_bits on every input but NaN (any
+// quiet NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 // a.x b.x + a.y b.y + c over bf16 pairs (v_dot2c_f32_bf16).

@@ -121,7 +121,7 @@ template <>
 __device__ __forceinline__ void store8<BF16T>(uint16_t* out, int64_t base, const float v[8]) {
     uint32_t p[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) p[j] = f32_to_bf16_bits(v[2 * j]) | (f32_to_bf16_bits(v[2 * j + 1]) << 16);
+    for (int j = 0; j < 4; j++) p[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
     store_stream16(out + base, make_uint4(p[0], p[1], p[2], p[3]));
 }
 template <>
@@ -341,36 +341,73 @@ __device__ __forceinline__ uint32_t lds_half(const uint8_t* b, int o) {
     return BIG ? (uint32_t(b[o]) << 8) | b[o + 1] : uint32_t(b[o]) | (uint32_t(b[o + 1]) << 8);
 }
 
-// Code of value i (0..31) of unit u of a block.
+// 8 bytes at an even LDS offset as two words: byte j in byte j % 4 of lo (j < 4)
+// or hi.  Blocks of 22 / 110 / 210 bytes sit at 2-byte alignment in LDS, so
+// the words are assembled from 16-bit reads.
+__device__ __forceinline__ void lds_8b(const uint8_t* p, uint32_t& lo, uint32_t& hi) {
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+    lo = uint32_t(q[0]) | (uint32_t(q[1]) << 16);
+    hi = uint32_t(q[2]) | (uint32_t(q[3]) << 16);
+}
+
+// Bits 0..3 of t moved to bit 0 of bytes 0..3 (the four shifted copies of t
+// do not overlap, so the product carries nothing).
+__device__ __forceinline__ uint32_t spread4(uint32_t t) { return ((t & 15u) * 0x204081u) & 0x01010101u; }
+
+// Codes of values i0 .. i0 + 7 (i0 a multiple of 8) of unit u of a block, as
+// byte lanes: value i0 + j in byte j % 4 of c0 (j < 4) or c1.  Every code of
+// a byte lane is extracted by one shift and mask of the word.
 template <int T, bool BIG>
-__device__ __forceinline__ uint32_t kq_code(const uint8_t* b, int u, int i) {
+__device__ __forceinline__ void kq_codes8(const uint8_t* b, int u, int i0, uint32_t& c0, uint32_t& c1) {
+    uint32_t a0, a1, h0, h1;
     if constexpr (T == EQ_GGML_Q4_1) {
         // low nibbles of bytes 4..20 are values 0..15, high nibbles 16..31 (convert.rs:367-370)
-        return (b[4 + (i & 15)] >> ((i >> 4) * 4)) & 15u;
+        lds_8b(b + 4 + (i0 & 15), a0, a1);
+        const int sh = (i0 >> 4) * 4;
+        c0 = (a0 >> sh) & 0x0f0f0f0fu;
+        c1 = (a1 >> sh) & 0x0f0f0f0fu;
     } else if constexpr (T == EQ_GGML_Q5_0 || T == EQ_GGML_Q5_1) {
-        // nibble as Q4_1 plus bit i of the u32 at 2 (Q5_0) or 4 (Q5_1) (convert.rs:553-562)
+        // nibbles as Q4_1 at 6 / 8, plus bit i of the u32 at 2 / 4 as bit 4 (convert.rs:553-562):
+        // bits i0 .. i0 + 7 are byte i0 / 8 of that word in its byte order
         constexpr int qh = T == EQ_GGML_Q5_0 ? 2 : 4, qs = qh + 4;
-        const uint32_t lo = (b[qs + (i & 15)] >> ((i >> 4) * 4)) & 15u;
-        const uint32_t hi = (b[qh + (BIG ? 3 - (i >> 3) : (i >> 3))] >> (i & 7)) & 1u;
-        return lo | (hi << 4);
+        lds_8b(b + qs + (i0 & 15), a0, a1);
+        const int sh = (i0 >> 4) * 4;
+        const uint32_t hb = b[qh + (BIG ? 3 - (i0 >> 3) : (i0 >> 3))];
+        c0 = ((a0 >> sh) & 0x0f0f0f0fu) | (spread4(hb) << 4);
+        c1 = ((a1 >> sh) & 0x0f0f0f0fu) | (spread4(hb >> 4) << 4);
     } else if constexpr (T == EQ_GGML_Q2_K) {
-        // group g = 2u + i/16 takes 2 bits at shift 2 (g % 8) / 2 of byte
-        // 16 + (g / 8) 32 + (g % 2) 16 + i % 16 (convert.rs:501-505)
-        return (b[16 + (u >> 2) * 32 + i] >> ((u & 3) * 2)) & 3u;
+        // group g = 2u + i/16 takes 2 bits at shift 2 ((g % 8) / 2) = 2 (u % 4) of byte
+        // 16 + (g / 8) 32 + (g % 2) 16 + i % 16 = 16 + (u / 4) 32 + i (convert.rs:501-505)
+        lds_8b(b + 16 + (u >> 2) * 32 + i0, a0, a1);
+        const int sh = (u & 3) * 2;
+        c0 = (a0 >> sh) & 0x03030303u;
+        c1 = (a1 >> sh) & 0x03030303u;
     } else if constexpr (T == EQ_GGML_Q3_K) {
-        // as Q2_K at byte 32, plus bit g / 2 = u of hm[i] as bit 2 (convert.rs:531-539)
-        const uint32_t lo = (b[32 + (u >> 2) * 32 + i] >> ((u & 3) * 2)) & 3u;
-        return lo | (((uint32_t(b[i]) >> u) & 1u) << 2);
+        // as Q2_K at byte 32, plus bit g / 2 = u of hm[(g % 2) 16 + i % 16] = hm[i] as bit 2
+        // (convert.rs:531-539)
+        lds_8b(b + 32 + (u >> 2) * 32 + i0, a0, a1);
+        lds_8b(b + i0, h0, h1);
+        const int sh = (u & 3) * 2;
+        c0 = ((a0 >> sh) & 0x03030303u) | (((h0 >> u) & 0x01010101u) << 2);
+        c1 = ((a1 >> sh) & 0x03030303u) | (((h1 >> u) & 0x01010101u) << 2);
     } else if constexpr (T == EQ_GGML_Q5_K) {
-        // unit = group g: nibble g % 2 of qs[(g / 2) 32 + i] at 48, bit g of qh[i] at 16 (convert.rs:453-461)
-        const uint32_t lo = (b[48 + (u >> 1) * 32 + i] >> ((u & 1) * 4)) & 15u;
-        return lo | (((uint32_t(b[16 + i]) >> u) & 1u) << 4);
+        // unit = group g: nibble g % 2 of qs[(g / 2) 32 + i] at 48, bit g of qh[i] at 16
+        // as bit 4 (convert.rs:453-461)
+        lds_8b(b + 48 + (u >> 1) * 32 + i0, a0, a1);
+        lds_8b(b + 16 + i0, h0, h1);
+        const int sh = (u & 1) * 4;
+        c0 = ((a0 >> sh) & 0x0f0f0f0fu) | (((h0 >> u) & 0x01010101u) << 4);
+        c1 = ((a1 >> sh) & 0x0f0f0f0fu) | (((h1 >> u) & 0x01010101u) << 4);
     } else {
         // Q6_K: unit u is value run k = u % 4 of half h = u / 4: nibble k / 2 of
-        // ql[h 64 + (k % 2) 32 + i], bits 2k..2k+1 of qh[128 + h 32 + i] (convert.rs:472-477)
+        // ql[h 64 + (k % 2) 32 + i], bits 2k, 2k + 1 of qh[128 + h 32 + i] as bits 4, 5
+        // (convert.rs:472-477)
         const int h = u >> 2, k = u & 3;
-        const uint32_t lo = (b[h * 64 + (k & 1) * 32 + i] >> ((k >> 1) * 4)) & 15u;
-        return lo | (((uint32_t(b[128 + h * 32 + i]) >> (2 * k)) & 3u) << 4);
+        lds_8b(b + h * 64 + (k & 1) * 32 + i0, a0, a1);
+        lds_8b(b + 128 + h * 32 + i0, h0, h1);
+        const int sh = (k >> 1) * 4;
+        c0 = ((a0 >> sh) & 0x0f0f0f0fu) | (((h0 >> (2 * k)) & 0x03030303u) << 4);
+        c1 = ((a1 >> sh) & 0x0f0f0f0fu) | (((h1 >> (2 * k)) & 0x03030303u) << 4);
     }
 }
 
@@ -435,6 +472,40 @@ __device__ __forceinline__ void store_unit(uint32_t* w, const uint32_t* wd) {
     }
 }
 
+// Four 2-bit codes in byte lanes -> 8 bits, code j at bits 2j.
+__device__ __forceinline__ uint32_t crumbs(uint32_t x) {
+    x |= x >> 6;
+    return (x | (x >> 12)) & 0xffu;
+}
+
+// LSB-first pack (convert.rs:413-427) of a unit's 32 codes, given as eight
+// byte-lane words, into BITS words.  Widths 3, 5 and 6 go four codes (one
+// 4 BITS-bit chunk) at a time; every shift is a constant once unrolled.
+template <int BITS>
+__device__ __forceinline__ void pack_unit(const uint32_t cw[8], uint32_t wd[BITS]) {
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) wd[j] = lo_nibbles(cw[2 * j]) | (lo_nibbles(cw[2 * j + 1]) << 16);
+    } else if constexpr (BITS == 2) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            wd[j] = crumbs(cw[4 * j]) | (crumbs(cw[4 * j + 1]) << 8) | (crumbs(cw[4 * j + 2]) << 16) |
+                    (crumbs(cw[4 * j + 3]) << 24);
+    } else {
+#pragma unroll
+        for (int j = 0; j < BITS; j++) wd[j] = 0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const uint32_t x = cw[q];
+            const uint32_t chunk = (x & 0xffu) | (((x >> 8) & 0xffu) << BITS) | (((x >> 16) & 0xffu) << (2 * BITS)) |
+                                   ((x >> 24) << (3 * BITS));
+            const int off = q * 4 * BITS, sh = off & 31;
+            wd[off >> 5] |= chunk << sh;
+            if (sh + 4 * BITS > 32) wd[(off >> 5) + 1] |= chunk >> (32 - sh);
+        }
+    }
+}
+
 template <int T, bool BIG>
 __global__ __launch_bounds__(256) void kq_to_affine(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
                                                     uint32_t* __restrict__ w, uint16_t* __restrict__ s,
@@ -448,18 +519,10 @@ __global__ __launch_bounds__(256) void kq_to_affine(const uint8_t* __restrict__ 
     const int lb = threadIdx.x / P::units, u = threadIdx.x % P::units;
     if (lb >= nb) return;
     const uint8_t* b = reinterpret_cast<const uint8_t*>(lds) + lb * P::bytes;
-    // LSB-first pack of the unit's 32 codes (convert.rs:413-427); offsets are
-    // constants once the loop is unrolled
-    uint32_t wd[P::bits];
+    uint32_t cw[8], wd[P::bits];
 #pragma unroll
-    for (int j = 0; j < P::bits; j++) wd[j] = 0;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const uint32_t c = kq_code<T, BIG>(b, u, i);
-        const int off = i * P::bits, sh = off & 31;
-        wd[off >> 5] |= c << sh;
-        if (sh + P::bits > 32) wd[(off >> 5) + 1] |= c >> (32 - sh);
-    }
+    for (int q = 0; q < 4; q++) kq_codes8<T, BIG>(b, u, 8 * q, cw[2 * q], cw[2 * q + 1]);
+    pack_unit<P::bits>(cw, wd);
     const int64_t unit = (blk0 + lb) * P::units + u;
     store_unit<P::bits>(w + unit * P::bits, wd);
 #pragma unroll
@@ -475,7 +538,7 @@ __global__ __launch_bounds__(256) void kq_to_affine(const uint8_t* __restrict__ 
 // (convert.rs:81-101); for these types it is also the native definition
 // (Q5_1's native decoder d * q + m uses the same unrounded d and m,
 // native_quantization.rs:3499-3509).  Lane quarter c of unit lu decodes values
-// [8c, 8c + 8).
+// [8c, 8c + 8); each code converts from its byte lane in one instruction.
 template <int T, bool BIG, typename OUT>
 __global__ __launch_bounds__(256) void kq_dense(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
                                                 typename OUT::storage* __restrict__ out) {
@@ -492,12 +555,16 @@ __global__ __launch_bounds__(256) void kq_dense(const uint8_t* __restrict__ raw,
         const int lb = lu / P::units, u = lu % P::units;
         if (lb >= nb) break;
         const uint8_t* b = reinterpret_cast<const uint8_t*>(lds) + lb * P::bytes;
-        uint32_t sb, bb;
+        uint32_t sb, bb, c0, c1;
         kq_group<T, BIG>(b, (u * 32 + 8 * c) / P::gs, sb, bb);
+        kq_codes8<T, BIG>(b, u, 8 * c, c0, c1);
         const float scale = f16_bits_to_f32(sb), bv = f16_bits_to_f32(bb);
         float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = scale * float(kq_code<T, BIG>(b, u, 8 * c + i)) + bv;
+        for (int i = 0; i < 4; i++) {
+            v[i] = scale * float((c0 >> (8 * i)) & 0xffu) + bv;
+            v[4 + i] = scale * float((c1 >> (8 * i)) & 0xffu) + bv;
+        }
         store8<OUT>(out, ((blk0 + lb) * P::units + u) * 32 + 8 * c, v);
     }
 }

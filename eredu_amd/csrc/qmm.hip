@@ -51,17 +51,11 @@
 namespace eq {
 
 typedef uint32_t q_u32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 q_bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 128, kBN = 256, kBK = 64;
 constexpr int kQmmThreads = 512;        // two K-groups of 4 waves
 constexpr int kLdsBuf = kBM * kBK * 2;  // bytes per activation buffer
 constexpr int kRing = 3;                // slots of the load rings (codes in registers, activations in LDS)
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    const q_bf16x2 p = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};  // RNE (v_cvt_pk_bf16_f32)
-    return __builtin_bit_cast(uint32_t, p);
-}
 
 // 8 codes in k order -> 4 registers of bf16 pairs (s*q + b).
 template <int BITS>
