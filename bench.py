@@ -259,7 +259,7 @@ def bench_gguf(steps, warmup):
             out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": k}
         del dense, aw, asb, abb
-        if ty in (G.GgmlType.Q8_0, G.GgmlType.Q4K):
+        if ty.has_device_linear():
             # batch-1 linear straight from the blocks: y [1, 4096] = x [1, 14336] . W^T
             x = torch.randn((1, cols), device="cuda").to(torch.bfloat16)
             y = torch.empty((1, rows), dtype=torch.bfloat16, device="cuda")

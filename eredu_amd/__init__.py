@@ -10,7 +10,8 @@ host-side mirror of the reference's operator API:
   ``quantize[_with_mode]``, ``QuantizedLinear``.
 * :mod:`eredu_amd.gguf` -- eredu-gguf ``conversion_kind`` routing, ``convert``,
   ``convert_affine`` / ``AffineTensor``, ``NativeTensor`` (blocks kept as
-  stored), dense dequantization and the native Q4_K / Q8_0 linear.
+  stored), dense dequantization and the native Q4_K / Q5_K / Q6_K / Q5_1 /
+  Q8_0 linear.
 * :mod:`eredu_amd.nn` -- the linear-layer dispatch (``LinearSpec`` ->
   dense ``Linear`` or ``QuantizedLinear`` for affine / MXFP4 / native GGUF).
 * :mod:`eredu_amd.checkpoint` -- MLX-LM quantized SafeTensors checkpoints.

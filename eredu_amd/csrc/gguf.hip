@@ -737,6 +737,111 @@ __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, cons
     }
 }
 
+// ------------------------------------- native linear for Q5_K / Q6_K / Q5_1
+//
+// NativeQuantizedTensor::linear, transpose = true, for the other encodings
+// eredu keeps native (safemlx/src/native_quantization.rs:741-772; its Metal
+// kernels q5k / q6k / q5_1 _linear_metal, :1320-1400, 1856): y[m, n] =
+// sum_k x[m, k] W[n, k] with W decoded in f32 without f16 rounding of the
+// group factors -- Q6_K d sc (q - 32), Q5_K d sc q - dmin m, Q5_1 d q + m --
+// as those kernels decode.  A workgroup stages the payload of R consecutive
+// weight rows (contiguous bytes) through LDS with 16-byte loads; wave w takes
+// rows w, w + 4, ... and its lanes split each row's 32-value units.  Per unit
+// the codes come from kq_codes8 as byte lanes, are turned into bf16 pairs
+// 128 + q by byte permutes, and meet x in v_dot2c_f32_bf16; per group
+// sum x q = e - 128 sum x.  Up to kLinRows activation rows per launch.
+template <int T, bool BIG>
+__device__ __forceinline__ void kq_native_group(const uint8_t* b, int g, float& scale, float& bias) {
+    if constexpr (T == EQ_GGML_Q5_1) {
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 0));  // native_quantization.rs:3499-3509
+        bias = f16_bits_to_f32(lds_half<BIG>(b, 2));
+    } else if constexpr (T == EQ_GGML_Q5_K) {
+        uint32_t sc, m;
+        scale_min_bytes(b + 4, g, sc, m);
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 0)) * float(sc);
+        bias = -(f16_bits_to_f32(lds_half<BIG>(b, 2)) * float(m));
+    } else {
+        static_assert(T == EQ_GGML_Q6_K, "native linear covers Q5_1, Q5_K and Q6_K here");
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 208)) * float(int8_t(b[192 + g]));
+        bias = -32.0f * scale;
+    }
+}
+
+template <int T, bool BIG, bool MANY>
+__global__ __launch_bounds__(256) void kq_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
+                                                 const uint8_t* __restrict__ raw, int M, int N, int K, int R,
+                                                 bool vec_ok) {
+    using P = KQuant<T>;
+    constexpr int G = 32 / P::gs, VG = 32 / G;  // groups per unit, values per group
+    extern __shared__ __attribute__((aligned(16))) uint16_t kq_lds[];
+    const int row_bytes = K / (32 * P::units) * P::bytes, U = K / 32;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t c43 = 0x43434343u;
+    for (int64_t n0 = int64_t(blockIdx.x) * R; n0 < N; n0 += int64_t(gridDim.x) * R) {
+        const int nr = int(min<int64_t>(R, N - n0));
+        const int nbytes = nr * row_bytes;
+        const uint8_t* src = raw + n0 * row_bytes;
+        if (vec_ok && (nbytes & 15) == 0) {
+            for (int i = threadIdx.x; i < nbytes / 16; i += 256)
+                reinterpret_cast<uint4*>(kq_lds)[i] = load_stream16(src + 16 * int64_t(i));
+        } else {
+            for (int i = threadIdx.x; i < nbytes / 2; i += 256) kq_lds[i] = reinterpret_cast<const uint16_t*>(src)[i];
+        }
+        __syncthreads();
+        for (int r = wave; r < nr; r += 4) {
+            const uint8_t* row = reinterpret_cast<const uint8_t*>(kq_lds) + r * row_bytes;
+            float acc[kLinRows];
+#pragma unroll
+            for (int m = 0; m < kLinRows; m++) acc[m] = 0.f;
+            for (int u = lane; u < U; u += 64) {
+                const uint8_t* b = row + (u / P::units) * P::bytes;
+                const int uu = u % P::units;
+                uint32_t cp[16];  // bf16 pairs (128 + q) of values 2j, 2j + 1
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    uint32_t c0, c1;
+                    kq_codes8<T, BIG>(b, uu, 8 * q, c0, c1);
+                    cp[4 * q] = __builtin_amdgcn_perm(c43, c0, 0x04010400u);
+                    cp[4 * q + 1] = __builtin_amdgcn_perm(c43, c0, 0x04030402u);
+                    cp[4 * q + 2] = __builtin_amdgcn_perm(c43, c1, 0x04010400u);
+                    cp[4 * q + 3] = __builtin_amdgcn_perm(c43, c1, 0x04030402u);
+                }
+                float sc[G], bi[G];
+#pragma unroll
+                for (int g = 0; g < G; g++) kq_native_group<T, BIG>(b, uu * G + g, sc[g], bi[g]);
+#pragma unroll
+                for (int m = 0; m < (MANY ? kLinRows : 1); m++) {
+                    if (m >= M) break;
+                    const uint4* xp = reinterpret_cast<const uint4*>(x + int64_t(m) * K + int64_t(u) * 32);
+                    uint32_t xw[16];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint4 v = xp[i];
+                        xw[4 * i] = v.x, xw[4 * i + 1] = v.y, xw[4 * i + 2] = v.z, xw[4 * i + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        float e = 0.f, sx = 0.f;
+#pragma unroll
+                        for (int j = 0; j < VG / 2; j++) {
+                            e = dot2_bf16(xw[g * VG / 2 + j], cp[g * VG / 2 + j], e);
+                            sx = dot2_bf16(xw[g * VG / 2 + j], kBf16Ones, sx);
+                        }
+                        acc[m] += sc[g] * (e - 128.f * sx) + bi[g] * sx;
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < (MANY ? kLinRows : 1); m++) {
+                if (m >= M) break;
+                const float v = wave_sum(acc[m]);
+                if (lane == 0) y[int64_t(m) * N + n0 + r] = uint16_t(f32_to_bf16_bits(v));
+            }
+        }
+        __syncthreads();  // the rows are read before the next group is staged
+    }
+}
+
 // ------------------------------------------- native Q4_K linear on MFMA
 //
 // The same product as q4k_linear for up to 8 activation rows per launch, on
@@ -1400,8 +1505,9 @@ extern "C" int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len
 extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
                               int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream) {
     clear_error();
-    if (ggml_type != EQ_GGML_Q4_K && ggml_type != EQ_GGML_Q8_0) {
-        set_error("native GGUF linear covers Q4_K and Q8_0");
+    const bool kq = ggml_type == EQ_GGML_Q5_1 || ggml_type == EQ_GGML_Q5_K || ggml_type == EQ_GGML_Q6_K;
+    if (ggml_type != EQ_GGML_Q4_K && ggml_type != EQ_GGML_Q8_0 && !kq) {
+        set_error("native GGUF linear covers Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0");
         return 1;
     }
     Geometry geo;
@@ -1426,6 +1532,44 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool big = endian == EQ_ENDIAN_BIG;
+    if (kq) {
+        // R weight rows per workgroup, staged whole in LDS: 8 while they fit
+        // in 64 KB, fewer for long rows, one row up to the device's LDS
+        const int64_t row_bytes = K / geo.values * geo.bytes;
+        int R = 8;
+        while (R > 1 && R * row_bytes > 65536) R /= 2;
+        if (R * row_bytes > lds_limit()) {
+            set_error("native linear: one weight row (" + std::to_string(row_bytes) + " bytes) exceeds LDS");
+            return 1;
+        }
+        const int lds = int(R * row_bytes);
+        const bool vec_ok = aligned(raw, 16) && lds % 16 == 0;
+        const int64_t wgs = (N + R - 1) / R;
+        const unsigned grid = unsigned(wgs < 16384 ? wgs : 16384);
+        if (!with_kq(ggml_type, big, [&](auto t, auto b) {
+                constexpr int T = decltype(t)::value;
+                if constexpr (T == EQ_GGML_Q5_1 || T == EQ_GGML_Q5_K || T == EQ_GGML_Q6_K) {
+                    constexpr bool B = decltype(b)::value;
+                    for (int64_t m0 = 0; m0 < M; m0 += kLinRows) {
+                        const int mc = int(M - m0 < kLinRows ? M - m0 : kLinRows);
+                        auto go = [&](auto kernel) {
+                            if (lds > 65536)
+                                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+                            kernel<<<grid, 256, size_t(lds), st>>>(static_cast<uint16_t*>(y) + m0 * N,
+                                                                  static_cast<const uint16_t*>(x) + m0 * K, raw, mc,
+                                                                  int(N), int(K), R, vec_ok);
+                        };
+                        if (mc == 1)
+                            go(kq_linear<T, B, false>);
+                        else
+                            go(kq_linear<T, B, true>);
+                    }
+                }
+            }))
+            return 1;
+        return check_launch("gguf linear");
+    }
     if (ggml_type == EQ_GGML_Q4_K &&
         launch_q4k_mfma(static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), raw, M, N, K, big, st))
         return check_launch("gguf linear");

@@ -23,8 +23,8 @@ from ._native import EreduError, check
 class GgmlType(enum.IntEnum):
     """GGML tensor type codes (eredu-gguf/src/format.rs:295-365).  The device
     path converts and dequantizes every type with an affine form and executes
-    Q4_K and Q8_0 blocks natively; the rest are named so that routing
-    (``conversion_kind``) covers every code the container holds."""
+    Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0 blocks natively; the rest are named so
+    that routing (``conversion_kind``) covers every code the container holds."""
 
     F32 = 0
     F16 = 1
@@ -74,8 +74,9 @@ class GgmlType(enum.IntEnum):
         return affine_config(self) is not None
 
     def has_device_linear(self) -> bool:
-        """Encodings this library multiplies straight from their blocks (eq_gguf_linear)."""
-        return self in (GgmlType.Q8_0, GgmlType.Q4K)
+        """Encodings this library multiplies straight from their blocks
+        (eq_gguf_linear): the non-IQ encodings eredu executes natively."""
+        return self in (GgmlType.Q8_0, GgmlType.Q4K, GgmlType.Q5K, GgmlType.Q6K, GgmlType.Q5_1)
 
 
 _BLOCK_AND_BYTES = {
@@ -273,13 +274,14 @@ def dequantize(
 
 def linear(x: torch.Tensor, desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little) -> torch.Tensor:
     """y = x . W^T with W the GGUF tensor of ``desc`` decoded by the native
-    definition, straight from its Q4_K or Q8_0 blocks (no affine expansion):
-    NativeQuantizedTensor::linear with transpose = true
+    definition, straight from its Q4_K, Q5_K, Q6_K, Q5_1 or Q8_0 blocks (no
+    affine expansion): NativeQuantizedTensor::linear with transpose = true
     (safemlx/src/native_quantization.rs:741-772); C ABI eq_gguf_linear.
     x is bf16 [..., K] on the GPU; W's MLX shape is [N, K]."""
     ty = _device_type(desc)
     if not ty.has_device_linear():
-        raise EreduError(f"tensor '{desc.name}': no native linear for GGML type {int(ty)} (Q4_K and Q8_0 only)")
+        raise EreduError(f"tensor '{desc.name}': no native linear for GGML type {int(ty)} "
+                         f"(Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0)")
     _check_raw(desc, raw)
     shape, N, K = _rows_cols(desc)
     if len(shape) != 2:
@@ -399,10 +401,11 @@ class DenseTensor:
 def convert(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little):
     """eredu_gguf's convert (convert.rs:276-313) on device payloads, routed by
     ``conversion_kind``: a DenseTensor (dense types), a NativeTensor (blocks
-    kept as stored: little-endian Q4_K / Q8_0), an MxFp4Tensor (type 39), or
-    an AffineTensor (Q4_0, Q4_1, Q5_0, Q2_K, Q3_K in either byte order; the
-    natively executed types in big-endian files).  Encodings without device
-    kernels are refused with the type named."""
+    kept as stored: little-endian Q4_K / Q5_K / Q6_K / Q5_1 / Q8_0), an
+    MxFp4Tensor (type 39), or an AffineTensor (Q4_0, Q4_1, Q5_0, Q2_K, Q3_K in
+    either byte order; the natively executed types in big-endian files).
+    Encodings without device kernels (the IQ types) are refused with the type
+    named."""
     if raw.dtype != torch.uint8 or not raw.is_cuda:
         raise EreduError("raw GGUF payload must be a uint8 tensor on the GPU")
     if raw.numel() != desc.byte_len:
@@ -417,7 +420,7 @@ def convert(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.L
     if kind.kind == "native":
         if not ty.has_device_linear():
             raise EreduError(f"tensor '{desc.name}': GGML type {int(ty)} stays native in eredu, and this library "
-                             f"executes only Q4_K and Q8_0 blocks")
+                             f"executes only Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0 blocks")
         shape = desc.mlx_shape()
         values, _ = ty.block_and_bytes()
         if not shape or shape[-1] % values != 0:

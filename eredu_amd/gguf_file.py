@@ -15,10 +15,10 @@ raw blocks of each tensor go file -> pinned host buffer -> HBM on a copy
 stream while the previous tensor is converted on the compute stream (two
 pinned staging buffers, ordered by events), so file reads, PCIe copies and
 conversion overlap.  Tensors are routed as eredu routes them
-(eredu-gguf/src/convert.rs:125-140): little-endian Q4_K / Q8_0 stay in their
-blocks (executed by the native linear), Q4_0 and big-endian Q4_K / Q8_0 are
-expanded to the MLX affine triple by ``eq_gguf_convert_affine``, dense
-tensors are copied as they are.  ``stream_convert_affine`` expands every
+(eredu-gguf/src/convert.rs:125-140): little-endian Q4_K / Q5_K / Q6_K /
+Q5_1 / Q8_0 stay in their blocks (executed by the native linear), Q4_0,
+Q4_1, Q5_0, Q2_K, Q3_K and big-endian blocks are expanded to the MLX affine
+triple by ``eq_gguf_convert_affine``, dense tensors are copied as they are.  ``stream_convert_affine`` expands every
 quantized tensor (the explicit convert_affine of portable backends).
 """
 from __future__ import annotations
@@ -341,10 +341,11 @@ def stream_convert(path: str, names: Optional[Sequence[str]] = None, staging_byt
     routed by conversion_kind, :125-140; safemlx/src/ops/gguf.rs:421-528):
 
     * dense F32 / F16 / BF16 (and the integer dense types) -> ``gguf.DenseTensor``,
-    * little-endian Q4_K / Q8_0 -> ``gguf.NativeTensor`` (blocks kept as stored,
-      executed by the native linear),
+    * little-endian Q4_K / Q5_K / Q6_K / Q5_1 / Q8_0 -> ``gguf.NativeTensor``
+      (blocks kept as stored, executed by the native linear),
     * MXFP4 (type 39) -> ``gguf.MxFp4Tensor`` (E2M1 codes + E8M0 scale bytes),
-    * Q4_0, and big-endian Q4_K / Q8_0 -> ``gguf.AffineTensor``.
+    * Q4_0, Q4_1, Q5_0, Q2_K, Q3_K, and big-endian blocks of the native
+      types -> ``gguf.AffineTensor``.
 
     Returns {name: tensor}.  Two pinned staging buffers of ``staging_bytes``
     alternate: while tensor i is copied to the device and converted, tensor

@@ -208,7 +208,8 @@ def test_quantize_rejects_bad_arguments():
 def test_gguf_linear_rejects_bad_arguments():
     bf16 = _native.EQ_DTYPE_BF16
     # Q4_0 is not a native-linear type; payload length must match; bf16 only
-    _rejects(L.eq_gguf_linear(16, 16, 16, 18 * 8, 2, 1, 2, 128, 0, bf16, None), "Q4_K and Q8_0")
+    _rejects(L.eq_gguf_linear(16, 16, 16, 18 * 8, 2, 1, 2, 128, 0, bf16, None), "Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0")
+    _rejects(L.eq_gguf_linear(16, 16, 16, 84 * 2, 10, 1, 2, 256, 0, bf16, None), "Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0")
     _rejects(L.eq_gguf_linear(16, 16, 16, 100, 12, 1, 2, 256, 0, bf16, None), "payload length")
     _rejects(L.eq_gguf_linear(16, 16, 16, 2 * 144, 12, 1, 2, 256, 0, _native.EQ_DTYPE_F32, None), "bf16")
     _rejects(L.eq_gguf_linear(16, 18, 16, 2 * 144, 12, 1, 2, 256, 0, bf16, None), "aligned")

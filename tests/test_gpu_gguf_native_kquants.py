@@ -1,0 +1,104 @@
+"""Native GGUF linear for Q5_K, Q6_K and Q5_1 (eq_gguf_linear, the encodings
+eredu keeps in their blocks besides Q4_K / Q8_0): y = x . W^T straight from
+the blocks, against the fp64 product with W from ggml's closed-form decoders
+(the unrounded factors the reference's native kernels use;
+tests/test_oracle_kquants.py pins those closed forms), within the matmul
+rule |y - y_ref| <= 1e-2 RMS(y_ref) + 1/2 ulp_bf16."""
+import numpy as np
+import pytest
+import torch
+
+from eredu_amd import EreduError
+from eredu_amd import gguf as G
+from oracle import oracle as orc
+from tests.fixtures import dev_bf16, dev_u8, host_f32, synthetic_blocks, synthetic_x
+from tests.test_oracle_kquants import _q5_closed, _q5k_closed, _q6k_closed, _to_big_endian
+
+pytestmark = pytest.mark.gpu
+
+T = G.GgmlType
+
+
+def closed_form(ty, raw, N, K):
+    if ty == T.Q5_1:
+        W = _q5_closed(raw, False)
+    elif ty == T.Q5K:
+        W = _q5k_closed(raw)[0]
+    else:
+        W = _q6k_closed(raw)[0]
+    return W.reshape(N, K)
+
+
+def run_case(ty, N, K, M, seed, endian=G.Endian.Little, offset=0):
+    vals, nbytes = ty.block_and_bytes()
+    raw = synthetic_blocks(int(ty), N * K // vals, seed=seed)
+    stored = _to_big_endian(int(ty), raw) if endian == G.Endian.Big else raw
+    buf = torch.zeros(stored.size + 16, dtype=torch.uint8, device="cuda")
+    buf[offset:offset + stored.size] = dev_u8(stored)
+    desc = G.TensorDescriptor("blk.0.ffn_down.weight", [K, N], ty, stored.size)
+    xb = synthetic_x(M, K, seed + 1)
+    y = G.linear(dev_bf16(xb), desc, buf[offset:offset + stored.size], endian)
+    assert list(y.shape) == [M, N] and y.dtype == torch.bfloat16
+    ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ closed_form(ty, raw, N, K).T
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(y), ref, True)
+    assert ok, (ty.name, N, K, M, endian, worst)
+
+
+# K: Q5_1 rows of 128 and 129 blocks; Q5_K / Q6_K rows of 5, 16 and 56
+# superblocks (8 rows per workgroup up to 64 KB of rows, 4 at K = 14336).
+# N = 390 leaves a partial row group (its bytes not a multiple of 16: the
+# 2-byte staging path); M = 11 takes two launches (8 + 3).
+CASES = [(T.Q5_1, 4096), (T.Q5_1, 4128), (T.Q5K, 1280), (T.Q5K, 4096), (T.Q6K, 1280), (T.Q6K, 4096),
+         (T.Q6K, 14336)]
+
+
+@pytest.mark.parametrize("ty,K", CASES)
+@pytest.mark.parametrize("M", [1, 3, 8, 11])
+def test_native_linear(cuda, ty, K, M):
+    print(f"[case] native {ty.name} N=390 K={K} M={M}", flush=True)
+    run_case(ty, 390, K, M, seed=K + M + int(ty))
+
+
+@pytest.mark.parametrize("ty", [T.Q5_1, T.Q5K, T.Q6K])
+def test_native_linear_big_endian_and_unaligned_payload(cuda, ty):
+    print(f"[case] native {ty.name} big-endian / offset payload", flush=True)
+    run_case(ty, 200, 2048, 2, seed=7, endian=G.Endian.Big)
+    run_case(ty, 200, 2048, 1, seed=8, offset=2)
+
+
+def test_native_q6k_row_longer_than_64k(cuda):
+    """One Q6_K row of 400 superblocks (84000 bytes): one row per workgroup
+    with LDS raised past 64 KB."""
+    print("[case] native Q6K K=102400", flush=True)
+    run_case(T.Q6K, 24, 102400, 1, seed=9)
+
+
+def test_llama_shapes_q6k_down_and_head(cuda):
+    """Q4_K_M files store ffn_down (and the output head) as Q6_K: 4096 x 14336
+    and a 4096-wide head of 32768 rows, at decode."""
+    print("[case] native Q6K 4096x14336 and 32768x4096", flush=True)
+    run_case(T.Q6K, 4096, 14336, 1, seed=10)
+    run_case(T.Q6K, 32768, 4096, 1, seed=11)
+
+
+def test_convert_keeps_the_new_native_types_in_blocks(cuda):
+    """convert.rs:125-140: little-endian Q5_K / Q6_K / Q5_1 stay native; the
+    NativeTensor's linear and dequantize run on the device."""
+    for ty in (T.Q5_1, T.Q5K, T.Q6K):
+        vals, _ = ty.block_and_bytes()
+        N, K = 64, 512
+        raw = synthetic_blocks(int(ty), N * K // vals, seed=4)
+        nt = G.convert(G.TensorDescriptor("w", [K, N], ty, raw.size), dev_u8(raw), G.Endian.Little)
+        assert isinstance(nt, G.NativeTensor) and nt.shape == [N, K]
+        xb = synthetic_x(2, K, 5)
+        ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ closed_form(ty, raw, N, K).T
+        ok, worst, _ = orc.matmul_within_tolerance(host_f32(nt.linear(dev_bf16(xb))), ref, True)
+        assert ok, (ty.name, worst)
+        dense = nt.dequantize(torch.float32).cpu().numpy().reshape(-1)
+        assert np.array_equal(dense.view(np.uint32), orc.gguf_dequant_f32(int(ty), raw, 1).view(np.uint32))
+
+
+def test_native_linear_refuses_non_native_types(cuda):
+    raw = dev_u8(np.zeros(84 * 2, np.uint8))
+    with pytest.raises(EreduError, match="no native linear"):
+        G.linear(dev_bf16(synthetic_x(1, 256, 0)), G.TensorDescriptor("w", [256, 2], T.Q2K, 168), raw)
