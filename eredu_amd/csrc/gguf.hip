@@ -767,33 +767,78 @@ __device__ __forceinline__ void kq_native_group(const uint8_t* b, int g, float& 
     }
 }
 
-template <int T, bool BIG, bool MANY>
-__global__ __launch_bounds__(256) void kq_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
-                                                 const uint8_t* __restrict__ raw, int M, int N, int K, int R,
-                                                 bool vec_ok) {
+constexpr int kKqStageVec = 8;  // 16-byte pieces per lane of one staged row group
+
+// Persistent workgroups walk row groups grp, grp + gridDim.x, ...; a full
+// group on a 16-byte-aligned payload is fetched into registers one group
+// ahead (its loads in flight while the current group is multiplied), a
+// ragged or unaligned one is staged with 2-byte loads when its turn comes.
+// Sums of x over every group of K are taken once per launch into LDS.
+template <int T, bool BIG, bool MANY, int W>
+__global__ __launch_bounds__(64 * W) void kq_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
+                                                    const uint8_t* __restrict__ raw, int M, int N, int K, int R,
+                                                    bool vec_ok) {
     using P = KQuant<T>;
-    constexpr int G = 32 / P::gs, VG = 32 / G;  // groups per unit, values per group
+    constexpr int G = 32 / P::gs, VG = 32 / G, NT = 64 * W;  // groups per unit, values per group
     extern __shared__ __attribute__((aligned(16))) uint16_t kq_lds[];
-    const int row_bytes = K / (32 * P::units) * P::bytes, U = K / 32;
+    const int row_bytes = K / (32 * P::units) * P::bytes, U = K / 32, ngk = K / VG;
+    const int gbytes = R * row_bytes;
+    float* sxs = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(kq_lds) + ((gbytes + 15) & ~15));
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wpr = R >= W ? 1 : W / R;  // waves per row (R is a power of two)
+    __shared__ float red[W * kLinRows];
     const uint32_t c43 = 0x43434343u;
-    for (int64_t n0 = int64_t(blockIdx.x) * R; n0 < N; n0 += int64_t(gridDim.x) * R) {
+    for (int i = threadIdx.x; i < M * ngk; i += NT) {
+        const uint4* xp = reinterpret_cast<const uint4*>(x + int64_t(i / ngk) * K + int64_t(i % ngk) * VG);
+        float sx = 0.f;
+#pragma unroll
+        for (int j = 0; j < VG / 8; j++) {
+            const uint4 v = xp[j];
+            sx = dot2_bf16(v.x, kBf16Ones, sx);
+            sx = dot2_bf16(v.y, kBf16Ones, sx);
+            sx = dot2_bf16(v.z, kBf16Ones, sx);
+            sx = dot2_bf16(v.w, kBf16Ones, sx);
+        }
+        sxs[i] = sx;
+    }
+    const int64_t ngroups = (int64_t(N) + R - 1) / R;
+    auto pipelined = [&](int64_t gi) { return vec_ok && (gi + 1) * R <= N; };
+    uint4 buf[kKqStageVec];
+    auto fetch = [&](int64_t gi) {
+        const uint4* src = reinterpret_cast<const uint4*>(raw + gi * gbytes);
+#pragma unroll
+        for (int i = 0; i < kKqStageVec; i++) {
+            const int idx = threadIdx.x + i * NT;
+            if (idx < gbytes / 16) buf[i] = load_stream16(src + idx);
+        }
+    };
+    int64_t grp = blockIdx.x;
+    if (grp < ngroups && pipelined(grp)) fetch(grp);
+    for (; grp < ngroups; grp += gridDim.x) {
+        const int64_t n0 = grp * R;
         const int nr = int(min<int64_t>(R, N - n0));
-        const int nbytes = nr * row_bytes;
-        const uint8_t* src = raw + n0 * row_bytes;
-        if (vec_ok && (nbytes & 15) == 0) {
-            for (int i = threadIdx.x; i < nbytes / 16; i += 256)
-                reinterpret_cast<uint4*>(kq_lds)[i] = load_stream16(src + 16 * int64_t(i));
+        if (pipelined(grp)) {
+#pragma unroll
+            for (int i = 0; i < kKqStageVec; i++) {
+                const int idx = threadIdx.x + i * NT;
+                if (idx < gbytes / 16) reinterpret_cast<uint4*>(kq_lds)[idx] = buf[i];
+            }
         } else {
-            for (int i = threadIdx.x; i < nbytes / 2; i += 256) kq_lds[i] = reinterpret_cast<const uint16_t*>(src)[i];
+            const uint16_t* src = reinterpret_cast<const uint16_t*>(raw + n0 * row_bytes);
+            for (int i = threadIdx.x; i < nr * row_bytes / 2; i += NT) kq_lds[i] = src[i];
         }
         __syncthreads();
-        for (int r = wave; r < nr; r += 4) {
+        const int64_t next = grp + gridDim.x;
+        if (next < ngroups && pipelined(next)) fetch(next);
+        // wpr waves per row when the group has fewer rows than waves: each
+        // takes every wpr-th run of 64 units, and their sums meet in red
+        for (int rb = 0; rb < nr; rb += W / wpr) {
+            const int r = rb + wave / wpr, part = wave % wpr;
             const uint8_t* row = reinterpret_cast<const uint8_t*>(kq_lds) + r * row_bytes;
             float acc[kLinRows];
 #pragma unroll
             for (int m = 0; m < kLinRows; m++) acc[m] = 0.f;
-            for (int u = lane; u < U; u += 64) {
+            for (int u = (r < nr ? part * 64 + lane : U); u < U; u += 64 * wpr) {
                 const uint8_t* b = row + (u / P::units) * P::bytes;
                 const int uu = u % P::units;
                 uint32_t cp[16];  // bf16 pairs (128 + q) of values 2j, 2j + 1
@@ -821,12 +866,10 @@ __global__ __launch_bounds__(256) void kq_linear(uint16_t* __restrict__ y, const
                     }
 #pragma unroll
                     for (int g = 0; g < G; g++) {
-                        float e = 0.f, sx = 0.f;
+                        float e = 0.f;
 #pragma unroll
-                        for (int j = 0; j < VG / 2; j++) {
-                            e = dot2_bf16(xw[g * VG / 2 + j], cp[g * VG / 2 + j], e);
-                            sx = dot2_bf16(xw[g * VG / 2 + j], kBf16Ones, sx);
-                        }
+                        for (int j = 0; j < VG / 2; j++) e = dot2_bf16(xw[g * VG / 2 + j], cp[g * VG / 2 + j], e);
+                        const float sx = sxs[m * ngk + u * G + g];
                         acc[m] += sc[g] * (e - 128.f * sx) + bi[g] * sx;
                     }
                 }
@@ -835,7 +878,21 @@ __global__ __launch_bounds__(256) void kq_linear(uint16_t* __restrict__ y, const
             for (int m = 0; m < (MANY ? kLinRows : 1); m++) {
                 if (m >= M) break;
                 const float v = wave_sum(acc[m]);
-                if (lane == 0) y[int64_t(m) * N + n0 + r] = uint16_t(f32_to_bf16_bits(v));
+                if (wpr == 1) {
+                    if (lane == 0 && r < nr) y[int64_t(m) * N + n0 + r] = uint16_t(f32_to_bf16_bits(v));
+                } else if (lane == 0) {
+                    red[wave * kLinRows + m] = v;
+                }
+            }
+            if (wpr > 1) {
+                __syncthreads();
+                const int t = threadIdx.x, rr = rb + t / (MANY ? kLinRows : 1), m = t % (MANY ? kLinRows : 1);
+                if (t < (W / wpr) * (MANY ? kLinRows : 1) && rr < nr && m < M) {
+                    float v = 0.f;
+                    for (int q = 0; q < wpr; q++) v += red[((rr - rb) * wpr + q) * kLinRows + m];
+                    y[int64_t(m) * N + n0 + rr] = uint16_t(f32_to_bf16_bits(v));
+                }
+                __syncthreads();
             }
         }
         __syncthreads();  // the rows are read before the next group is staged
@@ -1535,35 +1592,46 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
     if (kq) {
         // R weight rows per workgroup, staged whole in LDS: 8 while they fit
         // in 64 KB, fewer for long rows, one row up to the device's LDS
+        // R weight rows per group: as many as fit the register stage (up to
+        // 8, kKqStageVec 16-byte pieces per lane), then sums of x for up to
+        // kLinRows activation rows behind them in LDS.  A row longer than the
+        // stage takes groups of one row staged with 2-byte loads.
+        constexpr int W = 4;
         const int64_t row_bytes = K / geo.values * geo.bytes;
+        const int64_t stage = int64_t(kKqStageVec) * 16 * 64 * W;
         int R = 8;
-        while (R > 1 && R * row_bytes > 65536) R /= 2;
-        if (R * row_bytes > lds_limit()) {
+        while (R > 1 && R * row_bytes > stage) R /= 2;
+        const int64_t rows_lds = (R * row_bytes + 15) / 16 * 16;
+        const int64_t sx_row = (K / geo.gs) * 4;  // sums of x of one activation row
+        if (rows_lds + sx_row > lds_limit()) {
             set_error("native linear: one weight row (" + std::to_string(row_bytes) + " bytes) exceeds LDS");
             return 1;
         }
-        const int lds = int(R * row_bytes);
-        const bool vec_ok = aligned(raw, 16) && lds % 16 == 0;
-        const int64_t wgs = (N + R - 1) / R;
-        const unsigned grid = unsigned(wgs < 16384 ? wgs : 16384);
+        int mcap = kLinRows;  // activation rows per launch: as many as LDS holds, up to kLinRows
+        while (rows_lds + mcap * sx_row > lds_limit()) mcap--;
+        const bool vec_ok = aligned(raw, 16) && (R * row_bytes) % 16 == 0 && R * row_bytes <= stage;
+        const int64_t groups = (N + R - 1) / R;
+        const int64_t cap = int64_t(device_cu_count()) * 4;  // 2, 8, 32 per CU measured slower
+        const unsigned grid = unsigned(groups < cap ? groups : cap);
         if (!with_kq(ggml_type, big, [&](auto t, auto b) {
                 constexpr int T = decltype(t)::value;
                 if constexpr (T == EQ_GGML_Q5_1 || T == EQ_GGML_Q5_K || T == EQ_GGML_Q6_K) {
                     constexpr bool B = decltype(b)::value;
-                    for (int64_t m0 = 0; m0 < M; m0 += kLinRows) {
-                        const int mc = int(M - m0 < kLinRows ? M - m0 : kLinRows);
+                    for (int64_t m0 = 0; m0 < M; m0 += mcap) {
+                        const int mc = int(M - m0 < mcap ? M - m0 : mcap);
+                        const int lds = int(rows_lds + mc * sx_row);
                         auto go = [&](auto kernel) {
                             if (lds > 65536)
                                 (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-                            kernel<<<grid, 256, size_t(lds), st>>>(static_cast<uint16_t*>(y) + m0 * N,
+                            kernel<<<grid, 64 * W, size_t(lds), st>>>(static_cast<uint16_t*>(y) + m0 * N,
                                                                   static_cast<const uint16_t*>(x) + m0 * K, raw, mc,
                                                                   int(N), int(K), R, vec_ok);
                         };
                         if (mc == 1)
-                            go(kq_linear<T, B, false>);
+                            go(kq_linear<T, B, false, W>);
                         else
-                            go(kq_linear<T, B, true>);
+                            go(kq_linear<T, B, true, W>);
                     }
                 }
             }))
