@@ -162,12 +162,14 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
 
 /*
  * Native GGUF linear: y[M, N] = x[M, K] . W^T with W the GGUF tensor (MLX
- * shape [N, K], raw Q4_K or Q8_0 blocks as stored, raw_len bytes) decoded by
- * the native definition (Q4_K: d*sc*q - dmin*m, Q8_0: d*q) without an affine
- * expansion; f32 accumulation, bf16 x and y.  Replaces
- * NativeQuantizedTensor::linear with transpose = true
- * (safemlx/src/native_quantization.rs:741-772), whose CUDA/CPU builds decode
- * on the host (:846-913).  x 16-byte aligned; a Q4_K payload 16-byte aligned.
+ * shape [N, K], raw Q4_K, Q5_K, Q6_K, Q5_1 or Q8_0 blocks as stored, raw_len
+ * bytes) decoded by the native definition (Q4_K: d*sc*q - dmin*m, Q5_K the
+ * same with 5-bit q, Q6_K: d*sc*(q - 32), Q5_1: d*q + m, Q8_0: d*q; factors
+ * in f32, not rounded to f16) without an affine expansion; f32 accumulation,
+ * bf16 x and y.  Replaces NativeQuantizedTensor::linear with transpose = true
+ * (safemlx/src/native_quantization.rs:741-772; its Metal kernels for these
+ * formats at :1320-1400,1856), whose CUDA/CPU builds decode on the host
+ * (:846-913).  x 16-byte aligned; a Q4_K payload 16-byte aligned.
  */
 int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
                    int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream);
