@@ -358,10 +358,11 @@ def stream_convert(path: str, names: Optional[Sequence[str]] = None, staging_byt
 
 
 def stream_convert_affine(path: str, names: Optional[Sequence[str]] = None, staging_bytes: int = 256 << 20):
-    """stream_convert with every Q4_0 / Q8_0 / Q4_K tensor expanded to the
-    MLX affine triple (the explicit eredu_gguf::convert_affine,
-    convert.rs:318-465, which portable backends use); dense tensors as in
-    stream_convert.  Returns {name: AffineTensor | torch.Tensor (dense)}."""
+    """stream_convert with every quantized tensor of an affine type (Q4_0,
+    Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K) expanded to the MLX
+    affine triple (the explicit eredu_gguf::convert_affine, convert.rs:318-564,
+    which portable backends use); dense tensors as in stream_convert.  Returns
+    {name: AffineTensor | torch.Tensor (dense)}."""
     from . import gguf as G
 
     def conv(desc, raw, endian):

@@ -102,3 +102,55 @@ def test_native_linear_refuses_non_native_types(cuda):
     raw = dev_u8(np.zeros(84 * 2, np.uint8))
     with pytest.raises(EreduError, match="no native linear"):
         G.linear(dev_bf16(synthetic_x(1, 256, 0)), G.TensorDescriptor("w", [256, 2], T.Q2K, 168), raw)
+
+
+def test_streamed_file_of_every_affine_type(cuda, tmp_path):
+    """A GGUF file holding each of the seven added types, streamed through
+    small pinned buffers: stream_convert keeps the little-endian natives
+    (Q5_K, Q6_K, Q5_1) in blocks and expands the rest, each bit for bit;
+    stream_convert_affine expands all seven."""
+    from eredu_amd import gguf_file as F
+    from tests.fixtures import host_bits16
+
+    print("[case] stream every k-quant type", flush=True)
+    spec = [(T.Q4_1, 256, 12), (T.Q5_0, 256, 12), (T.Q5_1, 512, 8), (T.Q2K, 512, 6), (T.Q3K, 768, 5),
+            (T.Q5K, 512, 7), (T.Q6K, 1024, 9)]
+    tensors, raws = [], {}
+    for i, (ty, cols, rows) in enumerate(spec):
+        vals, _ = ty.block_and_bytes()
+        raw = synthetic_blocks(int(ty), rows * cols // vals, seed=70 + i)
+        name = f"blk.{i}.w.weight"
+        raws[name] = (ty, cols, rows, raw)
+        tensors.append((name, [cols, rows], int(ty), raw.tobytes()))
+    path = tmp_path / "k.gguf"
+    with open(path, "wb") as f:
+        F.write_gguf(f, {}, tensors, alignment=32)
+    routed = F.stream_convert(str(path), staging_bytes=4096)
+    expanded = F.stream_convert_affine(str(path), staging_bytes=4096)
+    for name, (ty, cols, rows, raw) in raws.items():
+        w, s, b = orc.gguf_convert_affine(int(ty), raw)
+        a = expanded[name]
+        assert np.array_equal(a.weights.cpu().numpy().view(np.uint32).reshape(-1), w), name
+        assert np.array_equal(host_bits16(a.scales).reshape(-1), s) and np.array_equal(host_bits16(a.biases).reshape(-1), b)
+        r = routed[name]
+        if ty.has_device_linear():
+            assert isinstance(r, G.NativeTensor) and r.shape == [rows, cols]
+            assert torch.equal(r.data.cpu(), torch.from_numpy(raw))
+        else:
+            assert isinstance(r, G.AffineTensor)
+            assert np.array_equal(r.weights.cpu().numpy().view(np.uint32).reshape(-1), w), name
+
+
+def test_native_layer_placeholder_for_q6k(cuda):
+    """QuantizedLinear.unloaded_iq (quantized.rs:709-750) for Q6_K block rows,
+    filled and run: forward is the native linear."""
+    from eredu_amd import QuantizedLinear
+
+    N, K = 48, 1024
+    raw = synthetic_blocks(int(T.Q6K), N * K // 256, seed=80)
+    lin = QuantizedLinear.unloaded_iq(K, N, int(T.Q6K), 0, False, torch.device("cuda"))
+    lin.weight.copy_(dev_u8(raw).view(N, -1))
+    xb = synthetic_x(3, K, 81)
+    ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ closed_form(T.Q6K, raw, N, K).T
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(lin.forward(dev_bf16(xb))), ref, True)
+    assert ok, worst
