@@ -72,14 +72,18 @@ class EreduError(RuntimeError):
 
 
 def lib() -> ctypes.CDLL:
+    """The HIP library: eredu_amd/_lib/liberedu_hip.so, or the file the
+    EREDU_AMD_LIB environment variable names (another build of it, e.g. the
+    sanitizer build of the host code that tests/test_host_sanitize.py makes)."""
     global _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(LIB_PATH):
+            path = os.environ.get("EREDU_AMD_LIB") or LIB_PATH
+            if not os.path.exists(path):
                 raise EreduError(
-                    f"HIP kernel library not found at {LIB_PATH}; build it with `python -m eredu_amd.build`"
+                    f"HIP kernel library not found at {path}; build it with `python -m eredu_amd.build`"
                 )
-            L = ctypes.CDLL(LIB_PATH)
+            L = ctypes.CDLL(path)
             for name, (args, res) in SIGNATURES.items():
                 fn = getattr(L, name)
                 fn.argtypes = args

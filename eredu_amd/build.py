@@ -73,5 +73,55 @@ def build(verbose: bool = True) -> str:
     return LIB_PATH
 
 
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer build (the C ABI's
+# argument checks, error state and planners; device code is built as usual).
+# Each sanitizer flag applies to the host compilation only.
+SAN_DIR = os.path.join(OBJ_DIR, "asan")
+SAN_LIB = os.path.join(SAN_DIR, "liberedu_hip_asan.so")
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address,undefined", "-Xarch_host", "-fno-sanitize-recover=all",
+             "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def _compile_sanitized(src: str) -> str:
+    obj = os.path.join(SAN_DIR, os.path.basename(src).replace(".hip", ".o"))
+    flags = [f for f in HIP_FLAGS if f != "-O3"] + ["-O1", "-g"]
+    res = subprocess.run([HIPCC, *flags, *SAN_FLAGS, "-c", src, "-o", obj], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc (sanitized host) failed for {src}:\n{res.stderr}")
+    return obj
+
+
+def build_host_sanitized() -> str:
+    """Builds ``_build/asan/liberedu_hip_asan.so`` (only when a source is newer
+    than it) and returns its path.  Load it with clang's ASan runtime preloaded
+    (``sanitizer_runtime()``) and ``EREDU_AMD_LIB`` pointing at it."""
+    os.makedirs(SAN_DIR, exist_ok=True)
+    srcs = sources()
+    newest = max(os.path.getmtime(f) for f in srcs + [os.path.join(ROOT, "include", "eredu_hip.h")] +
+                 [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hpp")])
+    if os.path.exists(SAN_LIB) and os.path.getmtime(SAN_LIB) > newest:
+        return SAN_LIB
+    workers = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), 8)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
+        objs = list(ex.map(_compile_sanitized, srcs))
+    tmp = SAN_LIB + ".tmp"
+    res = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *SAN_FLAGS, "-o", tmp, *objs],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link (sanitized host) failed:\n{res.stderr}")
+    os.replace(tmp, SAN_LIB)
+    return SAN_LIB
+
+
+def sanitizer_runtime() -> str:
+    """Path of the ASan runtime of hipcc's clang (to preload into a process
+    that loads the sanitized library)."""
+    clang = os.path.join(os.path.dirname(os.path.realpath(HIPCC)), "..", "lib", "llvm", "bin", "clang")
+    if not os.path.exists(clang):
+        clang = "/opt/rocm/llvm/bin/clang"
+    res = subprocess.run([clang, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    return res.stdout.strip()
+
+
 if __name__ == "__main__":
     build()
