@@ -219,7 +219,8 @@ def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
 def bench_gguf(steps, warmup):
     """GGUF 4096x14336 dequant (bf16) and convert (affine) GB/s,
     for every block type with an affine form (Q4_0 / Q8_0 / Q4_K first, the
-    configs' types)."""
+    configs' types), and dequant for IQ4_NL / IQ4_XS; the native linear at
+    M = 1 for the natively executed types."""
     import torch
 
     from eredu_amd import gguf as G
@@ -228,16 +229,17 @@ def bench_gguf(steps, warmup):
     rows, cols = 4096, 14336
     out = {}
     T = G.GgmlType
-    for ty in (T.Q4_0, T.Q8_0, T.Q4K, T.Q4_1, T.Q5_0, T.Q5_1, T.Q2K, T.Q3K, T.Q5K, T.Q6K):
+    for ty in (T.Q4_0, T.Q8_0, T.Q4K, T.Q4_1, T.Q5_0, T.Q5_1, T.Q2K, T.Q3K, T.Q5K, T.Q6K, T.IQ4NL, T.IQ4XS):
         vals, nbytes = ty.block_and_bytes()
         nraw = rows * cols // vals * nbytes
-        bits, gs = G.affine_config(ty)
+        affine = G.affine_config(ty) is not None  # (the IQ4 types have none: dequant and linear only)
+        bits, gs = G.affine_config(ty) if affine else (4, 32)
         conv_bytes = rows * cols * bits // 8 + 2 * 2 * rows * (cols // gs)
         # each copy is a distinct input and its own output, rotating >= ROTATE_BYTES
         copies = rotation(nraw + rows * cols * 2)
         raws = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(rotation(nraw))]
         dense = [torch.empty((rows, cols), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
-        cc = rotation(nraw + conv_bytes)
+        cc = rotation(nraw + conv_bytes) if affine else 0
         aw = [torch.empty((rows, cols * bits // 32), dtype=torch.int32, device="cuda") for _ in range(cc)]
         asb = [torch.empty((rows, cols // gs), dtype=torch.float16, device="cuda") for _ in range(cc)]
         abb = [torch.empty((rows, cols // gs), dtype=torch.float16, device="cuda") for _ in range(cc)]
@@ -252,8 +254,10 @@ def bench_gguf(steps, warmup):
                 n.check(n.lib().eq_gguf_convert_affine(aw[i].data_ptr(), asb[i].data_ptr(), abb[i].data_ptr(),
                                                        raws[i].data_ptr(), nraw, int(ty), rows, cols, 0, st))
 
-        for label, fn, out_bytes, k in (("dequant_bf16", deq, rows * cols * 2, copies),
-                                        (f"convert_affine_g{gs}", conv, conv_bytes, cc)):
+        legs = [("dequant_bf16", deq, rows * cols * 2, copies)]
+        if affine:
+            legs.append((f"convert_affine_g{gs}", conv, conv_bytes, cc))
+        for label, fn, out_bytes, k in legs:
             ms = Timer(fn).ms_per_replay(max(steps // 4, 5), warmup) / k
             gbs = (nraw + out_bytes) / (ms * 1e-3) / 1e9
             out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),

@@ -327,13 +327,34 @@ __global__ __launch_bounds__(256) void q4k_dense(const uint8_t* __restrict__ raw
 
 template <int T>
 struct KQuant;
-template <> struct KQuant<EQ_GGML_Q4_1> { static constexpr int bytes = 20, units = 1, bits = 4, gs = 32; };
-template <> struct KQuant<EQ_GGML_Q5_0> { static constexpr int bytes = 22, units = 1, bits = 5, gs = 32; };
-template <> struct KQuant<EQ_GGML_Q5_1> { static constexpr int bytes = 24, units = 1, bits = 5, gs = 32; };
-template <> struct KQuant<EQ_GGML_Q2_K> { static constexpr int bytes = 84, units = 8, bits = 2, gs = 16; };
-template <> struct KQuant<EQ_GGML_Q3_K> { static constexpr int bytes = 110, units = 8, bits = 3, gs = 16; };
-template <> struct KQuant<EQ_GGML_Q5_K> { static constexpr int bytes = 176, units = 8, bits = 5, gs = 32; };
-template <> struct KQuant<EQ_GGML_Q6_K> { static constexpr int bytes = 210, units = 8, bits = 6, gs = 16; };
+// levels: the codes index the IQ4 level table instead of being affine codes.
+template <> struct KQuant<EQ_GGML_Q4_1> { static constexpr int bytes = 20, units = 1, bits = 4, gs = 32; static constexpr bool levels = false; };
+template <> struct KQuant<EQ_GGML_Q5_0> { static constexpr int bytes = 22, units = 1, bits = 5, gs = 32; static constexpr bool levels = false; };
+template <> struct KQuant<EQ_GGML_Q5_1> { static constexpr int bytes = 24, units = 1, bits = 5, gs = 32; static constexpr bool levels = false; };
+template <> struct KQuant<EQ_GGML_Q2_K> { static constexpr int bytes = 84, units = 8, bits = 2, gs = 16; static constexpr bool levels = false; };
+template <> struct KQuant<EQ_GGML_Q3_K> { static constexpr int bytes = 110, units = 8, bits = 3, gs = 16; static constexpr bool levels = false; };
+template <> struct KQuant<EQ_GGML_Q5_K> { static constexpr int bytes = 176, units = 8, bits = 5, gs = 32; static constexpr bool levels = false; };
+template <> struct KQuant<EQ_GGML_Q6_K> { static constexpr int bytes = 210, units = 8, bits = 6, gs = 16; static constexpr bool levels = false; };
+template <> struct KQuant<EQ_GGML_IQ4_NL> { static constexpr int bytes = 18, units = 1, bits = 4, gs = 32; static constexpr bool levels = true; };
+template <> struct KQuant<EQ_GGML_IQ4_XS> { static constexpr int bytes = 136, units = 8, bits = 4, gs = 32; static constexpr bool levels = true; };
+
+// The 16 levels of IQ4_NL / IQ4_XS (the GGML format's kvalues_iq4nl; the
+// reference's KVALUES_IQ4NL, eredu-gguf/src/iquant_tables.rs:1920), each plus
+// 128 (1 .. 241) as the bytes of four words: entries 4w .. 4w + 3 in word w.
+constexpr uint32_t kIq4Lut0 = 1u | (24u << 8) | (45u << 16) | (63u << 24);      // -127 -104 -83 -65
+constexpr uint32_t kIq4Lut1 = 79u | (93u << 8) | (106u << 16) | (118u << 24);   //  -49  -35 -22 -10
+constexpr uint32_t kIq4Lut2 = 129u | (141u << 8) | (153u << 16) | (166u << 24); //    1   13  25  38
+constexpr uint32_t kIq4Lut3 = 181u | (197u << 8) | (217u << 16) | (241u << 24); //   53   69  89 113
+
+// Nibble codes in byte lanes -> level + 128 in the same lanes: two byte
+// permutes pick from entries 0..7 and 8..15, bit 3 of each code chooses.
+__device__ __forceinline__ uint32_t iq4_level_bytes(uint32_t c) {
+    const uint32_t sel = c & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4Lut1, kIq4Lut0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4Lut3, kIq4Lut2, sel);
+    const uint32_t m = ((c >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
 
 // f16 field at byte offset o of a block in LDS.
 template <bool BIG>
@@ -360,7 +381,14 @@ __device__ __forceinline__ uint32_t spread4(uint32_t t) { return ((t & 15u) * 0x
 template <int T, bool BIG>
 __device__ __forceinline__ void kq_codes8(const uint8_t* b, int u, int i0, uint32_t& c0, uint32_t& c1) {
     uint32_t a0, a1, h0, h1;
-    if constexpr (T == EQ_GGML_Q4_1) {
+    if constexpr (T == EQ_GGML_IQ4_NL || T == EQ_GGML_IQ4_XS) {
+        // level indices: byte 2 + i (IQ4_NL) or 8 + 16 ib + i (IQ4_XS, unit = group ib)
+        // holds value i in its low nibble and value 16 + i in its high (iquant.rs:271-301)
+        lds_8b(b + (T == EQ_GGML_IQ4_NL ? 2 : 8 + 16 * u) + (i0 & 15), a0, a1);
+        const int sh = (i0 >> 4) * 4;
+        c0 = (a0 >> sh) & 0x0f0f0f0fu;
+        c1 = (a1 >> sh) & 0x0f0f0f0fu;
+    } else if constexpr (T == EQ_GGML_Q4_1) {
         // low nibbles of bytes 4..20 are values 0..15, high nibbles 16..31 (convert.rs:367-370)
         lds_8b(b + 4 + (i0 & 15), a0, a1);
         const int sh = (i0 >> 4) * 4;
@@ -454,6 +482,34 @@ __device__ __forceinline__ void kq_group(const uint8_t* b, int g, uint32_t& sb, 
         const float sc = f16_bits_to_f32(lds_half<BIG>(b, 208)) * float(int8_t(b[192 + g]));
         sb = f32_to_f16_bits(sc);
         bb = f32_to_f16_bits(-32.0f * sc);
+    }
+}
+
+// Group factors in f32 without f16 rounding: the native definition (and, for
+// the IQ4 types, the only one).
+template <int T, bool BIG>
+__device__ __forceinline__ void kq_native_group(const uint8_t* b, int g, float& scale, float& bias) {
+    if constexpr (T == EQ_GGML_Q5_1) {
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 0));  // native_quantization.rs:3499-3509
+        bias = f16_bits_to_f32(lds_half<BIG>(b, 2));
+    } else if constexpr (T == EQ_GGML_Q5_K) {
+        uint32_t sc, m;
+        scale_min_bytes(b + 4, g, sc, m);
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 0)) * float(sc);
+        bias = -(f16_bits_to_f32(lds_half<BIG>(b, 2)) * float(m));
+    } else if constexpr (T == EQ_GGML_IQ4_NL) {
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 0));  // iquant.rs:273
+        bias = 0.f;
+    } else if constexpr (T == EQ_GGML_IQ4_XS) {
+        // 6-bit ls: nibble g % 2 of byte 4 + g / 2, bits 2g, 2g + 1 of the u16 at 2 (iquant.rs:287-290)
+        const uint32_t ls = ((uint32_t(b[4 + (g >> 1)]) >> (4 * (g & 1))) & 15u) |
+                            (((lds_half<BIG>(b, 2) >> (2 * g)) & 3u) << 4);
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 0)) * float(int(ls) - 32);
+        bias = 0.f;
+    } else {
+        static_assert(T == EQ_GGML_Q6_K, "native linear covers Q5_1, Q5_K, Q6_K, IQ4_NL and IQ4_XS here");
+        scale = f16_bits_to_f32(lds_half<BIG>(b, 208)) * float(int8_t(b[192 + g]));
+        bias = -32.0f * scale;
     }
 }
 
@@ -555,15 +611,31 @@ __global__ __launch_bounds__(256) void kq_dense(const uint8_t* __restrict__ raw,
         const int lb = lu / P::units, u = lu % P::units;
         if (lb >= nb) break;
         const uint8_t* b = reinterpret_cast<const uint8_t*>(lds) + lb * P::bytes;
-        uint32_t sb, bb, c0, c1;
-        kq_group<T, BIG>(b, (u * 32 + 8 * c) / P::gs, sb, bb);
+        uint32_t c0, c1;
         kq_codes8<T, BIG>(b, u, 8 * c, c0, c1);
-        const float scale = f16_bits_to_f32(sb), bv = f16_bits_to_f32(bb);
+        float scale, bv;
+        if constexpr (P::levels) {
+            // w = factor * level, level = (level + 128) - 128 exactly; the
+            // product is exact in f32, as in the reference (iquant.rs:275, 294),
+            // and carries its sign of zero (a zero factor)
+            kq_native_group<T, BIG>(b, (u * 32 + 8 * c) / P::gs, scale, bv);
+            c0 = iq4_level_bytes(c0);
+            c1 = iq4_level_bytes(c1);
+        } else {
+            uint32_t sb, bb;
+            kq_group<T, BIG>(b, (u * 32 + 8 * c) / P::gs, sb, bb);
+            scale = f16_bits_to_f32(sb), bv = f16_bits_to_f32(bb);
+        }
         float v[8];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            v[i] = scale * float((c0 >> (8 * i)) & 0xffu) + bv;
-            v[4 + i] = scale * float((c1 >> (8 * i)) & 0xffu) + bv;
+            if constexpr (P::levels) {
+                v[i] = scale * (float((c0 >> (8 * i)) & 0xffu) - 128.f);
+                v[4 + i] = scale * (float((c1 >> (8 * i)) & 0xffu) - 128.f);
+            } else {
+                v[i] = scale * float((c0 >> (8 * i)) & 0xffu) + bv;
+                v[4 + i] = scale * float((c1 >> (8 * i)) & 0xffu) + bv;
+            }
         }
         store8<OUT>(out, ((blk0 + lb) * P::units + u) * 32 + 8 * c, v);
     }
@@ -750,22 +822,6 @@ __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, cons
 // the codes come from kq_codes8 as byte lanes, are turned into bf16 pairs
 // 128 + q by byte permutes, and meet x in v_dot2c_f32_bf16; per group
 // sum x q = e - 128 sum x.  Up to kLinRows activation rows per launch.
-template <int T, bool BIG>
-__device__ __forceinline__ void kq_native_group(const uint8_t* b, int g, float& scale, float& bias) {
-    if constexpr (T == EQ_GGML_Q5_1) {
-        scale = f16_bits_to_f32(lds_half<BIG>(b, 0));  // native_quantization.rs:3499-3509
-        bias = f16_bits_to_f32(lds_half<BIG>(b, 2));
-    } else if constexpr (T == EQ_GGML_Q5_K) {
-        uint32_t sc, m;
-        scale_min_bytes(b + 4, g, sc, m);
-        scale = f16_bits_to_f32(lds_half<BIG>(b, 0)) * float(sc);
-        bias = -(f16_bits_to_f32(lds_half<BIG>(b, 2)) * float(m));
-    } else {
-        static_assert(T == EQ_GGML_Q6_K, "native linear covers Q5_1, Q5_K and Q6_K here");
-        scale = f16_bits_to_f32(lds_half<BIG>(b, 208)) * float(int8_t(b[192 + g]));
-        bias = -32.0f * scale;
-    }
-}
 
 constexpr int kKqStageVec = 8;  // 16-byte pieces per lane of one staged row group
 
@@ -846,10 +902,20 @@ __global__ __launch_bounds__(64 * W) void kq_linear(uint16_t* __restrict__ y, co
                 for (int q = 0; q < 4; q++) {
                     uint32_t c0, c1;
                     kq_codes8<T, BIG>(b, uu, 8 * q, c0, c1);
-                    cp[4 * q] = __builtin_amdgcn_perm(c43, c0, 0x04010400u);
-                    cp[4 * q + 1] = __builtin_amdgcn_perm(c43, c0, 0x04030402u);
-                    cp[4 * q + 2] = __builtin_amdgcn_perm(c43, c1, 0x04010400u);
-                    cp[4 * q + 3] = __builtin_amdgcn_perm(c43, c1, 0x04030402u);
+                    if constexpr (P::levels) {
+                        // level + 128 (up to 241: exact in bf16, past the 0x43 trick's
+                        // range) converted per byte
+                        const uint32_t l0 = iq4_level_bytes(c0), l1 = iq4_level_bytes(c1);
+                        cp[4 * q] = pack_bf16x2(float(l0 & 0xffu), float((l0 >> 8) & 0xffu));
+                        cp[4 * q + 1] = pack_bf16x2(float((l0 >> 16) & 0xffu), float(l0 >> 24));
+                        cp[4 * q + 2] = pack_bf16x2(float(l1 & 0xffu), float((l1 >> 8) & 0xffu));
+                        cp[4 * q + 3] = pack_bf16x2(float((l1 >> 16) & 0xffu), float(l1 >> 24));
+                    } else {
+                        cp[4 * q] = __builtin_amdgcn_perm(c43, c0, 0x04010400u);
+                        cp[4 * q + 1] = __builtin_amdgcn_perm(c43, c0, 0x04030402u);
+                        cp[4 * q + 2] = __builtin_amdgcn_perm(c43, c1, 0x04010400u);
+                        cp[4 * q + 3] = __builtin_amdgcn_perm(c43, c1, 0x04030402u);
+                    }
                 }
                 float sc[G], bi[G];
 #pragma unroll
@@ -1222,6 +1288,7 @@ __global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, con
 
 struct Geometry {
     int values, bytes, bits, gs;
+    bool affine = true;  // has an affine form (convert.rs:142-152); the IQ4 types do not
 };
 
 bool geometry(int type, Geometry& g) {
@@ -1236,6 +1303,8 @@ bool geometry(int type, Geometry& g) {
     case EQ_GGML_Q4_K: g = {256, 144, 4, 32}; return true;
     case EQ_GGML_Q5_K: g = {256, 176, 5, 32}; return true;
     case EQ_GGML_Q6_K: g = {256, 210, 6, 16}; return true;
+    case EQ_GGML_IQ4_NL: g = {32, 18, 4, 32, false}; return true;
+    case EQ_GGML_IQ4_XS: g = {256, 136, 4, 32, false}; return true;
     default: return false;
     }
 }
@@ -1245,7 +1314,7 @@ int validate(const uint8_t* raw, int64_t raw_len, int type, int64_t rows, int64_
              Geometry& geo, int64_t& nblocks) {
     if (!geometry(type, geo)) {
         set_error("unsupported GGML tensor type " + std::to_string(type) +
-                  " (device path covers Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)");
+                  " (device path covers Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS)");
         return 1;
     }
     if (endian != EQ_ENDIAN_LITTLE && endian != EQ_ENDIAN_BIG) {
@@ -1301,6 +1370,8 @@ bool with_kq(int type, bool big, F&& f) {
     case EQ_GGML_Q3_K: return go(std::integral_constant<int, EQ_GGML_Q3_K>{});
     case EQ_GGML_Q5_K: return go(std::integral_constant<int, EQ_GGML_Q5_K>{});
     case EQ_GGML_Q6_K: return go(std::integral_constant<int, EQ_GGML_Q6_K>{});
+    case EQ_GGML_IQ4_NL: return go(std::integral_constant<int, EQ_GGML_IQ4_NL>{});
+    case EQ_GGML_IQ4_XS: return go(std::integral_constant<int, EQ_GGML_IQ4_XS>{});
     default: return false;
     }
 }
@@ -1317,6 +1388,10 @@ extern "C" int eq_gguf_convert_affine(uint32_t* weights, uint16_t* scales, uint1
     Geometry geo;
     int64_t nblocks;
     if (validate(raw, raw_len, ggml_type, rows, cols, endian, geo, nblocks)) return 1;
+    if (!geo.affine) {
+        set_error("tensor encoding has no affine conversion (GGML type " + std::to_string(ggml_type) + ")");
+        return 1;
+    }
     if (!weights || !scales || !biases) {
         set_error("null output pointer");
         return 1;
@@ -1332,8 +1407,9 @@ extern "C" int eq_gguf_convert_affine(uint32_t* weights, uint16_t* scales, uint1
     if (with_kq(ggml_type, big, [&](auto t, auto b) {
             constexpr int T = decltype(t)::value;
             constexpr int NB = 256 / KQuant<T>::units;
-            kq_to_affine<T, decltype(b)::value><<<dim3(unsigned((nblocks + NB - 1) / NB)), 256, 0, st>>>(
-                raw, nblocks, vec_ok, weights, scales, biases);
+            if constexpr (!KQuant<T>::levels)
+                kq_to_affine<T, decltype(b)::value><<<dim3(unsigned((nblocks + NB - 1) / NB)), 256, 0, st>>>(
+                    raw, nblocks, vec_ok, weights, scales, biases);
         }))
         return check_launch("gguf convert_affine");
     if (ggml_type == EQ_GGML_Q4_K) {
@@ -1562,9 +1638,10 @@ extern "C" int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len
 extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
                               int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream) {
     clear_error();
-    const bool kq = ggml_type == EQ_GGML_Q5_1 || ggml_type == EQ_GGML_Q5_K || ggml_type == EQ_GGML_Q6_K;
+    const bool kq = ggml_type == EQ_GGML_Q5_1 || ggml_type == EQ_GGML_Q5_K || ggml_type == EQ_GGML_Q6_K ||
+                    ggml_type == EQ_GGML_IQ4_NL || ggml_type == EQ_GGML_IQ4_XS;
     if (ggml_type != EQ_GGML_Q4_K && ggml_type != EQ_GGML_Q8_0 && !kq) {
-        set_error("native GGUF linear covers Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0");
+        set_error("native GGUF linear covers Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL and IQ4_XS");
         return 1;
     }
     Geometry geo;
@@ -1615,7 +1692,8 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
         const unsigned grid = unsigned(groups < cap ? groups : cap);
         if (!with_kq(ggml_type, big, [&](auto t, auto b) {
                 constexpr int T = decltype(t)::value;
-                if constexpr (T == EQ_GGML_Q5_1 || T == EQ_GGML_Q5_K || T == EQ_GGML_Q6_K) {
+                if constexpr (T == EQ_GGML_Q5_1 || T == EQ_GGML_Q5_K || T == EQ_GGML_Q6_K || T == EQ_GGML_IQ4_NL ||
+                              T == EQ_GGML_IQ4_XS) {
                     constexpr bool B = decltype(b)::value;
                     for (int64_t m0 = 0; m0 < M; m0 += mcap) {
                         const int mc = int(M - m0 < mcap ? M - m0 : mcap);

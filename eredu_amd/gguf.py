@@ -22,9 +22,10 @@ from ._native import EreduError, check
 
 class GgmlType(enum.IntEnum):
     """GGML tensor type codes (eredu-gguf/src/format.rs:295-365).  The device
-    path converts and dequantizes every type with an affine form and executes
-    Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0 blocks natively; the rest are named so
-    that routing (``conversion_kind``) covers every code the container holds."""
+    path converts and dequantizes every type with an affine form, dequantizes
+    IQ4_NL / IQ4_XS, and executes Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL and
+    IQ4_XS blocks natively; the rest are named so that routing
+    (``conversion_kind``) covers every code the container holds."""
 
     F32 = 0
     F16 = 1
@@ -69,14 +70,15 @@ class GgmlType(enum.IntEnum):
         return self in (GgmlType.Q4K, GgmlType.Q5K, GgmlType.Q6K, GgmlType.Q5_1, GgmlType.Q8_0) or self.is_iq()
 
     def has_device_kernels(self) -> bool:
-        """Encodings this library converts and dequantizes: those with an
-        affine form (convert.rs:142-152)."""
-        return affine_config(self) is not None
+        """Encodings this library dequantizes (and, with an affine form,
+        convert.rs:142-152, converts): the ten affine types, IQ4_NL, IQ4_XS."""
+        return affine_config(self) is not None or self in (GgmlType.IQ4NL, GgmlType.IQ4XS)
 
     def has_device_linear(self) -> bool:
         """Encodings this library multiplies straight from their blocks
         (eq_gguf_linear): the non-IQ encodings eredu executes natively."""
-        return self in (GgmlType.Q8_0, GgmlType.Q4K, GgmlType.Q5K, GgmlType.Q6K, GgmlType.Q5_1)
+        return self in (GgmlType.Q8_0, GgmlType.Q4K, GgmlType.Q5K, GgmlType.Q6K, GgmlType.Q5_1, GgmlType.IQ4NL,
+                        GgmlType.IQ4XS)
 
 
 _BLOCK_AND_BYTES = {
@@ -221,6 +223,8 @@ def convert_affine(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = E
     """GGML blocks -> MLX affine triple, byte-identical to
     eredu_gguf::convert_affine (convert.rs:318-564); C ABI eq_gguf_convert_affine."""
     ty = _device_type(desc)
+    if affine_config(ty) is None:  # convert.rs:329-330
+        raise EreduError(f"tensor '{desc.name}': tensor encoding has no affine conversion")
     _check_raw(desc, raw)
     shape, rows, cols = _rows_cols(desc)
     bits, gs = affine_config(ty)
@@ -281,7 +285,7 @@ def linear(x: torch.Tensor, desc: TensorDescriptor, raw: torch.Tensor, endian: E
     ty = _device_type(desc)
     if not ty.has_device_linear():
         raise EreduError(f"tensor '{desc.name}': no native linear for GGML type {int(ty)} "
-                         f"(Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0)")
+                         f"(Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL and IQ4_XS)")
     _check_raw(desc, raw)
     shape, N, K = _rows_cols(desc)
     if len(shape) != 2:
@@ -324,7 +328,8 @@ class NativeTensor:
 
     def dequantize_f32(self) -> torch.Tensor:
         """IQuantTensor::dequantize_f32 (convert.rs:43-56): for the non-IQ
-        encodings the affine route, convert_affine then AffineTensor::dequantize."""
+        encodings the affine route, convert_affine then AffineTensor::dequantize;
+        IQ4_NL / IQ4_XS decode factor x level (iquant.rs:271-301)."""
         return dequantize(self.descriptor(), self.data, self.endian, DequantDefinition.Affine, torch.float32)
 
     def dequantize(self, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
@@ -420,7 +425,7 @@ def convert(desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.L
     if kind.kind == "native":
         if not ty.has_device_linear():
             raise EreduError(f"tensor '{desc.name}': GGML type {int(ty)} stays native in eredu, and this library "
-                             f"executes only Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0 blocks")
+                             f"executes only Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL and IQ4_XS blocks")
         shape = desc.mlx_shape()
         values, _ = ty.block_and_bytes()
         if not shape or shape[-1] % values != 0:

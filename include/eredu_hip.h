@@ -33,7 +33,8 @@ enum eq_dtype { EQ_DTYPE_F32 = 0, EQ_DTYPE_F16 = 1, EQ_DTYPE_BF16 = 2, EQ_DTYPE_
 /* GGML block types handled on the device (codes of eredu-gguf/src/format.rs:297-330). */
 enum eq_ggml_type {
     EQ_GGML_Q4_0 = 2, EQ_GGML_Q4_1 = 3, EQ_GGML_Q5_0 = 6, EQ_GGML_Q5_1 = 7, EQ_GGML_Q8_0 = 8,
-    EQ_GGML_Q2_K = 10, EQ_GGML_Q3_K = 11, EQ_GGML_Q4_K = 12, EQ_GGML_Q5_K = 13, EQ_GGML_Q6_K = 14
+    EQ_GGML_Q2_K = 10, EQ_GGML_Q3_K = 11, EQ_GGML_Q4_K = 12, EQ_GGML_Q5_K = 13, EQ_GGML_Q6_K = 14,
+    EQ_GGML_IQ4_NL = 20, EQ_GGML_IQ4_XS = 23 /* dequantize and native linear only: no affine form */
 };
 
 /* Byte order of multi-byte block fields (eredu-gguf/src/format.rs:5-23 Endian). */

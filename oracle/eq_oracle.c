@@ -24,6 +24,9 @@
  *                                    the reference test's tolerance and exact
  *                                    under MLX's two-rounding f16 arithmetic),
  *                                    the Q5_0/Q5_1 rows' f16 weights (exact).
+ *   or_iq4_dequant_f32               pinned: llama-c0bc8591-iq.oracle rows 20, 23
+ *                                    (llama.cpp's f16 outputs, exact), zero
+ *                                    blocks, byte-order swap (iquant.rs tests).
  *   or_gguf_dequant_f32 (native)     pinned: closed form d*sc*q - dmin*m in
  *                                    f64, and the <=1e-6 native-vs-affine
  *                                    tests' sample blocks.
@@ -120,7 +123,8 @@ static float load_scalar(const void* p, int dtype, int64_t i) {
 
 enum {
     OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8,
-    OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14
+    OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14,
+    OR_IQ4_NL = 20, OR_IQ4_XS = 23
 };
 
 static uint16_t rd16(const uint8_t* b, int big_endian) {
@@ -169,6 +173,8 @@ int or_gguf_block_geometry(int type, int* values, int* bytes) {
     case OR_Q4_K: *values = 256; *bytes = 144; return 0;
     case OR_Q5_K: *values = 256; *bytes = 176; return 0;
     case OR_Q6_K: *values = 256; *bytes = 210; return 0;
+    case OR_IQ4_NL: *values = 32; *bytes = 18; return 0;
+    case OR_IQ4_XS: *values = 256; *bytes = 136; return 0;
     default: return 1;
     }
 }
@@ -387,6 +393,56 @@ void or_affine_dequant_f32(const uint32_t* w, const void* scales, const void* bi
     }
 }
 
+/* The 16 non-uniform 4-bit levels of IQ4_NL / IQ4_XS: the GGML format's
+ * table (kvalues_iq4nl; the reference's copy is KVALUES_IQ4NL,
+ * eredu-gguf/src/iquant_tables.rs:1920). */
+static const int8_t kIq4Levels[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/*
+ * IQ4_NL / IQ4_XS blocks -> f32, the reference's decode_f32 for these types
+ * (eredu-gguf/src/iquant.rs:271-301):
+ *   IQ4_NL (32 values, 18 B): d = f16 at 0; byte 2 + i holds value i (low
+ *     nibble) and value 16 + i (high nibble); w = d * level[nibble].
+ *   IQ4_XS (256 values, 136 B): d = f16 at 0, scales_high u16 at 2, scales_low
+ *     bytes 4..8, codes at 8; group ib (32 values): 6-bit ls = nibble ib % 2 of
+ *     scales_low[ib / 2] | bits 2 ib, 2 ib + 1 of scales_high << 4;
+ *     dl = d * (ls - 32); codes 8 + 16 ib + i as in IQ4_NL; w = dl * level.
+ * Every product is exact in f32 (the levels need 8 bits, dl at most 17).
+ * Returns 0, or 1 for another type.
+ */
+int or_iq4_dequant_f32(int type, int big_endian, const uint8_t* raw, int64_t nblocks, float* out) {
+    if (type == OR_IQ4_NL) {
+        for (int64_t blk = 0; blk < nblocks; blk++) {
+            const uint8_t* p = raw + blk * 18;
+            float d = or_f16_to_f32(rd16(p, big_endian));
+            for (int i = 0; i < 16; i++) {
+                out[blk * 32 + i] = d * (float)kIq4Levels[p[2 + i] & 15];
+                out[blk * 32 + 16 + i] = d * (float)kIq4Levels[p[2 + i] >> 4];
+            }
+        }
+        return 0;
+    }
+    if (type == OR_IQ4_XS) {
+        for (int64_t blk = 0; blk < nblocks; blk++) {
+            const uint8_t* p = raw + blk * 136;
+            float d = or_f16_to_f32(rd16(p, big_endian));
+            uint16_t sh = rd16(p + 2, big_endian);
+            for (int ib = 0; ib < 8; ib++) {
+                int low = (p[4 + ib / 2] >> (4 * (ib % 2))) & 15;
+                int high = (sh >> (2 * ib)) & 3;
+                float dl = d * (float)((low | (high << 4)) - 32);
+                const uint8_t* q = p + 8 + 16 * ib;
+                for (int i = 0; i < 16; i++) {
+                    out[blk * 256 + 32 * ib + i] = dl * (float)kIq4Levels[q[i] & 15];
+                    out[blk * 256 + 32 * ib + 16 + i] = dl * (float)kIq4Levels[q[i] >> 4];
+                }
+            }
+        }
+        return 0;
+    }
+    return 1;
+}
+
 /*
  * Dense dequant of GGML blocks to f32.
  * definition 0 ("affine route"): convert_affine then AffineTensor::dequantize
@@ -404,6 +460,7 @@ int or_gguf_dequant_f32(int type, int big_endian, int definition, const uint8_t*
                         float* out) {
     int values, bytes;
     if (or_gguf_block_geometry(type, &values, &bytes)) return 1;
+    if (type == OR_IQ4_NL || type == OR_IQ4_XS) return or_iq4_dequant_f32(type, big_endian, raw, nblocks, out);
     if (definition == 1 && type == OR_Q4_K) {
         for (int64_t blk = 0; blk < nblocks; blk++) {
             const uint8_t* p = raw + blk * 144;

@@ -39,6 +39,8 @@ BLOCK_GEOMETRY = {Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24)
 AFFINE_CONFIG = {Q4_0: (4, 32), Q4_1: (4, 32), Q5_0: (5, 32), Q5_1: (5, 32), Q8_0: (8, 32),
                  Q2_K: (2, 16), Q3_K: (3, 16), Q4_K: (4, 32), Q5_K: (5, 32), Q6_K: (6, 16)}  # convert.rs:142-152
 GGUF_TYPES = tuple(BLOCK_GEOMETRY)
+IQ4_NL, IQ4_XS = 20, 23
+BLOCK_GEOMETRY.update({IQ4_NL: (32, 18), IQ4_XS: (256, 136)})  # format.rs:368-400 (no affine form)
 
 _lib = None
 

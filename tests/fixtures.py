@@ -18,6 +18,23 @@ def parse_field(field: str):
     return prefix, dtype, data
 
 
+GOLDEN_IQ = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "llama-c0bc8591-iq.oracle")
+
+
+def golden_iq_rows():
+    """{ggml code: (raw block bytes, expected f16 bits)} of llama-c0bc8591-iq.oracle
+    (eredu-gguf/tests/iquant.rs:113-127: two blocks per IQ type, llama.cpp's
+    outputs rounded to f16, native byte order)."""
+    rows = {}
+    with open(GOLDEN_IQ) as f:
+        for line in f:
+            line = line.strip()
+            if line:
+                code, raw, expected = line.split("|")
+                rows[int(code)] = (unhex(raw), np.frombuffer(unhex(expected), dtype="<u2").copy())
+    return rows
+
+
 def golden_rows():
     """{ggml code: dict(raw=bytes, weight=bytes, scales=bytes, biases=bytes, dequantized=bytes, block=int)}"""
     rows = {}
@@ -56,6 +73,8 @@ KQUANT_HEADERS = {
     11: (110, (108,), ()),    # Q3_K: d
     13: (176, (0, 2), ()),    # Q5_K: d, dmin
     14: (210, (208,), ()),    # Q6_K: d
+    20: (18, (0,), ()),       # IQ4_NL: d
+    23: (136, (0,), ()),      # IQ4_XS: d (the u16 of high scale bits at 2 stays random)
 }
 
 

@@ -112,6 +112,7 @@ def test_error_message_is_thread_local():
         (dict(ty=39), "unsupported GGML tensor type"),
         (dict(cols=48), "not divisible by group size 32"),
         (dict(cols=264, ty=14), "not divisible by group size 16"),
+        (dict(ty=20), "no affine conversion"),
         (dict(cols=288, ty=12), "not divisible by block length 256"),
         (dict(raw_len=17), "payload length does not match descriptor"),
         (dict(endian=5), "invalid endian"),
@@ -208,8 +209,8 @@ def test_quantize_rejects_bad_arguments():
 def test_gguf_linear_rejects_bad_arguments():
     bf16 = _native.EQ_DTYPE_BF16
     # Q4_0 is not a native-linear type; payload length must match; bf16 only
-    _rejects(L.eq_gguf_linear(16, 16, 16, 18 * 8, 2, 1, 2, 128, 0, bf16, None), "Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0")
-    _rejects(L.eq_gguf_linear(16, 16, 16, 84 * 2, 10, 1, 2, 256, 0, bf16, None), "Q4_K, Q5_K, Q6_K, Q5_1 and Q8_0")
+    _rejects(L.eq_gguf_linear(16, 16, 16, 18 * 8, 2, 1, 2, 128, 0, bf16, None), "Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL and IQ4_XS")
+    _rejects(L.eq_gguf_linear(16, 16, 16, 84 * 2, 10, 1, 2, 256, 0, bf16, None), "Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL and IQ4_XS")
     _rejects(L.eq_gguf_linear(16, 16, 16, 100, 12, 1, 2, 256, 0, bf16, None), "payload length")
     _rejects(L.eq_gguf_linear(16, 16, 16, 2 * 144, 12, 1, 2, 256, 0, _native.EQ_DTYPE_F32, None), "bf16")
     _rejects(L.eq_gguf_linear(16, 18, 16, 2 * 144, 12, 1, 2, 256, 0, bf16, None), "aligned")

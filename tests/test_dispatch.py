@@ -41,7 +41,7 @@ def test_block_geometry_table():
     assert T.Q4_0.block_and_bytes() == (32, 18) and T.MXFP4.block_and_bytes() == (32, 17)
     assert T.IQ4XS.block_and_bytes() == (256, 136) and T.F64.block_and_bytes() == (1, 8)
     assert [t for t in T if t.has_device_kernels()] == [T.Q4_0, T.Q4_1, T.Q5_0, T.Q5_1, T.Q8_0, T.Q2K, T.Q3K,
-                                                        T.Q4K, T.Q5K, T.Q6K]
+                                                        T.Q4K, T.Q5K, T.Q6K, T.IQ4NL, T.IQ4XS]
 
 
 def test_weight_quantization_variants():
