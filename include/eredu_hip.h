@@ -151,8 +151,9 @@ int eq_gguf_convert_mxfp4(uint32_t* weights, uint8_t* scales, const uint8_t* raw
 
 /*
  * GGML blocks -> dense [rows, cols] of out_dtype (EQ_DTYPE_BF16 or EQ_DTYPE_F32),
- * following `definition` (eq_dequant_definition).  bf16 output is the
- * round-to-nearest-even image of the reference's f32 result.
+ * following `definition` (eq_dequant_definition; IQ4_NL / IQ4_XS have one
+ * definition, factor * level, eredu-gguf/src/iquant.rs:271-301).  bf16 output
+ * is the round-to-nearest-even image of the reference's f32 result.
  * Replaces IQuantTensor::dequantize_f32 (eredu-gguf/src/convert.rs:43-56) and
  * NativeQuantizedTensor::dequantize's CPU decoders
  * (safemlx/src/native_quantization.rs:3417-3542).
@@ -163,10 +164,11 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
 
 /*
  * Native GGUF linear: y[M, N] = x[M, K] . W^T with W the GGUF tensor (MLX
- * shape [N, K], raw Q4_K, Q5_K, Q6_K, Q5_1 or Q8_0 blocks as stored, raw_len
+ * shape [N, K], raw Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL or IQ4_XS blocks as stored, raw_len
  * bytes) decoded by the native definition (Q4_K: d*sc*q - dmin*m, Q5_K the
- * same with 5-bit q, Q6_K: d*sc*(q - 32), Q5_1: d*q + m, Q8_0: d*q; factors
- * in f32, not rounded to f16) without an affine expansion; f32 accumulation,
+ * same with 5-bit q, Q6_K: d*sc*(q - 32), Q5_1: d*q + m, Q8_0: d*q, IQ4_NL /
+ * IQ4_XS: factor*level; factors in f32, not rounded to f16) without an
+ * affine expansion; f32 accumulation,
  * bf16 x and y.  Replaces NativeQuantizedTensor::linear with transpose = true
  * (safemlx/src/native_quantization.rs:741-772; its Metal kernels for these
  * formats at :1320-1400,1856), whose CUDA/CPU builds decode on the host
