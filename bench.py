@@ -216,6 +216,30 @@ def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
     return out
 
 
+def bench_qmm_widths(steps, warmup, M=512):
+    """Prefill TFLOP/s at the other code widths and group size 16 (the widths
+    GGUF k-quants convert to and MLX-LM admits): 2/3/5/6-bit codes go through
+    the byte re-pack and the 8-bit matrix-core kernel, 4/8-bit g16 straight to
+    it; q/o and gate/up shapes at M = 512, weights rotating as in bench_qmm."""
+    import torch
+
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    out = {}
+    for bits, gs in ((2, 16), (3, 16), (5, 32), (6, 16), (4, 16), (8, 16)):
+        for (name, N, K) in [("q/o", HIDDEN, HIDDEN), ("gate/up", FFN, HIDDEN)]:
+            lins = [Linear(N, K, gen, bits=bits, gs=gs) for _ in range(rotation(qmv_bytes(0, N, K, bits, gs), 4))]
+            x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+            y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+            t = Timer(lambda st: [run_one(l, x, y, st, bits=bits, gs=gs) for l in lins])
+            ms = t.ms_per_replay(max(steps // 4, 5), warmup) / len(lins)
+            tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            out[f"b{bits} g{gs} M{M} {N}x{K}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
+                                                  "frac_mfma": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
+            del lins
+            torch.cuda.empty_cache()
+    return out
+
+
 def bench_gguf(steps, warmup):
     """GGUF 4096x14336 dequant (bf16) and convert (affine) GB/s,
     for every block type with an affine form (Q4_0 / Q8_0 / Q4_K first, the
@@ -777,6 +801,8 @@ def main():
         if args.prefill_only:
             log("[bench] qmm prefill")
             out["qmm"] = bench_qmm(args.steps, args.warmup)
+            log("[bench] qmm prefill, other widths")
+            out["qmm_widths"] = bench_qmm_widths(args.steps, args.warmup)
         if args.gguf_only:
             log("[bench] gguf")
             out["gguf"] = bench_gguf(args.steps, args.warmup)
@@ -835,6 +861,8 @@ def main():
     if not args.quick:
         log("[bench] qmm prefill")
         detail["qmm"] = bench_qmm(args.steps, args.warmup)
+        log("[bench] qmm prefill, other widths")
+        detail["qmm_widths"] = bench_qmm_widths(args.steps, args.warmup)
         log("[bench] gguf")
         detail["gguf"] = bench_gguf(args.steps, args.warmup)
         log("[bench] gguf streaming load")

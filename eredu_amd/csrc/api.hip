@@ -370,7 +370,12 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
                             w, scales, biases, int(M), int(N), int(K), st))
             return check_launch("quantized_matmul (qmv)");
     }
-    if (mfma_ok && M > 16 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8)) {
+    // prefill on the matrix cores: 4/8-bit codes directly, 2/3/5/6-bit codes
+    // re-packed to bytes slice by slice in the workspace
+    const bool odd_ok = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 2 || bits == 3 || bits == 5 || bits == 6) &&
+                        (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && aligned(x, 16) &&
+                        aligned(w, 4);
+    if ((mfma_ok || odd_ok) && M > 16 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8)) {
         if (launch_qmm_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
                             w, scales, biases, int(M), int(N), int(K), ws, st))
             return check_launch("quantized_matmul (qmm)");

@@ -478,7 +478,10 @@ bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const ui
 // N % 128 == 0, K % 64 == 0, 16-byte aligned x and w, 8-byte aligned y.  Any
 // buffer size: launches are split so that every buffer offset fits 32 bits.
 // Split K takes its partial tiles from `ws` (null: the library workspace);
-// without room for them the launch runs unsplit.
+// without room for them the launch runs unsplit.  Bits 4 and 8 at group 16,
+// 32, 64 or 128; bits 2, 3, 5 and 6 (4-byte aligned w) re-pack their codes
+// to bytes in `ws` slice by slice and run the 8-bit kernel (false when no
+// workspace can be had).
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st);
 

@@ -227,8 +227,9 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         soff[j] = int(n) < N ? (n * uint32_t(G)) * PB + (PW ? uint32_t(c_begin) * 2u : uint32_t((32 * kb) / GS) * PB)
                              : kOutOfRange;
     }
-    // (a lane's 32 codes lie in one group: group sizes are multiples of 32 and
-    // chunks start at multiples of 64, so its group is k0 / GS + 32 kb / GS)
+    // (a lane's 32 codes lie in one group when the group size is a multiple of
+    // 32 -- chunks start at multiples of 64, so its group is k0 / GS + 32 kb /
+    // GS -- and in groups 2 kb, 2 kb + 1 of the chunk at group size 16)
 
     // Loads of this K-group's chunk i, i.e. chunk 2i + kgrp of the split (past
     // the split's end: the last chunk again, in cache and never computed).
@@ -256,6 +257,10 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
             if constexpr (MX) {
                 S.s[j] = __builtin_amdgcn_raw_buffer_load_b8(sr, soff[j], kp, 0);
                 S.b[j] = 0u;
+            } else if constexpr (GS == 16) {
+                // the lane's 32 codes span two groups: both parameters in one word
+                S.s[j] = __builtin_amdgcn_raw_buffer_load_b32(sr, soff[j], kp, 0);
+                S.b[j] = __builtin_amdgcn_raw_buffer_load_b32(br, soff[j], kp, 0);
             } else if constexpr (!PW) {
                 S.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], kp, 0);
                 S.b[j] = __builtin_amdgcn_raw_buffer_load_b16(br, soff[j], kp, 0);
@@ -314,11 +319,14 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
                     bq[j][t] = q_u32x4{p[0], p[1], p[2], p[3]};
                 }
             } else {
-                const float s = qmm_param<ST>(sbits[j]);
-                const float b = qmm_param<ST>(bbits[j]);
+                // (group 16: codes 0..15 of the lane's 32 take the low halves, 16..31 the high)
+                const float s0 = qmm_param<ST>(sbits[j]), b0 = qmm_param<ST>(bbits[j]);
+                const float s1 = GS == 16 ? qmm_param<ST>(sbits[j] >> 16) : s0;
+                const float b1 = GS == 16 ? qmm_param<ST>(bbits[j] >> 16) : b0;
 #pragma unroll
                 for (int t = 0; t < 4; t++)
-                    bq[j][t] = dequant8<BITS>(reinterpret_cast<const uint32_t*>(&S.w[j][0]) + t * BITS / 4, s, b);
+                    bq[j][t] = dequant8<BITS>(reinterpret_cast<const uint32_t*>(&S.w[j][0]) + t * BITS / 4,
+                                              t < 2 ? s0 : s1, t < 2 ? b0 : b1);
             }
         }
         const char* base = buf + gofs;
@@ -527,9 +535,12 @@ static void launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
 // Buffer offsets in the kernel are 32-bit: a weight matrix of 2^31 bytes or
 // more runs in row pieces (multiples of the 256-column tile), an activation
 // matrix that large in row pieces (multiples of the 128-row tile).
+// y's row stride is ldy (N when negative); split K only when y is one whole
+// piece of stride N.
 template <int BITS, int GS, typename ST>
 static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b, int M,
-                         int N, int K, const WsSource* src, hipStream_t st) {
+                         int N, int K, const WsSource* src, hipStream_t st, int ldy = -1) {
+    if (ldy < 0) ldy = N;
     const int64_t limit = (int64_t(1) << 31) - 1;
     const int64_t row_bytes = int64_t(K) * BITS / 8;
     const int64_t G = K / GS;
@@ -537,7 +548,7 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     int64_t m_piece = limit / (int64_t(K) * 2) / kBM * kBM;
     n_piece = n_piece < kBN ? kBN : n_piece;
     m_piece = m_piece < kBM ? kBM : m_piece;
-    const bool whole = n_piece >= N && m_piece >= M;
+    const bool whole = n_piece >= N && m_piece >= M && ldy == N;
     for (int64_t m0 = 0; m0 < M; m0 += m_piece) {
         const int mc = int(M - m0 < m_piece ? M - m0 : m_piece);
         for (int64_t n0 = 0; n0 < N; n0 += n_piece) {
@@ -545,8 +556,8 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
             constexpr int64_t PB = __is_same(ST, E8M0T) ? 1 : 2;
             const char* sp = static_cast<const char*>(s) + n0 * G * PB;
             const char* bp = b ? static_cast<const char*>(b) + n0 * G * PB : nullptr;
-            launch_qmm_piece<BITS, GS, ST>(y + m0 * N + n0, N, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp, mc, nc,
-                                           K, whole, src, st);
+            launch_qmm_piece<BITS, GS, ST>(y + m0 * ldy + n0, ldy, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp, mc,
+                                           nc, K, whole, src, st);
         }
     }
 }
@@ -555,6 +566,7 @@ template <int BITS, typename ST>
 static bool launch_qmm_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
                           int M, int N, int K, const WsSource* src, hipStream_t st) {
     switch (gs) {
+    case 16: launch_qmm_t<BITS, 16, ST>(y, x, w, s, b, M, N, K, src, st); return true;
     case 32: launch_qmm_t<BITS, 32, ST>(y, x, w, s, b, M, N, K, src, st); return true;
     case 64: launch_qmm_t<BITS, 64, ST>(y, x, w, s, b, M, N, K, src, st); return true;
     case 128: launch_qmm_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, src, st); return true;
@@ -702,6 +714,93 @@ bool launch_qmm_grouped_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w,
     return launch_qmm_grouped_t<4, 32, E8M0T>(y, x, w, s, nullptr, lhs, rhs, batch, x_batches, experts, N, K, st);
 }
 
+// ------------------------------------------- prefill at 2, 3, 5 and 6 bits
+//
+// The codes of these widths are an LSB-first bit stream (a 32-code unit of a
+// row is exactly BITS words).  For M > 16 they are re-packed, a slice of
+// weight rows at a time, to one byte per code in the stream's workspace and
+// multiplied by the 8-bit matrix-core kernel with the same scales and biases
+// and group size: the code values, and so the products, are unchanged.
+
+// One thread per 32-code unit: BITS words in, 8 words (32 byte codes) out.
+template <int BITS>
+__global__ __launch_bounds__(256) void qmm_codes_to_bytes(const uint32_t* __restrict__ w, uint4* __restrict__ out,
+                                                          int64_t units) {
+    const int64_t u = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (u >= units) return;
+    uint32_t in[BITS];
+#pragma unroll
+    for (int i = 0; i < BITS; i++) in[i] = w[u * BITS + i];
+    uint32_t o[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int bit = (4 * q + e) * BITS, wd = bit >> 5, sh = bit & 31;
+            uint32_t c = in[wd] >> sh;
+            if (sh + BITS > 32) c |= in[wd + 1] << (32 - sh);
+            v |= (c & ((1u << BITS) - 1u)) << (8 * e);
+        }
+        o[q] = v;
+    }
+    out[2 * u] = make_uint4(o[0], o[1], o[2], o[3]);
+    out[2 * u + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+template <typename ST>
+static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
+                             const void* b, int M, int N, int K, const WsSource* src, hipStream_t st) {
+    if (gs != 16 && gs != 32 && gs != 64 && gs != 128) return false;
+    // rows per slice: their byte codes within 64 MiB, a multiple of the 256-column tile
+    int64_t nc = (int64_t(64) << 20) / K / kBN * kBN;
+    nc = nc < kBN ? kBN : nc;
+    nc = nc > N ? N : nc;
+    const size_t code_bytes = (size_t(nc) * size_t(K) + 255) & ~size_t(255);
+    // room after the codes for the split-K partials of a slice the planner would split
+    const int tiles = int((M + kBM - 1) / kBM * ((nc + kBN - 1) / kBN));
+    int splits = qmm_cu_count() / (tiles > 0 ? tiles : 1);
+    splits = splits > K / kBK / 8 ? K / kBK / 8 : splits;
+    const size_t part_bytes = splits > 1 ? size_t(splits) * size_t(M) * size_t(nc) * 4u : 0;
+    size_t want = code_bytes + part_bytes;
+    char* base = static_cast<char*>(ws_acquire(src, want, st));
+    if (!base) base = static_cast<char*>(ws_acquire(src, want = code_bytes, st));
+    if (!base) return false;
+    const size_t cap = src ? src->cap : want;
+    WsSource rest{base + code_bytes, cap > code_bytes ? cap - code_bytes : 0, nullptr};
+    const int64_t G = K / gs;
+    constexpr int64_t PB = 2;
+    for (int64_t n0 = 0; n0 < N; n0 += nc) {
+        const int ncs = int(N - n0 < nc ? N - n0 : nc);
+        const int64_t units = int64_t(ncs) * (K / 32);
+        const dim3 grid(unsigned((units + 255) / 256));
+        const uint32_t* wr = w + n0 * (int64_t(K) * bits / 32);
+        uint4* codes = reinterpret_cast<uint4*>(base);
+        switch (bits) {
+        case 2: qmm_codes_to_bytes<2><<<grid, 256, 0, st>>>(wr, codes, units); break;
+        case 3: qmm_codes_to_bytes<3><<<grid, 256, 0, st>>>(wr, codes, units); break;
+        case 5: qmm_codes_to_bytes<5><<<grid, 256, 0, st>>>(wr, codes, units); break;
+        default: qmm_codes_to_bytes<6><<<grid, 256, 0, st>>>(wr, codes, units); break;
+        }
+        const char* sp = static_cast<const char*>(s) + n0 * G * PB;
+        const char* bp = b ? static_cast<const char*>(b) + n0 * G * PB : nullptr;
+        const uint32_t* w8 = reinterpret_cast<const uint32_t*>(base);
+        const WsSource* parts = rest.cap > 0 ? &rest : nullptr;
+        if (!parts) {
+            // no room for partials: a fixed region of exactly the codes, no split
+            static const WsSource none{nullptr, 0, nullptr};
+            parts = &none;
+        }
+        switch (gs) {
+        case 16: launch_qmm_t<8, 16, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
+        case 32: launch_qmm_t<8, 32, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
+        case 64: launch_qmm_t<8, 64, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
+        default: launch_qmm_t<8, 128, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
+        }
+    }
+    return true;
+}
+
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st) {
     if (bits == 4) {
@@ -710,6 +809,9 @@ bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint1
     } else if (bits == 8) {
         if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st);
         if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, ws, st);
+    } else if (bits == 2 || bits == 3 || bits == 5 || bits == 6) {
+        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_odd_t<BF16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_odd_t<F16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st);
     }
     return false;
 }

@@ -117,3 +117,50 @@ def test_gather_widths(cuda, bits, gs, transpose):
         ref = orc.quantized_matmul_f64(xi, orc.BF16, *packs[e], orc.BF16, transpose, gs, bits, N, K)
         ok, worst, _ = orc.matmul_within_tolerance(host_f32(y[i]), ref, out_is_bf16=True)
         assert ok, (i, worst)
+
+
+# Prefill (M > 16, transpose, bf16 x) on the matrix cores at the other widths:
+# 2/3/5/6-bit codes re-packed to bytes in the workspace and run by the 8-bit
+# kernel, and group size 16 in that kernel (two groups per lane's 32 codes) --
+# also for 4- and 8-bit codes directly.  N = 384 leaves a partial 256-column
+# tile; M = 17 and 130 partial 128-row tiles; 4096 x 4096 at M = 128 splits K.
+PREFILL = [(2, 16, orc.BF16, True), (3, 16, orc.F16, True), (3, 64, orc.BF16, False), (5, 32, orc.F16, True),
+           (5, 128, orc.BF16, True), (6, 16, orc.BF16, True), (6, 32, orc.F16, False), (4, 16, orc.BF16, True),
+           (8, 16, orc.F16, True)]
+
+
+@pytest.mark.parametrize("bits,gs,sdt,biases", PREFILL)
+@pytest.mark.parametrize("M,N,K", [(17, 384, 1024), (130, 256, 2048), (128, 4096, 4096)])
+def test_prefill_widths_on_matrix_cores(cuda, bits, gs, sdt, biases, M, N, K):
+    print(f"[case] prefill widths bits={bits} gs={gs} M={M} N={N} K={K}", flush=True)
+    w, s, b = synthetic_linear(N, K, gs, bits, seed=bits * 17 + gs + M + N, scale_dtype=sdt)
+    if not biases:
+        b = None
+    xb = synthetic_x(M, K, seed=bits + gs + M + 1)
+    y = quantized_matmul_with_mode(dev_bf16(xb), dev_words(w), dev_param(s, sdt),
+                                   dev_param(b, sdt) if b is not None else None, True, gs, bits)
+    torch.cuda.synchronize()
+    rows = np.arange(N) if N <= 512 else np.random.default_rng(M).choice(N, 96, replace=False)
+    ref = orc.quantized_matmul_f64(xb, orc.BF16, w[rows], s[rows], None if b is None else b[rows], sdt, True, gs,
+                                   bits, len(rows), K)
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(y)[:, rows], ref, out_is_bf16=True)
+    assert y.shape == (M, N)
+    assert ok, worst
+
+
+def test_prefill_odd_width_in_weight_slices(cuda):
+    """More weight rows than one 64 MiB slice of byte codes (16384 rows at
+    K = 4096): two slices, each writing its columns of y (no split K)."""
+    from tests.fixtures import device_random_linear, host_rows
+
+    print("[case] prefill 6-bit g16 N=16640 K=4096 M=24", flush=True)
+    N, K, M, bits, gs = 16640, 4096, 24, 6, 16
+    w, s, b = device_random_linear(N, K, gs, bits, seed=5)
+    xb = synthetic_x(M, K, seed=6)
+    y = quantized_matmul_with_mode(dev_bf16(xb), w, s, b, True, gs, bits)
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.arange(0, 32), np.arange(16352, 16416), np.arange(N - 32, N)])
+    wr, sr, br = host_rows(w, s, b, rows)
+    ref = orc.quantized_matmul_f64(xb, orc.BF16, wr, sr, br, orc.BF16, True, gs, bits, len(rows), K)
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(y)[:, rows], ref, out_is_bf16=True)
+    assert ok, worst
