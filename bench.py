@@ -240,11 +240,21 @@ def bench_qmm_widths(steps, warmup, M=512):
     return out
 
 
+def lin_m(n, ty, y, x, raws, nraw, M, rows, cols):
+    """One eq_gguf_linear per payload copy: y [M, rows] = x [M, cols] . W^T."""
+    def lin(st):
+        for r in raws:
+            n.check(n.lib().eq_gguf_linear(y.data_ptr(), x.data_ptr(), r.data_ptr(), nraw, int(ty), M, rows, cols, 0,
+                                           n.EQ_DTYPE_BF16, st))
+    return lin
+
+
 def bench_gguf(steps, warmup):
     """GGUF 4096x14336 dequant (bf16) and convert (affine) GB/s,
     for every block type with an affine form (Q4_0 / Q8_0 / Q4_K first, the
     configs' types), and dequant for IQ4_NL / IQ4_XS; the native linear at
-    M = 1 for the natively executed types."""
+    M = 1 (GB/s) and M = 512 (TFLOP/s, the matrix-core prefill) for the
+    natively executed types."""
     import torch
 
     from eredu_amd import gguf as G
@@ -291,16 +301,21 @@ def bench_gguf(steps, warmup):
             # batch-1 linear straight from the blocks: y [1, 4096] = x [1, 14336] . W^T
             x = torch.randn((1, cols), device="cuda").to(torch.bfloat16)
             y = torch.empty((1, rows), dtype=torch.bfloat16, device="cuda")
-
-            def lin(st):
-                for r in raws:
-                    n.check(n.lib().eq_gguf_linear(y.data_ptr(), x.data_ptr(), r.data_ptr(), nraw, int(ty), 1, rows,
-                                                   cols, 0, n.EQ_DTYPE_BF16, st))
-
-            ms = Timer(lin).ms_per_replay(max(steps // 4, 5), warmup) / len(raws)
+            ms = Timer(lin_m(n, ty, y, x, raws, nraw, 1, rows, cols)).ms_per_replay(max(steps // 4, 5), warmup)
+            ms /= len(raws)
             gbs = (nraw + cols * 2 + rows * 2) / (ms * 1e-3) / 1e9
             out[f"{ty.name} linear_M1"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": len(raws)}
+            # prefill: 512 activation rows, through the matrix cores (blocks re-packed per call)
+            M = 512
+            x = torch.randn((M, cols), device="cuda").to(torch.bfloat16)
+            y = torch.empty((M, rows), dtype=torch.bfloat16, device="cuda")
+            ms = Timer(lin_m(n, ty, y, x, raws, nraw, M, rows, cols)).ms_per_replay(max(steps // 4, 5), warmup)
+            ms /= len(raws)
+            tf = 2.0 * M * rows * cols / (ms * 1e-3) / 1e12
+            out[f"{ty.name} linear_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                                             "frac_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "copies": len(raws)}
+            del x, y
         del raws
         torch.cuda.empty_cache()
     return out

@@ -481,9 +481,11 @@ bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const ui
 // without room for them the launch runs unsplit.  Bits 4 and 8 at group 16,
 // 32, 64 or 128; bits 2, 3, 5 and 6 (4-byte aligned w) re-pack their codes
 // to bytes in `ws` slice by slice and run the 8-bit kernel (false when no
-// workspace can be had).
+// workspace can be had).  y's row stride is ldy (N when negative; split K
+// only when it is N).
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
-                     const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st);
+                     const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st,
+                     int ldy = -1);
 
 // The same two launchers for MXFP4 codes (E8M0 scale bytes, no biases).
 bool launch_qmm_mfma_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, int M, int N, int K,

@@ -590,6 +590,55 @@ __global__ __launch_bounds__(256) void kq_to_affine(const uint8_t* __restrict__ 
     }
 }
 
+// One byte per value and f16 group factors: the 8-bit affine form the
+// prefill kernels take, written straight from the blocks (no packed-code pass
+// in between).  Affine types: the code itself, with the scale and bias of
+// kq_group (the affine conversion's, so s * byte + bias is its value
+// exactly).  IQ4_NL / IQ4_XS: level + 128, with s = f16(factor) and bias
+// -128 s (exact), so that s * byte + bias = s * level (the factor's f16
+// rounding is the only change; IQ4_NL's d is f16 already).
+template <int T, bool BIG>
+__global__ __launch_bounds__(256) void kq_to_bytes(const uint8_t* __restrict__ raw, int64_t nblocks, bool vec_ok,
+                                                   uint4* __restrict__ w, uint16_t* __restrict__ s,
+                                                   uint16_t* __restrict__ bias) {
+    using P = KQuant<T>;
+    constexpr int NB = 256 / P::units, G = 32 / P::gs;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[NB * P::bytes / 2];
+    const int64_t blk0 = int64_t(blockIdx.x) * NB;
+    const int nb = int(min<int64_t>(NB, nblocks - blk0));
+    stage_blocks<P::bytes, NB>(lds, raw, blk0, nb, vec_ok);
+    const int lb = threadIdx.x / P::units, u = threadIdx.x % P::units;
+    if (lb >= nb) return;
+    const uint8_t* b = reinterpret_cast<const uint8_t*>(lds) + lb * P::bytes;
+    uint32_t cw[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        kq_codes8<T, BIG>(b, u, 8 * q, cw[2 * q], cw[2 * q + 1]);
+        if constexpr (P::levels) {
+            cw[2 * q] = iq4_level_bytes(cw[2 * q]);
+            cw[2 * q + 1] = iq4_level_bytes(cw[2 * q + 1]);
+        }
+    }
+    const int64_t unit = (blk0 + lb) * P::units + u;
+    w[2 * unit] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+    w[2 * unit + 1] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+    if constexpr (P::levels) {
+        float factor, zero;
+        kq_native_group<T, BIG>(b, u, factor, zero);
+        const uint32_t sb = f32_to_f16_bits(factor);
+        s[unit] = uint16_t(sb);
+        bias[unit] = uint16_t(f32_to_f16_bits(-128.f * f16_bits_to_f32(sb)));
+    } else {
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            uint32_t sb, bb;
+            kq_group<T, BIG>(b, u * G + j, sb, bb);
+            s[unit * G + j] = uint16_t(sb);
+            bias[unit * G + j] = uint16_t(bb);
+        }
+    }
+}
+
 // Dense decode by the affine route, f32(scale) * code + f32(bias)
 // (convert.rs:81-101); for these types it is also the native definition
 // (Q5_1's native decoder d * q + m uses the same unrounded d and m,
@@ -1376,6 +1425,106 @@ bool with_kq(int type, bool big, F&& f) {
     }
 }
 
+// The convert kernels of an affine type (geometry checked by the caller).
+void launch_convert_affine(int ggml_type, bool big, const uint8_t* raw, int64_t nblocks, bool vec_ok,
+                           uint32_t* weights, uint16_t* scales, uint16_t* biases, hipStream_t st) {
+    uint4* w4 = reinterpret_cast<uint4*>(weights);
+    if (with_kq(ggml_type, big, [&](auto t, auto b) {
+            constexpr int T = decltype(t)::value;
+            constexpr int NB = 256 / KQuant<T>::units;
+            if constexpr (!KQuant<T>::levels)
+                kq_to_affine<T, decltype(b)::value><<<dim3(unsigned((nblocks + NB - 1) / NB)), 256, 0, st>>>(
+                    raw, nblocks, vec_ok, weights, scales, biases);
+        }))
+        return;
+    if (ggml_type == EQ_GGML_Q4_K) {
+        const int64_t ngroups = nblocks * 8;
+        const dim3 grid(unsigned((ngroups + 255) / 256));
+        if (big)
+            q4k_to_affine<true><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, w4, scales, biases);
+        else
+            q4k_to_affine<false><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, w4, scales, biases);
+    } else {
+        const dim3 grid(unsigned((nblocks + kBlocksPerWG - 1) / kBlocksPerWG));
+        if (ggml_type == EQ_GGML_Q4_0) {
+            if (big)
+                q4_0_to_affine<true><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+            else
+                q4_0_to_affine<false><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+        } else {
+            if (big)
+                q8_0_to_affine<true><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+            else
+                q8_0_to_affine<false><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
+        }
+    }
+}
+
+// Native linear at M > kLinRows on the matrix cores: a slice of weight rows
+// at a time is converted to the affine triple (convert_affine, f16 group
+// factors; 5- and 6-bit codes and IQ4 levels as bytes, kq_to_bytes) in the
+// stream's workspace and
+// multiplied by the affine prefill kernels, writing its columns of y.  The affine route is the dense fallback of the
+// reference's native linear on its non-Metal backends for Q5_K / Q6_K
+// (native_quantization.rs:846-862 via IQuantTensor::dequantize_f32); for
+// Q4_K, Q5_1 and Q8_0 it differs from the native decoders only by the f16
+// rounding of the group factors (none for Q5_1, and for Q8_0 only when
+// -128 d overflows f16).  False, launching nothing, when the shape does not
+// suit the prefill kernels or no workspace can be had.
+bool launch_native_prefill(int ggml_type, bool big, const Geometry& geo, uint16_t* y, const uint16_t* x,
+                           const uint8_t* raw, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+    if (N % 128 != 0 || K % 64 != 0 || !aligned(y, 8)) return false;
+    // one byte per value for the widths the matrix-core kernel takes as bytes
+    // (Q5_1 / Q5_K / Q6_K) and for the IQ4 levels: kq_to_bytes
+    const bool as_bytes = !geo.affine || (geo.bits != 4 && geo.bits != 8);
+    const int bits = as_bytes ? 8 : geo.bits;
+    const int64_t row_bytes = K / geo.values * geo.bytes;
+    const int64_t wbytes_row = K * bits / 8, pbytes_row = K / geo.gs * 2;
+    // rows per slice: the slice's triple within 128 MiB (a 4096 x 14336
+    // projection's in one slice at every width), a multiple of 256 rows
+    int64_t nc = (int64_t(128) << 20) / (wbytes_row + 2 * pbytes_row) / 256 * 256;
+    nc = nc < 256 ? 256 : nc;
+    nc = nc > N ? N : nc;
+    // slices of equal size (a short last slice would leave most CUs idle)
+    const int64_t nslices = (N + nc - 1) / nc;
+    nc = ((N + nslices - 1) / nslices + 255) / 256 * 256;
+    nc = nc > N ? N : nc;
+    auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
+    const size_t wsz = up(size_t(nc * wbytes_row)), psz = up(size_t(nc * pbytes_row));
+    const size_t triple = wsz + 2 * psz;
+    // behind the triple: the 2/3/5/6-bit path's byte codes and split-K partials
+    const size_t rest = size_t(nc) * size_t(K) + size_t(4) * size_t(M) * size_t(nc) * 4u + 512;
+    size_t want = triple + rest;
+    char* base = static_cast<char*>(ws_acquire(nullptr, want, st));
+    if (!base) base = static_cast<char*>(ws_acquire(nullptr, want = triple, st));
+    if (!base) return false;
+    uint32_t* w = reinterpret_cast<uint32_t*>(base);
+    uint16_t* s = reinterpret_cast<uint16_t*>(base + wsz);
+    uint16_t* b = reinterpret_cast<uint16_t*>(base + wsz + psz);
+    const WsSource tail{base + triple, want - triple, nullptr};
+    const bool vec_ok = aligned(raw, 16);
+    for (int64_t n0 = 0; n0 < N; n0 += nc) {
+        const int64_t ncs = N - n0 < nc ? N - n0 : nc;
+        const uint8_t* rs = raw + n0 * row_bytes;
+        const int64_t nb = ncs * K / geo.values;
+        const bool v16 = vec_ok && (n0 * row_bytes) % 16 == 0;
+        if (!as_bytes) {
+            launch_convert_affine(ggml_type, big, rs, nb, v16, w, s, b, st);
+        } else if (!with_kq(ggml_type, big, [&](auto t, auto bt) {
+                       constexpr int T = decltype(t)::value;
+                       constexpr int NB = 256 / KQuant<T>::units;
+                       kq_to_bytes<T, decltype(bt)::value><<<dim3(unsigned((nb + NB - 1) / NB)), 256, 0, st>>>(
+                           rs, nb, v16, reinterpret_cast<uint4*>(w), s, b);
+                   })) {
+            return false;
+        }
+        if (!launch_qmm_mfma(bits, geo.gs, EQ_DTYPE_F16, y + n0, x, w, s, b, int(M), int(ncs), int(K), &tail, st,
+                             int(N)))
+            return false;
+    }
+    return true;
+}
+
 }  // namespace
 }  // namespace eq
 
@@ -1400,39 +1549,8 @@ extern "C" int eq_gguf_convert_affine(uint32_t* weights, uint16_t* scales, uint1
         set_error("weights must be 16-byte aligned and scales/biases 2-byte aligned");
         return 1;
     }
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool vec_ok = aligned(raw, 16);
-    const bool big = endian == EQ_ENDIAN_BIG;
-    uint4* w4 = reinterpret_cast<uint4*>(weights);
-    if (with_kq(ggml_type, big, [&](auto t, auto b) {
-            constexpr int T = decltype(t)::value;
-            constexpr int NB = 256 / KQuant<T>::units;
-            if constexpr (!KQuant<T>::levels)
-                kq_to_affine<T, decltype(b)::value><<<dim3(unsigned((nblocks + NB - 1) / NB)), 256, 0, st>>>(
-                    raw, nblocks, vec_ok, weights, scales, biases);
-        }))
-        return check_launch("gguf convert_affine");
-    if (ggml_type == EQ_GGML_Q4_K) {
-        const int64_t ngroups = nblocks * 8;
-        const dim3 grid(unsigned((ngroups + 255) / 256));
-        if (big)
-            q4k_to_affine<true><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, w4, scales, biases);
-        else
-            q4k_to_affine<false><<<grid, 256, 0, st>>>(raw, ngroups, vec_ok, w4, scales, biases);
-    } else {
-        const dim3 grid(unsigned((nblocks + kBlocksPerWG - 1) / kBlocksPerWG));
-        if (ggml_type == EQ_GGML_Q4_0) {
-            if (big)
-                q4_0_to_affine<true><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
-            else
-                q4_0_to_affine<false><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
-        } else {
-            if (big)
-                q8_0_to_affine<true><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
-            else
-                q8_0_to_affine<false><<<grid, 256, 0, st>>>(raw, nblocks, vec_ok, w4, scales, biases);
-        }
-    }
+    launch_convert_affine(ggml_type, endian == EQ_ENDIAN_BIG, raw, nblocks, aligned(raw, 16), weights, scales,
+                          biases, reinterpret_cast<hipStream_t>(stream));
     return check_launch("gguf convert_affine");
 }
 
@@ -1666,6 +1784,9 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool big = endian == EQ_ENDIAN_BIG;
+    if (M > kLinRows && launch_native_prefill(ggml_type, big, geo, static_cast<uint16_t*>(y),
+                                        static_cast<const uint16_t*>(x), raw, M, N, K, st))
+        return check_launch("gguf linear (prefill)");
     if (kq) {
         // R weight rows per workgroup, staged whole in LDS: 8 while they fit
         // in 64 KB, fewer for long rows, one row up to the device's LDS

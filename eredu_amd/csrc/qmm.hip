@@ -447,8 +447,11 @@ done:
 }
 
 // y = bf16(sum over splits of the partial tiles), splits summed in order.
+// y[m, n] (row stride ldy) = bf16(sum over splits of ws[split, m, n]), the
+// partials dense [splits, M, N] f32; four outputs per thread (vec: y 8-byte
+// aligned and N, ldy multiples of 4, so the four stay in one row).
 __global__ __launch_bounds__(256) void qmm_split_reduce(uint16_t* __restrict__ y, const float* __restrict__ ws,
-                                                         int64_t mn, int splits, bool vec) {
+                                                         int64_t mn, int64_t n, int64_t ldy, int splits, bool vec) {
     typedef float f32x4_t __attribute__((ext_vector_type(4)));
     const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
     if (i >= mn) return;
@@ -458,14 +461,17 @@ __global__ __launch_bounds__(256) void qmm_split_reduce(uint16_t* __restrict__ y
             const f32x4_t u = *reinterpret_cast<const f32x4_t*>(ws + int64_t(s) * mn + i);
             v = f32x4_t{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
         }
+        const int64_t row = i / n, col = i - row * n;
         typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-        *reinterpret_cast<u16x4*>(y + i) = u16x4{uint16_t(f32_to_bf16_bits(v[0])), uint16_t(f32_to_bf16_bits(v[1])),
-                                                 uint16_t(f32_to_bf16_bits(v[2])), uint16_t(f32_to_bf16_bits(v[3]))};
+        *reinterpret_cast<u16x4*>(y + row * ldy + col) =
+            u16x4{uint16_t(f32_to_bf16_bits(v[0])), uint16_t(f32_to_bf16_bits(v[1])),
+                  uint16_t(f32_to_bf16_bits(v[2])), uint16_t(f32_to_bf16_bits(v[3]))};
     } else {
-        for (int64_t e = i; e < mn; e++) {
+        for (int64_t e = i; e < mn && e < i + 4; e++) {
             float v = ws[e];
             for (int s = 1; s < splits; s++) v += ws[int64_t(s) * mn + e];
-            y[e] = uint16_t(f32_to_bf16_bits(v));
+            const int64_t row = e / n;
+            y[row * ldy + (e - row * n)] = uint16_t(f32_to_bf16_bits(v));
         }
     }
 }
@@ -527,9 +533,9 @@ static void launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
     }
     if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64><<<grid, block, 0, st>>>(a);
     else qmm_mfma_kernel<BITS, GS, ST, true, false><<<grid, block, 0, st>>>(a);
-    const int64_t mn = int64_t(M) * N;  // (split only when y is one whole piece: ldy == N)
-    qmm_split_reduce<<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(y, a.ws, mn, splits,
-                                                                                    aligned(y, 8));
+    const int64_t mn = int64_t(M) * N;
+    qmm_split_reduce<<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(
+        y, a.ws, mn, N, ldy, splits, aligned(y, 8) && N % 4 == 0 && ldy % 4 == 0);
 }
 
 // Buffer offsets in the kernel are 32-bit: a weight matrix of 2^31 bytes or
@@ -548,7 +554,7 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     int64_t m_piece = limit / (int64_t(K) * 2) / kBM * kBM;
     n_piece = n_piece < kBN ? kBN : n_piece;
     m_piece = m_piece < kBM ? kBM : m_piece;
-    const bool whole = n_piece >= N && m_piece >= M && ldy == N;
+    const bool whole = n_piece >= N && m_piece >= M;
     for (int64_t m0 = 0; m0 < M; m0 += m_piece) {
         const int mc = int(M - m0 < m_piece ? M - m0 : m_piece);
         for (int64_t n0 = 0; n0 < N; n0 += n_piece) {
@@ -564,12 +570,12 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
 
 template <int BITS, typename ST>
 static bool launch_qmm_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
-                          int M, int N, int K, const WsSource* src, hipStream_t st) {
+                          int M, int N, int K, const WsSource* src, hipStream_t st, int ldy = -1) {
     switch (gs) {
-    case 16: launch_qmm_t<BITS, 16, ST>(y, x, w, s, b, M, N, K, src, st); return true;
-    case 32: launch_qmm_t<BITS, 32, ST>(y, x, w, s, b, M, N, K, src, st); return true;
-    case 64: launch_qmm_t<BITS, 64, ST>(y, x, w, s, b, M, N, K, src, st); return true;
-    case 128: launch_qmm_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, src, st); return true;
+    case 16: launch_qmm_t<BITS, 16, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
+    case 32: launch_qmm_t<BITS, 32, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
+    case 64: launch_qmm_t<BITS, 64, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
+    case 128: launch_qmm_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
     default: return false;
     }
 }
@@ -750,8 +756,9 @@ __global__ __launch_bounds__(256) void qmm_codes_to_bytes(const uint32_t* __rest
 
 template <typename ST>
 static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
-                             const void* b, int M, int N, int K, const WsSource* src, hipStream_t st) {
+                             const void* b, int M, int N, int K, const WsSource* src, hipStream_t st, int ldy = -1) {
     if (gs != 16 && gs != 32 && gs != 64 && gs != 128) return false;
+    if (ldy < 0) ldy = N;
     // rows per slice: their byte codes within 64 MiB, a multiple of the 256-column tile
     int64_t nc = (int64_t(64) << 20) / K / kBN * kBN;
     nc = nc < kBN ? kBN : nc;
@@ -792,26 +799,28 @@ static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, c
             parts = &none;
         }
         switch (gs) {
-        case 16: launch_qmm_t<8, 16, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
-        case 32: launch_qmm_t<8, 32, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
-        case 64: launch_qmm_t<8, 64, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
-        default: launch_qmm_t<8, 128, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, N); break;
+        case 16: launch_qmm_t<8, 16, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
+        case 32: launch_qmm_t<8, 32, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
+        case 64: launch_qmm_t<8, 64, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
+        default: launch_qmm_t<8, 128, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
         }
     }
     return true;
 }
 
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
-                     const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st) {
+                     const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st,
+                     int ldy) {
     if (bits == 4) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<4, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<4, F16T>(gs, y, x, w, s, b, M, N, K, ws, st);
+        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<4, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<4, F16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
     } else if (bits == 8) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, ws, st);
+        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
     } else if (bits == 2 || bits == 3 || bits == 5 || bits == 6) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_odd_t<BF16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_odd_t<F16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st);
+        if (scale_dtype == EQ_DTYPE_BF16)
+            return launch_qmm_odd_t<BF16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st, ldy);
+        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_odd_t<F16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st, ldy);
     }
     return false;
 }

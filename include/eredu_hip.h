@@ -173,6 +173,12 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
  * (safemlx/src/native_quantization.rs:741-772; its Metal kernels for these
  * formats at :1320-1400,1856), whose CUDA/CPU builds decode on the host
  * (:846-913).  x 16-byte aligned; a Q4_K payload 16-byte aligned.
+ * Above 8 activation rows (prefill) the blocks are re-packed per call, in
+ * slices of at most 128 MiB held in the library's per-stream workspace, to the
+ * affine triple (f16 scale and bias; IQ4: levels as bytes with an f16
+ * factor) and multiplied on the bf16 matrix cores, weights dequantized to
+ * bf16 as MLX's quantized matmul does; the first such call on a stream may
+ * allocate that workspace.
  */
 int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
                    int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream);

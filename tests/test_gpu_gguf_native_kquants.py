@@ -154,3 +154,56 @@ def test_native_layer_placeholder_for_q6k(cuda):
     ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ closed_form(T.Q6K, raw, N, K).T
     ok, worst, _ = orc.matmul_within_tolerance(host_f32(lin.forward(dev_bf16(xb))), ref, True)
     assert ok, worst
+
+
+def native_closed_form(ty, raw, N, K):
+    """fp64 W of the native definition for the types with an affine form."""
+    from tests.test_oracle import _q4k_closed_form_f64
+
+    if ty == T.Q4K:
+        return _q4k_closed_form_f64(raw).astype(np.float64).reshape(N, K)
+    if ty == T.Q8_0:
+        b = raw.reshape(-1, 34)
+        d = b[:, 0:2].copy().view(np.float16).astype(np.float64)
+        return (d * b[:, 2:].view(np.int8).astype(np.float64)).reshape(N, K)
+    return closed_form(ty, raw, N, K)
+
+
+# Prefill (M > 8): the slice's blocks converted to the affine triple in the
+# workspace and multiplied on the matrix cores (4/8-bit directly, 5/6-bit
+# through the byte re-pack); M = 12, 17 and 130 leave partial 128-row tiles.
+@pytest.mark.parametrize("ty,K", [(T.Q4K, 2048), (T.Q5K, 1024), (T.Q6K, 2048), (T.Q5_1, 1024), (T.Q8_0, 2048)])
+@pytest.mark.parametrize("M", [12, 17, 64, 130])
+def test_native_linear_prefill(cuda, ty, K, M):
+    print(f"[case] native prefill {ty.name} N=384 K={K} M={M}", flush=True)
+    N = 384
+    vals, _ = ty.block_and_bytes()
+    raw = synthetic_blocks(int(ty), N * K // vals, seed=K + M + int(ty) + 1)
+    desc = G.TensorDescriptor("blk.0.ffn_up.weight", [K, N], ty, raw.size)
+    xb = synthetic_x(M, K, M)
+    y = G.linear(dev_bf16(xb), desc, dev_u8(raw))
+    ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ native_closed_form(ty, raw, N, K).T
+    ok, worst, _ = orc.matmul_within_tolerance(host_f32(y), ref, True)
+    assert ok, (ty.name, M, worst)
+    if ty in (T.Q6K, T.Q4K):  # big-endian blocks
+        stored = _to_big_endian(int(ty), raw) if ty == T.Q6K else raw.reshape(-1, 144)[:, [1, 0, 3, 2] + list(range(4, 144))].reshape(-1)
+        yb = G.linear(dev_bf16(xb), desc, dev_u8(stored), G.Endian.Big)
+        ok, worst, _ = orc.matmul_within_tolerance(host_f32(yb), ref, True)
+        assert ok, (ty.name, M, "big", worst)
+
+
+def test_native_prefill_in_slices(cuda):
+    """Q8_0 with more rows than one 128 MiB slice of the re-packed triple
+    (28928 rows at K = 4096): two equal slices of 14848 rows (the second
+    14592), each writing its columns of y."""
+    print("[case] native prefill Q8_0 N=29440 K=4096 M=40", flush=True)
+    N, K, M = 29440, 4096, 40
+    raw = synthetic_blocks(int(T.Q8_0), N * K // 32, seed=12)
+    desc = G.TensorDescriptor("w", [K, N], T.Q8_0, raw.size)
+    xb = synthetic_x(M, K, 13)
+    y = host_f32(G.linear(dev_bf16(xb), desc, dev_u8(raw)))
+    rows = np.concatenate([np.arange(0, 64), np.arange(14800, 14900), np.arange(N - 64, N)])
+    Wr = native_closed_form(T.Q8_0, raw.reshape(N, -1)[rows].reshape(-1), len(rows), K)
+    ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ Wr.T
+    ok, worst, _ = orc.matmul_within_tolerance(y[:, rows], ref, True)
+    assert ok, worst

@@ -150,7 +150,8 @@ def test_prefill_widths_on_matrix_cores(cuda, bits, gs, sdt, biases, M, N, K):
 
 def test_prefill_odd_width_in_weight_slices(cuda):
     """More weight rows than one 64 MiB slice of byte codes (16384 rows at
-    K = 4096): two slices, each writing its columns of y (no split K)."""
+    K = 4096): two slices, each writing its columns of y (split K, the
+    reduce writing at y's row stride)."""
     from tests.fixtures import device_random_linear, host_rows
 
     print("[case] prefill 6-bit g16 N=16640 K=4096 M=24", flush=True)
