@@ -1753,6 +1753,88 @@ extern "C" int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len
     return check_launch("gguf dequantize");
 }
 
+namespace eq {
+namespace {
+
+// Rows of a tensor's blocks picked by device token ids into a contiguous
+// buffer, one workgroup per token (16-byte copies when every row starts
+// 16-byte aligned).  An id outside [0, rows) copies nothing; its output row
+// is cleared after the decode by embedding_clear_rows.
+__global__ __launch_bounds__(256) void embedding_gather_rows(uint8_t* __restrict__ dst,
+                                                             const uint8_t* __restrict__ raw,
+                                                             const int32_t* __restrict__ tokens, int64_t rows,
+                                                             int64_t row_bytes, bool vec) {
+    const int64_t t = blockIdx.x;
+    const int32_t id = tokens[t];
+    if (id < 0 || id >= rows) return;
+    const uint8_t* src = raw + int64_t(id) * row_bytes;
+    uint8_t* d = dst + t * row_bytes;
+    if (vec) {
+        const int64_t n16 = row_bytes / 16;
+        for (int64_t i = threadIdx.x; i < n16; i += blockDim.x)
+            reinterpret_cast<uint4*>(d)[i] = reinterpret_cast<const uint4*>(src)[i];
+    } else {
+        for (int64_t i = threadIdx.x; i < row_bytes; i += blockDim.x) d[i] = src[i];
+    }
+}
+
+// Zeroes (+0) the output row of every id outside [0, rows).
+template <typename E>
+__global__ __launch_bounds__(256) void embedding_clear_rows(E* __restrict__ out, const int32_t* __restrict__ tokens,
+                                                            int64_t rows, int64_t cols) {
+    const int64_t t = blockIdx.x;
+    const int32_t id = tokens[t];
+    if (id >= 0 && id < rows) return;
+    for (int64_t i = threadIdx.x; i < cols; i += blockDim.x) out[t * cols + i] = E(0);
+}
+
+}  // namespace
+}  // namespace eq
+
+extern "C" int eq_gguf_embedding(void* out, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t rows,
+                                 int64_t cols, const int32_t* tokens, int64_t n_tokens, int endian, int out_dtype,
+                                 eq_stream_t stream) {
+    clear_error();
+    Geometry geo;
+    int64_t nblocks;
+    if (validate(raw, raw_len, ggml_type, rows, cols, endian, geo, nblocks)) return 1;
+    if (out_dtype != EQ_DTYPE_BF16 && out_dtype != EQ_DTYPE_F32) {
+        set_error("embedding output must be bf16 or f32");
+        return 1;
+    }
+    if (n_tokens < 0 || n_tokens > INT32_MAX) {
+        set_error("token count must be in [0, 2^31 - 1]");
+        return 1;
+    }
+    if (n_tokens == 0) return 0;
+    if (!out || !tokens || !aligned(out, 16) || !aligned(tokens, 4)) {
+        set_error("out must be a non-null 16-byte aligned pointer and tokens a non-null int32 pointer");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int64_t row_bytes = cols / geo.values * geo.bytes;
+    uint8_t* picked = static_cast<uint8_t*>(ws_acquire(nullptr, size_t(n_tokens) * size_t(row_bytes), st));
+    if (!picked) {
+        set_error("could not obtain " + std::to_string(n_tokens * row_bytes) +
+                  " bytes of workspace for the picked rows (first call on a stream under graph capture?)");
+        return 1;
+    }
+    const bool vec = aligned(raw, 16) && row_bytes % 16 == 0;
+    embedding_gather_rows<<<dim3(unsigned(n_tokens)), 256, 0, st>>>(picked, raw, tokens, rows, row_bytes, vec);
+    const bool big = endian == EQ_ENDIAN_BIG;
+    const int64_t nb = n_tokens * (cols / geo.values);
+    if (out_dtype == EQ_DTYPE_BF16) {
+        launch_dense<BF16T>(ggml_type, big, true, picked, nb, row_bytes % 16 == 0, static_cast<uint16_t*>(out), st);
+        embedding_clear_rows<uint16_t><<<dim3(unsigned(n_tokens)), 256, 0, st>>>(static_cast<uint16_t*>(out), tokens,
+                                                                                 rows, cols);
+    } else {
+        launch_dense<F32T>(ggml_type, big, true, picked, nb, row_bytes % 16 == 0, static_cast<float*>(out), st);
+        embedding_clear_rows<float><<<dim3(unsigned(n_tokens)), 256, 0, st>>>(static_cast<float*>(out), tokens, rows,
+                                                                              cols);
+    }
+    return check_launch("gguf embedding");
+}
+
 extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
                               int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream) {
     clear_error();

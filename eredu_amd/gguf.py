@@ -276,6 +276,41 @@ def dequantize(
     return out
 
 
+def embedding(
+    indices: torch.Tensor,
+    desc: TensorDescriptor,
+    raw: torch.Tensor,
+    endian: Endian = Endian.Little,
+    dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Rows ``indices`` of the GGUF tensor of ``desc`` decoded by the native
+    definition, shape indices.shape + [cols], float32 like the reference (or
+    bfloat16, its round-to-nearest-even image): NativeQuantizedTensor::embedding
+    (safemlx/src/native_quantization.rs:774-789, 915-939); C ABI
+    eq_gguf_embedding.  An index outside [0, rows) raises the reference's
+    error (checked here, one device read of the ids, as the reference
+    evaluates them on the host)."""
+    ty = _device_type(desc)
+    _check_raw(desc, raw)
+    _, rows, cols = _rows_cols(desc)
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise EreduError("embedding output dtype must be bfloat16 or float32")
+    ids = indices.to(device=raw.device, dtype=torch.int32).contiguous()
+    flat = ids.view(-1)
+    bad = ((flat < 0) | (flat >= rows)).nonzero()
+    if bad.numel():
+        raise EreduError(f"native embedding index {int(flat[int(bad[0])].item())} is outside 0..{rows}")
+    out = torch.empty(list(ids.shape) + [cols], dtype=dtype, device=raw.device)
+    code = _native.EQ_DTYPE_BF16 if dtype == torch.bfloat16 else _native.EQ_DTYPE_F32
+    check(
+        _native.lib().eq_gguf_embedding(
+            out.data_ptr(), raw.contiguous().data_ptr(), raw.numel(), int(ty), rows, cols, ids.data_ptr(),
+            ids.numel(), int(endian), code, torch.cuda.current_stream().cuda_stream,
+        )
+    )
+    return out
+
+
 def linear(x: torch.Tensor, desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little) -> torch.Tensor:
     """y = x . W^T with W the GGUF tensor of ``desc`` decoded by the native
     definition, straight from its Q4_K, Q5_K, Q6_K, Q5_1 or Q8_0 blocks (no
@@ -336,6 +371,11 @@ class NativeTensor:
         """NativeQuantizedTensor::dequantize: the native decoders
         (safemlx/src/native_quantization.rs:3417-3542)."""
         return dequantize(self.descriptor(), self.data, self.endian, DequantDefinition.Native, dtype)
+
+    def embedding(self, indices: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """NativeQuantizedTensor::embedding (native_quantization.rs:774-789):
+        rows ``indices`` decoded by the native definition."""
+        return embedding(indices, self.descriptor(), self.data, self.endian, dtype)
 
     def linear(self, x: torch.Tensor, transpose: bool = True) -> torch.Tensor:
         """NativeQuantizedTensor::linear (native_quantization.rs:741-772): y = x . W^T

@@ -163,6 +163,23 @@ int eq_gguf_dequantize(void* out, const uint8_t* raw, int64_t raw_len, int ggml_
                        eq_stream_t stream);
 
 /*
+ * Native GGUF embedding: out[t, :] = row tokens[t] of the [rows, cols] GGUF
+ * tensor (raw blocks as stored, raw_len bytes) decoded by the native
+ * definition (as eq_gguf_dequantize with EQ_DEQUANT_NATIVE), as out_dtype
+ * (EQ_DTYPE_F32, the reference's output, or EQ_DTYPE_BF16, its
+ * round-to-nearest-even image).  tokens: n_tokens device int32 ids; an id
+ * outside [0, rows) gives a row of +0 (the ids are not read on the host).
+ * The picked rows' blocks are copied into the library's per-stream
+ * workspace (n_tokens * row bytes; the first call on a stream may allocate)
+ * and decoded there.  out 16-byte aligned.  Replaces
+ * NativeQuantizedTensor::embedding (safemlx/src/native_quantization.rs:
+ * 774-789; its CPU streaming path :915-939 with decode_native_row :948-996,
+ * whose out-of-range id is an error).
+ */
+int eq_gguf_embedding(void* out, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t rows, int64_t cols,
+                      const int32_t* tokens, int64_t n_tokens, int endian, int out_dtype, eq_stream_t stream);
+
+/*
  * Native GGUF linear: y[M, N] = x[M, K] . W^T with W the GGUF tensor (MLX
  * shape [N, K], raw Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL or IQ4_XS blocks as stored, raw_len
  * bytes) decoded by the native definition (Q4_K: d*sc*q - dmin*m, Q5_K the

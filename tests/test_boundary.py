@@ -27,7 +27,8 @@ def test_header_declares_the_boundary():
         ["eq_last_error", "eq_version", "eq_quantized_matmul", "eq_quantized_matmul_batched", "eq_dequantize",
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
          "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
-         "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc", "eq_gguf_convert_mxfp4"]
+         "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc", "eq_gguf_convert_mxfp4",
+         "eq_gguf_embedding"]
     )
 
 
@@ -148,6 +149,20 @@ def test_gguf_dequant_rejects_bad_definition_and_dtype():
     assert "definition" in L.eq_last_error().decode()
     assert L.eq_gguf_dequantize(aligned, aligned, 36, 2, 2, 32, 0, 0, 1, None) != 0
     assert "bf16 or f32" in L.eq_last_error().decode()
+
+
+def test_gguf_embedding_rejects():
+    buf = ctypes.create_string_buffer(4096)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a = (p.value + 15) // 16 * 16
+    f32, bf16 = 0, 2
+    _rejects(L.eq_gguf_embedding(a, a, 144, 12, 1, 256, a, 1, 0, 1, None), "bf16 or f32")
+    _rejects(L.eq_gguf_embedding(a, a, 144, 12, 1, 256, a, -1, 0, f32, None), "token count")
+    _rejects(L.eq_gguf_embedding(None, a, 144, 12, 1, 256, a, 1, 0, f32, None), "non-null")
+    _rejects(L.eq_gguf_embedding(a, a, 144, 12, 1, 256, None, 1, 0, bf16, None), "non-null")
+    _rejects(L.eq_gguf_embedding(a + 8, a, 144, 12, 1, 256, a, 1, 0, f32, None), "aligned")
+    _rejects(L.eq_gguf_embedding(a, a, 143, 12, 1, 256, a, 1, 0, f32, None), "")  # payload length
+    assert L.eq_gguf_embedding(None, a, 144, 12, 1, 256, None, 0, 0, f32, None) == 0  # no tokens
 
 
 def test_host_mirror_fails_loudly_without_gpu_tensors():
