@@ -321,6 +321,40 @@ def bench_gguf(steps, warmup):
     return out
 
 
+def bench_gguf_grouped(steps, warmup):
+    """Native GGUF mixture-of-experts linear (eq_gguf_grouped_linear): an
+    expert bank of 8 x 14336 x 4096 (Mixtral's gate projection shape) in
+    Q4_K and Q6_K blocks; decode = 2 routes (top-2 of one token), prefill =
+    1024 routes (512 tokens x top-2, sorted ids).  Banks rotate >= 300 MB."""
+    import torch
+
+    n = _lib()
+    out = {}
+    from eredu_amd.gguf import GgmlType as T
+    experts, N, K = 8, 14336, 4096
+    for ty in (T.Q4K, T.Q6K):
+        vals, nbytes = ty.block_and_bytes()
+        nraw = experts * N * K // vals * nbytes
+        banks = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(rotation(nraw))]
+        for label, routes in (("decode_2routes", 2), ("prefill_1024routes", 1024)):
+            ids = torch.sort(torch.randint(0, experts, (routes,), device="cuda", dtype=torch.int32)).values
+            x = torch.randn((routes, K), device="cuda").to(torch.bfloat16)
+            y = torch.empty((routes, N), dtype=torch.bfloat16, device="cuda")
+
+            def call(st):
+                for bnk in banks:
+                    n.check(n.lib().eq_gguf_grouped_linear(y.data_ptr(), x.data_ptr(), bnk.data_ptr(), nraw, int(ty),
+                                                           experts, N, K, ids.data_ptr(), routes, 0,
+                                                           n.EQ_DTYPE_BF16, True, st))
+
+            ms = Timer(call).ms_per_replay(max(steps // 4, 5), warmup) / len(banks)
+            tf = 2.0 * routes * N * K / (ms * 1e-3) / 1e12
+            out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "copies": len(banks)}
+        del banks
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_qmm_n(steps, warmup):
     """transpose = false at M = 1 (x . W, W [K, N] packed along N; the
     safemlx default layout): N x K = 4096 x 4096 and 14336 x 4096, weight
@@ -821,6 +855,8 @@ def main():
         if args.gguf_only:
             log("[bench] gguf")
             out["gguf"] = bench_gguf(args.steps, args.warmup)
+            log("[bench] gguf mixture-of-experts linear")
+            out["gguf_grouped"] = bench_gguf_grouped(args.steps, args.warmup)
             log("[bench] gguf streaming load")
             out["gguf_stream"] = bench_gguf_stream()
             log("[bench] affine dequantize / quantize")
@@ -880,6 +916,8 @@ def main():
         detail["qmm_widths"] = bench_qmm_widths(args.steps, args.warmup)
         log("[bench] gguf")
         detail["gguf"] = bench_gguf(args.steps, args.warmup)
+        log("[bench] gguf mixture-of-experts linear")
+        detail["gguf_grouped"] = bench_gguf_grouped(args.steps, args.warmup)
         log("[bench] gguf streaming load")
         detail["gguf_stream"] = bench_gguf_stream()
         log("[bench] affine dequantize / quantize")

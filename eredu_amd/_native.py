@@ -27,6 +27,7 @@ SIGNATURES = {
     "eq_gguf_dequantize": ([_vp, _vp, _i64, _i32, _i64, _i64, _i32, _i32, _i32, _vp], _i32),
     "eq_gguf_linear": ([_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i32, _i32, _vp], _i32),
     "eq_gguf_embedding": ([_vp, _vp, _i64, _i32, _i64, _i64, _vp, _i64, _i32, _i32, _vp], _i32),
+    "eq_gguf_grouped_linear": ([_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _b, _vp], _i32),
     "eq_gather_qmm": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _b, _i32, _i32,
                        ctypes.c_char_p, _i32, _i32, _b, _vp], _i32),
     "eq_quantize": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, ctypes.c_char_p, _i32, _vp], _i32),

@@ -472,7 +472,16 @@ unsigned* ws_counters(const WsSource* src, hipStream_t st);
 // workspace cannot be provided or the combination has no kernel.
 bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                         const void* s, const void* b, const int32_t* lhs, const int32_t* rhs, int batch,
-                        int64_t x_batches, int experts, int N, int K, hipStream_t st);
+                        int64_t x_batches, int experts, int N, int K, hipStream_t st,
+                        const WsSource* src = nullptr);
+
+// Everything of eq_gather_qmm after argument validation (gather.hip); `src`
+// (or the stream's workspace when null) holds the grouped path's scratch.
+int gather_qmm_launch(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                      const int32_t* lhs_indices, const int32_t* rhs_indices, int64_t batch, int64_t x_batches,
+                      int64_t w_batches, int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
+                      QuantMode qm, int x_dtype, int scale_dtype, bool sorted_indices, const WsSource* src,
+                      hipStream_t st);
 
 // Prefill qmm (qmm.hip): M > 16, x bf16, transpose, 4/8-bit, bf16/f16 scales,
 // N % 128 == 0, K % 64 == 0, 16-byte aligned x and w, 8-byte aligned y.  Any

@@ -235,6 +235,78 @@ void launch_gather_qmv_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, 
 
 using namespace eq;
 
+namespace eq {
+
+int gather_qmm_launch(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                      const int32_t* lhs_indices, const int32_t* rhs_indices, int64_t batch, int64_t x_batches,
+                      int64_t w_batches, int64_t M, int64_t N, int64_t K, bool transpose, int group_size, int bits,
+                      QuantMode qm, int x_dtype, int scale_dtype, bool sorted_indices, const WsSource* src,
+                      hipStream_t st) {
+    const GatherIdx g{lhs_indices, rhs_indices, x_batches, w_batches};
+    if (qm == kModeMxFp4)
+        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), g, batch, M, N, K, transpose, x_dtype,
+                            sorted_indices, nullptr, st);
+
+    // many routes over sorted experts: one MFMA GEMM per expert's rows
+    const bool grouped = transpose && M == 1 && sorted_indices && rhs_indices && x_dtype == EQ_DTYPE_BF16 &&
+                         scale_dtype != EQ_DTYPE_F32 && (bits == 4 || bits == 8) && batch >= 64 &&
+                         batch >= 2 * w_batches && batch <= INT32_MAX && w_batches <= INT32_MAX && N % 128 == 0 &&
+                         K % 64 == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 8) &&
+                         int64_t(N) * K * bits / 8 < (int64_t(1) << 31) && batch * K * 2 < (int64_t(1) << 31);
+    if (grouped && launch_qmm_grouped(bits, group_size, scale_dtype, static_cast<uint16_t*>(y),
+                                      static_cast<const uint16_t*>(x), w, scales, biases, lhs_indices, rhs_indices,
+                                      int(batch), x_batches, int(w_batches), int(N), int(K), st, src))
+        return check_launch("gather_qmm (grouped qmm)");
+    const bool fast = transpose && M == 1 && x_dtype == EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F32 &&
+                      (bits == 4 || bits == 8) && fast_group_size(group_size) && aligned(x, 16) && aligned(w, 16);
+    if (!transpose && M <= 8 && x_dtype == EQ_DTYPE_BF16 &&
+        launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales,
+                           biases, g, batch, int(M), int(N), int(K), group_size, nullptr, st))
+        return check_launch("gather_qmm (qmm_n)");
+    for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
+        const unsigned nb = unsigned(batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY);
+        if (fast) {
+            uint16_t* yy = static_cast<uint16_t*>(y);
+            const uint16_t* xx = static_cast<const uint16_t*>(x);
+            const uint16_t* ss = static_cast<const uint16_t*>(scales);
+            const uint16_t* bb = static_cast<const uint16_t*>(biases);
+            if (scale_dtype == EQ_DTYPE_BF16) {
+                if (bits == 4) launch_gather_qmv_gs<4, BF16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
+                else launch_gather_qmv_gs<8, BF16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
+            } else {
+                if (bits == 4) launch_gather_qmv_gs<4, F16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
+                else launch_gather_qmv_gs<8, F16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
+            }
+            continue;
+        }
+        with_bits(bits, [&](auto bc) {
+            constexpr int B = decltype(bc)::value;
+            with_dtype(x_dtype, [&](auto xt) {
+                typedef decltype(xt) XT;
+                with_dtype(scale_dtype, [&](auto stt) {
+                    typedef decltype(stt) ST;
+                    typedef typename XT::storage XS;
+                    typedef typename ST::storage SS;
+                    if (transpose) {
+                        const dim3 grid(unsigned((N + kGenRowsPerWG - 1) / kGenRowsPerWG), nb);
+                        gather_t_general<B, XT, ST><<<grid, 64 * kGenRowsPerWG, 0, st>>>(
+                            static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
+                            static_cast<const SS*>(biases), g, b0, M, N, K, group_size);
+                    } else {
+                        const dim3 grid(unsigned((N + 255) / 256), unsigned((M + kGenMChunk - 1) / kGenMChunk), nb);
+                        gather_n_general<B, XT, ST><<<grid, 256, 0, st>>>(
+                            static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
+                            static_cast<const SS*>(biases), g, b0, M, N, K, group_size);
+                    }
+                });
+            });
+        });
+    }
+    return check_launch("gather_qmm");
+}
+
+}  // namespace eq
+
 extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
                              const int32_t* lhs_indices, const int32_t* rhs_indices, int64_t batch, int64_t x_batches,
                              int64_t w_batches, int64_t M, int64_t N, int64_t K, bool transpose, int group_size,
@@ -285,66 +357,7 @@ extern "C" int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const vo
         set_error("M exceeds " + std::to_string(kMaxGridY * kGenMChunk) + " rows per batch (transpose = false)");
         return 1;
     }
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const GatherIdx g{lhs_indices, rhs_indices, x_batches, w_batches};
-    if (qm == kModeMxFp4)
-        return mxfp4_matmul(y, x, w, static_cast<const uint8_t*>(scales), g, batch, M, N, K, transpose, x_dtype,
-                            sorted_indices, nullptr, st);
-
-    // many routes over sorted experts: one MFMA GEMM per expert's rows
-    const bool grouped = transpose && M == 1 && sorted_indices && rhs_indices && x_dtype == EQ_DTYPE_BF16 &&
-                         scale_dtype != EQ_DTYPE_F32 && (bits == 4 || bits == 8) && batch >= 64 &&
-                         batch >= 2 * w_batches && batch <= INT32_MAX && w_batches <= INT32_MAX && N % 128 == 0 &&
-                         K % 64 == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 8) &&
-                         int64_t(N) * K * bits / 8 < (int64_t(1) << 31) && batch * K * 2 < (int64_t(1) << 31);
-    if (grouped && launch_qmm_grouped(bits, group_size, scale_dtype, static_cast<uint16_t*>(y),
-                                      static_cast<const uint16_t*>(x), w, scales, biases, lhs_indices, rhs_indices,
-                                      int(batch), x_batches, int(w_batches), int(N), int(K), st))
-        return check_launch("gather_qmm (grouped qmm)");
-    const bool fast = transpose && M == 1 && x_dtype == EQ_DTYPE_BF16 && scale_dtype != EQ_DTYPE_F32 &&
-                      (bits == 4 || bits == 8) && fast_group_size(group_size) && aligned(x, 16) && aligned(w, 16);
-    if (!transpose && M <= 8 && x_dtype == EQ_DTYPE_BF16 &&
-        launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales,
-                           biases, g, batch, int(M), int(N), int(K), group_size, nullptr, st))
-        return check_launch("gather_qmm (qmm_n)");
-    for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
-        const unsigned nb = unsigned(batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY);
-        if (fast) {
-            uint16_t* yy = static_cast<uint16_t*>(y);
-            const uint16_t* xx = static_cast<const uint16_t*>(x);
-            const uint16_t* ss = static_cast<const uint16_t*>(scales);
-            const uint16_t* bb = static_cast<const uint16_t*>(biases);
-            if (scale_dtype == EQ_DTYPE_BF16) {
-                if (bits == 4) launch_gather_qmv_gs<4, BF16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
-                else launch_gather_qmv_gs<8, BF16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
-            } else {
-                if (bits == 4) launch_gather_qmv_gs<4, F16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
-                else launch_gather_qmv_gs<8, F16T>(group_size, yy, xx, w, ss, bb, g, b0, nb, int(N), int(K), st);
-            }
-            continue;
-        }
-        with_bits(bits, [&](auto bc) {
-            constexpr int B = decltype(bc)::value;
-            with_dtype(x_dtype, [&](auto xt) {
-                typedef decltype(xt) XT;
-                with_dtype(scale_dtype, [&](auto stt) {
-                    typedef decltype(stt) ST;
-                    typedef typename XT::storage XS;
-                    typedef typename ST::storage SS;
-                    if (transpose) {
-                        const dim3 grid(unsigned((N + kGenRowsPerWG - 1) / kGenRowsPerWG), nb);
-                        gather_t_general<B, XT, ST><<<grid, 64 * kGenRowsPerWG, 0, st>>>(
-                            static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
-                            static_cast<const SS*>(biases), g, b0, M, N, K, group_size);
-                    } else {
-                        const dim3 grid(unsigned((N + 255) / 256), unsigned((M + kGenMChunk - 1) / kGenMChunk), nb);
-                        gather_n_general<B, XT, ST><<<grid, 256, 0, st>>>(
-                            static_cast<XS*>(y), static_cast<const XS*>(x), w, static_cast<const SS*>(scales),
-                            static_cast<const SS*>(biases), g, b0, M, N, K, group_size);
-                    }
-                });
-            });
-        });
-    }
-    return check_launch("gather_qmm");
+    return gather_qmm_launch(y, x, w, scales, biases, lhs_indices, rhs_indices, batch, x_batches, w_batches, M, N, K,
+                             transpose, group_size, bits, qm, x_dtype, scale_dtype, sorted_indices, nullptr,
+                             reinterpret_cast<hipStream_t>(stream));
 }

@@ -1951,3 +1951,139 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
     }
     return check_launch("gguf linear");
 }
+
+namespace eq {
+namespace {
+
+// Routes at or below this count take one native linear launch per route on a
+// copy of the route's expert matrix; above it the bank is re-packed once and
+// the routes run as one gathered (grouped when sorted) matrix product.
+constexpr int64_t kGroupedCopyRoutes = 16;
+
+// Matrix ids[r] of an expert bank (matrix_bytes each) copied to
+// dst + r * matrix_bytes; grid (chunks, routes).  An id outside
+// [0, experts) copies nothing (its output row is cleared afterwards).
+__global__ __launch_bounds__(256) void expert_gather_matrices(uint8_t* __restrict__ dst,
+                                                              const uint8_t* __restrict__ raw,
+                                                              const int32_t* __restrict__ ids, int64_t experts,
+                                                              int64_t matrix_bytes, bool vec) {
+    const int64_t r = blockIdx.y;
+    const int32_t e = ids[r];
+    if (e < 0 || e >= experts) return;
+    const uint8_t* src = raw + int64_t(e) * matrix_bytes;
+    uint8_t* d = dst + r * matrix_bytes;
+    const int64_t step = int64_t(gridDim.x) * blockDim.x;
+    if (vec) {
+        const int64_t n16 = matrix_bytes / 16;
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += step)
+            reinterpret_cast<uint4*>(d)[i] = reinterpret_cast<const uint4*>(src)[i];
+    } else {
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < matrix_bytes; i += step) d[i] = src[i];
+    }
+}
+
+}  // namespace
+}  // namespace eq
+
+extern "C" int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type,
+                                      int64_t experts, int64_t N, int64_t K, const int32_t* ids, int64_t routes,
+                                      int endian, int x_dtype, bool sorted_ids, eq_stream_t stream) {
+    clear_error();
+    const bool native = ggml_type == EQ_GGML_Q4_K || ggml_type == EQ_GGML_Q8_0 || ggml_type == EQ_GGML_Q5_1 ||
+                        ggml_type == EQ_GGML_Q5_K || ggml_type == EQ_GGML_Q6_K || ggml_type == EQ_GGML_IQ4_NL ||
+                        ggml_type == EQ_GGML_IQ4_XS;
+    if (!native) {
+        set_error("native GGUF grouped linear covers Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL and IQ4_XS");
+        return 1;
+    }
+    if (experts <= 0 || N <= 0 || experts > INT32_MAX || N > INT32_MAX || K > INT32_MAX ||
+        experts * N > INT64_MAX / (K > 0 ? K : 1)) {
+        set_error("invalid expert bank shape");
+        return 1;
+    }
+    Geometry geo;
+    int64_t nblocks;
+    if (validate(raw, raw_len, ggml_type, experts * N, K, endian, geo, nblocks)) return 1;
+    if (x_dtype != EQ_DTYPE_BF16) {
+        set_error("native GGUF grouped linear takes bf16 activations");
+        return 1;
+    }
+    if (routes < 0 || routes > INT32_MAX) {
+        set_error("route count must be in [0, 2^31 - 1]");
+        return 1;
+    }
+    if (routes == 0) return 0;
+    if (!y || !x || !ids || !aligned(ids, 4)) {
+        set_error("null pointer argument");
+        return 1;
+    }
+    if (!aligned(x, 16) || !aligned(y, 8)) {
+        set_error("x must be 16-byte and y 8-byte aligned");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool big = endian == EQ_ENDIAN_BIG;
+    const int64_t row_bytes = K / geo.values * geo.bytes, matrix_bytes = N * row_bytes;
+    uint16_t* yy = static_cast<uint16_t*>(y);
+    const uint16_t* xx = static_cast<const uint16_t*>(x);
+    if (routes <= kGroupedCopyRoutes) {
+        // decode: each route's matrix copied out, then the native linear at M = 1 on it
+        uint8_t* mats = static_cast<uint8_t*>(ws_acquire(nullptr, size_t(routes) * size_t(matrix_bytes), st));
+        if (!mats) {
+            set_error("could not obtain workspace for the routes' expert matrices");
+            return 1;
+        }
+        const int64_t n16 = matrix_bytes / 16;
+        const unsigned chunks = unsigned(n16 / 256 + 1 < 1024 ? n16 / 256 + 1 : 1024);
+        expert_gather_matrices<<<dim3(chunks, unsigned(routes)), 256, 0, st>>>(
+            mats, raw, ids, experts, matrix_bytes, aligned(raw, 16) && matrix_bytes % 16 == 0);
+        if (check_launch("gguf grouped linear (gather)")) return 1;
+        for (int64_t r = 0; r < routes; r++) {
+            if (eq_gguf_linear(yy + r * N, xx + r * K, mats + r * matrix_bytes, matrix_bytes, ggml_type, 1, N, K,
+                               endian, x_dtype, stream))
+                return 1;
+        }
+    } else {
+        // prefill: the bank re-packed once (as the native prefill does), then the gathered product
+        if (N % 128 != 0 || K % 64 != 0) {
+            set_error("more than " + std::to_string(kGroupedCopyRoutes) +
+                      " routes need N % 128 == 0 and K % 64 == 0");
+            return 1;
+        }
+        const bool as_bytes = !geo.affine || (geo.bits != 4 && geo.bits != 8);
+        const int bits = as_bytes ? 8 : geo.bits;
+        auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
+        const size_t wsz = up(size_t(experts * N) * size_t(K) * bits / 8);
+        const size_t psz = up(size_t(experts * N) * size_t(K / geo.gs) * 2);
+        const size_t triple = wsz + 2 * psz;
+        const int cap = int(experts + (routes + 127) / 128);
+        const size_t rest = up(size_t(routes) * size_t(K) * 2) + size_t(cap) * 16 + 256;
+        char* base = static_cast<char*>(ws_acquire(nullptr, triple + rest, st));
+        if (!base) {
+            set_error("could not obtain workspace for the re-packed expert bank");
+            return 1;
+        }
+        uint32_t* w = reinterpret_cast<uint32_t*>(base);
+        uint16_t* s = reinterpret_cast<uint16_t*>(base + wsz);
+        uint16_t* b = reinterpret_cast<uint16_t*>(base + wsz + psz);
+        const WsSource tail{base + triple, rest, nullptr};
+        const bool v16 = aligned(raw, 16);
+        if (!as_bytes) {
+            launch_convert_affine(ggml_type, big, raw, nblocks, v16, w, s, b, st);
+        } else if (!with_kq(ggml_type, big, [&](auto t, auto bt) {
+                       constexpr int T = decltype(t)::value;
+                       constexpr int NB = 256 / KQuant<T>::units;
+                       kq_to_bytes<T, decltype(bt)::value><<<dim3(unsigned((nblocks + NB - 1) / NB)), 256, 0, st>>>(
+                           raw, nblocks, v16, reinterpret_cast<uint4*>(w), s, b);
+                   })) {
+            set_error("no re-pack kernel for this encoding");
+            return 1;
+        }
+        if (gather_qmm_launch(y, x, w, s, b, nullptr, ids, routes, routes, experts, 1, N, K, true, geo.gs, bits,
+                              kModeAffine, EQ_DTYPE_BF16, EQ_DTYPE_F16, sorted_ids, &tail, st))
+            return 1;
+    }
+    // the rows of ids outside the bank are +0
+    embedding_clear_rows<uint16_t><<<dim3(unsigned(routes)), 256, 0, st>>>(yy, ids, experts, N);
+    return check_launch("gguf grouped linear");
+}

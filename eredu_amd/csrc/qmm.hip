@@ -654,12 +654,12 @@ __global__ __launch_bounds__(256) void qmm_zero(uint16_t* __restrict__ y, int64_
 template <int BITS, int GS, typename ST>
 static bool launch_qmm_grouped_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
                                  const int32_t* lhs, const int32_t* rhs, int batch, int64_t x_batches, int experts,
-                                 int N, int K, hipStream_t st) {
+                                 int N, int K, hipStream_t st, const WsSource* src = nullptr) {
     const int cap = experts + (batch + kBM - 1) / kBM;  // sum over experts of ceil(rows / kBM)
     // one launch with 32-bit offsets: each expert's codes and the gathered rows below 2^31 bytes
     if (int64_t(N) * K * BITS / 8 >= (int64_t(1) << 31) || int64_t(batch) * K * 2 >= (int64_t(1) << 31)) return false;
     const size_t xg_bytes = (size_t(batch) * size_t(K) * 2u + 255u) & ~size_t(255);
-    void* ws = ws_acquire(nullptr, xg_bytes + size_t(cap) * sizeof(int4), st);
+    void* ws = ws_acquire(src, xg_bytes + size_t(cap) * sizeof(int4), st);
     if (!ws) return false;
     uint16_t* xg = reinterpret_cast<uint16_t*>(ws);
     int4* list = reinterpret_cast<int4*>(reinterpret_cast<char*>(ws) + xg_bytes);
@@ -682,28 +682,37 @@ static bool launch_qmm_grouped_t(uint16_t* y, const uint16_t* x, const uint32_t*
 template <int BITS, typename ST>
 static bool launch_qmm_grouped_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
                                   const void* b, const int32_t* lhs, const int32_t* rhs, int batch,
-                                  int64_t x_batches, int experts, int N, int K, hipStream_t st) {
+                                  int64_t x_batches, int experts, int N, int K, const WsSource* src, hipStream_t st) {
     switch (gs) {
-    case 32: return launch_qmm_grouped_t<BITS, 32, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
-    case 64: return launch_qmm_grouped_t<BITS, 64, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
-    case 128: return launch_qmm_grouped_t<BITS, 128, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+    case 16:
+        return launch_qmm_grouped_t<BITS, 16, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st, src);
+    case 32:
+        return launch_qmm_grouped_t<BITS, 32, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st, src);
+    case 64:
+        return launch_qmm_grouped_t<BITS, 64, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st, src);
+    case 128:
+        return launch_qmm_grouped_t<BITS, 128, ST>(y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st, src);
     default: return false;
     }
 }
 
 bool launch_qmm_grouped(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                         const void* s, const void* b, const int32_t* lhs, const int32_t* rhs, int batch,
-                        int64_t x_batches, int experts, int N, int K, hipStream_t st) {
+                        int64_t x_batches, int experts, int N, int K, hipStream_t st, const WsSource* src) {
     if (bits == 4) {
         if (scale_dtype == EQ_DTYPE_BF16)
-            return launch_qmm_grouped_gs<4, BF16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+            return launch_qmm_grouped_gs<4, BF16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, src,
+                                                   st);
         if (scale_dtype == EQ_DTYPE_F16)
-            return launch_qmm_grouped_gs<4, F16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+            return launch_qmm_grouped_gs<4, F16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, src,
+                                                  st);
     } else if (bits == 8) {
         if (scale_dtype == EQ_DTYPE_BF16)
-            return launch_qmm_grouped_gs<8, BF16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+            return launch_qmm_grouped_gs<8, BF16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, src,
+                                                   st);
         if (scale_dtype == EQ_DTYPE_F16)
-            return launch_qmm_grouped_gs<8, F16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, st);
+            return launch_qmm_grouped_gs<8, F16T>(gs, y, x, w, s, b, lhs, rhs, batch, x_batches, experts, N, K, src,
+                                                  st);
     }
     return false;
 }

@@ -311,6 +311,44 @@ def embedding(
     return out
 
 
+def native_grouped_linear(input: torch.Tensor, weight: "NativeTensor", group_ids: torch.Tensor) -> torch.Tensor:
+    """y[r] = input[r] . W[group_ids[r]]^T for an expert bank W [experts, N, K]
+    kept in its GGUF blocks: safemlx's native_grouped_linear
+    (safemlx/src/native_quantization.rs:1039-1072; its CPU loop :1002-1037),
+    as eredu's MoE calls it on the routes' sorted expert ids
+    (eredu/src/backend/mlx/nn/moe.rs:1080-1092).  bf16 input [routes, K] ->
+    bf16 [routes, N]; C ABI eq_gguf_grouped_linear.  The reference's shape
+    and expert-range errors are raised here (one device read of the ids, as
+    the reference evaluates them on the host); whether they are sorted is
+    read the same way and picks the grouped matrix-core path."""
+    shape = list(weight.shape)
+    if input.dim() != 2 or group_ids.dim() != 1 or input.shape[0] != group_ids.shape[0] or len(shape) != 3 or \
+            input.shape[1] != shape[2]:
+        raise EreduError(f"native grouped linear shape mismatch: input {list(input.shape)}, ids "
+                         f"{list(group_ids.shape)}, weight {shape}")
+    experts, N, K = shape
+    ty = _device_type(weight.descriptor())
+    _check_raw(weight.descriptor(), weight.data)
+    if input.dtype != torch.bfloat16:
+        raise EreduError("native GGUF grouped linear takes bfloat16 activations")
+    ids = group_ids.to(device=weight.data.device, dtype=torch.int32).contiguous()
+    bad = ((ids < 0) | (ids >= experts)).nonzero()
+    if bad.numel():
+        raise EreduError(f"native grouped expert {int(ids[int(bad[0])].item())} is outside 0..{experts}")
+    routes = ids.numel()
+    sorted_ids = bool((ids[1:] >= ids[:-1]).all().item()) if routes > 1 else True
+    x = input.contiguous()
+    y = torch.empty((routes, N), dtype=torch.bfloat16, device=x.device)
+    check(
+        _native.lib().eq_gguf_grouped_linear(
+            y.data_ptr(), x.data_ptr(), weight.data.contiguous().data_ptr(), weight.data.numel(), int(ty), experts,
+            N, K, ids.data_ptr(), routes, int(weight.endian), _native.EQ_DTYPE_BF16, sorted_ids,
+            torch.cuda.current_stream().cuda_stream,
+        )
+    )
+    return y
+
+
 def linear(x: torch.Tensor, desc: TensorDescriptor, raw: torch.Tensor, endian: Endian = Endian.Little) -> torch.Tensor:
     """y = x . W^T with W the GGUF tensor of ``desc`` decoded by the native
     definition, straight from its Q4_K, Q5_K, Q6_K, Q5_1 or Q8_0 blocks (no

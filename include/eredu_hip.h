@@ -180,6 +180,27 @@ int eq_gguf_embedding(void* out, const uint8_t* raw, int64_t raw_len, int ggml_t
                       const int32_t* tokens, int64_t n_tokens, int endian, int out_dtype, eq_stream_t stream);
 
 /*
+ * Native GGUF grouped linear (mixture-of-experts): y[r, :] = x[r, :] . W[ids[r]]^T
+ * for r < routes, with W an expert bank [experts, N, K] of Q4_K, Q5_K, Q6_K,
+ * Q5_1, Q8_0, IQ4_NL or IQ4_XS blocks as stored (raw_len bytes, experts * N
+ * rows of K values); x [routes, K] and y [routes, N] bf16; ids device int32,
+ * an id outside [0, experts) gives a row of +0.  Up to 16 routes: each
+ * route's expert matrix is copied into the library's per-stream workspace
+ * and run through eq_gguf_linear at M = 1 (native definition, f32 factors).
+ * More routes (N % 128 == 0, K % 64 == 0): the bank is re-packed once into
+ * the workspace as eq_gguf_linear's prefill does and the routes run as one
+ * gathered product (sorted_ids: ascending ids promised, the grouped
+ * matrix-core kernel; unsorted ids under the promise give wrong rows but
+ * stay in bounds).  The first call on a stream may allocate the workspace.
+ * Replaces native_grouped_linear (safemlx/src/native_quantization.rs:
+ * 1039-1072; its CPU loop :1002-1037) as eredu's MoE calls it
+ * (eredu/src/backend/mlx/nn/moe.rs:1080-1092).  x 16-byte, y 8-byte aligned.
+ */
+int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type,
+                           int64_t experts, int64_t N, int64_t K, const int32_t* ids, int64_t routes, int endian,
+                           int x_dtype, bool sorted_ids, eq_stream_t stream);
+
+/*
  * Native GGUF linear: y[M, N] = x[M, K] . W^T with W the GGUF tensor (MLX
  * shape [N, K], raw Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL or IQ4_XS blocks as stored, raw_len
  * bytes) decoded by the native definition (Q4_K: d*sc*q - dmin*m, Q5_K the

@@ -28,7 +28,7 @@ def test_header_declares_the_boundary():
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
          "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
          "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc", "eq_gguf_convert_mxfp4",
-         "eq_gguf_embedding"]
+         "eq_gguf_embedding", "eq_gguf_grouped_linear"]
     )
 
 
@@ -163,6 +163,24 @@ def test_gguf_embedding_rejects():
     _rejects(L.eq_gguf_embedding(a + 8, a, 144, 12, 1, 256, a, 1, 0, f32, None), "aligned")
     _rejects(L.eq_gguf_embedding(a, a, 143, 12, 1, 256, a, 1, 0, f32, None), "")  # payload length
     assert L.eq_gguf_embedding(None, a, 144, 12, 1, 256, None, 0, 0, f32, None) == 0  # no tokens
+
+
+def test_gguf_grouped_linear_rejects():
+    buf = ctypes.create_string_buffer(8192)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a = (p.value + 15) // 16 * 16
+    bf16 = _native.EQ_DTYPE_BF16
+    # 2 experts x 8 rows x 256 Q8_0 values: 2 * 8 * 8 * 34 bytes
+    nraw = 2 * 8 * 8 * 34
+    _rejects(L.eq_gguf_grouped_linear(a, a, a, nraw, 2, 2, 8, 256, a, 1, 0, bf16, True, None), "covers Q4_K")
+    _rejects(L.eq_gguf_grouped_linear(a, a, a, nraw, 8, 0, 8, 256, a, 1, 0, bf16, True, None), "bank shape")
+    _rejects(L.eq_gguf_grouped_linear(a, a, a, nraw - 1, 8, 2, 8, 256, a, 1, 0, bf16, True, None), "")
+    _rejects(L.eq_gguf_grouped_linear(a, a, a, nraw, 8, 2, 8, 256, a, 1, 0, 1, True, None), "bf16 activations")
+    _rejects(L.eq_gguf_grouped_linear(a, a, a, nraw, 8, 2, 8, 256, a, -1, 0, bf16, True, None), "route count")
+    _rejects(L.eq_gguf_grouped_linear(a, a, a, nraw, 8, 2, 8, 256, None, 1, 0, bf16, True, None), "null")
+    _rejects(L.eq_gguf_grouped_linear(a, a + 2, a, nraw, 8, 2, 8, 256, a, 1, 0, bf16, True, None), "aligned")
+    _rejects(L.eq_gguf_grouped_linear(a, a, a, nraw, 8, 2, 8, 256, a, 17, 0, bf16, True, None), "N % 128")
+    assert L.eq_gguf_grouped_linear(None, None, a, nraw, 8, 2, 8, 256, None, 0, 0, bf16, True, None) == 0
 
 
 def test_host_mirror_fails_loudly_without_gpu_tensors():
