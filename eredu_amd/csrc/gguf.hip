@@ -22,6 +22,22 @@
 namespace eq {
 namespace {
 
+// An expert matrix picked on the device for the native linear kernels:
+// raw += ids[0] * stride.  An id outside [0, experts) reads expert 0 (every
+// access stays in the bank); the caller clears that output row afterwards.
+struct ExpertSel {
+    const int32_t* ids = nullptr;
+    int64_t stride = 0;
+    int experts = 0;
+};
+
+__device__ __forceinline__ const uint8_t* select_expert(const uint8_t* raw, const ExpertSel& sel) {
+    if (!sel.ids) return raw;
+    int e = sel.ids[0];
+    e = (e < 0 || e >= sel.experts) ? 0 : e;
+    return raw + int64_t(e) * sel.stride;
+}
+
 constexpr int kBlocksPerWG = 256;
 
 __device__ __forceinline__ uint32_t bswap16(uint32_t v) { return ((v & 0xffu) << 8) | ((v >> 8) & 0xffu); }
@@ -773,7 +789,9 @@ __device__ __forceinline__ void team_reduce(LinAcc<MANY>& acc, float* red, uint1
 // slower: fewer waves in flight.)
 template <bool BIG, int T, bool MANY>
 __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
-                                                  const uint8_t* __restrict__ raw, int M, int N, int K) {
+                                                  const uint8_t* __restrict__ raw, int M, int N, int K,
+                                                  ExpertSel sel) {
+    raw = select_expert(raw, sel);
     constexpr int S = 256 / T;
     __shared__ float red[4 * kLinRows * kTeamRows];
     __shared__ float lacc[MANY ? kLinRows * kTeamRows * 256 : 1];
@@ -882,7 +900,8 @@ constexpr int kKqStageVec = 8;  // 16-byte pieces per lane of one staged row gro
 template <int T, bool BIG, bool MANY, int W>
 __global__ __launch_bounds__(64 * W) void kq_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
                                                     const uint8_t* __restrict__ raw, int M, int N, int K, int R,
-                                                    bool vec_ok) {
+                                                    bool vec_ok, ExpertSel sel) {
+    raw = select_expert(raw, sel);
     using P = KQuant<T>;
     constexpr int G = 32 / P::gs, VG = 32 / G, NT = 64 * W;  // groups per unit, values per group
     extern __shared__ __attribute__((aligned(16))) uint16_t kq_lds[];
@@ -1058,6 +1077,7 @@ struct Q4kMfmaArgs {
     uint16_t* y;
     const uint16_t* x;
     const uint8_t* raw;
+    ExpertSel sel;  // raw + the picked expert's offset (none by default)
     int M, N, K;  // M <= kQ4kMaxRows; y [M, ldy] (columns [0, N)), x [M, K]
     int ldy;
     int sbw;      // superblocks per wave
@@ -1106,7 +1126,7 @@ __global__ __launch_bounds__(64 * W) void q4k_mfma_linear(const Q4kMfmaArgs args
 
     // Weight loads: rows past N read zero (offsets out of range, fixed step 0).
     const bool row_live = n0 + ln < N;
-    const __amdgpu_buffer_rsrc_t wr = raw_rsrc(args.raw, uint32_t(N) * row_bytes);
+    const __amdgpu_buffer_rsrc_t wr = raw_rsrc(select_expert(args.raw, args.sel), uint32_t(N) * row_bytes);
     const uint32_t hoff = row_live ? uint32_t(n0 + ln) * row_bytes : kOutOfRange;
     const uint32_t hstep = row_live ? 144u : 0u;
     auto load_sb = [&](Q4kSb& b, int j) __attribute__((always_inline)) {
@@ -1268,7 +1288,9 @@ __global__ __launch_bounds__(64 * W) void q4k_mfma_linear(const Q4kMfmaArgs args
 // 16-byte aligned, else 2-byte loads), then each lane takes whole blocks.
 template <bool BIG>
 __global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
-                                                   const uint8_t* __restrict__ raw, int M, int N, int K) {
+                                                   const uint8_t* __restrict__ raw, int M, int N, int K,
+                                                   ExpertSel sel) {
+    raw = select_expert(raw, sel);
     constexpr int kRun = 256;
     __shared__ uint16_t lds[4][kRun * 17];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1626,14 +1648,15 @@ int lds_limit() {
 // in chunks of < 2^31 payload bytes (32-bit buffer offsets).  False, launching
 // nothing, when even one activation row does not fit in LDS.
 bool launch_q4k_mfma(uint16_t* y, const uint16_t* x, const uint8_t* raw, int64_t M, int64_t N, int64_t K, bool big,
-                     hipStream_t st) {
+                     hipStream_t st, ExpertSel sel = ExpertSel{}) {
     Q4kMfmaArgs a{};
+    a.sel = sel;
     int mcap = kQ4kMaxRows;
     while (mcap > 0 && q4k_mfma_layout(K, mcap, a) > lds_limit()) mcap--;
     if (mcap == 0) return false;
     const int64_t nsb = K / 256, row_bytes = nsb * 144;
     int64_t rows_cap = ((int64_t(1) << 31) - 1) / row_bytes / 16 * 16;
-    if (rows_cap < 16) return false;
+    if (rows_cap < 16 || (sel.ids && rows_cap < N)) return false;
     for (int64_t m0 = 0; m0 < M; m0 += mcap) {
         const int mc = int(M - m0 < mcap ? M - m0 : mcap);
         const int lds = int(q4k_mfma_layout(K, mc, a));
@@ -1835,6 +1858,103 @@ extern "C" int eq_gguf_embedding(void* out, const uint8_t* raw, int64_t raw_len,
     return check_launch("gguf embedding");
 }
 
+namespace eq {
+namespace {
+
+// The native linear's launches after argument checks: `sel` picks the
+// matrix of an expert bank on the device (none: raw is the matrix).
+int native_linear_run(void* y, const void* x, const uint8_t* raw, int ggml_type, const Geometry& geo, bool kq,
+                      int64_t M, int64_t N, int64_t K, bool big, ExpertSel sel, hipStream_t st) {
+    if (M > kLinRows && !sel.ids && launch_native_prefill(ggml_type, big, geo, static_cast<uint16_t*>(y),
+                                        static_cast<const uint16_t*>(x), raw, M, N, K, st))
+        return check_launch("gguf linear (prefill)");
+    if (kq) {
+        // R weight rows per workgroup, staged whole in LDS: 8 while they fit
+        // in 64 KB, fewer for long rows, one row up to the device's LDS
+        // R weight rows per group: as many as fit the register stage (up to
+        // 8, kKqStageVec 16-byte pieces per lane), then sums of x for up to
+        // kLinRows activation rows behind them in LDS.  A row longer than the
+        // stage takes groups of one row staged with 2-byte loads.
+        constexpr int W = 4;
+        const int64_t row_bytes = K / geo.values * geo.bytes;
+        const int64_t stage = int64_t(kKqStageVec) * 16 * 64 * W;
+        int R = 8;
+        while (R > 1 && R * row_bytes > stage) R /= 2;
+        const int64_t rows_lds = (R * row_bytes + 15) / 16 * 16;
+        const int64_t sx_row = (K / geo.gs) * 4;  // sums of x of one activation row
+        if (rows_lds + sx_row > lds_limit()) {
+            set_error("native linear: one weight row (" + std::to_string(row_bytes) + " bytes) exceeds LDS");
+            return 1;
+        }
+        int mcap = kLinRows;  // activation rows per launch: as many as LDS holds, up to kLinRows
+        while (rows_lds + mcap * sx_row > lds_limit()) mcap--;
+        const bool vec_ok = aligned(raw, 16) && sel.stride % 16 == 0 && (R * row_bytes) % 16 == 0 &&
+                            R * row_bytes <= stage;
+        const int64_t groups = (N + R - 1) / R;
+        const int64_t cap = int64_t(device_cu_count()) * 4;  // 2, 8, 32 per CU measured slower
+        const unsigned grid = unsigned(groups < cap ? groups : cap);
+        if (!with_kq(ggml_type, big, [&](auto t, auto b) {
+                constexpr int T = decltype(t)::value;
+                if constexpr (T == EQ_GGML_Q5_1 || T == EQ_GGML_Q5_K || T == EQ_GGML_Q6_K || T == EQ_GGML_IQ4_NL ||
+                              T == EQ_GGML_IQ4_XS) {
+                    constexpr bool B = decltype(b)::value;
+                    for (int64_t m0 = 0; m0 < M; m0 += mcap) {
+                        const int mc = int(M - m0 < mcap ? M - m0 : mcap);
+                        const int lds = int(rows_lds + mc * sx_row);
+                        auto go = [&](auto kernel) {
+                            if (lds > 65536)
+                                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+                            kernel<<<grid, 64 * W, size_t(lds), st>>>(static_cast<uint16_t*>(y) + m0 * N,
+                                                                  static_cast<const uint16_t*>(x) + m0 * K, raw, mc,
+                                                                  int(N), int(K), R, vec_ok, sel);
+                        };
+                        if (mc == 1)
+                            go(kq_linear<T, B, false, W>);
+                        else
+                            go(kq_linear<T, B, true, W>);
+                    }
+                }
+            }))
+            return 1;
+        return check_launch("gguf linear");
+    }
+    if (ggml_type == EQ_GGML_Q4_K &&
+        launch_q4k_mfma(static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), raw, M, N, K, big, st, sel))
+        return check_launch("gguf linear");
+    // Q4_K: 32-code chunks per row -> teams per workgroup; Q8_0: a wave per row
+    const int64_t nch = K / 32;
+    const int teams = nch <= 64 ? 4 : nch <= 128 ? 2 : 1;
+    const int64_t rows_per_wg = ggml_type == EQ_GGML_Q4_K ? int64_t(teams) * kTeamRows : 4;
+    const int64_t wgs = (N + rows_per_wg - 1) / rows_per_wg;
+    const unsigned grid = unsigned(wgs < 8192 ? wgs : 8192);
+    for (int64_t m0 = 0; m0 < M; m0 += kLinRows) {
+        const int mc = int(M - m0 < kLinRows ? M - m0 : kLinRows);
+        uint16_t* yy = static_cast<uint16_t*>(y) + m0 * N;
+        const uint16_t* xx = static_cast<const uint16_t*>(x) + m0 * K;
+        const int n = int(N), k = int(K);
+#define EQ_LIN_MANY(KERNEL, T, MANY)                                                        \
+    (big ? KERNEL<true, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel)          \
+         : KERNEL<false, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel))
+#define EQ_LIN_T(KERNEL, T) (mc == 1 ? EQ_LIN_MANY(KERNEL, T, false) : EQ_LIN_MANY(KERNEL, T, true))
+#define EQ_LIN(KERNEL) \
+    (teams == 4 ? EQ_LIN_T(KERNEL, 4) : teams == 2 ? EQ_LIN_T(KERNEL, 2) : EQ_LIN_T(KERNEL, 1))
+        if (ggml_type == EQ_GGML_Q4_K) {
+            EQ_LIN(q4k_linear);
+        } else {
+            if (big) q8_0_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel);
+            else q8_0_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel);
+        }
+#undef EQ_LIN_MANY
+#undef EQ_LIN_T
+#undef EQ_LIN
+    }
+    return check_launch("gguf linear");
+}
+
+}  // namespace
+}  // namespace eq
+
 extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type, int64_t M,
                               int64_t N, int64_t K, int endian, int x_dtype, eq_stream_t stream) {
     clear_error();
@@ -1866,121 +1986,17 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool big = endian == EQ_ENDIAN_BIG;
-    if (M > kLinRows && launch_native_prefill(ggml_type, big, geo, static_cast<uint16_t*>(y),
-                                        static_cast<const uint16_t*>(x), raw, M, N, K, st))
-        return check_launch("gguf linear (prefill)");
-    if (kq) {
-        // R weight rows per workgroup, staged whole in LDS: 8 while they fit
-        // in 64 KB, fewer for long rows, one row up to the device's LDS
-        // R weight rows per group: as many as fit the register stage (up to
-        // 8, kKqStageVec 16-byte pieces per lane), then sums of x for up to
-        // kLinRows activation rows behind them in LDS.  A row longer than the
-        // stage takes groups of one row staged with 2-byte loads.
-        constexpr int W = 4;
-        const int64_t row_bytes = K / geo.values * geo.bytes;
-        const int64_t stage = int64_t(kKqStageVec) * 16 * 64 * W;
-        int R = 8;
-        while (R > 1 && R * row_bytes > stage) R /= 2;
-        const int64_t rows_lds = (R * row_bytes + 15) / 16 * 16;
-        const int64_t sx_row = (K / geo.gs) * 4;  // sums of x of one activation row
-        if (rows_lds + sx_row > lds_limit()) {
-            set_error("native linear: one weight row (" + std::to_string(row_bytes) + " bytes) exceeds LDS");
-            return 1;
-        }
-        int mcap = kLinRows;  // activation rows per launch: as many as LDS holds, up to kLinRows
-        while (rows_lds + mcap * sx_row > lds_limit()) mcap--;
-        const bool vec_ok = aligned(raw, 16) && (R * row_bytes) % 16 == 0 && R * row_bytes <= stage;
-        const int64_t groups = (N + R - 1) / R;
-        const int64_t cap = int64_t(device_cu_count()) * 4;  // 2, 8, 32 per CU measured slower
-        const unsigned grid = unsigned(groups < cap ? groups : cap);
-        if (!with_kq(ggml_type, big, [&](auto t, auto b) {
-                constexpr int T = decltype(t)::value;
-                if constexpr (T == EQ_GGML_Q5_1 || T == EQ_GGML_Q5_K || T == EQ_GGML_Q6_K || T == EQ_GGML_IQ4_NL ||
-                              T == EQ_GGML_IQ4_XS) {
-                    constexpr bool B = decltype(b)::value;
-                    for (int64_t m0 = 0; m0 < M; m0 += mcap) {
-                        const int mc = int(M - m0 < mcap ? M - m0 : mcap);
-                        const int lds = int(rows_lds + mc * sx_row);
-                        auto go = [&](auto kernel) {
-                            if (lds > 65536)
-                                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-                            kernel<<<grid, 64 * W, size_t(lds), st>>>(static_cast<uint16_t*>(y) + m0 * N,
-                                                                  static_cast<const uint16_t*>(x) + m0 * K, raw, mc,
-                                                                  int(N), int(K), R, vec_ok);
-                        };
-                        if (mc == 1)
-                            go(kq_linear<T, B, false, W>);
-                        else
-                            go(kq_linear<T, B, true, W>);
-                    }
-                }
-            }))
-            return 1;
-        return check_launch("gguf linear");
-    }
-    if (ggml_type == EQ_GGML_Q4_K &&
-        launch_q4k_mfma(static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), raw, M, N, K, big, st))
-        return check_launch("gguf linear");
-    // Q4_K: 32-code chunks per row -> teams per workgroup; Q8_0: a wave per row
-    const int64_t nch = K / 32;
-    const int teams = nch <= 64 ? 4 : nch <= 128 ? 2 : 1;
-    const int64_t rows_per_wg = ggml_type == EQ_GGML_Q4_K ? int64_t(teams) * kTeamRows : 4;
-    const int64_t wgs = (N + rows_per_wg - 1) / rows_per_wg;
-    const unsigned grid = unsigned(wgs < 8192 ? wgs : 8192);
-    for (int64_t m0 = 0; m0 < M; m0 += kLinRows) {
-        const int mc = int(M - m0 < kLinRows ? M - m0 : kLinRows);
-        uint16_t* yy = static_cast<uint16_t*>(y) + m0 * N;
-        const uint16_t* xx = static_cast<const uint16_t*>(x) + m0 * K;
-        const int n = int(N), k = int(K);
-#define EQ_LIN_MANY(KERNEL, T, MANY)                                                        \
-    (big ? KERNEL<true, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k)               \
-         : KERNEL<false, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k))
-#define EQ_LIN_T(KERNEL, T) (mc == 1 ? EQ_LIN_MANY(KERNEL, T, false) : EQ_LIN_MANY(KERNEL, T, true))
-#define EQ_LIN(KERNEL) \
-    (teams == 4 ? EQ_LIN_T(KERNEL, 4) : teams == 2 ? EQ_LIN_T(KERNEL, 2) : EQ_LIN_T(KERNEL, 1))
-        if (ggml_type == EQ_GGML_Q4_K) {
-            EQ_LIN(q4k_linear);
-        } else {
-            if (big) q8_0_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k);
-            else q8_0_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k);
-        }
-#undef EQ_LIN_MANY
-#undef EQ_LIN_T
-#undef EQ_LIN
-    }
-    return check_launch("gguf linear");
+    return native_linear_run(y, x, raw, ggml_type, geo, kq, M, N, K, big, ExpertSel{}, st);
 }
 
 namespace eq {
 namespace {
 
-// Routes at or below this count take one native linear launch per route on a
-// copy of the route's expert matrix; above it the bank is re-packed once and
-// the routes run as one gathered (grouped when sorted) matrix product.
+// Routes at or below this count take one native linear launch per route,
+// the route's expert picked on the device; above it the bank is re-packed
+// once and the routes run as one gathered (grouped when sorted) matrix
+// product.
 constexpr int64_t kGroupedCopyRoutes = 16;
-
-// Matrix ids[r] of an expert bank (matrix_bytes each) copied to
-// dst + r * matrix_bytes; grid (chunks, routes).  An id outside
-// [0, experts) copies nothing (its output row is cleared afterwards).
-__global__ __launch_bounds__(256) void expert_gather_matrices(uint8_t* __restrict__ dst,
-                                                              const uint8_t* __restrict__ raw,
-                                                              const int32_t* __restrict__ ids, int64_t experts,
-                                                              int64_t matrix_bytes, bool vec) {
-    const int64_t r = blockIdx.y;
-    const int32_t e = ids[r];
-    if (e < 0 || e >= experts) return;
-    const uint8_t* src = raw + int64_t(e) * matrix_bytes;
-    uint8_t* d = dst + r * matrix_bytes;
-    const int64_t step = int64_t(gridDim.x) * blockDim.x;
-    if (vec) {
-        const int64_t n16 = matrix_bytes / 16;
-        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += step)
-            reinterpret_cast<uint4*>(d)[i] = reinterpret_cast<const uint4*>(src)[i];
-    } else {
-        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < matrix_bytes; i += step) d[i] = src[i];
-    }
-}
 
 }  // namespace
 }  // namespace eq
@@ -2017,8 +2033,8 @@ extern "C" int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw
         set_error("null pointer argument");
         return 1;
     }
-    if (!aligned(x, 16) || !aligned(y, 8)) {
-        set_error("x must be 16-byte and y 8-byte aligned");
+    if (!aligned(x, 16) || !aligned(y, 8) || (ggml_type == EQ_GGML_Q4_K && !aligned(raw, 16))) {
+        set_error("x (and a Q4_K payload) must be 16-byte and y 8-byte aligned");
         return 1;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -2027,20 +2043,11 @@ extern "C" int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw
     uint16_t* yy = static_cast<uint16_t*>(y);
     const uint16_t* xx = static_cast<const uint16_t*>(x);
     if (routes <= kGroupedCopyRoutes) {
-        // decode: each route's matrix copied out, then the native linear at M = 1 on it
-        uint8_t* mats = static_cast<uint8_t*>(ws_acquire(nullptr, size_t(routes) * size_t(matrix_bytes), st));
-        if (!mats) {
-            set_error("could not obtain workspace for the routes' expert matrices");
-            return 1;
-        }
-        const int64_t n16 = matrix_bytes / 16;
-        const unsigned chunks = unsigned(n16 / 256 + 1 < 1024 ? n16 / 256 + 1 : 1024);
-        expert_gather_matrices<<<dim3(chunks, unsigned(routes)), 256, 0, st>>>(
-            mats, raw, ids, experts, matrix_bytes, aligned(raw, 16) && matrix_bytes % 16 == 0);
-        if (check_launch("gguf grouped linear (gather)")) return 1;
+        // decode: the native linear at M = 1 per route, its expert picked on the device
         for (int64_t r = 0; r < routes; r++) {
-            if (eq_gguf_linear(yy + r * N, xx + r * K, mats + r * matrix_bytes, matrix_bytes, ggml_type, 1, N, K,
-                               endian, x_dtype, stream))
+            if (native_linear_run(yy + r * N, xx + r * K, raw, ggml_type, geo, ggml_type != EQ_GGML_Q4_K &&
+                                  ggml_type != EQ_GGML_Q8_0, 1, N, K, big,
+                                  ExpertSel{ids + r, matrix_bytes, int(experts)}, st))
                 return 1;
         }
     } else {

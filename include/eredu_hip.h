@@ -184,17 +184,18 @@ int eq_gguf_embedding(void* out, const uint8_t* raw, int64_t raw_len, int ggml_t
  * for r < routes, with W an expert bank [experts, N, K] of Q4_K, Q5_K, Q6_K,
  * Q5_1, Q8_0, IQ4_NL or IQ4_XS blocks as stored (raw_len bytes, experts * N
  * rows of K values); x [routes, K] and y [routes, N] bf16; ids device int32,
- * an id outside [0, experts) gives a row of +0.  Up to 16 routes: each
- * route's expert matrix is copied into the library's per-stream workspace
- * and run through eq_gguf_linear at M = 1 (native definition, f32 factors).
+ * an id outside [0, experts) gives a row of +0.  Up to 16 routes: one
+ * launch of eq_gguf_linear's M = 1 kernels per route, the route's expert
+ * matrix picked on the device from ids (native definition, f32 factors).
  * More routes (N % 128 == 0, K % 64 == 0): the bank is re-packed once into
  * the workspace as eq_gguf_linear's prefill does and the routes run as one
  * gathered product (sorted_ids: ascending ids promised, the grouped
  * matrix-core kernel; unsorted ids under the promise give wrong rows but
- * stay in bounds).  The first call on a stream may allocate the workspace.
- * Replaces native_grouped_linear (safemlx/src/native_quantization.rs:
+ * stay in bounds; the first such call on a stream may allocate the
+ * workspace).  Replaces native_grouped_linear (safemlx/src/native_quantization.rs:
  * 1039-1072; its CPU loop :1002-1037) as eredu's MoE calls it
- * (eredu/src/backend/mlx/nn/moe.rs:1080-1092).  x 16-byte, y 8-byte aligned.
+ * (eredu/src/backend/mlx/nn/moe.rs:1080-1092).  x 16-byte, y 8-byte aligned, a
+ * Q4_K bank 16-byte aligned.
  */
 int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw, int64_t raw_len, int ggml_type,
                            int64_t experts, int64_t N, int64_t K, const int32_t* ids, int64_t routes, int endian,
