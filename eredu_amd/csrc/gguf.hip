@@ -22,21 +22,27 @@
 namespace eq {
 namespace {
 
-// An expert matrix picked on the device for the native linear kernels:
-// raw += ids[0] * stride.  An id outside [0, experts) reads expert 0 (every
-// access stays in the bank); the caller clears that output row afterwards.
+// Routes of a mixture-of-experts call in one launch of the native linear
+// kernels: route r = blockIdx.y reads x row r, writes y row r, and takes the
+// expert matrix raw + ids[r] * stride.  An id outside [0, experts) reads
+// expert 0 (every access stays in the bank); the caller clears that output
+// row afterwards.  ids null: one matrix, one route (grid.y = 1).
 struct ExpertSel {
     const int32_t* ids = nullptr;
     int64_t stride = 0;
     int experts = 0;
+    int routes = 1;
 };
 
 __device__ __forceinline__ const uint8_t* select_expert(const uint8_t* raw, const ExpertSel& sel) {
     if (!sel.ids) return raw;
-    int e = sel.ids[0];
+    int e = sel.ids[blockIdx.y];
     e = (e < 0 || e >= sel.experts) ? 0 : e;
     return raw + int64_t(e) * sel.stride;
 }
+
+// Row offset of this block's route (0 without ids).
+__device__ __forceinline__ int64_t route_row(const ExpertSel& sel) { return sel.ids ? int64_t(blockIdx.y) : 0; }
 
 constexpr int kBlocksPerWG = 256;
 
@@ -792,6 +798,8 @@ __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, cons
                                                   const uint8_t* __restrict__ raw, int M, int N, int K,
                                                   ExpertSel sel) {
     raw = select_expert(raw, sel);
+    x += route_row(sel) * K;
+    y += route_row(sel) * N;
     constexpr int S = 256 / T;
     __shared__ float red[4 * kLinRows * kTeamRows];
     __shared__ float lacc[MANY ? kLinRows * kTeamRows * 256 : 1];
@@ -902,6 +910,8 @@ __global__ __launch_bounds__(64 * W) void kq_linear(uint16_t* __restrict__ y, co
                                                     const uint8_t* __restrict__ raw, int M, int N, int K, int R,
                                                     bool vec_ok, ExpertSel sel) {
     raw = select_expert(raw, sel);
+    x += route_row(sel) * K;
+    y += route_row(sel) * N;
     using P = KQuant<T>;
     constexpr int G = 32 / P::gs, VG = 32 / G, NT = 64 * W;  // groups per unit, values per group
     extern __shared__ __attribute__((aligned(16))) uint16_t kq_lds[];
@@ -1143,7 +1153,7 @@ __global__ __launch_bounds__(64 * W) void q4k_mfma_linear(const Q4kMfmaArgs args
     // before the first D - 1 superblocks of the ring, the stores after them:
     // loads complete in order, so the stores wait for the activations only.
     constexpr int NCH = 4;
-    const __amdgpu_buffer_rsrc_t xr = raw_rsrc(args.x, uint32_t(M) * uint32_t(K) * 2u);
+    const __amdgpu_buffer_rsrc_t xr = raw_rsrc(args.x + route_row(args.sel) * K, uint32_t(M) * uint32_t(K) * 2u);
     const int cpr = K / 8, total = M * cpr;
     auto stage_load = [&](int c0, q4k_u32x4* v) __attribute__((always_inline)) {
 #pragma unroll
@@ -1279,7 +1289,7 @@ __global__ __launch_bounds__(64 * W) void q4k_mfma_linear(const Q4kMfmaArgs args
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < W; w++) v += red[(w * kQ4kMaxRows + m) * 16 + n];
-        if (n0 + n < N) args.y[int64_t(m) * args.ldy + n0 + n] = uint16_t(f32_to_bf16_bits(v));
+        if (n0 + n < N) args.y[(route_row(args.sel) + m) * args.ldy + n0 + n] = uint16_t(f32_to_bf16_bits(v));
     }
 }
 
@@ -1291,6 +1301,8 @@ __global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, con
                                                    const uint8_t* __restrict__ raw, int M, int N, int K,
                                                    ExpertSel sel) {
     raw = select_expert(raw, sel);
+    x += route_row(sel) * K;
+    y += route_row(sel) * N;
     constexpr int kRun = 256;
     __shared__ uint16_t lds[4][kRun * 17];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1674,7 +1686,7 @@ bool launch_q4k_mfma(uint16_t* y, const uint16_t* x, const uint8_t* raw, int64_t
                 if (lds > 65536)
                     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-                kernel<<<dim3(unsigned((nc + 15) / 16)), dim3(64 * W), size_t(lds), st>>>(a);
+                kernel<<<dim3(unsigned((nc + 15) / 16), unsigned(sel.routes)), dim3(64 * W), size_t(lds), st>>>(a);
             };
             auto pick = [&](auto big_tag) {
                 constexpr bool B = decltype(big_tag)::value;
@@ -1905,7 +1917,8 @@ int native_linear_run(void* y, const void* x, const uint8_t* raw, int ggml_type,
                             if (lds > 65536)
                                 (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-                            kernel<<<grid, 64 * W, size_t(lds), st>>>(static_cast<uint16_t*>(y) + m0 * N,
+                            kernel<<<dim3(grid, unsigned(sel.routes)), 64 * W, size_t(lds), st>>>(
+                                static_cast<uint16_t*>(y) + m0 * N,
                                                                   static_cast<const uint16_t*>(x) + m0 * K, raw, mc,
                                                                   int(N), int(K), R, vec_ok, sel);
                         };
@@ -1934,16 +1947,16 @@ int native_linear_run(void* y, const void* x, const uint8_t* raw, int ggml_type,
         const uint16_t* xx = static_cast<const uint16_t*>(x) + m0 * K;
         const int n = int(N), k = int(K);
 #define EQ_LIN_MANY(KERNEL, T, MANY)                                                        \
-    (big ? KERNEL<true, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel)          \
-         : KERNEL<false, T, MANY><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel))
+    (big ? KERNEL<true, T, MANY><<<dim3(grid, unsigned(sel.routes)), 256, 0, st>>>(yy, xx, raw, mc, n, k, sel) \
+         : KERNEL<false, T, MANY><<<dim3(grid, unsigned(sel.routes)), 256, 0, st>>>(yy, xx, raw, mc, n, k, sel))
 #define EQ_LIN_T(KERNEL, T) (mc == 1 ? EQ_LIN_MANY(KERNEL, T, false) : EQ_LIN_MANY(KERNEL, T, true))
 #define EQ_LIN(KERNEL) \
     (teams == 4 ? EQ_LIN_T(KERNEL, 4) : teams == 2 ? EQ_LIN_T(KERNEL, 2) : EQ_LIN_T(KERNEL, 1))
         if (ggml_type == EQ_GGML_Q4_K) {
             EQ_LIN(q4k_linear);
         } else {
-            if (big) q8_0_linear<true><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel);
-            else q8_0_linear<false><<<grid, 256, 0, st>>>(yy, xx, raw, mc, n, k, sel);
+            if (big) q8_0_linear<true><<<dim3(grid, unsigned(sel.routes)), 256, 0, st>>>(yy, xx, raw, mc, n, k, sel);
+            else q8_0_linear<false><<<dim3(grid, unsigned(sel.routes)), 256, 0, st>>>(yy, xx, raw, mc, n, k, sel);
         }
 #undef EQ_LIN_MANY
 #undef EQ_LIN_T
@@ -1992,8 +2005,9 @@ extern "C" int eq_gguf_linear(void* y, const void* x, const uint8_t* raw, int64_
 namespace eq {
 namespace {
 
-// Routes at or below this count take one native linear launch per route,
-// the route's expert picked on the device; above it the bank is re-packed
+// Routes at or below this count take one launch of the native linear
+// kernels (a grid row per route, the route's expert picked on the device);
+// above it the bank is re-packed
 // once and the routes run as one gathered (grouped when sorted) matrix
 // product.
 constexpr int64_t kGroupedCopyRoutes = 16;
@@ -2043,13 +2057,11 @@ extern "C" int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw
     uint16_t* yy = static_cast<uint16_t*>(y);
     const uint16_t* xx = static_cast<const uint16_t*>(x);
     if (routes <= kGroupedCopyRoutes) {
-        // decode: the native linear at M = 1 per route, its expert picked on the device
-        for (int64_t r = 0; r < routes; r++) {
-            if (native_linear_run(yy + r * N, xx + r * K, raw, ggml_type, geo, ggml_type != EQ_GGML_Q4_K &&
-                                  ggml_type != EQ_GGML_Q8_0, 1, N, K, big,
-                                  ExpertSel{ids + r, matrix_bytes, int(experts)}, st))
-                return 1;
-        }
+        // decode: one launch of the native M = 1 kernels, route r = grid row r,
+        // its expert picked on the device
+        if (native_linear_run(yy, xx, raw, ggml_type, geo, ggml_type != EQ_GGML_Q4_K && ggml_type != EQ_GGML_Q8_0, 1,
+                              N, K, big, ExpertSel{ids, matrix_bytes, int(experts), int(routes)}, st))
+            return 1;
     } else {
         // prefill: the bank re-packed once (as the native prefill does), then the gathered product
         if (N % 128 != 0 || K % 64 != 0) {

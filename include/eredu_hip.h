@@ -185,8 +185,9 @@ int eq_gguf_embedding(void* out, const uint8_t* raw, int64_t raw_len, int ggml_t
  * Q5_1, Q8_0, IQ4_NL or IQ4_XS blocks as stored (raw_len bytes, experts * N
  * rows of K values); x [routes, K] and y [routes, N] bf16; ids device int32,
  * an id outside [0, experts) gives a row of +0.  Up to 16 routes: one
- * launch of eq_gguf_linear's M = 1 kernels per route, the route's expert
- * matrix picked on the device from ids (native definition, f32 factors).
+ * launch of eq_gguf_linear's M = 1 kernels for all routes, each route's
+ * expert matrix picked on the device from ids (native definition, f32
+ * factors).
  * More routes (N % 128 == 0, K % 64 == 0): the bank is re-packed once into
  * the workspace as eq_gguf_linear's prefill does and the routes run as one
  * gathered product (sorted_ids: ascending ids promised, the grouped
