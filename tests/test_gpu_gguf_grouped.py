@@ -60,7 +60,7 @@ def test_decode_routes(cuda, ty):
     run(ty, 4, 256, 1024, [1], seed=int(ty) + 7)
 
 
-@pytest.mark.parametrize("ty", [T.Q4K, T.Q5K, T.Q6K, T.Q5_1, T.Q8_0, T.IQ4NL])
+@pytest.mark.parametrize("ty", [T.Q4K, T.Q5K, T.Q6K, T.Q5_1, T.Q8_0, T.IQ4NL, T.IQ4XS])
 def test_prefill_routes_sorted_and_unsorted(cuda, ty):
     rng = np.random.default_rng(int(ty))
     ids = np.sort(rng.integers(0, 4, 96)).tolist()  # sorted: the grouped matrix-core product
