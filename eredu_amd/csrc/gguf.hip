@@ -25,8 +25,7 @@ namespace {
 // Routes of a mixture-of-experts call in one launch of the native linear
 // kernels: route r = blockIdx.y reads x row r, writes y row r, and takes the
 // expert matrix raw + ids[r] * stride.  An id outside [0, experts) reads
-// expert 0 (every access stays in the bank); the caller clears that output
-// row afterwards.  ids null: one matrix, one route (grid.y = 1).
+// expert 0 (every access stays in the bank) and its row is written as +0.  ids null: one matrix, one route (grid.y = 1).
 struct ExpertSel {
     const int32_t* ids = nullptr;
     int64_t stride = 0;
@@ -43,6 +42,13 @@ __device__ __forceinline__ const uint8_t* select_expert(const uint8_t* raw, cons
 
 // Row offset of this block's route (0 without ids).
 __device__ __forceinline__ int64_t route_row(const ExpertSel& sel) { return sel.ids ? int64_t(blockIdx.y) : 0; }
+
+// False for a route whose id is outside the bank: its row is written as +0.
+__device__ __forceinline__ bool route_ok(const ExpertSel& sel) {
+    if (!sel.ids) return true;
+    const int e = sel.ids[blockIdx.y];
+    return e >= 0 && e < sel.experts;
+}
 
 constexpr int kBlocksPerWG = 256;
 
@@ -761,7 +767,7 @@ struct LinAcc<true> {
 // reused.
 template <int T, bool MANY>
 __device__ __forceinline__ void team_reduce(LinAcc<MANY>& acc, float* red, uint16_t* __restrict__ y, int M, int N,
-                                            int row0) {
+                                            int row0, bool keep) {
     constexpr int S = 256 / T, WPT = S / 64;  // waves per team
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 #pragma unroll 1
@@ -780,7 +786,7 @@ __device__ __forceinline__ void team_reduce(LinAcc<MANY>& acc, float* red, uint1
 #pragma unroll
         for (int w = 0; w < WPT; w++) v += red[(team * WPT + w) * kLinRows * kTeamRows + m * kTeamRows + r];
         const int n = row0 + team * kTeamRows + r;
-        if (n < N) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(v));
+        if (n < N) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(keep ? v : 0.f));
     }
     __syncthreads();
 }
@@ -800,6 +806,7 @@ __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, cons
     raw = select_expert(raw, sel);
     x += route_row(sel) * K;
     y += route_row(sel) * N;
+    const bool keep = route_ok(sel);
     constexpr int S = 256 / T;
     __shared__ float red[4 * kLinRows * kTeamRows];
     __shared__ float lacc[MANY ? kLinRows * kTeamRows * 256 : 1];
@@ -880,7 +887,7 @@ __global__ __launch_bounds__(256) void q4k_linear(uint16_t* __restrict__ y, cons
                 }
             }
         }
-        team_reduce<T, MANY>(acc, red, y, M, N, row0);
+        team_reduce<T, MANY>(acc, red, y, M, N, row0, route_ok(sel));
     }
 }
 
@@ -912,6 +919,7 @@ __global__ __launch_bounds__(64 * W) void kq_linear(uint16_t* __restrict__ y, co
     raw = select_expert(raw, sel);
     x += route_row(sel) * K;
     y += route_row(sel) * N;
+    const bool keep = route_ok(sel);
     using P = KQuant<T>;
     constexpr int G = 32 / P::gs, VG = 32 / G, NT = 64 * W;  // groups per unit, values per group
     extern __shared__ __attribute__((aligned(16))) uint16_t kq_lds[];
@@ -1023,7 +1031,7 @@ __global__ __launch_bounds__(64 * W) void kq_linear(uint16_t* __restrict__ y, co
                 if (m >= M) break;
                 const float v = wave_sum(acc[m]);
                 if (wpr == 1) {
-                    if (lane == 0 && r < nr) y[int64_t(m) * N + n0 + r] = uint16_t(f32_to_bf16_bits(v));
+                    if (lane == 0 && r < nr) y[int64_t(m) * N + n0 + r] = uint16_t(f32_to_bf16_bits(keep ? v : 0.f));
                 } else if (lane == 0) {
                     red[wave * kLinRows + m] = v;
                 }
@@ -1034,7 +1042,7 @@ __global__ __launch_bounds__(64 * W) void kq_linear(uint16_t* __restrict__ y, co
                 if (t < (W / wpr) * (MANY ? kLinRows : 1) && rr < nr && m < M) {
                     float v = 0.f;
                     for (int q = 0; q < wpr; q++) v += red[((rr - rb) * wpr + q) * kLinRows + m];
-                    y[int64_t(m) * N + n0 + rr] = uint16_t(f32_to_bf16_bits(v));
+                    y[int64_t(m) * N + n0 + rr] = uint16_t(f32_to_bf16_bits(keep ? v : 0.f));
                 }
                 __syncthreads();
             }
@@ -1289,7 +1297,8 @@ __global__ __launch_bounds__(64 * W) void q4k_mfma_linear(const Q4kMfmaArgs args
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < W; w++) v += red[(w * kQ4kMaxRows + m) * 16 + n];
-        if (n0 + n < N) args.y[(route_row(args.sel) + m) * args.ldy + n0 + n] = uint16_t(f32_to_bf16_bits(v));
+        if (n0 + n < N) args.y[(route_row(args.sel) + m) * args.ldy + n0 + n] =
+                uint16_t(f32_to_bf16_bits(route_ok(args.sel) ? v : 0.f));
     }
 }
 
@@ -1303,6 +1312,7 @@ __global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, con
     raw = select_expert(raw, sel);
     x += route_row(sel) * K;
     y += route_row(sel) * N;
+    const bool keep = route_ok(sel);
     constexpr int kRun = 256;
     __shared__ uint16_t lds[4][kRun * 17];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1364,7 +1374,7 @@ __global__ __launch_bounds__(256) void q8_0_linear(uint16_t* __restrict__ y, con
         for (int m = 0; m < kLinRows; m++) {
             if (m >= M) break;
             const float v = wave_sum(acc[m]);
-            if (lane == 0) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(v));
+            if (lane == 0) y[int64_t(m) * N + n] = uint16_t(f32_to_bf16_bits(keep ? v : 0.f));
         }
     }
 }
@@ -2101,8 +2111,8 @@ extern "C" int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw
         if (gather_qmm_launch(y, x, w, s, b, nullptr, ids, routes, routes, experts, 1, N, K, true, geo.gs, bits,
                               kModeAffine, EQ_DTYPE_BF16, EQ_DTYPE_F16, sorted_ids, &tail, st))
             return 1;
+        // the rows of ids outside the bank are +0 (the decode kernels write them so themselves)
+        embedding_clear_rows<uint16_t><<<dim3(unsigned(routes)), 256, 0, st>>>(yy, ids, experts, N);
     }
-    // the rows of ids outside the bank are +0
-    embedding_clear_rows<uint16_t><<<dim3(unsigned(routes)), 256, 0, st>>>(yy, ids, experts, N);
     return check_launch("gguf grouped linear");
 }
