@@ -2085,7 +2085,7 @@ extern "C" int eq_gguf_grouped_linear(void* y, const void* x, const uint8_t* raw
         const size_t wsz = up(size_t(experts * N) * size_t(K) * bits / 8);
         const size_t psz = up(size_t(experts * N) * size_t(K / geo.gs) * 2);
         const size_t triple = wsz + 2 * psz;
-        const int cap = int(experts + (routes + 127) / 128);
+        const int64_t cap = experts + (routes + 127) / 128;  // entries of the grouped tile list
         const size_t rest = up(size_t(routes) * size_t(K) * 2) + size_t(cap) * 16 + 256;
         char* base = static_cast<char*>(ws_acquire(nullptr, triple + rest, st));
         if (!base) {
