@@ -321,6 +321,40 @@ def bench_gguf(steps, warmup):
     return out
 
 
+def bench_gguf_embedding(steps, warmup):
+    """Native GGUF embedding (eq_gguf_embedding): rows of a 128256 x 4096
+    token table (Llama-3's vocabulary) in Q6_K and Q4_K blocks, f32 out, for
+    1 token (decode) and 512 tokens (prefill); tables rotate >= 300 MB.
+    GB/s over the picked rows' blocks read plus the f32 rows written."""
+    import torch
+
+    from eredu_amd.gguf import GgmlType as T
+
+    n = _lib()
+    out = {}
+    rows, cols = 128256, 4096
+    for ty in (T.Q6K, T.Q4K):
+        vals, nbytes = ty.block_and_bytes()
+        nraw = rows * cols // vals * nbytes
+        row_bytes = cols // vals * nbytes
+        tables = [torch.randint(0, 256, (nraw,), dtype=torch.uint8, device="cuda") for _ in range(rotation(nraw))]
+        for label, count in (("1_token", 1), ("512_tokens", 512)):
+            ids = torch.randint(0, rows, (count,), device="cuda", dtype=torch.int32)
+            y = torch.empty((count, cols), dtype=torch.float32, device="cuda")
+
+            def call(st):
+                for t in tables:
+                    n.check(n.lib().eq_gguf_embedding(y.data_ptr(), t.data_ptr(), nraw, int(ty), rows, cols,
+                                                      ids.data_ptr(), count, 0, n.EQ_DTYPE_F32, st))
+
+            ms = Timer(call).ms_per_replay(max(steps // 4, 5), warmup) / len(tables)
+            gbs = count * (row_bytes + cols * 4) / (ms * 1e-3) / 1e9
+            out[f"{ty.name} {label}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "copies": len(tables)}
+        del tables
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_gguf_grouped(steps, warmup):
     """Native GGUF mixture-of-experts linear (eq_gguf_grouped_linear): an
     expert bank of 8 x 14336 x 4096 (Mixtral's gate projection shape) in
@@ -857,6 +891,8 @@ def main():
             out["gguf"] = bench_gguf(args.steps, args.warmup)
             log("[bench] gguf mixture-of-experts linear")
             out["gguf_grouped"] = bench_gguf_grouped(args.steps, args.warmup)
+            log("[bench] gguf native embedding")
+            out["gguf_embedding"] = bench_gguf_embedding(args.steps, args.warmup)
             log("[bench] gguf streaming load")
             out["gguf_stream"] = bench_gguf_stream()
             log("[bench] affine dequantize / quantize")
@@ -918,6 +954,8 @@ def main():
         detail["gguf"] = bench_gguf(args.steps, args.warmup)
         log("[bench] gguf mixture-of-experts linear")
         detail["gguf_grouped"] = bench_gguf_grouped(args.steps, args.warmup)
+        log("[bench] gguf native embedding")
+        detail["gguf_embedding"] = bench_gguf_embedding(args.steps, args.warmup)
         log("[bench] gguf streaming load")
         detail["gguf_stream"] = bench_gguf_stream()
         log("[bench] affine dequantize / quantize")
