@@ -82,8 +82,9 @@ class Linear:
 
 
 class Timer:
-    """Replays a captured HIP graph on its own stream and times it with HIP
-    events recorded on that same stream."""
+    """Replays a captured HIP graph on its own stream and times each replay
+    with HIP events recorded on that same stream; a replay's time is the
+    median over the timed replays (the mean is kept in ``last_mean_ms``)."""
 
     def __init__(self, fn):
         import torch
@@ -105,13 +106,15 @@ class Timer:
             for _ in range(warmup):
                 self.graph.replay()
             torch.cuda.synchronize()
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record(self.stream)
-            for _ in range(steps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+            ev[0].record(self.stream)
+            for i in range(steps):
                 self.graph.replay()
-            end.record(self.stream)
+                ev[i + 1].record(self.stream)
         torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps
+        times = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+        self.last_mean_ms = ev[0].elapsed_time(ev[-1]) / steps
+        return float(np.median(times))
 
 
 def _lib():
@@ -830,6 +833,62 @@ def cpu_baseline(layer, budget_s=20.0):
     return res, threads
 
 
+def cpu_baseline_prefill(threads, budget_s=8.0, M=512, N=256, K=HIDDEN):
+    """The restated MLX CPU _qmm_t loop (or_qmm_t_f32, f32 accumulate) at the
+    prefill point M = 512 of the 4096 x 4096 projection, on a bounded sample:
+    N = 256 of its 4096 output features (the loop's cost is linear in N), 4-bit
+    group 64, single-threaded and on `threads` threads.  TFLOP/s = 2 M N K / s."""
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(1)
+    w = rng.integers(0, 2**32, (N, K * BITS // 32), dtype=np.uint32)
+    s = orc.f32_to_bf16_bits(rng.random((N, K // GS), dtype=np.float32) * 0.004 + 0.004)
+    b = orc.f32_to_bf16_bits(-7.5 * orc.bf16_bits_to_f32(s))
+    x = orc.f32_to_bf16_bits(rng.standard_normal((M, K), dtype=np.float32))
+    res = {}
+    for nthreads in sorted({1, threads}):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.qmm_t_f32(x, orc.BF16, w, s, b, orc.BF16, M, N, K, GS, BITS, threads=nthreads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > budget_s / 2 or reps >= 100:
+                break
+        res[nthreads] = {"TFLOP/s": round(2.0 * M * N * K * reps / el / 1e12, 6), "passes": reps,
+                         "seconds": round(el, 2)}
+    return {"unit": "TFLOP/s", "kind": "port", "threads": threads,
+            "value": res[threads]["TFLOP/s"], "single_thread_TFLOP/s": res[1]["TFLOP/s"],
+            "sample": f"M={M} x N={N} (of 4096) x K={K}, 4-bit group 64, bf16 x/scales/biases: restated MLX CPU "
+                      f"_qmm_t loop (oracle/eq_oracle.c or_qmm_t_f32)", "runs": res}
+
+
+def cpu_baseline_gguf(budget_s=6.0, rows=4096, cols=14336):
+    """eredu-gguf's convert_affine (convert.rs:318-465) as the oracle restates it
+    (oracle/eq_oracle.c or_gguf_convert_affine), single-threaded like the
+    reference's scalar loop, on uniform random blocks of a 4096 x 14336
+    tensor (the GPU leg's input); GB/s counts blocks in + codes/scales/biases
+    out, as the GPU leg does."""
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(2)
+    out = {}
+    geo = {"Q4_0": (2, 32, 18, 4, 32), "Q8_0": (8, 32, 34, 8, 32), "Q4_K": (12, 256, 144, 4, 32)}
+    for name, (code, vals, nbytes, bits, gs) in geo.items():
+        nraw = rows * cols // vals * nbytes
+        raw = rng.integers(0, 256, nraw, dtype=np.uint8)
+        moved = nraw + rows * cols * bits // 8 + 2 * 2 * rows * (cols // gs)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.gguf_convert_affine(code, raw)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > budget_s / 3 or reps >= 50:
+                break
+        out[name] = {"GB/s": round(moved * reps / el / 1e9, 4), "passes": reps, "seconds": round(el, 2)}
+    return {"unit": "GB/s", "kind": "port", "threads": 1, "convert_affine": out,
+            "sample": f"{rows} x {cols} tensors of uniform random blocks, one thread"}
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmv_lds_decode_M1_grouped.md")
 
 
@@ -943,6 +1002,10 @@ def main():
                "single_thread_GB/s": round(v1[0], 3), "host": host_cpu(),
                "threads_note": "threads = min(16, CPUs in this process's affinity): 16 is the GPU box's CPU share "
                                "per GPU"}
+        log("[bench] CPU baseline, prefill qmm")
+        cpu["prefill_qmm_M512"] = cpu_baseline_prefill(threads)
+        log("[bench] CPU baseline, GGUF convert")
+        cpu["gguf_convert"] = cpu_baseline_gguf()
     del layers
     torch.cuda.empty_cache()
     if not args.quick:
@@ -978,6 +1041,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "timing": "median over the timed replays of one HIP graph per step (HIP events around each replay)",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -22,8 +22,16 @@ namespace eq {
 
 static thread_local std::string g_last_error;
 
+static thread_local bool g_refused = false;
+
 void set_error(const std::string& msg) { g_last_error = msg; }
 void clear_error() { g_last_error.clear(); }
+void note_refusal() { g_refused = true; }
+bool take_refusal() {
+    const bool r = g_refused;
+    g_refused = false;
+    return r;
+}
 
 int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
@@ -378,7 +386,7 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
     if ((mfma_ok || odd_ok) && M > 16 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8)) {
         if (launch_qmm_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
                             w, scales, biases, int(M), int(N), int(K), ws, st))
-            return check_launch("quantized_matmul (qmm)");
+            return take_refusal() ? 1 : check_launch("quantized_matmul (qmm)");
     }
     if (transpose && x_dtype == EQ_DTYPE_BF16 && M <= 16 &&
         launch_qmv_any(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w,

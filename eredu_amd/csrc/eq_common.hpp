@@ -22,6 +22,13 @@ void clear_error();
 // Checks the launch status of the kernels just enqueued.
 int check_launch(const char* what);
 
+// A launcher that takes a shape but cannot run its plan (its scratch memory
+// cannot be provided) sets the message and records a refusal instead of
+// running another plan; the entry point then fails.  take_refusal() reads
+// and clears it.
+void note_refusal();
+bool take_refusal();
+
 // Compute units of the current device (cached per device; 256 if the query fails).
 int device_cu_count();
 

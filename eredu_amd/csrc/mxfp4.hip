@@ -261,7 +261,7 @@ int mxfp4_matmul(void* y, const void* x, const uint32_t* w, const uint8_t* scale
     // reading W again, cost more than one MFMA tile of 128 rows): the MFMA qmm
     if (mfma_ok && plain && M > 4 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8) &&
         launch_qmm_mfma_mxfp4(yb, xb, w, scales, int(M), int(N), int(K), ws, st))
-        return check_launch("quantized_matmul (mxfp4 qmm)");
+        return take_refusal() ? 1 : check_launch("quantized_matmul (mxfp4 qmm)");
     // the decode shape: the any-width decode kernel with E2M1 codes
     if (bf16_t && plain && M <= 16 && launch_qmv_any_mxfp4(yb, xb, w, scales, int(M), int(N), int(K), st))
         return check_launch("quantized_matmul (mxfp4 decode)");

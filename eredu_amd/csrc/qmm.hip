@@ -486,7 +486,7 @@ static int qmm_cu_count() {
 
 // One launch (plus the split reduction): every buffer below 2^31 bytes.
 template <int BITS, int GS, typename ST>
-static void launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
+static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
                              int M, int N, int K, bool may_split, const WsSource* src, hipStream_t st) {
     QmmArgs a{};
     a.y = y, a.x = x, a.w = w, a.s = static_cast<const uint16_t*>(s), a.b = static_cast<const uint16_t*>(b);
@@ -518,6 +518,18 @@ static void launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
         }
         if (splits > 1) {
             a.ws = static_cast<float*>(ws_acquire(src, size_t(splits) * per_split, st));
+            if (!a.ws && !src) {
+                // The library workspace cannot grow (the stream is capturing,
+                // or the allocation failed).  Running unsplit would be a
+                // different plan with a different summation order than the
+                // same call made eagerly, so the call fails instead.
+                set_error("quantized_matmul (qmm): the split-K plan needs " +
+                          std::to_string(size_t(splits) * per_split) +
+                          " bytes of workspace on this stream, which cannot grow while the stream is capturing "
+                          "(make one call of this shape on the stream before capturing)");
+                note_refusal();
+                return false;
+            }
             if (!a.ws) splits = 1;
         }
     }
@@ -529,13 +541,14 @@ static void launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
     if (splits == 1) {
         if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64><<<grid, block, 0, st>>>(a);
         else qmm_mfma_kernel<BITS, GS, ST, false, false><<<grid, block, 0, st>>>(a);
-        return;
+        return true;
     }
     if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64><<<grid, block, 0, st>>>(a);
     else qmm_mfma_kernel<BITS, GS, ST, true, false><<<grid, block, 0, st>>>(a);
     const int64_t mn = int64_t(M) * N;
     qmm_split_reduce<<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(
         y, a.ws, mn, N, ldy, splits, aligned(y, 8) && N % 4 == 0 && ldy % 4 == 0);
+    return true;
 }
 
 // Buffer offsets in the kernel are 32-bit: a weight matrix of 2^31 bytes or
@@ -562,8 +575,10 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
             constexpr int64_t PB = __is_same(ST, E8M0T) ? 1 : 2;
             const char* sp = static_cast<const char*>(s) + n0 * G * PB;
             const char* bp = b ? static_cast<const char*>(b) + n0 * G * PB : nullptr;
-            launch_qmm_piece<BITS, GS, ST>(y + m0 * ldy + n0, ldy, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp, mc,
-                                           nc, K, whole, src, st);
+            // (only a whole problem splits K, so a refusal comes before any launch)
+            if (!launch_qmm_piece<BITS, GS, ST>(y + m0 * ldy + n0, ldy, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp,
+                                                mc, nc, K, whole, src, st))
+                return;
         }
     }
 }
@@ -780,6 +795,15 @@ static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, c
     const size_t part_bytes = splits > 1 ? size_t(splits) * size_t(M) * size_t(nc) * 4u : 0;
     size_t want = code_bytes + part_bytes;
     char* base = static_cast<char*>(ws_acquire(src, want, st));
+    if (!base && !src) {
+        // the library workspace cannot grow (capture): fail rather than run
+        // another plan than the same call made eagerly
+        set_error("quantized_matmul (qmm, " + std::to_string(bits) + "-bit): the plan needs " + std::to_string(want) +
+                  " bytes of workspace on this stream, which cannot grow while the stream is capturing "
+                  "(make one call of this shape on the stream before capturing)");
+        note_refusal();
+        return true;
+    }
     if (!base) base = static_cast<char*>(ws_acquire(src, want = code_bytes, st));
     if (!base) return false;
     const size_t cap = src ? src->cap : want;

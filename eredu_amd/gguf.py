@@ -327,10 +327,12 @@ def native_grouped_linear(input: torch.Tensor, weight: "NativeTensor", group_ids
         raise EreduError(f"native grouped linear shape mismatch: input {list(input.shape)}, ids "
                          f"{list(group_ids.shape)}, weight {shape}")
     experts, N, K = shape
-    ty = _device_type(weight.descriptor())
-    _check_raw(weight.descriptor(), weight.data)
     if input.dtype != torch.bfloat16:
         raise EreduError("native GGUF grouped linear takes bfloat16 activations")
+    if not input.is_cuda or input.device != weight.data.device:
+        raise EreduError("native GGUF grouped linear expected a CUDA input on the weight's device")
+    ty = _device_type(weight.descriptor())
+    _check_raw(weight.descriptor(), weight.data)
     ids = group_ids.to(device=weight.data.device, dtype=torch.int32).contiguous()
     bad = ((ids < 0) | (ids >= experts)).nonzero()
     if bad.numel():

@@ -617,19 +617,15 @@ class QuantizedEmbedding:
         return cls(native.data.view(native.shape[0], -1), None, None, values, nbytes, QuantizationMode.Affine, native)
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
-        flat = ids.reshape(-1).to(torch.int64)
         if self.native is not None:
-            from . import gguf as G
-
-            nt = self.native
-            rows = nt.data.view(nt.shape[0], -1).index_select(0, flat).contiguous().view(-1)
-            sub = G.NativeTensor(nt.name, [flat.numel(), nt.shape[-1]], nt.ggml_type, nt.endian, rows)
-            out = sub.dequantize(torch.bfloat16)
-        else:
-            w = self.weight.index_select(0, flat)
-            s = self.scales.index_select(0, flat)
-            b = self.biases.index_select(0, flat) if self.biases is not None else None
-            out = dequantize_with_mode(w, s, b, self.group_size, self.bits, self.mode)
+            # native_quantization.rs:915-939: float32 rows, ids checked against
+            # the table before any device work
+            return self.native.embedding(ids, torch.float32)
+        flat = ids.reshape(-1).to(torch.int64)
+        w = self.weight.index_select(0, flat)
+        s = self.scales.index_select(0, flat)
+        b = self.biases.index_select(0, flat) if self.biases is not None else None
+        out = dequantize_with_mode(w, s, b, self.group_size, self.bits, self.mode)
         return out.reshape(*ids.shape, -1)
 
     __call__ = forward

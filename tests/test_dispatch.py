@@ -98,3 +98,13 @@ def test_layer_factory_shapes():
         QuantizedLinear.unloaded_iq(512, 64, int(T.Q4_0), 0, False, cpu)
     spec = nn.LinearSpec(512, 64, False, "blk.0.attn_q.weight", None)
     assert isinstance(nn.linear(spec, cpu), nn.Linear)
+
+
+def test_native_grouped_linear_rejects_host_input():
+    """A host input never reaches eq_gguf_grouped_linear: its pointers would be
+    read by the device kernels."""
+    bank = G.NativeTensor("blk.0.ffn_up_exps.weight", [2, 128, 256], T.Q4K, G.Endian.Little,
+                          torch.zeros(2 * 128 * 256 // 256 * 144, dtype=torch.uint8))
+    x = torch.zeros((1, 256), dtype=torch.bfloat16)
+    with pytest.raises(EreduError, match="CUDA input"):
+        G.native_grouped_linear(x, bank, torch.zeros(1, dtype=torch.int32))

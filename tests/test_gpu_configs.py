@@ -75,6 +75,34 @@ def test_lm_head_vocab_128256(cuda):
     assert ok, f"max|err|/RMS = {worst:.3e}"
 
 
+@pytest.mark.parametrize("M", [1, 32])
+def test_weight_beyond_2_31_bytes(cuda, M):
+    """An 8-bit 262144 x 8192 weight holds 2^31 bytes of codes, past the
+    32-bit buffer offsets of the kernels: the prefill launcher runs it in row
+    pieces of 261888 rows (multiples of the 256-column tile), the decode
+    launcher in row chunks below 2^31 bytes.  Output features on both sides
+    of the piece boundary, the first and the last are checked against the
+    oracle."""
+    N, K, bits = 262144, 8192, 8
+    boundary = ((2**31 - 1) // K) // 256 * 256  # 261888
+    print(f"[case] weight beyond 2^31 bytes M={M} N={N} K={K} bits={bits}", flush=True)
+    w, s, b = device_random_linear(N, K, 64, bits, seed=31 + M)
+    assert w.numel() * 4 == 2**31
+    xb = synthetic_x(M, K, seed=32 + M)
+    y = quantized_matmul_with_mode(dev_bf16(xb), w, s, b, True, 64, bits)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(33)
+    n_sel = np.unique(np.concatenate([np.arange(boundary - 160, boundary + 160), [0, 1, N - 2, N - 1],
+                                      rng.choice(N, 256, replace=False)]))
+    wr, sr, br = host_rows(w, s, b, n_sel)
+    ref = orc.quantized_matmul_f64(xb, orc.BF16, wr, sr, br, orc.BF16, True, 64, bits, len(n_sel), K)
+    got = host_f32(y)[:, n_sel]
+    del w, s, b, y
+    torch.cuda.empty_cache()
+    ok, worst, _ = orc.matmul_within_tolerance(got, ref, out_is_bf16=True)
+    assert ok, f"max|err|/RMS = {worst:.3e}"
+
+
 def _bits(x):
     return orc.f32_to_bf16_bits(np.asarray(x, dtype=np.float32))
 

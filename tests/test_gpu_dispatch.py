@@ -150,10 +150,14 @@ def test_quantized_embedding_affine_and_native(cuda):
     y = emb.as_linear(dev_bf16(xb))
     yref = orc.quantized_matmul_f64(xb, orc.BF16, w, s, b, orc.BF16, True, 64, 4, V, D)
     assert orc.matmul_within_tolerance(host_f32(y), yref, out_is_bf16=True)[0]
-    # native Q8_0 rows: the native decoder of the gathered blocks
+    # native Q8_0 rows: NativeQuantizedTensor::embedding (native_quantization.rs:915-939),
+    # float32 rows of the native decoder, and the reference's range error
     raw = synthetic_blocks(8, V * D // 32, seed=8)
     nt = G.NativeTensor("tok_embd.weight", [V, D], G.GgmlType.Q8_0, G.Endian.Little, dev_u8(raw))
     nemb = QuantizedEmbedding.from_native(nt)
-    got = host_bits16(nemb(ids)).reshape(len(flat), D)
-    dense = orc.gguf_dequant_bf16(8, raw, int(G.DequantDefinition.Native)).reshape(V, D)
-    assert np.array_equal(got, dense[flat])
+    out = nemb(ids)
+    assert tuple(out.shape) == (2, 3, D) and out.dtype == torch.float32
+    dense = orc.gguf_dequant_f32(8, raw, int(G.DequantDefinition.Native)).reshape(V, D)
+    assert np.array_equal(out.cpu().numpy().reshape(len(flat), D).view(np.uint32), dense[flat].view(np.uint32))
+    with pytest.raises(EreduError, match="outside 0..200"):
+        nemb(torch.tensor([5, 200], dtype=torch.int32, device="cuda"))

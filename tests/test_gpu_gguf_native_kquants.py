@@ -3,7 +3,9 @@ eredu keeps in their blocks besides Q4_K / Q8_0): y = x . W^T straight from
 the blocks, against the fp64 product with W from ggml's closed-form decoders
 (the unrounded factors the reference's native kernels use;
 tests/test_oracle_kquants.py pins those closed forms), within the matmul
-rule |y - y_ref| <= 1e-2 RMS(y_ref) + 1/2 ulp_bf16."""
+rule |y - y_ref| <= 1e-2 RMS(y_ref) + 1/2 ulp_bf16.  Q5_K and Q6_K are also
+held to the same rule against the reference's other numerics for them, the
+f16-rounded affine decode of its non-Metal row path."""
 import numpy as np
 import pytest
 import torch
@@ -39,9 +41,20 @@ def run_case(ty, N, K, M, seed, endian=G.Endian.Little, offset=0):
     xb = synthetic_x(M, K, seed + 1)
     y = G.linear(dev_bf16(xb), desc, buf[offset:offset + stored.size], endian)
     assert list(y.shape) == [M, N] and y.dtype == torch.bfloat16
-    ref = orc.bf16_bits_to_f32(xb).astype(np.float64) @ closed_form(ty, raw, N, K).T
-    ok, worst, _ = orc.matmul_within_tolerance(host_f32(y), ref, True)
+    xf = orc.bf16_bits_to_f32(xb).astype(np.float64)
+    ref = xf @ closed_form(ty, raw, N, K).T
+    got = host_f32(y)
+    ok, worst, _ = orc.matmul_within_tolerance(got, ref, True)
     assert ok, (ty.name, N, K, M, endian, worst)
+    if ty in (T.Q5K, T.Q6K):
+        # The reference's non-Metal route for these two formats decodes rows
+        # through IQuantTensor::dequantize_f32, the affine form with d * sc
+        # rounded to f16 (safemlx/src/native_quantization.rs:987-1000,
+        # eredu-gguf/src/convert.rs:43-56,439-564): the same product must
+        # also sit within the matmul rule of that numerics.
+        W_aff = orc.gguf_dequant_f32(int(ty), raw, int(G.DequantDefinition.Affine)).reshape(N, K)
+        ok, worst, _ = orc.matmul_within_tolerance(got, xf @ W_aff.astype(np.float64).T, True)
+        assert ok, ("f16-rounded route", ty.name, N, K, M, endian, worst)
 
 
 # K: Q5_1 rows of 128 and 129 blocks; Q5_K / Q6_K rows of 5, 16 and 56

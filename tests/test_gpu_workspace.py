@@ -155,3 +155,47 @@ def test_streams_keep_apart_and_replays_reset_counters(cuda):
             qmm_n_call(outs[1], probs[1][3], probs[1][0], probs[1][1], probs[1][2], N, K, streams[0].cuda_stream)
         torch.cuda.synchronize()
         assert torch.equal(outs[1].view(torch.int16), refs[1].view(torch.int16)), f"eager after replay {rep}"
+
+
+def test_captured_qmm_runs_the_eager_plan(cuda):
+    """M = 512 x 4096 x 4096 splits K through the stream's workspace.  On a
+    fresh stream the workspace cannot grow while capturing, so the capture
+    fails with a message instead of recording an unsplit plan (which would
+    sum in another order than the eager call).  After one eager call on the
+    stream, the captured call runs the eager plan: every replay equals the
+    eager result bit for bit."""
+    M, N, K = 512, 4096, 4096
+    w, s, b = synthetic_linear(N, K, 64, 4, seed=21)
+    wd, sd, bd = dev_words(w), dev_bf16(s), dev_bf16(b)
+    x = dev_bf16(synthetic_x(M, K, seed=22))
+    y_eager, y_graph = (torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for _ in range(2))
+    stream = torch.cuda.Stream()
+    st = stream.cuda_stream
+    stream.wait_stream(torch.cuda.current_stream())
+    print("[case] capture on a fresh stream", flush=True)
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with pytest.raises(n.EreduError, match="cannot grow while the stream is capturing"):
+            with torch.cuda.graph(graph, stream=stream):
+                qmm_call(y_graph, x, wd, sd, bd, M, N, K, st)
+    torch.cuda.synchronize()
+    print("[case] capture after an eager call", flush=True)
+    with torch.cuda.stream(stream):
+        qmm_call(y_eager, x, wd, sd, bd, M, N, K, st)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            qmm_call(y_graph, x, wd, sd, bd, M, N, K, st)
+    torch.cuda.synchronize()
+    other = torch.empty_like(y_eager)
+    for rep in range(3):
+        y_graph.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph.view(torch.int16), y_eager.view(torch.int16)), f"replay {rep}"
+        with torch.cuda.stream(stream):  # eager work between replays
+            qmm_call(other, x, wd, sd, bd, M, N, K, st)
+        torch.cuda.synchronize()
+        assert torch.equal(other.view(torch.int16), y_eager.view(torch.int16)), f"eager after replay {rep}"
