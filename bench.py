@@ -731,7 +731,9 @@ def build_decoder(layers, gen, fused=None):
     for r0 in range(0, VOCAB, 8192):
         embed[r0:r0 + 8192] = torch.randn((min(8192, VOCAB - r0), HIDDEN), device="cuda", generator=gen).to(bf)
     lm = Linear(VOCAB, HIDDEN, gen)
-    max_seq = CACHE_TOKENS + 1
+    # room past the 1024 cached rows for the positions that the device-position
+    # graph's replays advance through
+    max_seq = CACHE_TOKENS + 256
     caches = [[torch.randn((N_KV_HEADS, max_seq, 128), device="cuda", generator=gen).to(bf) for _ in layers]
               for _ in range(2)]
     freqs = E.llama3_rope_freqs(128, 500000.0, 8.0, 1.0, 4.0, 8192)
@@ -740,8 +742,11 @@ def build_decoder(layers, gen, fused=None):
 
 
 def bench_decode_step(layers, steps, warmup, gen):
-    """Full batch-1 decode step as one HIP graph: tok/s, and the
-    step's algorithmic bytes against 8 TB/s."""
+    """Full batch-1 decode step: tok/s of one HIP graph that
+    decodes successive tokens (the position in device memory, advanced by
+    each replay, from the 1024 cached tokens on), and the step's algorithmic
+    bytes against 8 TB/s.  Also the step at a position fixed by the capture
+    (one graph per position) for comparison."""
     from eredu_amd import decode as E
 
     dec = build_decoder(layers, gen)
@@ -750,18 +755,28 @@ def bench_decode_step(layers, steps, warmup, gen):
                            eps=1e-5, freqs=dec.freqs.cpu().numpy(), max_seq=dec.max_seq, k_caches=dec.k_caches,
                            v_caches=dec.v_caches, fused=not dec.fused)
     pos = CACHE_TOKENS
-    ms_a = Timer(lambda st: dec.step(pos)).ms_per_replay(steps, warmup)
-    ms_b = Timer(lambda st: other.step(pos)).ms_per_replay(steps, warmup)
+    ms_host = Timer(lambda st: dec.step(pos)).ms_per_replay(steps, warmup)
+
+    def device_ms(d):
+        d.set_position(pos)  # the Timer's eager call decodes pos, the replays pos + 1, pos + 2, ...
+        return Timer(lambda st: d.step_device()).ms_per_replay(steps, warmup)
+
+    ms_a, ms_b = device_ms(dec), device_ms(other)
     if ms_b < ms_a:
         dec, other, ms_a, ms_b = other, dec, ms_b, ms_a
     ms = ms_a
-    nbytes = dec.bytes_per_step(pos)
+    mean_pos = pos + warmup + (steps + 1) // 2  # mean position of the timed replays
+    nbytes = dec.bytes_per_step(mean_pos)
     gbs = nbytes / (ms * 1e-3) / 1e9
     roof = HBM_PEAK_GBS * 1e9 / nbytes
     out = {"ms": round(ms, 4), "tok/s": round(1e3 / ms, 1), "bytes_per_token": nbytes, "GB/s": round(gbs, 1),
            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "roofline_tok/s": round(roof, 1),
-           "launches": dec.launches_per_step(), "fused_prologues": dec.fused,
-           "other_variant_ms": round(ms_b, 4), "other_variant_launches": other.launches_per_step(),
+           "launches": dec.launches_per_step(device_position=True), "fused_prologues": dec.fused,
+           "position": f"device memory, advanced by each replay of one graph; timed replays at positions "
+                       f"{pos + warmup + 1}..{pos + warmup + steps}",
+           "other_variant_ms": round(ms_b, 4),
+           "other_variant_launches": other.launches_per_step(device_position=True),
+           "host_position_ms": round(ms_host, 4), "host_position_launches": dec.launches_per_step(),
            "workload": "batch 1, 32 layers, H 4096, 32 q / 8 kv heads x 128, FFN 14336, vocab 128256, 4-bit g64 "
                        "linears incl. LM head, bf16 embeddings/norms, 1024-token bf16 KV cache, greedy argmax"}
     del dec, other

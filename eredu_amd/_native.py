@@ -36,6 +36,9 @@ SIGNATURES = {
                                   _i32, _vp], _i32),
     "eq_rope_attention_decode_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32,
                                           ctypes.c_float, _i32, _vp], _i32),
+    "eq_rope_attention_decode_at": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32,
+                                     ctypes.c_float, _i32, _vp], _i32),
+    "eq_advance_position": ([_vp, _vp], _i32),
     "eq_silu_mul": ([_vp, _vp, _vp, _i64, _i32, _vp], _i32),
     "eq_embedding": ([_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp], _i32),
     "eq_argmax": ([_vp, _vp, _i64, _i64, _i32, _vp], _i32),

@@ -155,18 +155,26 @@ __device__ __forceinline__ void rope_pair(float* head, const float* __restrict__
 // to the workspace for the combine pass.  The chunk that holds `pos` also
 // rotates the new key and stores it and the new value into the cache; no
 // other workgroup reads position `pos`.
+//
+// pos_p, when not null, names the position in device memory (read when the
+// kernel runs) and the grid covers every chunk of max_seq: workgroups of
+// chunks past the position leave at once, and a position outside
+// [0, max_seq) does nothing.  nchunks is the chunk stride of ws per head.
 __global__ __launch_bounds__(256) void attn_partial_kernel(float* __restrict__ ws, const uint16_t* __restrict__ q,
                                                            const uint16_t* __restrict__ k_new,
                                                            const uint16_t* __restrict__ v_new,
                                                            uint16_t* __restrict__ k_cache,
                                                            uint16_t* __restrict__ v_cache,
-                                                           const float* __restrict__ freqs, int pos, int max_seq,
+                                                           const float* __restrict__ freqs, int pos_arg,
+                                                           const int32_t* __restrict__ pos_p, int max_seq,
                                                            int n_heads, int n_kv_heads, int nchunks, float scale) {
     __shared__ float qs[4][kHeadDim];                            // rotated queries of this group
     __shared__ __attribute__((aligned(16))) uint16_t ks[kAttnChunk][kRowPad];
     __shared__ __attribute__((aligned(16))) uint16_t vs[kAttnChunk][kRowPad];
     __shared__ float knew[kHeadDim];
     const int g = blockIdx.x, c = blockIdx.y;
+    const int pos = pos_p ? __builtin_amdgcn_readfirstlane(*pos_p) : pos_arg;
+    if (pos < 0 || pos >= max_seq || c * kAttnChunk > pos) return;
     const int group = n_heads / n_kv_heads;  // <= 4
     const int p0 = c * kAttnChunk, np = min(kAttnChunk, pos + 1 - p0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -249,18 +257,33 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(float* __restrict__ w
     }
 }
 
+// pos[0] += 1 (the next decode position), one thread.
+__global__ void advance_position_kernel(int32_t* pos) { pos[0] += 1; }
+
 // One workgroup of 256 threads per query head: the chunks' partial states
 // (max, weight sum, weighted values) merged -- their maxima and rescale
 // factors computed in parallel into LDS, then two halves of the threads sum
 // alternate chunks for each dimension with independent loads -- divided by
 // the total weight, rounded to bf16.
+// With pos_p (device position) the chunk count comes from the position
+// (zeros for one outside [0, max_seq)); ws holds `stride` chunks per head.
 __global__ __launch_bounds__(256) void attn_combine_kernel(uint16_t* __restrict__ out, const float* __restrict__ ws,
-                                                           int nchunks) {
+                                                           int nchunks_arg, const int32_t* __restrict__ pos_p,
+                                                           int max_seq, int stride) {
     __shared__ float fac[kMaxChunks];
     __shared__ float red[4];
     __shared__ float part[128];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float* base = ws + int64_t(h) * nchunks * (kHeadDim + 2);
+    int nchunks = nchunks_arg;
+    if (pos_p) {
+        const int pos = __builtin_amdgcn_readfirstlane(*pos_p);
+        nchunks = pos >= 0 && pos < max_seq ? pos / kAttnChunk + 1 : 0;
+        if (nchunks == 0) {
+            if (tid < kHeadDim) out[int64_t(h) * kHeadDim + tid] = 0;
+            return;
+        }
+    }
+    const float* base = ws + int64_t(h) * stride * (kHeadDim + 2);
     float m = -INFINITY;
     for (int c = tid; c < nchunks; c += 256) m = fmaxf(m, base[c * (kHeadDim + 2)]);
 #pragma unroll
@@ -537,9 +560,10 @@ static void launch_attention(float* ws, void* out, const void* q, const void* k_
                              int n_kv_heads, int nchunks, float scale, hipStream_t st) {
     attn_partial_kernel<<<dim3(unsigned(n_kv_heads), unsigned(nchunks)), dim3(256), 0, st>>>(
         ws, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
-        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, int(pos), int(max_seq), n_heads,
-        n_kv_heads, nchunks, scale);
-    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, nchunks);
+        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, int(pos), nullptr, int(max_seq),
+        n_heads, n_kv_heads, nchunks, scale);
+    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, nchunks,
+                                                                       nullptr, int(max_seq), nchunks);
 }
 
 static size_t attention_scratch_bytes(int64_t pos, int n_heads, int& nchunks) {
@@ -567,6 +591,54 @@ extern "C" int eq_rope_attention_decode(void* out, const void* q, const void* k_
     launch_attention(ws, out, q, k_new, v_new, k_cache, v_cache, freqs, pos, max_seq, n_heads, n_kv_heads, nchunks,
                      scale, st);
     return check_launch("eq_rope_attention_decode");
+}
+
+extern "C" int eq_rope_attention_decode_at(void* out, const void* q, const void* k_new, const void* v_new,
+                                           void* k_cache, void* v_cache, const float* freqs, const int32_t* pos,
+                                           int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
+                                           int dtype, eq_stream_t stream) {
+    clear_error();
+    const char* who = "eq_rope_attention_decode_at";
+    if (!pos) {
+        set_error(std::string(who) + ": null pointer argument");
+        return 1;
+    }
+    // the shape rules of the by-value entry point, checked at position 0 (the
+    // position itself is read by the kernel; one outside [0, max_seq) gives zeros)
+    if (!attention_args_ok(who, out, q, k_new, v_new, k_cache, v_cache, freqs, 0, max_seq, n_heads, n_kv_heads,
+                           head_dim, dtype))
+        return 1;
+    if (max_seq > int64_t(kMaxChunks) * kAttnChunk) {
+        set_error(std::string(who) + ": max_seq must be at most 131072");
+        return 1;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    // every chunk of max_seq has a slot; the kernels read the position
+    const int nchunks = int((max_seq + kAttnChunk - 1) / kAttnChunk);
+    const size_t ws_bytes = size_t(n_heads) * size_t(nchunks) * (kHeadDim + 2) * sizeof(float);
+    float* ws = static_cast<float*>(ws_acquire(nullptr, ws_bytes, st));
+    if (!ws) {
+        set_error(std::string(who) + ": no workspace (its stream's workspace cannot grow while capturing: make one "
+                  "call with this max_seq on the stream before capturing)");
+        return 1;
+    }
+    attn_partial_kernel<<<dim3(unsigned(n_kv_heads), unsigned(nchunks)), dim3(256), 0, st>>>(
+        ws, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
+        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, 0, pos, int(max_seq), n_heads,
+        n_kv_heads, nchunks, scale);
+    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, 0, pos,
+                                                                       int(max_seq), nchunks);
+    return check_launch(who);
+}
+
+extern "C" int eq_advance_position(int32_t* pos, eq_stream_t stream) {
+    clear_error();
+    if (!pos) {
+        set_error("eq_advance_position: null pointer argument");
+        return 1;
+    }
+    advance_position_kernel<<<1, 1, 0, reinterpret_cast<hipStream_t>(stream)>>>(pos);
+    return check_launch("eq_advance_position");
 }
 
 // ---------------------------------------------------- allocation-free variant

@@ -13,10 +13,13 @@ matmul C ABI (q/k/v and gate/up as one grouped launch each, results
 bit-identical to separate calls); the rest through the decode entry points of
 ``include/eredu_hip.h``.  Every buffer is allocated once, so a step can be
 captured in a HIP graph; the token id lives in device memory and the step
-reads it (embedding) and overwrites it (argmax).  The position is an argument
-of the step that the capture records: one graph replays one position (it
-re-reads cache rows 0..pos and rewrites row pos), so autoregressive decoding
-captures one graph per position.  There is no CPU fallback.
+reads it (embedding) and overwrites it (argmax).  The position is either an
+argument of the step that a capture records (``step(pos)``: one graph replays
+one position), or lives in device memory too (``step_device()``: attention
+reads it when it runs and the step ends by advancing it, so one captured
+graph decodes successive tokens, as the reference's token loop advances its
+cache offset every token, eredu/src/runtime/generation/streaming.rs:1038-1050).
+There is no CPU fallback.
 """
 from __future__ import annotations
 
@@ -96,6 +99,24 @@ def rope_attention_decode(q, k_new, v_new, k_cache, v_cache, freqs: torch.Tensor
     return out
 
 
+def rope_attention_decode_at(q, k_new, v_new, k_cache, v_cache, freqs: torch.Tensor, pos: torch.Tensor,
+                             n_heads: int, n_kv_heads: int, scale: float) -> torch.Tensor:
+    """rope_attention_decode at the position held by the int32 device tensor
+    ``pos`` (read when the kernel runs; C ABI: eq_rope_attention_decode_at)."""
+    for t, n in ((q, "q"), (k_new, "k_new"), (v_new, "v_new"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _bf16(t, n)
+    if freqs.dtype != torch.float32 or not freqs.is_cuda:
+        raise _native.EreduError("freqs must be a float32 CUDA tensor")
+    if pos.dtype != torch.int32 or not pos.is_cuda:
+        raise _native.EreduError("pos must be an int32 CUDA tensor")
+    out = torch.empty((n_heads * HEAD_DIM,), dtype=torch.bfloat16, device=q.device)
+    check(_native.lib().eq_rope_attention_decode_at(
+        out.data_ptr(), q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        freqs.data_ptr(), pos.data_ptr(), k_cache.shape[1], n_heads, n_kv_heads, HEAD_DIM, float(scale),
+        _native.EQ_DTYPE_BF16, _stream()))
+    return out
+
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up with the reference's bf16 roundings (C ABI: eq_silu_mul)."""
     _bf16(gate, "gate")
@@ -164,7 +185,10 @@ class LlamaDecoder:
     """Batch-1 greedy decode of a Llama-shaped model.  ``step(pos)`` embeds the
     token in ``self.token``, runs every layer with the cache row ``pos`` as the
     new position, and writes the argmax of the logits back into ``self.token``.
-    ``step`` enqueues on the current stream and allocates nothing.
+    ``step_device()`` does the same at the position held in ``self.position``
+    (int32 device memory, set with ``set_position``) and then advances it by
+    one, so that replays of one captured graph decode successive tokens.  Both
+    enqueue on the current stream and allocate nothing.
 
     ``fused`` (default: when the shapes allow it) folds each residual add +
     RMSNorm into the launch of the projections that consume it, and SiLU-mul
@@ -201,6 +225,7 @@ class LlamaDecoder:
         self.gate, self.up, self.act, self.down = e(self.ffn), e(self.ffn), e(self.ffn), e(H)
         self.logits = e(lm_head.N)
         self.token = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.position = torch.zeros((1,), dtype=torch.int32, device=dev)
         lins = [getattr(Lr, p) for Lr in self.layers for p in ("q", "k", "v", "o", "gate", "up", "down")]
         can_fuse = (H <= 4096 and H % 64 == 0 and self.ffn % 64 == 0 and lm_head.N % 16 == 0 and
                     all(l.group_size == 64 and l.bits in (4, 8) and l.N % 16 == 0 and l.scales.dtype == torch.bfloat16
@@ -267,30 +292,61 @@ class LlamaDecoder:
             lin.biases.data_ptr() if lin.biases is not None else None, 1, lin.N, lin.K, True, lin.group_size,
             lin.bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, st))
 
-    def launches_per_step(self) -> int:
+    def launches_per_step(self, device_position: bool = False) -> int:
         # embedding; per layer 2 norms, 4 projection launches, attention (2
-        # kernels), silu_mul; final norm, LM head, argmax (fused: the norms
-        # and silu_mul ride in the projections' launches)
-        if self.fused:
-            return 1 + len(self.layers) * 6 + 2
-        return 1 + len(self.layers) * 9 + 3
+        # kernels), silu_mul; final norm, LM head, argmax, and the position
+        # advance of step_device (fused: the norms and silu_mul ride in the
+        # projections' launches)
+        per_layer = 6 if self.fused else 9
+        tail = (2 if self.fused else 3) + (1 if device_position else 0)
+        return 1 + len(self.layers) * per_layer + tail
 
     def _pro(self, probs, count: int, lin: QLinear, pro, st: int) -> None:
         n = _native
         check(n.lib().eq_quantized_matmul_batched_prologue(probs, count, 1, True, lin.group_size, lin.bits, b"affine",
                                                            n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, ctypes.byref(pro), st))
 
-    def _step_fused(self, pos: int, st: int) -> None:
+    def _attend(self, li: int, pos: Optional[int], st: int) -> None:
+        """Layer li's attention at ``pos``, or at the device position when None."""
+        n, L = _native, _native.lib()
+        if pos is None:
+            check(L.eq_rope_attention_decode_at(
+                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                self.k_caches[li].data_ptr(), self.v_caches[li].data_ptr(), self.freqs.data_ptr(),
+                self.position.data_ptr(), self.max_seq, self.n_heads, self.n_kv_heads, HEAD_DIM, self.scale,
+                n.EQ_DTYPE_BF16, st))
+        else:
+            check(L.eq_rope_attention_decode(
+                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                self.k_caches[li].data_ptr(), self.v_caches[li].data_ptr(), self.freqs.data_ptr(), pos, self.max_seq,
+                self.n_heads, self.n_kv_heads, HEAD_DIM, self.scale, n.EQ_DTYPE_BF16, st))
+
+    def set_position(self, pos: int) -> None:
+        """Writes the device position that ``step_device`` decodes next (a copy
+        on the current stream; not inside a capture)."""
+        if not 0 <= pos < self.max_seq:
+            raise _native.EreduError(f"position {pos} outside the cache of {self.max_seq}")
+        self.position.fill_(int(pos))
+
+    def step_device(self) -> None:
+        """One step at the device position, then position += 1 (one launch).  A
+        position that reaches max_seq makes attention write no cache row and
+        return zeros; the caller stops before that, as it would with step()."""
+        st = _stream()
+        if self.fused:
+            self._step_fused(None, st)
+        else:
+            self._step_unfused(None, st)
+        check(_native.lib().eq_advance_position(self.position.data_ptr(), st))
+
+    def _step_fused(self, pos: Optional[int], st: int) -> None:
         n, L = _native, _native.lib()
         bf = n.EQ_DTYPE_BF16
         check(L.eq_embedding(self.x.data_ptr(), self.embed.data_ptr(), self.token.data_ptr(), 1, self.vocab,
                              self.hidden, bf, st))
         for li, Lr in enumerate(self.layers):
             self._pro(self._fqkv[li], 3, Lr.q, self._pro_in[li], st)
-            check(L.eq_rope_attention_decode(
-                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                self.k_caches[li].data_ptr(), self.v_caches[li].data_ptr(), self.freqs.data_ptr(), pos, self.max_seq,
-                self.n_heads, self.n_kv_heads, HEAD_DIM, self.scale, bf, st))
+            self._attend(li, pos, st)
             self._linear(Lr.o, self.att, self.o, st)
             self._pro(self._fgu[li], 2, Lr.gate, self._pro_post[li], st)
             self._pro(self._fdown[li], 1, Lr.down, self._pro_silu, st)
@@ -300,11 +356,14 @@ class LlamaDecoder:
     def step(self, pos: int) -> None:
         if not 0 <= pos < self.max_seq:
             raise _native.EreduError(f"position {pos} outside the cache of {self.max_seq}")
-        n, L = _native, _native.lib()
         st = _stream()
         if self.fused:
             self._step_fused(pos, st)
-            return
+        else:
+            self._step_unfused(pos, st)
+
+    def _step_unfused(self, pos: Optional[int], st: int) -> None:
+        n, L = _native, _native.lib()
         bf = n.EQ_DTYPE_BF16
         H, F = self.hidden, self.ffn
         check(L.eq_embedding(self.x.data_ptr(), self.embed.data_ptr(), self.token.data_ptr(), 1, self.vocab, H, bf,
@@ -314,10 +373,7 @@ class LlamaDecoder:
             check(L.eq_rms_norm(self.h.data_ptr(), self.x.data_ptr(), resid, Lr.in_norm.data_ptr(), 1, H, self.eps,
                                 bf, st))
             self._group(self._qkv[li], 3, Lr.q, st)
-            check(L.eq_rope_attention_decode(
-                self.att.data_ptr(), self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                self.k_caches[li].data_ptr(), self.v_caches[li].data_ptr(), self.freqs.data_ptr(), pos, self.max_seq,
-                self.n_heads, self.n_kv_heads, HEAD_DIM, self.scale, bf, st))
+            self._attend(li, pos, st)
             self._linear(Lr.o, self.att, self.o, st)
             check(L.eq_rms_norm(self.h.data_ptr(), self.x.data_ptr(), self.o.data_ptr(), Lr.post_norm.data_ptr(), 1,
                                 H, self.eps, bf, st))

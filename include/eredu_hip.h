@@ -347,6 +347,27 @@ int eq_rope_attention_decode_noalloc(void* out, const void* q, const void* k_new
                                      int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
                                      int dtype, eq_stream_t stream);
 
+/* eq_rope_attention_decode at a position read from device memory when the
+ * kernel runs (pos: one int32 in device memory), so that one captured HIP
+ * graph decodes successive positions: the reference advances its cache
+ * offset every token (eredu/src/runtime/generation/streaming.rs:1038-1050,
+ * through Attention::attend, llama.rs:296-330).  Same shapes, rules, kernels
+ * and results as eq_rope_attention_decode at that position: the launch covers
+ * every 32-position chunk of max_seq and the chunks past the position end at
+ * once.  The chunk states live in the library workspace of `stream`, sized by
+ * max_seq (n_heads * ceil(max_seq / 32) * 520 bytes), so a capture needs an
+ * earlier call with this max_seq on that stream.  A position outside
+ * [0, max_seq) writes no cache row and gives zeros.  max_seq <= 131072. */
+int eq_rope_attention_decode_at(void* out, const void* q, const void* k_new, const void* v_new,
+                                void* k_cache, void* v_cache, const float* freqs, const int32_t* pos,
+                                int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
+                                int dtype, eq_stream_t stream);
+
+/* pos[0] += 1 on `stream` (pos: one int32 in device memory): the end of a
+ * decode step whose position lives on the device, the cache offset advance of
+ * the reference's token loop (streaming.rs:1038-1050). */
+int eq_advance_position(int32_t* pos, eq_stream_t stream);
+
 /* out[n] = silu(gate) * up, silu(x) = x * sigmoid(x), each op rounded to bf16
  * (Mlp::hidden, llama.rs:414-422; eredu/src/backend/mlx/nn/layers.rs:21).
  * n % 8 == 0, 16-byte aligned. */

@@ -28,7 +28,7 @@ def test_header_declares_the_boundary():
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
          "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
          "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc", "eq_gguf_convert_mxfp4",
-         "eq_gguf_embedding", "eq_gguf_grouped_linear"]
+         "eq_gguf_embedding", "eq_gguf_grouped_linear", "eq_rope_attention_decode_at", "eq_advance_position"]
     )
 
 
@@ -218,6 +218,17 @@ def test_decode_ops_reject_bad_arguments():
     _rejects(att(pos=64), "pos")
     _rejects(att(pos=-1), "pos")
     _rejects(att(dt=f32), "only bf16")
+    # attention at a device position: the same shape rules, the position pointer, max_seq
+    att_at = lambda **k: L.eq_rope_attention_decode_at(16, 16, 16, 16, 16, 16, 16, k.get("pos", 16),
+                                                        k.get("max_seq", 64), k.get("h", 32), k.get("kv", 8),
+                                                        k.get("d", 128), 0.088, k.get("dt", bf16), None)
+    _rejects(att_at(d=64), "head_dim")
+    _rejects(att_at(h=64, kv=8), "n_heads")
+    _rejects(att_at(pos=None), "null")
+    _rejects(att_at(max_seq=0), "max_seq")
+    _rejects(att_at(max_seq=131073), "131072")
+    _rejects(att_at(dt=f32), "only bf16")
+    _rejects(L.eq_advance_position(None, None), "null")
     # silu_mul, embedding, argmax
     _rejects(L.eq_silu_mul(16, 16, 16, 12, bf16, None), "multiple of 8")
     _rejects(L.eq_embedding(16, 16, 16, 70000, 100, 64, bf16, None), "n_tokens")

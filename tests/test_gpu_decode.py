@@ -90,6 +90,48 @@ def test_rope_attention_decode(cuda, n_heads, n_kv, pos):
     assert ok, f"max|err|/RMS = {worst:.3e}"
 
 
+@pytest.mark.parametrize("n_heads,n_kv,max_seq", [(32, 8, 1100), (4, 1, 1100), (8, 4, 4000), (32, 8, 64)])
+@pytest.mark.parametrize("pos", [0, 5, 31, 32, 33, 100, 1024, 2500])
+def test_rope_attention_decode_at_device_position(cuda, n_heads, n_kv, max_seq, pos):
+    """eq_rope_attention_decode_at: the position read from device memory by
+    the kernels, whose grid covers every chunk of max_seq.  Same oracle and
+    cache rules as the by-value entry point, and bit-equal to it; a position
+    outside the cache writes nothing and gives zeros."""
+    print(f"[case] attention at device pos heads={n_heads}/{n_kv} max_seq={max_seq} pos={pos}", flush=True)
+    seed = pos * 5 + n_heads + max_seq
+    q = randn_bits(n_heads * 128, seed)
+    kn = randn_bits(n_kv * 128, seed + 1)
+    vn = randn_bits(n_kv * 128, seed + 2)
+    kc = randn_bits((n_kv, max_seq, 128), seed + 3)
+    vc = randn_bits((n_kv, max_seq, 128), seed + 4)
+    freqs = D.llama3_rope_freqs(128, 500000.0)
+    scale = 1.0 / np.sqrt(128.0)
+    kcd, vcd = dev_bf16(kc), dev_bf16(vc)
+    pos_d = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    out = E.rope_attention_decode_at(dev_bf16(q), dev_bf16(kn), dev_bf16(vn), kcd, vcd,
+                                     torch.from_numpy(freqs).cuda(), pos_d, n_heads, n_kv, scale)
+    torch.cuda.synchronize()
+    got_k, got_v = host_bits16(kcd), host_bits16(vcd)
+    if pos >= max_seq:
+        assert np.array_equal(got_k, kc) and np.array_equal(got_v, vc)
+        assert not host_f32(out).any()
+        return
+    ref, kc_ref, vc_ref = D.attention_decode(q, kn, vn, kc, vc, freqs, pos, n_heads, n_kv, scale)
+    assert np.array_equal(got_v, vc_ref)
+    mask = np.ones(max_seq, dtype=bool)
+    mask[pos] = False
+    assert np.array_equal(got_k[:, mask], kc[:, mask])
+    rot = D.rope(D.bits_to_f64(kn).reshape(n_kv, 128), pos, freqs)
+    assert within_ulps(got_k[:, pos], rot, 1)
+    ok, worst, rms = orc.matmul_within_tolerance(host_f32(out).reshape(n_heads, 128), ref, out_is_bf16=True)
+    assert ok, f"max|err|/RMS = {worst:.3e}"
+    kc2, vc2 = dev_bf16(kc), dev_bf16(vc)
+    out2 = E.rope_attention_decode(dev_bf16(q), dev_bf16(kn), dev_bf16(vn), kc2, vc2,
+                                   torch.from_numpy(freqs).cuda(), pos, n_heads, n_kv, scale)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(kcd, kc2) and torch.equal(vcd, vc2)
+
+
 def test_attention_matches_torch_sdpa(cuda):
     """Cross-check with torch's own attention in f32 on the rotated inputs."""
     n_heads, n_kv, pos, max_seq = 32, 8, 777, 1024
@@ -231,6 +273,57 @@ def test_decode_step_graph_replay(cuda, fused):
         toks2.append(int(dec2.token.item()))
         assert torch.equal(dec.logits, dec2.logits)
     assert toks == toks2
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_one_graph_decodes_successive_positions(cuda, fused):
+    """step_device() reads the position from device memory and advances it:
+    one captured graph, replayed three times from position p, gives the
+    tokens and logits of eager device-position steps at p, p + 1, p + 2, and
+    the same caches; the first of those steps is also checked against the
+    oracle at p."""
+    host, dec, kcs, vcs = tiny_model(seed=4, fused=fused)
+    _, dec2, _, _ = tiny_model(seed=4, fused=fused)
+    p0 = 17
+    for d in (dec, dec2):
+        d.token.fill_(9)
+        d.set_position(p0)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        # one eager step first (workspace and counters of this stream), at a
+        # position the replays overwrite; then back to p0
+        dec.step_device()
+        torch.cuda.synchronize()
+        dec.token.fill_(9)
+        dec.set_position(p0)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            dec.step_device()
+    torch.cuda.synchronize()
+    assert int(dec.position.item()) == p0  # capture runs nothing
+    kref = [k.copy() for k in kcs]
+    vref = [v.copy() for v in vcs]
+    for i in range(3):
+        print(f"[case] one-graph decode fused={fused} pos={p0 + i}", flush=True)
+        token_in = int(dec2.token.item())
+        with torch.cuda.stream(st):
+            g.replay()
+        torch.cuda.synchronize()
+        dec2.step_device()
+        torch.cuda.synchronize()
+        assert int(dec.position.item()) == p0 + i + 1 == int(dec2.position.item())
+        assert torch.equal(dec.logits, dec2.logits), f"replay {i}"
+        assert int(dec.token.item()) == int(dec2.token.item())
+        if i == 0:
+            logits_ref, _ = D.decode_step(host, token_in, p0, kref, vref)
+            got = host_f32(dec.logits)
+            rms = np.sqrt(np.mean(logits_ref ** 2))
+            err = np.abs(got - logits_ref)
+            assert np.all(err <= 2e-2 * rms + 0.5 * ulp_bf16(logits_ref)), f"max|err|/RMS = {err.max() / rms:.3e}"
+    for a, b in zip(dec.k_caches + dec.v_caches, dec2.k_caches + dec2.v_caches):
+        assert torch.equal(a, b)
 
 
 def _prologue_call(problems, lins, pro):
