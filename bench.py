@@ -123,11 +123,20 @@ def _lib():
     return _native
 
 
+def _dtype_code(t):
+    import torch
+
+    n = _lib()
+    return n.EQ_DTYPE_F16 if t.dtype == torch.float16 else n.EQ_DTYPE_BF16
+
+
 def run_one(lin, x, y, stream, bits=BITS, gs=GS):
+    """One eq_quantized_matmul; activation and scale types from the tensors
+    (bf16 or f16)."""
     n = _lib()
     n.check(n.lib().eq_quantized_matmul(
         y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(), x.shape[0], lin.N, lin.K,
-        True, gs, bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, stream))
+        True, gs, bits, b"affine", _dtype_code(x), _dtype_code(lin.s), stream))
 
 
 def run_group(lins, xs, ys, stream, bits=BITS, gs=GS):
@@ -137,16 +146,17 @@ def run_group(lins, xs, ys, stream, bits=BITS, gs=GS):
         arr[i] = n.QmmProblem(y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.s.data_ptr(), lin.b.data_ptr(),
                               lin.N, lin.K)
     n.check(n.lib().eq_quantized_matmul_batched(arr, len(lins), xs[0].shape[0], True, gs, bits, b"affine",
-                                                n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, stream))
+                                                _dtype_code(xs[0]), _dtype_code(lins[0].s), stream))
 
 
-def decode_step_fn(layers, M, groups):
+def decode_step_fn(layers, M, groups, act_dtype=None):
     """Step of all layers' projections at batch M; groups=None issues one launch per
     projection, else one grouped launch per listed set.  Returns (fn, launches)."""
     import torch
 
-    xs = {K: torch.randn((M, K), device="cuda").to(torch.bfloat16) for K in (HIDDEN, FFN)}
-    ys = {name: torch.empty((M, N), device="cuda", dtype=torch.bfloat16) for name, N, K in LAYER_SHAPES}
+    dt = torch.bfloat16 if act_dtype is None else act_dtype
+    xs = {K: torch.randn((M, K), device="cuda").to(dt) for K in (HIDDEN, FFN)}
+    ys = {name: torch.empty((M, N), device="cuda", dtype=dt) for name, N, K in LAYER_SHAPES}
     Ks = {name: K for name, N, K in LAYER_SHAPES}
 
     def step(stream):
@@ -162,8 +172,8 @@ def decode_step_fn(layers, M, groups):
     return step, launches
 
 
-def bench_decode(layers, M, groups, steps, warmup):
-    step, launches = decode_step_fn(layers, M, groups)
+def bench_decode(layers, M, groups, steps, warmup, act_dtype=None):
+    step, launches = decode_step_fn(layers, M, groups, act_dtype)
     ms = Timer(step).ms_per_replay(steps, warmup)
     nbytes = len(layers) * sum(qmv_bytes(M, N, K) for _, N, K in LAYER_SHAPES)
     return ms, nbytes, launches
@@ -216,6 +226,47 @@ def bench_qmm(steps, warmup, bits_list=(4, 8), Ms=(128, 512, 2048)):
                                                 "frac_mfma": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
             del lins
             torch.cuda.empty_cache()
+    return out
+
+
+class F16View:
+    """A layer's packed codes with its scales and biases as f16 (an f16 model's
+    parameters), for the f16-activation figures."""
+
+    def __init__(self, lin):
+        import torch
+
+        self.N, self.K, self.w = lin.N, lin.K, lin.w
+        self.s, self.b = lin.s.to(torch.float16), lin.b.to(torch.float16)
+
+
+def bench_f16(layers, steps, warmup):
+    """f16 activations with f16 scales/biases on the same kernels as bf16: the
+    grouped decode step at M = 1 and 8 over the 32 layers' codes,
+    and prefill qmm at M = 512 for the four shapes (configs[2], 4-bit g64)."""
+    import torch
+
+    out = {}
+    f16layers = [{name: F16View(L[name]) for name, _, _ in LAYER_SHAPES} for L in layers]
+    for M in (1, 8):
+        ms, nb, launches = bench_decode(f16layers, M, DECODE_GROUPS, max(steps // 2, 5), warmup, torch.float16)
+        out[f"decode_M{M}_grouped"] = {"ms": round(ms, 4), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                                       "launches": launches}
+    del f16layers
+    torch.cuda.empty_cache()
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    M = 512
+    for (name, N, K) in [("q/o", HIDDEN, HIDDEN), ("k/v", KV, HIDDEN), ("gate/up", FFN, HIDDEN), ("down", HIDDEN, FFN)]:
+        lins = [F16View(Linear(N, K, gen)) for _ in range(rotation(qmv_bytes(0, N, K), 4))]
+        x = torch.randn((M, K), device="cuda").to(torch.float16)
+        y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+        t = Timer(lambda st: [run_one(l, x, y, st) for l in lins])
+        ms = t.ms_per_replay(max(steps // 4, 5), warmup) / len(lins)
+        tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out[f"qmm M{M} {N}x{K}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
+                                    "frac_mfma": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
+        del lins
+        torch.cuda.empty_cache()
     return out
 
 
@@ -1003,6 +1054,8 @@ def main():
         log("[bench] per-shape qmv")
         detail["qmv_M1_per_shape"] = bench_per_shape(layers, 1, args.steps, args.warmup)
         detail["qmv_M8_per_shape"] = bench_per_shape(layers, 8, args.steps, args.warmup)
+        log("[bench] f16 activations")
+        detail["f16_activations"] = bench_f16(layers, args.steps, args.warmup)
 
     cpu = None
     if not args.no_cpu:

@@ -370,22 +370,24 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
                             st);
     }
 
-    const bool mfma_ok = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
+    // matrix-core kernels: bf16 or f16 activations (the output in the same type)
+    const bool x16 = x_dtype == EQ_DTYPE_BF16 || x_dtype == EQ_DTYPE_F16;
+    const bool mfma_ok = transpose && x16 && (bits == 4 || bits == 8) &&
                          (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && aligned(x, 16) &&
                          aligned(w, 16);
     if (mfma_ok && M <= 16 && N % 16 == 0) {
         if (launch_qmv_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
-                            w, scales, biases, int(M), int(N), int(K), st))
+                            w, scales, biases, int(M), int(N), int(K), st, x_dtype))
             return check_launch("quantized_matmul (qmv)");
     }
     // prefill on the matrix cores: 4/8-bit codes directly, 2/3/5/6-bit codes
     // re-packed to bytes slice by slice in the workspace
-    const bool odd_ok = transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 2 || bits == 3 || bits == 5 || bits == 6) &&
+    const bool odd_ok = transpose && x16 && (bits == 2 || bits == 3 || bits == 5 || bits == 6) &&
                         (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && aligned(x, 16) &&
                         aligned(w, 4);
     if ((mfma_ok || odd_ok) && M > 16 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8)) {
         if (launch_qmm_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
-                            w, scales, biases, int(M), int(N), int(K), ws, st))
+                            w, scales, biases, int(M), int(N), int(K), ws, st, -1, x_dtype))
             return take_refusal() ? 1 : check_launch("quantized_matmul (qmm)");
     }
     if (transpose && x_dtype == EQ_DTYPE_BF16 && M <= 16 &&
@@ -493,8 +495,8 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     // Decode-shaped groups go to one grouped launch per kQmvMaxProblems problems.
-    bool grouped = qm == kModeAffine && transpose && x_dtype == EQ_DTYPE_BF16 && (bits == 4 || bits == 8) &&
-                   (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && M <= 16;
+    bool grouped = qm == kModeAffine && transpose && (x_dtype == EQ_DTYPE_BF16 || x_dtype == EQ_DTYPE_F16) &&
+                   (bits == 4 || bits == 8) && (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && M <= 16;
     std::vector<QmvSpec> specs;
     for (int i = 0; i < count && grouped; i++) {
         const eq_qmm_problem& p = problems[i];
@@ -502,7 +504,7 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
         specs.push_back(QmvSpec{static_cast<const uint16_t*>(p.x), p.w, p.scales, p.biases, static_cast<uint16_t*>(p.y),
                                 int(p.N), int(p.K), int(p.N)});
     }
-    if (grouped && launch_qmv_batched(bits, group_size, scale_dtype, specs.data(), count, int(M), st))
+    if (grouped && launch_qmv_batched(bits, group_size, scale_dtype, specs.data(), count, int(M), st, x_dtype))
         return check_launch("quantized_matmul_batched (qmv)");
     // Otherwise one call per problem (same results: every problem runs the
     // same kernels either way).

@@ -49,9 +49,11 @@ struct QmvSpec {
 // launch_qmv_batched takes several sharing M, bits, group size and scale type
 // and returns false, launching nothing, if the grouped path cannot take them
 // all (the caller then issues them one by one).
+// x_dtype (EQ_DTYPE_BF16 or EQ_DTYPE_F16) is the activation type, which y shares.
 bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
-                     const void* s, const void* b, int M, int N, int K, hipStream_t st);
-bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st);
+                     const void* s, const void* b, int M, int N, int K, hipStream_t st, int x_dtype = EQ_DTYPE_BF16);
+bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st,
+                        int x_dtype = EQ_DTYPE_BF16);
 // Decode for the other widths (qmv_any.hip): transpose, bf16 x, M <= 16, bits
 // 2..8, group 16 or a multiple of 32, K a multiple of 32; false, launching
 // nothing, when it does not take the problem.
@@ -501,7 +503,7 @@ int gather_qmm_launch(void* y, const void* x, const uint32_t* w, const void* sca
 // only when it is N).
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st,
-                     int ldy = -1);
+                     int ldy = -1, int x_dtype = EQ_DTYPE_BF16);
 
 // The same two launchers for MXFP4 codes (E8M0 scale bytes, no biases).
 bool launch_qmm_mfma_mxfp4(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint8_t* s, int M, int N, int K,

@@ -57,30 +57,56 @@ constexpr int kQmmThreads = 512;        // two K-groups of 4 waves
 constexpr int kLdsBuf = kBM * kBK * 2;  // bytes per activation buffer
 constexpr int kRing = 3;                // slots of the load rings (codes in registers, activations in LDS)
 
-// 8 codes in k order -> 4 registers of bf16 pairs (s*q + b).
-template <int BITS>
-__device__ __forceinline__ q_u32x4 dequant8(const uint32_t* words, float s, float b);
+typedef _Float16 q_f16x8 __attribute__((ext_vector_type(8)));
+
+// Activation types of the prefill kernel: the 16-bit type both MFMA operands
+// take (the dequantized weights are rounded to it), the MFMA and the output.
+template <typename XT>
+struct QmmAct;
 template <>
-__device__ __forceinline__ q_u32x4 dequant8<4>(const uint32_t* words, float s, float b) {
-    const uint32_t w = words[0];
-    uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;  // codes 2i | 2i+1 in byte i
-    // (opaque to the optimiser, so that each code converts with one
-    // v_cvt_f32_ubyte{0..3} instead of a bit-field extract plus a convert)
-    asm volatile("" : "+v"(lo), "+v"(hi));
-    q_u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        r[i] = pack_bf16x2(fmaf(s, float((lo >> (8 * i)) & 0xffu), b), fmaf(s, float((hi >> (8 * i)) & 0xffu), b));
-    return r;
-}
+struct QmmAct<BF16T> {
+    __device__ static __forceinline__ uint32_t pack(float a, float b) { return pack_bf16x2(a, b); }
+    __device__ static __forceinline__ f32x16 mfma(q_u32x4 wq, bf16x8 a, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wq), a, c, 0, 0, 0);
+    }
+    __device__ static __forceinline__ uint16_t out(float v) { return uint16_t(f32_to_bf16_bits(v)); }
+};
 template <>
-__device__ __forceinline__ q_u32x4 dequant8<8>(const uint32_t* words, float s, float b) {
+struct QmmAct<F16T> {
+    // two f32 -> one word of f16 (a low), round to nearest even (v_cvt_pk_f16_f32)
+    __device__ static __forceinline__ uint32_t pack(float a, float b) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+    }
+    __device__ static __forceinline__ f32x16 mfma(q_u32x4 wq, bf16x8 a, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(q_f16x8, wq), __builtin_bit_cast(q_f16x8, a),
+                                                      c, 0, 0, 0);
+    }
+    __device__ static __forceinline__ uint16_t out(float v) { return uint16_t(f32_to_f16_bits(v)); }
+};
+
+// 8 codes in k order -> 4 registers of 16-bit pairs (s*q + b) in XT.
+template <int BITS, typename XT = BF16T>
+__device__ __forceinline__ q_u32x4 dequant8(const uint32_t* words, float s, float b) {
     q_u32x4 r;
+    if constexpr (BITS == 4) {
+        const uint32_t w = words[0];
+        uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;  // codes 2i | 2i+1 in byte i
+        // (opaque to the optimiser, so that each code converts with one
+        // v_cvt_f32_ubyte{0..3} instead of a bit-field extract plus a convert)
+        asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t w = words[i >> 1];
-        const int sh = (i & 1) * 16;
-        r[i] = pack_bf16x2(fmaf(s, float((w >> sh) & 0xffu), b), fmaf(s, float((w >> (sh + 8)) & 0xffu), b));
+        for (int i = 0; i < 4; i++)
+            r[i] = QmmAct<XT>::pack(fmaf(s, float((lo >> (8 * i)) & 0xffu), b),
+                                    fmaf(s, float((hi >> (8 * i)) & 0xffu), b));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = words[i >> 1];
+            const int sh = (i & 1) * 16;
+            r[i] = QmmAct<XT>::pack(fmaf(s, float((w >> sh) & 0xffu), b), fmaf(s, float((w >> (sh + 8)) & 0xffu), b));
+        }
     }
     return r;
 }
@@ -147,7 +173,7 @@ struct QmmArgs {
 // block and step, which touch one cache line per row each, a lane loads the
 // scales and biases of 6 consecutive groups (3 steps of each K-group) with
 // one 12-byte load each.
-template <int BITS, int GS, typename ST, bool SPLIT, bool PW>
+template <int BITS, int GS, typename ST, bool SPLIT, bool PW, typename XT = BF16T>
 __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void qmm_mfma_kernel(
     const QmmArgs args) {
     // Activation ring: three buffers per K-group.  Separate arrays, so that
@@ -157,6 +183,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     constexpr bool MX = __is_same(ST, E8M0T);
     constexpr uint32_t PB = MX ? 1u : 2u;  // bytes per scale / bias
     static_assert(!MX || (BITS == 4 && GS == 32 && !PW), "MXFP4: 4-bit codes, group 32");
+    static_assert(!MX || std::is_same<XT, BF16T>::value, "MXFP4 prefill takes bf16 activations");
     const int N = args.N, K = args.K, G = K / GS;
     int M = args.M;
 
@@ -325,8 +352,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
                 const float b1 = GS == 16 ? qmm_param<ST>(bbits[j] >> 16) : b0;
 #pragma unroll
                 for (int t = 0; t < 4; t++)
-                    bq[j][t] = dequant8<BITS>(reinterpret_cast<const uint32_t*>(&S.w[j][0]) + t * BITS / 4,
-                                              t < 2 ? s0 : s1, t < 2 ? b0 : b1);
+                    bq[j][t] = dequant8<BITS, XT>(reinterpret_cast<const uint32_t*>(&S.w[j][0]) + t * BITS / 4,
+                                                  t < 2 ? s0 : s1, t < 2 ? b0 : b1);
             }
         }
         const char* base = buf + gofs;
@@ -339,9 +366,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
             for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bq[j][t]), a[mi],
-                                                                         acc[mi][j], 0, 0, 0);
+                for (int j = 0; j < 2; j++) acc[mi][j] = QmmAct<XT>::mfma(bq[j][t], a[mi], acc[mi][j]);
         }
     };
 
@@ -438,7 +463,7 @@ done:
                     if constexpr (SPLIT) {
                         *reinterpret_cast<f32x4*>(args.ws + (int64_t(split) * M + m) * N + n) = v;
                     } else {
-                        const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
+                        const uint32_t lo = QmmAct<XT>::pack(v[0], v[1]), hi = QmmAct<XT>::pack(v[2], v[3]);
                         *reinterpret_cast<uint2*>(yp + int64_t(m) * args.ldy + n) = make_uint2(lo, hi);
                     }
                 }
@@ -450,6 +475,7 @@ done:
 // y[m, n] (row stride ldy) = bf16(sum over splits of ws[split, m, n]), the
 // partials dense [splits, M, N] f32; four outputs per thread (vec: y 8-byte
 // aligned and N, ldy multiples of 4, so the four stay in one row).
+template <typename XT = BF16T>
 __global__ __launch_bounds__(256) void qmm_split_reduce(uint16_t* __restrict__ y, const float* __restrict__ ws,
                                                          int64_t mn, int64_t n, int64_t ldy, int splits, bool vec) {
     typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -464,14 +490,13 @@ __global__ __launch_bounds__(256) void qmm_split_reduce(uint16_t* __restrict__ y
         const int64_t row = i / n, col = i - row * n;
         typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
         *reinterpret_cast<u16x4*>(y + row * ldy + col) =
-            u16x4{uint16_t(f32_to_bf16_bits(v[0])), uint16_t(f32_to_bf16_bits(v[1])),
-                  uint16_t(f32_to_bf16_bits(v[2])), uint16_t(f32_to_bf16_bits(v[3]))};
+            u16x4{QmmAct<XT>::out(v[0]), QmmAct<XT>::out(v[1]), QmmAct<XT>::out(v[2]), QmmAct<XT>::out(v[3])};
     } else {
         for (int64_t e = i; e < mn && e < i + 4; e++) {
             float v = ws[e];
             for (int s = 1; s < splits; s++) v += ws[int64_t(s) * mn + e];
             const int64_t row = e / n;
-            y[row * ldy + (e - row * n)] = uint16_t(f32_to_bf16_bits(v));
+            y[row * ldy + (e - row * n)] = QmmAct<XT>::out(v);
         }
     }
 }
@@ -485,7 +510,7 @@ static int qmm_cu_count() {
 }
 
 // One launch (plus the split reduction): every buffer below 2^31 bytes.
-template <int BITS, int GS, typename ST>
+template <int BITS, int GS, typename ST, typename XT = BF16T>
 static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
                              int M, int N, int K, bool may_split, const WsSource* src, hipStream_t st) {
     QmmArgs a{};
@@ -539,14 +564,14 @@ static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
     const bool pw = GS == 64 && (K / GS) % 2 == 0 && a.cps % 2 == 0;
     const dim3 grid(unsigned(tiles * splits)), block(kQmmThreads);
     if (splits == 1) {
-        if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64><<<grid, block, 0, st>>>(a);
-        else qmm_mfma_kernel<BITS, GS, ST, false, false><<<grid, block, 0, st>>>(a);
+        if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64, XT><<<grid, block, 0, st>>>(a);
+        else qmm_mfma_kernel<BITS, GS, ST, false, false, XT><<<grid, block, 0, st>>>(a);
         return true;
     }
-    if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64><<<grid, block, 0, st>>>(a);
-    else qmm_mfma_kernel<BITS, GS, ST, true, false><<<grid, block, 0, st>>>(a);
+    if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64, XT><<<grid, block, 0, st>>>(a);
+    else qmm_mfma_kernel<BITS, GS, ST, true, false, XT><<<grid, block, 0, st>>>(a);
     const int64_t mn = int64_t(M) * N;
-    qmm_split_reduce<<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(
+    qmm_split_reduce<XT><<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(
         y, a.ws, mn, N, ldy, splits, aligned(y, 8) && N % 4 == 0 && ldy % 4 == 0);
     return true;
 }
@@ -556,7 +581,7 @@ static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
 // matrix that large in row pieces (multiples of the 128-row tile).
 // y's row stride is ldy (N when negative); split K only when y is one whole
 // piece of stride N.
-template <int BITS, int GS, typename ST>
+template <int BITS, int GS, typename ST, typename XT = BF16T>
 static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b, int M,
                          int N, int K, const WsSource* src, hipStream_t st, int ldy = -1) {
     if (ldy < 0) ldy = N;
@@ -576,21 +601,21 @@ static void launch_qmm_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
             const char* sp = static_cast<const char*>(s) + n0 * G * PB;
             const char* bp = b ? static_cast<const char*>(b) + n0 * G * PB : nullptr;
             // (only a whole problem splits K, so a refusal comes before any launch)
-            if (!launch_qmm_piece<BITS, GS, ST>(y + m0 * ldy + n0, ldy, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp,
+            if (!launch_qmm_piece<BITS, GS, ST, XT>(y + m0 * ldy + n0, ldy, x + m0 * K, w + n0 * (row_bytes / 4), sp, bp,
                                                 mc, nc, K, whole, src, st))
                 return;
         }
     }
 }
 
-template <int BITS, typename ST>
+template <int BITS, typename ST, typename XT = BF16T>
 static bool launch_qmm_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
                           int M, int N, int K, const WsSource* src, hipStream_t st, int ldy = -1) {
     switch (gs) {
-    case 16: launch_qmm_t<BITS, 16, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
-    case 32: launch_qmm_t<BITS, 32, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
-    case 64: launch_qmm_t<BITS, 64, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
-    case 128: launch_qmm_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
+    case 16: launch_qmm_t<BITS, 16, ST, XT>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
+    case 32: launch_qmm_t<BITS, 32, ST, XT>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
+    case 64: launch_qmm_t<BITS, 64, ST, XT>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
+    case 128: launch_qmm_t<BITS, 128, ST, XT>(y, x, w, s, b, M, N, K, src, st, ldy); return true;
     default: return false;
     }
 }
@@ -778,7 +803,7 @@ __global__ __launch_bounds__(256) void qmm_codes_to_bytes(const uint32_t* __rest
     out[2 * u + 1] = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
-template <typename ST>
+template <typename ST, typename XT = BF16T>
 static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s,
                              const void* b, int M, int N, int K, const WsSource* src, hipStream_t st, int ldy = -1) {
     if (gs != 16 && gs != 32 && gs != 64 && gs != 128) return false;
@@ -832,10 +857,10 @@ static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, c
             parts = &none;
         }
         switch (gs) {
-        case 16: launch_qmm_t<8, 16, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
-        case 32: launch_qmm_t<8, 32, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
-        case 64: launch_qmm_t<8, 64, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
-        default: launch_qmm_t<8, 128, ST>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
+        case 16: launch_qmm_t<8, 16, ST, XT>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
+        case 32: launch_qmm_t<8, 32, ST, XT>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
+        case 64: launch_qmm_t<8, 64, ST, XT>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
+        default: launch_qmm_t<8, 128, ST, XT>(y + n0, x, w8, sp, bp, M, ncs, K, parts, st, ldy); break;
         }
     }
     return true;
@@ -843,18 +868,23 @@ static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, c
 
 bool launch_qmm_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
                      const void* s, const void* b, int M, int N, int K, const WsSource* ws, hipStream_t st,
-                     int ldy) {
-    if (bits == 4) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<4, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<4, F16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
-    } else if (bits == 8) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmm_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
-    } else if (bits == 2 || bits == 3 || bits == 5 || bits == 6) {
-        if (scale_dtype == EQ_DTYPE_BF16)
-            return launch_qmm_odd_t<BF16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st, ldy);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmm_odd_t<F16T>(bits, gs, y, x, w, s, b, M, N, K, ws, st, ldy);
-    }
+                     int ldy, int x_dtype) {
+    auto by_x = [&](auto stt) -> bool {
+        typedef decltype(stt) ST;
+        auto go = [&](auto xt) -> bool {
+            typedef decltype(xt) XT;
+            if (bits == 4) return launch_qmm_gs<4, ST, XT>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
+            if (bits == 8) return launch_qmm_gs<8, ST, XT>(gs, y, x, w, s, b, M, N, K, ws, st, ldy);
+            if (bits == 2 || bits == 3 || bits == 5 || bits == 6)
+                return launch_qmm_odd_t<ST, XT>(bits, gs, y, x, w, s, b, M, N, K, ws, st, ldy);
+            return false;
+        };
+        if (x_dtype == EQ_DTYPE_BF16) return go(BF16T{});
+        if (x_dtype == EQ_DTYPE_F16) return go(F16T{});
+        return false;
+    };
+    if (scale_dtype == EQ_DTYPE_BF16) return by_x(BF16T{});
+    if (scale_dtype == EQ_DTYPE_F16) return by_x(F16T{});
     return false;
 }
 

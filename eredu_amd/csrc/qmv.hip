@@ -42,19 +42,55 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Loop-invariant constants kept in VGPRs (opaque to the optimiser), so that
 // (p & mask) | bias compiles to one v_and_or_b32: on gfx9 a VOP3 instruction
-// takes no literal operands.
+// takes no literal operands.  The code images depend on the activation type
+// XT the MFMA multiplies in: bf16 0x43XX = 128 + XX (unit ulp for XX < 128),
+// f16 0x64XX = 1024 + XX (unit ulp for XX < 1024).
 struct UnpackConsts {
     uint32_t nib_mask;  // 0x000f000f
-    uint32_t bf16_128;  // 0x43004300: bf16 0x43XX = 128 + XX for XX < 128
-    uint32_t c43;       // 0x43434343 (uniform)
+    uint32_t bf16_128;  // 0x43004300 (bf16) or 0x64006400 (f16): the offset's image in both halves
+    uint32_t c43;       // 0x43434343 or 0x64646464 (uniform): its high byte in every byte
 };
+template <typename XT = BF16T>
 __device__ __forceinline__ UnpackConsts make_unpack_consts() {
     UnpackConsts c;
     asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(c.nib_mask));
-    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.bf16_128));
-    asm volatile("s_mov_b32 %0, 0x43434343" : "=s"(c.c43));
+    if constexpr (std::is_same<XT, F16T>::value) {
+        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.bf16_128));
+        asm volatile("s_mov_b32 %0, 0x64646464" : "=s"(c.c43));
+    } else {
+        asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.bf16_128));
+        asm volatile("s_mov_b32 %0, 0x43434343" : "=s"(c.c43));
+    }
     return c;
 }
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Activation types of the decode kernels: the offset the 16-bit code images
+// carry, the all-ones operand, the MFMA, and the output rounding.
+template <typename XT>
+struct QmvAct;
+template <>
+struct QmvAct<BF16T> {
+    static constexpr uint32_t kOnes = 0x3f803f80u;  // bf16 1.0 pairs
+    template <int BITS>
+    static constexpr float offset() { return BITS == 4 ? 128.f : 0.f; }  // 8-bit codes convert exactly
+    __device__ static __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static __forceinline__ uint16_t out(float v) { return uint16_t(f32_to_bf16_bits(v)); }
+};
+template <>
+struct QmvAct<F16T> {
+    static constexpr uint32_t kOnes = 0x3c003c00u;  // f16 1.0 pairs
+    template <int BITS>
+    static constexpr float offset() { return 1024.f; }  // 1024 + q, both widths
+    __device__ static __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    }
+    __device__ static __forceinline__ uint16_t out(float v) { return uint16_t(f32_to_f16_bits(v)); }
+};
 
 // 8 consecutive 4-bit codes (one word, LSB first) -> 8 bf16 values 128 + q,
 // in k order: pair i holds codes 2i (low half) and 2i+1 (high half).
@@ -86,6 +122,17 @@ __device__ __forceinline__ bf16x8 unpack8_bf16(uint32_t w0, uint32_t w1) {
         p[2 * h] = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
         p[2 * h + 1] = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
     }
+    return __builtin_bit_cast(bf16x8, p);
+}
+
+// 8 consecutive 8-bit codes (two words) -> 8 f16 values 1024 + q, exact, in k
+// order: four byte permutes against the constant 0x64 bytes.
+__device__ __forceinline__ bf16x8 unpack8_f16_offset1024(uint32_t w0, uint32_t w1, uint32_t c64) {
+    u32x4 p;
+    p[0] = __builtin_amdgcn_perm(c64, w0, 0x04010400u);  // [w0.b0, 64, w0.b1, 64]
+    p[1] = __builtin_amdgcn_perm(c64, w0, 0x04030402u);
+    p[2] = __builtin_amdgcn_perm(c64, w1, 0x04010400u);
+    p[3] = __builtin_amdgcn_perm(c64, w1, 0x04030402u);
     return __builtin_bit_cast(bf16x8, p);
 }
 
@@ -275,10 +322,13 @@ __device__ __forceinline__ float pick_param(const uint32_t* words, int base, int
 // (activations) and the codes wd, then acc += s * t + b' * xs with the span's
 // scale s and bias b of this lane's result group:
 // 4-bit: t = x . (128 + q), b' = b - 128 s; 8-bit: t = x . q, b' = b.
-template <int BITS, int GS, typename ST, int MREG, bool PERM = false>
+// With f16 activations (XT = F16T) the code images are f16 1024 + q for both
+// widths and t = x . (1024 + q), b' = b - 1024 s.
+template <int BITS, int GS, typename ST, int MREG, bool PERM = false, typename XT = BF16T>
 __device__ __forceinline__ void qmv_span(f32x4& acc, const bf16x8* xa, const u32x4& wd, float sc, float bi,
                                          const UnpackConsts& uc, bf16x8 ones) {
     typedef QmvGeom<BITS, GS> Geo;
+    typedef QmvAct<XT> A;
     f32x4 t4 = {0.f, 0.f, 0.f, 0.f};
     f32x4 xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -286,12 +336,15 @@ __device__ __forceinline__ void qmv_span(f32x4& acc, const bf16x8* xa, const u32
         bf16x8 bq;
         if (BITS == 4)
             bq = PERM ? unpack4_bf16_offset128_perm(wd[t], uc.c43) : unpack4_bf16_offset128(wd[t], uc);
+        else if constexpr (std::is_same<XT, F16T>::value)
+            bq = unpack8_f16_offset1024(wd[2 * t], wd[2 * t + 1], uc.c43);
         else
             bq = unpack8_bf16(wd[2 * t], wd[2 * t + 1]);
-        t4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], bq, t4, 0, 0, 0);
-        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], ones, xs, 0, 0, 0);
+        t4 = A::mfma(xa[t], bq, t4);
+        xs = A::mfma(xa[t], ones, xs);
     }
-    const float beff = BITS == 4 ? fmaf(-128.f, sc, bi) : bi;
+    constexpr float off = A::template offset<BITS>();
+    const float beff = off != 0.f ? fmaf(-off, sc, bi) : bi;
 #pragma unroll
     for (int r = 0; r < MREG; r++) acc[r] = fmaf(sc, t4[r], fmaf(beff, xs[r], acc[r]));
 }
@@ -311,7 +364,7 @@ __device__ __forceinline__ void qmv_params(const uint32_t* sw, const uint32_t* b
     }
 }
 
-template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC>
+template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC, typename XT = BF16T>
 __device__ __forceinline__ void qmv_compute(f32x4& acc, const QmvBlock<BITS, GS, NU, VEC>& b, int r_p,
                                             float bias_on, const UnpackConsts& uc, bf16x8 ones) {
     // Loads issued before this block stay before it (no load may be sunk
@@ -321,7 +374,7 @@ __device__ __forceinline__ void qmv_compute(f32x4& acc, const QmvBlock<BITS, GS,
     for (int u = 0; u < NU; u++) {
         float sc, bi;
         qmv_params<BITS, GS, ST, NU, VEC>(b.sw, b.bw, u, r_p, bias_on, sc, bi);
-        qmv_span<BITS, GS, ST, MREG>(acc, b.xa[u], b.wd[u], sc, bi, uc, ones);
+        qmv_span<BITS, GS, ST, MREG, false, XT>(acc, b.xa[u], b.wd[u], sc, bi, uc, ones);
     }
 }
 
@@ -332,7 +385,7 @@ __device__ __forceinline__ void qmv_compute(f32x4& acc, const QmvBlock<BITS, GS,
 // Occupancy target 2 waves per SIMD: the two register blocks of the
 // double-buffered span pipeline must both stay live (the default target of
 // higher occupancy makes the scheduler serialise the prefetch instead).
-template <int BITS, int GS, typename ST, int MREG, bool VEC>
+template <int BITS, int GS, typename ST, int MREG, bool VEC, typename XT>
 __global__ __launch_bounds__(64 * kQmvMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_mfma_kernel(
     uint16_t* __restrict__ y, const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases, int M, int N, int K, int ldy,
@@ -376,8 +429,9 @@ __global__ __launch_bounds__(64 * kQmvMaxWaves) __attribute__((amdgpu_waves_per_
     L.r_p = r_p;
     const float bias_on = biases ? 1.f : 0.f;
 
-    const UnpackConsts uc = make_unpack_consts();
-    u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const UnpackConsts uc = make_unpack_consts<XT>();
+    constexpr uint32_t k1 = QmvAct<XT>::kOnes;
+    u32x4 ones_bits = {k1, k1, k1, k1};
     const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_bits);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 
@@ -392,19 +446,19 @@ __global__ __launch_bounds__(64 * kQmvMaxWaves) __attribute__((amdgpu_waves_per_
         qmv_load<BITS, GS, U, VEC>(ba, L, j_begin);
         for (int i = 0; i + 1 < nblk; i += 2) {
             qmv_load<BITS, GS, U, VEC>(bb, L, j_begin + (i + 1) * U);
-            if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, ba, r_p, bias_on, uc, ones);
+            if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC, XT>(acc, ba, r_p, bias_on, uc, ones);
             else qmv_retire(ba);
             qmv_load<BITS, GS, U, VEC>(ba, L, j_begin + min(i + 2, nblk - 1) * U);
-            if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, bb, r_p, bias_on, uc, ones);
+            if (opaque_one()) qmv_compute<BITS, GS, ST, MREG, U, VEC, XT>(acc, bb, r_p, bias_on, uc, ones);
             else qmv_retire(bb);
         }
-        if (nblk & 1) qmv_compute<BITS, GS, ST, MREG, U, VEC>(acc, ba, r_p, bias_on, uc, ones);  // block nblk - 1
+        if (nblk & 1) qmv_compute<BITS, GS, ST, MREG, U, VEC, XT>(acc, ba, r_p, bias_on, uc, ones);  // block nblk - 1
     }
     // Remaining whole spans one at a time.
     for (int j = j_begin + nblk * U; j < j_full_end; j++) {
         QmvBlock<BITS, GS, 1, VEC> b1;
         qmv_load<BITS, GS, 1, VEC>(b1, L, j);
-        qmv_compute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, r_p, bias_on, uc, ones);
+        qmv_compute<BITS, GS, ST, MREG, 1, VEC, XT>(acc, b1, r_p, bias_on, uc, ones);
     }
     // A ragged last span (K % SPAN != 0): chunks past the end of the row see
     // zero activations (their codes belong to the next row, or read as zero
@@ -418,7 +472,7 @@ __global__ __launch_bounds__(64 * kQmvMaxWaves) __attribute__((amdgpu_waves_per_
         if (!g_in) T.soff = kOutOfRange;
         QmvBlock<BITS, GS, 1, VEC> b1;
         qmv_load<BITS, GS, 1, VEC>(b1, T, j);
-        qmv_compute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, r_p, bias_on, uc, ones);
+        qmv_compute<BITS, GS, ST, MREG, 1, VEC, XT>(acc, b1, r_p, bias_on, uc, ones);
     }
 
     // Result lane (n = ln, block kq) register r is row 4kq + r = (group block, m) with
@@ -440,7 +494,7 @@ __global__ __launch_bounds__(64 * kQmvMaxWaves) __attribute__((amdgpu_waves_per_
         const int m = t >> 4, n = t & 15;
         float v = 0.f;
         for (int i = 0; i < nwaves; i++) v += red[i][m][n];
-        y[int64_t(m) * ldy + n0 + n] = uint16_t(f32_to_bf16_bits(v));
+        y[int64_t(m) * ldy + n0 + n] = QmvAct<XT>::out(v);
     }
 }
 
@@ -577,7 +631,7 @@ __device__ __forceinline__ void qmv_wload_ring(QmvWBlock<BITS, GS, NU, true>& b,
 
 // A operands of span j0 + u are read from LDS at xa_t + j0 * xstep + u * SPAN * 2
 // (dead rows have xstep 0 and xa_t in the zero block, which covers NU spans).
-template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC>
+template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC, typename XT = BF16T>
 __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, GS, NU, VEC>& b, const char* smem,
                                              const uint32_t* xa_t, uint32_t xstep, int j0, int r_p,
                                              float bias_on, const UnpackConsts& uc, bf16x8 ones) {
@@ -594,7 +648,7 @@ __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, G
             xa[t] = *reinterpret_cast<const bf16x8*>(smem + xb[t] + u * Geo::SPAN * 2);
         float sc, bi;
         qmv_params<BITS, GS, ST, NU, VEC>(b.sw, b.bw, u, r_p, bias_on, sc, bi);
-        qmv_span<BITS, GS, ST, MREG, BITS == 4>(acc, xa, b.wd[u], sc, bi, uc, ones);
+        qmv_span<BITS, GS, ST, MREG, BITS == 4, XT>(acc, xa, b.wd[u], sc, bi, uc, ones);
     }
 }
 
@@ -803,7 +857,7 @@ __device__ __forceinline__ u32x4 qmv_norm8(const u32x4 a, const u32x4 w, float i
 // With PRO = 2 the staged row (K <= 2 * 16 * 64 * NW values) is one round of
 // at most 2 chunks per thread, kept in registers across the workgroup's sum
 // of squares.
-template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL, int PRO = 0>
+template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL, int PRO = 0, typename XT = BF16T>
 __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
     const QmvBatch batch) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -833,6 +887,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // order in which unpack4_bf16_offset128_perm delivers the codes.
     const int zero_lds = __builtin_amdgcn_readfirstlane(batch.zero_lds);
     static_assert(PRO == 0 || MREG == 1, "activation prologues are for one activation row");
+    static_assert(PRO == 0 || std::is_same<XT, BF16T>::value, "activation prologues are for bf16 rows");
     constexpr int NCH = PRO == 2 ? 2 : 8;  // chunks per thread and staging round
     u32x4 x2v[PRO != 0 ? NCH : 1];         // second input (up, residual); with PRO = 2 also the norm weight
     u32x4 nwv[PRO == 2 ? NCH : 1];
@@ -941,8 +996,9 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         *reinterpret_cast<u32x4*>(smem + zero_lds + threadIdx.x * 16) = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
 
-    const UnpackConsts uc = make_unpack_consts();
-    u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const UnpackConsts uc = make_unpack_consts<XT>();
+    constexpr uint32_t k1 = QmvAct<XT>::kOnes;
+    u32x4 ones_bits = {k1, k1, k1, k1};
     const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_bits);
     // A operand row ln is activation row ln % MB of group block ln / MB; live when
     // that block is the group of this lane's k-slots (block kq * P / 4).
@@ -965,7 +1021,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         for (int j = jc; j < V.j_full_end; j++) {
             QmvWBlock<BITS, GS, 1, VEC> b1;
             qmv_wload<BITS, GS, 1, VEC>(b1, V.L, j);
-            qmv_wcompute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, smem, V.xa_t, V.xstep, j, r_p, V.bias_on, uc, ones);
+            qmv_wcompute<BITS, GS, ST, MREG, 1, VEC, XT>(acc, b1, smem, V.xa_t, V.xstep, j, r_p, V.bias_on, uc, ones);
         }
         // Ragged last span: chunks past K see the zero block, groups past K
         // have zero scale and bias.
@@ -981,7 +1037,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
                 xt[t] = chunk_in ? V.xa_t[t] : uint32_t(batch.zero_lds) - uint32_t(j) * V.xstep;
             QmvWBlock<BITS, GS, 1, VEC> b1;
             qmv_wload<BITS, GS, 1, VEC>(b1, T, j);
-            qmv_wcompute<BITS, GS, ST, MREG, 1, VEC>(acc, b1, smem, xt, V.xstep, j, r_p, V.bias_on, uc, ones);
+            qmv_wcompute<BITS, GS, ST, MREG, 1, VEC, XT>(acc, b1, smem, xt, V.xstep, j, r_p, V.bias_on, uc, ones);
         }
         }
         // Fold the P group blocks, then combine the waves through LDS (two
@@ -1011,7 +1067,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             float v = 0.f;
 #pragma unroll
             for (int i = 0; i < NW; i++) v += slot[(i * M + m) * 16 + n];
-            pr.y[int64_t(m) * pr.ldy + V.n0 + n] = uint16_t(f32_to_bf16_bits(v));
+            pr.y[int64_t(m) * pr.ldy + V.n0 + n] = QmvAct<XT>::out(v);
         }
         iter++;
         acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1034,7 +1090,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             ring_load(ring[(d + D - 1) % D]);
             qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
             if (opaque_one()) {
-                qmv_wcompute<BITS, GS, ST, MREG, U, VEC>(acc, ring[d], smem, V.xa_t, V.xstep, jc, r_p, V.bias_on, uc,
+                qmv_wcompute<BITS, GS, ST, MREG, U, VEC, XT>(acc, ring[d], smem, V.xa_t, V.xstep, jc, r_p, V.bias_on, uc,
                                                           ones);
             } else {
                 qmv_retire(ring[d]);
@@ -1053,7 +1109,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     }
 }
 
-template <int BITS, int GS, typename ST, bool VEC>
+template <int BITS, int GS, typename ST, bool VEC, typename XT>
 static void launch_qmv_v(uint16_t* y, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                          int M, int N, int K, int ldy, int spw, int waves, hipStream_t st) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -1065,9 +1121,9 @@ static void launch_qmv_v(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
         uint16_t* yc = y + int64_t(m0) * ldy;
         const uint16_t* xc = x + int64_t(m0) * K;
         if (mc == 1)
-            qmv_mfma_kernel<BITS, GS, ST, 1, VEC><<<grid, block, 0, st>>>(yc, xc, w, s, b, mc, N, K, ldy, spw);
+            qmv_mfma_kernel<BITS, GS, ST, 1, VEC, XT><<<grid, block, 0, st>>>(yc, xc, w, s, b, mc, N, K, ldy, spw);
         else
-            qmv_mfma_kernel<BITS, GS, ST, 4, VEC><<<grid, block, 0, st>>>(yc, xc, w, s, b, mc, N, K, ldy, spw);
+            qmv_mfma_kernel<BITS, GS, ST, 4, VEC, XT><<<grid, block, 0, st>>>(yc, xc, w, s, b, mc, N, K, ldy, spw);
     }
 }
 
@@ -1158,7 +1214,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     return true;
 }
 
-template <int BITS, int GS, typename ST>
+template <int BITS, int GS, typename ST, typename XT = BF16T>
 static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
     auto go = [&](auto kernel) {
         // (a refusal surfaces as a launch error)
@@ -1168,27 +1224,27 @@ static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
         kernel<<<dim3(unsigned(plan.grid)), dim3(64 * plan.waves), size_t(plan.lds), st>>>(plan.B);
     };
     if (plan.B.M == 1) {
-        if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 1, true, false>);
-        else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true, true>);
-        else go(qmv_lds_kernel<BITS, GS, ST, 1, false, true>);
+        if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 1, true, false, 0, XT>);
+        else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true, true, 0, XT>);
+        else go(qmv_lds_kernel<BITS, GS, ST, 1, false, true, 0, XT>);
     } else {
-        if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 4, true, false>);
-        else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true, true>);
-        else go(qmv_lds_kernel<BITS, GS, ST, 4, false, true>);
+        if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 4, true, false, 0, XT>);
+        else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true, true, 0, XT>);
+        else go(qmv_lds_kernel<BITS, GS, ST, 4, false, true, 0, XT>);
     }
 }
 
-template <int BITS, int GS, typename ST>
+template <int BITS, int GS, typename ST, typename XT>
 static bool launch_qmv_lds(const QmvSpec* specs, int count, int M, hipStream_t st) {
     QmvLdsPlan plan;
     if (!plan_qmv_lds<BITS, GS, ST>(specs, count, M, plan)) return false;
-    run_qmv_lds<BITS, GS, ST>(plan, st);
+    run_qmv_lds<BITS, GS, ST, XT>(plan, st);
     return true;
 }
 
 // Grouped decode launch: problems in groups of kQmvMaxProblems, activation
 // rows in chunks of MB; every launch is planned before any is issued.
-template <int BITS, int GS, typename ST>
+template <int BITS, int GS, typename ST, typename XT>
 static bool launch_qmv_group_t(const QmvSpec* specs, int count, int M, hipStream_t st) {
     typedef QmvGeom<BITS, GS> Geo;
     std::vector<QmvLdsPlan> plans;
@@ -1206,11 +1262,11 @@ static bool launch_qmv_group_t(const QmvSpec* specs, int count, int M, hipStream
             if (!plan_qmv_lds<BITS, GS, ST>(chunk, n, mc, plans.back())) return false;
         }
     }
-    for (const QmvLdsPlan& plan : plans) run_qmv_lds<BITS, GS, ST>(plan, st);
+    for (const QmvLdsPlan& plan : plans) run_qmv_lds<BITS, GS, ST, XT>(plan, st);
     return true;
 }
 
-template <int BITS, int GS, typename ST>
+template <int BITS, int GS, typename ST, typename XT>
 static void launch_qmv_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* sv, const void* bv, int M,
                          int N, int K, hipStream_t st) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -1220,7 +1276,7 @@ static void launch_qmv_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
     for (; m0 < M; m0 += Geo::MB) {
         const int mc = M - m0 < Geo::MB ? M - m0 : Geo::MB;
         const QmvSpec q{x + int64_t(m0) * K, w, sv, bv, y + int64_t(m0) * N, N, K, N};
-        if (!launch_qmv_lds<BITS, GS, ST>(&q, 1, mc, st)) break;
+        if (!launch_qmv_lds<BITS, GS, ST, XT>(&q, 1, mc, st)) break;
     }
     if (m0 >= M) return;
     x += int64_t(m0) * K;
@@ -1252,45 +1308,59 @@ static void launch_qmv_t(uint16_t* y, const uint16_t* x, const uint32_t* w, cons
         const uint16_t* bc = b ? b + n0 * G : nullptr;
         // y rows are strided by N; a row chunk writes columns [n0, n0 + nc) of y.
         if (vec)
-            launch_qmv_v<BITS, GS, ST, true>(y + n0, x, wc, sc, bc, M, nc, K, N, spw, waves, st);
+            launch_qmv_v<BITS, GS, ST, true, XT>(y + n0, x, wc, sc, bc, M, nc, K, N, spw, waves, st);
         else
-            launch_qmv_v<BITS, GS, ST, false>(y + n0, x, wc, sc, bc, M, nc, K, N, spw, waves, st);
+            launch_qmv_v<BITS, GS, ST, false, XT>(y + n0, x, wc, sc, bc, M, nc, K, N, spw, waves, st);
         if (N - n0 <= rows_per_launch) break;
     }
 }
 
-template <int BITS, typename ST>
+template <int BITS, typename ST, typename XT>
 static bool launch_qmv_gs(int gs, uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
                           int M, int N, int K, hipStream_t st) {
     switch (gs) {
-    case 32: launch_qmv_t<BITS, 32, ST>(y, x, w, s, b, M, N, K, st); return true;
-    case 64: launch_qmv_t<BITS, 64, ST>(y, x, w, s, b, M, N, K, st); return true;
-    case 128: launch_qmv_t<BITS, 128, ST>(y, x, w, s, b, M, N, K, st); return true;
+    case 32: launch_qmv_t<BITS, 32, ST, XT>(y, x, w, s, b, M, N, K, st); return true;
+    case 64: launch_qmv_t<BITS, 64, ST, XT>(y, x, w, s, b, M, N, K, st); return true;
+    case 128: launch_qmv_t<BITS, 128, ST, XT>(y, x, w, s, b, M, N, K, st); return true;
     default: return false;
     }
 }
 
-// Entry used by the dispatcher (api.hip).  Preconditions checked there:
-// x bf16, transpose, 1 <= M <= 16, N % 16 == 0, K % gs == 0, 16-byte aligned
-// x and weight pointers, scale dtype bf16 or f16.
-bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
-                     const void* s, const void* b, int M, int N, int K, hipStream_t st) {
-    if (bits == 4) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_gs<4, BF16T>(gs, y, x, w, s, b, M, N, K, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmv_gs<4, F16T>(gs, y, x, w, s, b, M, N, K, st);
-    } else if (bits == 8) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_gs<8, BF16T>(gs, y, x, w, s, b, M, N, K, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmv_gs<8, F16T>(gs, y, x, w, s, b, M, N, K, st);
-    }
+// Calls f(bits, scale type, activation type) as compile-time values for the
+// combinations the decode kernels take; false for the others.
+template <typename F>
+static bool with_qmv_types(int bits, int scale_dtype, int x_dtype, F&& f) {
+    auto by_x = [&](auto bc, auto st) -> bool {
+        if (x_dtype == EQ_DTYPE_BF16) return f(bc, st, BF16T{});
+        if (x_dtype == EQ_DTYPE_F16) return f(bc, st, F16T{});
+        return false;
+    };
+    auto by_s = [&](auto bc) -> bool {
+        if (scale_dtype == EQ_DTYPE_BF16) return by_x(bc, BF16T{});
+        if (scale_dtype == EQ_DTYPE_F16) return by_x(bc, F16T{});
+        return false;
+    };
+    if (bits == 4) return by_s(std::integral_constant<int, 4>{});
+    if (bits == 8) return by_s(std::integral_constant<int, 8>{});
     return false;
 }
 
-template <int BITS, typename ST>
+// Entry used by the dispatcher (api.hip).  Preconditions checked there:
+// x bf16 or f16 (y in x's type), transpose, 1 <= M <= 16, N % 16 == 0,
+// K % gs == 0, 16-byte aligned x and weight pointers, scale dtype bf16 or f16.
+bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                     const void* s, const void* b, int M, int N, int K, hipStream_t st, int x_dtype) {
+    return with_qmv_types(bits, scale_dtype, x_dtype, [&](auto bc, auto stt, auto xt) {
+        return launch_qmv_gs<decltype(bc)::value, decltype(stt), decltype(xt)>(gs, y, x, w, s, b, M, N, K, st);
+    });
+}
+
+template <int BITS, typename ST, typename XT>
 static bool launch_qmv_group_gs(int gs, const QmvSpec* specs, int count, int M, hipStream_t st) {
     switch (gs) {
-    case 32: return launch_qmv_group_t<BITS, 32, ST>(specs, count, M, st);
-    case 64: return launch_qmv_group_t<BITS, 64, ST>(specs, count, M, st);
-    case 128: return launch_qmv_group_t<BITS, 128, ST>(specs, count, M, st);
+    case 32: return launch_qmv_group_t<BITS, 32, ST, XT>(specs, count, M, st);
+    case 64: return launch_qmv_group_t<BITS, 64, ST, XT>(specs, count, M, st);
+    case 128: return launch_qmv_group_t<BITS, 128, ST, XT>(specs, count, M, st);
     default: return false;
     }
 }
@@ -1335,15 +1405,11 @@ bool launch_qmv_prologue(int bits, int gs, int scale_dtype, const QmvSpec* specs
     return false;
 }
 
-bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st) {
-    if (bits == 4) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_group_gs<4, BF16T>(gs, specs, count, M, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmv_group_gs<4, F16T>(gs, specs, count, M, st);
-    } else if (bits == 8) {
-        if (scale_dtype == EQ_DTYPE_BF16) return launch_qmv_group_gs<8, BF16T>(gs, specs, count, M, st);
-        if (scale_dtype == EQ_DTYPE_F16) return launch_qmv_group_gs<8, F16T>(gs, specs, count, M, st);
-    }
-    return false;
+bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st,
+                        int x_dtype) {
+    return with_qmv_types(bits, scale_dtype, x_dtype, [&](auto bc, auto stt, auto xt) {
+        return launch_qmv_group_gs<decltype(bc)::value, decltype(stt), decltype(xt)>(gs, specs, count, M, st);
+    });
 }
 
 }  // namespace eq
