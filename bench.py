@@ -982,6 +982,9 @@ def main():
                     help="the headline step only (the run a kernel-trace profile of the roofline kernel uses)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill qmm sweep, one JSON object of its figures (for kernel-trace profiles)")
+    ap.add_argument("--prefill-m", type=int, default=None,
+                    help="with --prefill-only: this M only, 4- and 8-bit at the four shapes, no other widths "
+                         "(for counter profiles of one prefill size)")
     ap.add_argument("--gguf-only", action="store_true",
                     help="only the GGUF dequant/convert sweep, one JSON object of its figures")
     ap.add_argument("--gather-only", action="store_true",
@@ -1008,9 +1011,12 @@ def main():
             out["mxfp4"] = bench_mxfp4(args.steps, args.warmup)
         if args.prefill_only:
             log("[bench] qmm prefill")
-            out["qmm"] = bench_qmm(args.steps, args.warmup)
-            log("[bench] qmm prefill, other widths")
-            out["qmm_widths"] = bench_qmm_widths(args.steps, args.warmup)
+            if args.prefill_m:
+                out["qmm"] = bench_qmm(args.steps, args.warmup, Ms=(args.prefill_m,))
+            else:
+                out["qmm"] = bench_qmm(args.steps, args.warmup)
+                log("[bench] qmm prefill, other widths")
+                out["qmm_widths"] = bench_qmm_widths(args.steps, args.warmup)
         if args.gguf_only:
             log("[bench] gguf")
             out["gguf"] = bench_gguf(args.steps, args.warmup)
@@ -1125,7 +1131,7 @@ def main():
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "qmv_lds_kernel<4,64,BF16T,1,true,false>",
+            "kernel": "qmv_lds_kernel<4,64,BF16T,1,true,false,0,BF16T>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
