@@ -663,6 +663,16 @@ __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, G
 #endif
 constexpr int kQmvLdsMaxWaves = 8;              // waves per workgroup of the LDS variant, at most
 constexpr int kQmvLdsWaves = EQ_QMV_LDS_WAVES;  // the planner's choice
+// Span stride between a wave's consecutive blocks in a tile.  TAIL = false
+// kernels (every K a whole number of blocks) interleave the waves' blocks
+// along K -- wave w takes blocks w, w + NW, ... -- so that a workgroup's
+// concurrent loads walk each row of its tile front to back together instead
+// of four separate quarters of every row: fewer DRAM pages open at once
+// (measured on the headline step: 3363 -> 3439 GB/s; gate/up 16.9 -> 16.2 us,
+// down 9.7 -> 9.5 us per launch).  TAIL kernels give each wave one contiguous
+// range (their ragged spans sit at the end of it).
+template <bool TAIL>
+constexpr int qmv_block_stride() { return !TAIL ? kQmvUnroll * kQmvLdsWaves : kQmvUnroll; }
 
 // Register blocks in the load ring of the LDS variant: loads run RING - 1
 // blocks ahead of the block being computed.  Measured on MI355X (decode
@@ -700,10 +710,16 @@ __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& b
     v.n0 = (tile - pr.tile0) * 16;
     v.S_full = K / Geo::SPAN;
     const int S = (K + Geo::SPAN - 1) / Geo::SPAN;
-    v.j_begin = wave * pr.spw;
+    v.j_begin = qmv_block_stride<TAIL>() != kQmvUnroll ? wave * kQmvUnroll : wave * pr.spw;
     v.j_end = min(S, v.j_begin + pr.spw);
     v.j_full_end = min(v.S_full, v.j_end);
     v.nblk = max(0, (v.j_full_end - v.j_begin) / kQmvUnroll);
+    if constexpr (qmv_block_stride<TAIL>() != kQmvUnroll) {
+        // blocks wave, wave + NW, ... of the tile's v.S_full / U (whole K)
+        const int nb = v.S_full / kQmvUnroll;
+        v.nblk = nb > wave ? (nb - wave + kQmvLdsWaves - 1) / kQmvLdsWaves : 0;
+        v.j_end = v.j_full_end = v.S_full;
+    }
     const uint32_t row_bytes = uint32_t(K) * BITS / 8;
     v.L.wr = raw_rsrc(pr.w, uint32_t(N) * row_bytes);
     v.L.sr = raw_rsrc(pr.s, uint32_t(N) * uint32_t(G) * 2u);
@@ -761,7 +777,7 @@ __device__ __forceinline__ void qmv_stream_seek(const QmvBatch& batch, QmvStream
             st.L = v.L;
             st.tile = tile;
             st.j = v.j_begin;
-            st.j_stop = v.j_begin + v.nblk * kQmvUnroll;
+            st.j_stop = v.j_begin + v.nblk * qmv_block_stride<TAIL>();
             return;
         }
         st.done = true;
@@ -776,7 +792,7 @@ __device__ __forceinline__ void qmv_stream_seek(const QmvBatch& batch, QmvStream
             st.L = v.L;
             st.tile = tile;
             st.j = v.j_begin;
-            st.j_stop = v.j_begin + v.nblk * kQmvUnroll;
+            st.j_stop = v.j_begin + v.nblk * qmv_block_stride<TAIL>();
             return;
         }
     }
@@ -789,8 +805,8 @@ template <int BITS, int GS, bool TAIL>
 __device__ __forceinline__ void qmv_stream_next(const QmvBatch& batch, QmvStream& st, int wave, int ln, int kq,
                                                 int r_p) {
     if (st.done) return;
-    if (st.j + kQmvUnroll < st.j_stop) {
-        st.j += kQmvUnroll;
+    if (st.j + qmv_block_stride<TAIL>() < st.j_stop) {
+        st.j += qmv_block_stride<TAIL>();
         return;
     }
     qmv_stream_seek<BITS, GS, TAIL>(batch, st, st.tile + gridDim.x, wave, ln, kq, r_p);
@@ -1095,7 +1111,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             } else {
                 qmv_retire(ring[d]);
             }
-            jc += U;
+            jc += qmv_block_stride<TAIL>();
             if (--left == 0) {
                 if constexpr (TAIL) {
                     do {
