@@ -543,6 +543,10 @@ struct QmvBatch {
     int stage[kQmvMaxProblems];  // problem whose x each staged matrix is
     int zero_lds, zero_bytes;
     int red_lds;             // 2 x waves x M x 16 floats
+    // K phases (one problem, one tile per workgroup, activations too long for
+    // LDS): LDS holds phase_spans spans of the rows at a time, phase p
+    // covering spans [p * phase_spans, (p + 1) * phase_spans); 0 = no phases.
+    int phase_spans;
     // Activation prologue (M = 1, one staged input): 1 = silu(x) * pro_second,
     // 2 = RMSNorm(x + pro_second) * pro_weight, the sum also written to
     // pro_hidden_out by workgroup 0.  Applied while staging.
@@ -907,7 +911,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     constexpr int NCH = PRO == 2 ? 2 : 8;  // chunks per thread and staging round
     u32x4 x2v[PRO != 0 ? NCH : 1];         // second input (up, residual); with PRO = 2 also the norm weight
     u32x4 nwv[PRO == 2 ? NCH : 1];
-    auto stage_load = [&](int r, int c0, u32x4* v, int* dst) __attribute__((always_inline)) {
+    auto stage_load = [&](int r, int c0, u32x4* v, int* dst, int k0 = 0) __attribute__((always_inline)) {
         const QmvProblem& pr = batch.p[batch.stage[r]];
         const __amdgpu_buffer_rsrc_t xr = raw_rsrc(pr.x, uint32_t(M) * uint32_t(pr.K) * 2u);
         // (the prologue's inputs: with PRO = 2 a missing residual reads zero)
@@ -927,7 +931,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             // 0.5 / cpr >= 2^-15, of (c + 0.5) / cpr to an integer
             const int m = MREG == 1 ? 0 : int((float(c) + 0.5f) * inv_cpr), cc = c - m * cpr;
             const bool live = c < total;
-            const uint32_t off = (live & (cc * 8 < K)) ? (uint32_t(m) * uint32_t(K) + uint32_t(cc) * 8u) * 2u : kOutOfRange;
+            const uint32_t off = (live & (k0 + cc * 8 < K))
+                                     ? (uint32_t(m) * uint32_t(K) + uint32_t(k0 + cc * 8)) * 2u : kOutOfRange;
             v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
             if constexpr (PRO != 0) x2v[i] = __builtin_amdgcn_raw_buffer_load_b128(x2r, off, 0, 0);
             if constexpr (PRO == 2) nwv[i] = __builtin_amdgcn_raw_buffer_load_b128(nwr, off, 0, 0);
@@ -1100,14 +1105,34 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         while (left == 0)
             if (!finish()) return;
     }
+    // K phases (batch.phase_spans > 0; one problem, one tile per workgroup, no
+    // tail): LDS holds the rows' spans [phase_base, phase_end).  Every wave has
+    // the same number of blocks in each phase but the last, so all of them
+    // reach each phase change, where the workgroup stages the next phase's
+    // activations (the ring's weight loads stay in flight across it).
+    int phase_base = 0, phase_end = batch.phase_spans > 0 ? batch.phase_spans : 0x7fffffff;
+    auto restage = [&]() __attribute__((always_inline)) {
+        __syncthreads();  // every wave is done with the previous phase's activations
+        const int total = M * (batch.p[0].kpad / 8);
+        for (int c0 = int(threadIdx.x); c0 < total; c0 += NCH * 64 * NW) {
+            stage_load(0, c0, xv, xdst, phase_end * SPAN);
+            stage_store(xv, xdst, c0);
+        }
+        __syncthreads();
+        phase_base = phase_end;
+        phase_end += batch.phase_spans;
+    };
     for (;;) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             ring_load(ring[(d + D - 1) % D]);
             qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
+            if constexpr (!TAIL && PRO == 0) {
+                if (jc >= phase_end) restage();
+            }
             if (opaque_one()) {
-                qmv_wcompute<BITS, GS, ST, MREG, U, VEC, XT>(acc, ring[d], smem, V.xa_t, V.xstep, jc, r_p, V.bias_on, uc,
-                                                          ones);
+                qmv_wcompute<BITS, GS, ST, MREG, U, VEC, XT>(acc, ring[d], smem, V.xa_t, V.xstep, jc - phase_base, r_p,
+                                                          V.bias_on, uc, ones);
             } else {
                 qmv_retire(ring[d]);
             }
@@ -1212,20 +1237,43 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
         }
     }
     B.total_tiles = tiles;
+    B.phase_spans = 0;
+    const int zero_bytes = (U * Geo::SPAN * 2 + 64 + 15) / 16 * 16;
+    const int red_bytes = 2 * W * M * 16 * 4;
+    // Per-CU workgroups of the grid (EQ_QMV_WAVES_PER_CU waves per CU).
+    const int per_cu = EQ_QMV_WAVES_PER_CU / W > 0 ? EQ_QMV_WAVES_PER_CU / W : 1;
+    const int cap = per_cu * device_cu_count();
+    if (lds + zero_bytes + red_bytes > device_lds_bytes()) {
+        // Activations too long for LDS: stage them in K phases, for one
+        // problem with whole blocks and at most one tile per workgroup, the
+        // phase length a whole number of the waves' interleave stride.
+        const QmvSpec& q = specs[0];
+        const int S = q.K / Geo::SPAN, stride = U * W;
+        if (count != 1 || tail || tiles > cap || S % stride != 0 || S / U < W) return false;
+        const int nstrides = S / stride;
+        int ps = 0;
+        for (int P = 2; P <= nstrides && ps == 0; P++) {
+            const int per = (nstrides + P - 1) / P;  // strides per phase (the last may have fewer)
+            if (M * per * stride * Geo::SPAN * 2 + zero_bytes + red_bytes <= device_lds_bytes()) ps = per * stride;
+        }
+        if (ps == 0) return false;
+        QmvProblem& p = B.p[0];
+        p.kpad = ps * Geo::SPAN;
+        p.inv_cpr = 1.0f / float(p.kpad / 8);
+        B.phase_spans = ps;
+        lds = M * p.kpad * 2;
+    }
     B.zero_lds = lds;
-    B.zero_bytes = (U * Geo::SPAN * 2 + 64 + 15) / 16 * 16;
+    B.zero_bytes = zero_bytes;
     lds += B.zero_bytes;
     B.red_lds = lds;
-    lds += 2 * W * M * 16 * 4;
+    lds += red_bytes;
 
     if (lds > device_lds_bytes()) return false;
     plan.lds = lds;
     plan.vec = vec;
     plan.tail = tail;
-    // Workgroups resident per CU: EQ_QMV_WAVES_PER_CU waves.
-    const int per_cu = EQ_QMV_WAVES_PER_CU / W > 0 ? EQ_QMV_WAVES_PER_CU / W : 1;
     plan.waves = W;
-    const int cap = per_cu * device_cu_count();
     plan.grid = tiles < cap ? tiles : cap;
     return true;
 }
@@ -1389,7 +1437,8 @@ static bool launch_qmv_group_gs(int gs, const QmvSpec* specs, int count, int M, 
 template <int BITS, int GS, typename ST, int PRO>
 static bool launch_qmv_pro_t(const QmvSpec* specs, int count, const QmvPrologue& pro, hipStream_t st) {
     QmvLdsPlan plan;
-    if (!plan_qmv_lds<BITS, GS, ST>(specs, count, 1, plan) || plan.B.nstage != 1) return false;
+    if (!plan_qmv_lds<BITS, GS, ST>(specs, count, 1, plan) || plan.B.nstage != 1 || plan.B.phase_spans != 0)
+        return false;
     const int K = specs[0].K;
     if (PRO == 2 && K > 2 * 8 * 64 * kQmvLdsWaves) return false;
     plan.B.pro_second = pro.second;

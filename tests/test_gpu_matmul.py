@@ -264,3 +264,12 @@ def test_batched_falls_back_per_problem(cuda):
         x3 = torch.zeros(3, 256, dtype=torch.bfloat16, device="cuda")
         quantized_matmul_batched([(x2, probs[0][1], probs[0][2], None), (x3, probs[0][1], probs[0][2], None)],
                                  group_size=32)
+
+
+@pytest.mark.parametrize("M,K,gs,bits", [(8, 14336, 64, 4), (8, 14336, 64, 8), (5, 14336, 64, 4), (16, 8192, 128, 4),
+                                         (2, 98304, 64, 4), (8, 12288, 64, 4)])
+def test_qmv_activations_staged_in_k_phases(cuda, M, K, gs, bits):
+    """Activations longer than one workgroup's LDS (M x K x 2 bytes) on a
+    problem of at most one tile per workgroup: the decode kernel stages them
+    in K phases (the down projection at batch 8 among them)."""
+    run_case(M, 256, K, gs, bits, seed=M + K + bits)
