@@ -137,180 +137,288 @@ __global__ __launch_bounds__(1024) void rms_norm_kernel(uint16_t* __restrict__ o
     }
 }
 
-// Non-traditional (half-split) rotation of one head held in LDS as f32:
-// out[i] = x[i] cos - x[i+h] sin, out[i+h] = x[i+h] cos + x[i] sin, angle
-// pos / freqs[i] (Llama3Rope::forward).  128 threads per head.
-__device__ __forceinline__ void rope_pair(float* head, const float* __restrict__ freqs, float pos, int i) {
-    const float a = pos / freqs[i];
-    float s, c;
-    sincosf(a, &s, &c);
-    const float x1 = head[i], x2 = head[i + kHeadDim / 2];
-    head[i] = x1 * c - x2 * s;
-    head[i + kHeadDim / 2] = x2 * c + x1 * s;
+// Decode attention keeps, per query head, kAttnSplits softmax states, state
+// y over the 32-position chunks y, y + kAttnSplits, ... of positions 0..pos:
+// a row of kAttnStateFloats floats [m, l, o[0..127]] = the maximum scaled
+// score, the sum of exp(score - m) and the exp-weighted value rows.  Only the
+// first min(chunks, kAttnSplits) states of a head are written and read.
+constexpr int kAttnSplits = 64;
+constexpr int kAttnStateFloats = kHeadDim + 2;
+
+// DPP lane moves within rows of 16 lanes (quad_perm [1,0,3,2] = 0xB1,
+// quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Maximum / sum over each row of 16 lanes, in every lane of the row.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    return fmaxf(v, dpp_move<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_move<0xB1>(v);
+    v += dpp_move<0x4E>(v);
+    v += dpp_move<0x141>(v);
+    return v + dpp_move<0x140>(v);
+}
+__device__ __forceinline__ float lane_value(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
-// One workgroup (256 threads, 4 waves) per (KV head, chunk of 32 positions):
-// the query heads of the group (q rotated here), the chunk's keys and values
-// staged in LDS, partial softmax state (max, sum, weighted values) written
-// to the workspace for the combine pass.  The chunk that holds `pos` also
-// rotates the new key and stores it and the new value into the cache; no
-// other workgroup reads position `pos`.
+// Grid (n_kv_heads, kAttnSplits), 256 threads (4 waves; wave h = query head
+// g * group + h of KV head g).  Split y walks its chunks: each chunk's keys
+// and values go through registers into LDS (the first chunk's are requested
+// before the position is known, bounded by max_seq; each next chunk's while
+// the current one is computed), the group's queries are rotated once (the 64
+// angles' sines and cosines computed once per workgroup), and the chunk that
+// holds pos rotates the new key and writes it and the new value into the
+// cache (no other chunk reads row pos).  Per query head the split keeps a
+// running softmax state merged chunk by chunk (m' = max(m, m_c); l, o scaled
+// by e^(m - m') and e^(m_c - m')) and writes it to states[head][y].
+// Scores: lane = position (lane / 2) x half of the dimensions (lane % 2), the
+// query half in registers, the key half-row in 16-byte LDS reads; maxima and
+// sums by DPP within rows of 16 lanes and lane reads across the rows.
 //
 // pos_p, when not null, names the position in device memory (read when the
-// kernel runs) and the grid covers every chunk of max_seq: workgroups of
-// chunks past the position leave at once, and a position outside
-// [0, max_seq) does nothing.  nchunks is the chunk stride of ws per head.
-__global__ __launch_bounds__(256) void attn_partial_kernel(float* __restrict__ ws, const uint16_t* __restrict__ q,
-                                                           const uint16_t* __restrict__ k_new,
-                                                           const uint16_t* __restrict__ v_new,
-                                                           uint16_t* __restrict__ k_cache,
-                                                           uint16_t* __restrict__ v_cache,
-                                                           const float* __restrict__ freqs, int pos_arg,
-                                                           const int32_t* __restrict__ pos_p, int max_seq,
-                                                           int n_heads, int n_kv_heads, int nchunks, float scale) {
-    __shared__ float qs[4][kHeadDim];                            // rotated queries of this group
+// kernel runs); a position outside [0, max_seq) writes nothing.
+__global__ __launch_bounds__(256) void attn_states_kernel(float* __restrict__ states, const uint16_t* __restrict__ q,
+                                                          const uint16_t* __restrict__ k_new,
+                                                          const uint16_t* __restrict__ v_new,
+                                                          uint16_t* __restrict__ k_cache,
+                                                          uint16_t* __restrict__ v_cache,
+                                                          const float* __restrict__ freqs, int pos_arg,
+                                                          const int32_t* __restrict__ pos_p, int max_seq,
+                                                          int n_heads, int n_kv_heads, float scale) {
+    __shared__ __attribute__((aligned(16))) float qs[4][kHeadDim];  // rotated queries of this group
     __shared__ __attribute__((aligned(16))) uint16_t ks[kAttnChunk][kRowPad];
     __shared__ __attribute__((aligned(16))) uint16_t vs[kAttnChunk][kRowPad];
     __shared__ float knew[kHeadDim];
-    const int g = blockIdx.x, c = blockIdx.y;
+    __shared__ float rot[2][kHeadDim / 2];  // cos, sin of the angles pos / freqs[i]
     const int pos = pos_p ? __builtin_amdgcn_readfirstlane(*pos_p) : pos_arg;
-    if (pos < 0 || pos >= max_seq || c * kAttnChunk > pos) return;
+    const int g = blockIdx.x, split = blockIdx.y;
     const int group = n_heads / n_kv_heads;  // <= 4
-    const int p0 = c * kAttnChunk, np = min(kAttnChunk, pos + 1 - p0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float fpos = float(pos);
-
-    // queries of the group, the new key (if this chunk holds pos) and the
-    // chunk's cached keys and values, all requested before any waits
-    for (int i = tid; i < group * kHeadDim; i += 256)
-        qs[i / kHeadDim][i % kHeadDim] = bf16_bits_to_f32(q[(int64_t(g) * group + i / kHeadDim) * kHeadDim + i % kHeadDim]);
-    const bool has_new = pos >= p0 && pos < p0 + kAttnChunk;
-    if (has_new && tid < kHeadDim) knew[tid] = bf16_bits_to_f32(k_new[int64_t(g) * kHeadDim + tid]);
     uint16_t* kc = k_cache + int64_t(g) * max_seq * kHeadDim;
     uint16_t* vc = v_cache + int64_t(g) * max_seq * kHeadDim;
-    for (int i = tid; i < np * (kHeadDim / 8); i += 256) {
-        const int p = i / (kHeadDim / 8), v = i % (kHeadDim / 8);
-        if (p0 + p == pos) continue;
-        reinterpret_cast<uint4*>(&ks[p][0])[v] = reinterpret_cast<const uint4*>(kc + int64_t(p0 + p) * kHeadDim)[v];
-        reinterpret_cast<uint4*>(&vs[p][0])[v] = reinterpret_cast<const uint4*>(vc + int64_t(p0 + p) * kHeadDim)[v];
+
+    // the group's queries, the new key and the frequencies first, so that
+    // waiting for them does not wait for the chunk
+    float qv[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = tid + 256 * r;
+        qv[r] = i < group * kHeadDim ? bf16_bits_to_f32(q[int64_t(g) * group * kHeadDim + i]) : 0.f;
+    }
+    const float kn = tid < kHeadDim ? bf16_bits_to_f32(k_new[int64_t(g) * kHeadDim + tid]) : 0.f;
+    const float fr = tid < kHeadDim / 2 ? freqs[tid] : 1.f;
+    // this thread's two 16-byte pieces of a chunk's keys and of its values:
+    // piece i = tid + 256 r is position i / 16, dimensions 8 (i % 16) ..
+    uint4 kr[2], vr[2];
+    auto fetch = [&](int c, int limit) __attribute__((always_inline)) {
+        const int p0 = c * kAttnChunk;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int i = tid + 256 * r, p = p0 + i / (kHeadDim / 8), v = i % (kHeadDim / 8);
+            const bool live = p < limit;
+            kr[r] = live ? reinterpret_cast<const uint4*>(kc + int64_t(p) * kHeadDim)[v] : make_uint4(0u, 0u, 0u, 0u);
+            vr[r] = live ? reinterpret_cast<const uint4*>(vc + int64_t(p) * kHeadDim)[v] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    fetch(split, max_seq);  // rows past pos are masked out below
+    const bool valid = pos >= 0 && pos < max_seq;
+    const int nch = valid ? pos / kAttnChunk + 1 : 0;
+    if (split >= nch) return;
+    const float fpos = float(pos);
+    const int c_new = pos / kAttnChunk;  // the chunk holding pos
+    const bool mine_new = c_new % kAttnSplits == split;
+
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = tid + 256 * r;
+        if (i < group * kHeadDim) qs[i / kHeadDim][i % kHeadDim] = qv[r];
+    }
+    if (tid < kHeadDim) knew[tid] = kn;
+    if (tid < kHeadDim / 2) {
+        float sn, cs;
+        sincosf(fpos / fr, &sn, &cs);
+        rot[0][tid] = cs;
+        rot[1][tid] = sn;
     }
     __syncthreads();
-    for (int i = tid; i < group * (kHeadDim / 2); i += 256) rope_pair(qs[i / (kHeadDim / 2)], freqs, fpos, i % (kHeadDim / 2));
-    if (has_new && tid < kHeadDim / 2) rope_pair(knew, freqs, fpos, tid);
+    // non-traditional (half-split) rotation, Llama3Rope::forward: pairs
+    // (d, d + 64) of each query head, and of the new key in its chunk's split
+    for (int i = tid; i < (group + (mine_new ? 1 : 0)) * (kHeadDim / 2); i += 256) {
+        const int hh = i / (kHeadDim / 2), d = i % (kHeadDim / 2);
+        float* head = hh < group ? qs[hh] : knew;
+        const float cs = rot[0][d], sn = rot[1][d];
+        const float x1 = head[d], x2 = head[d + kHeadDim / 2];
+        head[d] = x1 * cs - x2 * sn;
+        head[d + kHeadDim / 2] = x2 * cs + x1 * sn;
+    }
     __syncthreads();
-    // position pos: the rotated new key (rounded to bf16) and the new value,
-    // into LDS and into the cache
-    if (has_new && tid < kHeadDim / 8) {
-        const int p = pos - p0, v = tid;
-        uint4 kk;
-        uint32_t* pk = reinterpret_cast<uint32_t*>(&kk);
+    // position pos: the rotated new key rounded to bf16, and the new value,
+    // into the cache (and into LDS when its chunk is staged)
+    uint4 kk_new = make_uint4(0u, 0u, 0u, 0u), vv_new = make_uint4(0u, 0u, 0u, 0u);
+    if (mine_new && tid < kHeadDim / 8) {
+        const int v = tid;
+        uint32_t* pk = reinterpret_cast<uint32_t*>(&kk_new);
 #pragma unroll
         for (int e = 0; e < 4; e++)
             pk[e] = f32_to_bf16_bits(knew[8 * v + 2 * e]) | (f32_to_bf16_bits(knew[8 * v + 2 * e + 1]) << 16);
-        const uint4 vv = reinterpret_cast<const uint4*>(v_new + int64_t(g) * kHeadDim)[v];
-        reinterpret_cast<uint4*>(kc + int64_t(pos) * kHeadDim)[v] = kk;
-        reinterpret_cast<uint4*>(vc + int64_t(pos) * kHeadDim)[v] = vv;
-        reinterpret_cast<uint4*>(&ks[p][0])[v] = kk;
-        reinterpret_cast<uint4*>(&vs[p][0])[v] = vv;
+        vv_new = reinterpret_cast<const uint4*>(v_new + int64_t(g) * kHeadDim)[v];
+        reinterpret_cast<uint4*>(kc + int64_t(pos) * kHeadDim)[v] = kk_new;
+        reinterpret_cast<uint4*>(vc + int64_t(pos) * kHeadDim)[v] = vv_new;
     }
-    __syncthreads();
+    const int h = wave, p = lane >> 1, half = lane & 1;
+    float qreg[kHeadDim / 2];
+    if (h < group) {
+#pragma unroll
+        for (int j = 0; j < kHeadDim / 8; j++) {
+            const float4 t = reinterpret_cast<const float4*>(&qs[h][half * (kHeadDim / 2)])[j];
+            qreg[4 * j] = t.x;
+            qreg[4 * j + 1] = t.y;
+            qreg[4 * j + 2] = t.z;
+            qreg[4 * j + 3] = t.w;
+        }
+    }
 
-    // wave h: query head g*group + h.  Scores: lane = position (p < 32) x half
-    // of the dimensions (lane / 32), summed over the pair.
-    for (int h = wave; h < group; h += 4) {
-        const int p = lane & 31, half = lane >> 5;
-        float s = 0.f;
-        if (p < np) {
-            const uint32_t* kr = reinterpret_cast<const uint32_t*>(&ks[p][half * (kHeadDim / 2)]);
-            const float* qh = &qs[h][half * (kHeadDim / 2)];
-#pragma unroll 8
-            for (int d = 0; d < kHeadDim / 4; d++) {
-                const uint32_t kk = kr[d];
-                s = fmaf(qh[2 * d], bf16_bits_to_f32(kk & 0xffffu), s);
-                s = fmaf(qh[2 * d + 1], bf16_bits_to_f32(kk >> 16), s);
+    float m_run = -INFINITY, l_run = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int c = split; c < nch; c += kAttnSplits) {
+        const int p0 = c * kAttnChunk, np = min(kAttnChunk, pos + 1 - p0);
+        __syncthreads();  // the previous chunk's LDS reads are done
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int i = tid + 256 * r, pr = i / (kHeadDim / 8), v = i % (kHeadDim / 8);
+            reinterpret_cast<uint4*>(&ks[pr][0])[v] = kr[r];
+            reinterpret_cast<uint4*>(&vs[pr][0])[v] = vr[r];
+        }
+        if (c == c_new && tid < kHeadDim / 8) {
+            reinterpret_cast<uint4*>(&ks[pos - p0][0])[tid] = kk_new;
+            reinterpret_cast<uint4*>(&vs[pos - p0][0])[tid] = vv_new;
+        }
+        __syncthreads();
+        if (c + kAttnSplits < nch) fetch(c + kAttnSplits, pos);  // in flight while this chunk is computed
+        if (h < group) {
+            float sa = 0.f, sb = 0.f;
+            if (p < np) {
+                const uint4* kr4 = reinterpret_cast<const uint4*>(&ks[p][half * (kHeadDim / 2)]);
+#pragma unroll
+                for (int j = 0; j < kHeadDim / 16; j++) {
+                    const uint4 kk = kr4[j];
+                    const uint32_t w4[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        sa = fmaf(qreg[8 * j + 2 * e], bf16_bits_to_f32(w4[e] & 0xffffu), sa);
+                        sb = fmaf(qreg[8 * j + 2 * e + 1], bf16_bits_to_f32(w4[e] >> 16), sb);
+                    }
+                }
+            }
+            float sc = sa + sb;
+            sc += dpp_move<0xB1>(sc);  // the other half of the dimensions
+            sc = p < np ? sc * scale : -INFINITY;
+            const float rm = row16_max(sc);
+            const float mc = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)),
+                                   fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
+            const float e = p < np ? expf(sc - mc) : 0.f;
+            const float rs = row16_sum(half == 0 ? e : 0.f);
+            const float lc = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
+            // weighted values: lane owns dimensions 2 lane, 2 lane + 1; every
+            // row is read (rows past np hold finite or stale data, skipped)
+            uint32_t vv[kAttnChunk];
+#pragma unroll
+            for (int pp = 0; pp < kAttnChunk; pp++) vv[pp] = reinterpret_cast<const uint32_t*>(&vs[pp][0])[lane];
+            float c0 = 0.f, c1 = 0.f;
+#pragma unroll
+            for (int pp = 0; pp < kAttnChunk; pp++) {
+                if (pp < np) {
+                    const float w = lane_value(e, 2 * pp);
+                    c0 = fmaf(w, bf16_bits_to_f32(vv[pp] & 0xffffu), c0);
+                    c1 = fmaf(w, bf16_bits_to_f32(vv[pp] >> 16), c1);
+                }
+            }
+            if (c == split) {
+                m_run = mc;
+                l_run = lc;
+                o0 = c0;
+                o1 = c1;
+            } else {
+                const float mn = fmaxf(m_run, mc);
+                const float fa = expf(m_run - mn), fb = expf(mc - mn);
+                l_run = l_run * fa + lc * fb;
+                o0 = o0 * fa + c0 * fb;
+                o1 = o1 * fa + c1 * fb;
+                m_run = mn;
             }
         }
-        s += __shfl_xor(s, 32);
-        s = p < np ? s * scale : -INFINITY;
-        float m = s;
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float e = p < np ? expf(s - m) : 0.f;
-        float l = e;
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) l += __shfl_xor(l, o);
-        // weighted values: lane owns dimensions 2 lane, 2 lane + 1
-        float o0 = 0.f, o1 = 0.f;
-        for (int pp = 0; pp < np; pp++) {
-            const float w = __shfl(e, pp);
-            const uint32_t vv = reinterpret_cast<const uint32_t*>(&vs[pp][0])[lane];
-            o0 = fmaf(w, bf16_bits_to_f32(vv & 0xffffu), o0);
-            o1 = fmaf(w, bf16_bits_to_f32(vv >> 16), o1);
-        }
-        float* dst = ws + (int64_t(g * group + h) * nchunks + c) * (kHeadDim + 2);
+    }
+    if (h < group) {
+        float* dst = states + (int64_t(g * group + h) * kAttnSplits + split) * kAttnStateFloats;
         if (lane == 0) {
-            dst[0] = m;
-            dst[1] = l;
+            dst[0] = m_run;
+            dst[1] = l_run;
         }
-        dst[2 + 2 * lane] = o0;
-        dst[3 + 2 * lane] = o1;
+        reinterpret_cast<float2*>(dst + 2)[lane] = make_float2(o0, o1);
+    }
+}
+
+// One workgroup of 256 threads per query head, over the first
+// ns = min(chunks, kAttnSplits) states: M = max m_y, f_y = e^(m_y - M); wave
+// w sums f_y o_y over the states y = w, w + 4, ... (all its loads issued
+// together), lane d for dimensions 2 d and 2 d + 1; the waves' sums are added
+// in wave order and divided by sum f_y l_y; rounded to bf16.  A position
+// outside [0, max_seq) gives zeros.
+__global__ __launch_bounds__(256) void attn_states_combine_kernel(uint16_t* __restrict__ out,
+                                                                  const float* __restrict__ states, int pos_arg,
+                                                                  const int32_t* __restrict__ pos_p, int max_seq) {
+    __shared__ float2 part[4][64];
+    const int pos = pos_p ? __builtin_amdgcn_readfirstlane(*pos_p) : pos_arg;
+    const int h = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int nch = pos >= 0 && pos < max_seq ? pos / kAttnChunk + 1 : 0;
+    const int ns = min(nch, kAttnSplits);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + int64_t(h) * kHeadDim) + lane;
+    if (ns == 0) {
+        if (w == 0) *dst = 0u;
+        return;
+    }
+    const float* st = states + int64_t(h) * kAttnSplits * kAttnStateFloats;
+    float2 o[kAttnSplits / 4];
+#pragma unroll
+    for (int k = 0; k < kAttnSplits / 4; k++) {
+        const int y = w + 4 * k;
+        o[k] = y < ns ? reinterpret_cast<const float2*>(st + y * kAttnStateFloats + 2)[lane] : make_float2(0.f, 0.f);
+    }
+    const float m = lane < ns ? st[lane * kAttnStateFloats] : -INFINITY;
+    const float l = lane < ns ? st[lane * kAttnStateFloats + 1] : 0.f;
+    float mx = m;
+#pragma unroll
+    for (int of = 32; of > 0; of >>= 1) mx = fmaxf(mx, __shfl_xor(mx, of));
+    const float f = lane < ns ? expf(m - mx) : 0.f;
+    const float lsum = wave_sum(f * l);
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < kAttnSplits / 4; k++) {
+        const float fy = lane_value(f, w + 4 * k);  // 0 past ns
+        a0 = fmaf(fy, o[k].x, a0);
+        a1 = fmaf(fy, o[k].y, a1);
+    }
+    part[w][lane] = make_float2(a0, a1);
+    __syncthreads();
+    if (w == 0) {
+        float2 t = part[0][lane];
+#pragma unroll
+        for (int i = 1; i < 4; i++) {
+            t.x += part[i][lane].x;
+            t.y += part[i][lane].y;
+        }
+        *dst = f32_to_bf16_bits(t.x / lsum) | (f32_to_bf16_bits(t.y / lsum) << 16);
     }
 }
 
 // pos[0] += 1 (the next decode position), one thread.
 __global__ void advance_position_kernel(int32_t* pos) { pos[0] += 1; }
-
-// One workgroup of 256 threads per query head: the chunks' partial states
-// (max, weight sum, weighted values) merged -- their maxima and rescale
-// factors computed in parallel into LDS, then two halves of the threads sum
-// alternate chunks for each dimension with independent loads -- divided by
-// the total weight, rounded to bf16.
-// With pos_p (device position) the chunk count comes from the position
-// (zeros for one outside [0, max_seq)); ws holds `stride` chunks per head.
-__global__ __launch_bounds__(256) void attn_combine_kernel(uint16_t* __restrict__ out, const float* __restrict__ ws,
-                                                           int nchunks_arg, const int32_t* __restrict__ pos_p,
-                                                           int max_seq, int stride) {
-    __shared__ float fac[kMaxChunks];
-    __shared__ float red[4];
-    __shared__ float part[128];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int nchunks = nchunks_arg;
-    if (pos_p) {
-        const int pos = __builtin_amdgcn_readfirstlane(*pos_p);
-        nchunks = pos >= 0 && pos < max_seq ? pos / kAttnChunk + 1 : 0;
-        if (nchunks == 0) {
-            if (tid < kHeadDim) out[int64_t(h) * kHeadDim + tid] = 0;
-            return;
-        }
-    }
-    const float* base = ws + int64_t(h) * stride * (kHeadDim + 2);
-    float m = -INFINITY;
-    for (int c = tid; c < nchunks; c += 256) m = fmaxf(m, base[c * (kHeadDim + 2)]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float l = 0.f;
-    for (int c = tid; c < nchunks; c += 256) {
-        const float f = expf(base[c * (kHeadDim + 2)] - mx);
-        fac[c] = f;
-        l = fmaf(f, base[c * (kHeadDim + 2) + 1], l);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    if (lane == 0) red[wave] = l;
-    __syncthreads();
-    const float lsum = (red[0] + red[1]) + (red[2] + red[3]);
-    const int d = tid & (kHeadDim - 1), half = tid >> 7;
-    float o = 0.f;
-#pragma unroll 8
-    for (int c = half; c < nchunks; c += 2) o = fmaf(fac[c], base[c * (kHeadDim + 2) + 2 + d], o);
-    if (half == 1) part[d] = o;
-    __syncthreads();
-    if (half == 0) out[int64_t(h) * kHeadDim + d] = uint16_t(f32_to_bf16_bits((o + part[d]) / lsum));
-}
 
 // silu(gate) * up with the reference's roundings: sigmoid, the product with
 // gate and the product with up each round to bf16.  8 values per thread.
@@ -522,8 +630,8 @@ extern "C" int eq_rms_norm(void* out, void* x, const void* residual, const void*
     return check_launch("eq_rms_norm");
 }
 
-// Validation shared by the two attention entry points; the number of
-// position chunks on success.
+// Validation shared by the attention entry points (true when the arguments
+// are accepted; else the error is set).
 static bool attention_args_ok(const char* name, const void* out, const void* q, const void* k_new,
                               const void* v_new, const void* k_cache, const void* v_cache, const float* freqs,
                               int64_t pos, int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, int dtype) {
@@ -553,22 +661,22 @@ static bool attention_args_ok(const char* name, const void* out, const void* q, 
     return true;
 }
 
-// The two attention passes: per-chunk partial softmax states into ws, then
-// their combination per query head.
-static void launch_attention(float* ws, void* out, const void* q, const void* k_new, const void* v_new, void* k_cache,
-                             void* v_cache, const float* freqs, int64_t pos, int64_t max_seq, int n_heads,
-                             int n_kv_heads, int nchunks, float scale, hipStream_t st) {
-    attn_partial_kernel<<<dim3(unsigned(n_kv_heads), unsigned(nchunks)), dim3(256), 0, st>>>(
-        ws, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
-        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, int(pos), nullptr, int(max_seq),
-        n_heads, n_kv_heads, nchunks, scale);
-    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, nchunks,
-                                                                       nullptr, int(max_seq), nchunks);
+// The two attention passes: kAttnSplits softmax states per query head into
+// `states`, then their combination.  pos_p (device position) or pos.
+static void launch_attention(float* states, void* out, const void* q, const void* k_new, const void* v_new,
+                             void* k_cache, void* v_cache, const float* freqs, int64_t pos, const int32_t* pos_p,
+                             int64_t max_seq, int n_heads, int n_kv_heads, float scale, hipStream_t st) {
+    attn_states_kernel<<<dim3(unsigned(n_kv_heads), unsigned(kAttnSplits)), dim3(256), 0, st>>>(
+        states, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new),
+        static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs,
+        int(pos), pos_p, int(max_seq), n_heads, n_kv_heads, scale);
+    attn_states_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), states,
+                                                                               int(pos), pos_p, int(max_seq));
 }
 
-static size_t attention_scratch_bytes(int64_t pos, int n_heads, int& nchunks) {
-    nchunks = int((pos + kAttnChunk) / kAttnChunk);
-    return size_t(n_heads) * size_t(nchunks) * (kHeadDim + 2) * sizeof(float);
+// Bytes of softmax states of one attention call (n_heads * 64 * 520).
+static size_t attention_states_bytes(int n_heads) {
+    return size_t(n_heads) * kAttnSplits * kAttnStateFloats * sizeof(float);
 }
 
 extern "C" int eq_rope_attention_decode(void* out, const void* q, const void* k_new, const void* v_new,
@@ -580,15 +688,13 @@ extern "C" int eq_rope_attention_decode(void* out, const void* q, const void* k_
                            n_heads, n_kv_heads, head_dim, dtype))
         return 1;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    int nchunks = 0;
-    const size_t ws_bytes = attention_scratch_bytes(pos, n_heads, nchunks);
-    float* ws = static_cast<float*>(ws_acquire(nullptr, ws_bytes, st));
+    float* ws = static_cast<float*>(ws_acquire(nullptr, attention_states_bytes(n_heads), st));
     if (!ws) {
         set_error("eq_rope_attention_decode: no workspace (its stream's workspace cannot grow while capturing: "
-                  "make one call of at least this position on the stream before capturing)");
+                  "make one call with this head count on the stream before capturing)");
         return 1;
     }
-    launch_attention(ws, out, q, k_new, v_new, k_cache, v_cache, freqs, pos, max_seq, n_heads, n_kv_heads, nchunks,
+    launch_attention(ws, out, q, k_new, v_new, k_cache, v_cache, freqs, pos, nullptr, max_seq, n_heads, n_kv_heads,
                      scale, st);
     return check_launch("eq_rope_attention_decode");
 }
@@ -613,21 +719,14 @@ extern "C" int eq_rope_attention_decode_at(void* out, const void* q, const void*
         return 1;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    // every chunk of max_seq has a slot; the kernels read the position
-    const int nchunks = int((max_seq + kAttnChunk - 1) / kAttnChunk);
-    const size_t ws_bytes = size_t(n_heads) * size_t(nchunks) * (kHeadDim + 2) * sizeof(float);
-    float* ws = static_cast<float*>(ws_acquire(nullptr, ws_bytes, st));
+    float* ws = static_cast<float*>(ws_acquire(nullptr, attention_states_bytes(n_heads), st));
     if (!ws) {
         set_error(std::string(who) + ": no workspace (its stream's workspace cannot grow while capturing: make one "
-                  "call with this max_seq on the stream before capturing)");
+                  "call with this head count on the stream before capturing)");
         return 1;
     }
-    attn_partial_kernel<<<dim3(unsigned(n_kv_heads), unsigned(nchunks)), dim3(256), 0, st>>>(
-        ws, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
-        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs, 0, pos, int(max_seq), n_heads,
-        n_kv_heads, nchunks, scale);
-    attn_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), ws, 0, pos,
-                                                                       int(max_seq), nchunks);
+    launch_attention(ws, out, q, k_new, v_new, k_cache, v_cache, freqs, 0, pos, max_seq, n_heads, n_kv_heads, scale,
+                     st);
     return check_launch(who);
 }
 
@@ -643,8 +742,8 @@ extern "C" int eq_advance_position(int32_t* pos, eq_stream_t stream) {
 
 // ---------------------------------------------------- allocation-free variant
 
-// Scratch of eq_rope_attention_decode_noalloc: the attention partials
-// (n_heads * chunks * 520 bytes).  Every GPU the library runs on holds its own
+// Scratch of eq_rope_attention_decode_noalloc: the attention softmax states
+// (n_heads * 64 * 520 bytes, at most 252 heads).  Every GPU the library runs on holds its own
 // copy until the process ends.  The array's name is a host-side stand-in in
 // host code; the device address comes from attention_scratch_address().
 constexpr size_t kAttnScratchBytes = size_t(8) << 20;
@@ -682,18 +781,17 @@ extern "C" int eq_rope_attention_decode_noalloc(void* out, const void* q, const 
     if (!attention_args_ok("eq_rope_attention_decode_noalloc", out, q, k_new, v_new, k_cache, v_cache, freqs, pos,
                            max_seq, n_heads, n_kv_heads, head_dim, dtype))
         return 1;
-    int nchunks = 0;
-    const size_t ws_bytes = attention_scratch_bytes(pos, n_heads, nchunks);
+    const size_t ws_bytes = attention_states_bytes(n_heads);
     if (ws_bytes > kAttnScratchBytes) {
-        set_error("eq_rope_attention_decode_noalloc: n_heads * (pos / 32 + 1) * 520 = " + std::to_string(ws_bytes) +
+        set_error("eq_rope_attention_decode_noalloc: n_heads * 64 * 520 = " + std::to_string(ws_bytes) +
                   " bytes of scratch, more than the " + std::to_string(kAttnScratchBytes) +
                   " this entry point holds (use eq_rope_attention_decode)");
         return 1;
     }
     void* ws = attention_scratch_address();
     if (!ws) return 1;
-    launch_attention(static_cast<float*>(ws), out, q, k_new, v_new, k_cache, v_cache, freqs, pos, max_seq, n_heads,
-                     n_kv_heads, nchunks, scale, reinterpret_cast<hipStream_t>(stream));
+    launch_attention(static_cast<float*>(ws), out, q, k_new, v_new, k_cache, v_cache, freqs, pos, nullptr, max_seq,
+                     n_heads, n_kv_heads, scale, reinterpret_cast<hipStream_t>(stream));
     return check_launch("eq_rope_attention_decode_noalloc");
 }
 

@@ -321,11 +321,13 @@ int eq_rms_norm(void* out, void* hidden, const void* residual, const void* weigh
  *   reading KV head h / (n_heads / n_kv_heads).
  * Replaces Attention::attend (llama.rs:296-330): rotary forward, cache
  * update_for_attention and fast::scaled_dot_product_attention.  head_dim must
- * be 128 and n_heads / n_kv_heads at most 4.  The attention partials live in
- * the library workspace of `stream` (grow-only, never freed while the process
+ * be 128 and n_heads / n_kv_heads at most 4.  Two launches: 8 softmax states
+ * per query head (each over every 8th 32-position chunk of the cache), then
+ * their combination.  The states (n_heads * 8 * 520 bytes) live in the
+ * library workspace of `stream` (grow-only, never freed while the process
  * runs); it cannot grow while `stream` is capturing, so a capture needs an
- * earlier call at least this large on that stream (else the call fails), or
- * eq_rope_attention_decode_noalloc. */
+ * earlier call with at least this head count on that stream (else the call
+ * fails), or eq_rope_attention_decode_noalloc. */
 int eq_rope_attention_decode(void* out, const void* q, const void* k_new, const void* v_new,
                              void* k_cache, void* v_cache, const float* freqs, int64_t pos,
                              int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,
@@ -335,10 +337,10 @@ int eq_rope_attention_decode(void* out, const void* q, const void* k_new, const 
  * the reference.  For callers that cannot allocate device memory -- code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  Same arguments, validation and results (the same kernels); the
- * attention partials live in a library-owned static device array of 8 MiB
- * per GPU, held until the process ends, instead of the stream's workspace.
- * A call needing more than that -- n_heads * (pos / 32 + 1) * 520 bytes, e.g.
- * 32 heads at pos >= 16128 -- is rejected with a message.  Every call on one
+ * attention softmax states live in a library-owned static device array of
+ * 1 MiB per GPU, held until the process ends, instead of the stream's
+ * workspace.  A call needing more than that -- n_heads * 8 * 520 bytes, i.e.
+ * more than 252 query heads -- is rejected with a message.  Every call on one
  * GPU shares that GPU's array: calls that overlap in time on one GPU (two
  * streams, or two processes' graphs) race and must be serialised by the
  * caller.  The first call on each device resolves the array's address. */
@@ -352,12 +354,12 @@ int eq_rope_attention_decode_noalloc(void* out, const void* q, const void* k_new
  * graph decodes successive positions: the reference advances its cache
  * offset every token (eredu/src/runtime/generation/streaming.rs:1038-1050,
  * through Attention::attend, llama.rs:296-330).  Same shapes, rules, kernels
- * and results as eq_rope_attention_decode at that position: the launch covers
- * every 32-position chunk of max_seq and the chunks past the position end at
- * once.  The chunk states live in the library workspace of `stream`, sized by
- * max_seq (n_heads * ceil(max_seq / 32) * 520 bytes), so a capture needs an
- * earlier call with this max_seq on that stream.  A position outside
- * [0, max_seq) writes no cache row and gives zeros.  max_seq <= 131072. */
+ * and results as eq_rope_attention_decode at that position (the same
+ * launches; the kernels take their chunk counts from the position).  The
+ * softmax states live in the library workspace of `stream` (n_heads * 8 *
+ * 520 bytes), so a capture needs an earlier call with this head count on that
+ * stream.  A position outside [0, max_seq) writes no cache row and gives
+ * zeros.  max_seq <= 131072. */
 int eq_rope_attention_decode_at(void* out, const void* q, const void* k_new, const void* v_new,
                                 void* k_cache, void* v_cache, const float* freqs, const int32_t* pos,
                                 int64_t max_seq, int n_heads, int n_kv_heads, int head_dim, float scale,

@@ -3,7 +3,8 @@ eq_rope_attention_decode) through the C ABI: its outputs and cache writes
 equal the allocating entry point's bit for bit (both run the same kernels on
 the same inputs; only the scratch differs), on two calls in a row, the
 second at a smaller position, and once under HIP graph capture with replays;
-calls past its 8 MiB scratch are rejected with a message."""
+calls past its 1 MiB scratch (n_heads * 8 * 520 bytes of softmax states) are
+rejected with a message."""
 import ctypes
 
 import numpy as np
@@ -59,8 +60,8 @@ def test_noalloc_equals_the_allocating_entry_point(cuda):
 
 
 def test_noalloc_under_graph_capture(cuda):
-    """Captured at a position whose partials the stream's workspace has never
-    held, replayed three times with eager work in between."""
+    """Captured on a fresh stream (whose workspace has never been grown),
+    replayed three times with eager work in between."""
     L = n.lib()
     freqs = _freqs()
     n_heads, n_kv, max_seq, pos = 32, 8, 3000, 2999
@@ -95,17 +96,23 @@ def test_noalloc_under_graph_capture(cuda):
         torch.cuda.synchronize()
 
 
-def test_noalloc_rejects_positions_past_its_scratch(cuda):
+def test_noalloc_rejects_head_counts_past_its_scratch(cuda):
     L = n.lib()
     freqs = _freqs()
-    n_heads, n_kv, max_seq = 32, 8, 16200
-    q, kn, vn, kc, vc = _inputs(n_heads, n_kv, max_seq, seed=9)
-    out = torch.empty(n_heads * 128, dtype=torch.bfloat16, device="cuda")
-    # 32 heads * 505 chunks * 520 B > 8 MiB
-    assert _call(L.eq_rope_attention_decode_noalloc, out, q, kn, vn, kc, vc, freqs, 16128, max_seq, n_heads, n_kv,
-                 None) == 1
+    max_seq, pos = 64, 40
+    # 256 heads * 8 states * 520 B > 1 MiB
+    q, kn, vn, kc, vc = _inputs(256, 64, max_seq, seed=9)
+    out = torch.empty(256 * 128, dtype=torch.bfloat16, device="cuda")
+    assert _call(L.eq_rope_attention_decode_noalloc, out, q, kn, vn, kc, vc, freqs, pos, max_seq, 256, 64, None) == 1
     assert "scratch" in L.eq_last_error().decode()
-    # the largest position that fits still runs
-    assert _call(L.eq_rope_attention_decode_noalloc, out, q, kn, vn, kc, vc, freqs, 16127, max_seq, n_heads, n_kv,
+    # the largest head count that fits (252 * 8 * 520 B) still runs, equal to
+    # the allocating entry point
+    q, kn, vn, kc, vc = _inputs(252, 63, max_seq, seed=10)
+    kc2, vc2 = kc.clone(), vc.clone()
+    out = torch.empty(252 * 128, dtype=torch.bfloat16, device="cuda")
+    ref = torch.empty_like(out)
+    assert _call(L.eq_rope_attention_decode_noalloc, out, q, kn, vn, kc, vc, freqs, pos, max_seq, 252, 63,
                  None) == 0, L.eq_last_error()
+    assert _call(L.eq_rope_attention_decode, ref, q, kn, vn, kc2, vc2, freqs, pos, max_seq, 252, 63, None) == 0
     torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
