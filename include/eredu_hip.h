@@ -321,9 +321,10 @@ int eq_rms_norm(void* out, void* hidden, const void* residual, const void* weigh
  *   reading KV head h / (n_heads / n_kv_heads).
  * Replaces Attention::attend (llama.rs:296-330): rotary forward, cache
  * update_for_attention and fast::scaled_dot_product_attention.  head_dim must
- * be 128 and n_heads / n_kv_heads at most 4.  Two launches: 8 softmax states
- * per query head (each over every 8th 32-position chunk of the cache), then
- * their combination.  The states (n_heads * 8 * 520 bytes) live in the
+ * be 128 and n_heads / n_kv_heads at most 4.  Two launches: 64 softmax
+ * states per query head (state y over the 32-position chunks y, y + 64, ...
+ * of the cache), then their combination.  The states (n_heads * 64 * 520
+ * bytes, whatever the position) live in the
  * library workspace of `stream` (grow-only, never freed while the process
  * runs); it cannot grow while `stream` is capturing, so a capture needs an
  * earlier call with at least this head count on that stream (else the call
@@ -338,8 +339,8 @@ int eq_rope_attention_decode(void* out, const void* q, const void* k_new, const 
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  Same arguments, validation and results (the same kernels); the
  * attention softmax states live in a library-owned static device array of
- * 1 MiB per GPU, held until the process ends, instead of the stream's
- * workspace.  A call needing more than that -- n_heads * 8 * 520 bytes, i.e.
+ * 8 MiB per GPU, held until the process ends, instead of the stream's
+ * workspace.  A call needing more than that -- n_heads * 64 * 520 bytes, i.e.
  * more than 252 query heads -- is rejected with a message.  Every call on one
  * GPU shares that GPU's array: calls that overlap in time on one GPU (two
  * streams, or two processes' graphs) race and must be serialised by the
@@ -356,7 +357,7 @@ int eq_rope_attention_decode_noalloc(void* out, const void* q, const void* k_new
  * through Attention::attend, llama.rs:296-330).  Same shapes, rules, kernels
  * and results as eq_rope_attention_decode at that position (the same
  * launches; the kernels take their chunk counts from the position).  The
- * softmax states live in the library workspace of `stream` (n_heads * 8 *
+ * softmax states live in the library workspace of `stream` (n_heads * 64 *
  * 520 bytes), so a capture needs an earlier call with this head count on that
  * stream.  A position outside [0, max_seq) writes no cache row and gives
  * zeros.  max_seq <= 131072. */

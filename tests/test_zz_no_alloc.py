@@ -3,7 +3,7 @@ eq_rope_attention_decode) through the C ABI: its outputs and cache writes
 equal the allocating entry point's bit for bit (both run the same kernels on
 the same inputs; only the scratch differs), on two calls in a row, the
 second at a smaller position, and once under HIP graph capture with replays;
-calls past its 1 MiB scratch (n_heads * 8 * 520 bytes of softmax states) are
+calls past its 8 MiB scratch (n_heads * 64 * 520 bytes of softmax states) are
 rejected with a message."""
 import ctypes
 
@@ -100,12 +100,12 @@ def test_noalloc_rejects_head_counts_past_its_scratch(cuda):
     L = n.lib()
     freqs = _freqs()
     max_seq, pos = 64, 40
-    # 256 heads * 8 states * 520 B > 1 MiB
+    # 256 heads * 64 states * 520 B > 8 MiB
     q, kn, vn, kc, vc = _inputs(256, 64, max_seq, seed=9)
     out = torch.empty(256 * 128, dtype=torch.bfloat16, device="cuda")
     assert _call(L.eq_rope_attention_decode_noalloc, out, q, kn, vn, kc, vc, freqs, pos, max_seq, 256, 64, None) == 1
     assert "scratch" in L.eq_last_error().decode()
-    # the largest head count that fits (252 * 8 * 520 B) still runs, equal to
+    # the largest head count that fits (252 * 64 * 520 B) still runs, equal to
     # the allocating entry point
     q, kn, vn, kc, vc = _inputs(252, 63, max_seq, seed=10)
     kc2, vc2 = kc.clone(), vc.clone()
