@@ -188,12 +188,16 @@ int eq_gguf_embedding(void* out, const uint8_t* raw, int64_t raw_len, int ggml_t
  * launch of eq_gguf_linear's M = 1 kernels for all routes, each route's
  * expert matrix picked on the device from ids (native definition, f32
  * factors).
- * More routes (N % 128 == 0, K % 64 == 0): the bank is re-packed once into
+ * More routes (N % 128 == 0, K % 64 == 0): the whole bank is re-packed into
  * the workspace as eq_gguf_linear's prefill does and the routes run as one
  * gathered product (sorted_ids: ascending ids promised, the grouped
  * matrix-core kernel; unsorted ids under the promise give wrong rows but
- * stay in bounds; the first such call on a stream may allocate the
- * workspace).  Replaces native_grouped_linear (safemlx/src/native_quantization.rs:
+ * stay in bounds).  The re-packed bank takes experts * N * (K * b / 8 +
+ * 4 * K / gs) bytes of the stream's workspace (b = 4 for Q4_K, 8 for the
+ * others; gs = 32, or 16 for Q6_K), every expert whether ids reference it or
+ * not, plus routes * K * 2 bytes of gathered rows; the workspace only grows
+ * and is kept until the process ends, so one call on a wide bank holds that
+ * memory for the process's lifetime.  Replaces native_grouped_linear (safemlx/src/native_quantization.rs:
  * 1039-1072; its CPU loop :1002-1037) as eredu's MoE calls it
  * (eredu/src/backend/mlx/nn/moe.rs:1080-1092).  x 16-byte, y 8-byte aligned, a
  * Q4_K bank 16-byte aligned.
