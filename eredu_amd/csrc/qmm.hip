@@ -170,9 +170,11 @@ struct QmmArgs {
 
 // PW (parameter windows, group size 64 with an even number of groups per row
 // and an even first chunk per split): instead of two 2-byte loads per column
-// block and step, which touch one cache line per row each, a lane loads the
-// scales and biases of 6 consecutive groups (3 steps of each K-group) with
-// one 12-byte load each.
+// block and step, which touch one cache line per row each, the workgroup
+// stages the scales and biases of 12 consecutive groups (6 steps of each
+// K-group) of its 256 columns in LDS, each row's 24 bytes loaded by two lanes
+// (every wave loads 32 rows of each), and every lane reads its column's word
+// of a step from there.
 template <int BITS, int GS, typename ST, bool SPLIT, bool PW, typename XT = BF16T>
 __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void qmm_mfma_kernel(
     const QmmArgs args) {
@@ -229,6 +231,9 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const __amdgpu_buffer_rsrc_t wr = raw_rsrc(wp, uint32_t(N) * row_bytes);
     const __amdgpu_buffer_rsrc_t sr = raw_rsrc(sp, uint32_t(N) * uint32_t(G) * PB);
     const __amdgpu_buffer_rsrc_t br = raw_rsrc(bp ? bp : sp, bp ? uint32_t(N) * uint32_t(G) * PB : 0u);
+    // Parameter windows in LDS: [buffer][scale, bias][column * 6 + word], word
+    // w of a column holding groups 2w (low half) and 2w + 1 of the window.
+    __shared__ __attribute__((aligned(16))) uint32_t pbuf[2][2][kBN * 6];
 
     // Lane offsets (chunk 0); rows past M and columns past N read zero.
     // Activations go straight from memory to LDS: load i of wave w fills the
@@ -250,9 +255,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     for (int j = 0; j < 2; j++) {
         const uint32_t n = uint32_t(n0 + 64 * wave + 32 * j + l32);
         woff[j] = int(n) < N ? n * row_bytes + uint32_t(32 * kb) * BITS / 8u : kOutOfRange;
-        // (windows: the row's parameters from the split's first group on)
-        soff[j] = int(n) < N ? (n * uint32_t(G)) * PB + (PW ? uint32_t(c_begin) * 2u : uint32_t((32 * kb) / GS) * PB)
-                             : kOutOfRange;
+        // (not used with parameter windows, which have their own offsets)
+        soff[j] = int(n) < N ? (n * uint32_t(G)) * PB + uint32_t((32 * kb) / GS) * PB : kOutOfRange;
     }
     // (a lane's 32 codes lie in one group when the group size is a multiple of
     // 32 -- chunks start at multiples of 64, so its group is k0 / GS + 32 kb /
@@ -294,28 +298,39 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
             }
         }
     };
-    // Parameter window w (steps 3w .. 3w + 2, groups 6w .. 6w + 5 of the
-    // split): [slot][j][scale, bias][word]; step i reads word i % 3, half kgrp.
+    // Parameter window w (steps 6w .. 6w + 5, groups 12w .. 12w + 11 of the
+    // split): wave v of the workgroup (v = 4 kgrp + wave) loads rows
+    // 32 v .. 32 v + 31 of the tile, lane l the 12 bytes (6 groups) at half
+    // l % 2 of row 32 v + l / 2, into registers (one step) and then into LDS.
     typedef uint32_t q_u32x3 __attribute__((ext_vector_type(3)));
-    q_u32x3 pwin[2][2][2];
-    auto load_pw = [&](q_u32x3 (&P)[2][2], int w) __attribute__((always_inline)) {
-        const uint32_t kq = __builtin_amdgcn_readfirstlane(uint32_t(6 * w) * 2u);
+    q_u32x3 pst[2];
+    const int prow = 32 * (4 * kgrp + wave) + (lane >> 1);
+    const uint32_t poff = n0 + prow < N ? uint32_t(n0 + prow) * uint32_t(G) * PB + uint32_t(c_begin) * 2u +
+                                              uint32_t(lane & 1) * 12u
+                                        : kOutOfRange;
+    auto load_pw = [&](int w) __attribute__((always_inline)) {
+        const uint32_t kq = __builtin_amdgcn_readfirstlane(uint32_t(12 * w) * 2u);
+        pst[0] = __builtin_amdgcn_raw_buffer_load_b96(sr, poff, kq, 0);
+        pst[1] = __builtin_amdgcn_raw_buffer_load_b96(br, poff, kq, 0);
+    };
+    auto store_pw = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            P[j][0] = __builtin_amdgcn_raw_buffer_load_b96(sr, soff[j], kq, 0);
-            P[j][1] = __builtin_amdgcn_raw_buffer_load_b96(br, soff[j], kq, 0);
+        for (int a = 0; a < 2; a++) {
+            uint32_t* d = &pbuf[buf][a][prow * 6 + (lane & 1) * 3];
+            d[0] = pst[a][0];
+            d[1] = pst[a][1];
+            d[2] = pst[a][2];
         }
     };
     // Before a barrier: this wave's activation loads for the next step have
     // landed (only the newest step's loads, codes then activations, may still
-    // be in flight; memory operations complete in order).  With windows, a
-    // step that also requested a window has 4 more loads in flight.  (Per
-    // step: 2 NW code loads, 4 parameter loads -- 2 for MXFP4, none with
-    // windows -- and 4 activation loads.)
-    auto wait_a = [&](bool window_step) __attribute__((always_inline)) {
+    // be in flight; memory operations complete in order).  (Per step: 2 NW
+    // code loads, 4 parameter loads -- 2 for MXFP4, none with windows, whose
+    // loads come first in their step and so land before its barrier -- and 4
+    // activation loads.)
+    auto wait_a = [&]() __attribute__((always_inline)) {
         constexpr int n = 2 * NW + (MX ? 2 : PW ? 0 : 4) + 4;
-        if (PW && window_step) wait_vmcnt<n + 4>();
-        else wait_vmcnt<n>();
+        wait_vmcnt<n>();
     };
     auto barrier = [&]() __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
 
@@ -370,37 +385,44 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         }
     };
 
-    // Prologue: codes and activations of chunks 0 and 1 requested.
+    // Prologue: the first parameter window, codes and activations of chunks
+    // 0 and 1 requested; the window stored to LDS.
     Slot ring[kRing];
-    if constexpr (PW) load_pw(pwin[0], 0);
+    if constexpr (PW) load_pw(0);
     load_b(ring[0], 0);
     load_a(abuf0, 0);
     load_b(ring[1], 1);
     load_a(abuf1, 1);
-    wait_a(false);
+    if constexpr (PW) {
+        store_pw(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the window's LDS stores are done
+    }
+    wait_a();
     barrier();
 
     // Step i: request chunk i + 2's codes and activations (into the buffer
     // every wave finished reading before the last barrier) and, with windows,
-    // at i % 3 == 1 the next window; compute chunk i, wait for chunk i + 1's
-    // activations, synchronise.
+    // at i % 6 == 0 the next window (stored to the other LDS window at
+    // i % 6 == 1, ahead of that step's barrier); compute chunk i, wait for
+    // chunk i + 1's activations, synchronise.
     constexpr int U = PW ? 2 * kRing : kRing;
     for (int i0 = 0;; i0 += U) {
+        const int pw_cur = (i0 / U) & 1;  // this iteration's parameter window buffer
 #pragma unroll
         for (int r = 0; r < U; r++) {
             const int i = i0 + r;
             char* const bufs[3] = {abuf0, abuf1, abuf2};
-            const bool wstep = PW && r % 3 == 1;
             if constexpr (PW)
-                if (wstep) load_pw(pwin[(r / 3 + 1) % 2], i / 3 + 1);
+                if (r == 0) load_pw(i0 / U + 1);
             load_b(ring[(r + 2) % kRing], i + 2);
             load_a(bufs[(r + 2) % 3], i + 2);
             uint32_t sb[2], bb[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 if constexpr (PW) {
-                    sb[j] = pwin[(r / 3) % 2][j][0][r % 3] >> (16 * kgrp);
-                    bb[j] = pwin[(r / 3) % 2][j][1][r % 3] >> (16 * kgrp);
+                    const int col = 64 * wave + 32 * j + l32;
+                    sb[j] = pbuf[pw_cur][0][col * 6 + r] >> (16 * kgrp);
+                    bb[j] = pbuf[pw_cur][1][col * 6 + r] >> (16 * kgrp);
                 } else {
                     sb[j] = ring[r % kRing].s[j];
                     bb[j] = ring[r % kRing].b[j];
@@ -409,7 +431,13 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
             if (opaque_one() && 2 * i + kgrp < nloc) compute(ring[r % kRing], bufs[r % 3], sb, bb);
             else qmm_retire(ring[r % kRing]);
             if (i + 1 >= steps) goto done;
-            wait_a(wstep);
+            if constexpr (PW) {
+                if (r == 1) {
+                    store_pw(pw_cur ^ 1);
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) before the barrier
+                }
+            }
+            wait_a();
             barrier();
         }
     }
