@@ -346,10 +346,9 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = f32x16{};
 
-    auto compute = [&](const Slot& S, const char* buf, const uint32_t* sbits, const uint32_t* bbits)
+    // Codes of one chunk -> the B operands of its 4 MFMA steps (2 column blocks).
+    auto dequant = [&](const Slot& S, const uint32_t* sbits, const uint32_t* bbits, q_u32x4 (&bq)[2][4])
                        __attribute__((always_inline)) {
-        asm volatile("" ::: "memory");
-        q_u32x4 bq[2][4];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             if constexpr (MX) {
@@ -371,6 +370,10 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
                                                   t < 2 ? s0 : s1, t < 2 ? b0 : b1);
             }
         }
+    };
+    // The chunk's 32 MFMAs (4 steps x 4 row blocks x 2 column blocks), A
+    // operands from this K-group's part of the activation buffer.
+    auto mma = [&](const q_u32x4 (&bq)[2][4], const char* buf) __attribute__((always_inline)) {
         const char* base = buf + gofs;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -382,6 +385,22 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
             for (int mi = 0; mi < 4; mi++)
 #pragma unroll
                 for (int j = 0; j < 2; j++) acc[mi][j] = QmmAct<XT>::mfma(bq[j][t], a[mi], acc[mi][j]);
+        }
+    };
+    // Scale and bias words of this K-group's chunk at unrolled step r (0 ..
+    // U; U is the next window's first step) of the current window.
+    auto params = [&](const Slot& S, int r, int pw_cur, uint32_t* sb, uint32_t* bb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            if constexpr (PW) {
+                const int col = 64 * wave + 32 * j + l32;
+                const int buf = r < 6 ? pw_cur : pw_cur ^ 1, w = r < 6 ? r : r - 6;
+                sb[j] = pbuf[buf][0][col * 6 + w] >> (16 * kgrp);
+                bb[j] = pbuf[buf][1][col * 6 + w] >> (16 * kgrp);
+            } else {
+                sb[j] = S.s[j];
+                bb[j] = S.b[j];
+            }
         }
     };
 
@@ -403,45 +422,80 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // Step i: request chunk i + 2's codes and activations (into the buffer
     // every wave finished reading before the last barrier) and, with windows,
     // at i % 6 == 0 the next window (stored to the other LDS window at
-    // i % 6 == 1, ahead of that step's barrier); compute chunk i, wait for
-    // chunk i + 1's activations, synchronise.
+    // i % 6 == 1, ahead of that step's barrier); then the two K-groups work
+    // in opposite phase, so that on every SIMD one wave issues MFMAs while the
+    // other dequantizes: the first (KG = 0) multiplies its chunk of step i
+    // (dequantized in step i - 1) and then dequantizes its chunk of step
+    // i + 1, the second dequantizes its chunk of step i and then multiplies
+    // it.  Wait for chunk i + 1's activations, synchronise.  The schedule is
+    // a constant of each copy of the loop, so each has its own register plan.
+    // 8-bit codes (twice the code registers) keep the in-step order for both
+    // K-groups, dequantization and MFMAs interleaved by the compiler: with
+    // the dequantized operands held across the barrier they run out of
+    // registers.
+    //   SCHED 0: multiply step i, then dequantize step i + 1 (anti-phase first K-group)
+    //   SCHED 1: dequantize step i, then multiply it, kept apart (anti-phase second K-group)
+    //   SCHED 2: dequantize step i and multiply it, interleaved (both K-groups, 8-bit codes)
     constexpr int U = PW ? 2 * kRing : kRing;
-    for (int i0 = 0;; i0 += U) {
-        const int pw_cur = (i0 / U) & 1;  // this iteration's parameter window buffer
-#pragma unroll
-        for (int r = 0; r < U; r++) {
-            const int i = i0 + r;
-            char* const bufs[3] = {abuf0, abuf1, abuf2};
-            if constexpr (PW)
-                if (r == 0) load_pw(i0 / U + 1);
-            load_b(ring[(r + 2) % kRing], i + 2);
-            load_a(bufs[(r + 2) % 3], i + 2);
+    constexpr bool kAnti = BITS == 4;
+    auto main_loop = [&](auto sched_c) __attribute__((always_inline)) {
+        constexpr int SCHED = decltype(sched_c)::value;
+        q_u32x4 bq[2][4];  // dequantized B operands
+        if constexpr (SCHED == 0) {
             uint32_t sb[2], bb[2];
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                if constexpr (PW) {
-                    const int col = 64 * wave + 32 * j + l32;
-                    sb[j] = pbuf[pw_cur][0][col * 6 + r] >> (16 * kgrp);
-                    bb[j] = pbuf[pw_cur][1][col * 6 + r] >> (16 * kgrp);
-                } else {
-                    sb[j] = ring[r % kRing].s[j];
-                    bb[j] = ring[r % kRing].b[j];
-                }
-            }
-            if (opaque_one() && 2 * i + kgrp < nloc) compute(ring[r % kRing], bufs[r % 3], sb, bb);
-            else qmm_retire(ring[r % kRing]);
-            if (i + 1 >= steps) goto done;
-            if constexpr (PW) {
-                if (r == 1) {
-                    store_pw(pw_cur ^ 1);
-                    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) before the barrier
-                }
-            }
-            wait_a();
-            barrier();
+            params(ring[0], 0, 0, sb, bb);
+            dequant(ring[0], sb, bb, bq);
         }
+        for (int i0 = 0;; i0 += U) {
+            const int pw_cur = (i0 / U) & 1;  // this iteration's parameter window buffer
+#pragma unroll
+            for (int r = 0; r < U; r++) {
+                const int i = i0 + r;
+                char* const bufs[3] = {abuf0, abuf1, abuf2};
+                if constexpr (PW)
+                    if (r == 0) load_pw(i0 / U + 1);
+                load_b(ring[(r + 2) % kRing], i + 2);
+                load_a(bufs[(r + 2) % 3], i + 2);
+                if constexpr (SCHED == 0) {
+                    // (the first K-group has a chunk at every step)
+                    mma(bq, bufs[r % 3]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (opaque_one() && i + 1 < steps) {
+                        uint32_t sb[2], bb[2];
+                        params(ring[(r + 1) % kRing], r + 1, pw_cur, sb, bb);
+                        dequant(ring[(r + 1) % kRing], sb, bb, bq);
+                    } else {
+                        qmm_retire(ring[(r + 1) % kRing]);
+                    }
+                } else {
+                    if (opaque_one() && 2 * i + kgrp < nloc) {
+                        uint32_t sb[2], bb[2];
+                        params(ring[r % kRing], r, pw_cur, sb, bb);
+                        dequant(ring[r % kRing], sb, bb, bq);
+                        if constexpr (SCHED == 1) __builtin_amdgcn_sched_barrier(0);
+                        mma(bq, bufs[r % 3]);
+                    } else {
+                        qmm_retire(ring[r % kRing]);
+                    }
+                }
+                if (i + 1 >= steps) return;
+                if constexpr (PW) {
+                    if (r == 1) {
+                        store_pw(pw_cur ^ 1);
+                        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) before the barrier
+                    }
+                }
+                wait_a();
+                barrier();
+            }
+        }
+    };
+    if constexpr (kAnti) {
+        if (kgrp == 0) main_loop(std::integral_constant<int, 0>{});
+        else main_loop(std::integral_constant<int, 1>{});
+    } else {
+        main_loop(std::integral_constant<int, 2>{});
     }
-done:
     // Every load has landed (the ring buffers are reused below).
     __builtin_amdgcn_s_waitcnt(0);
     // The second K-group's sums go to LDS, one row block (32 KiB) at a time
