@@ -432,12 +432,15 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // 8-bit codes (twice the code registers) keep the in-step order for both
     // K-groups, dequantization and MFMAs interleaved by the compiler: with
     // the dequantized operands held across the barrier they run out of
-    // registers.
+    // registers.  So do 4-bit codes at group sizes 16 and 32 with biases,
+    // whose per-step parameter loads sit in the ring (measured 2-5 % slower
+    // in opposite phase; group 64 with windows, group 128 and MXFP4 gain
+    // 4-16 %).
     //   SCHED 0: multiply step i, then dequantize step i + 1 (anti-phase first K-group)
     //   SCHED 1: dequantize step i, then multiply it, kept apart (anti-phase second K-group)
     //   SCHED 2: dequantize step i and multiply it, interleaved (both K-groups, 8-bit codes)
     constexpr int U = PW ? 2 * kRing : kRing;
-    constexpr bool kAnti = BITS == 4;
+    constexpr bool kAnti = BITS == 4 && (PW || GS == 128 || MX);
     auto main_loop = [&](auto sched_c) __attribute__((always_inline)) {
         constexpr int SCHED = decltype(sched_c)::value;
         q_u32x4 bq[2][4];  // dequantized B operands
