@@ -429,18 +429,20 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // i + 1, the second dequantizes its chunk of step i and then multiplies
     // it.  Wait for chunk i + 1's activations, synchronise.  The schedule is
     // a constant of each copy of the loop, so each has its own register plan.
-    // 8-bit codes (twice the code registers) keep the in-step order for both
-    // K-groups, dequantization and MFMAs interleaved by the compiler: with
-    // the dequantized operands held across the barrier they run out of
-    // registers.  So do 4-bit codes at group sizes 16 and 32 with biases,
-    // whose per-step parameter loads sit in the ring (measured 2-5 % slower
-    // in opposite phase; group 64 with windows, group 128 and MXFP4 gain
-    // 4-16 %).
+    // With 8-bit codes (twice the code registers) the second K-group lets
+    // the compiler interleave its dequantization with its MFMAs (SCHED 2)
+    // instead of keeping them apart.  4-bit codes at group sizes 16 and 32
+    // with biases, whose per-step parameter loads sit in the ring, and 8-bit
+    // codes without windows keep the in-step order for both K-groups (SCHED 2
+    // for both; opposite phase measured 2-5 % slower there, against 4-16 %
+    // faster for 4-bit group 64 with windows, group 128 and MXFP4, and up to
+    // 8 % for 8-bit group 64 with windows).
     //   SCHED 0: multiply step i, then dequantize step i + 1 (anti-phase first K-group)
     //   SCHED 1: dequantize step i, then multiply it, kept apart (anti-phase second K-group)
-    //   SCHED 2: dequantize step i and multiply it, interleaved (both K-groups, 8-bit codes)
+    //   SCHED 2: dequantize step i and multiply it, interleaved by the compiler
     constexpr int U = PW ? 2 * kRing : kRing;
-    constexpr bool kAnti = BITS == 4 && (PW || GS == 128 || MX);
+    constexpr bool kAnti = (BITS == 4 && (PW || GS == 128 || MX)) || (BITS == 8 && PW);
+    constexpr int kSecond = BITS == 8 ? 2 : 1;  // the second K-group's schedule in opposite phase
     auto main_loop = [&](auto sched_c) __attribute__((always_inline)) {
         constexpr int SCHED = decltype(sched_c)::value;
         q_u32x4 bq[2][4];  // dequantized B operands
@@ -495,7 +497,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     };
     if constexpr (kAnti) {
         if (kgrp == 0) main_loop(std::integral_constant<int, 0>{});
-        else main_loop(std::integral_constant<int, 1>{});
+        else main_loop(std::integral_constant<int, kSecond>{});
     } else {
         main_loop(std::integral_constant<int, 2>{});
     }
