@@ -67,6 +67,9 @@ class ActivationPrologue(ctypes.Structure):
 SIGNATURES["eq_quantized_matmul_batched_prologue"] = (
     [ctypes.POINTER(QmmProblem), _i32, _i64, _b, _i32, _i32, ctypes.c_char_p, _i32, _i32,
      ctypes.POINTER(ActivationPrologue), _vp], _i32)
+SIGNATURES["eq_quantized_matmul_swiglu"] = (
+    [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, ctypes.c_char_p, _i32, _i32, ctypes.POINTER(ActivationPrologue),
+     _vp], _i32)
 
 _lib = None
 _lock = threading.Lock()

@@ -637,6 +637,86 @@ extern "C" int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* proble
     return check_launch("quantized_matmul_batched_prologue");
 }
 
+extern "C" int eq_quantized_matmul_swiglu(void* out, const void* x, const uint32_t* w, const void* scales,
+                                          const void* biases, int64_t F, int64_t K, int group_size, int bits,
+                                          const char* mode, int x_dtype, int scale_dtype,
+                                          const eq_activation_prologue* prologue, eq_stream_t stream) {
+    clear_error();
+    if (check_mode(mode) || check_gs_bits(group_size, bits)) return 1;
+    if (prologue && prologue->kind != EQ_PROLOGUE_RMS_NORM) {
+        set_error("swiglu: the prologue, when given, must be EQ_PROLOGUE_RMS_NORM");
+        return 1;
+    }
+    if (x_dtype != EQ_DTYPE_BF16 || scale_dtype != EQ_DTYPE_BF16 || group_size != 64 || (bits != 4 && bits != 8)) {
+        set_error("swiglu: supported for bf16 activations and scales, group size 64, 4- or 8-bit codes");
+        return 1;
+    }
+    if (!out || !x || !w || !scales) {
+        set_error("swiglu: null pointer argument");
+        return 1;
+    }
+    if (F <= 0 || F % 8 != 0 || 2 * F > INT32_MAX || K <= 0 || K % 64 != 0 || K > INT32_MAX) {
+        set_error("swiglu: F must be a positive multiple of 8 and K a positive multiple of 64");
+        return 1;
+    }
+    if (!aligned(x, 16) || !aligned(w, 16)) {
+        set_error("swiglu: x and w must be 16-byte aligned");
+        return 1;
+    }
+    const int64_t bytes = K * 2;
+    if (prologue) {
+        const eq_activation_prologue& pr = *prologue;
+        if (K > 4096) {
+            set_error("swiglu: the rms_norm prologue takes rows of at most 4096 values");
+            return 1;
+        }
+        if (!pr.weight || !aligned(pr.weight, 16) || (pr.second && !aligned(pr.second, 16)) ||
+            (pr.hidden_out && !aligned(pr.hidden_out, 16))) {
+            set_error("swiglu: rms_norm needs a weight and 16-byte aligned vectors");
+            return 1;
+        }
+        if (!(pr.eps >= 0.f)) {
+            set_error("swiglu: eps must be >= 0");
+            return 1;
+        }
+    }
+    // every workgroup reads x (and the prologue's inputs) and the weights
+    // while others write out (and hidden_out)
+    const int64_t G = K / group_size, N = 2 * F;
+    std::vector<ByteRange> reads{{x, bytes}, {w, N * K * bits / 8}, {scales, N * G * 2}, {biases, N * G * 2}};
+    std::vector<ByteRange> writes{{out, F * 2}};
+    if (prologue) {
+        reads.push_back({prologue->second, bytes});
+        reads.push_back({prologue->weight, bytes});
+        writes.push_back({prologue->hidden_out, bytes});
+    }
+    for (size_t i = 0; i < writes.size(); i++) {
+        for (const ByteRange& r : reads)
+            if (ranges_overlap(writes[i], r)) {
+                set_error("swiglu: an output (out or hidden_out) overlaps an input");
+                return 1;
+            }
+        for (size_t j = i + 1; j < writes.size(); j++)
+            if (ranges_overlap(writes[i], writes[j])) {
+                set_error("swiglu: out and hidden_out must not overlap");
+                return 1;
+            }
+    }
+    const QmvSpec spec{static_cast<const uint16_t*>(x), w, scales, biases, static_cast<uint16_t*>(out), int(N), int(K),
+                       int(N)};
+    QmvPrologue q{};
+    if (prologue)
+        q = QmvPrologue{prologue->kind, static_cast<const uint16_t*>(prologue->second),
+                        static_cast<const uint16_t*>(prologue->weight), static_cast<uint16_t*>(prologue->hidden_out),
+                        prologue->eps};
+    if (!launch_qmv_swiglu(bits, spec, prologue ? &q : nullptr, reinterpret_cast<hipStream_t>(stream))) {
+        set_error("swiglu: this shape does not fit one decode launch (K a multiple of the code block, shared LDS "
+                  "budget)");
+        return 1;
+    }
+    return check_launch("quantized_matmul_swiglu");
+}
+
 extern "C" int eq_quantize(uint32_t* w_out, void* scales, void* biases, const void* w, int64_t rows, int64_t cols,
                            int group_size, int bits, const char* mode, int dtype, eq_stream_t stream) {
     clear_error();

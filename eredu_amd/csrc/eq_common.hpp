@@ -76,6 +76,9 @@ struct QmvPrologue {
 };
 bool launch_qmv_prologue(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, const QmvPrologue& pro,
                          hipStream_t st);
+// One interleaved gate/up problem (group 64, bf16) with the SwiGLU epilogue,
+// optionally after the RMSNorm prologue (pro: null or kind 2).
+bool launch_qmv_swiglu(int bits, const QmvSpec& spec, const QmvPrologue* pro, hipStream_t st);
 
 // ---------------------------------------------------------------- device side
 

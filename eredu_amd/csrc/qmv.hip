@@ -838,6 +838,15 @@ __device__ __forceinline__ u32x4 qmv_silu_mul8(const u32x4 g, const u32x4 u) {
     return r;
 }
 
+// qmv_silu_mul8 on one pair of bf16 values (bits), the result's bits.
+__device__ __forceinline__ uint16_t qmv_silu_mul1(uint32_t g, uint32_t u) {
+    const float x = bf16_bits_to_f32(g & 0xffffu);
+    const float up = bf16_bits_to_f32(u & 0xffffu);
+    const float sg = silu_sigmoid_bf16(x);
+    const float sl = float(static_cast<__bf16>(x * sg));
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(sl * up));
+}
+
 // a + b on 8 bf16 values, each sum rounded to bf16 (the residual add).
 __device__ __forceinline__ u32x4 qmv_add8(const u32x4 a, const u32x4 b) {
     u32x4 r;
@@ -877,7 +886,12 @@ __device__ __forceinline__ u32x4 qmv_norm8(const u32x4 a, const u32x4 w, float i
 // With PRO = 2 the staged row (K <= 2 * 16 * 64 * NW values) is one round of
 // at most 2 chunks per thread, kept in registers across the workgroup's sum
 // of squares.
-template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL, int PRO = 0, typename XT = BF16T>
+// EPI: epilogue, 0 none, 1 SwiGLU: the (one) problem's matrix holds, in each
+// 16-row tile t, gate rows 8t .. 8t + 7 then up rows 8t .. 8t + 7, and the
+// tile writes y[8t + i] = silu(bf16(gate_i)) * bf16(up_i) with the roundings
+// of qmv_silu_mul8 (M = 1).
+template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL, int PRO = 0, typename XT = BF16T,
+          int EPI = 0>
 __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
     const QmvBatch batch) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -1088,7 +1102,14 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             float v = 0.f;
 #pragma unroll
             for (int i = 0; i < NW; i++) v += slot[(i * M + m) * 16 + n];
-            pr.y[int64_t(m) * pr.ldy + V.n0 + n] = QmvAct<XT>::out(v);
+            if constexpr (EPI == 1) {
+                static_assert(MREG == 1 && std::is_same<XT, BF16T>::value, "SwiGLU epilogue: one bf16 row");
+                // row n + 8 (the up row of gate row n), from the lane holding it
+                const float u = __shfl(v, int(threadIdx.x) | 8);
+                if (n < 8) pr.y[(V.n0 >> 1) + n] = qmv_silu_mul1(f32_to_bf16_bits(v), f32_to_bf16_bits(u));
+            } else {
+                pr.y[int64_t(m) * pr.ldy + V.n0 + n] = QmvAct<XT>::out(v);
+            }
         }
         iter++;
         acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1467,6 +1488,36 @@ bool launch_qmv_prologue(int bits, int gs, int scale_dtype, const QmvSpec* specs
         if (bits == 4) return launch_qmv_pro_t<4, 64, BF16T, 2>(specs, count, pro, st);
         if (bits == 8) return launch_qmv_pro_t<8, 64, BF16T, 2>(specs, count, pro, st);
     }
+    return false;
+}
+
+// The SwiGLU launch: one problem (an interleaved gate/up matrix, N = 2F),
+// one activation row, whole blocks, optionally the RMSNorm prologue.
+template <int BITS, int PRO>
+static bool launch_qmv_swiglu_t(const QmvSpec& spec, const QmvPrologue* pro, hipStream_t st) {
+    QmvLdsPlan plan;
+    if (!plan_qmv_lds<BITS, 64, BF16T>(&spec, 1, 1, plan) || plan.B.nstage != 1 || plan.B.phase_spans != 0 ||
+        !plan.vec || plan.tail)
+        return false;
+    if (PRO == 2) {
+        if (spec.K > 2 * 8 * 64 * kQmvLdsWaves) return false;
+        plan.B.pro_second = pro->second;
+        plan.B.pro_weight = pro->weight;
+        plan.B.pro_hidden_out = pro->hidden_out;
+        plan.B.pro_eps = pro->eps;
+    }
+    auto kernel = qmv_lds_kernel<BITS, 64, BF16T, 1, true, false, PRO, BF16T, 1>;
+    if (plan.lds > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  plan.lds);
+    kernel<<<dim3(unsigned(plan.grid)), dim3(64 * plan.waves), size_t(plan.lds), st>>>(plan.B);
+    return true;
+}
+
+bool launch_qmv_swiglu(int bits, const QmvSpec& spec, const QmvPrologue* pro, hipStream_t st) {
+    if (pro && pro->kind != 2) return false;
+    if (bits == 4) return pro ? launch_qmv_swiglu_t<4, 2>(spec, pro, st) : launch_qmv_swiglu_t<4, 0>(spec, pro, st);
+    if (bits == 8) return pro ? launch_qmv_swiglu_t<8, 2>(spec, pro, st) : launch_qmv_swiglu_t<8, 0>(spec, pro, st);
     return false;
 }
 

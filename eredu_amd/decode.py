@@ -168,6 +168,39 @@ class QLinear:
         return self.w.shape[1] * 32 // self.bits
 
 
+def interleave_gate_up(gate: QLinear, up: QLinear) -> QLinear:
+    """The gate and up projections as one packed matrix [2F, K] in
+    eq_quantized_matmul_swiglu's layout: rows 16t .. 16t + 7 are gate rows
+    8t .. 8t + 7, rows 16t + 8 .. 16t + 15 up rows 8t .. 8t + 7 (codes, scales
+    and biases moved row by row; a copy on the device)."""
+    if (gate.N != up.N or gate.K != up.K or gate.bits != up.bits or gate.group_size != up.group_size or
+            (gate.biases is None) != (up.biases is None) or gate.N % 8 != 0):
+        raise _native.EreduError("gate and up must share shape, bits, group size and bias presence, N % 8 == 0")
+
+    def il(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        F = a.shape[0]
+        return torch.stack((a.reshape(F // 8, 8, -1), b.reshape(F // 8, 8, -1)), dim=1).reshape(2 * F, -1).contiguous()
+
+    return QLinear(il(gate.w, up.w), il(gate.scales, up.scales),
+                   il(gate.biases, up.biases) if gate.biases is not None else None, gate.bits, gate.group_size)
+
+
+def gate_up_swiglu(x: torch.Tensor, gate_up: QLinear, prologue=None) -> torch.Tensor:
+    """silu(x . Wg^T) * (x . Wu^T) for one bf16 row x [K], gate_up from
+    interleave_gate_up (C ABI: eq_quantized_matmul_swiglu); prologue: an
+    _native.ActivationPrologue (RMS_NORM) or None."""
+    _bf16(x, "x")
+    F = gate_up.N // 2
+    out = torch.empty((F,), dtype=torch.bfloat16, device=x.device)
+    n = _native
+    check(n.lib().eq_quantized_matmul_swiglu(
+        out.data_ptr(), x.data_ptr(), gate_up.w.data_ptr(), gate_up.scales.data_ptr(),
+        gate_up.biases.data_ptr() if gate_up.biases is not None else None, F, gate_up.K, gate_up.group_size,
+        gate_up.bits, b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16,
+        ctypes.byref(prologue) if prologue is not None else None, _stream()))
+    return out
+
+
 @dataclass
 class DecoderLayer:
     in_norm: torch.Tensor
@@ -191,10 +224,14 @@ class LlamaDecoder:
     enqueue on the current stream and allocate nothing.
 
     ``fused`` (default: when the shapes allow it) folds each residual add +
-    RMSNorm into the launch of the projections that consume it, and SiLU-mul
-    into the down projection's launch (eq_quantized_matmul_batched_prologue):
-    6 launches per layer instead of 9.  The hidden state then alternates
-    between two buffers (every workgroup of a launch reads the old one)."""
+    RMSNorm into the launch of the projections that consume it
+    (eq_quantized_matmul_batched_prologue), and SiLU-mul into the gate/up
+    launch (eq_quantized_matmul_swiglu, on an interleaved copy of each
+    layer's gate and up matrices made at construction; into the down
+    projection's launch instead when K is not a whole number of the decode
+    kernel's code blocks): 6 launches per layer instead of 9.  The hidden
+    state then alternates between two buffers (every workgroup of a launch
+    reads the old one)."""
 
     def __init__(self, layers: Sequence[DecoderLayer], embed: torch.Tensor, final_norm: torch.Tensor,
                  lm_head: QLinear, *, n_heads: int, n_kv_heads: int, eps: float, freqs: np.ndarray, max_seq: int,
@@ -234,6 +271,7 @@ class LlamaDecoder:
         if self.fused and not can_fuse:
             raise _native.EreduError("fused decode needs hidden <= 4096, group size 64, 4/8-bit codes, bf16 scales")
         self.x2 = e(H)  # the hidden state's second buffer (fused mode)
+        self.swiglu = False  # (fused mode: SiLU-mul in the gate/up launch)
         # grouped problems (pointers fixed for the decoder's lifetime)
         n = _native
         self._qkv, self._gu = [], []
@@ -270,6 +308,12 @@ class LlamaDecoder:
                 self._pro_in.append(pin)
                 self._pro_post.append(ppost)
             self._pro_silu = n.ActivationPrologue(n.EQ_PROLOGUE_SILU_MUL, self.up.data_ptr(), None, None, 0.0)
+            # SwiGLU in the gate/up launch: K a whole number of code blocks
+            # (512 values at 4 bits, 256 at 8) and F % 8 == 0
+            self.swiglu = all(Lr.gate.K % (512 if Lr.gate.bits == 4 else 256) == 0 and Lr.gate.N % 8 == 0 and
+                              Lr.gate.bits == Lr.up.bits and (Lr.gate.biases is None) == (Lr.up.biases is None)
+                              for Lr in self.layers)
+            self._gu_il = [interleave_gate_up(Lr.gate, Lr.up) for Lr in self.layers] if self.swiglu else []
             self._flm = (n.QmmProblem * 1)()
             self._flm[0] = self._problem(lm_head, self.x2, self.logits)
             self._pro_final = n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, self.down.data_ptr(),
@@ -348,8 +392,16 @@ class LlamaDecoder:
             self._pro(self._fqkv[li], 3, Lr.q, self._pro_in[li], st)
             self._attend(li, pos, st)
             self._linear(Lr.o, self.att, self.o, st)
-            self._pro(self._fgu[li], 2, Lr.gate, self._pro_post[li], st)
-            self._pro(self._fdown[li], 1, Lr.down, self._pro_silu, st)
+            if self.swiglu:
+                gu = self._gu_il[li]
+                check(L.eq_quantized_matmul_swiglu(
+                    self.act.data_ptr(), self.x.data_ptr(), gu.w.data_ptr(), gu.scales.data_ptr(),
+                    gu.biases.data_ptr() if gu.biases is not None else None, self.ffn, gu.K, gu.group_size, gu.bits,
+                    b"affine", bf, bf, ctypes.byref(self._pro_post[li]), st))
+                self._linear(Lr.down, self.act, self.down, st)
+            else:
+                self._pro(self._fgu[li], 2, Lr.gate, self._pro_post[li], st)
+                self._pro(self._fdown[li], 1, Lr.down, self._pro_silu, st)
         self._pro(self._flm, 1, self.lm_head, self._pro_final, st)
         check(L.eq_argmax(self.token.data_ptr(), self.logits.data_ptr(), 1, self.lm_head.N, bf, st))
 

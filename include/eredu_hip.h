@@ -300,6 +300,31 @@ int eq_quantized_matmul_batched_prologue(const eq_qmm_problem* problems, int cou
                                          const eq_activation_prologue* prologue, eq_stream_t stream);
 
 /*
+ * The gate/up projection of a SwiGLU MLP with the activation folded into the
+ * launch (batch 1):
+ *   out[f] = silu(g_f) * u_f,  g_f = bf16(x' . Wg[f]),  u_f = bf16(x' . Wu[f]),
+ * each op rounded to bf16 as in eq_silu_mul (Mlp::hidden,
+ * eredu-architectures/src/llama.rs:414-422), x' = x or, with `prologue`
+ * (kind EQ_PROLOGUE_RMS_NORM only; NULL for none), the residual add + RMSNorm
+ * of eq_quantized_matmul_batched_prologue.  w / scales / biases hold the two
+ * projections interleaved in blocks of 8 rows: rows 16t .. 16t + 7 are gate
+ * rows 8t .. 8t + 7 and rows 16t + 8 .. 16t + 15 are up rows 8t .. 8t + 7
+ * ([2F, K] in the affine layout of eq_quantized_matmul, transpose = true);
+ * the same packed rows, moved, so that a decode workgroup's 16-row tile
+ * holds both halves of 8 outputs.  Results equal eq_quantized_matmul_batched
+ * on the two projections followed by eq_silu_mul, bit for bit.  No
+ * counterpart in the reference's C ABI (it folds the MLX ops between the
+ * gate/up and down projections into one launch).  Supported: bf16 x and
+ * scales, group size 64, 4/8-bit, F % 8 == 0, K a multiple of the decode
+ * kernel's code block (512 values at 4 bits, 256 at 8), K <= 4096 with the
+ * prologue; x and w 16-byte aligned; out (F values) must not overlap any
+ * input.
+ */
+int eq_quantized_matmul_swiglu(void* out, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                               int64_t F, int64_t K, int group_size, int bits, const char* mode, int x_dtype,
+                               int scale_dtype, const eq_activation_prologue* prologue, eq_stream_t stream);
+
+/*
  * Decode-step operations around the quantized projections of a Llama-shaped
  * decoder at batch 1 (configs[4] of the measurement plan).  bf16 only
  * (dtype must be EQ_DTYPE_BF16); no counterpart in the quantized-linear C ABI

@@ -28,7 +28,8 @@ def test_header_declares_the_boundary():
          "eq_gguf_convert_affine", "eq_gguf_dequantize", "eq_rms_norm", "eq_rope_attention_decode", "eq_silu_mul",
          "eq_embedding", "eq_argmax", "eq_quantized_matmul_batched_prologue", "eq_quantize",
          "eq_gguf_linear", "eq_gather_qmm", "eq_rope_attention_decode_noalloc", "eq_gguf_convert_mxfp4",
-         "eq_gguf_embedding", "eq_gguf_grouped_linear", "eq_rope_attention_decode_at", "eq_advance_position"]
+         "eq_gguf_embedding", "eq_gguf_grouped_linear", "eq_rope_attention_decode_at", "eq_advance_position",
+         "eq_quantized_matmul_swiglu"]
     )
 
 
@@ -229,6 +230,23 @@ def test_decode_ops_reject_bad_arguments():
     _rejects(att_at(max_seq=131073), "131072")
     _rejects(att_at(dt=f32), "only bf16")
     _rejects(L.eq_advance_position(None, None), "null")
+    # gate/up with the SwiGLU epilogue: shape, layout and prologue rules, before any launch
+    import ctypes
+    from eredu_amd import _native as n
+    sw = lambda pro=None, **k: L.eq_quantized_matmul_swiglu(
+        k.get("out", 1 << 20), 16, 16, 1 << 21, None, k.get("F", 512), k.get("K", 4096), k.get("gs", 64),
+        k.get("bits", 4), b"affine", k.get("xdt", bf16), bf16, ctypes.byref(pro) if pro is not None else None, None)
+    _rejects(sw(F=500), "multiple of 8")
+    _rejects(sw(K=100), "multiple of 64")
+    _rejects(sw(gs=32), "group size 64")
+    _rejects(sw(bits=3), "4- or 8-bit")
+    _rejects(sw(xdt=f32), "bf16")
+    _rejects(sw(out=None), "null")
+    _rejects(sw(n.ActivationPrologue(n.EQ_PROLOGUE_SILU_MUL, 16, None, None, 0.0)), "RMS_NORM")
+    _rejects(sw(n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, None, 16, None, 1e-5), K=8192), "4096")
+    _rejects(sw(n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, None, 16, None, -1.0)), "eps")
+    # the output overlapping the packed codes
+    _rejects(sw(out=64), "overlaps")
     # silu_mul, embedding, argmax
     _rejects(L.eq_silu_mul(16, 16, 16, 12, bf16, None), "multiple of 8")
     _rejects(L.eq_embedding(16, 16, 16, 70000, 100, 64, bf16, None), "n_tokens")

@@ -226,6 +226,7 @@ def tiny_model(seed=0, layers=2, n_heads=4, n_kv=2, ffn=1024, vocab=1024, max_se
 def test_decode_step_end_to_end(cuda, fused):
     host, dec, kcs, vcs = tiny_model(fused=fused)
     assert dec.fused == fused
+    assert dec.swiglu == fused  # the fused step folds SiLU-mul into the gate/up launch
     kcs = [k.copy() for k in kcs]
     vcs = [v.copy() for v in vcs]
     token = 7
@@ -395,6 +396,77 @@ def test_prologue_rms_norm(cuda, K, with_residual):
         ref = orc.quantized_matmul_f64(h_ref, orc.BF16, w, s, b, orc.BF16, True, 64, 4, N, K_)
         ok, worst, _ = orc.matmul_within_tolerance(host_f32(y).reshape(1, -1), ref, out_is_bf16=True)
         assert ok, worst
+
+
+@pytest.mark.parametrize("nbits", [4, 8])
+@pytest.mark.parametrize("F,K", [(1024, 512), (14336, 4096)])
+@pytest.mark.parametrize("with_norm", [False, True])
+def test_swiglu_equals_gate_up_then_silu_mul(cuda, nbits, F, K, with_norm):
+    """eq_quantized_matmul_swiglu on the interleaved gate/up matrix equals the
+    gate and up projections (eq_quantized_matmul_batched, or its RMSNorm
+    prologue) followed by eq_silu_mul, bit for bit; the RMSNorm prologue's
+    hidden_out bit-equal too; and the result within the matmul rule of the
+    oracle (f64 projections of the oracle's normalized row, the oracle's
+    silu_mul roundings)."""
+    from eredu_amd import _native as n
+
+    print(f"[case] swiglu bits={nbits} F={F} K={K} norm={with_norm}", flush=True)
+    (gate, (wg, sg, bg)), (up, (wu, su, bu)) = _qlin(F, K, 300 + nbits, nbits), _qlin(F, K, 400 + nbits, nbits)
+    gu = E.interleave_gate_up(gate, up)
+    xb, rb = randn_bits(K, 11), randn_bits(K, 12)
+    wb = bits(1.0 + 0.1 * np.random.default_rng(13).standard_normal(K))
+    x, r, nw = dev_bf16(xb), dev_bf16(rb), dev_bf16(wb)
+    hid, hid2 = (torch.empty(K, dtype=torch.bfloat16, device="cuda") for _ in range(2))
+    g, u = (torch.empty(F, dtype=torch.bfloat16, device="cuda") for _ in range(2))
+    if with_norm:
+        pro = n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, r.data_ptr(), nw.data_ptr(), hid.data_ptr(), 1e-5)
+        pro2 = n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, r.data_ptr(), nw.data_ptr(), hid2.data_ptr(), 1e-5)
+        out = E.gate_up_swiglu(x, gu, pro)
+        _prologue_call([(x, gate, g), (x, up, u)], [gate, up], pro2)
+    else:
+        out = E.gate_up_swiglu(x, gu)
+        arr = (n.QmmProblem * 2)()
+        for i, (lin, y) in enumerate(((gate, g), (up, u))):
+            arr[i] = n.QmmProblem(y.data_ptr(), x.data_ptr(), lin.w.data_ptr(), lin.scales.data_ptr(),
+                                  lin.biases.data_ptr(), F, K)
+        n.check(n.lib().eq_quantized_matmul_batched(arr, 2, 1, True, 64, nbits, b"affine", n.EQ_DTYPE_BF16,
+                                                    n.EQ_DTYPE_BF16, None))
+    ref = E.silu_mul(g, u)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    if with_norm:
+        assert torch.equal(hid.view(torch.int16), hid2.view(torch.int16))
+        _, h_ref = D.rms_norm_bf16(xb, wb, 1e-5, rb)
+    else:
+        h_ref = xb
+    gr = orc.quantized_matmul_f64(h_ref, orc.BF16, wg, sg, bg, orc.BF16, True, 64, nbits, F, K)
+    ur = orc.quantized_matmul_f64(h_ref, orc.BF16, wu, su, bu, orc.BF16, True, 64, nbits, F, K)
+    act_ref = orc.bf16_bits_to_f32(D.silu_mul_bf16(orc.f32_to_bf16_bits(gr.astype(np.float32)),
+                                                   orc.f32_to_bf16_bits(ur.astype(np.float32)))).astype(np.float64)
+    got = host_f32(out).astype(np.float64)
+    rms = float(np.sqrt(np.mean(act_ref.reshape(-1) ** 2)))
+    assert np.max(np.abs(got - act_ref.reshape(-1))) <= 2e-2 * rms + 1e-6
+
+
+def test_swiglu_rejects_unsupported(cuda):
+    from eredu_amd import _native as n
+    import ctypes
+
+    (gate, _), (up, _) = _qlin(512, 8192, 5), _qlin(512, 8192, 6)
+    gu = E.interleave_gate_up(gate, up)
+    x = dev_bf16(randn_bits(8192, 1))
+    out = torch.empty(512, dtype=torch.bfloat16, device="cuda")
+    call = lambda pro=None, F=512, gs=64: n.lib().eq_quantized_matmul_swiglu(
+        out.data_ptr(), x.data_ptr(), gu.w.data_ptr(), gu.scales.data_ptr(), gu.biases.data_ptr(), F, 8192, gs, 4,
+        b"affine", n.EQ_DTYPE_BF16, n.EQ_DTYPE_BF16, ctypes.byref(pro) if pro is not None else None, None)
+    wv = dev_bf16(randn_bits(8192, 2))
+    assert call(n.ActivationPrologue(n.EQ_PROLOGUE_RMS_NORM, None, wv.data_ptr(), None, 1e-5)) == 1
+    assert "4096" in n.lib().eq_last_error().decode()
+    assert call(n.ActivationPrologue(n.EQ_PROLOGUE_SILU_MUL, wv.data_ptr(), None, None, 0.0)) == 1
+    assert "RMS_NORM" in n.lib().eq_last_error().decode()
+    assert call(F=508) == 1 and "multiple of 8" in n.lib().eq_last_error().decode()
+    assert call() == 0, n.lib().eq_last_error()  # K = 8192 without the prologue runs
+    torch.cuda.synchronize()
 
 
 def test_prologue_rejects_unsupported(cuda):
