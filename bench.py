@@ -1131,7 +1131,7 @@ def main():
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "qmv_lds_kernel<4,64,BF16T,1,true,false,0,BF16T>",
+            "kernel": "qmv_lds_kernel<4,64,BF16T,1,true,false,0,BF16T,0>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
