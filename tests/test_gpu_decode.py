@@ -132,6 +132,29 @@ def test_rope_attention_decode_at_device_position(cuda, n_heads, n_kv, max_seq, 
     assert torch.equal(kcd, kc2) and torch.equal(vcd, vc2)
 
 
+@pytest.mark.parametrize("pos", [64 * 32 - 1, 64 * 32, 100000])
+def test_rope_attention_decode_long_context(cuda, pos):
+    """Positions whose chunks outnumber the 64 softmax states per head: each
+    state merges several chunks (up to 49 at pos 100000) before the combine;
+    at 2047 every state holds one chunk, at 2048 state 0 holds two."""
+    print(f"[case] attention long context pos={pos}", flush=True)
+    n_heads, n_kv, max_seq = 4, 1, pos + 1
+    q = randn_bits(n_heads * 128, pos)
+    kn, vn = randn_bits(n_kv * 128, pos + 1), randn_bits(n_kv * 128, pos + 2)
+    kc = randn_bits((n_kv, max_seq, 128), pos + 3)
+    vc = randn_bits((n_kv, max_seq, 128), pos + 4)
+    freqs = D.llama3_rope_freqs(128, 500000.0)
+    scale = 1.0 / np.sqrt(128.0)
+    kcd, vcd = dev_bf16(kc), dev_bf16(vc)
+    out = E.rope_attention_decode(dev_bf16(q), dev_bf16(kn), dev_bf16(vn), kcd, vcd,
+                                  torch.from_numpy(freqs).cuda(), pos, n_heads, n_kv, scale)
+    torch.cuda.synchronize()
+    ref, kc_ref, vc_ref = D.attention_decode(q, kn, vn, kc, vc, freqs, pos, n_heads, n_kv, scale)
+    assert np.array_equal(host_bits16(vcd), vc_ref)
+    ok, worst, rms = orc.matmul_within_tolerance(host_f32(out).reshape(n_heads, 128), ref, out_is_bf16=True)
+    assert ok, f"max|err|/RMS = {worst:.3e}"
+
+
 def test_attention_matches_torch_sdpa(cuda):
     """Cross-check with torch's own attention in f32 on the rotated inputs."""
     n_heads, n_kv, pos, max_seq = 32, 8, 777, 1024
