@@ -12,7 +12,10 @@
 // wave keeps a large output block; at the end the second K-group adds its
 // sums into the first through LDS.  Wave w of a K-group owns the 64 columns
 // [64w, 64w + 64) and all 128 rows: 4 x 2 tiles of v_mfma_f32_32x32x16_bf16
-// with f32 accumulators.
+// with f32 accumulators.  Outputs with too few such tiles to fill the GPU
+// without splitting K into short pieces take 64 x 128 tiles instead (wave w:
+// columns [32w, 32w + 32), all 64 rows, 2 x 1 MFMA tiles; the planner,
+// qmm_plan, chooses).
 //
 //  * Weights never touch LDS.  Each wave dequantizes only its own columns,
 //    straight from 16-byte loads into the B-operand registers: lane l reads
@@ -52,10 +55,9 @@ namespace eq {
 
 typedef uint32_t q_u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128, kBN = 256, kBK = 64;
-constexpr int kQmmThreads = 512;        // two K-groups of 4 waves
-constexpr int kLdsBuf = kBM * kBK * 2;  // bytes per activation buffer
-constexpr int kRing = 3;                // slots of the load rings (codes in registers, activations in LDS)
+constexpr int kBM = 128, kBN = 256, kBK = 64;  // the default tile (rows, columns) and the K chunk
+constexpr int kQmmThreads = 512;               // two K-groups of 4 waves
+constexpr int kRing = 3;                       // slots of the load rings (codes in registers, activations in LDS)
 
 typedef _Float16 q_f16x8 __attribute__((ext_vector_type(8)));
 
@@ -111,29 +113,29 @@ __device__ __forceinline__ q_u32x4 dequant8(const uint32_t* words, float s, floa
     return r;
 }
 
-// One ring slot: this lane's codes (2 column blocks x 32 codes) and, unless
+// One ring slot: this lane's codes (TN column blocks x 32 codes) and, unless
 // the parameters come in windows, the scale and bias of each block.
-template <int BITS, bool PARAMS>
+template <int BITS, bool PARAMS, int TN = 2>
 struct QmmSlot {
     static constexpr int WORDS = BITS;  // 32 codes * BITS / 32
-    q_u32x4 w[2][WORDS / 4];
-    uint32_t s[2], b[2];
+    q_u32x4 w[TN][WORDS / 4];
+    uint32_t s[TN], b[TN];
 };
-template <int BITS>
-struct QmmSlot<BITS, false> {
+template <int BITS, int TN>
+struct QmmSlot<BITS, false, TN> {
     static constexpr int WORDS = BITS;
-    q_u32x4 w[2][WORDS / 4];
+    q_u32x4 w[TN][WORDS / 4];
 };
 
 // Reads every register of a slot in an empty asm statement (the never-taken
 // side of an opaque_one() guard): every path then retires the slot's loads,
 // which keeps the compiler's wait analysis exact at the join.
-template <int BITS, bool PARAMS>
-__device__ __forceinline__ void qmm_retire(const QmmSlot<BITS, PARAMS>& s) {
+template <int BITS, bool PARAMS, int TN>
+__device__ __forceinline__ void qmm_retire(const QmmSlot<BITS, PARAMS, TN>& s) {
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < TN; j++) {
 #pragma unroll
-        for (int i = 0; i < QmmSlot<BITS, PARAMS>::WORDS / 4; i++) asm volatile("" ::"v"(s.w[j][i]));
+        for (int i = 0; i < QmmSlot<BITS, PARAMS, TN>::WORDS / 4; i++) asm volatile("" ::"v"(s.w[j][i]));
         if constexpr (PARAMS) asm volatile("" ::"v"(s.s[j]), "v"(s.b[j]));
     }
 }
@@ -175,13 +177,20 @@ struct QmmArgs {
 // K-group) of its 256 columns in LDS, each row's 24 bytes loaded by two lanes
 // (every wave loads 32 rows of each), and every lane reads its column's word
 // of a step from there.
-template <int BITS, int GS, typename ST, bool SPLIT, bool PW, typename XT = BF16T>
+//
+// TM x TN: 32-row blocks and 32-column blocks of each wave's output block;
+// the workgroup's tile is 32 TM rows x 128 TN columns (4 x 2: 128 x 256, the
+// default; 2 x 1: 64 x 128, for outputs with too few large tiles to fill the
+// GPU, which then need no split of K or fewer splits).
+template <int BITS, int GS, typename ST, bool SPLIT, bool PW, typename XT = BF16T, int TM = 4, int TN = 2>
 __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void qmm_mfma_kernel(
     const QmmArgs args) {
+    constexpr int BM = 32 * TM, BN = 128 * TN, LBUF = BM * kBK * 2;  // LBUF: bytes per K-group buffer
+    static_assert((TM == 4 && TN == 2) || (TM == 2 && TN == 1), "tile shapes");
     // Activation ring: three buffers per K-group.  Separate arrays, so that
     // the compiler's LDS alias scopes tell the buffers apart and a read of one
     // does not wait for the loads still landing in another.
-    __shared__ __attribute__((aligned(16))) char abuf0[2 * kLdsBuf], abuf1[2 * kLdsBuf], abuf2[2 * kLdsBuf];
+    __shared__ __attribute__((aligned(16))) char abuf0[2 * LBUF], abuf1[2 * LBUF], abuf2[2 * LBUF];
     constexpr bool MX = __is_same(ST, E8M0T);
     constexpr uint32_t PB = MX ? 1u : 2u;  // bytes per scale / bias
     static_assert(!MX || (BITS == 4 && GS == 32 && !PW), "MXFP4: 4-bit codes, group 32");
@@ -196,8 +205,8 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
     const int split = bid % args.splits, tile = bid / args.splits;
     const int tm = tile / args.ntiles, tn = tile % args.ntiles;
-    int m0 = tm * kBM;
-    const int n0 = tn * kBN;
+    int m0 = tm * BM;
+    const int n0 = tn * BN;
     const uint16_t* xp = args.x;
     const uint32_t* wp = args.w;
     const char* sp = reinterpret_cast<const char*>(args.s);
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const int tid = threadIdx.x & 255;                                         // thread within the K-group
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);                 // column quarter
     const int l32 = lane & 31, kb = lane >> 5;
-    const int gofs = kgrp * kLdsBuf;  // this K-group's part of each ring buffer
+    const int gofs = kgrp * LBUF;  // this K-group's part of each ring buffer
     const int steps = (nloc + 1) / 2;  // chunks per K-group (the second may have one fewer)
 
     const __amdgpu_buffer_rsrc_t xr = raw_rsrc(xp, uint32_t(M) * uint32_t(K) * 2u);
@@ -233,27 +242,27 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     const __amdgpu_buffer_rsrc_t br = raw_rsrc(bp ? bp : sp, bp ? uint32_t(N) * uint32_t(G) * PB : 0u);
     // Parameter windows in LDS: [buffer][scale, bias][column * 6 + word], word
     // w of a column holding groups 2w (low half) and 2w + 1 of the window.
-    __shared__ __attribute__((aligned(16))) uint32_t pbuf[2][2][kBN * 6];
+    __shared__ __attribute__((aligned(16))) uint32_t pbuf[2][2][BN * 6];
 
     // Lane offsets (chunk 0); rows past M and columns past N read zero.
     // Activations go straight from memory to LDS: load i of wave w fills the
-    // 1 KiB (8 rows of 128 B) at (4 w + i) KiB of the 128 x 64 tile, lane l
-    // the 16 B at 16 l, i.e. row 8 (4 w + i) + l / 8, slot l % 8.  Slot p of
+    // 1 KiB (8 rows of 128 B) at (TM w + i) KiB of the BM x 64 tile, lane l
+    // the 16 B at 16 l, i.e. row 8 (TM w + i) + l / 8, slot l % 8.  Slot p of
     // row r holds the row's 16-byte chunk p ^ ((r / 2) & 7), so the lane loads
     // chunk (l % 8) ^ ((row / 2) & 7).  (A 16-lane group of an A-operand read
     // takes rows r .. r + 15 at one chunk; 64 banks of 4 bytes span two rows,
     // so the rows of one parity must land in 8 different 16-byte bank groups.)
-    uint32_t a_goff[4];
+    uint32_t a_goff[4];  // (the first TM used; a bound of TM fails clang's host pass when a lambda captures it)
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = 8 * (4 * wave + i) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+    for (int i = 0; i < TM; i++) {
+        const int row = 8 * (TM * wave + i) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
         a_goff[i] = m0 + row < M ? (uint32_t(m0 + row) * uint32_t(K) + uint32_t(8 * c)) * 2u : kOutOfRange;
     }
-    // Weight rows of this lane: columns n0 + 64 wave + 32 j + l32, codes from 32 kb.
-    uint32_t woff[2], soff[2];
+    // Weight rows of this lane: columns n0 + 32 TN wave + 32 j + l32, codes from 32 kb.
+    uint32_t woff[TN], soff[TN];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const uint32_t n = uint32_t(n0 + 64 * wave + 32 * j + l32);
+    for (int j = 0; j < TN; j++) {
+        const uint32_t n = uint32_t(n0 + 32 * TN * wave + 32 * j + l32);
         woff[j] = int(n) < N ? n * row_bytes + uint32_t(32 * kb) * BITS / 8u : kOutOfRange;
         // (not used with parameter windows, which have their own offsets)
         soff[j] = int(n) < N ? (n * uint32_t(G)) * PB + uint32_t((32 * kb) / GS) * PB : kOutOfRange;
@@ -270,19 +279,19 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     auto load_a = [&](char* buf, int i) __attribute__((always_inline)) {
         const uint32_t ks = __builtin_amdgcn_readfirstlane(uint32_t(chunk_k0(i)) * 2u);
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+        for (int q = 0; q < TM; q++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                xr, (__attribute__((address_space(3))) void*)(buf + gofs + (4 * wave + q) * 1024), 16,
+                xr, (__attribute__((address_space(3))) void*)(buf + gofs + (TM * wave + q) * 1024), 16,
                 a_goff[q], ks, 0, 0);
     };
-    typedef QmmSlot<BITS, !PW> Slot;
+    typedef QmmSlot<BITS, !PW, TN> Slot;
     constexpr int NW = Slot::WORDS / 4;  // 16-byte code loads per column block
     auto load_b = [&](Slot& S, int i) __attribute__((always_inline)) {
         const int k0 = chunk_k0(i);
         const uint32_t kw = __builtin_amdgcn_readfirstlane(uint32_t(k0) * BITS / 8u);
         const uint32_t kp = __builtin_amdgcn_readfirstlane(uint32_t(k0 / GS) * PB);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < TN; j++) {
 #pragma unroll
             for (int q = 0; q < NW; q++) S.w[j][q] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j] + 16 * q, kw, 0);
             if constexpr (MX) {
@@ -299,21 +308,24 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
         }
     };
     // Parameter window w (steps 6w .. 6w + 5, groups 12w .. 12w + 11 of the
-    // split): wave v of the workgroup (v = 4 kgrp + wave) loads rows
+    // split): wave v of the workgroup (v = 4 kgrp + wave < BN / 32) loads rows
     // 32 v .. 32 v + 31 of the tile, lane l the 12 bytes (6 groups) at half
     // l % 2 of row 32 v + l / 2, into registers (one step) and then into LDS.
     typedef uint32_t q_u32x3 __attribute__((ext_vector_type(3)));
     q_u32x3 pst[2];
     const int prow = 32 * (4 * kgrp + wave) + (lane >> 1);
+    const bool pw_wave = 4 * kgrp + wave < BN / 32;  // (wave-uniform)
     const uint32_t poff = n0 + prow < N ? uint32_t(n0 + prow) * uint32_t(G) * PB + uint32_t(c_begin) * 2u +
                                               uint32_t(lane & 1) * 12u
                                         : kOutOfRange;
     auto load_pw = [&](int w) __attribute__((always_inline)) {
+        if (!pw_wave) return;
         const uint32_t kq = __builtin_amdgcn_readfirstlane(uint32_t(12 * w) * 2u);
         pst[0] = __builtin_amdgcn_raw_buffer_load_b96(sr, poff, kq, 0);
         pst[1] = __builtin_amdgcn_raw_buffer_load_b96(br, poff, kq, 0);
     };
     auto store_pw = [&](int buf) __attribute__((always_inline)) {
+        if (!pw_wave) return;
 #pragma unroll
         for (int a = 0; a < 2; a++) {
             uint32_t* d = &pbuf[buf][a][prow * 6 + (lane & 1) * 3];
@@ -324,12 +336,12 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     };
     // Before a barrier: this wave's activation loads for the next step have
     // landed (only the newest step's loads, codes then activations, may still
-    // be in flight; memory operations complete in order).  (Per step: 2 NW
-    // code loads, 4 parameter loads -- 2 for MXFP4, none with windows, whose
-    // loads come first in their step and so land before its barrier -- and 4
+    // be in flight; memory operations complete in order).  (Per step: TN NW
+    // code loads, 2 TN parameter loads -- TN for MXFP4, none with windows, whose
+    // loads come first in their step and so land before its barrier -- and TM
     // activation loads.)
     auto wait_a = [&]() __attribute__((always_inline)) {
-        constexpr int n = 2 * NW + (MX ? 2 : PW ? 0 : 4) + 4;
+        constexpr int n = TN * NW + (MX ? TN : PW ? 0 : 2 * TN) + TM;
         wait_vmcnt<n>();
     };
     auto barrier = [&]() __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
@@ -340,17 +352,17 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
     for (int t = 0; t < 4; t++) aoff[t] = uint32_t(l32 * (kBK * 2) + (((4 * kb + t) ^ ((l32 >> 1) & 7)) << 4));
 
-    f32x16 acc[4][2];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = f32x16{};
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
 
-    // Codes of one chunk -> the B operands of its 4 MFMA steps (2 column blocks).
-    auto dequant = [&](const Slot& S, const uint32_t* sbits, const uint32_t* bbits, q_u32x4 (&bq)[2][4])
+    // Codes of one chunk -> the B operands of its 4 MFMA steps (TN column blocks).
+    auto dequant = [&](const Slot& S, const uint32_t* sbits, const uint32_t* bbits, q_u32x4 (&bq)[TN][4])
                        __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < TN; j++) {
             if constexpr (MX) {
                 const float s = e8m0_to_f32(sbits[j]);
 #pragma unroll
@@ -371,29 +383,29 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
             }
         }
     };
-    // The chunk's 32 MFMAs (4 steps x 4 row blocks x 2 column blocks), A
-    // operands from this K-group's part of the activation buffer.
-    auto mma = [&](const q_u32x4 (&bq)[2][4], const char* buf) __attribute__((always_inline)) {
+    // The chunk's 4 TM TN MFMAs (4 steps x TM row blocks x TN column blocks),
+    // A operands from this K-group's part of the activation buffer.
+    auto mma = [&](const q_u32x4 (&bq)[TN][4], const char* buf) __attribute__((always_inline)) {
         const char* base = buf + gofs;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            bf16x8 a[4];
+            bf16x8 a[TM];
 #pragma unroll
-            for (int mi = 0; mi < 4; mi++)
+            for (int mi = 0; mi < TM; mi++)
                 a[mi] = *reinterpret_cast<const bf16x8*>(base + aoff[t] + mi * 32 * (kBK * 2));
 #pragma unroll
-            for (int mi = 0; mi < 4; mi++)
+            for (int mi = 0; mi < TM; mi++)
 #pragma unroll
-                for (int j = 0; j < 2; j++) acc[mi][j] = QmmAct<XT>::mfma(bq[j][t], a[mi], acc[mi][j]);
+                for (int j = 0; j < TN; j++) acc[mi][j] = QmmAct<XT>::mfma(bq[j][t], a[mi], acc[mi][j]);
         }
     };
     // Scale and bias words of this K-group's chunk at unrolled step r (0 ..
     // U; U is the next window's first step) of the current window.
     auto params = [&](const Slot& S, int r, int pw_cur, uint32_t* sb, uint32_t* bb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < TN; j++) {
             if constexpr (PW) {
-                const int col = 64 * wave + 32 * j + l32;
+                const int col = 32 * TN * wave + 32 * j + l32;
                 const int buf = r < 6 ? pw_cur : pw_cur ^ 1, w = r < 6 ? r : r - 6;
                 sb[j] = pbuf[buf][0][col * 6 + w] >> (16 * kgrp);
                 bb[j] = pbuf[buf][1][col * 6 + w] >> (16 * kgrp);
@@ -445,9 +457,9 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     constexpr int kSecond = BITS == 8 ? 2 : 1;  // the second K-group's schedule in opposite phase
     auto main_loop = [&](auto sched_c) __attribute__((always_inline)) {
         constexpr int SCHED = decltype(sched_c)::value;
-        q_u32x4 bq[2][4];  // dequantized B operands
+        q_u32x4 bq[TN][4];  // dequantized B operands
         if constexpr (SCHED == 0) {
-            uint32_t sb[2], bb[2];
+            uint32_t sb[TN], bb[TN];
             params(ring[0], 0, 0, sb, bb);
             dequant(ring[0], sb, bb, bq);
         }
@@ -456,9 +468,9 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
             for (int r = 0; r < U; r++) {
                 const int i = i0 + r;
-                char* const bufs[3] = {abuf0, abuf1, abuf2};
                 if constexpr (PW)
                     if (r == 0) load_pw(i0 / U + 1);
+                char* const bufs[3] = {abuf0, abuf1, abuf2};
                 load_b(ring[(r + 2) % kRing], i + 2);
                 load_a(bufs[(r + 2) % 3], i + 2);
                 if constexpr (SCHED == 0) {
@@ -466,7 +478,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
                     mma(bq, bufs[r % 3]);
                     __builtin_amdgcn_sched_barrier(0);
                     if (opaque_one() && i + 1 < steps) {
-                        uint32_t sb[2], bb[2];
+                        uint32_t sb[TN], bb[TN];
                         params(ring[(r + 1) % kRing], r + 1, pw_cur, sb, bb);
                         dequant(ring[(r + 1) % kRing], sb, bb, bq);
                     } else {
@@ -474,7 +486,7 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
                     }
                 } else {
                     if (opaque_one() && 2 * i + kgrp < nloc) {
-                        uint32_t sb[2], bb[2];
+                        uint32_t sb[TN], bb[TN];
                         params(ring[r % kRing], r, pw_cur, sb, bb);
                         dequant(ring[r % kRing], sb, bb, bq);
                         if constexpr (SCHED == 1) __builtin_amdgcn_sched_barrier(0);
@@ -503,28 +515,30 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     }
     // Every load has landed (the ring buffers are reused below).
     __builtin_amdgcn_s_waitcnt(0);
-    // The second K-group's sums go to LDS, one row block (32 KiB) at a time
-    // through alternating buffers, and the first adds them.  Layout:
-    // [wave][j][q][lane] x 16 B, q = the run of 4 accumulator registers.
+    // The second K-group's sums go to LDS, one row block (16 TN KiB, at most
+    // a buffer's 2 LBUF bytes) at a time through alternating buffers, and the
+    // first adds them.  Layout: [wave][j][q][lane] x 16 B, q = the run of 4
+    // accumulator registers.
+    static_assert(4 * TN * 4 * 64 * 16 <= 2 * LBUF, "a row block's sums fit one buffer");
     __syncthreads();
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++) {
+    for (int mi = 0; mi < TM; mi++) {
         f32x4* red = reinterpret_cast<f32x4*>(mi == 1 ? abuf1 : mi == 2 ? abuf2 : abuf0);
         if (kgrp == 1) {
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++)
-                    red[((wave * 2 + j) * 4 + q) * 64 + lane] =
+                    red[((wave * TN + j) * 4 + q) * 64 + lane] =
                         f32x4{acc[mi][j][4 * q], acc[mi][j][4 * q + 1], acc[mi][j][4 * q + 2], acc[mi][j][4 * q + 3]};
         }
         __syncthreads();
         if (kgrp == 0) {
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const f32x4 v = red[((wave * 2 + j) * 4 + q) * 64 + lane];
+                    const f32x4 v = red[((wave * TN + j) * 4 + q) * 64 + lane];
 #pragma unroll
                     for (int e = 0; e < 4; e++) acc[mi][j][4 * q + e] += v[e];
                 }
@@ -536,16 +550,16 @@ __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 
     // of lane l holds row m = 32 mi + l % 32 and column n = 32 j + 8 (r / 4) +
     // 4 (l / 32) + r % 4, so each run of 4 registers is 4 adjacent columns of
     // one row.  Columns past N are whole waves (N % 128 == 0).
-    if (n0 + 64 * wave >= N) return;
+    if (n0 + 32 * TN * wave >= N) return;
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++) {
+    for (int mi = 0; mi < TM; mi++) {
         const int m = m0 + 32 * mi + l32;
         if (m < M) {
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < TN; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const int n = n0 + 64 * wave + 32 * j + 8 * q + 4 * kb;
+                    const int n = n0 + 32 * TN * wave + 32 * j + 8 * q + 4 * kb;
                     const f32x4 v = {acc[mi][j][4 * q], acc[mi][j][4 * q + 1], acc[mi][j][4 * q + 2], acc[mi][j][4 * q + 3]};
                     if constexpr (SPLIT) {
                         *reinterpret_cast<f32x4*>(args.ws + (int64_t(split) * M + m) * N + n) = v;
@@ -596,6 +610,42 @@ static int qmm_cu_count() {
     return v;
 }
 
+#ifndef EQ_QMM_SMALL_TILES
+#define EQ_QMM_SMALL_TILES 1  // 0: 128 x 256 tiles only; 1: the planner's choice; 2: 64 x 128 whenever it may split
+#endif
+
+// Tile shape and split of K of one launch.  128 x 256 tiles when there are
+// at least 3/4 as many as CUs, or when K split to fill the CUs still leaves
+// each split 32 chunks or more; otherwise 64 x 128 tiles (four times as many,
+// each dequantized code used by 64 rows instead of 128).  K is split so that
+// the grid fills the CUs without exceeding them (a second round would double
+// the time), at least 8 chunks per split (4 per K-group).  At M = 512,
+// N = 4096, K = 4096 the large tiles needed 4 splits of 16 chunks: f32
+// partials of 4 x M x N, a reduction pass and a short pipeline per
+// workgroup; the small tiles need no split.
+struct QmmPlan {
+    bool small;
+    int mtiles, ntiles, splits;
+};
+static int qmm_splits(int tiles, int slots, int nchunks) {
+    int s = slots / (tiles > 0 ? tiles : 1);
+    s = s > nchunks / 8 ? nchunks / 8 : s;
+    return s < 1 ? 1 : s;
+}
+static QmmPlan qmm_plan(int M, int N, int K, bool may_split) {
+    QmmPlan p{};
+    const int cu = qmm_cu_count(), nchunks = K / kBK;
+    const int big = ((M + 127) / 128) * ((N + 255) / 256);
+    const int big_splits = may_split ? qmm_splits(big, cu, nchunks) : 1;
+    const bool big_ok = 4 * big >= 3 * cu || nchunks / big_splits >= 32;
+    p.small = EQ_QMM_SMALL_TILES == 2 ? may_split : EQ_QMM_SMALL_TILES == 1 && !big_ok;
+    p.mtiles = p.small ? (M + 63) / 64 : (M + 127) / 128;
+    p.ntiles = p.small ? (N + 127) / 128 : (N + 255) / 256;
+    p.splits = !may_split ? 1 : p.small ? qmm_splits(p.mtiles * p.ntiles, cu, nchunks)
+                                        : big_splits;
+    return p;
+}
+
 // One launch (plus the split reduction): every buffer below 2^31 bytes.
 template <int BITS, int GS, typename ST, typename XT = BF16T>
 static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
@@ -603,15 +653,10 @@ static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
     QmmArgs a{};
     a.y = y, a.x = x, a.w = w, a.s = static_cast<const uint16_t*>(s), a.b = static_cast<const uint16_t*>(b);
     a.M = M, a.N = N, a.K = K, a.ldy = ldy;
-    a.mtiles = (M + kBM - 1) / kBM, a.ntiles = (N + kBN - 1) / kBN;
+    const QmmPlan plan = qmm_plan(M, N, K, may_split);
+    a.mtiles = plan.mtiles, a.ntiles = plan.ntiles;
     const int tiles = a.mtiles * a.ntiles, nchunks = K / kBK;
-    // Split K so that the grid fills the CUs without exceeding them (one
-    // workgroup per CU: a second round of workgroups would double the time),
-    // at least 8 chunks per split (4 per K-group).
-    int splits = may_split ? qmm_cu_count() / tiles : 1;
-    splits = splits < 1 ? 1 : splits;
-    splits = splits > nchunks / 8 ? nchunks / 8 : splits;
-    splits = splits < 1 ? 1 : splits;
+    int splits = plan.splits;
     if (splits > 1) {
         a.cps = (nchunks + splits - 1) / splits;
         a.cps += a.cps & 1;  // even, so that parameter windows stay 4-byte aligned
@@ -650,13 +695,19 @@ static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
     // parameter windows: group size 64, rows of an even number of groups
     const bool pw = GS == 64 && (K / GS) % 2 == 0 && a.cps % 2 == 0;
     const dim3 grid(unsigned(tiles * splits)), block(kQmmThreads);
-    if (splits == 1) {
-        if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64, XT><<<grid, block, 0, st>>>(a);
-        else qmm_mfma_kernel<BITS, GS, ST, false, false, XT><<<grid, block, 0, st>>>(a);
-        return true;
-    }
-    if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64, XT><<<grid, block, 0, st>>>(a);
-    else qmm_mfma_kernel<BITS, GS, ST, true, false, XT><<<grid, block, 0, st>>>(a);
+    auto go = [&](auto tm, auto tn) {
+        constexpr int TM = decltype(tm)::value, TN = decltype(tn)::value;
+        if (splits == 1) {
+            if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64, XT, TM, TN><<<grid, block, 0, st>>>(a);
+            else qmm_mfma_kernel<BITS, GS, ST, false, false, XT, TM, TN><<<grid, block, 0, st>>>(a);
+        } else {
+            if (pw) qmm_mfma_kernel<BITS, GS, ST, true, GS == 64, XT, TM, TN><<<grid, block, 0, st>>>(a);
+            else qmm_mfma_kernel<BITS, GS, ST, true, false, XT, TM, TN><<<grid, block, 0, st>>>(a);
+        }
+    };
+    if (plan.small) go(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
+    else go(std::integral_constant<int, 4>{}, std::integral_constant<int, 2>{});
+    if (splits == 1) return true;
     const int64_t mn = int64_t(M) * N;
     qmm_split_reduce<XT><<<dim3(unsigned((mn / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(
         y, a.ws, mn, N, ldy, splits, aligned(y, 8) && N % 4 == 0 && ldy % 4 == 0);
@@ -801,8 +852,8 @@ static bool launch_qmm_grouped_t(uint16_t* y, const uint16_t* x, const uint32_t*
     a.groups = list;
     const bool pw = GS == 64 && (K / GS) % 2 == 0 && a.cps % 2 == 0;
     const dim3 grid(unsigned(a.mtiles * a.ntiles)), block(kQmmThreads);
-    if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64><<<grid, block, 0, st>>>(a);
-    else qmm_mfma_kernel<BITS, GS, ST, false, false><<<grid, block, 0, st>>>(a);
+    if (pw) qmm_mfma_kernel<BITS, GS, ST, false, GS == 64, BF16T, 4, 2><<<grid, block, 0, st>>>(a);
+    else qmm_mfma_kernel<BITS, GS, ST, false, false, BF16T, 4, 2><<<grid, block, 0, st>>>(a);
     return true;
 }
 
@@ -901,9 +952,7 @@ static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, c
     nc = nc > N ? N : nc;
     const size_t code_bytes = (size_t(nc) * size_t(K) + 255) & ~size_t(255);
     // room after the codes for the split-K partials of a slice the planner would split
-    const int tiles = int((M + kBM - 1) / kBM * ((nc + kBN - 1) / kBN));
-    int splits = qmm_cu_count() / (tiles > 0 ? tiles : 1);
-    splits = splits > K / kBK / 8 ? K / kBK / 8 : splits;
+    const int splits = qmm_plan(M, int(nc), K, true).splits;
     const size_t part_bytes = splits > 1 ? size_t(splits) * size_t(M) * size_t(nc) * 4u : 0;
     size_t want = code_bytes + part_bytes;
     char* base = static_cast<char*>(ws_acquire(src, want, st));

@@ -158,13 +158,13 @@ def test_streams_keep_apart_and_replays_reset_counters(cuda):
 
 
 def test_captured_qmm_runs_the_eager_plan(cuda):
-    """M = 512 x 4096 x 4096 splits K through the stream's workspace.  On a
+    """M = 128 x 4096 x 4096 splits K through the stream's workspace.  On a
     fresh stream the workspace cannot grow while capturing, so the capture
     fails with a message instead of recording an unsplit plan (which would
     sum in another order than the eager call).  After one eager call on the
     stream, the captured call runs the eager plan: every replay equals the
     eager result bit for bit."""
-    M, N, K = 512, 4096, 4096
+    M, N, K = 128, 4096, 4096
     w, s, b = synthetic_linear(N, K, 64, 4, seed=21)
     wd, sd, bd = dev_words(w), dev_bf16(s), dev_bf16(b)
     x = dev_bf16(synthetic_x(M, K, seed=22))
