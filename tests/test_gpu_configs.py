@@ -9,7 +9,9 @@ configs[4]), against the fp64 oracle on the same packed inputs.
 * configs[4] decode: the 4-bit LM head at N = 128256 (8016 row tiles, a
   262 MB weight buffer) on a seeded subset of output features; one
   full-size layer (H 4096, 32/8 heads, FFN 14336, 1024 cached positions)
-  against oracle/decode_oracle.py, fused and unfused; and the whole 32-layer,
+  against oracle/decode_oracle.py, fused and unfused; three such layers in
+  one step against the oracle (the residual stream and the fused decoder's
+  buffer alternation across layers); and the whole 32-layer,
   vocab-128256 step, where the fused and unfused decoders must agree on the
   greedy token over three consecutive positions.
 
@@ -160,6 +162,93 @@ def test_full_size_layer_against_the_oracle(cuda, full_layer_model, fused):
     v_ref = orc.bf16_bits_to_f32(vcs[0][:, pos]).astype(np.float64).reshape(1, -1)
     v_got = orc.bf16_bits_to_f32(host_bits16(dec.v_caches[0])[:, pos]).reshape(1, -1)
     assert orc.matmul_within_tolerance(v_got, v_ref, out_is_bf16=True, rel=1e-2)[0]
+
+
+@pytest.fixture(scope="module")
+def three_layer_model():
+    """Three Llama-3-8B-sized layers (host weights from the oracle's
+    quantizer, each layer its own seeds), a 1024-row vocabulary and caches
+    holding 1024 positions per layer."""
+    H, nh, nkv, F, V, max_seq, layers = 4096, 32, 8, 14336, 1024, 1040, 3
+    rng = np.random.default_rng(41)
+
+    def lin(N, K, seed):
+        w, sc, b = synthetic_linear(N, K, 64, 4, seed)
+        return {"w": w, "s": sc, "b": b, "bits": 4, "gs": 64}
+
+    host = {"hidden": H, "n_heads": nh, "n_kv_heads": nkv, "eps": 1e-5,
+            "freqs": D.llama3_rope_freqs(128, 500000.0),
+            "embed": _bits(rng.standard_normal((V, H))), "final_norm": _bits(1.0 + 0.1 * rng.standard_normal(H)),
+            "layers": [{"in_norm": _bits(1.0 + 0.1 * rng.standard_normal(H)),
+                        "post_norm": _bits(1.0 + 0.1 * rng.standard_normal(H)),
+                        "q": lin(nh * 128, H, 50 + 10 * i), "k": lin(nkv * 128, H, 51 + 10 * i),
+                        "v": lin(nkv * 128, H, 52 + 10 * i), "o": lin(H, nh * 128, 53 + 10 * i),
+                        "gate": lin(F, H, 54 + 10 * i), "up": lin(F, H, 55 + 10 * i), "down": lin(H, F, 56 + 10 * i)}
+                       for i in range(layers)],
+            "lm_head": lin(V, H, 49)}
+    kcs = [_bits(np.random.default_rng(60 + i).standard_normal((nkv, max_seq, 128))) for i in range(layers)]
+    vcs = [_bits(np.random.default_rng(70 + i).standard_normal((nkv, max_seq, 128))) for i in range(layers)]
+    return host, kcs, vcs, max_seq
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_three_full_size_layers_against_the_oracle(cuda, three_layer_model, fused):
+    """Three layers in one step against oracle/decode_oracle.py: what one
+    layer cannot show -- the residual stream carried from layer to layer, the
+    fused decoder's hidden state alternating between its two buffers (layer
+    0 reads the embedding row, later layers the other buffer) and each
+    layer's cache -- with every projection kernel the 32-layer step runs.
+    The final hidden state (bf16, after three layers' roundings) and the
+    logits are checked against the oracle's: RMS(err) <= 2e-2 * RMS(ref) and
+    every |err| <= 8e-2 * RMS(ref) + 1/2 ulp -- a one-ulp bf16 difference
+    where device and oracle round a sum on opposite sides of a tie grows
+    through the later layers (measured: RMS 7.6e-3, max 2.9e-2 of RMS),
+    while a wrong buffer, residual or cache makes errors of the order of
+    the values themselves.  Every layer's new cache row (one value
+    projection each) is checked at the matmul rule."""
+    host, kcs0, vcs0, max_seq = three_layer_model
+    pos, token = 1024, 321
+    print(f"[case] three full-size layers fused={fused} pos={pos}", flush=True)
+
+    def qlin(d):
+        return E.QLinear(dev_words(d["w"]), dev_bf16(d["s"]), dev_bf16(d["b"]), 4, 64)
+
+    layers = [E.DecoderLayer(dev_bf16(L["in_norm"]), dev_bf16(L["post_norm"]),
+                             *(qlin(L[p]) for p in ("q", "k", "v", "o", "gate", "up", "down")))
+              for L in host["layers"]]
+    dec = E.LlamaDecoder(layers, dev_bf16(host["embed"]), dev_bf16(host["final_norm"]), qlin(host["lm_head"]),
+                         n_heads=32, n_kv_heads=8, eps=1e-5, freqs=host["freqs"], max_seq=max_seq,
+                         k_caches=[dev_bf16(k) for k in kcs0], v_caches=[dev_bf16(v) for v in vcs0], fused=fused)
+    assert dec.swiglu == fused
+    dec.token.fill_(token)
+    dec.step(pos)
+    torch.cuda.synchronize()
+    kcs, vcs = [k.copy() for k in kcs0], [v.copy() for v in vcs0]
+    logits_ref, x_ref = D.decode_step(host, token, pos, kcs, vcs)
+    # the hidden state after the last layer: the residual sum the final norm
+    # writes back (unfused: dec.x; fused: the buffer the LM head's prologue
+    # reads plus the last down projection -- compared through the logits)
+    got = host_f32(dec.logits)
+    rms = np.sqrt(np.mean(logits_ref ** 2))
+    err = np.abs(got - logits_ref)
+    print(f"  logits max|err|/RMS = {err.max() / rms:.3e}, RMS(err)/RMS = {np.sqrt(np.mean(err ** 2)) / rms:.3e}",
+          flush=True)
+    assert np.sqrt(np.mean(err ** 2)) <= 2e-2 * rms, f"RMS(err)/RMS = {np.sqrt(np.mean(err ** 2)) / rms:.3e}"
+    assert np.all(err <= 8e-2 * rms + orc.bf16_half_ulp(logits_ref)), f"max|err|/RMS = {err.max() / rms:.3e}"
+    if not fused:
+        hx = orc.bf16_bits_to_f32(host_bits16(dec.x)).astype(np.float64)
+        hr = orc.bf16_bits_to_f32(x_ref).astype(np.float64)
+        hrms = np.sqrt(np.mean(hr ** 2))
+        herr = np.abs(hx - hr)
+        print(f"  hidden max|err|/RMS = {herr.max() / hrms:.3e}", flush=True)
+        assert np.sqrt(np.mean(herr ** 2)) <= 2e-2 * hrms, "hidden RMS(err)"
+        assert np.all(herr <= 8e-2 * hrms + orc.bf16_half_ulp(hr)), f"hidden max|err|/RMS = {herr.max() / hrms:.3e}"
+    for li in range(len(layers)):
+        v_ref = orc.bf16_bits_to_f32(vcs[li][:, pos]).astype(np.float64).reshape(1, -1)
+        v_got = orc.bf16_bits_to_f32(host_bits16(dec.v_caches[li])[:, pos]).reshape(1, -1)
+        assert orc.matmul_within_tolerance(v_got, v_ref, out_is_bf16=True, rel=2e-2)[0], f"layer {li} value row"
+        # rows other than pos are untouched
+        assert np.array_equal(host_bits16(dec.v_caches[li])[:, :pos], vcs0[li][:, :pos]), f"layer {li} cache"
 
 
 def test_full_model_fused_and_unfused_agree(cuda):
