@@ -4,7 +4,8 @@
 //
 // Dispatch of eq_quantized_matmul:
 //   transpose, bf16 x, bits 4/8, bf16/f16 scales, group size 32/64/128:
-//     M <= 16  -> qmv (qmv.hip), the decode path (N % 16 == 0)
+//     M <= 16  -> qmv (qmv.hip), the decode path (N % 16 == 0), unless the
+//                 rows need several passes over the weights (decode_rows)
 //     M  > 16  -> qmm_mfma (qmm.hip), the prefill path (N % 128 == 0, K % 64 == 0)
 //   transpose = false, bf16 x, bits 4/8, M <= 8 -> qmm_n (qmm_n.hip)
 // Everything else -- f32/f16 activations, f32 scales, bits 2/3/5/6 (3/5/6-bit
@@ -18,7 +19,27 @@
 
 #include "eq_common.hpp"
 
+#ifndef EQ_QMV_ONE_PASS
+#define EQ_QMV_ONE_PASS 1  // 1: multi-pass decode calls go to the prefill kernel when it can take them; 0: M <= 16 to qmv
+#endif
+
 namespace eq {
+
+// Whether an M-row call of 4/8-bit codes (transpose, 16-bit x) takes the
+// decode kernels: up to 16 rows, unless they would read the weights in
+// several passes (a pass multiplies 16 / groups-per-span rows: 8 at 4-bit
+// group 64, 4 at 4-bit group 32, 16 at 8-bit group 64) and the prefill
+// kernel, which reads them once for any M, can take the call (qmm_shape).
+// Measured on the Llama-3-8B shapes: two passes of 4-bit group 64 or of
+// 8-bit group 32 1.0-1.6x slower than the prefill kernel; two passes of
+// 4-bit group 32 within 0.9-1.1x of it, three or more 1.3-2.1x slower.
+static bool decode_rows(int64_t M, int bits, int group_size, bool qmm_shape) {
+    if (M > 16) return false;
+    if (!EQ_QMV_ONE_PASS || !qmm_shape) return true;
+    const int rows = qmv_rows_per_pass(bits, group_size);
+    const int passes = (int(M) + rows - 1) / rows;
+    return passes < (bits == 4 && group_size < 64 ? 3 : 2);
+}
 
 static thread_local std::string g_last_error;
 
@@ -375,17 +396,19 @@ static int quantized_matmul_impl(void* y, const void* x, const uint32_t* w, cons
     const bool mfma_ok = transpose && x16 && (bits == 4 || bits == 8) &&
                          (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && aligned(x, 16) &&
                          aligned(w, 16);
-    if (mfma_ok && M <= 16 && N % 16 == 0) {
-        if (launch_qmv_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
-                            w, scales, biases, int(M), int(N), int(K), st, x_dtype))
-            return check_launch("quantized_matmul (qmv)");
-    }
     // prefill on the matrix cores: 4/8-bit codes directly, 2/3/5/6-bit codes
     // re-packed to bytes slice by slice in the workspace
     const bool odd_ok = transpose && x16 && (bits == 2 || bits == 3 || bits == 5 || bits == 6) &&
                         (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && aligned(x, 16) &&
                         aligned(w, 4);
-    if ((mfma_ok || odd_ok) && M > 16 && N % 128 == 0 && K % 64 == 0 && aligned(y, 8)) {
+    const bool qmm_shape = N % 128 == 0 && K % 64 == 0 && aligned(y, 8);
+    const bool qmv_rows = decode_rows(M, bits, group_size, qmm_shape);
+    if (mfma_ok && qmv_rows && N % 16 == 0) {
+        if (launch_qmv_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
+                            w, scales, biases, int(M), int(N), int(K), st, x_dtype))
+            return check_launch("quantized_matmul (qmv)");
+    }
+    if ((mfma_ok ? !qmv_rows : odd_ok && M > 16) && qmm_shape) {
         if (launch_qmm_mfma(bits, group_size, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x),
                             w, scales, biases, int(M), int(N), int(K), ws, st, -1, x_dtype))
             return take_refusal() ? 1 : check_launch("quantized_matmul (qmm)");
@@ -494,13 +517,15 @@ extern "C" int eq_quantized_matmul_batched(const eq_qmm_problem* problems, int c
         return 1;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    // Decode-shaped groups go to one grouped launch per kQmvMaxProblems problems.
+    // Decode-shaped groups go to one grouped launch per kQmvMaxProblems
+    // problems, when every problem would take the decode kernels alone.
     bool grouped = qm == kModeAffine && transpose && (x_dtype == EQ_DTYPE_BF16 || x_dtype == EQ_DTYPE_F16) &&
                    (bits == 4 || bits == 8) && (scale_dtype == EQ_DTYPE_BF16 || scale_dtype == EQ_DTYPE_F16) && M <= 16;
     std::vector<QmvSpec> specs;
     for (int i = 0; i < count && grouped; i++) {
         const eq_qmm_problem& p = problems[i];
-        grouped = p.N % 16 == 0 && aligned(p.x, 16) && aligned(p.w, 16);
+        grouped = p.N % 16 == 0 && aligned(p.x, 16) && aligned(p.w, 16) &&
+                  decode_rows(M, bits, group_size, p.N % 128 == 0 && p.K % 64 == 0 && aligned(p.y, 8));
         specs.push_back(QmvSpec{static_cast<const uint16_t*>(p.x), p.w, p.scales, p.biases, static_cast<uint16_t*>(p.y),
                                 int(p.N), int(p.K), int(p.N)});
     }

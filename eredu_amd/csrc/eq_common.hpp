@@ -54,6 +54,11 @@ bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint1
                      const void* s, const void* b, int M, int N, int K, hipStream_t st, int x_dtype = EQ_DTYPE_BF16);
 bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st,
                         int x_dtype = EQ_DTYPE_BF16);
+// Activation rows one pass of launch_qmv_mfma's kernels multiplies for 4/8-bit
+// codes at group size gs (a 16-row MFMA operand holds 16 / (groups per span)
+// rows): 8 for 4-bit group 64, 16 for 8-bit group 64; more rows read the
+// weights once per pass.
+int qmv_rows_per_pass(int bits, int gs);
 // Decode for the other widths (qmv_any.hip): transpose, bf16 x, M <= 16, bits
 // 2..8, group 16 or a multiple of 32, K a multiple of 32; false, launching
 // nothing, when it does not take the problem.

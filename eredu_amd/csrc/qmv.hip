@@ -1430,6 +1430,12 @@ static bool with_qmv_types(int bits, int scale_dtype, int x_dtype, F&& f) {
     return false;
 }
 
+int qmv_rows_per_pass(int bits, int gs) {
+    const int span = 4 * (128 / bits);  // QmvGeom<BITS, GS>::SPAN
+    const int groups = gs > 0 && span > gs ? span / gs : 1;
+    return 16 / groups;
+}
+
 // Entry used by the dispatcher (api.hip).  Preconditions checked there:
 // x bf16 or f16 (y in x's type), transpose, 1 <= M <= 16, N % 16 == 0,
 // K % gs == 0, 16-byte aligned x and weight pointers, scale dtype bf16 or f16.

@@ -76,7 +76,12 @@ int eq_version(void);
  * 4, scale_dtype EQ_DTYPE_U8 (E8M0 bytes, 2^(e - 127), 255 = NaN), biases
  * NULL; W[r, c] = 2^(e[r, c/32] - 127) * e2m1(q[r, c]) with the E2M1 code
  * bit 3 = sign, magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6.
- * Accumulation is f32.
+ * Accumulation is f32.  Calls the matrix-core prefill kernel takes (M > 16,
+ * or fewer rows than that which the decode kernel would multiply in several
+ * passes over the weights) may split K through f32 partials in the library
+ * workspace of `stream`, which cannot grow while `stream` is capturing: such
+ * a capture fails with a message until one eager call of that shape has run
+ * on the stream (it never records another plan than the eager call's).
  */
 int eq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                         const void* biases, int64_t M, int64_t N, int64_t K, bool transpose,
@@ -98,9 +103,13 @@ typedef struct eq_qmm_problem {
  * Grouped quantized matmul: `count` independent problems that share M,
  * transpose, group_size, bits, mode and dtypes, with the results of `count`
  * eq_quantized_matmul calls (bit for bit: each problem runs the same kernel
- * code either way).  Decode-shaped groups (M <= 16, transpose, bf16 x) run as
- * one persistent launch per 8 problems, which streams the weights of all of
- * them back to back instead of paying a kernel launch per projection.
+ * code either way).  Decode-shaped groups (transpose, 16-bit x, 4/8-bit
+ * codes, M <= 16 rows that one pass of the decode kernel multiplies: 8 at
+ * 4-bit group 64, 16 at 8-bit group 64, 4 at group 32) run as one persistent
+ * launch per 8 problems, which streams the weights of all of them back to
+ * back instead of paying a kernel launch per projection; rows that would
+ * take the decode kernel several passes go, as in eq_quantized_matmul, to
+ * the prefill kernel one problem at a time.
  * No single counterpart in the reference's C ABI: it stands for the
  * consecutive mlx_quantized_matmul calls (safemlx-sys/src/mlx-c/mlx/c/ops.h:809-819)
  * that a decoder layer issues on one input, e.g. the q/k/v projections of

@@ -223,10 +223,14 @@ def _batch_problems(specs, M, gs, bits, sdt=orc.BF16, seed=0, biases=True):
     return probs, host
 
 
-@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("M", [1, 3, 8, 12, 16])
 def test_batched_equals_separate_calls_bitwise(cuda, M):
-    # a decoder layer's projections: q, k, v, o, gate, up (x of K=4096) and down (K=14336), scaled down
+    # a decoder layer's projections: q, k, v, o, gate, up (x of K=4096) and down (K=14336), scaled down.
+    # Above 8 rows (two passes of the 4-bit group-64 decode kernel) the separate calls take the prefill
+    # kernel where N % 128 == 0 and the decode kernel otherwise (N = 48): the batched call must match both.
     specs = [(512, 1024), (128, 1024), (128, 1024), (512, 512), (1792, 1024), (1792, 1024), (1024, 3584)]
+    if M > 8:
+        specs.append((48, 1024))
     probs, host = _batch_problems(specs, M, 64, 4, seed=M, biases=False)
     ys = quantized_matmul_batched(probs, transpose=True, group_size=64, bits=4)
     torch.cuda.synchronize()
