@@ -617,12 +617,17 @@ static int qmm_cu_count() {
 // Tile shape and split of K of one launch.  128 x 256 tiles when there are
 // at least 3/4 as many as CUs, or when K split to fill the CUs still leaves
 // each split 32 chunks or more; otherwise 64 x 128 tiles (four times as many,
-// each dequantized code used by 64 rows instead of 128).  K is split so that
-// the grid fills the CUs without exceeding them (a second round would double
-// the time), at least 8 chunks per split (4 per K-group).  At M = 512,
-// N = 4096, K = 4096 the large tiles needed 4 splits of 16 chunks: f32
-// partials of 4 x M x N, a reduction pass and a short pipeline per
-// workgroup; the small tiles need no split.
+// each dequantized code used by 64 rows instead of 128) when the large tiles
+// would split K 8 ways or more, or at group size 64 (parameter windows,
+// whose dequantization is the cheapest per code).  K is split so that the
+// grid fills the CUs without exceeding them (a second round would double
+// the time), at least 8 chunks per split (4 per K-group).  Measured: at
+// M = 512, N = 4096, K = 4096, 4-bit group 64, the large tiles split K 4
+// ways (f32 partials of 4 x M x N, a reduction pass, a short pipeline per
+// workgroup) in 37.7 us, the small tiles need no split: 34.4 us; at group 16
+// (the 2/3/5/6-bit re-packed codes included) the small tiles' per-code
+// work made them 2-8 % slower there; at M = 128 (8-16 large-tile splits)
+// and N = 1024 they are 1.2-1.5x faster.
 struct QmmPlan {
     bool small;
     int mtiles, ntiles, splits;
@@ -632,13 +637,14 @@ static int qmm_splits(int tiles, int slots, int nchunks) {
     s = s > nchunks / 8 ? nchunks / 8 : s;
     return s < 1 ? 1 : s;
 }
-static QmmPlan qmm_plan(int M, int N, int K, bool may_split) {
+static QmmPlan qmm_plan(int M, int N, int K, int gs, bool may_split) {
     QmmPlan p{};
     const int cu = qmm_cu_count(), nchunks = K / kBK;
     const int big = ((M + 127) / 128) * ((N + 255) / 256);
     const int big_splits = may_split ? qmm_splits(big, cu, nchunks) : 1;
     const bool big_ok = 4 * big >= 3 * cu || nchunks / big_splits >= 32;
-    p.small = EQ_QMM_SMALL_TILES == 2 ? may_split : EQ_QMM_SMALL_TILES == 1 && !big_ok;
+    const bool small_ok = big_splits >= 8 || gs == 64;
+    p.small = EQ_QMM_SMALL_TILES == 2 ? may_split : EQ_QMM_SMALL_TILES == 1 && !big_ok && small_ok;
     p.mtiles = p.small ? (M + 63) / 64 : (M + 127) / 128;
     p.ntiles = p.small ? (N + 127) / 128 : (N + 255) / 256;
     p.splits = !may_split ? 1 : p.small ? qmm_splits(p.mtiles * p.ntiles, cu, nchunks)
@@ -653,7 +659,7 @@ static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
     QmmArgs a{};
     a.y = y, a.x = x, a.w = w, a.s = static_cast<const uint16_t*>(s), a.b = static_cast<const uint16_t*>(b);
     a.M = M, a.N = N, a.K = K, a.ldy = ldy;
-    const QmmPlan plan = qmm_plan(M, N, K, may_split);
+    const QmmPlan plan = qmm_plan(M, N, K, GS, may_split);
     a.mtiles = plan.mtiles, a.ntiles = plan.ntiles;
     const int tiles = a.mtiles * a.ntiles, nchunks = K / kBK;
     int splits = plan.splits;
@@ -952,7 +958,7 @@ static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, c
     nc = nc > N ? N : nc;
     const size_t code_bytes = (size_t(nc) * size_t(K) + 255) & ~size_t(255);
     // room after the codes for the split-K partials of a slice the planner would split
-    const int splits = qmm_plan(M, int(nc), K, true).splits;
+    const int splits = qmm_plan(M, int(nc), K, gs, true).splits;
     const size_t part_bytes = splits > 1 ? size_t(splits) * size_t(M) * size_t(nc) * 4u : 0;
     size_t want = code_bytes + part_bytes;
     char* base = static_cast<char*>(ws_acquire(src, want, st));
