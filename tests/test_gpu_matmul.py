@@ -106,6 +106,15 @@ def test_qmm_pipeline_depths(cuda, bits, K):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,gs", [(65, 64), (100, 64), (100, 32)])
+def test_qmm_tiles_ragged(cuda, bits, M, gs):
+    # N = 384: three 64 x 128 tiles (group 64) or two 128 x 256 tiles, the
+    # second half past N (group 32, which keeps the large tile); M not a
+    # multiple of either tile height; K split 4 ways in both plans
+    run_case(M, 384, 2048, gs, bits, seed=M + gs + bits)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 def test_qmm_split_k(cuda, bits):
     # 6 output tiles, 32 chunks: K split 8 ways, partial tiles summed in order
     run_case(300, 512, 2048, 64, bits, seed=bits + 77)
