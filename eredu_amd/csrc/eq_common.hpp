@@ -54,6 +54,14 @@ bool launch_qmv_mfma(int bits, int gs, int scale_dtype, uint16_t* y, const uint1
                      const void* s, const void* b, int M, int N, int K, hipStream_t st, int x_dtype = EQ_DTYPE_BF16);
 bool launch_qmv_batched(int bits, int gs, int scale_dtype, const QmvSpec* specs, int count, int M, hipStream_t st,
                         int x_dtype = EQ_DTYPE_BF16);
+// Routed decode for gather_qmm (qmv.hip): y[b] = x[lhs(b)] . W[rhs(b)]^T for
+// `batch` output batches of one bf16 row each, 4/8-bit codes, group 32/64/128,
+// bf16 or f16 parameters, N % 16 == 0, the indices read on the device; false,
+// launching nothing, when the shapes do not fit the decode kernel.
+struct GatherIdx;
+bool launch_qmv_gather(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                       const void* s, const void* b, const GatherIdx& g, int64_t batch, int N, int K,
+                       hipStream_t st);
 // Activation rows one pass of launch_qmv_mfma's kernels multiplies for 4/8-bit
 // codes at group size gs (a 16-row MFMA operand holds 16 / (groups per span)
 // rows): 8 for 4-bit group 64, 16 for 8-bit group 64; more rows read the

@@ -11,8 +11,11 @@
 // index outside its operand's batches makes that batch's output rows zero
 // and reads nothing (MLX leaves such gathers undefined).
 //
-// Kernels: gather_qmv -- transpose = true, one activation row per batch, 4-
-// or 8-bit codes, bf16 activations (the routed-expert decode): the team
+// Kernels: the routed-expert decode (transpose = true, one bf16 activation
+// row per batch, 4/8-bit codes, N % 16 == 0, K a whole number of the decode
+// kernel's blocks) runs qmv.hip's persistent decode kernel, up to 8 batches
+// per launch, with each batch's x row and expert found from the indices on
+// the device (launch_qmv_gather).  gather_qmv -- the other decode shapes: the team
 // layout of a workgroup (T teams of 256 / T lanes, 4 weight rows per team,
 // lanes splitting a row's 16-byte code chunks, so a chunk's activations are
 // loaded once for 4 rows); 4-bit sums run on v_dot2c_f32_bf16 with codes as
@@ -263,6 +266,11 @@ int gather_qmm_launch(void* y, const void* x, const uint32_t* w, const void* sca
         launch_qmm_n_small(bits, scale_dtype, static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), w, scales,
                            biases, g, batch, int(M), int(N), int(K), group_size, nullptr, st))
         return check_launch("gather_qmm (qmm_n)");
+    // the routed decode on the persistent decode kernel (qmv.hip) where its
+    // shapes fit: codes streamed as the dense decode streams them
+    if (fast && launch_qmv_gather(bits, group_size, scale_dtype, static_cast<uint16_t*>(y),
+                                  static_cast<const uint16_t*>(x), w, scales, biases, g, batch, int(N), int(K), st))
+        return check_launch("gather_qmm (qmv)");
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const unsigned nb = unsigned(batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY);
         if (fast) {

@@ -554,7 +554,64 @@ struct QmvBatch {
     const uint16_t* pro_weight;
     uint16_t* pro_hidden_out;
     float pro_eps;
+    // Routed problems (gather_qmm's decode; kernels with GATHER): problem i
+    // is output batch g_b0 + i, its x row and its expert's codes, scales and
+    // biases at the bases in p[i] plus the batch's index (g_lhs / g_rhs; null:
+    // the batch itself, or 0 when there is one batch) times g_x_stride
+    // elements, g_w_stride words and g_s_stride parameters.  An index outside
+    // its operand's batches gives a zero row.
+    const int32_t* g_lhs;
+    const int32_t* g_rhs;
+    int64_t g_xb, g_wb, g_x_stride, g_w_stride, g_s_stride;
+    int g_b0;
 };
+
+// Routed problems: the x and expert indices of each problem of the launch,
+// resolved once per workgroup from device memory into LDS (routes[2 pi] =
+// x batch, routes[2 pi + 1] = expert; -1 for both when either index is out
+// of range), so that the tiles' address computations read LDS.
+template <bool GATHER>
+__device__ __forceinline__ void qmv_load_routes(const QmvBatch& batch, int* routes) {
+    if constexpr (GATHER) {
+        const int pi = int(threadIdx.x);
+        if (pi < batch.count) {
+            const int64_t bb = int64_t(batch.g_b0) + pi;
+            const int64_t xb = batch.g_lhs ? int64_t(batch.g_lhs[bb]) : (batch.g_xb == 1 ? 0 : bb);
+            const int64_t wb = batch.g_rhs ? int64_t(batch.g_rhs[bb]) : (batch.g_wb == 1 ? 0 : bb);
+            const bool live = xb >= 0 && xb < batch.g_xb && wb >= 0 && wb < batch.g_wb;
+            routes[2 * pi] = live ? int(xb) : -1;
+            routes[2 * pi + 1] = live ? int(wb) : -1;
+        }
+        __syncthreads();
+    }
+}
+
+// The operands of problem pi: p[pi]'s pointers, offset by the route's
+// indices with GATHER; live is false for a route whose index is out of
+// range (its loads then read zero).
+struct QmvPtrs {
+    const uint16_t* x;
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    bool live;
+};
+template <bool GATHER>
+__device__ __forceinline__ QmvPtrs qmv_ptrs(const QmvBatch& batch, int pi, const int* routes) {
+    const QmvProblem& pr = batch.p[pi];
+    QmvPtrs r{pr.x, pr.w, pr.s, pr.b, true};
+    if constexpr (GATHER) {
+        const int xb = __builtin_amdgcn_readfirstlane(routes[2 * pi]);
+        const int wb = __builtin_amdgcn_readfirstlane(routes[2 * pi + 1]);
+        r.live = xb >= 0;
+        const int64_t xo = r.live ? xb : 0, wo = r.live ? wb : 0;
+        r.x += xo * batch.g_x_stride;
+        r.w += wo * batch.g_w_stride;
+        r.s += wo * batch.g_s_stride;
+        if (r.b) r.b += wo * batch.g_s_stride;
+    }
+    return r;
+}
 
 // Registers of one block of NU spans of the LDS variant: codes and scale words.
 template <int BITS, int GS, int NU, bool VEC>
@@ -703,11 +760,13 @@ struct QmvTileView {
 // range is whole blocks; a wave without blocks in a tile gets one virtual
 // block instead (loads out of range read zero, activations from the zero
 // block), so that every tile takes at least one block from the ring.
-template <int BITS, int GS, bool TAIL>
+template <int BITS, int GS, bool TAIL, bool GATHER = false>
 __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& batch, int pi, int tile, int wave,
-                                                              int ln, int kq, int a_m, bool a_live, int r_p) {
+                                                              int ln, int kq, int a_m, bool a_live, int r_p,
+                                                              const int* routes = nullptr) {
     typedef QmvGeom<BITS, GS> Geo;
     const QmvProblem& pr = batch.p[pi];
+    const QmvPtrs op = qmv_ptrs<GATHER>(batch, pi, routes);
     QmvTileView<BITS, GS> v;
     const int N = pr.N, K = pr.K, G = K / GS;
     v.K = K;
@@ -725,13 +784,14 @@ __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& b
         v.j_end = v.j_full_end = v.S_full;
     }
     const uint32_t row_bytes = uint32_t(K) * BITS / 8;
-    v.L.wr = raw_rsrc(pr.w, uint32_t(N) * row_bytes);
-    v.L.sr = raw_rsrc(pr.s, uint32_t(N) * uint32_t(G) * 2u);
-    v.L.br = pr.b ? raw_rsrc(pr.b, uint32_t(N) * uint32_t(G) * 2u) : v.L.sr;
+    const uint32_t live = op.live ? 1u : 0u;  // (a dead route's loads read zero)
+    v.L.wr = raw_rsrc(op.w, live * uint32_t(N) * row_bytes);
+    v.L.sr = raw_rsrc(op.s, live * uint32_t(N) * uint32_t(G) * 2u);
+    v.L.br = op.b ? raw_rsrc(op.b, live * uint32_t(N) * uint32_t(G) * 2u) : v.L.sr;
     v.L.woff = uint32_t(v.n0 + ln) * row_bytes + uint32_t(kq) * 16u;
     v.L.soff = uint32_t(v.n0 + ln) * uint32_t(G) * 2u;
     v.L.r_p = r_p;
-    v.bias_on = pr.b ? 1.f : 0.f;
+    v.bias_on = op.b ? 1.f : 0.f;
 #pragma unroll
     for (int t = 0; t < Geo::STEPS; t++)
         v.xa_t[t] = a_live ? uint32_t(pr.x_lds + a_m * pr.kpad * 2 + (((kq * Geo::CPL / 8 + t) ^ (a_m & 7)) * 16))
@@ -770,14 +830,14 @@ struct QmvStream {
     bool done;
 };
 
-template <int BITS, int GS, bool TAIL>
+template <int BITS, int GS, bool TAIL, bool GATHER = false>
 __device__ __forceinline__ void qmv_stream_seek(const QmvBatch& batch, QmvStream& st, int tile, int wave, int ln,
-                                                int kq, int r_p) {
+                                                int kq, int r_p, const int* routes = nullptr) {
     if constexpr (!TAIL) {
         // every tile has a block (real or virtual)
         if (tile < batch.total_tiles) {
             st.pi = qmv_problem_of(batch, tile, st.pi);
-            const QmvTileView<BITS, GS> v = qmv_tile_view<BITS, GS, TAIL>(batch, st.pi, tile, wave, ln, kq, 0, false, r_p);
+            const QmvTileView<BITS, GS> v = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, st.pi, tile, wave, ln, kq, 0, false, r_p, routes);
             st.L = v.L;
             st.tile = tile;
             st.j = v.j_begin;
@@ -791,7 +851,7 @@ __device__ __forceinline__ void qmv_stream_seek(const QmvBatch& batch, QmvStream
     }
     for (; tile < batch.total_tiles; tile += gridDim.x) {
         st.pi = qmv_problem_of(batch, tile, st.pi);
-        const QmvTileView<BITS, GS> v = qmv_tile_view<BITS, GS, TAIL>(batch, st.pi, tile, wave, ln, kq, 0, false, r_p);
+        const QmvTileView<BITS, GS> v = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, st.pi, tile, wave, ln, kq, 0, false, r_p, routes);
         if (v.nblk > 0) {
             st.L = v.L;
             st.tile = tile;
@@ -805,15 +865,15 @@ __device__ __forceinline__ void qmv_stream_seek(const QmvBatch& batch, QmvStream
     st.L.woff = st.L.soff = kOutOfRange;
 }
 
-template <int BITS, int GS, bool TAIL>
+template <int BITS, int GS, bool TAIL, bool GATHER = false>
 __device__ __forceinline__ void qmv_stream_next(const QmvBatch& batch, QmvStream& st, int wave, int ln, int kq,
-                                                int r_p) {
+                                                int r_p, const int* routes = nullptr) {
     if (st.done) return;
     if (st.j + qmv_block_stride<TAIL>() < st.j_stop) {
         st.j += qmv_block_stride<TAIL>();
         return;
     }
-    qmv_stream_seek<BITS, GS, TAIL>(batch, st, st.tile + gridDim.x, wave, ln, kq, r_p);
+    qmv_stream_seek<BITS, GS, TAIL, GATHER>(batch, st, st.tile + gridDim.x, wave, ln, kq, r_p, routes);
 }
 
 // silu(g) * u on 8 bf16 values with the decoder's roundings: sigmoid, the
@@ -891,7 +951,7 @@ __device__ __forceinline__ u32x4 qmv_norm8(const u32x4 a, const u32x4 w, float i
 // tile writes y[8t + i] = silu(bf16(gate_i)) * bf16(up_i) with the roundings
 // of qmv_silu_mul8 (M = 1).
 template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL, int PRO = 0, typename XT = BF16T,
-          int EPI = 0>
+          int EPI = 0, bool GATHER = false>
 __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
     const QmvBatch batch) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -914,6 +974,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     const int r_p = kq * P / 4;  // result group block of this lane
     prefetch_args(batch);
     if (int(blockIdx.x) >= batch.total_tiles) return;
+    __shared__ int routes[GATHER ? 2 * kQmvMaxProblems : 1];
+    qmv_load_routes<GATHER>(batch, routes);
 
     // Activation staging, one round: eight 16-byte chunks per thread are loaded
     // before any is written, so a round costs one trip to L2.  For 4-bit codes
@@ -927,7 +989,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     u32x4 nwv[PRO == 2 ? NCH : 1];
     auto stage_load = [&](int r, int c0, u32x4* v, int* dst, int k0 = 0) __attribute__((always_inline)) {
         const QmvProblem& pr = batch.p[batch.stage[r]];
-        const __amdgpu_buffer_rsrc_t xr = raw_rsrc(pr.x, uint32_t(M) * uint32_t(pr.K) * 2u);
+        const QmvPtrs op = qmv_ptrs<GATHER>(batch, batch.stage[r], routes);
+        const __amdgpu_buffer_rsrc_t xr = raw_rsrc(op.x, op.live ? uint32_t(M) * uint32_t(pr.K) * 2u : 0u);
         // (the prologue's inputs: with PRO = 2 a missing residual reads zero)
         const __amdgpu_buffer_rsrc_t x2r =
             raw_rsrc(PRO != 0 && batch.pro_second ? batch.pro_second : pr.x,
@@ -999,11 +1062,11 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     stage_load(0, threadIdx.x, xv, xdst);
     QmvStream ls;
     ls.pi = qmv_problem_of(batch, blockIdx.x, 0);
-    ls.L = qmv_tile_view<BITS, GS, TAIL>(batch, ls.pi, blockIdx.x, wave, ln, kq, 0, false, r_p).L;
+    ls.L = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, ls.pi, blockIdx.x, wave, ln, kq, 0, false, r_p, routes).L;
     ls.tile = blockIdx.x;
     ls.j = ls.j_stop = 0;
     ls.done = false;
-    qmv_stream_seek<BITS, GS, TAIL>(batch, ls, blockIdx.x, wave, ln, kq, r_p);
+    qmv_stream_seek<BITS, GS, TAIL, GATHER>(batch, ls, blockIdx.x, wave, ln, kq, r_p, routes);
     typedef QmvWBlock<BITS, GS, U, VEC> RingBlock;
     RingBlock ring[D];
     auto ring_load = [&](RingBlock& b) __attribute__((always_inline)) {
@@ -1013,7 +1076,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
 #pragma unroll
     for (int d = 0; d < D - 1; d++) {
         ring_load(ring[d]);
-        qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
+        qmv_stream_next<BITS, GS, TAIL, GATHER>(batch, ls, wave, ln, kq, r_p, routes);
     }
     stage_store(xv, xdst, int(threadIdx.x));
     if constexpr (PRO != 2) {  // (the planner keeps a normalized row to one round)
@@ -1045,7 +1108,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // blocks from the ring, then the spans that do not fill a block.
     int tile = blockIdx.x;
     int pi = qmv_problem_of(batch, tile, 0);
-    QmvTileView<BITS, GS> V = qmv_tile_view<BITS, GS, TAIL>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p);
+    QmvTileView<BITS, GS> V = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p,
+                                                                    routes);
     int left = V.nblk, jc = V.j_begin, iter = 0;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 
@@ -1116,7 +1180,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         tile = tile1;
         if (!has1) return false;
         pi = qmv_problem_of(batch, tile, pi);
-        V = qmv_tile_view<BITS, GS, TAIL>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p);
+        V = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p, routes);
         left = V.nblk;
         jc = V.j_begin;
         return true;
@@ -1147,7 +1211,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
 #pragma unroll
         for (int d = 0; d < D; d++) {
             ring_load(ring[(d + D - 1) % D]);
-            qmv_stream_next<BITS, GS, TAIL>(batch, ls, wave, ln, kq, r_p);
+            qmv_stream_next<BITS, GS, TAIL, GATHER>(batch, ls, wave, ln, kq, r_p, routes);
             if constexpr (!TAIL && PRO == 0) {
                 if (jc >= phase_end) restage();
             }
@@ -1215,7 +1279,7 @@ struct QmvLdsPlan {
 // size, scale type and M (<= MB).  Returns false when the problems do not fit
 // it (too many, LDS too small, buffers of 2^31 bytes or more, N % 16 != 0).
 template <int BITS, int GS, typename ST>
-static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& plan) {
+static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& plan, bool share_x = true) {
     typedef QmvGeom<BITS, GS> Geo;
     constexpr int W = kQmvLdsWaves, U = kQmvUnroll;
     static_assert(W >= 1 && W <= kQmvLdsMaxWaves, "waves per workgroup");
@@ -1249,7 +1313,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
         vec = vec && (G * 2) % align == 0 && aligned(q.s, align) && (q.b == nullptr || aligned(q.b, align));
         // stage each distinct activation matrix once
         p.x_lds = -1;
-        for (int j = 0; j < i; j++)
+        for (int j = 0; j < i && share_x; j++)
             if (B.p[j].x == q.x && B.p[j].K == q.K) p.x_lds = B.p[j].x_lds;
         if (p.x_lds < 0) {
             p.x_lds = lds;
@@ -1524,6 +1588,72 @@ bool launch_qmv_swiglu(int bits, const QmvSpec& spec, const QmvPrologue* pro, hi
     if (pro && pro->kind != 2) return false;
     if (bits == 4) return pro ? launch_qmv_swiglu_t<4, 2>(spec, pro, st) : launch_qmv_swiglu_t<4, 0>(spec, pro, st);
     if (bits == 8) return pro ? launch_qmv_swiglu_t<8, 2>(spec, pro, st) : launch_qmv_swiglu_t<8, 0>(spec, pro, st);
+    return false;
+}
+
+// Routed decode (gather_qmm, transpose, one bf16 activation row per output
+// batch): output batches in launches of up to kQmvMaxProblems problems whose
+// activation rows all fit LDS at once; every K a whole number of blocks and
+// vector-aligned parameters.  False, launching nothing, when the call does
+// not fit that (the caller then runs the general routed kernel).
+template <int BITS, int GS, typename ST>
+static bool launch_qmv_gather_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* s, const void* b,
+                                const GatherIdx& g, int64_t batch, int N, int K, hipStream_t st) {
+    const int kpad = (K + 63) / 64 * 64;
+    int per = (device_lds_bytes() - 16384) / (kpad * 2);
+    per = per > kQmvMaxProblems ? kQmvMaxProblems : per;
+    // at most two launches: many routes run faster as the single launch of
+    // the general routed kernel (4096 routes of 768 x 2048: 0.7 against 6.6 ms)
+    if (per < 1 || batch < 1 || batch > 2 * per) return false;
+    const int64_t G = K / GS;
+    std::vector<QmvLdsPlan> plans;
+    for (int64_t b0 = 0; b0 < batch; b0 += per) {
+        const int count = int(batch - b0 < per ? batch - b0 : per);
+        QmvSpec specs[kQmvMaxProblems];
+        for (int i = 0; i < count; i++)
+            specs[i] = QmvSpec{x, w, s, b, y + (b0 + i) * int64_t(N), N, K, N};
+        QmvLdsPlan plan;
+        if (!plan_qmv_lds<BITS, GS, ST>(specs, count, 1, plan, false) || !plan.vec || plan.tail ||
+            plan.B.phase_spans != 0)
+            return false;
+        plan.B.g_lhs = g.lhs;
+        plan.B.g_rhs = g.rhs;
+        plan.B.g_xb = g.x_batches;
+        plan.B.g_wb = g.w_batches;
+        plan.B.g_x_stride = K;
+        plan.B.g_w_stride = int64_t(N) * (int64_t(K) * BITS / 32);
+        plan.B.g_s_stride = int64_t(N) * G;
+        plan.B.g_b0 = int(b0);
+        plans.push_back(plan);
+    }
+    auto kernel = qmv_lds_kernel<BITS, GS, ST, 1, true, false, 0, BF16T, 0, true>;
+    for (const QmvLdsPlan& plan : plans) {
+        if (plan.lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, plan.lds);
+        kernel<<<dim3(unsigned(plan.grid)), dim3(64 * plan.waves), size_t(plan.lds), st>>>(plan.B);
+    }
+    return true;
+}
+
+bool launch_qmv_gather(int bits, int gs, int scale_dtype, uint16_t* y, const uint16_t* x, const uint32_t* w,
+                       const void* s, const void* b, const GatherIdx& g, int64_t batch, int N, int K,
+                       hipStream_t st) {
+    if (N % 16 != 0 || batch > INT32_MAX || (bits != 4 && bits != 8)) return false;
+    auto by_gs = [&](auto bc, auto stt) -> bool {
+        constexpr int B = decltype(bc)::value;
+        typedef decltype(stt) ST;
+        switch (gs) {
+        case 32: return launch_qmv_gather_t<B, 32, ST>(y, x, w, s, b, g, batch, N, K, st);
+        case 64: return launch_qmv_gather_t<B, 64, ST>(y, x, w, s, b, g, batch, N, K, st);
+        case 128: return launch_qmv_gather_t<B, 128, ST>(y, x, w, s, b, g, batch, N, K, st);
+        default: return false;
+        }
+    };
+    if (scale_dtype == EQ_DTYPE_BF16)
+        return bits == 4 ? by_gs(std::integral_constant<int, 4>{}, BF16T{}) : by_gs(std::integral_constant<int, 8>{}, BF16T{});
+    if (scale_dtype == EQ_DTYPE_F16)
+        return bits == 4 ? by_gs(std::integral_constant<int, 4>{}, F16T{}) : by_gs(std::integral_constant<int, 8>{}, F16T{});
     return false;
 }
 

@@ -4,7 +4,9 @@ oracle's fp64 gather_qmm_f64 on the same packed expert banks.
 Tolerance (the matmul rule, per output batch): |y - y_ref| <= 1e-2 *
 RMS(y_ref[b]) + 1/2 ulp_bf16(y_ref) for bf16 outputs, 1e-2 * RMS for f32.
 Cases: the routed-expert decode of eredu/src/backend/mlx/nn/moe.rs:121-139
-(x [routes, 1, K], lhs = arange, rhs = expert per route; the fast kernel),
+(x [routes, 1, K], lhs = arange, rhs = expert per route; the persistent
+decode kernel where N % 16 == 0 and K is whole blocks, the team kernel
+otherwise),
 the general kernels (M > 1, transpose = false, f16 / f32 activations, 2-bit),
 MLX's index broadcasting, out-of-range indices (zero rows), launches split at
 65535 batches, and the sorted_indices hint.
@@ -72,6 +74,19 @@ def test_routed_decode(cuda, bits, gs, sdt):
     """12 routes over 8 experts (repeats included), N = 390 (a partial team)."""
     rhs = np.array([5, 0, 7, 5, 2, 2, 1, 6, 3, 0, 4, 7])
     run(8, 390, 1024, gs, bits, np.arange(12), rhs, Bx=12, sdt=sdt, seed=bits * gs, biases=(gs != 128))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("sdt", [orc.BF16, orc.F16])
+def test_routed_decode_on_the_decode_kernel(cuda, bits, gs, sdt):
+    """N % 16 == 0 and K whole blocks: the persistent decode kernel with the
+    indices read on the device.  12 routes (two launches of up to 8), repeated
+    experts and x rows, one x index and one expert index out of range (zero
+    rows)."""
+    lhs = np.array([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 13, 2])
+    rhs = np.array([5, 0, 7, 5, 2, -1, 1, 6, 3, 0, 4, 7])
+    run(8, 256, 1024, gs, bits, lhs, rhs, Bx=12, sdt=sdt, seed=bits * gs + 5, biases=(gs != 128))
 
 
 @pytest.mark.parametrize("K", [4096, 8192, 12288])
