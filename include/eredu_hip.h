@@ -270,8 +270,9 @@ int eq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
  * 4, biases NULL): scales are u8 E8M0 bytes, the smallest power of two 2^e,
  * e in [-127, 127], with max|w| / 2^e <= 6 (a group with a NaN or infinity:
  * 255, an all-zero group: 0), and each code the nearest E2M1 value of
- * w / 2^e, ties to the even code, sign bit set for w < 0 (the OCP
- * microscaling rule; MLX's own quantizer is not available to check against).
+ * w / 2^e, ties to the even code, sign bit set for w < 0.  Nothing
+ * saturates, unlike the OCP MX v1.0 rule (2^(floor(log2 max|w|) - 2), then a
+ * clamp to 6); MLX's own quantizer is not available to check against.
  */
 int eq_quantize(uint32_t* w_out, void* scales, void* biases, const void* w, int64_t rows, int64_t cols,
                 int group_size, int bits, const char* mode, int dtype, eq_stream_t stream);

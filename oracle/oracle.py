@@ -299,9 +299,10 @@ def mxfp4_dequant_f64(w, scales, rows, cols) -> np.ndarray:
 
 def mxfp4_quantize(wf32: np.ndarray):
     """(u32 codes, u8 scales) of w [rows, cols] in groups of 32 along the last
-    axis, by the OCP MX v1.0 rule (sec. 6.3) with the exponent chosen so that
-    nothing saturates: the scale is the smallest power of two 2^e, e in
-    [-127, 127], with amax / 2^e <= 6; every value is w / 2^e rounded to the
+    axis: the scale is the smallest power of two 2^e, e in [-127, 127], with
+    amax / 2^e <= 6, so nothing saturates (this is not the OCP MX v1.0
+    sec. 6.3 rule, which takes 2^(floor(log2 amax) - 2) and clamps to 6:
+    at amax = 7 that rule gives scale 1, this one 2); every value is w / 2^e rounded to the
     nearest E2M1 value, ties to the even code, sign bit set for w < 0; a
     group with a NaN or an infinity gets scale byte 255 (NaN) and magnitude
     codes 0, an all-zero group byte 0.  Found by
