@@ -191,31 +191,40 @@ __global__ __launch_bounds__(256) void attn_states_kernel(float* __restrict__ st
                                                           uint16_t* __restrict__ v_cache,
                                                           const float* __restrict__ freqs, int pos_arg,
                                                           const int32_t* __restrict__ pos_p, int max_seq,
-                                                          int n_heads, int n_kv_heads, float scale) {
+                                                          int group, float scale) {
     __shared__ __attribute__((aligned(16))) float qs[4][kHeadDim];  // rotated queries of this group
     __shared__ __attribute__((aligned(16))) uint16_t ks[kAttnChunk][kRowPad];
     __shared__ __attribute__((aligned(16))) uint16_t vs[kAttnChunk][kRowPad];
     __shared__ float knew[kHeadDim];
     __shared__ float rot[2][kHeadDim / 2];  // cos, sin of the angles pos / freqs[i]
-    const int pos = pos_p ? __builtin_amdgcn_readfirstlane(*pos_p) : pos_arg;
+    // Every load of the prologue is requested before any is waited for, so
+    // that they cost one memory round trip: the position by a vector load
+    // (a scalar one would be waited for together with the argument loads
+    // the addresses below need), then the group's queries, the new key, the
+    // frequencies and the split's first chunk, each at an in-range index
+    // with dead lanes' values selected away afterwards (a load behind a
+    // per-lane branch is waited for where the branch joins).
+    const uint32_t pos_v = __builtin_amdgcn_raw_buffer_load_b32(raw_rsrc(pos_p, pos_p ? 4u : 0u), 0u, 0u, 0);
     const int g = blockIdx.x, split = blockIdx.y;
-    const int group = n_heads / n_kv_heads;  // <= 4
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint16_t* kc = k_cache + int64_t(g) * max_seq * kHeadDim;
     uint16_t* vc = v_cache + int64_t(g) * max_seq * kHeadDim;
 
-    // the group's queries, the new key and the frequencies first, so that
-    // waiting for them does not wait for the chunk
     float qv[2];
 #pragma unroll
     for (int r = 0; r < 2; r++) {
         const int i = tid + 256 * r;
-        qv[r] = i < group * kHeadDim ? bf16_bits_to_f32(q[int64_t(g) * group * kHeadDim + i]) : 0.f;
+        const bool live = i < group * kHeadDim;
+        const float v = bf16_bits_to_f32(q[int64_t(g) * group * kHeadDim + (live ? i : 0)]);
+        qv[r] = live ? v : 0.f;
     }
-    const float kn = tid < kHeadDim ? bf16_bits_to_f32(k_new[int64_t(g) * kHeadDim + tid]) : 0.f;
-    const float fr = tid < kHeadDim / 2 ? freqs[tid] : 1.f;
+    const float kn_v = bf16_bits_to_f32(k_new[int64_t(g) * kHeadDim + (tid & (kHeadDim - 1))]);
+    const float fr_v = freqs[tid & (kHeadDim / 2 - 1)];
+    const float kn = tid < kHeadDim ? kn_v : 0.f;
+    const float fr = tid < kHeadDim / 2 ? fr_v : 1.f;
     // this thread's two 16-byte pieces of a chunk's keys and of its values:
-    // piece i = tid + 256 r is position i / 16, dimensions 8 (i % 16) ..
+    // piece i = tid + 256 r is position i / 16, dimensions 8 (i % 16) ..;
+    // pieces past `limit` read row 0 and are replaced by zeros
     uint4 kr[2], vr[2];
     auto fetch = [&](int c, int limit) __attribute__((always_inline)) {
         const int p0 = c * kAttnChunk;
@@ -223,11 +232,15 @@ __global__ __launch_bounds__(256) void attn_states_kernel(float* __restrict__ st
         for (int r = 0; r < 2; r++) {
             const int i = tid + 256 * r, p = p0 + i / (kHeadDim / 8), v = i % (kHeadDim / 8);
             const bool live = p < limit;
-            kr[r] = live ? reinterpret_cast<const uint4*>(kc + int64_t(p) * kHeadDim)[v] : make_uint4(0u, 0u, 0u, 0u);
-            vr[r] = live ? reinterpret_cast<const uint4*>(vc + int64_t(p) * kHeadDim)[v] : make_uint4(0u, 0u, 0u, 0u);
+            const int64_t row = live ? int64_t(p) * kHeadDim : 0;
+            const uint4 kx = reinterpret_cast<const uint4*>(kc + row)[v];
+            const uint4 vx = reinterpret_cast<const uint4*>(vc + row)[v];
+            kr[r] = live ? kx : make_uint4(0u, 0u, 0u, 0u);
+            vr[r] = live ? vx : make_uint4(0u, 0u, 0u, 0u);
         }
     };
     fetch(split, max_seq);  // rows past pos are masked out below
+    const int pos = pos_p ? int(__builtin_amdgcn_readfirstlane(pos_v)) : pos_arg;
     const bool valid = pos >= 0 && pos < max_seq;
     const int nch = valid ? pos / kAttnChunk + 1 : 0;
     if (split >= nch) return;
@@ -374,8 +387,18 @@ __global__ __launch_bounds__(256) void attn_states_combine_kernel(uint16_t* __re
                                                                   const float* __restrict__ states, int pos_arg,
                                                                   const int32_t* __restrict__ pos_p, int max_seq) {
     __shared__ float2 part[4][64];
-    const int pos = pos_p ? __builtin_amdgcn_readfirstlane(*pos_p) : pos_arg;
+    // The position (a vector load, as in attn_states_kernel) and all 64
+    // states of the head are requested together; states past the position's
+    // chunk count (stale) are selected away once the position is known.
+    const uint32_t pos_v = __builtin_amdgcn_raw_buffer_load_b32(raw_rsrc(pos_p, pos_p ? 4u : 0u), 0u, 0u, 0);
     const int h = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float* st = states + int64_t(h) * kAttnSplits * kAttnStateFloats;
+    float2 ov[kAttnSplits / 4];
+#pragma unroll
+    for (int k = 0; k < kAttnSplits / 4; k++)
+        ov[k] = reinterpret_cast<const float2*>(st + (w + 4 * k) * kAttnStateFloats + 2)[lane];
+    const float m_v = st[lane * kAttnStateFloats], l_v = st[lane * kAttnStateFloats + 1];
+    const int pos = pos_p ? int(__builtin_amdgcn_readfirstlane(pos_v)) : pos_arg;
     const int nch = pos >= 0 && pos < max_seq ? pos / kAttnChunk + 1 : 0;
     const int ns = min(nch, kAttnSplits);
     uint32_t* dst = reinterpret_cast<uint32_t*>(out + int64_t(h) * kHeadDim) + lane;
@@ -383,15 +406,11 @@ __global__ __launch_bounds__(256) void attn_states_combine_kernel(uint16_t* __re
         if (w == 0) *dst = 0u;
         return;
     }
-    const float* st = states + int64_t(h) * kAttnSplits * kAttnStateFloats;
     float2 o[kAttnSplits / 4];
 #pragma unroll
-    for (int k = 0; k < kAttnSplits / 4; k++) {
-        const int y = w + 4 * k;
-        o[k] = y < ns ? reinterpret_cast<const float2*>(st + y * kAttnStateFloats + 2)[lane] : make_float2(0.f, 0.f);
-    }
-    const float m = lane < ns ? st[lane * kAttnStateFloats] : -INFINITY;
-    const float l = lane < ns ? st[lane * kAttnStateFloats + 1] : 0.f;
+    for (int k = 0; k < kAttnSplits / 4; k++) o[k] = w + 4 * k < ns ? ov[k] : make_float2(0.f, 0.f);
+    const float m = lane < ns ? m_v : -INFINITY;
+    const float l = lane < ns ? l_v : 0.f;
     float mx = m;
 #pragma unroll
     for (int of = 32; of > 0; of >>= 1) mx = fmaxf(mx, __shfl_xor(mx, of));
@@ -669,7 +688,7 @@ static void launch_attention(float* states, void* out, const void* q, const void
     attn_states_kernel<<<dim3(unsigned(n_kv_heads), unsigned(kAttnSplits)), dim3(256), 0, st>>>(
         states, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new),
         static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), freqs,
-        int(pos), pos_p, int(max_seq), n_heads, n_kv_heads, scale);
+        int(pos), pos_p, int(max_seq), n_heads / n_kv_heads, scale);
     attn_states_combine_kernel<<<dim3(unsigned(n_heads)), dim3(256), 0, st>>>(static_cast<uint16_t*>(out), states,
                                                                                int(pos), pos_p, int(max_seq));
 }

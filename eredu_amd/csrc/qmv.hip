@@ -528,25 +528,30 @@ struct QmvProblem {
     uint16_t* y;
     int N, K, ldy;
     int spw;             // spans per wave
-    int tile0;           // first global tile of this problem
     int x_lds;           // LDS byte offset of its activations
     int kpad;            // activation row length in LDS (multiple of 64)
     float inv_cpr;       // 1 / (kpad / 8): row of a 16-byte LDS chunk by multiplication
 };
 
+// Field order: every workgroup starts by reading its arguments through the
+// scalar cache, where one round of requests covers 8 lines of 64 bytes (a
+// larger first round is split by the compiler into two dependent ones).  The
+// header, the routed/prologue fields and problems 0-3 sit in the first 512
+// bytes, which the kernel requests together at entry; problems 4-7 (launches
+// of more than four problems) are read when used.
 struct QmvBatch {
-    QmvProblem p[kQmvMaxProblems];
     int count;               // problems
     int M;                   // activation rows (all problems)
     int total_tiles;
     int nstage;              // distinct activation matrices to stage
-    int stage[kQmvMaxProblems];  // problem whose x each staged matrix is
+    int tile0[kQmvMaxProblems];  // first global tile of each problem; INT_MAX past count
     int zero_lds, zero_bytes;
     int red_lds;             // 2 x waves x M x 16 floats
     // K phases (one problem, one tile per workgroup, activations too long for
     // LDS): LDS holds phase_spans spans of the rows at a time, phase p
     // covering spans [p * phase_spans, (p + 1) * phase_spans); 0 = no phases.
     int phase_spans;
+    int stage[kQmvMaxProblems];  // problem whose x each staged matrix is
     // Activation prologue (M = 1, one staged input): 1 = silu(x) * pro_second,
     // 2 = RMSNorm(x + pro_second) * pro_weight, the sum also written to
     // pro_hidden_out by workgroup 0.  Applied while staging.
@@ -560,11 +565,16 @@ struct QmvBatch {
     // the batch itself, or 0 when there is one batch) times g_x_stride
     // elements, g_w_stride words and g_s_stride parameters.  An index outside
     // its operand's batches gives a zero row.
+    int g_b0;
     const int32_t* g_lhs;
     const int32_t* g_rhs;
     int64_t g_xb, g_wb, g_x_stride, g_w_stride, g_s_stride;
-    int g_b0;
+    QmvProblem p[kQmvMaxProblems];
 };
+constexpr int kQmvArgLines = 8;  // 64-byte lines requested at entry
+static_assert(offsetof(QmvBatch, p) + 4 * sizeof(QmvProblem) <= 64 * kQmvArgLines,
+              "the header and problems 0-3 fit the lines requested at entry");
+
 
 // Routed problems: the x and expert indices of each problem of the launch,
 // resolved once per workgroup from device memory into LDS (routes[2 pi] =
@@ -770,7 +780,7 @@ __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& b
     QmvTileView<BITS, GS> v;
     const int N = pr.N, K = pr.K, G = K / GS;
     v.K = K;
-    v.n0 = (tile - pr.tile0) * 16;
+    v.n0 = (tile - batch.tile0[pi]) * 16;
     v.S_full = K / Geo::SPAN;
     const int S = (K + Geo::SPAN - 1) / Geo::SPAN;
     v.j_begin = qmv_block_stride<TAIL>() != kQmvUnroll ? wave * kQmvUnroll : wave * pr.spw;
@@ -814,7 +824,7 @@ __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& b
 __device__ __forceinline__ int qmv_problem_of(const QmvBatch& batch, int t, int /*hint*/) {
     int pi = 0;
 #pragma unroll
-    for (int i = 1; i < kQmvMaxProblems; i++) pi += (i < batch.count && t >= batch.p[i].tile0) ? 1 : 0;
+    for (int i = 1; i < kQmvMaxProblems; i++) pi += t >= batch.tile0[i] ? 1 : 0;
     return __builtin_amdgcn_readfirstlane(pi);
 }
 
@@ -972,7 +982,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     const int kq = lane >> 4;
     const int M = batch.M;
     const int r_p = kq * P / 4;  // result group block of this lane
-    prefetch_args(batch);
+    prefetch_args<kQmvArgLines, offsetof(QmvBatch, total_tiles) / 4>(batch);
     if (int(blockIdx.x) >= batch.total_tiles) return;
     __shared__ int routes[GATHER ? 2 * kQmvMaxProblems : 1];
     qmv_load_routes<GATHER>(batch, routes);
@@ -1286,6 +1296,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     if (count < 1 || count > kQmvMaxProblems || M < 1 || M > Geo::MB) return false;
     QmvBatch& B = plan.B;
     B = QmvBatch{};
+    for (int i = 0; i < kQmvMaxProblems; i++) B.tile0[i] = INT_MAX;
     B.count = count;
     B.M = M;
     const int pbytes = QmvParamWords<BITS, GS, U>::WORDS * 4;
@@ -1306,7 +1317,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
         // spans per wave: a multiple of U (blocks start at multiples of U)
         p.spw = ((S + W - 1) / W + U - 1) / U * U;
         tail = tail || q.K % (U * Geo::SPAN) != 0;
-        p.tile0 = tiles;
+        B.tile0[i] = tiles;
         tiles += q.N / 16;
         p.kpad = (q.K + 63) / 64 * 64;
         p.inv_cpr = 1.0f / float(p.kpad / 8);
