@@ -180,6 +180,10 @@ struct QmvGeom {
     static constexpr int SPAN = 4 * CPL;                    // codes per row per span
     static constexpr int P = SPAN > GS ? SPAN / GS : 1;     // quantization groups per span
     static constexpr int MB = 16 / P;                       // A-operand rows per group block
+    // Activation rows one pass of the LDS kernel takes: MB, or with four
+    // groups per span (4-bit, group 32) two sets of MB rows, each set its own
+    // MFMAs on the same unpacked codes.
+    static constexpr int RPL = P == 4 ? 2 * MB : MB;
     static constexpr int STEPS = CPL / 8;                   // MFMAs per span
     static constexpr int SPAN_WORDS = SPAN * BITS / 32;     // = 16
 };
@@ -347,6 +351,34 @@ __device__ __forceinline__ void qmv_span(f32x4& acc, const bf16x8* xa, const u32
     const float beff = off != 0.f ? fmaf(-off, sc, bi) : bi;
 #pragma unroll
     for (int r = 0; r < MREG; r++) acc[r] = fmaf(sc, t4[r], fmaf(beff, xs[r], acc[r]));
+}
+
+// qmv_span for two sets of four activation rows (group size 32, 4-bit codes,
+// MREG 8): rows 0-3 through the A operand xa, rows 4-7 through xa2, on the
+// same unpacked codes; acc holds rows 0-3 and acc2 rows 4-7.
+template <int BITS, int GS, typename ST, bool PERM, typename XT>
+__device__ __forceinline__ void qmv_span2(f32x4& acc, f32x4& acc2, const bf16x8* xa, const bf16x8* xa2,
+                                          const u32x4& wd, float sc, float bi, const UnpackConsts& uc, bf16x8 ones) {
+    typedef QmvGeom<BITS, GS> Geo;
+    typedef QmvAct<XT> A;
+    static_assert(BITS == 4 && Geo::P == 4, "two row sets: 4-bit codes, four groups per span");
+    f32x4 t4 = {0.f, 0.f, 0.f, 0.f}, xs = {0.f, 0.f, 0.f, 0.f};
+    f32x4 t4b = {0.f, 0.f, 0.f, 0.f}, xsb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < Geo::STEPS; t++) {
+        const bf16x8 bq = PERM ? unpack4_bf16_offset128_perm(wd[t], uc.c43) : unpack4_bf16_offset128(wd[t], uc);
+        t4 = A::mfma(xa[t], bq, t4);
+        xs = A::mfma(xa[t], ones, xs);
+        t4b = A::mfma(xa2[t], bq, t4b);
+        xsb = A::mfma(xa2[t], ones, xsb);
+    }
+    constexpr float off = A::template offset<BITS>();
+    const float beff = off != 0.f ? fmaf(-off, sc, bi) : bi;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        acc[r] = fmaf(sc, t4[r], fmaf(beff, xs[r], acc[r]));
+        acc2[r] = fmaf(sc, t4b[r], fmaf(beff, xsb[r], acc2[r]));
+    }
 }
 
 // Scale and bias of span u of a block for this lane's result group r_p.
@@ -702,15 +734,22 @@ __device__ __forceinline__ void qmv_wload_ring(QmvWBlock<BITS, GS, NU, true>& b,
 
 // A operands of span j0 + u are read from LDS at xa_t + j0 * xstep + u * SPAN * 2
 // (dead rows have xstep 0 and xa_t in the zero block, which covers NU spans).
+// MREG 8: the second row set's A operands at xa_t2 + j0 * xstep2 (acc2).
 template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC, typename XT = BF16T>
 __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, GS, NU, VEC>& b, const char* smem,
                                              const uint32_t* xa_t, uint32_t xstep, int j0, int r_p,
-                                             float bias_on, const UnpackConsts& uc, bf16x8 ones) {
+                                             float bias_on, const UnpackConsts& uc, bf16x8 ones,
+                                             f32x4* acc2 = nullptr, const uint32_t* xa_t2 = nullptr,
+                                             uint32_t xstep2 = 0) {
     typedef QmvGeom<BITS, GS> Geo;
     asm volatile("" ::: "memory");
-    uint32_t xb[Geo::STEPS];
+    uint32_t xb[Geo::STEPS], xb2[MREG == 8 ? Geo::STEPS : 1];
 #pragma unroll
     for (int t = 0; t < Geo::STEPS; t++) xb[t] = xa_t[t] + uint32_t(j0) * xstep;
+    if constexpr (MREG == 8) {
+#pragma unroll
+        for (int t = 0; t < Geo::STEPS; t++) xb2[t] = xa_t2[t] + uint32_t(j0) * xstep2;
+    }
 #pragma unroll
     for (int u = 0; u < NU; u++) {
         bf16x8 xa[Geo::STEPS];
@@ -719,7 +758,15 @@ __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, G
             xa[t] = *reinterpret_cast<const bf16x8*>(smem + xb[t] + u * Geo::SPAN * 2);
         float sc, bi;
         qmv_params<BITS, GS, ST, NU, VEC>(b.sw, b.bw, u, r_p, bias_on, sc, bi);
-        qmv_span<BITS, GS, ST, MREG, BITS == 4, XT>(acc, xa, b.wd[u], sc, bi, uc, ones);
+        if constexpr (MREG == 8) {
+            bf16x8 xa2[Geo::STEPS];
+#pragma unroll
+            for (int t = 0; t < Geo::STEPS; t++)
+                xa2[t] = *reinterpret_cast<const bf16x8*>(smem + xb2[t] + u * Geo::SPAN * 2);
+            qmv_span2<BITS, GS, ST, BITS == 4, XT>(acc, *acc2, xa, xa2, b.wd[u], sc, bi, uc, ones);
+        } else {
+            qmv_span<BITS, GS, ST, MREG, BITS == 4, XT>(acc, xa, b.wd[u], sc, bi, uc, ones);
+        }
     }
 }
 
@@ -764,6 +811,9 @@ struct QmvTileView {
     float bias_on;
     uint32_t xa_t[QmvGeom<BITS, GS>::STEPS];
     uint32_t xstep;
+    // the second row set (rows MB .. 2 MB - 1 of the group blocks; MREG 8)
+    uint32_t xa_t2[QmvGeom<BITS, GS>::STEPS];
+    uint32_t xstep2;
 };
 
 // TAIL = false: every problem's K is a multiple of U * SPAN, so a wave's
@@ -773,7 +823,7 @@ struct QmvTileView {
 template <int BITS, int GS, bool TAIL, bool GATHER = false>
 __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& batch, int pi, int tile, int wave,
                                                               int ln, int kq, int a_m, bool a_live, int r_p,
-                                                              const int* routes = nullptr) {
+                                                              const int* routes = nullptr, bool a_live2 = false) {
     typedef QmvGeom<BITS, GS> Geo;
     const QmvProblem& pr = batch.p[pi];
     const QmvPtrs op = qmv_ptrs<GATHER>(batch, pi, routes);
@@ -807,14 +857,23 @@ __device__ __forceinline__ QmvTileView<BITS, GS> qmv_tile_view(const QmvBatch& b
         v.xa_t[t] = a_live ? uint32_t(pr.x_lds + a_m * pr.kpad * 2 + (((kq * Geo::CPL / 8 + t) ^ (a_m & 7)) * 16))
                            : uint32_t(batch.zero_lds);
     v.xstep = a_live ? Geo::SPAN * 2 : 0;
+    {
+        const int a_m2 = a_m + Geo::MB;
+#pragma unroll
+        for (int t = 0; t < Geo::STEPS; t++)
+            v.xa_t2[t] = a_live2
+                             ? uint32_t(pr.x_lds + a_m2 * pr.kpad * 2 + (((kq * Geo::CPL / 8 + t) ^ (a_m2 & 7)) * 16))
+                             : uint32_t(batch.zero_lds);
+        v.xstep2 = a_live2 ? Geo::SPAN * 2 : 0;
+    }
     if (!TAIL && v.nblk == 0) {
         v.nblk = 1;
         v.j_begin = v.j_end = v.j_full_end = 0;
         v.S_full = 1 << 20;  // no ragged span
         v.L.woff = v.L.soff = kOutOfRange;
 #pragma unroll
-        for (int t = 0; t < Geo::STEPS; t++) v.xa_t[t] = uint32_t(batch.zero_lds);
-        v.xstep = 0;
+        for (int t = 0; t < Geo::STEPS; t++) v.xa_t[t] = v.xa_t2[t] = uint32_t(batch.zero_lds);
+        v.xstep = v.xstep2 = 0;
     }
     return v;
 }
@@ -993,6 +1052,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // order in which unpack4_bf16_offset128_perm delivers the codes.
     const int zero_lds = __builtin_amdgcn_readfirstlane(batch.zero_lds);
     static_assert(PRO == 0 || MREG == 1, "activation prologues are for one activation row");
+    static_assert(MREG != 8 || (Geo::RPL == 8 && !TAIL && VEC), "two row sets: group 32, whole blocks, vector parameters");
     static_assert(PRO == 0 || std::is_same<XT, BF16T>::value, "activation prologues are for bf16 rows");
     constexpr int NCH = PRO == 2 ? 2 : 8;  // chunks per thread and staging round
     u32x4 x2v[PRO != 0 ? NCH : 1];         // second input (up, residual); with PRO = 2 also the norm weight
@@ -1112,6 +1172,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // that block is the group of this lane's k-slots (block kq * P / 4).
     const int a_m = ln % MB;
     const bool a_live = (ln / MB) == (kq * P / 4) && a_m < M;
+    const bool a_live2 = MREG == 8 && (ln / MB) == (kq * P / 4) && a_m + MB < M;  // the second row set
     float* red = reinterpret_cast<float*>(smem + batch.red_lds);
 
     // The compute side walks the same tiles; per tile it takes its V.nblk
@@ -1119,9 +1180,10 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     int tile = blockIdx.x;
     int pi = qmv_problem_of(batch, tile, 0);
     QmvTileView<BITS, GS> V = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p,
-                                                                    routes);
+                                                                    routes, a_live2);
     int left = V.nblk, jc = V.j_begin, iter = 0;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};  // rows MB .. 2 MB - 1 (MREG 8)
 
     // Ends the current tile: leftover spans, the cross-wave sum, the store;
     // then moves to the next tile.  False when the workgroup has no more.
@@ -1151,17 +1213,25 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         }
         // Fold the P group blocks, then combine the waves through LDS (two
         // slots: a wave may fill the next tile's slot while this one is read).
+        constexpr int R1 = MREG < 4 ? MREG : 4;  // registers of the first row set
 #pragma unroll
-        for (int r = 0; r < MREG; r++) {
+        for (int r = 0; r < R1; r++) {
             if (P >= 4) acc[r] += __shfl_xor(acc[r], 16);
             if (P >= 2) acc[r] += __shfl_xor(acc[r], 32);
+            if constexpr (MREG == 8) {
+                acc2[r] += __shfl_xor(acc2[r], 16);
+                acc2[r] += __shfl_xor(acc2[r], 32);
+            }
         }
         float* slot = red + (iter & 1) * (nwaves * M * 16);
         if (r_p == 0) {
 #pragma unroll
-            for (int r = 0; r < MREG; r++) {
+            for (int r = 0; r < R1; r++) {
                 const int m = 4 * kq + r;
                 if (m < M) slot[(wave * M + m) * 16 + ln] = acc[r];
+                if constexpr (MREG == 8) {
+                    if (m + MB < M) slot[(wave * M + m + MB) * 16 + ln] = acc2[r];
+                }
             }
         }
         const int tile1 = tile + int(gridDim.x);
@@ -1187,10 +1257,11 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         }
         iter++;
         acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc2 = f32x4{0.f, 0.f, 0.f, 0.f};
         tile = tile1;
         if (!has1) return false;
         pi = qmv_problem_of(batch, tile, pi);
-        V = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p, routes);
+        V = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, pi, tile, wave, ln, kq, a_m, a_live, r_p, routes, a_live2);
         left = V.nblk;
         jc = V.j_begin;
         return true;
@@ -1227,7 +1298,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
             }
             if (opaque_one()) {
                 qmv_wcompute<BITS, GS, ST, MREG, U, VEC, XT>(acc, ring[d], smem, V.xa_t, V.xstep, jc - phase_base, r_p,
-                                                          V.bias_on, uc, ones);
+                                                          V.bias_on, uc, ones, &acc2, V.xa_t2, V.xstep2);
             } else {
                 qmv_retire(ring[d]);
             }
@@ -1293,7 +1364,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     typedef QmvGeom<BITS, GS> Geo;
     constexpr int W = kQmvLdsWaves, U = kQmvUnroll;
     static_assert(W >= 1 && W <= kQmvLdsMaxWaves, "waves per workgroup");
-    if (count < 1 || count > kQmvMaxProblems || M < 1 || M > Geo::MB) return false;
+    if (count < 1 || count > kQmvMaxProblems || M < 1 || M > Geo::RPL) return false;
     QmvBatch& B = plan.B;
     B = QmvBatch{};
     for (int i = 0; i < kQmvMaxProblems; i++) B.tile0[i] = INT_MAX;
@@ -1366,6 +1437,7 @@ static bool plan_qmv_lds(const QmvSpec* specs, int count, int M, QmvLdsPlan& pla
     lds += red_bytes;
 
     if (lds > device_lds_bytes()) return false;
+    if (M > Geo::MB && (!vec || tail)) return false;  // two row sets: whole blocks, vector parameters
     plan.lds = lds;
     plan.vec = vec;
     plan.tail = tail;
@@ -1383,6 +1455,12 @@ static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
                                       plan.lds);
         kernel<<<dim3(unsigned(plan.grid)), dim3(64 * plan.waves), size_t(plan.lds), st>>>(plan.B);
     };
+    if constexpr (QmvGeom<BITS, GS>::RPL > QmvGeom<BITS, GS>::MB) {
+        if (plan.B.M > QmvGeom<BITS, GS>::MB) {  // (the planner checked vec and whole blocks)
+            go(qmv_lds_kernel<BITS, GS, ST, 8, true, false, 0, XT>);
+            return;
+        }
+    }
     if (plan.B.M == 1) {
         if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 1, true, false, 0, XT>);
         else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true, true, 0, XT>);
@@ -1394,6 +1472,25 @@ static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
     }
 }
 
+// Activation rows per launch of the LDS kernel for these problems: RPL when
+// the two-row-set kernel takes them (every K whole blocks, vector parameter
+// loads), else MB.
+template <int BITS, int GS>
+static int qmv_launch_rows(const QmvSpec* specs, int count) {
+    typedef QmvGeom<BITS, GS> Geo;
+    if (Geo::RPL == Geo::MB) return Geo::MB;
+    const int pbytes = QmvParamWords<BITS, GS, kQmvUnroll>::WORDS * 4;
+    const int align = pbytes < 16 ? pbytes : 16;
+    for (int i = 0; i < count; i++) {
+        const QmvSpec& q = specs[i];
+        const int64_t G = q.K / GS;
+        if (q.K % (kQmvUnroll * Geo::SPAN) != 0 || (G * 2) % align != 0 || !aligned(q.s, align) ||
+            (q.b != nullptr && !aligned(q.b, align)))
+            return Geo::MB;
+    }
+    return Geo::RPL;
+}
+
 template <int BITS, int GS, typename ST, typename XT>
 static bool launch_qmv_lds(const QmvSpec* specs, int count, int M, hipStream_t st) {
     QmvLdsPlan plan;
@@ -1403,14 +1500,15 @@ static bool launch_qmv_lds(const QmvSpec* specs, int count, int M, hipStream_t s
 }
 
 // Grouped decode launch: problems in groups of kQmvMaxProblems, activation
-// rows in chunks of MB; every launch is planned before any is issued.
+// rows in chunks of qmv_launch_rows; every launch is planned before any is
+// issued.
 template <int BITS, int GS, typename ST, typename XT>
 static bool launch_qmv_group_t(const QmvSpec* specs, int count, int M, hipStream_t st) {
-    typedef QmvGeom<BITS, GS> Geo;
     std::vector<QmvLdsPlan> plans;
     QmvSpec chunk[kQmvMaxProblems];
-    for (int m0 = 0; m0 < M; m0 += Geo::MB) {
-        const int mc = M - m0 < Geo::MB ? M - m0 : Geo::MB;
+    const int rows = qmv_launch_rows<BITS, GS>(specs, count);
+    for (int m0 = 0; m0 < M; m0 += rows) {
+        const int mc = M - m0 < rows ? M - m0 : rows;
         for (int i0 = 0; i0 < count; i0 += kQmvMaxProblems) {
             const int n = count - i0 < kQmvMaxProblems ? count - i0 : kQmvMaxProblems;
             for (int i = 0; i < n; i++) {
@@ -1430,11 +1528,14 @@ template <int BITS, int GS, typename ST, typename XT>
 static void launch_qmv_t(uint16_t* y, const uint16_t* x, const uint32_t* w, const void* sv, const void* bv, int M,
                          int N, int K, hipStream_t st) {
     typedef QmvGeom<BITS, GS> Geo;
-    // Persistent LDS variant, in chunks of at most MB activation rows; the rows
-    // it does not take (activations too large for LDS) go to the kernel above.
+    // Persistent LDS variant, in chunks of at most qmv_launch_rows activation
+    // rows; the rows it does not take (activations too large for LDS) go to
+    // the kernel above.
     int m0 = 0;
-    for (; m0 < M; m0 += Geo::MB) {
-        const int mc = M - m0 < Geo::MB ? M - m0 : Geo::MB;
+    const QmvSpec q0{x, w, sv, bv, y, N, K, N};
+    const int rows = qmv_launch_rows<BITS, GS>(&q0, 1);
+    for (; m0 < M; m0 += rows) {
+        const int mc = M - m0 < rows ? M - m0 : rows;
         const QmvSpec q{x + int64_t(m0) * K, w, sv, bv, y + int64_t(m0) * N, N, K, N};
         if (!launch_qmv_lds<BITS, GS, ST, XT>(&q, 1, mc, st)) break;
     }

@@ -286,3 +286,41 @@ def test_qmv_activations_staged_in_k_phases(cuda, M, K, gs, bits):
     problem of at most one tile per workgroup: the decode kernel stages them
     in K phases (the down projection at batch 8 among them)."""
     run_case(M, 256, K, gs, bits, seed=M + K + bits)
+
+
+@pytest.mark.parametrize("sdt", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("M,K", [(6, 2048), (8, 4096), (7, 2080), (8, 14336)])
+def test_qmv_group32_two_row_sets(cuda, sdt, M, K):
+    """4-bit group 32 at 5-8 activation rows: one pass of the decode kernel
+    takes them as two sets of four rows (K a whole number of 512-code blocks;
+    K = 2080 runs as 4-row passes, K = 14336 stages its activations in K
+    phases).  Against the oracle, and each row bit-equal to the same row
+    computed alone (M = 1), whichever pass structure took it."""
+    N = 256
+    w, s, b = synthetic_linear(N, K, 32, 4, seed=M + K, scale_dtype=sdt)
+    xb = synthetic_x(M, K, seed=K + 3)
+    wd, sd, bd = dev_words(w), dev_param(s, sdt), dev_param(b, sdt)
+    y = quantized_matmul_with_mode(dev_bf16(xb), wd, sd, bd, True, 32, 4)
+    torch.cuda.synchronize()
+    ref = orc.quantized_matmul_f64(xb, orc.BF16, w, s, b, sdt, True, 32, 4, N, K)
+    ok, worst, rms = orc.matmul_within_tolerance(host_f32(y), ref, True)
+    assert ok, f"max|err|/RMS = {worst:.3e}"
+    for m in range(M):
+        y1 = quantized_matmul_with_mode(dev_bf16(xb[m:m + 1]), wd, sd, bd, True, 32, 4)
+        torch.cuda.synchronize()
+        assert torch.equal(y[m:m + 1].view(torch.int16), y1.view(torch.int16)), f"row {m}"
+
+
+def test_batched_group32_two_row_sets_equal_separate_calls(cuda):
+    # 8 rows of 4-bit group-32 problems whose K are whole blocks: the grouped
+    # launch and the separate calls both take one two-row-set pass
+    specs = [(256, 1024), (128, 1024), (384, 2048)]
+    probs, host = _batch_problems(specs, 8, 32, 4, seed=32, biases=True)
+    ys = quantized_matmul_batched(probs, transpose=True, group_size=32, bits=4)
+    torch.cuda.synchronize()
+    for (x, w, s, b), y, (xh, wh, sh, bh, N, K) in zip(probs, ys, host):
+        y1 = quantized_matmul_with_mode(x, w, s, b, True, 32, 4)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y1.view(torch.int16))
+        ref = orc.quantized_matmul_f64(xh, orc.BF16, wh, sh, bh, orc.BF16, True, 32, 4, N, K)
+        assert orc.matmul_within_tolerance(host_f32(y), ref, True)[0]
