@@ -186,7 +186,7 @@ template <int BITS, int GS, typename ST, bool SPLIT, bool PW, typename XT = BF16
 __global__ __launch_bounds__(kQmmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void qmm_mfma_kernel(
     const QmmArgs args) {
     constexpr int BM = 32 * TM, BN = 128 * TN, LBUF = BM * kBK * 2;  // LBUF: bytes per K-group buffer
-    static_assert((TM == 4 && TN == 2) || (TM == 2 && TN == 1), "tile shapes");
+    static_assert((TM == 4 && TN == 2) || (TM == 2 && TN == 1) || (TM == 4 && TN == 1), "tile shapes");
     // Activation ring: three buffers per K-group.  Separate arrays, so that
     // the compiler's LDS alias scopes tell the buffers apart and a read of one
     // does not wait for the loads still landing in another.
@@ -628,8 +628,12 @@ static int qmm_cu_count() {
 // (the 2/3/5/6-bit re-packed codes included) the small tiles' per-code
 // work made them 2-8 % slower there; at M = 128 (8-16 large-tile splits)
 // and N = 1024 they are 1.2-1.5x faster.
+#ifndef EQ_QMM_MID_TILES
+#define EQ_QMM_MID_TILES 1  // 0: no 128 x 128 tiles
+#endif
 struct QmmPlan {
-    bool small;
+    bool small;  // 64 x 128 tiles
+    bool mid;    // 128 x 128 tiles
     int mtiles, ntiles, splits;
 };
 static int qmm_splits(int tiles, int slots, int nchunks) {
@@ -637,7 +641,7 @@ static int qmm_splits(int tiles, int slots, int nchunks) {
     s = s > nchunks / 8 ? nchunks / 8 : s;
     return s < 1 ? 1 : s;
 }
-static QmmPlan qmm_plan(int M, int N, int K, int gs, bool may_split) {
+static QmmPlan qmm_plan(int M, int N, int K, int gs, int bits, bool may_split) {
     QmmPlan p{};
     const int cu = qmm_cu_count(), nchunks = K / kBK;
     const int big = ((M + 127) / 128) * ((N + 255) / 256);
@@ -645,10 +649,26 @@ static QmmPlan qmm_plan(int M, int N, int K, int gs, bool may_split) {
     const bool big_ok = 4 * big >= 3 * cu || nchunks / big_splits >= 32;
     const bool small_ok = big_splits >= 8 || gs == 64;
     p.small = EQ_QMM_SMALL_TILES == 2 ? may_split : EQ_QMM_SMALL_TILES == 1 && !big_ok && small_ok;
+    // 128 x 128 tiles (group size 64) in place of the small tiles, or of large
+    // tiles that split K, when their own split leaves each piece at least 24
+    // chunks, fills 3/4 of the CUs and writes f32 partials of at most twice
+    // the weight bytes: every code then feeds 128 rows, as in the large tile,
+    // with twice the large tile's workgroups.
+    if (EQ_QMM_MID_TILES && EQ_QMM_SMALL_TILES == 1 && may_split && gs == 64 && (p.small || big_splits > 1)) {
+        const int mid = ((M + 127) / 128) * ((N + 127) / 128);
+        const int ms = qmm_splits(mid, cu, nchunks);
+        const bool fills = 4 * mid * ms >= 3 * cu;
+        const bool long_k = nchunks / ms >= 24;
+        const bool partials_ok =
+            ms == 1 || double(ms) * M * N * 4.0 <= 2.0 * double(N) * double(K) * bits / 8.0;
+        if (fills && long_k && partials_ok && (p.small || ms < big_splits)) {
+            p.small = false;
+            p.mid = true;
+        }
+    }
     p.mtiles = p.small ? (M + 63) / 64 : (M + 127) / 128;
-    p.ntiles = p.small ? (N + 127) / 128 : (N + 255) / 256;
-    p.splits = !may_split ? 1 : p.small ? qmm_splits(p.mtiles * p.ntiles, cu, nchunks)
-                                        : big_splits;
+    p.ntiles = (p.small || p.mid) ? (N + 127) / 128 : (N + 255) / 256;
+    p.splits = !may_split ? 1 : (p.small || p.mid) ? qmm_splits(p.mtiles * p.ntiles, cu, nchunks) : big_splits;
     return p;
 }
 
@@ -659,7 +679,7 @@ static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
     QmmArgs a{};
     a.y = y, a.x = x, a.w = w, a.s = static_cast<const uint16_t*>(s), a.b = static_cast<const uint16_t*>(b);
     a.M = M, a.N = N, a.K = K, a.ldy = ldy;
-    const QmmPlan plan = qmm_plan(M, N, K, GS, may_split);
+    const QmmPlan plan = qmm_plan(M, N, K, GS, BITS, may_split);
     a.mtiles = plan.mtiles, a.ntiles = plan.ntiles;
     const int tiles = a.mtiles * a.ntiles, nchunks = K / kBK;
     int splits = plan.splits;
@@ -712,6 +732,7 @@ static bool launch_qmm_piece(uint16_t* y, int ldy, const uint16_t* x, const uint
         }
     };
     if (plan.small) go(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
+    else if (plan.mid) go(std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{});
     else go(std::integral_constant<int, 4>{}, std::integral_constant<int, 2>{});
     if (splits == 1) return true;
     const int64_t mn = int64_t(M) * N;
@@ -958,7 +979,7 @@ static bool launch_qmm_odd_t(int bits, int gs, uint16_t* y, const uint16_t* x, c
     nc = nc > N ? N : nc;
     const size_t code_bytes = (size_t(nc) * size_t(K) + 255) & ~size_t(255);
     // room after the codes for the split-K partials of a slice the planner would split
-    const int splits = qmm_plan(M, int(nc), K, gs, true).splits;
+    const int splits = qmm_plan(M, int(nc), K, gs, 8, true).splits;
     const size_t part_bytes = splits > 1 ? size_t(splits) * size_t(M) * size_t(nc) * 4u : 0;
     size_t want = code_bytes + part_bytes;
     char* base = static_cast<char*>(ws_acquire(src, want, st));

@@ -115,6 +115,18 @@ def test_qmm_tiles_ragged(cuda, bits, M, gs):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K", [(500, 3968, 4096), (400, 3968, 14336)])
+def test_qmm_mid_tiles_ragged(cuda, bits, M, N, K):
+    # 128 x 128 tiles with K split twice, M not a multiple of 128 and N of
+    # 256 (31 column tiles): in place of the 64 x 128 tiles at K = 4096 and
+    # of the 128 x 256 tiles' 4-way split at K = 14336.  (Seed 4476 at
+    # M = 500, N = 3968, K = 4096, 8 bits puts one of the 2e6 outputs just
+    # over the rule: the matrix-core path rounds each dequantized weight to
+    # bf16, and the 64 x 128 plan gives that element the same value.)
+    run_case(M, N, K, 64, bits, seed=1 + bits)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 def test_qmm_split_k(cuda, bits):
     # 6 output tiles, 32 chunks: K split 8 ways, partial tiles summed in order
     run_case(300, 512, 2048, 64, bits, seed=bits + 77)

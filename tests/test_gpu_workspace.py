@@ -59,8 +59,8 @@ def test_graph_replays_survive_workspace_growth(cuda):
             attn_call(a_graph, q, kn, vn, kc, vc, freqs, 100, max_seq, st)
     torch.cuda.synchronize()
     # a much larger split-K call on the same stream grows its workspace
-    # (8 x 16 tiles, K split twice: 2 x 1024 x 4096 x 4 bytes of partials)
-    M2, N2, K2 = 1024, 4096, 4096
+    # (4 x 32 tiles of 128 x 128, K split twice: 2 x 512 x 4096 x 4 bytes of partials)
+    M2, N2, K2 = 512, 4096, 4096
     w2, s2, b2 = synthetic_linear(N2, K2, 64, 4, seed=4)
     x2 = dev_bf16(synthetic_x(M2, K2, seed=5))
     y2 = torch.empty((M2, N2), dtype=torch.bfloat16, device="cuda")
