@@ -735,7 +735,9 @@ __device__ __forceinline__ void qmv_wload_ring(QmvWBlock<BITS, GS, NU, true>& b,
 // A operands of span j0 + u are read from LDS at xa_t + j0 * xstep + u * SPAN * 2
 // (dead rows have xstep 0 and xa_t in the zero block, which covers NU spans).
 // MREG 8: the second row set's A operands at xa_t2 + j0 * xstep2 (acc2).
-template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC, typename XT = BF16T>
+// PERM4: the staged activations of 4-bit codes are permuted per 8-element
+// chunk (qmv_permute_x8); false: in k order (codes unpacked in k order).
+template <int BITS, int GS, typename ST, int MREG, int NU, bool VEC, typename XT = BF16T, bool PERM4 = true>
 __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, GS, NU, VEC>& b, const char* smem,
                                              const uint32_t* xa_t, uint32_t xstep, int j0, int r_p,
                                              float bias_on, const UnpackConsts& uc, bf16x8 ones,
@@ -763,9 +765,9 @@ __device__ __forceinline__ void qmv_wcompute(f32x4& acc, const QmvWBlock<BITS, G
 #pragma unroll
             for (int t = 0; t < Geo::STEPS; t++)
                 xa2[t] = *reinterpret_cast<const bf16x8*>(smem + xb2[t] + u * Geo::SPAN * 2);
-            qmv_span2<BITS, GS, ST, BITS == 4, XT>(acc, *acc2, xa, xa2, b.wd[u], sc, bi, uc, ones);
+            qmv_span2<BITS, GS, ST, BITS == 4 && PERM4, XT>(acc, *acc2, xa, xa2, b.wd[u], sc, bi, uc, ones);
         } else {
-            qmv_span<BITS, GS, ST, MREG, BITS == 4, XT>(acc, xa, b.wd[u], sc, bi, uc, ones);
+            qmv_span<BITS, GS, ST, MREG, BITS == 4 && PERM4, XT>(acc, xa, b.wd[u], sc, bi, uc, ones);
         }
     }
 }
@@ -1019,8 +1021,12 @@ __device__ __forceinline__ u32x4 qmv_norm8(const u32x4 a, const u32x4 w, float i
 // 16-row tile t, gate rows 8t .. 8t + 7 then up rows 8t .. 8t + 7, and the
 // tile writes y[8t + i] = silu(bf16(gate_i)) * bf16(up_i) with the roundings
 // of qmv_silu_mul8 (M = 1).
+// DIRECT (launches planned in K phases): each phase's activations go from
+// memory straight to LDS (one buffer_load ... lds per KiB, every piece of
+// the phase in flight at once, the XOR swizzle chosen through the source
+// addresses), in k order, so 4-bit codes are unpacked in k order too.
 template <int BITS, int GS, typename ST, int MREG, bool VEC, bool TAIL, int PRO = 0, typename XT = BF16T,
-          int EPI = 0, bool GATHER = false>
+          int EPI = 0, bool GATHER = false, bool DIRECT = false>
 __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_per_eu(1, 2))) void qmv_lds_kernel(
     const QmvBatch batch) {
     typedef QmvGeom<BITS, GS> Geo;
@@ -1127,9 +1133,30 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // Order of the first requests: the activations, then the weight blocks.
     // Loads complete in order, so the activations can be stored (and the
     // workgroup synchronised) while the weights are still on their way.
+    static_assert(!DIRECT || (PRO == 0 && EPI == 0 && !GATHER && !TAIL && MREG == 4),
+                  "direct staging: K-phase launches (one plain problem, whole blocks, up to 8 rows)");
+    // DIRECT: slot s of the phase buffer (row m = s / cpr, slot p) holds the
+    // 16-byte chunk p ^ (m & 7) of the phase, one wave load per 1 KiB; the
+    // planner makes M * cpr a multiple of 64.
+    auto stage_direct = [&](int k0) __attribute__((always_inline)) {
+        const QmvProblem& pr = batch.p[0];
+        const __amdgpu_buffer_rsrc_t xr = raw_rsrc(pr.x, uint32_t(M) * uint32_t(pr.K) * 2u);
+        const int cpr = pr.kpad / 8, pieces = M * cpr / 64;
+        const float inv_cpr = pr.inv_cpr;
+        for (int pc = wave; pc < pieces; pc += NW) {
+            const int sl = pc * 64 + lane;
+            // sl / cpr exactly (sl < 2^15, as in stage_load)
+            const int m = int((float(sl) + 0.5f) * inv_cpr), cc = (sl - m * cpr) ^ (m & 7);
+            const uint32_t off =
+                k0 + cc * 8 < pr.K ? (uint32_t(m) * uint32_t(pr.K) + uint32_t(k0 + cc * 8)) * 2u : kOutOfRange;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void*)(smem + pr.x_lds + pc * 1024), 16, off, 0, 0, 0);
+        }
+    };
     u32x4 xv[NCH];
     int xdst[NCH];
-    stage_load(0, threadIdx.x, xv, xdst);
+    if constexpr (DIRECT) stage_direct(0);
+    else stage_load(0, threadIdx.x, xv, xdst);
     QmvStream ls;
     ls.pi = qmv_problem_of(batch, blockIdx.x, 0);
     ls.L = qmv_tile_view<BITS, GS, TAIL, GATHER>(batch, ls.pi, blockIdx.x, wave, ln, kq, 0, false, r_p, routes).L;
@@ -1148,8 +1175,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
         ring_load(ring[d]);
         qmv_stream_next<BITS, GS, TAIL, GATHER>(batch, ls, wave, ln, kq, r_p, routes);
     }
-    stage_store(xv, xdst, int(threadIdx.x));
-    if constexpr (PRO != 2) {  // (the planner keeps a normalized row to one round)
+    if constexpr (!DIRECT) stage_store(xv, xdst, int(threadIdx.x));
+    if constexpr (PRO != 2 && !DIRECT) {  // (the planner keeps a normalized row to one round)
         for (int r = 0; r < batch.nstage; r++) {
             const QmvProblem& pr = batch.p[batch.stage[r]];
             const int total = M * (pr.kpad / 8);
@@ -1162,6 +1189,7 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     static_assert(U * SPAN * 2 + 64 <= 16 * 64 * NW, "one pass clears the zero block");
     if (int(threadIdx.x) < batch.zero_bytes / 16)
         *reinterpret_cast<u32x4*>(smem + zero_lds + threadIdx.x * 16) = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (DIRECT) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's pieces have landed
     __syncthreads();
 
     const UnpackConsts uc = make_unpack_consts<XT>();
@@ -1279,10 +1307,15 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     int phase_base = 0, phase_end = batch.phase_spans > 0 ? batch.phase_spans : 0x7fffffff;
     auto restage = [&]() __attribute__((always_inline)) {
         __syncthreads();  // every wave is done with the previous phase's activations
-        const int total = M * (batch.p[0].kpad / 8);
-        for (int c0 = int(threadIdx.x); c0 < total; c0 += NCH * 64 * NW) {
-            stage_load(0, c0, xv, xdst, phase_end * SPAN);
-            stage_store(xv, xdst, c0);
+        if constexpr (DIRECT) {
+            stage_direct(phase_end * SPAN);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            const int total = M * (batch.p[0].kpad / 8);
+            for (int c0 = int(threadIdx.x); c0 < total; c0 += NCH * 64 * NW) {
+                stage_load(0, c0, xv, xdst, phase_end * SPAN);
+                stage_store(xv, xdst, c0);
+            }
         }
         __syncthreads();
         phase_base = phase_end;
@@ -1297,8 +1330,9 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
                 if (jc >= phase_end) restage();
             }
             if (opaque_one()) {
-                qmv_wcompute<BITS, GS, ST, MREG, U, VEC, XT>(acc, ring[d], smem, V.xa_t, V.xstep, jc - phase_base, r_p,
-                                                          V.bias_on, uc, ones, &acc2, V.xa_t2, V.xstep2);
+                qmv_wcompute<BITS, GS, ST, MREG, U, VEC, XT, !DIRECT>(acc, ring[d], smem, V.xa_t, V.xstep,
+                                                                    jc - phase_base, r_p, V.bias_on, uc, ones, &acc2,
+                                                                    V.xa_t2, V.xstep2);
             } else {
                 qmv_retire(ring[d]);
             }
@@ -1347,6 +1381,10 @@ static int device_lds_bytes() {
     }
     return v;
 }
+
+#ifndef EQ_QMV_DIRECT_PHASES
+#define EQ_QMV_DIRECT_PHASES 1  // 0: K-phase launches stage through registers
+#endif
 
 // Launch plan of the persistent LDS variant.
 struct QmvLdsPlan {
@@ -1466,7 +1504,10 @@ static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
         else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 1, true, true, 0, XT>);
         else go(qmv_lds_kernel<BITS, GS, ST, 1, false, true, 0, XT>);
     } else {
-        if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 4, true, false, 0, XT>);
+        if (EQ_QMV_DIRECT_PHASES && plan.B.phase_spans > 0 && plan.vec && !plan.tail &&
+            plan.B.p[0].x_lds == 0 && (plan.B.M * (plan.B.p[0].kpad / 8)) % 64 == 0)
+            go(qmv_lds_kernel<BITS, GS, ST, 4, true, false, 0, XT, 0, false, true>);
+        else if (plan.vec && !plan.tail) go(qmv_lds_kernel<BITS, GS, ST, 4, true, false, 0, XT>);
         else if (plan.vec) go(qmv_lds_kernel<BITS, GS, ST, 4, true, true, 0, XT>);
         else go(qmv_lds_kernel<BITS, GS, ST, 4, false, true, 0, XT>);
     }
