@@ -1133,8 +1133,8 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // Order of the first requests: the activations, then the weight blocks.
     // Loads complete in order, so the activations can be stored (and the
     // workgroup synchronised) while the weights are still on their way.
-    static_assert(!DIRECT || (PRO == 0 && EPI == 0 && !GATHER && !TAIL && MREG == 4),
-                  "direct staging: K-phase launches (one plain problem, whole blocks, up to 8 rows)");
+    static_assert(!DIRECT || (PRO == 0 && EPI == 0 && !GATHER && !TAIL && (MREG == 4 || MREG == 8)),
+                  "direct staging: K-phase launches (one plain problem, whole blocks, up to 16 rows)");
     // DIRECT: slot s of the phase buffer (row m = s / cpr, slot p) holds the
     // 16-byte chunk p ^ (m & 7) of the phase, one wave load per 1 KiB; the
     // planner makes M * cpr a multiple of 64.
@@ -1495,7 +1495,11 @@ static void run_qmv_lds(const QmvLdsPlan& plan, hipStream_t st) {
     };
     if constexpr (QmvGeom<BITS, GS>::RPL > QmvGeom<BITS, GS>::MB) {
         if (plan.B.M > QmvGeom<BITS, GS>::MB) {  // (the planner checked vec and whole blocks)
-            go(qmv_lds_kernel<BITS, GS, ST, 8, true, false, 0, XT>);
+            if (EQ_QMV_DIRECT_PHASES && plan.B.phase_spans > 0 && plan.B.p[0].x_lds == 0 &&
+                (plan.B.M * (plan.B.p[0].kpad / 8)) % 64 == 0)
+                go(qmv_lds_kernel<BITS, GS, ST, 8, true, false, 0, XT, 0, false, true>);
+            else
+                go(qmv_lds_kernel<BITS, GS, ST, 8, true, false, 0, XT>);
             return;
         }
     }
