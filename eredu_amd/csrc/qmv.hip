@@ -1135,9 +1135,11 @@ __global__ __launch_bounds__(64 * kQmvLdsMaxWaves) __attribute__((amdgpu_waves_p
     // workgroup synchronised) while the weights are still on their way.
     static_assert(!DIRECT || (PRO == 0 && EPI == 0 && !GATHER && !TAIL && (MREG == 4 || MREG == 8)),
                   "direct staging: K-phase launches (one plain problem, whole blocks, up to 16 rows)");
-    // DIRECT: slot s of the phase buffer (row m = s / cpr, slot p) holds the
-    // 16-byte chunk p ^ (m & 7) of the phase, one wave load per 1 KiB; the
-    // planner makes M * cpr a multiple of 64.
+    // DIRECT: slot sl of the phase buffer (row m = sl / cpr, slot p) holds
+    // the 16-byte chunk p ^ (m & 7) of the phase, one wave load per 1 KiB;
+    // the launcher takes this variant only when M * cpr is a multiple of 64
+    // (phases of whole interleave strides make it so), so every piece lies
+    // inside the activation region.
     auto stage_direct = [&](int k0) __attribute__((always_inline)) {
         const QmvProblem& pr = batch.p[0];
         const __amdgpu_buffer_rsrc_t xr = raw_rsrc(pr.x, uint32_t(M) * uint32_t(pr.K) * 2u);
